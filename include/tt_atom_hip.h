@@ -1,0 +1,145 @@
+/* tt_atom_hip.h -- C ABI of libttatom_hip.so, the MI355X (gfx950) kernels of the eSCN-MD (UMA)
+ * edgewise hot path.
+ *
+ * Conventions (every entry point):
+ *   - device pointers to caller-allocated buffers (the PyTorch caching allocator owns memory;
+ *     nothing here allocates), int64_t sizes, fp32 data, int32 indices, row-major layouts;
+ *   - work is enqueued on `stream` (hipStream_t, passed as void*), stream-ordered, reentrant;
+ *   - return 0 on success, non-zero on bad arguments / launch failure, with the message in
+ *     tta_last_error() (thread-local).  The Python layer raises RuntimeError on non-zero,
+ *     matching the reference's fail-loud validation (fused_rotate_device_operation.cpp:16-44
+ *     TT_FATAL -> RuntimeError, rotation.py:97-102).
+ *
+ * Layouts: node features [N, 9, C] natural (l, m) order; edge-frame tensors [E, 9, W] m-primed
+ * order (to_m = [0,2,6,3,7,1,5,8,4]); packed Wigner coefficients [E, 35] in the reference's
+ * pack order (rotation.py:196-208).  Internal edge order is destination-sorted (stable), with
+ * tgt_ptr [N+1] the destination CSR and (src_ptr [N+1], src_perm [E]) the source CSR.
+ */
+#ifndef TT_ATOM_HIP_H
+#define TT_ATOM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* tta_stream_t; /* hipStream_t */
+
+const char* tta_last_error(void);
+int tta_version(void);
+/* Writes the device's gcnArchName; non-zero unless it is gfx950. */
+int tta_check_device(char* name_out, int64_t name_len);
+
+/* ---------------------------------------------------------------- dense contractions (MFMA)
+ * C[b] = epi(A[b] @ B[b] + bias[b]); A [M,K] (lda), B [K,N] (ldb), C [M,N] (ldc), batch
+ * strides sA/sB/sC/sBias.  epilogue: 0 store, 1 silu, 2 accumulate, 3 store v and silu(v) to
+ * C2, 4 store v * silu'(aux).
+ * Replaces the ttnn.linear / ttnn.matmul calls of so2.py:106-115, 282-294 (SO(2) m-block GEMMs
+ * with the [[Wa,Wb],[-Wb,Wa]] fused weight of so2.py:230-253), forces.py:23-36 (_mm transpose
+ * GEMMs of the VJP), spectral.py:176-187, grid.py:64-75 and model.py:223-231 (energy head). */
+int tta_gemm_f32(const float* A, const float* B, float* C, const float* bias, float* C2,
+                 const float* aux, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                 int64_t ldc, int64_t batch, int64_t sA, int64_t sB, int64_t sC, int64_t sBias,
+                 int epilogue, tta_stream_t stream);
+
+/* ---------------------------------------------------------------- edge-frame rotation
+ * out[e, m, :] = (sum_j W[e,m,j] [x[src_e, j, :] | x[tgt_e, j, :]]) * rad[e, rb(m), :]
+ * x [N,9,C], out [E,9,2C], rad [E,6,2C] or NULL.  Fuses the src/tgt gather + interleave of
+ * edgewise.py:52-59, rotation.rotate -> ttnn.experimental.fused_rotate (rotation.py:211-222;
+ * fused_rotate.hpp:15-23) and the radial multiply of so2.py:263-277. */
+int tta_gather_rotate(const float* x, const int* src, const int* tgt, const float* coef,
+                      const float* rad, float* out, int64_t N, int64_t E, int64_t C,
+                      tta_stream_t stream);
+
+/* Backward of tta_gather_rotate: g_mcat [E,9,2C] (written), g_rad [E,6,2C] (written, duplicate
+ * radial blocks collapsed), g_coef [E,35] (accumulated).  Replaces rotation.rotate_bw ->
+ * fused_rotate (grouped by j) + fused_rotate_gc (rotation.py:225-260; fused_rotate_gc.hpp:15-23)
+ * and the radial adjoint of forces.py:164-170. */
+int tta_gather_rotate_bw(const float* g_xf, const float* rad, const float* x, const int* src,
+                         const int* tgt, const float* coef, float* g_rad, float* g_mcat,
+                         float* g_coef, int64_t N, int64_t E, int64_t C, tta_stream_t stream);
+
+/* out[n] = res[n] + sum_{e in dst segment n} contrib_e, contrib = W^T (m[e] env[e]) when
+ * env_first, else ((W^T pad(m[e])) env[e]) / div.  m [E, n_in, C] with n_in 9 or 3 (the m = 0
+ * block only).  Deterministic (ascending edge order, no atomics).  Replaces the inverse rotate +
+ * scatter of edgewise.py:72-86 (fused_rotate + one-hot matmul / scatter.segment_sum,
+ * scatter.py:62-89) and the edge-degree node init of geometry.py:268-276 / edge_degree.py:43-66. */
+int tta_rotate_env_segsum(const float* m, const float* coef, const float* env,
+                          const int* tgt_ptr, const float* res, float* out, int64_t N, int64_t E,
+                          int64_t C, int64_t n_in, int env_first, float div, tta_stream_t stream);
+
+/* Backward of tta_rotate_env_segsum: g_m [E, n_in, C] (written), g_coef (accumulated), g_env [E]
+ * (accumulated).  Replaces forces.py:366-376 and edge_degree.py:69-93. */
+int tta_rotate_env_segsum_bw(const float* g_node, const int* tgt, const float* m,
+                             const float* coef, const float* env, float* g_m, float* g_coef,
+                             float* g_env, int64_t N, int64_t E, int64_t C, int64_t n_in,
+                             int env_first, float div, tta_stream_t stream);
+
+/* out[n] = (sum_{src(e)=n} g_mcat[e,:,0:C] + sum_{tgt(e)=n} g_mcat[e,:,C:2C]) + res[n].
+ * Replaces the deinterleave + S_src / S scatters of forces.py:384-412. */
+int tta_node_gather_sum(const float* g_mcat, const int* src_ptr, const int* src_perm,
+                        const int* tgt_ptr, const float* res, float* out, int64_t N, int64_t E,
+                        int64_t C, tta_stream_t stream);
+
+/* ---------------------------------------------------------------- element / row-wise
+ * Gate: y[r,0] = silu(x[r,0]); y[r,c] = x[r,c] sigmoid(gating[r, idx8[c-1]]).  x, y [R,9,H],
+ * gating [R, L*H].  activation.py:29-70 (m-primed idx), spectral.py:129-144 (natural idx);
+ * backward forces.py:104-130 (and ttnn.experimental.fused_gate, fused_gate.hpp:14-21). */
+int tta_gate_fwd(const float* x, const float* gating, float* y, int64_t R, int64_t H, int64_t L,
+                 const int* idx8, tta_stream_t stream);
+int tta_gate_bwd(const float* g_y, const float* x, const float* gating, float* g_x,
+                 float* g_gating, int64_t R, int64_t H, int64_t L, const int* idx8,
+                 tta_stream_t stream);
+
+/* Radial MLP LayerNorm + SiLU: nrm = LN(a), s = silu(nrm) (so2.py:101-115) and its backward
+ * g_a (so2.py:117-143; ttnn.experimental.fused_ln_bw, fused_ln_bw.hpp:14-21). */
+int tta_ln_silu_fwd(const float* a, const float* gamma, const float* beta, float* nrm, float* s,
+                    int64_t R, int64_t n, float eps, tta_stream_t stream);
+int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm, const float* gamma,
+                    float* g_a, int64_t R, int64_t n, float eps, tta_stream_t stream);
+
+/* RMSNormSH (norm.py:59-111) with an optional l=0 addend (the system embedding of
+ * model.py:164-167); inv [N] kept for the backward (forces.py:49-98; res = residual adjoint). */
+int tta_rmsnorm_sh_fwd(const float* x, const float* aw, const float* ab, const float* add0,
+                       float* y, float* inv, int64_t N, int64_t C, float eps,
+                       tta_stream_t stream);
+int tta_rmsnorm_sh_bwd(const float* g, const float* x, const float* aw, const float* inv,
+                       const float* res, float* out, int64_t N, int64_t C, tta_stream_t stream);
+
+int tta_silu_bwd(const float* g, const float* x, float* out, int64_t n, tta_stream_t stream);
+/* Deterministic single-block sum of x[0], x[stride], ... (model.py:233-235 energy sum). */
+int tta_sum(const float* x, int64_t n, int64_t stride, float* out, tta_stream_t stream);
+int tta_fill(float* out, int64_t n, float value, tta_stream_t stream);
+
+/* ---------------------------------------------------------------- geometry
+ * ev = pos[src] - pos[tgt] (+ shift), dist = |ev|, coef = packed Wigner-D (geometry.py:209-224
+ * + 234-240, gauge gamma; jd = [Jd_0 | Jd_1 | Jd_2] 35 floats). */
+int tta_edge_wigner(const float* pos, const int* src, const int* tgt, const float* shift,
+                    const float* jd, float gamma, float* ev, float* dist, float* coef, int64_t N,
+                    int64_t E, tta_stream_t stream);
+/* x_edge = [gaussians(dist) | src_emb[zsrc] | tgt_emb[ztgt]], env = polynomial envelope
+ * (geometry.py:242-251). */
+int tta_edge_features(const float* dist, const int* zsrc, const int* ztgt, const float* src_emb,
+                      const float* tgt_emb, const float* offsets, float coeff, float cutoff,
+                      int64_t nb, int64_t ec, float* x_edge, float* env, int64_t E,
+                      tta_stream_t stream);
+/* g_ev from the coefficient, envelope and gaussian adjoints: the closed form of the host
+ * torch.autograd.grad finish of forces.py:580-586 (regularised acos/atan2 of geometry.py:87-109). */
+int tta_edge_geometry_bwd(const float* ev, const float* dist, const float* g_coef,
+                          const float* g_env, const float* g_gauss, int64_t ldg,
+                          const float* offsets, float coeff, float cutoff, int64_t nb,
+                          const float* jd, float gamma, float* g_ev, int64_t E,
+                          tta_stream_t stream);
+/* F[n] = -(sum_{src=n} g_ev - sum_{tgt=n} g_ev) (forces.py:586-589). */
+int tta_node_forces(const float* g_ev, const int* src_ptr, const int* src_perm,
+                    const int* tgt_ptr, float* forces, int64_t N, int64_t E, tta_stream_t stream);
+/* virial[3x3] = sum_e sym(ev (x) g_ev) = dE/dstrain (forces.py:516-524); work >= 256*9 floats. */
+int tta_virial(const float* ev, const float* g_ev, int64_t E, float* work, float* out,
+               tta_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TT_ATOM_HIP_H */

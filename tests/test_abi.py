@@ -1,0 +1,35 @@
+"""The C-ABI library loads and exports every symbol include/tt_atom_hip.h declares (CPU only:
+no compute call is made without a GPU)."""
+import pathlib
+import re
+
+from tt_atom import _native
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "tt_atom_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int)\s+(tta_\w+)\(", text, re.M)))
+
+
+def test_header_and_bindings_agree():
+    assert _declared() == sorted(_native.EXPORTS)
+
+
+def test_library_exports_every_symbol():
+    lib = _native.load_symbols_only()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.tta_version() == 1
+    assert lib.tta_last_error() is not None
+
+
+def test_argument_errors_are_reported_without_a_device():
+    lib = _native.load_symbols_only()
+    # invalid sizes are rejected on the host before any launch
+    assert lib.tta_gemm_f32(None, None, None, None, None, None, -1, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0,
+                            0, None) != 0
+    assert b"negative" in lib.tta_last_error()
+    assert lib.tta_gather_rotate(None, None, None, None, None, None, 1, 1, 6, None) != 0
+    assert b"unsupported channel count" in lib.tta_last_error()

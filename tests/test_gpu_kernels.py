@@ -1,0 +1,356 @@
+"""Per-kernel parity on the MI355X: every HIP kernel of the edgewise path against a torch-CPU
+(fp64) restatement of the same operation, or against the oracle.  Run with ``-m gpu``."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import geometry as OG
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def nat():
+    from tt_atom import _native
+    _native.load()
+    return _native
+
+
+def _pack_ij():
+    """(m-primed row, natural column) of the 35 packed coefficients, row-major (rotation.py:204-207)."""
+    deg = [0, 1, 2, 1, 2, 1, 2, 2, 2]
+    cols = {0: [0], 1: [1, 2, 3], 2: [4, 5, 6, 7, 8]}
+    return [(m, j) for m in range(9) for j in cols[deg[m]]]
+
+
+IJ = _pack_ij()
+
+
+def _dense(coef):
+    W = torch.zeros(coef.shape[0], 9, 9, dtype=coef.dtype)
+    ii = torch.tensor([i for i, _ in IJ])
+    jj = torch.tensor([j for _, j in IJ])
+    W[:, ii, jj] = coef
+    return W
+
+
+def _jd():
+    from tt_atom.synthetic import jd_matrices
+    return jd_matrices()
+
+
+def _rand_graph(N, E, seed):
+    g = torch.Generator().manual_seed(seed)
+    tgt = torch.sort(torch.randint(0, N, (E,), generator=g)).values
+    src = torch.randint(0, N, (E,), generator=g)
+    return src, tgt, g
+
+
+def _csr(idx, N):
+    ptr = torch.zeros(N + 1, dtype=torch.int64)
+    ptr[1:] = torch.cumsum(torch.bincount(idx, minlength=N), 0)
+    return ptr
+
+
+def _i32(t):
+    return t.to(torch.int32).to(DEV)
+
+
+# ------------------------------------------------------------------------------ GEMM
+@pytest.mark.parametrize("M,N,K,epi", [(256, 128, 128, 0), (300, 96, 40, 0), (37, 20, 9, 0),
+                                       (513, 640, 768, 0), (130, 132, 64, 1), (200, 64, 48, 2),
+                                       (64, 48, 32, 3), (90, 33, 17, 4)])
+def test_gemm_matches_torch(nat, M, N, K, epi):
+    g = torch.Generator().manual_seed(M * 7 + N)
+    A = torch.randn(M, K, generator=g)
+    B = torch.randn(K, N, generator=g)
+    bias = torch.randn(N, generator=g)
+    C0 = torch.randn(M, N, generator=g)
+    aux = torch.randn(M, N, generator=g)
+    ref = (A.double() @ B.double()) + bias.double()
+    Cd = C0.clone().to(DEV)
+    C2 = torch.zeros(M, N, device=DEV)
+    nat.gemm(A.to(DEV), B.to(DEV), Cd, M=M, N=N, K=K, lda=K, ldb=N, ldc=N, bias=bias.to(DEV),
+             epilogue=epi, C2=C2, aux=aux.to(DEV))
+    torch.cuda.synchronize()
+    if epi == 1:
+        ref = torch.nn.functional.silu(ref)
+    elif epi == 2:
+        ref = ref + C0.double()
+    elif epi == 4:
+        s = torch.sigmoid(aux.double())
+        ref = ref * (s * (1 + aux.double() * (1 - s)))
+    tol = 2e-5 * math.sqrt(K) * float(ref.abs().max())
+    assert (Cd.cpu().double() - ref).abs().max() < tol
+    if epi == 3:
+        assert (C2.cpu().double() - torch.nn.functional.silu(ref)).abs().max() < tol
+
+
+def test_gemm_batched_strided(nat):
+    g = torch.Generator().manual_seed(5)
+    N_, C, H = 50, 32, 24
+    x = torch.randn(N_, 9, C, generator=g)
+    W = torch.randn(9, C, H, generator=g)
+    b = torch.randn(9, H, generator=g)
+    out = torch.empty(N_, 9, H, device=DEV)
+    nat.gemm(x.to(DEV), W.to(DEV), out, bias=b.to(DEV), M=N_, N=H, K=C, lda=9 * C, ldb=H,
+             ldc=9 * H, batch=9, sA=C, sB=C * H, sC=H, sBias=H)
+    ref = torch.einsum("nic,ich->nih", x.double(), W.double()) + b.double()[None]
+    assert (out.cpu().double() - ref).abs().max() < 1e-4
+
+
+# ------------------------------------------------------------------------------ geometry
+def _oracle_wig(ev, jd):
+    eul = OG.euler_angles(ev)
+    wig = OG.eulers_to_wigner(eul, 2, [j.to(ev.dtype) for j in jd])
+    perm = torch.tensor([0, 2, 6, 3, 7, 1, 5, 8, 4])
+    return wig.index_select(1, perm)
+
+
+def _test_vectors(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    ev = torch.randn(n, 3, generator=g) * 2.0
+    # directions at and near the poles of the edge frame (the +-y axis) and along x / z
+    special = torch.tensor([[0.0, 1.0, 0.0], [0.0, -2.0, 0.0], [1e-4, 1.0, 0.0], [0.0, 1.0, 1e-5],
+                            [3.0, 0.0, 0.0], [0.0, 0.0, -1.5], [1.0, 1.0, 1.0], [-1e-3, -3.0, 2e-3]])
+    return torch.cat([ev, special], 0)
+
+
+def test_edge_wigner_matches_oracle(nat):
+    jd = _jd()
+    ev = _test_vectors(500, 0)
+    E = ev.shape[0]
+    pos = torch.cat([ev, torch.zeros(1, 3)], 0)                    # ev = pos[e] - pos[E]
+    src = torch.arange(E)
+    tgt = torch.full((E,), E)
+    jdf = torch.cat([j.reshape(-1) for j in jd]).to(DEV)
+    evd, dist, coef = (torch.empty(E, 3, device=DEV), torch.empty(E, device=DEV),
+                       torch.empty(E, 35, device=DEV))
+    nat.edge_wigner(pos.to(DEV), _i32(src), _i32(tgt), None, jdf, 0.0, evd, dist, coef)
+    torch.cuda.synchronize()
+    ref = _oracle_wig(ev.double(), jd)
+    ref_c = torch.stack([ref[:, i, j] for i, j in IJ], 1)
+    # fp64 for the generic directions; near the pole fp32 acos itself limits the accuracy
+    assert (coef.cpu().double() - ref_c)[:-8].abs().max() < 2e-6
+    assert (dist.cpu().double() - ev.double().norm(dim=1)).abs().max() < 1e-5
+    # the same through the fp32 oracle (what the parity tests compare against)
+    g32 = _oracle_wig(ev, [j.float() for j in jd])
+    assert (coef.cpu() - torch.stack([g32[:, i, j] for i, j in IJ], 1)).abs().max() < 2e-6
+
+
+def test_edge_features_matches_oracle(nat):
+    g = torch.Generator().manual_seed(3)
+    E, nb, ec = 400, 32, 8
+    dist = torch.rand(E, generator=g) * 6.5 + 0.2
+    zs, zt = torch.randint(0, 10, (E,), generator=g), torch.randint(0, 10, (E,), generator=g)
+    semb, temb = torch.randn(10, ec, generator=g), torch.randn(10, ec, generator=g)
+    off = torch.linspace(0, 6.0, nb)
+    coeff = -0.5 / float(2 * (off[1] - off[0])) ** 2
+    xe, env = torch.empty(E, nb + 2 * ec, device=DEV), torch.empty(E, device=DEV)
+    nat.edge_features(dist.to(DEV), _i32(zs), _i32(zt), semb.to(DEV), temb.to(DEV), off.to(DEV),
+                      coeff, 6.0, nb, ec, xe, env)
+    torch.cuda.synchronize()
+    gauss = torch.exp(coeff * (dist.view(-1, 1) - off.view(1, -1)) ** 2)
+    ref = torch.cat([gauss, semb[zs], temb[zt]], 1)
+    assert (xe.cpu() - ref).abs().max() < 1e-5
+    ds = dist / 6.0
+    ev_ = 1 + ds ** 5 * (-21 + ds * (35 - 15 * ds))
+    ref_env = torch.where(ds < 1, ev_, torch.zeros_like(ev_))
+    assert (env.cpu() - ref_env).abs().max() < 1e-5
+
+
+def test_geometry_vjp_matches_autograd(nat):
+    jd = _jd()
+    ev = _test_vectors(400, 1)
+    E = ev.shape[0]
+    nb, cutoff = 16, 6.0
+    off = torch.linspace(0, cutoff, nb, dtype=torch.float64)
+    coeff = -0.5 / float(2 * (off[1] - off[0])) ** 2
+    g = torch.Generator().manual_seed(11)
+    g_coef = torch.randn(E, 35, generator=g)
+    g_env = torch.randn(E, generator=g)
+    g_gauss = torch.randn(E, nb, generator=g)
+    # autograd reference in fp64 through the oracle's functions
+    e64 = ev.double().clone().requires_grad_(True)
+    wig = _oracle_wig(e64, jd)
+    coef = torch.stack([wig[:, i, j] for i, j in IJ], 1)
+    d = torch.linalg.norm(e64, dim=1)
+    gauss = torch.exp(coeff * (d.view(-1, 1) - off.view(1, -1)) ** 2)
+    ds = d / cutoff
+    envv = torch.where(ds < 1, 1 + ds ** 5 * (-21 + ds * (35 - 15 * ds)), torch.zeros_like(ds))
+    loss = (coef * g_coef.double()).sum() + (envv * g_env.double()).sum() + \
+           (gauss * g_gauss.double()).sum()
+    (ref,) = torch.autograd.grad(loss, e64)
+    out = torch.empty(E, 3, device=DEV)
+    jdf = torch.cat([j.reshape(-1) for j in jd]).to(DEV)
+    nat.edge_geometry_bwd(ev.to(DEV), ev.norm(dim=1).to(DEV), g_coef.to(DEV), g_env.to(DEV),
+                          g_gauss.to(DEV), nb, off.float().to(DEV), coeff, cutoff, nb, jdf, 0.0, out)
+    torch.cuda.synchronize()
+    err = (out.cpu().double() - ref).abs()
+    scale = ref.abs().clamp(min=1.0)
+    # exactly-on-pole vectors hit the EPS regularisation: compare those with a looser bound
+    assert (err[:-8] / scale[:-8]).max() < 5e-4
+    assert torch.isfinite(out).all()
+
+
+# ------------------------------------------------------------------------------ rotation
+@pytest.mark.parametrize("C", [16, 32, 128])
+def test_gather_rotate_fwd_bwd(nat, C):
+    N, E = 40, 300
+    src, tgt, g = _rand_graph(N, E, C)
+    x = torch.randn(N, 9, C, generator=g, dtype=torch.float64)
+    coef = torch.randn(E, 35, generator=g, dtype=torch.float64)
+    rad = torch.randn(E, 6, 2 * C, generator=g, dtype=torch.float64)
+    rb = [0, 1, 2, 3, 4, 3, 4, 5, 5]
+    xr, cr, rr = (t.clone().requires_grad_(True) for t in (x, coef, rad))
+    m = torch.bmm(_dense(cr), torch.cat([xr[src], xr[tgt]], 2)) * rr[:, rb, :]
+    gout = torch.randn(E, 9, 2 * C, generator=g, dtype=torch.float64)
+    gx, gc, grd = torch.autograd.grad((m * gout).sum(), [xr, cr, rr])
+    out = torch.empty(E, 9, 2 * C, device=DEV)
+    f = lambda t: t.float().to(DEV).contiguous()
+    nat.gather_rotate(f(x), _i32(src), _i32(tgt), f(coef), f(rad), out)
+    g_rad, g_mcat = torch.empty(E, 6, 2 * C, device=DEV), torch.empty(E, 9, 2 * C, device=DEV)
+    g_coef = torch.zeros(E, 35, device=DEV)
+    nat.gather_rotate_bw(f(gout), f(rad), f(x), _i32(src), _i32(tgt), f(coef), g_rad, g_mcat, g_coef)
+    # node adjoint via the src / tgt CSR sum
+    sptr, perm = _csr(src, N), torch.argsort(src, stable=True)
+    tptr = _csr(tgt, N)
+    gn = torch.empty(N, 9, C, device=DEV)
+    nat.node_gather_sum(g_mcat, _i32(sptr), _i32(perm), _i32(tptr), None, gn)
+    torch.cuda.synchronize()
+    assert (out.cpu().double() - m.detach()).abs().max() < 1e-4
+    assert (g_rad.cpu().double() - grd).abs().max() < 1e-4
+    assert (g_coef.cpu().double() - gc).abs().max() < 1e-3
+    assert (gn.cpu().double() - gx).abs().max() < 1e-3
+
+
+@pytest.mark.parametrize("n_in,env_first", [(9, True), (3, False)])
+def test_rotate_env_segsum_fwd_bwd(nat, n_in, env_first):
+    N, E, C = 30, 250, 32
+    src, tgt, g = _rand_graph(N, E, 7 + n_in)
+    m = torch.randn(E, n_in, C, generator=g, dtype=torch.float64)
+    coef = torch.randn(E, 35, generator=g, dtype=torch.float64)
+    env = torch.rand(E, generator=g, dtype=torch.float64)
+    res = torch.randn(N, 9, C, generator=g, dtype=torch.float64)
+    div = 1.0 if env_first else 5.0
+    mr, cr, er = (t.clone().requires_grad_(True) for t in (m, coef, env))
+    mp = torch.nn.functional.pad(mr, (0, 0, 0, 9 - n_in))
+    Wt = _dense(cr).transpose(1, 2)
+    if env_first:
+        v = torch.bmm(Wt, mp * er.view(-1, 1, 1))
+    else:
+        v = torch.bmm(Wt, mp) * er.view(-1, 1, 1) / div
+    out_ref = torch.zeros(N, 9, C, dtype=torch.float64).index_add(0, tgt, v) + res
+    gnode = torch.randn(N, 9, C, generator=g, dtype=torch.float64)
+    gm, gc, ge = torch.autograd.grad((out_ref * gnode).sum(), [mr, cr, er])
+    f = lambda t: t.float().to(DEV).contiguous()
+    out = torch.empty(N, 9, C, device=DEV)
+    nat.rotate_env_segsum(f(m), f(coef), f(env), _i32(_csr(tgt, N)), f(res), out, n_in=n_in,
+                          env_first=env_first, div=div)
+    g_m = torch.empty(E, n_in, C, device=DEV)
+    g_coef, g_env = torch.zeros(E, 35, device=DEV), torch.zeros(E, device=DEV)
+    nat.rotate_env_segsum_bw(f(gnode), _i32(tgt), f(m), f(coef), f(env), g_m, g_coef, g_env,
+                             n_in=n_in, env_first=env_first, div=div)
+    torch.cuda.synchronize()
+    assert (out.cpu().double() - out_ref.detach()).abs().max() < 1e-4
+    assert (g_m.cpu().double() - gm).abs().max() < 1e-4
+    assert (g_env.cpu().double() - ge).abs().max() < 1e-3
+    if n_in == 3:   # only coefficients with m-primed row < 3 receive an adjoint
+        rows = torch.tensor([i for i, _ in IJ])
+        gc = gc * (rows < 3).double()
+    assert (g_coef.cpu().double() - gc).abs().max() < 1e-3
+
+
+# ------------------------------------------------------------------------------ row-wise
+@pytest.mark.parametrize("natural", [False, True])
+def test_gate_fwd_bwd(nat, natural):
+    R, H = 200, 48
+    idx = (0, 0, 0, 1, 1, 1, 1, 1) if natural else (0, 1, 0, 1, 0, 1, 1, 1)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(R, 9, H, generator=g, dtype=torch.float64)
+    gat = torch.randn(R, 2 * H, generator=g, dtype=torch.float64)
+    xr, gr = x.clone().requires_grad_(True), gat.clone().requires_grad_(True)
+    sg = torch.sigmoid(gr).view(R, 2, H)[:, list(idx), :]
+    y = torch.cat([torch.nn.functional.silu(xr[:, :1]), xr[:, 1:] * sg], 1)
+    gy = torch.randn(R, 9, H, generator=g, dtype=torch.float64)
+    gx, gg = torch.autograd.grad((y * gy).sum(), [xr, gr])
+    f = lambda t: t.float().to(DEV).contiguous()
+    idx_t = torch.tensor(idx, dtype=torch.int32, device=DEV)
+    yo = torch.empty(R, 9, H, device=DEV)
+    nat.gate_fwd(f(x), f(gat), yo, idx_t)
+    gxo, ggo = torch.empty(R, 9, H, device=DEV), torch.empty(R, 2 * H, device=DEV)
+    nat.gate_bwd(f(gy), f(x), f(gat), gxo, ggo, idx_t)
+    torch.cuda.synchronize()
+    assert (yo.cpu().double() - y.detach()).abs().max() < 1e-5
+    assert (gxo.cpu().double() - gx).abs().max() < 1e-5
+    assert (ggo.cpu().double() - gg).abs().max() < 1e-5
+
+
+@pytest.mark.parametrize("n", [16, 128, 200])
+def test_ln_silu_fwd_bwd(nat, n):
+    R = 300
+    g = torch.Generator().manual_seed(n)
+    a = torch.randn(R, n, generator=g, dtype=torch.float64) * 2 + 0.5
+    gam = 1 + 0.1 * torch.randn(n, generator=g, dtype=torch.float64)
+    bet = 0.1 * torch.randn(n, generator=g, dtype=torch.float64)
+    ar = a.clone().requires_grad_(True)
+    nrm = torch.nn.functional.layer_norm(ar, (n,), gam, bet, 1e-5)
+    s = torch.nn.functional.silu(nrm)
+    gs = torch.randn(R, n, generator=g, dtype=torch.float64)
+    (ga,) = torch.autograd.grad((s * gs).sum(), [ar])
+    f = lambda t: t.float().to(DEV).contiguous()
+    no, so, gao = (torch.empty(R, n, device=DEV) for _ in range(3))
+    nat.ln_silu_fwd(f(a), f(gam), f(bet), no, so)
+    nat.ln_silu_bwd(f(gs), f(a), no, f(gam), gao)
+    torch.cuda.synchronize()
+    assert (no.cpu().double() - nrm.detach()).abs().max() < 1e-5
+    assert (so.cpu().double() - s.detach()).abs().max() < 1e-5
+    assert (gao.cpu().double() - ga).abs().max() < 1e-4
+
+
+@pytest.mark.parametrize("C", [16, 128, 96])
+def test_rmsnorm_sh_fwd_bwd(nat, C):
+    from oracle.uma import rms_norm_sh
+    N = 60
+    g = torch.Generator().manual_seed(C)
+    x = torch.randn(N, 9, C, generator=g, dtype=torch.float64)
+    w = {"p.affine_weight": 1 + 0.1 * torch.randn(3, C, generator=g, dtype=torch.float64),
+         "p.affine_bias": 0.1 * torch.randn(C, generator=g, dtype=torch.float64)}
+    add0 = torch.randn(N, C, generator=g, dtype=torch.float64)
+    res = torch.randn(N, 9, C, generator=g, dtype=torch.float64)
+    xr = x.clone().requires_grad_(True)
+    y = rms_norm_sh(xr, w, "p", 2, C)
+    y = torch.cat([y[:, :1] + add0[:, None], y[:, 1:]], 1)
+    gy = torch.randn(N, 9, C, generator=g, dtype=torch.float64)
+    (gx,) = torch.autograd.grad((y * gy).sum(), [xr])
+    f = lambda t: t.float().to(DEV).contiguous()
+    yo, inv, gxo = torch.empty(N, 9, C, device=DEV), torch.empty(N, device=DEV), torch.empty(N, 9, C, device=DEV)
+    nat.rmsnorm_sh_fwd(f(x), f(w["p.affine_weight"]), f(w["p.affine_bias"]), f(add0), yo, inv)
+    nat.rmsnorm_sh_bwd(f(gy), f(x), f(w["p.affine_weight"]), inv, f(res), gxo)
+    torch.cuda.synchronize()
+    assert (yo.cpu().double() - y.detach()).abs().max() < 1e-5
+    assert (gxo.cpu().double() - (gx + res)).abs().max() < 1e-4
+
+
+def test_forces_virial_and_sum(nat):
+    N, E = 50, 600
+    src, tgt, g = _rand_graph(N, E, 9)
+    g_ev = torch.randn(E, 3, generator=g)
+    ev = torch.randn(E, 3, generator=g)
+    ref_F = -(torch.zeros(N, 3).index_add(0, src, g_ev) - torch.zeros(N, 3).index_add(0, tgt, g_ev))
+    ref_V = 0.5 * (ev.T @ g_ev + g_ev.T @ ev)
+    Fo, Vo, work = torch.empty(N, 3, device=DEV), torch.empty(9, device=DEV), torch.empty(256 * 9, device=DEV)
+    nat.node_forces(g_ev.to(DEV), _i32(_csr(src, N)), _i32(torch.argsort(src, stable=True)),
+                    _i32(_csr(tgt, N)), Fo)
+    nat.virial(ev.to(DEV), g_ev.to(DEV), work, Vo)
+    x = torch.randn(5000, generator=g)
+    so = torch.empty(1, device=DEV)
+    nat.reduce_sum(x.to(DEV), 5000, 1, so)
+    torch.cuda.synchronize()
+    assert (Fo.cpu() - ref_F).abs().max() < 1e-5
+    assert (Vo.cpu().reshape(3, 3) - ref_V).abs().max() < 1e-3
+    assert abs(float(so) - float(x.double().sum())) < 1e-3

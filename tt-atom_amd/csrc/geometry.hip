@@ -1,0 +1,220 @@
+// Edge geometry kernels: positions -> (edge vectors, distances, packed Wigner coefficients,
+// radial features, envelope) and the reverse: coefficient / radial / envelope adjoints -> edge
+// vector adjoints -> forces (deterministic CSR sums) and the symmetric virial.
+//
+// Reference: tt_atom/geometry.py:226-280 (forward terms) and the host autograd finish of
+// forces.py:545-589 (here in closed form, geometry_math.h).
+#include "common.h"
+#include "geometry_math.h"
+
+namespace {
+
+// One thread per edge: ev = pos[src] - pos[tgt] (+ shift), dist = |ev|, coef = packed W(ev).
+__global__ __launch_bounds__(256) void k_edge_wigner(const float* __restrict__ pos,
+                                                     const int* __restrict__ src,
+                                                     const int* __restrict__ tgt,
+                                                     const float* __restrict__ shift,
+                                                     const float* __restrict__ jd, float gamma,
+                                                     float* __restrict__ ev_out,
+                                                     float* __restrict__ dist_out,
+                                                     float* __restrict__ coef_out, int E) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int s = src[e], t = tgt[e];
+  float ev[3];
+  for (int k = 0; k < 3; ++k) {
+    ev[k] = pos[s * 3 + k] - pos[t * 3 + k];
+    if (shift) ev[k] = ev[k] + shift[(int64_t)e * 3 + k];
+    ev_out[(int64_t)e * 3 + k] = ev[k];
+  }
+  dist_out[e] = sqrtf(ev[0] * ev[0] + ev[1] * ev[1] + ev[2] * ev[2]);
+  float jl[35];
+  for (int k = 0; k < 35; ++k) jl[k] = jd[k];
+  float c[35];
+  tta_geo::wigner_coef(ev, gamma, jl, c);
+  for (int k = 0; k < 35; ++k) coef_out[(int64_t)e * 35 + k] = c[k];
+}
+
+// x_edge[e] = [exp(coeff (d - off_k)^2) (nb) | src_emb[z_src] (ec) | tgt_emb[z_tgt] (ec)], env[e].
+__global__ __launch_bounds__(256) void k_edge_features(
+    const float* __restrict__ dist, const int* __restrict__ zs, const int* __restrict__ zt,
+    const float* __restrict__ semb, const float* __restrict__ temb, const float* __restrict__ off,
+    float coeff, float cutoff, int nb, int ec, float* __restrict__ x_edge,
+    float* __restrict__ env, int E) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int width = nb + 2 * ec;
+  if (gid >= (int64_t)E * width) return;
+  const int64_t e = gid / width;
+  const int k = (int)(gid % width);
+  const float d = dist[e];
+  float v;
+  if (k < nb) {
+    const float t = d - off[k];
+    v = expf(coeff * (t * t));
+  } else if (k < nb + ec) {
+    v = semb[(int64_t)zs[e] * ec + (k - nb)];
+  } else {
+    v = temb[(int64_t)zt[e] * ec + (k - nb - ec)];
+  }
+  x_edge[gid] = v;
+  if (k == 0) env[e] = tta_geo::envelope(d, cutoff);
+}
+
+// g_ev[e] = VJP of (coef, gaussians, envelope, |ev|) at the given adjoints.
+__global__ __launch_bounds__(256) void k_edge_geometry_bwd(
+    const float* __restrict__ ev, const float* __restrict__ dist,
+    const float* __restrict__ g_coef, const float* __restrict__ g_env,
+    const float* __restrict__ g_gauss, int64_t ldg, const float* __restrict__ off, float coeff,
+    float cutoff, int nb, const float* __restrict__ jd, float gamma, float* __restrict__ g_ev,
+    int E) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  float v[3] = {ev[(int64_t)e * 3], ev[(int64_t)e * 3 + 1], ev[(int64_t)e * 3 + 2]};
+  const float d = dist[e];
+  float gd = 0.f;
+  if (g_gauss) {
+    const float* gg = g_gauss + (int64_t)e * ldg;
+    for (int k = 0; k < nb; ++k) {
+      const float t = d - off[k];
+      const float gk = expf(coeff * (t * t));
+      gd += gg[k] * (gk * (coeff * (2.f * t)));
+    }
+  }
+  if (g_env) gd += g_env[e] * tta_geo::envelope_grad(d, cutoff);
+  float out[3] = {0.f, 0.f, 0.f};
+  if (d > 0.f)
+    for (int k = 0; k < 3; ++k) out[k] = gd * (v[k] / d);
+  if (g_coef) {
+    float jl[35], gc[35];
+    for (int k = 0; k < 35; ++k) jl[k] = jd[k];
+    for (int k = 0; k < 35; ++k) gc[k] = g_coef[(int64_t)e * 35 + k];
+    tta_geo::wigner_vjp(v, gamma, jl, gc, out);
+  }
+  for (int k = 0; k < 3; ++k) g_ev[(int64_t)e * 3 + k] = out[k];
+}
+
+// F[n] = -(sum_{src(e) = n} g_ev[e] - sum_{tgt(e) = n} g_ev[e])   (ev = pos[src] - pos[tgt])
+__global__ __launch_bounds__(256) void k_node_forces(const float* __restrict__ g_ev,
+                                                     const int* __restrict__ src_ptr,
+                                                     const int* __restrict__ src_perm,
+                                                     const int* __restrict__ tgt_ptr,
+                                                     float* __restrict__ forces, int N) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  float a[3] = {0.f, 0.f, 0.f}, b[3] = {0.f, 0.f, 0.f};
+  for (int k = src_ptr[n]; k < src_ptr[n + 1]; ++k) {
+    const int64_t e = src_perm[k];
+    for (int c = 0; c < 3; ++c) a[c] += g_ev[e * 3 + c];
+  }
+  for (int64_t e = tgt_ptr[n]; e < tgt_ptr[n + 1]; ++e)
+    for (int c = 0; c < 3; ++c) b[c] += g_ev[e * 3 + c];
+  for (int c = 0; c < 3; ++c) forces[(int64_t)n * 3 + c] = -(a[c] - b[c]);
+}
+
+// Virial dE/dstrain = sum_e 0.5 (ev_a g_b + ev_b g_a): fixed-order two-stage reduction.
+constexpr int kVirBlocks = 256;
+
+__global__ __launch_bounds__(256) void k_virial_partial(const float* __restrict__ ev,
+                                                        const float* __restrict__ g_ev, int E,
+                                                        float* __restrict__ part) {
+  __shared__ float sh[4][9];
+  float acc[9];
+  for (int i = 0; i < 9; ++i) acc[i] = 0.f;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < E;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    for (int a = 0; a < 3; ++a)
+      for (int b = 0; b < 3; ++b)
+        acc[a * 3 + b] += 0.5f * (ev[e * 3 + a] * g_ev[e * 3 + b] + ev[e * 3 + b] * g_ev[e * 3 + a]);
+  }
+  for (int i = 0; i < 9; ++i) acc[i] = tta_group_sum(acc[i], 64);
+  if ((threadIdx.x & 63) == 0)
+    for (int i = 0; i < 9; ++i) sh[threadIdx.x >> 6][i] = acc[i];
+  __syncthreads();
+  if (threadIdx.x < 9) {
+    float s = 0.f;
+    for (int w = 0; w < 4; ++w) s += sh[w][threadIdx.x];
+    part[blockIdx.x * 9 + threadIdx.x] = s;
+  }
+}
+
+__global__ __launch_bounds__(64) void k_virial_final(const float* __restrict__ part, int nb,
+                                                     float* __restrict__ out) {
+  const int i = threadIdx.x;
+  if (i >= 9) return;
+  float s = 0.f;
+  for (int b = 0; b < nb; ++b) s += part[b * 9 + i];
+  out[i] = s;
+}
+
+}  // namespace
+
+extern "C" int tta_edge_wigner(const float* pos, const int* src, const int* tgt,
+                               const float* shift, const float* jd, float gamma, float* ev,
+                               float* dist, float* coef, int64_t N, int64_t E,
+                               hipStream_t stream) {
+  TTA_CHECK_ARG(E >= 0 && E < (1ll << 31) && N >= 0, "tta_edge_wigner: bad sizes");
+  if (E == 0) return tta::kOk;
+  TTA_CHECK_ARG(pos && src && tgt && jd && ev && dist && coef, "tta_edge_wigner: null pointer");
+  hipLaunchKernelGGL(k_edge_wigner, dim3(tta_blocks(E, 256)), dim3(256), 0, stream, pos, src, tgt,
+                     shift, jd, gamma, ev, dist, coef, (int)E);
+  TTA_CHECK_LAUNCH("tta_edge_wigner");
+  return tta::kOk;
+}
+
+extern "C" int tta_edge_features(const float* dist, const int* zsrc, const int* ztgt,
+                                 const float* src_emb, const float* tgt_emb,
+                                 const float* offsets, float coeff, float cutoff, int64_t nb,
+                                 int64_t ec, float* x_edge, float* env, int64_t E,
+                                 hipStream_t stream) {
+  TTA_CHECK_ARG(E >= 0 && E < (1ll << 31) && nb > 0 && ec >= 0, "tta_edge_features: bad sizes");
+  if (E == 0) return tta::kOk;
+  TTA_CHECK_ARG(dist && offsets && x_edge && env && (ec == 0 || (zsrc && ztgt && src_emb && tgt_emb)),
+                "tta_edge_features: null pointer");
+  const int64_t total = E * (nb + 2 * ec);
+  hipLaunchKernelGGL(k_edge_features, dim3(tta_blocks(total, 256)), dim3(256), 0, stream, dist,
+                     zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, (int)nb, (int)ec,
+                     x_edge, env, (int)E);
+  TTA_CHECK_LAUNCH("tta_edge_features");
+  return tta::kOk;
+}
+
+extern "C" int tta_edge_geometry_bwd(const float* ev, const float* dist, const float* g_coef,
+                                     const float* g_env, const float* g_gauss, int64_t ldg,
+                                     const float* offsets, float coeff, float cutoff, int64_t nb,
+                                     const float* jd, float gamma, float* g_ev, int64_t E,
+                                     hipStream_t stream) {
+  TTA_CHECK_ARG(E >= 0 && E < (1ll << 31), "tta_edge_geometry_bwd: bad sizes");
+  if (E == 0) return tta::kOk;
+  TTA_CHECK_ARG(ev && dist && jd && g_ev, "tta_edge_geometry_bwd: null pointer");
+  TTA_CHECK_ARG(!g_gauss || (offsets && ldg >= nb), "tta_edge_geometry_bwd: bad gaussian adjoint");
+  hipLaunchKernelGGL(k_edge_geometry_bwd, dim3(tta_blocks(E, 256)), dim3(256), 0, stream, ev, dist,
+                     g_coef, g_env, g_gauss, ldg, offsets, coeff, cutoff, (int)nb, jd, gamma, g_ev,
+                     (int)E);
+  TTA_CHECK_LAUNCH("tta_edge_geometry_bwd");
+  return tta::kOk;
+}
+
+extern "C" int tta_node_forces(const float* g_ev, const int* src_ptr, const int* src_perm,
+                               const int* tgt_ptr, float* forces, int64_t N, int64_t E,
+                               hipStream_t stream) {
+  TTA_CHECK_ARG(N >= 0 && N < (1ll << 31) && E >= 0, "tta_node_forces: bad sizes");
+  if (N == 0) return tta::kOk;
+  TTA_CHECK_ARG(src_ptr && src_perm && tgt_ptr && forces && (g_ev || E == 0),
+                "tta_node_forces: null pointer");
+  hipLaunchKernelGGL(k_node_forces, dim3(tta_blocks(N, 256)), dim3(256), 0, stream, g_ev, src_ptr,
+                     src_perm, tgt_ptr, forces, (int)N);
+  TTA_CHECK_LAUNCH("tta_node_forces");
+  return tta::kOk;
+}
+
+// `work` must hold 256 * 9 floats.
+extern "C" int tta_virial(const float* ev, const float* g_ev, int64_t E, float* work, float* out,
+                          hipStream_t stream) {
+  TTA_CHECK_ARG(E >= 0 && E < (1ll << 31), "tta_virial: bad sizes");
+  TTA_CHECK_ARG(work && out && ((ev && g_ev) || E == 0), "tta_virial: null pointer");
+  hipLaunchKernelGGL(k_virial_partial, dim3(kVirBlocks), dim3(256), 0, stream, ev, g_ev, (int)E,
+                     work);
+  hipLaunchKernelGGL(k_virial_final, dim3(1), dim3(64), 0, stream, work, kVirBlocks, out);
+  TTA_CHECK_LAUNCH("tta_virial");
+  return tta::kOk;
+}

@@ -1,0 +1,370 @@
+// Row-wise and element-wise kernels of the eSCN-MD path: the gate activation (m-primed for the
+// SO(2) block, natural order for the spectral feed-forward), the radial MLP's fused
+// LayerNorm+SiLU forward/backward, the equivariant RMS norm over SH coefficients and small
+// deterministic reductions.
+#include "common.h"
+
+namespace {
+
+struct GateIdx {
+  int v[8];  // gate row per vector coefficient 1..8
+};
+
+// GateActivation (activation.py:29-70, spectral.py:129-144):
+//   y[r, 0, h] = silu(x[r, 0, h]);  y[r, c, h] = x[r, c, h] * sigmoid(gating[r, idx[c-1] * H + h])
+__global__ __launch_bounds__(256) void k_gate_fwd(const float* __restrict__ x,
+                                                  const float* __restrict__ gating,
+                                                  float* __restrict__ y, int64_t R, int H, int L,
+                                                  GateIdx idx) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= R * H) return;
+  const int64_t r = gid / H;
+  const int h = (int)(gid % H);
+  const float* xr = x + r * 9 * H;
+  float* yr = y + r * 9 * H;
+  float sg[8];
+  for (int t = 0; t < L; ++t) sg[t] = tta_sigmoid_acc(gating[r * L * H + t * H + h]);
+  yr[h] = tta_silu(xr[h]);
+#pragma unroll
+  for (int c = 1; c < 9; ++c) yr[c * H + h] = xr[c * H + h] * sg[idx.v[c - 1]];
+}
+
+// Backward (forces.py:104-130): g_x and g_gating = sigmoid'(gating) * sum_c g_y[c] x[c].
+__global__ __launch_bounds__(256) void k_gate_bwd(const float* __restrict__ g_y,
+                                                  const float* __restrict__ x,
+                                                  const float* __restrict__ gating,
+                                                  float* __restrict__ g_x,
+                                                  float* __restrict__ g_gating, int64_t R, int H,
+                                                  int L, GateIdx idx) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= R * H) return;
+  const int64_t r = gid / H;
+  const int h = (int)(gid % H);
+  const float* xr = x + r * 9 * H;
+  const float* gr = g_y + r * 9 * H;
+  float* gx = g_x + r * 9 * H;
+  float sg[8], acc[8];
+  for (int t = 0; t < L; ++t) {
+    sg[t] = tta_sigmoid_acc(gating[r * L * H + t * H + h]);
+    acc[t] = 0.f;
+  }
+  gx[h] = gr[h] * tta_silu_grad(xr[h]);
+#pragma unroll
+  for (int c = 1; c < 9; ++c) {
+    const int t = idx.v[c - 1];
+    const float g = gr[c * H + h];
+    gx[c * H + h] = g * sg[t];
+    acc[t] += g * xr[c * H + h];
+  }
+  for (int t = 0; t < L; ++t) g_gating[r * L * H + t * H + h] = acc[t] * (sg[t] * (1.f - sg[t]));
+}
+
+// ------------------------------------------------------------------ LayerNorm + SiLU (radial MLP)
+// One wave per row.  Forward (so2.py:101-115 / geometry.py:161-168):
+//   nrm = (a - mean) * rstd * gamma + beta,  s = silu(nrm)
+__global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a,
+                                                     const float* __restrict__ gamma,
+                                                     const float* __restrict__ beta,
+                                                     float* __restrict__ nrm,
+                                                     float* __restrict__ s, int64_t R, int n,
+                                                     float eps) {
+  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (row >= R) return;
+  const float* ar = a + row * n;
+  float sum = 0.f;
+  for (int i = lane; i < n; i += 64) sum += ar[i];
+  const float mean = tta_group_sum(sum, 64) / n;
+  float sq = 0.f;
+  for (int i = lane; i < n; i += 64) {
+    const float d = ar[i] - mean;
+    sq += d * d;
+  }
+  const float var = tta_group_sum(sq, 64) / n;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  for (int i = lane; i < n; i += 64) {
+    const float v = (ar[i] - mean) * rstd * gamma[i] + beta[i];
+    nrm[row * n + i] = v;
+    s[row * n + i] = tta_silu(v);
+  }
+}
+
+// Backward of silu(layer_norm(a)) w.r.t. a (so2.py:117-143):
+//   gy = g * silu'(nrm) * gamma;  xhat = (a - mean) * rstd;
+//   g_a = rstd * (gy - mean(gy) - xhat * mean(gy * xhat))
+__global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g,
+                                                     const float* __restrict__ a,
+                                                     const float* __restrict__ nrm,
+                                                     const float* __restrict__ gamma,
+                                                     float* __restrict__ g_a, int64_t R, int n,
+                                                     float eps) {
+  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (row >= R) return;
+  const float* ar = a + row * n;
+  float sum = 0.f;
+  for (int i = lane; i < n; i += 64) sum += ar[i];
+  const float mean = tta_group_sum(sum, 64) / n;
+  float sq = 0.f;
+  for (int i = lane; i < n; i += 64) {
+    const float d = ar[i] - mean;
+    sq += d * d;
+  }
+  const float rstd = 1.0f / sqrtf(tta_group_sum(sq, 64) / n + eps);
+  float m1 = 0.f, m2 = 0.f;
+  for (int i = lane; i < n; i += 64) {
+    const float gy = g[row * n + i] * tta_silu_grad(nrm[row * n + i]) * gamma[i];
+    const float xh = (ar[i] - mean) * rstd;
+    m1 += gy;
+    m2 += gy * xh;
+  }
+  m1 = tta_group_sum(m1, 64) / n;
+  m2 = tta_group_sum(m2, 64) / n;
+  for (int i = lane; i < n; i += 64) {
+    const float gy = g[row * n + i] * tta_silu_grad(nrm[row * n + i]) * gamma[i];
+    const float xh = (ar[i] - mean) * rstd;
+    g_a[row * n + i] = rstd * (gy - m1 - xh * m2);
+  }
+}
+
+// ------------------------------------------------------------------ RMSNormSH (lmax = 2)
+__device__ __forceinline__ int deg_of(int j) { return j == 0 ? 0 : (j < 4 ? 1 : 2); }
+__device__ __forceinline__ float bdw_of(int j) {
+  // 1 / (2l+1) / (lmax+1), rounded from double as the reference's torch.tensor([...]) does
+  const int l = deg_of(j);
+  return (float)(1.0 / (2 * l + 1) / 3.0);
+}
+
+// norm.py:59-111 / mirror.py:64-75: center coefficient 0 over channels; ms = mean_c(sum_j
+// bdw_j xc_j^2); inv = rsqrt(ms + eps); y = xc * (inv * aw[l(j)]); y[0] += ab (+ add0).
+// One wave per node; inv[n] is kept for the backward.
+__global__ __launch_bounds__(256) void k_rmsnorm_sh_fwd(const float* __restrict__ x,
+                                                        const float* __restrict__ aw,
+                                                        const float* __restrict__ ab,
+                                                        const float* __restrict__ add0,
+                                                        float* __restrict__ y,
+                                                        float* __restrict__ inv_out, int64_t N,
+                                                        int C, float eps) {
+  const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;
+  const float* xn = x + n * 9 * C;
+  float s0 = 0.f;
+  for (int c = lane; c < C; c += 64) s0 += xn[c];
+  const float mu = tta_group_sum(s0, 64) / C;
+  float ms = 0.f;
+  for (int c = lane; c < C; c += 64) {
+    float sc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      const float v = j == 0 ? xn[c] - mu : xn[j * C + c];
+      sc += v * v * bdw_of(j);
+    }
+    ms += sc;
+  }
+  ms = tta_group_sum(ms, 64) / C;
+  const float inv = 1.0f / sqrtf(ms + eps);
+  if (lane == 0 && inv_out) inv_out[n] = inv;
+  float* yn = y + n * 9 * C;
+  for (int c = lane; c < C; c += 64) {
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      const float v = j == 0 ? xn[c] - mu : xn[j * C + c];
+      float o = v * (inv * aw[deg_of(j) * C + c]);
+      if (j == 0) {
+        o = o + ab[c];
+        if (add0) o = o + add0[n * C + c];
+      }
+      yn[j * C + c] = o;
+    }
+  }
+}
+
+// forces.py:73-98 (VJP of RMSNormSH) + optional residual adjoint: out = g_x + res.
+__global__ __launch_bounds__(256) void k_rmsnorm_sh_bwd(const float* __restrict__ g,
+                                                        const float* __restrict__ x,
+                                                        const float* __restrict__ aw,
+                                                        const float* __restrict__ inv_in,
+                                                        const float* __restrict__ res,
+                                                        float* __restrict__ out, int64_t N,
+                                                        int C) {
+  const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;
+  const float* xn = x + n * 9 * C;
+  const float* gn = g + n * 9 * C;
+  const float inv = inv_in[n];
+  float s0 = 0.f;
+  for (int c = lane; c < C; c += 64) s0 += xn[c];
+  const float mu = tta_group_sum(s0, 64) / C;
+  float ginv = 0.f;
+  for (int c = lane; c < C; c += 64) {
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      const float v = j == 0 ? xn[c] - mu : xn[j * C + c];
+      ginv += gn[j * C + c] * v * aw[deg_of(j) * C + c];
+    }
+  }
+  ginv = tta_group_sum(ginv, 64);
+  const float gms = ginv * (inv * inv * inv) * -0.5f;
+  // l0 centering backward needs mean_c of g_xc[0]
+  float s1 = 0.f;
+  for (int c = lane; c < C; c += 64) {
+    const float v = xn[c] - mu;
+    s1 += gn[c] * (inv * aw[c]) + v * bdw_of(0) * gms * (2.0f / C);
+  }
+  const float m0 = tta_group_sum(s1, 64) / C;
+  float* on = out + n * 9 * C;
+  for (int c = lane; c < C; c += 64) {
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      const float v = j == 0 ? xn[c] - mu : xn[j * C + c];
+      float gx = gn[j * C + c] * (inv * aw[deg_of(j) * C + c]) + v * bdw_of(j) * gms * (2.0f / C);
+      if (j == 0) gx -= m0;
+      if (res) gx += res[n * 9 * C + j * C + c];
+      on[j * C + c] = gx;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ elementwise / reductions
+__global__ __launch_bounds__(256) void k_silu_bwd(const float* __restrict__ g,
+                                                  const float* __restrict__ x,
+                                                  float* __restrict__ out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = g[i] * tta_silu_grad(x[i]);
+}
+
+// Deterministic sum of n values with stride `stride` (single block, fixed order tree).
+__global__ __launch_bounds__(1024) void k_sum(const float* __restrict__ x, int64_t n,
+                                              int64_t stride, float* __restrict__ out) {
+  __shared__ float part[16];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) s += x[i * stride];
+  s = tta_group_sum(s, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    float v = threadIdx.x < 16 ? part[threadIdx.x] : 0.f;
+    v = tta_group_sum(v, 64);
+    if (threadIdx.x == 0) out[0] = v;
+  }
+}
+
+// out[r, c] = value for all c in [0, n): used to seed the energy adjoint with ones.
+__global__ __launch_bounds__(256) void k_fill(float* __restrict__ out, int64_t n, float value) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = value;
+}
+
+}  // namespace
+
+extern "C" int tta_gate_fwd(const float* x, const float* gating, float* y, int64_t R, int64_t H,
+                            int64_t L, const int* idx8, hipStream_t stream) {
+  TTA_CHECK_ARG(R >= 0 && H > 0 && L >= 1 && L <= 8, "tta_gate_fwd: bad sizes");
+  TTA_CHECK_ARG(idx8, "tta_gate_fwd: null index table");
+  GateIdx gi;
+  for (int i = 0; i < 8; ++i) {
+    TTA_CHECK_ARG(idx8[i] >= 0 && idx8[i] < L, "tta_gate_fwd: gate index out of range");
+    gi.v[i] = idx8[i];
+  }
+  if (R == 0) return tta::kOk;
+  TTA_CHECK_ARG(x && gating && y, "tta_gate_fwd: null pointer");
+  hipLaunchKernelGGL(k_gate_fwd, dim3(tta_blocks(R * H, 256)), dim3(256), 0, stream, x, gating, y,
+                     R, (int)H, (int)L, gi);
+  TTA_CHECK_LAUNCH("tta_gate_fwd");
+  return tta::kOk;
+}
+
+extern "C" int tta_gate_bwd(const float* g_y, const float* x, const float* gating, float* g_x,
+                            float* g_gating, int64_t R, int64_t H, int64_t L, const int* idx8,
+                            hipStream_t stream) {
+  TTA_CHECK_ARG(R >= 0 && H > 0 && L >= 1 && L <= 8, "tta_gate_bwd: bad sizes");
+  TTA_CHECK_ARG(idx8, "tta_gate_bwd: null index table");
+  GateIdx gi;
+  for (int i = 0; i < 8; ++i) {
+    TTA_CHECK_ARG(idx8[i] >= 0 && idx8[i] < L, "tta_gate_bwd: gate index out of range");
+    gi.v[i] = idx8[i];
+  }
+  if (R == 0) return tta::kOk;
+  TTA_CHECK_ARG(g_y && x && gating && g_x && g_gating, "tta_gate_bwd: null pointer");
+  hipLaunchKernelGGL(k_gate_bwd, dim3(tta_blocks(R * H, 256)), dim3(256), 0, stream, g_y, x,
+                     gating, g_x, g_gating, R, (int)H, (int)L, gi);
+  TTA_CHECK_LAUNCH("tta_gate_bwd");
+  return tta::kOk;
+}
+
+extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* beta, float* nrm,
+                               float* s, int64_t R, int64_t n, float eps, hipStream_t stream) {
+  TTA_CHECK_ARG(R >= 0 && n > 0, "tta_ln_silu_fwd: bad sizes");
+  if (R == 0) return tta::kOk;
+  TTA_CHECK_ARG(a && gamma && beta && nrm && s, "tta_ln_silu_fwd: null pointer");
+  hipLaunchKernelGGL(k_ln_silu_fwd, dim3(tta_blocks(R * 64, 256)), dim3(256), 0, stream, a, gamma,
+                     beta, nrm, s, R, (int)n, eps);
+  TTA_CHECK_LAUNCH("tta_ln_silu_fwd");
+  return tta::kOk;
+}
+
+extern "C" int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm,
+                               const float* gamma, float* g_a, int64_t R, int64_t n, float eps,
+                               hipStream_t stream) {
+  TTA_CHECK_ARG(R >= 0 && n > 0, "tta_ln_silu_bwd: bad sizes");
+  if (R == 0) return tta::kOk;
+  TTA_CHECK_ARG(g && a && nrm && gamma && g_a, "tta_ln_silu_bwd: null pointer");
+  hipLaunchKernelGGL(k_ln_silu_bwd, dim3(tta_blocks(R * 64, 256)), dim3(256), 0, stream, g, a, nrm,
+                     gamma, g_a, R, (int)n, eps);
+  TTA_CHECK_LAUNCH("tta_ln_silu_bwd");
+  return tta::kOk;
+}
+
+extern "C" int tta_rmsnorm_sh_fwd(const float* x, const float* aw, const float* ab,
+                                  const float* add0, float* y, float* inv, int64_t N, int64_t C,
+                                  float eps, hipStream_t stream) {
+  TTA_CHECK_ARG(N >= 0 && C > 0, "tta_rmsnorm_sh_fwd: bad sizes");
+  if (N == 0) return tta::kOk;
+  TTA_CHECK_ARG(x && aw && ab && y, "tta_rmsnorm_sh_fwd: null pointer");
+  hipLaunchKernelGGL(k_rmsnorm_sh_fwd, dim3(tta_blocks(N * 64, 256)), dim3(256), 0, stream, x, aw,
+                     ab, add0, y, inv, N, (int)C, eps);
+  TTA_CHECK_LAUNCH("tta_rmsnorm_sh_fwd");
+  return tta::kOk;
+}
+
+extern "C" int tta_rmsnorm_sh_bwd(const float* g, const float* x, const float* aw,
+                                  const float* inv, const float* res, float* out, int64_t N,
+                                  int64_t C, hipStream_t stream) {
+  TTA_CHECK_ARG(N >= 0 && C > 0, "tta_rmsnorm_sh_bwd: bad sizes");
+  if (N == 0) return tta::kOk;
+  TTA_CHECK_ARG(g && x && aw && inv && out, "tta_rmsnorm_sh_bwd: null pointer");
+  hipLaunchKernelGGL(k_rmsnorm_sh_bwd, dim3(tta_blocks(N * 64, 256)), dim3(256), 0, stream, g, x,
+                     aw, inv, res, out, N, (int)C);
+  TTA_CHECK_LAUNCH("tta_rmsnorm_sh_bwd");
+  return tta::kOk;
+}
+
+extern "C" int tta_silu_bwd(const float* g, const float* x, float* out, int64_t n,
+                            hipStream_t stream) {
+  TTA_CHECK_ARG(n >= 0, "tta_silu_bwd: bad size");
+  if (n == 0) return tta::kOk;
+  TTA_CHECK_ARG(g && x && out, "tta_silu_bwd: null pointer");
+  hipLaunchKernelGGL(k_silu_bwd, dim3(tta_blocks(n, 256)), dim3(256), 0, stream, g, x, out, n);
+  TTA_CHECK_LAUNCH("tta_silu_bwd");
+  return tta::kOk;
+}
+
+extern "C" int tta_sum(const float* x, int64_t n, int64_t stride, float* out,
+                       hipStream_t stream) {
+  TTA_CHECK_ARG(n >= 0 && stride >= 1, "tta_sum: bad size");
+  TTA_CHECK_ARG(out && (x || n == 0), "tta_sum: null pointer");
+  hipLaunchKernelGGL(k_sum, dim3(1), dim3(1024), 0, stream, x, n, stride, out);
+  TTA_CHECK_LAUNCH("tta_sum");
+  return tta::kOk;
+}
+
+extern "C" int tta_fill(float* out, int64_t n, float value, hipStream_t stream) {
+  TTA_CHECK_ARG(n >= 0, "tta_fill: bad size");
+  if (n == 0) return tta::kOk;
+  TTA_CHECK_ARG(out, "tta_fill: null pointer");
+  hipLaunchKernelGGL(k_fill, dim3(tta_blocks(n, 256)), dim3(256), 0, stream, out, n, value);
+  TTA_CHECK_LAUNCH("tta_fill");
+  return tta::kOk;
+}

@@ -1,0 +1,311 @@
+"""ctypes boundary to ``libttatom_hip.so`` (the C ABI declared in ``include/tt_atom_hip.h``).
+
+Every wrapper takes torch tensors that live on the current HIP device, checks dtype / size /
+contiguity on the host, passes raw device pointers plus the current torch stream, and raises
+``RuntimeError`` with the library's message on a non-zero status.  There is no fallback: if
+the library is missing or the device is not a gfx950 the call fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+
+import torch
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libttatom_hip.so"
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> argtypes (all return int status unless listed in _RESTYPE)
+_SIGS = {
+    "tta_version": [],
+    "tta_last_error": [],
+    "tta_check_device": [ctypes.c_char_p, _I64],
+    "tta_gemm_f32": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                     _I64, _I64, _I64, _I, _P],
+    "tta_gather_rotate": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "tta_gather_rotate_bw": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "tta_rotate_env_segsum": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _F, _P],
+    "tta_rotate_env_segsum_bw": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _F,
+                                 _P],
+    "tta_node_gather_sum": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "tta_gate_fwd": [_P, _P, _P, _I64, _I64, _I64, _P, _P],
+    "tta_gate_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P],
+    "tta_ln_silu_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _F, _P],
+    "tta_ln_silu_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _F, _P],
+    "tta_rmsnorm_sh_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _P],
+    "tta_rmsnorm_sh_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _P],
+    "tta_silu_bwd": [_P, _P, _P, _I64, _P],
+    "tta_sum": [_P, _I64, _I64, _P, _P],
+    "tta_fill": [_P, _I64, _F, _P],
+    "tta_edge_wigner": [_P, _P, _P, _P, _P, _F, _P, _P, _P, _I64, _I64, _P],
+    "tta_edge_features": [_P, _P, _P, _P, _P, _P, _F, _F, _I64, _I64, _P, _P, _I64, _P],
+    "tta_edge_geometry_bwd": [_P, _P, _P, _P, _P, _I64, _P, _F, _F, _I64, _P, _F, _P, _I64, _P],
+    "tta_node_forces": [_P, _P, _P, _P, _P, _I64, _I64, _P],
+    "tta_virial": [_P, _P, _I64, _P, _P, _P],
+}
+_RESTYPE = {"tta_last_error": ctypes.c_char_p}
+
+EXPORTS = tuple(_SIGS)
+
+_lib = None
+
+
+def load(require_device=True):
+    """Load the library (once).  torch's HIP runtime is initialised first so the library binds to
+    that already-loaded runtime (same SONAME) and torch streams are valid handles for it."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python __graft_entry__.py` "
+                           "(build()) or `make -C tt-atom_amd/csrc`")
+    if require_device:
+        if not torch.cuda.is_available():
+            raise RuntimeError("tt_atom (MI355X build) needs a HIP device; none is visible")
+        torch.cuda.init()
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, args in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPE.get(name, ctypes.c_int)
+    if require_device:
+        buf = ctypes.create_string_buffer(64)
+        if lib.tta_check_device(buf, 64) != 0:
+            raise RuntimeError(lib.tta_last_error().decode())
+    _lib = lib
+    return lib
+
+
+def load_symbols_only():
+    """Load without touching a device (CPU tests: symbol / ABI checks only)."""
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, args in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPE.get(name, ctypes.c_int)
+    return lib
+
+
+def _call(name, *args):
+    lib = load()
+    st = getattr(lib, name)(*args)
+    if st != 0:
+        raise RuntimeError(f"{name}: {lib.tta_last_error().decode()}")
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t, dtype=torch.float32, numel=None, name="tensor", contiguous=True):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype}, got {t.dtype}")
+    if contiguous and not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+    if numel is not None and t.numel() != numel:
+        raise RuntimeError(f"{name} has {t.numel()} elements, expected {numel}")
+    return t.data_ptr()
+
+
+def _i32(t, numel=None, name="index"):
+    return _ptr(t, torch.int32, numel, name)
+
+
+# ----------------------------------------------------------------------------- GEMM
+EPI_STORE, EPI_SILU, EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD = 0, 1, 2, 3, 4
+
+
+def gemm(A, B, C, *, M, N, K, lda, ldb, ldc, bias=None, epilogue=EPI_STORE, C2=None, aux=None,
+         batch=1, sA=0, sB=0, sC=0, sBias=0):
+    """C = epi(A @ B + bias) on raw strided views (A/B/C are base tensors; offsets are applied
+    by the caller through ``narrow``/slicing of contiguous storage -> data_ptr)."""
+    for t, nm in ((A, "A"), (B, "B"), (C, "C")):
+        if not t.is_cuda or t.dtype != torch.float32:
+            raise RuntimeError(f"gemm: {nm} must be an fp32 device tensor")
+    _call("tta_gemm_f32", A.data_ptr(), B.data_ptr(), C.data_ptr(),
+          None if bias is None else bias.data_ptr(), None if C2 is None else C2.data_ptr(),
+          None if aux is None else aux.data_ptr(), M, N, K, lda, ldb, ldc, batch, sA, sB, sC,
+          sBias, epilogue, _stream())
+
+
+def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None):
+    """y = x @ w_t (+ bias) for 2-D row-major x [M, K] (any row stride) and w_t [K, N]."""
+    M, K = x.shape
+    K2, N = w_t.shape
+    if K != K2:
+        raise RuntimeError(f"linear: inner dims {K} vs {K2}")
+    if out is None:
+        out = torch.empty(M, N, device=x.device, dtype=torch.float32)
+    gemm(x, w_t, out, M=M, N=N, K=K, lda=_ld(x, "x"), ldb=_ld(w_t, "w_t"), ldc=_ld(out, "out"),
+         bias=bias, epilogue=epilogue, C2=out2, aux=aux)
+    return out
+
+
+def _ld(t, name):
+    """Leading dimension of a row-major 2-D view (strides of size-1 dims do not matter)."""
+    if t.dim() != 2:
+        raise RuntimeError(f"linear: {name} must be 2-D")
+    if t.shape[1] > 1 and t.stride(1) != 1:
+        raise RuntimeError(f"linear: {name} must be row-major")
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+
+
+# ----------------------------------------------------------------------------- rotation
+def gather_rotate(x, src, tgt, coef, rad, out):
+    N, nsph, C = x.shape
+    E = src.numel()
+    _call("tta_gather_rotate", _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E), _i32(tgt, E),
+          _ptr(coef, numel=E * 35, name="coef"), _ptr(rad, numel=E * 12 * C, name="rad"),
+          _ptr(out, numel=E * 18 * C, name="out"), N, E, C, _stream())
+    return out
+
+
+def gather_rotate_bw(g_xf, rad, x, src, tgt, coef, g_rad, g_mcat, g_coef):
+    N, _, C = x.shape
+    E = src.numel()
+    _call("tta_gather_rotate_bw", _ptr(g_xf, numel=E * 18 * C, name="g_xf"),
+          _ptr(rad, numel=E * 12 * C, name="rad"), _ptr(x, numel=N * 9 * C, name="x"),
+          _i32(src, E), _i32(tgt, E), _ptr(coef, numel=E * 35, name="coef"),
+          _ptr(g_rad, numel=E * 12 * C, name="g_rad"), _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
+          _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream())
+
+
+def rotate_env_segsum(m, coef, env, tgt_ptr, res, out, *, n_in, env_first, div=1.0):
+    N, _, C = out.shape
+    E = coef.shape[0]
+    _call("tta_rotate_env_segsum", _ptr(m, numel=E * n_in * C, name="m"),
+          _ptr(coef, numel=E * 35, name="coef"), _ptr(env, numel=E, name="env"),
+          _i32(tgt_ptr, N + 1, "tgt_ptr"), _ptr(res, numel=N * 9 * C, name="res"),
+          _ptr(out, numel=N * 9 * C, name="out"), N, E, C, n_in, int(env_first), float(div),
+          _stream())
+    return out
+
+
+def rotate_env_segsum_bw(g_node, tgt, m, coef, env, g_m, g_coef, g_env, *, n_in, env_first,
+                         div=1.0):
+    N, _, C = g_node.shape
+    E = tgt.numel()
+    _call("tta_rotate_env_segsum_bw", _ptr(g_node, numel=N * 9 * C, name="g_node"), _i32(tgt, E),
+          _ptr(m, numel=E * n_in * C, name="m"), _ptr(coef, numel=E * 35, name="coef"),
+          _ptr(env, numel=E, name="env"), _ptr(g_m, numel=E * n_in * C, name="g_m"),
+          _ptr(g_coef, numel=E * 35, name="g_coef"), _ptr(g_env, numel=E, name="g_env"), N, E, C,
+          n_in, int(env_first), float(div), _stream())
+
+
+def node_gather_sum(g_mcat, src_ptr, src_perm, tgt_ptr, res, out):
+    N, _, C = out.shape
+    E = src_perm.numel()
+    _call("tta_node_gather_sum", _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
+          _i32(src_ptr, N + 1, "src_ptr"), _i32(src_perm, E, "src_perm"),
+          _i32(tgt_ptr, N + 1, "tgt_ptr"), _ptr(res, numel=N * 9 * C, name="res"),
+          _ptr(out, numel=N * 9 * C, name="out"), N, E, C, _stream())
+    return out
+
+
+# ----------------------------------------------------------------------------- row-wise
+def gate_fwd(x, gating, y, idx8):
+    R = x.shape[0]
+    H = x.numel() // (9 * R) if R else 0
+    L = gating.shape[1] // H if R else 1
+    _call("tta_gate_fwd", _ptr(x, name="x"), _ptr(gating, numel=R * L * H, name="gating"),
+          _ptr(y, numel=R * 9 * H, name="y"), R, H, L, _i32(idx8, 8, "idx8"), _stream())
+    return y
+
+
+def gate_bwd(g_y, x, gating, g_x, g_gating, idx8):
+    R = x.shape[0]
+    H = x.numel() // (9 * R) if R else 0
+    L = gating.shape[1] // H if R else 1
+    _call("tta_gate_bwd", _ptr(g_y, numel=R * 9 * H, name="g_y"), _ptr(x, name="x"),
+          _ptr(gating, numel=R * L * H, name="gating"), _ptr(g_x, numel=R * 9 * H, name="g_x"),
+          _ptr(g_gating, numel=R * L * H, name="g_gating"), R, H, L, _i32(idx8, 8, "idx8"),
+          _stream())
+
+
+def ln_silu_fwd(a, gamma, beta, nrm, s, eps=1e-5):
+    R, n = a.shape
+    _call("tta_ln_silu_fwd", _ptr(a, name="a"), _ptr(gamma, numel=n), _ptr(beta, numel=n),
+          _ptr(nrm, numel=R * n), _ptr(s, numel=R * n), R, n, eps, _stream())
+
+
+def ln_silu_bwd(g, a, nrm, gamma, g_a, eps=1e-5):
+    R, n = a.shape
+    _call("tta_ln_silu_bwd", _ptr(g, numel=R * n, name="g"), _ptr(a, name="a"),
+          _ptr(nrm, numel=R * n), _ptr(gamma, numel=n), _ptr(g_a, numel=R * n), R, n, eps,
+          _stream())
+
+
+def rmsnorm_sh_fwd(x, aw, ab, add0, y, inv, eps=1e-5):
+    N, _, C = x.shape
+    _call("tta_rmsnorm_sh_fwd", _ptr(x, numel=N * 9 * C, name="x"), _ptr(aw, numel=3 * C),
+          _ptr(ab, numel=C), _ptr(add0, numel=N * C, name="add0"), _ptr(y, numel=N * 9 * C),
+          _ptr(inv, numel=N, name="inv"), N, C, eps, _stream())
+
+
+def rmsnorm_sh_bwd(g, x, aw, inv, res, out):
+    N, _, C = x.shape
+    _call("tta_rmsnorm_sh_bwd", _ptr(g, numel=N * 9 * C, name="g"), _ptr(x, numel=N * 9 * C),
+          _ptr(aw, numel=3 * C), _ptr(inv, numel=N), _ptr(res, numel=N * 9 * C, name="res"),
+          _ptr(out, numel=N * 9 * C), N, C, _stream())
+
+
+def silu_bwd(g, x, out):
+    n = g.numel()
+    _call("tta_silu_bwd", _ptr(g, numel=n), _ptr(x, numel=n), _ptr(out, numel=n), n, _stream())
+
+
+def reduce_sum(x, n, stride, out):
+    _call("tta_sum", x.data_ptr(), n, stride, _ptr(out, numel=1), _stream())
+
+
+def fill(out, value):
+    _call("tta_fill", _ptr(out), out.numel(), float(value), _stream())
+
+
+# ----------------------------------------------------------------------------- geometry
+def edge_wigner(pos, src, tgt, shift, jd, gamma, ev, dist, coef):
+    N = pos.shape[0]
+    E = src.numel()
+    _call("tta_edge_wigner", _ptr(pos, numel=N * 3, name="pos"), _i32(src, E), _i32(tgt, E),
+          _ptr(shift, numel=E * 3, name="shift"), _ptr(jd, numel=35, name="jd"), float(gamma),
+          _ptr(ev, numel=E * 3), _ptr(dist, numel=E), _ptr(coef, numel=E * 35), N, E, _stream())
+
+
+def edge_features(dist, zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, nb, ec, x_edge, env):
+    E = dist.numel()
+    _call("tta_edge_features", _ptr(dist, numel=E), _i32(zsrc, E), _i32(ztgt, E),
+          _ptr(src_emb, name="src_emb"), _ptr(tgt_emb, name="tgt_emb"),
+          _ptr(offsets, numel=nb, name="offsets"), float(coeff), float(cutoff), nb, ec,
+          _ptr(x_edge, numel=E * (nb + 2 * ec), name="x_edge"), _ptr(env, numel=E), E, _stream())
+
+
+def edge_geometry_bwd(ev, dist, g_coef, g_env, g_gauss, ldg, offsets, coeff, cutoff, nb, jd,
+                      gamma, g_ev):
+    E = dist.numel()
+    _call("tta_edge_geometry_bwd", _ptr(ev, numel=E * 3), _ptr(dist, numel=E),
+          _ptr(g_coef, numel=E * 35, name="g_coef"), _ptr(g_env, numel=E, name="g_env"),
+          None if g_gauss is None else g_gauss.data_ptr(), ldg, _ptr(offsets, name="offsets"),
+          float(coeff), float(cutoff), nb, _ptr(jd, numel=35), float(gamma),
+          _ptr(g_ev, numel=E * 3), E, _stream())
+
+
+def node_forces(g_ev, src_ptr, src_perm, tgt_ptr, forces):
+    N = forces.shape[0]
+    E = src_perm.numel()
+    _call("tta_node_forces", _ptr(g_ev, numel=E * 3), _i32(src_ptr, N + 1), _i32(src_perm, E),
+          _i32(tgt_ptr, N + 1), _ptr(forces, numel=N * 3), N, E, _stream())
+
+
+def virial(ev, g_ev, work, out):
+    E = ev.shape[0]
+    _call("tta_virial", _ptr(ev, numel=E * 3), _ptr(g_ev, numel=E * 3), E,
+          _ptr(work, numel=256 * 9, name="work"), _ptr(out, numel=9), _stream())

@@ -1,0 +1,124 @@
+"""Geometry front end: neighbour list, system embedding and the device-side geometric constants.
+
+``radius_graph`` restates the reference's brute-force neighbour list (tt_atom/geometry.py:48-81)
+with the same fp32 comparisons and edge order, plus the optional per-receiver max-neighbour cap
+(builder decision D3).  It runs on the host once per topology, as in the reference.
+``HostGeometry`` keeps the reference class name and constructor (geometry.py:174-207) but holds
+the device constants of the per-step geometry kernels (Wigner ``Jd`` blocks, gaussian basis,
+envelope cutoff); the per-edge terms are computed on the GPU by the step engine.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+from .model import TO_M_PERM, _UNSUPPORTED
+
+
+def csd_embedding(w, charge, spin, sphere_channels=None, dataset="omat"):
+    """System (charge / spin / dataset) embedding -> [nsys, C] (geometry.py:23-45)."""
+    if "charge_embedding.rand_emb.weight" in w:
+        chg = F.embedding(charge.long() + 100, w["charge_embedding.rand_emb.weight"])
+        sp = F.embedding(spin.long(), w["spin_embedding.rand_emb.weight"])
+    else:
+        def enc(x, W, is_spin):
+            xp = x[:, None] * W[None, :] * 2 * math.pi
+            emb = torch.cat([torch.sin(xp), torch.cos(xp)], dim=-1)
+            if is_spin:
+                emb = emb.clone()
+                emb[torch.where(x == 0)[0]] = 0
+            return emb
+        chg = enc(charge.float(), w["charge_embedding.W"], False)
+        sp = enc(spin.float(), w["spin_embedding.W"], True)
+    ds = w[f"dataset_embedding.dataset_emb_dict.{dataset}.weight"][0].expand(charge.shape[0], -1)
+    return F.silu(F.linear(torch.cat([chg, sp, ds], dim=1), w["mix_csd.weight"], w["mix_csd.bias"]))
+
+
+def radius_graph(pos, cutoff, cell=None, pbc=None, max_neighbors=None):
+    """Neighbour list ``(edge_index [2,E] int64, cell_shift [E,3])`` on the host.
+
+    Aperiodic: keep ``0 < |pos_i - pos_j| < cutoff``, src-major order.  Periodic: image cells
+    ``ceil(cutoff * |b_k|)`` per periodic axis, keep ``1e-8 < d^2 <= cutoff^2``, order
+    (tgt, src, cell), ``edge_vec = pos[src] - pos[tgt] + cell_shift``.  With ``max_neighbors``
+    each receiver keeps its nearest sources by ``(d^2, src, cell)`` and the surviving edges keep
+    the uncapped order."""
+    pos = torch.as_tensor(pos, dtype=torch.float32).cpu()
+    periodic = cell is not None and pbc is not None and bool(torch.as_tensor(pbc).any())
+    if not periodic:
+        d = torch.linalg.norm(pos[:, None, :] - pos[None, :, :], dim=-1)
+        mask = (d < cutoff) & (d > 0)
+        src, tgt = torch.where(mask)
+        ei = torch.stack([src, tgt], 0)
+        shift = pos.new_zeros(ei.shape[1], 3)
+    else:
+        cell = torch.as_tensor(cell, dtype=pos.dtype).reshape(3, 3)
+        pbc = torch.as_tensor(pbc, dtype=torch.bool).reshape(-1).expand(3)
+        recip = torch.linalg.inv(cell).transpose(0, 1)
+        reps = [int(math.ceil(float(cutoff * torch.linalg.norm(recip[k])))) if bool(pbc[k]) else 0
+                for k in range(3)]
+        cells = torch.cartesian_prod(*[torch.arange(-r, r + 1, dtype=pos.dtype) for r in reps])
+        shifts = cells.reshape(-1, 3) @ cell
+        ei_parts, sh_parts = [], []
+        # receivers in chunks keep the [chunk, N, cells] displacement tensor bounded
+        chunk = max(1, int(2e7 // max(1, pos.shape[0] * shifts.shape[0])))
+        for i0 in range(0, pos.shape[0], chunk):
+            p = pos[i0:i0 + chunk]
+            disp = p[:, None, None, :] - (pos[None, :, None, :] + shifts[None, None, :, :])
+            d2 = (disp ** 2).sum(-1)
+            mask = (d2 <= cutoff * cutoff) & (d2 > 1e-8)
+            i, j, c = torch.where(mask)
+            ei_parts.append(torch.stack([j, i + i0], 0))
+            sh_parts.append(shifts[c])
+        ei = torch.cat(ei_parts, 1)
+        shift = torch.cat(sh_parts, 0)
+    if max_neighbors is not None and ei.shape[1]:
+        keep = _cap(pos, ei, shift, int(max_neighbors))
+        ei, shift = ei[:, keep], shift[keep]
+    return ei, shift
+
+
+def _cap(pos, ei, shift, k):
+    src, tgt = ei[0], ei[1]
+    ev = pos[src] - pos[tgt] + shift
+    d2 = (ev[:, 0] * ev[:, 0] + ev[:, 1] * ev[:, 1]) + ev[:, 2] * ev[:, 2]
+    E = ei.shape[1]
+    by_tgt = torch.argsort(tgt, stable=True)
+    o2 = torch.argsort(d2[by_tgt], stable=True)
+    o3 = torch.argsort(tgt[by_tgt][o2], stable=True)
+    ranked = by_tgt[o2[o3]]
+    counts = torch.bincount(tgt[ranked], minlength=int(pos.shape[0]))
+    starts = torch.cumsum(counts, 0) - counts
+    rank = torch.arange(E) - starts[tgt[ranked]]
+    keep = torch.zeros(E, dtype=torch.bool)
+    keep[ranked[rank < k]] = True
+    return keep
+
+
+class HostGeometry:
+    """Geometric constants of the step (reference geometry.py:174-207 constructor)."""
+
+    def __init__(self, weights, cfg, to_m, gauss_offset, gauss_coeff, *, gamma=0.0,
+                 coefficient_index=None, device="cuda"):
+        self.lmax = cfg["lmax"]
+        self.mmax = cfg.get("mmax", self.lmax)
+        if self.lmax != 2 or self.mmax != 2 or coefficient_index is not None:
+            raise RuntimeError(_UNSUPPORTED.format(what=f"lmax={self.lmax}, mmax={self.mmax}"))
+        tm = torch.as_tensor(to_m).float()
+        perm = tuple(int(v) for v in tm.abs().argmax(dim=1).tolist())
+        is_perm = bool(((tm == 0) | (tm == 1)).all()) and bool(((tm != 0).sum(1) == 1).all())
+        if not is_perm or perm != TO_M_PERM:
+            raise RuntimeError(_UNSUPPORTED.format(what=f"to_m permutation {perm}"))
+        self.C = cfg["sphere_channels"]
+        self.cutoff = float(cfg["cutoff"])
+        self.gamma = float(gamma)
+        dev = torch.device(device)
+        jd = torch.cat([weights[f"Jd_{l}"].reshape(-1).float() for l in range(3)])
+        if jd.numel() != 35:
+            raise RuntimeError("Jd blocks must be 1x1, 3x3, 5x5")
+        self.jd = jd.to(dev).contiguous()
+        self.offset = torch.as_tensor(gauss_offset).float().reshape(-1).to(dev).contiguous()
+        self.coeff = float(torch.as_tensor(gauss_coeff).reshape(-1)[0])
+        self.n_gauss = self.offset.numel()
+        self.rescale = float(cfg.get("edge_degree_rescale", 5.0))

@@ -1,0 +1,235 @@
+"""eSCN-MD backbone weights and per-topology graph context, laid out for the gfx950 kernels.
+
+``Backbone`` (reference model.py:175-247) uploads the bundle's torch-``Linear``-layout weights
+once, in the forms the HIP GEMMs consume: ``[in, out]`` for the forward and ``[out, in]`` for
+the input-adjoint (no weight gradients are needed for forces), the SO(2) m>0 blocks fused into
+``[[Wa, Wb], [-Wb, Wa]]`` (so2.py:230-253), the SO3_Linear per-degree weights expanded to one
+matrix per coefficient so a batched GEMM covers all nine (spectral.py:90-103).
+
+``GraphContext`` (reference model.py:42-135) holds the fixed-topology device buffers: the
+destination-sorted edge order, the destination CSR, the source CSR permutation and the
+per-edge element indices.  The per-step geometric terms live in the step engine.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+NSPH = 9
+# m-primed gate row per vector coefficient (activation.py:19-26 for lmax = mmax = 2) and the
+# natural-order one of the spectral feed-forward (spectral.py:77-88)
+GATE_IDX_MPRIME = (0, 1, 0, 1, 0, 1, 1, 1)
+GATE_IDX_NATURAL = (0, 0, 0, 1, 1, 1, 1, 1)
+TO_M_PERM = (0, 2, 6, 3, 7, 1, 5, 8, 4)
+
+_UNSUPPORTED = ("this MI355X build runs the uma-s shape (lmax = mmax = 2, permutation to_m); "
+                "got {what}")
+
+
+def _dev(t, device):
+    """Device copy with standard row-major strides (also for size-1 dimensions, whose stride
+    torch otherwise keeps from a transposed source)."""
+    t = t.detach()
+    out = torch.empty(tuple(t.shape), device=device, dtype=torch.float32)
+    out.copy_(t)
+    return out
+
+
+class RadialWeights:
+    """Linear -> LN -> SiLU -> Linear -> LN -> SiLU -> Linear (so2.py:54-163)."""
+
+    def __init__(self, w, prefix, device, n_gauss):
+        g = lambda k: w[f"{prefix}.{k}"]
+        self.k_in = g("net.0.weight").shape[1]
+        self.hidden = g("net.0.weight").shape[0]
+        self.n_out = g("net.6.weight").shape[0]
+        self.w0t = _dev(g("net.0.weight").T, device)
+        self.b0 = _dev(g("net.0.bias"), device)
+        self.ln1w, self.ln1b = _dev(g("net.1.weight"), device), _dev(g("net.1.bias"), device)
+        self.w3t = _dev(g("net.3.weight").T, device)
+        self.b3 = _dev(g("net.3.bias"), device)
+        self.ln4w, self.ln4b = _dev(g("net.4.weight"), device), _dev(g("net.4.bias"), device)
+        self.w6t = _dev(g("net.6.weight").T, device)
+        self.b6 = _dev(g("net.6.bias"), device)
+        # adjoint operands: g @ W for each Linear; only the gaussian columns of net.0 matter for
+        # the force (the element-embedding columns of x_edge do not depend on positions)
+        self.w6 = _dev(g("net.6.weight"), device)
+        self.w3 = _dev(g("net.3.weight"), device)
+        self.w0g = _dev(g("net.0.weight")[:, :n_gauss], device)
+
+
+def _so2_block(wm):
+    """torch weight [2*Hh, K] of one m>0 SO(2) linear -> fused [[Wa, Wb], [-Wb, Wa]] [2K, 2Hh]."""
+    wt = wm.T.float()                 # [K, 2Hh]
+    K, twoHh = wt.shape
+    Hh = twoHh // 2
+    Wa, Wb = wt[:, :Hh], wt[:, Hh:]
+    blk = torch.zeros(2 * K, 2 * Hh)
+    blk[:K, :Hh], blk[:K, Hh:] = Wa, Wb
+    blk[K:, :Hh], blk[K:, Hh:] = -Wb, Wa
+    return blk
+
+
+class SO2Weights:
+    """SO2Convolution (so2.py:166-330) for lmax = mmax = 2."""
+
+    def __init__(self, w, prefix, device, cin, hout, extra, n_gauss):
+        self.cin, self.hout, self.extra = cin, hout, extra
+        wm0 = w[f"{prefix}.fc_m0.weight"]            # [extra + 3 hout, 3 cin]
+        bm0 = w[f"{prefix}.fc_m0.bias"]
+        if wm0.shape != (extra + 3 * hout, 3 * cin):
+            raise RuntimeError(_UNSUPPORTED.format(what=f"fc_m0 {tuple(wm0.shape)}"))
+        self.wg_t = _dev(wm0[:extra].T, device) if extra else None      # -> gating
+        self.bg = _dev(bm0[:extra], device) if extra else None
+        self.wc_t = _dev(wm0[extra:].T, device)                         # -> coefficients 0..2
+        self.bc = _dev(bm0[extra:], device)
+        self.wg = _dev(wm0[:extra], device) if extra else None          # adjoint operands
+        self.wc = _dev(wm0[extra:], device)
+        b1 = _so2_block(w[f"{prefix}.so2_m_conv.0.fc.weight"])          # [4 cin, 4 hout]
+        b2 = _so2_block(w[f"{prefix}.so2_m_conv.1.fc.weight"])          # [2 cin, 2 hout]
+        if b1.shape != (4 * cin, 4 * hout) or b2.shape != (2 * cin, 2 * hout):
+            raise RuntimeError(_UNSUPPORTED.format(what="SO(2) m>0 weight shapes"))
+        self.w1, self.w1_t = _dev(b1, device), _dev(b1.T, device)
+        self.w2, self.w2_t = _dev(b2, device), _dev(b2.T, device)
+        self.rad = (RadialWeights(w, f"{prefix}.rad_func", device, n_gauss)
+                    if f"{prefix}.rad_func.net.0.weight" in w else None)
+
+
+class NormWeights:
+    def __init__(self, w, prefix, device):
+        self.aw = _dev(w[f"{prefix}.affine_weight"], device)   # [lmax+1, C]
+        self.ab = _dev(w[f"{prefix}.affine_bias"], device)     # [C]
+
+
+def _expand_so3(W, device):
+    """SO3_Linear weight [lmax+1, out, in] -> per-coefficient [9, in, out] and [9, out, in]."""
+    deg = [0, 1, 1, 1, 2, 2, 2, 2, 2]
+    fwd = torch.stack([W[l].T for l in deg])
+    bwd = torch.stack([W[l] for l in deg])
+    return _dev(fwd, device), _dev(bwd, device)
+
+
+class SpectralWeights:
+    """SpectralAtomwise (spectral.py:41-188)."""
+
+    def __init__(self, w, prefix, device, C, H):
+        self.ws_t = _dev(w[f"{prefix}.scalar_mlp.0.weight"].T, device)   # [C, L*H]
+        self.bs = _dev(w[f"{prefix}.scalar_mlp.0.bias"], device)
+        self.ws = _dev(w[f"{prefix}.scalar_mlp.0.weight"], device)       # [L*H, C]
+        self.w1_t, self.w1 = _expand_so3(w[f"{prefix}.so3_linear_1.weight"], device)
+        self.w2_t, self.w2 = _expand_so3(w[f"{prefix}.so3_linear_2.weight"], device)
+        b1 = torch.zeros(NSPH, H)
+        b1[0] = w[f"{prefix}.so3_linear_1.bias"]
+        b2 = torch.zeros(NSPH, C)
+        b2[0] = w[f"{prefix}.so3_linear_2.bias"]
+        self.b1, self.b2 = _dev(b1, device), _dev(b2, device)
+
+
+class GridWeights:
+    """GridAtomwise (grid.py:25-76): to_grid / from_grid projections around a channel MLP."""
+
+    def __init__(self, w, prefix, device, to_grid_mat, from_grid_mat):
+        b, a, nsph = to_grid_mat.shape
+        self.npts = b * a
+        tg = to_grid_mat.reshape(self.npts, nsph).float()
+        fg = from_grid_mat.reshape(self.npts, nsph).float()
+        self.tg, self.tg_t = _dev(tg, device), _dev(tg.T, device)      # [P, 9], [9, P]
+        self.fg, self.fg_t = _dev(fg, device), _dev(fg.T, device)
+        self.w0_t = _dev(w[f"{prefix}.grid_mlp.0.weight"].T, device)
+        self.w2_t = _dev(w[f"{prefix}.grid_mlp.2.weight"].T, device)
+        self.w4_t = _dev(w[f"{prefix}.grid_mlp.4.weight"].T, device)
+        self.w0 = _dev(w[f"{prefix}.grid_mlp.0.weight"], device)
+        self.w2 = _dev(w[f"{prefix}.grid_mlp.2.weight"], device)
+        self.w4 = _dev(w[f"{prefix}.grid_mlp.4.weight"], device)
+
+
+class BlockWeights:
+    def __init__(self, w, prefix, device, cfg, to_grid, from_grid, n_gauss):
+        C, H, L = cfg["sphere_channels"], cfg["hidden_channels"], cfg["lmax"]
+        self.norm_1 = NormWeights(w, f"{prefix}.norm_1", device)
+        self.norm_2 = NormWeights(w, f"{prefix}.norm_2", device)
+        self.so2_1 = SO2Weights(w, f"{prefix}.edge_wise.so2_conv_1", device, 2 * C, H, L * H, n_gauss)
+        self.so2_2 = SO2Weights(w, f"{prefix}.edge_wise.so2_conv_2", device, H, C, 0, n_gauss)
+        if self.so2_1.rad is None:
+            raise RuntimeError(_UNSUPPORTED.format(what="so2_conv_1 without a radial MLP"))
+        self.ff_type = cfg.get("ff_type", "grid")
+        if self.ff_type == "spectral":
+            self.atom_wise = SpectralWeights(w, f"{prefix}.atom_wise", device, C, H)
+        else:
+            self.atom_wise = GridWeights(w, f"{prefix}.atom_wise", device, to_grid, from_grid)
+
+
+class Backbone:
+    """eSCN-MD backbone + energy head weights on the device (reference model.py:175-247)."""
+
+    def __init__(self, weights, device, cfg, to_grid_mat=None, from_grid_mat=None, *, fast=False,
+                 n_gauss=None):
+        if fast:
+            raise RuntimeError("fast (reduced-precision) mode is not part of this fp32 build")
+        lmax, mmax = cfg["lmax"], cfg.get("mmax", cfg["lmax"])
+        if lmax != 2 or mmax != 2:
+            raise RuntimeError(_UNSUPPORTED.format(what=f"lmax={lmax}, mmax={mmax}"))
+        self.device = torch.device(device) if device is not None else torch.device("cuda")
+        self.cfg = dict(cfg)
+        self.C, self.H, self.L = cfg["sphere_channels"], cfg["hidden_channels"], lmax
+        if self.C % 4 or self.H % 4:
+            raise RuntimeError(_UNSUPPORTED.format(what="channel counts not a multiple of 4"))
+        nb = n_gauss if n_gauss is not None else cfg["num_distance_basis"]
+        self.n_gauss = nb
+        w = weights
+        dev = self.device
+        self.blocks = [BlockWeights(w, f"blocks.{i}", dev, cfg, to_grid_mat, from_grid_mat, nb)
+                       for i in range(cfg["num_layers"])]
+        self.final_norm = NormWeights(w, "norm", dev)
+        self.edge_degree = RadialWeights(w, "edge_degree_embedding.rad_func", dev, nb)
+        self.sphere_emb = _dev(w["sphere_embedding.weight"], dev)
+        self.src_emb = _dev(w["source_embedding.weight"], dev)
+        self.tgt_emb = _dev(w["target_embedding.weight"], dev)
+        self.edge_channels = w["source_embedding.weight"].shape[1]
+        eb = [w[f"energy_block.{i}.weight"] for i in (0, 2, 4)]
+        self.eh_w_t = [_dev(x.T, dev) for x in eb]
+        self.eh_w = [_dev(x, dev) for x in eb]
+        self.eh_b = [_dev(w[f"energy_block.{i}.bias"], dev) for i in (0, 2, 4)]
+        self.gate_idx_mprime = torch.tensor(GATE_IDX_MPRIME, dtype=torch.int32, device=dev)
+        self.gate_idx_natural = torch.tensor(GATE_IDX_NATURAL, dtype=torch.int32, device=dev)
+
+
+class GraphContext:
+    """Fixed-topology device buffers (reference model.py:42-135).
+
+    The reference's edge order is kept at the API; internally edges are stably sorted by their
+    destination (tgt) so every destination segment is contiguous, which makes the message scatter
+    a deterministic segmented sum in the same per-node order as ``index_add_``."""
+
+    def __init__(self, device, *, edge_index, num_nodes, atomic_numbers, edge_cell_shift=None):
+        ei = torch.as_tensor(edge_index).to("cpu", torch.int64)
+        if ei.dim() != 2 or ei.shape[0] != 2:
+            raise ValueError("edge_index must be [2, E]")
+        N = int(num_nodes)
+        E = int(ei.shape[1])
+        if E and (int(ei.min()) < 0 or int(ei.max()) >= N):
+            raise ValueError("edge_index out of range")
+        if N >= 2 ** 31 or E >= 2 ** 31:
+            raise ValueError("graph too large for int32 indices")
+        self.N, self.E = N, E
+        src_np, tgt_np = ei[0].numpy(), ei[1].numpy()
+        order = np.argsort(tgt_np, kind="stable")                # reference order -> dst-sorted
+        self.order = torch.from_numpy(order)
+        src_s, tgt_s = src_np[order], tgt_np[order]
+        tgt_ptr = np.zeros(N + 1, np.int64)
+        tgt_ptr[1:] = np.cumsum(np.bincount(tgt_s, minlength=N))
+        src_perm = np.argsort(src_s, kind="stable")              # dst-order edge ids by src
+        src_ptr = np.zeros(N + 1, np.int64)
+        src_ptr[1:] = np.cumsum(np.bincount(src_s, minlength=N))
+        dev = torch.device(device)
+        i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(dev)
+        self.src, self.tgt = i32(src_s), i32(tgt_s)
+        self.tgt_ptr, self.src_ptr, self.src_perm = i32(tgt_ptr), i32(src_ptr), i32(src_perm)
+        Z = torch.as_tensor(atomic_numbers).to("cpu", torch.int64).numpy()
+        self.Z = torch.from_numpy(Z.astype(np.int64)).to(dev)
+        self.zsrc, self.ztgt = i32(Z[src_s]), i32(Z[tgt_s])
+        self.shift = None
+        if edge_cell_shift is not None:
+            sh = torch.as_tensor(edge_cell_shift, dtype=torch.float32).cpu()[self.order]
+            self.shift = sh.contiguous().to(dev)
+        self.max_in_degree = int(np.diff(tgt_ptr).max()) if N else 0

@@ -1,0 +1,305 @@
+"""Fixed-topology energy + forces (+ virial) step on the GPU: the eSCN-MD forward and its
+hand-written reverse pass, every E-sized operation a gfx950 HIP kernel.
+
+Reference: the device forward (model.py:158-235, edgewise.py:39-87, so2.py:255-330,
+edge_degree.py:43-66), the device VJP (forces.py:104-495), the host geometry and its autograd
+finish (geometry.py:226-280, forces.py:545-589) and the trace engine interface
+(trace.py:83-215: build once per topology, then ``engine(pos)`` per step).  Here the geometric
+terms and their VJP are kernels too, so a step is positions in, (E, F[, virial]) out, with no
+host round trip in between.  All buffers are allocated once per topology.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _native as nat
+from .model import GraphContext, NSPH
+
+
+class _Buf:
+    pass
+
+
+class TracedEngine:
+    """``engine = TracedEngine(bb, geo, Z, edge_index, sys_emb, edge_cell_shift=None)``;
+    ``E, F = engine(pos)`` or ``E, F, virial = engine(pos, compute_stress=True)``.
+
+    ``pos`` may be a host or device tensor; returned forces live on the device of ``pos``."""
+
+    def __init__(self, bb, geo, atomic_numbers, edge_index, sys_emb, edge_cell_shift=None):
+        nat.load()
+        self.bb, self.geo = bb, geo
+        dev = bb.device
+        self.device = dev
+        N = int(torch.as_tensor(atomic_numbers).numel())
+        self.g = GraphContext(dev, edge_index=edge_index, num_nodes=N,
+                              atomic_numbers=atomic_numbers, edge_cell_shift=edge_cell_shift)
+        g = self.g
+        E = g.E
+        if E == 0:
+            raise ValueError("no edges within cutoff -- system too sparse for this model")
+        zmax = min(bb.sphere_emb.shape[0], bb.src_emb.shape[0], bb.tgt_emb.shape[0])
+        if N and (int(g.Z.min()) < 0 or int(g.Z.max()) >= zmax):
+            raise ValueError(f"atomic numbers must lie in [0, {zmax})")
+        C, H, L = bb.C, bb.H, bb.L
+        ec = bb.edge_channels
+        nb = geo.n_gauss
+        if nb != bb.n_gauss:
+            raise RuntimeError("gaussian basis size differs between geometry and backbone")
+        self.N, self.E, self.C, self.H, self.L, self.ec, self.nb = N, E, C, H, L, ec, nb
+        self.k_in = nb + 2 * ec
+        f32 = dict(device=dev, dtype=torch.float32)
+        z = lambda *s: torch.zeros(*s, **f32)
+        emp = lambda *s: torch.empty(*s, **f32)
+        hid = bb.edge_degree.hidden
+        # pos-independent node init: sphere_emb[Z] + sys_emb on coefficient 0 (geometry.py:257-258)
+        se = torch.as_tensor(sys_emb, dtype=torch.float32).reshape(N, C).to(dev)
+        self.sys_emb = se.contiguous()
+        self.l0 = z(N, NSPH, C)
+        self.l0[:, 0, :] = bb.sphere_emb[g.Z] + se
+        # per-step geometry
+        self.pos = emp(N, 3)
+        self.ev, self.dist, self.coef, self.env = emp(E, 3), emp(E), emp(E, 35), emp(E)
+        self.x_edge = emp(E, self.k_in)
+        # accumulated geometric adjoints
+        self.g_coef, self.g_env, self.g_gauss = emp(E, 35), emp(E), emp(E, nb)
+        self.g_ev, self.forces = emp(E, 3), emp(N, 3)
+        self.energy_buf, self.virial_buf, self.virial_work = emp(1), emp(9), emp(256 * 9)
+        # shared edge temporaries
+        self.xf, self.g_xf, self.g_mcat = emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C)
+        self.y, self.g_y, self.g_out1 = emp(E, NSPH, H), emp(E, NSPH, H), emp(E, NSPH, H)
+        self.g_mso2 = emp(E, NSPH, C)
+        self.g_gating = emp(E, L * H)
+        self.g_rad = emp(E, 6 * 2 * C)
+        self.s1, self.s2 = emp(E, hid), emp(E, hid)
+        self.t1, self.t2 = emp(E, hid), emp(E, hid)
+        # edge-degree caches
+        self.ed = self._radial_cache(E, hid, 3 * C, dev)
+        self.g_edm = emp(E, 3 * C)
+        # per-block caches
+        self.blk = []
+        for b in bb.blocks:
+            c = _Buf()
+            c.x_in, c.n1, c.x1, c.n2, c.x2 = (emp(N, NSPH, C) for _ in range(5))
+            c.inv1, c.inv2 = emp(N), emp(N)
+            c.rad = self._radial_cache(E, hid, 6 * 2 * C, dev)
+            c.out1, c.gating, c.mso2 = emp(E, NSPH, H), emp(E, L * H), emp(E, NSPH, C)
+            if b.ff_type == "spectral":
+                c.a_s, c.gat, c.h, c.gout = emp(N, L * H), emp(N, L * H), emp(N, NSPH, H), emp(N, NSPH, H)
+            else:
+                P = b.atom_wise.npts
+                c.xg, c.a1, c.sg1, c.a2, c.sg2, c.gg = (emp(N, P, C) for _ in range(6))
+            self.blk.append(c)
+        self.x_final, self.ne, self.inv_f = emp(N, NSPH, C), emp(N, NSPH, C), emp(N)
+        self.eh_a1, self.eh_s1 = emp(N, H), emp(N, H)
+        self.eh_a2, self.eh_s2 = emp(N, H), emp(N, H)
+        self.node_e = emp(N, 1)
+        self.ones = torch.ones(N, 1, **f32)
+        # node adjoint temporaries
+        self.gn_a, self.gn_b, self.gn_c = emp(N, NSPH, C), emp(N, NSPH, C), emp(N, NSPH, C)
+        self.g_eh1, self.g_eh2 = emp(N, H), emp(N, H)
+        self.gs_h, self.gs_h2, self.gs_g = emp(N, NSPH, H), emp(N, NSPH, H), emp(N, L * H)
+        self.gs_a = emp(N, L * H)
+        P = max([b.atom_wise.npts for b in bb.blocks if b.ff_type != "spectral"], default=0)
+        self.gt1, self.gt2 = emp(N * P, C), emp(N * P, C)
+
+    @staticmethod
+    def _radial_cache(E, hid, n_out, dev):
+        c = _Buf()
+        f32 = dict(device=dev, dtype=torch.float32)
+        c.a0, c.nrm1, c.a3, c.nrm4 = (torch.empty(E, hid, **f32) for _ in range(4))
+        c.out = torch.empty(E, n_out, **f32)
+        return c
+
+    # ------------------------------------------------------------------ radial MLP
+    def _radial_fwd(self, rw, c):
+        nat.linear(self.x_edge, rw.w0t, rw.b0, out=c.a0)
+        nat.ln_silu_fwd(c.a0, rw.ln1w, rw.ln1b, c.nrm1, self.s1)
+        nat.linear(self.s1, rw.w3t, rw.b3, out=c.a3)
+        nat.ln_silu_fwd(c.a3, rw.ln4w, rw.ln4b, c.nrm4, self.s2)
+        nat.linear(self.s2, rw.w6t, rw.b6, out=c.out)
+
+    def _radial_bwd(self, rw, c, g_out, first):
+        nat.linear(g_out, rw.w6, out=self.t1)
+        nat.ln_silu_bwd(self.t1, c.a3, c.nrm4, rw.ln4w, self.t2)
+        nat.linear(self.t2, rw.w3, out=self.t1)
+        nat.ln_silu_bwd(self.t1, c.a0, c.nrm1, rw.ln1w, self.t2)
+        nat.linear(self.t2, rw.w0g, out=self.g_gauss,
+                   epilogue=nat.EPI_STORE if first else nat.EPI_ACCUM)
+
+    # ------------------------------------------------------------------ feed-forward
+    def _spectral_fwd(self, aw, c, x, res, out):
+        N, C, H = self.N, self.C, self.H
+        x2d = x.view(N, NSPH * C)
+        nat.linear(x2d[:, :C], aw.ws_t, aw.bs, out=c.a_s, epilogue=nat.EPI_PRE_SILU, out2=c.gat)
+        nat.gemm(x, aw.w1_t, c.h, bias=aw.b1, M=N, N=H, K=C, lda=NSPH * C, ldb=H, ldc=NSPH * H,
+                 batch=NSPH, sA=C, sB=C * H, sC=H, sBias=H)
+        nat.gate_fwd(c.h, c.gat, c.gout, self.bb.gate_idx_natural)
+        out.copy_(res)
+        nat.gemm(c.gout, aw.w2_t, out, bias=aw.b2, M=N, N=C, K=H, lda=NSPH * H, ldb=C,
+                 ldc=NSPH * C, batch=NSPH, sA=H, sB=H * C, sC=C, sBias=C, epilogue=nat.EPI_ACCUM)
+
+    def _spectral_bwd(self, aw, c, g, out):
+        N, C, H = self.N, self.C, self.H
+        nat.gemm(g, aw.w2, self.gs_h, M=N, N=H, K=C, lda=NSPH * C, ldb=H, ldc=NSPH * H,
+                 batch=NSPH, sA=C, sB=C * H, sC=H)
+        g_h = self.gs_h2
+        nat.gate_bwd(self.gs_h, c.h, c.gat, g_h, self.gs_g, self.bb.gate_idx_natural)
+        nat.gemm(g_h, aw.w1, out, M=N, N=C, K=H, lda=NSPH * H, ldb=C, ldc=NSPH * C,
+                 batch=NSPH, sA=H, sB=H * C, sC=C)
+        nat.silu_bwd(self.gs_g, c.a_s, self.gs_a)
+        nat.linear(self.gs_a, aw.ws, out=out.view(N, NSPH * C)[:, :C], epilogue=nat.EPI_ACCUM)
+
+    def _grid_fwd(self, aw, c, x, res, out):
+        N, C, P = self.N, self.C, aw.npts
+        nat.gemm(aw.tg, x, c.xg, M=P, N=C, K=NSPH, lda=NSPH, ldb=C, ldc=C, batch=N, sA=0,
+                 sB=NSPH * C, sC=P * C)
+        xg, a1, s1, a2, s2, gg = (t.view(N * P, C) for t in (c.xg, c.a1, c.sg1, c.a2, c.sg2, c.gg))
+        nat.linear(xg, aw.w0_t, out=a1, epilogue=nat.EPI_PRE_SILU, out2=s1)
+        nat.linear(s1, aw.w2_t, out=a2, epilogue=nat.EPI_PRE_SILU, out2=s2)
+        nat.linear(s2, aw.w4_t, out=gg)
+        out.copy_(res)
+        nat.gemm(aw.fg_t, c.gg, out, M=NSPH, N=C, K=P, lda=P, ldb=C, ldc=C, batch=N, sA=0,
+                 sB=P * C, sC=NSPH * C, epilogue=nat.EPI_ACCUM)
+
+    def _grid_bwd(self, aw, c, g, out):
+        N, C, P = self.N, self.C, aw.npts
+        t1, t2 = self.gt1[:N * P], self.gt2[:N * P]
+        nat.gemm(aw.fg, g, t1, M=P, N=C, K=NSPH, lda=NSPH, ldb=C, ldc=C, batch=N, sA=0,
+                 sB=NSPH * C, sC=P * C)                                   # g wrt grid output
+        nat.linear(t1, aw.w4, out=t2, epilogue=nat.EPI_SILU_GRAD, aux=c.a2.view(N * P, C))
+        nat.linear(t2, aw.w2, out=t1, epilogue=nat.EPI_SILU_GRAD, aux=c.a1.view(N * P, C))
+        nat.linear(t1, aw.w0, out=t2)                                     # g wrt x_grid
+        nat.gemm(aw.tg_t, t2, out, M=NSPH, N=C, K=P, lda=P, ldb=C, ldc=C, batch=N, sA=0,
+                 sB=P * C, sC=NSPH * C)
+
+    # ------------------------------------------------------------------ forward
+    def _forward(self):
+        bb, geo, g = self.bb, self.geo, self.g
+        E, N, C, H = self.E, self.N, self.C, self.H
+        nat.edge_wigner(self.pos, g.src, g.tgt, g.shift, geo.jd, geo.gamma, self.ev, self.dist,
+                        self.coef)
+        nat.edge_features(self.dist, g.zsrc, g.ztgt, bb.src_emb, bb.tgt_emb, geo.offset,
+                          geo.coeff, geo.cutoff, self.nb, self.ec, self.x_edge, self.env)
+        # edge-degree node init (geometry.py:268-276)
+        self._radial_fwd(bb.edge_degree, self.ed)
+        x = self.blk[0].x_in if self.blk else self.x_final
+        nat.rotate_env_segsum(self.ed.out, self.coef, self.env, g.tgt_ptr, self.l0, x, n_in=3,
+                              env_first=False, div=geo.rescale)
+        Cin = 2 * C
+        for i, (bw, c) in enumerate(zip(bb.blocks, self.blk)):
+            s1w, s2w = bw.so2_1, bw.so2_2
+            nat.rmsnorm_sh_fwd(c.x_in, bw.norm_1.aw, bw.norm_1.ab, self.sys_emb, c.n1, c.inv1)
+            self._radial_fwd(s1w.rad, c.rad)
+            nat.gather_rotate(c.n1, g.src, g.tgt, self.coef, c.rad.out, self.xf)
+            xf = self.xf.view(E, NSPH * Cin)
+            o1 = c.out1.view(E, NSPH * H)
+            nat.linear(xf[:, :3 * Cin], s1w.wg_t, s1w.bg, out=c.gating)
+            nat.linear(xf[:, :3 * Cin], s1w.wc_t, s1w.bc, out=o1[:, :3 * H])
+            nat.linear(xf[:, 3 * Cin:7 * Cin], s1w.w1, out=o1[:, 3 * H:7 * H])
+            nat.linear(xf[:, 7 * Cin:], s1w.w2, out=o1[:, 7 * H:])
+            nat.gate_fwd(c.out1, c.gating, self.y, bb.gate_idx_mprime)
+            y = self.y.view(E, NSPH * H)
+            ms = c.mso2.view(E, NSPH * C)
+            nat.linear(y[:, :3 * H], s2w.wc_t, s2w.bc, out=ms[:, :3 * C])
+            nat.linear(y[:, 3 * H:7 * H], s2w.w1, out=ms[:, 3 * C:7 * C])
+            nat.linear(y[:, 7 * H:], s2w.w2, out=ms[:, 7 * C:])
+            nat.rotate_env_segsum(c.mso2, self.coef, self.env, g.tgt_ptr, c.x_in, c.x1, n_in=9,
+                                  env_first=True)
+            nat.rmsnorm_sh_fwd(c.x1, bw.norm_2.aw, bw.norm_2.ab, None, c.n2, c.inv2)
+            x_out = self.blk[i + 1].x_in if i + 1 < len(self.blk) else self.x_final
+            if bw.ff_type == "spectral":
+                self._spectral_fwd(bw.atom_wise, c, c.n2, c.x1, x_out)
+            else:
+                self._grid_fwd(bw.atom_wise, c, c.n2, c.x1, x_out)
+        nat.rmsnorm_sh_fwd(self.x_final, bb.final_norm.aw, bb.final_norm.ab, None, self.ne,
+                           self.inv_f)
+        ne2 = self.ne.view(N, NSPH * C)
+        nat.linear(ne2[:, :C], bb.eh_w_t[0], bb.eh_b[0], out=self.eh_a1,
+                   epilogue=nat.EPI_PRE_SILU, out2=self.eh_s1)
+        nat.linear(self.eh_s1, bb.eh_w_t[1], bb.eh_b[1], out=self.eh_a2,
+                   epilogue=nat.EPI_PRE_SILU, out2=self.eh_s2)
+        nat.linear(self.eh_s2, bb.eh_w_t[2], bb.eh_b[2], out=self.node_e)
+        nat.reduce_sum(self.node_e, N, 1, self.energy_buf)
+
+    # ------------------------------------------------------------------ reverse
+    def _backward(self):
+        bb, g = self.bb, self.g
+        E, N, C, H = self.E, self.N, self.C, self.H
+        Cin = 2 * C
+        nat.fill(self.g_coef, 0.0)
+        nat.fill(self.g_env, 0.0)
+        # energy head (forces.py:438-461): dE/dnode_e = 1
+        nat.linear(self.ones, bb.eh_w[2], out=self.g_eh2, epilogue=nat.EPI_SILU_GRAD, aux=self.eh_a2)
+        nat.linear(self.g_eh2, bb.eh_w[1], out=self.g_eh1, epilogue=nat.EPI_SILU_GRAD, aux=self.eh_a1)
+        nat.fill(self.gn_a, 0.0)
+        nat.linear(self.g_eh1, bb.eh_w[0], out=self.gn_a.view(N, NSPH * C)[:, :C])
+        gcur = self.gn_b
+        nat.rmsnorm_sh_bwd(self.gn_a, self.x_final, bb.final_norm.aw, self.inv_f, None, gcur)
+        first_rad = True
+        for bw, c in zip(reversed(bb.blocks), reversed(self.blk)):
+            s1w, s2w = bw.so2_1, bw.so2_2
+            # x2 = ff(norm2(x1)) + x1
+            g_n2 = self.gn_a
+            if bw.ff_type == "spectral":
+                self._spectral_bwd(bw.atom_wise, c, gcur, g_n2)
+            else:
+                self._grid_bwd(bw.atom_wise, c, gcur, g_n2)
+            g_x1 = self.gn_c
+            nat.rmsnorm_sh_bwd(g_n2, c.x1, bw.norm_2.aw, c.inv2, gcur, g_x1)
+            # x1 = edgewise(norm1(x_in)) + x_in
+            nat.rotate_env_segsum_bw(g_x1, g.tgt, c.mso2, self.coef, self.env, self.g_mso2,
+                                     self.g_coef, self.g_env, n_in=9, env_first=True)
+            gm = self.g_mso2.view(E, NSPH * C)
+            gy = self.g_y.view(E, NSPH * H)
+            nat.linear(gm[:, :3 * C], s2w.wc, out=gy[:, :3 * H])
+            nat.linear(gm[:, 3 * C:7 * C], s2w.w1_t, out=gy[:, 3 * H:7 * H])
+            nat.linear(gm[:, 7 * C:], s2w.w2_t, out=gy[:, 7 * H:])
+            nat.gate_bwd(self.g_y, c.out1, c.gating, self.g_out1, self.g_gating, bb.gate_idx_mprime)
+            go = self.g_out1.view(E, NSPH * H)
+            gx = self.g_xf.view(E, NSPH * Cin)
+            nat.linear(self.g_gating, s1w.wg, out=gx[:, :3 * Cin])
+            nat.linear(go[:, :3 * H], s1w.wc, out=gx[:, :3 * Cin], epilogue=nat.EPI_ACCUM)
+            nat.linear(go[:, 3 * H:7 * H], s1w.w1_t, out=gx[:, 3 * Cin:7 * Cin])
+            nat.linear(go[:, 7 * H:], s1w.w2_t, out=gx[:, 7 * Cin:])
+            nat.gather_rotate_bw(self.g_xf, c.rad.out, c.n1, g.src, g.tgt, self.coef, self.g_rad,
+                                 self.g_mcat, self.g_coef)
+            g_n1 = self.gn_a
+            nat.node_gather_sum(self.g_mcat, g.src_ptr, g.src_perm, g.tgt_ptr, None, g_n1)
+            g_in = self.gn_b
+            nat.rmsnorm_sh_bwd(g_n1, c.x_in, bw.norm_1.aw, c.inv1, g_x1, g_in)
+            gcur = g_in
+            self._radial_bwd(s1w.rad, c.rad, self.g_rad, first_rad)
+            first_rad = False
+        # edge-degree init backward (edge_degree.py:69-93)
+        nat.rotate_env_segsum_bw(gcur, g.tgt, self.ed.out, self.coef, self.env, self.g_edm,
+                                 self.g_coef, self.g_env, n_in=3, env_first=False,
+                                 div=self.geo.rescale)
+        self._radial_bwd(bb.edge_degree, self.ed, self.g_edm, first_rad)
+        # geometry VJP -> forces (forces.py:580-589 in closed form)
+        geo = self.geo
+        nat.edge_geometry_bwd(self.ev, self.dist, self.g_coef, self.g_env, self.g_gauss, self.nb,
+                              geo.offset, geo.coeff, geo.cutoff, self.nb, geo.jd, geo.gamma,
+                              self.g_ev)
+        nat.node_forces(self.g_ev, g.src_ptr, g.src_perm, g.tgt_ptr, self.forces)
+
+    # ------------------------------------------------------------------ step
+    def run(self, pos, compute_stress=False):
+        """Enqueue one step; results stay on the device (energy_buf, forces, virial_buf)."""
+        self.pos.copy_(torch.as_tensor(pos, dtype=torch.float32).reshape(self.N, 3),
+                       non_blocking=True)
+        self._forward()
+        self._backward()
+        if compute_stress:
+            nat.virial(self.ev, self.g_ev, self.virial_work, self.virial_buf)
+
+    def __call__(self, pos, compute_stress=False):
+        self.run(pos, compute_stress)
+        E = float(self.energy_buf.item())
+        F = self.forces.clone()
+        if not torch.as_tensor(pos).is_cuda:
+            F = F.cpu()
+        if compute_stress:
+            V = self.virial_buf.reshape(3, 3).clone()
+            return E, F, (V if torch.as_tensor(pos).is_cuda else V.cpu())
+        return E, F

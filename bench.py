@@ -1,0 +1,219 @@
+#!/usr/bin/env python
+"""Headline benchmark: energy + conservative forces of the uma-s-1-architecture eSCN-MD model
+(random-init weights) on the 2,048-atom C3 cluster, one MI355X, fp32.
+
+A step is positions -> (energy, forces) with a fixed topology (the neighbour list is built once,
+as in the reference's traced-MD convention): Wigner/edge geometry, edge-degree init, 4 eSCN-MD
+blocks, energy head, the full reverse pass and the geometric VJP, all in HIP kernels.
+``value`` = atoms * steps / wall time of the timed steps (atom-steps/s).
+
+Also reported on the same JSON line:
+  roofline      the dominant kernel (the fp32 MFMA GEMM, one kernel symbol for every GEMM of the
+                step): algorithmic FLOPs of its launches in the timed region / their HIP-event
+                durations (recorded on the launch stream), against the 157.3 TFLOP/s fp32 MFMA
+                peak; ``traffic`` = HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE
+                when profiles/gemm_f32_traffic_c3.txt holds them, else null.
+  cpu_baseline  the CPU oracle (PyTorch-CPU restatement of the reference path) on a bounded sample
+                of the same workload: the C3 model on a 512-atom cluster of the same density
+                (one step after a small warm-up), in atom-steps/s.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "tt-atom_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+METRIC = "atom-steps/s (energy+forces), uma-s-1 arch 2,048 atoms; % HBM/MFMA roofline"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+TRAFFIC_FILE = ROOT / "profiles" / "gemm_f32_traffic_c3.txt"
+
+
+class GemmEvents:
+    """HIP events around every GEMM launch (same stream as the launch)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pairs = []
+        self.flops = 0.0
+        self.nbytes = 0.0
+        self._cur = None
+
+    def before(self, flops, nbytes):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self._cur = e
+        self.flops += flops
+        self.nbytes += nbytes
+
+    def after(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self.pairs.append((self._cur, e))
+
+    def summary(self):
+        ms = sum(a.elapsed_time(b) for a, b in self.pairs)
+        n = len(self.pairs)
+        return n, self.flops, ms
+
+
+def build_c3(torch, n_atoms=2048, seed=None):
+    from tt_atom import geometry, synthetic
+    cfg = dict(synthetic.CFG_UMA_S)
+    w, host = synthetic.random_uma_bundle(cfg, synthetic.SEEDS["C3"] + synthetic.WEIGHT_SEED_OFFSET)
+    radius = 17.0 * (n_atoms / 2048.0) ** (1.0 / 3.0)
+    pos, Z = synthetic.c3_system(seed=synthetic.SEEDS["C3"] if seed is None else seed,
+                                 n=n_atoms, radius=radius)
+    pos, Z = torch.from_numpy(pos), torch.from_numpy(Z)
+    t0 = time.perf_counter()
+    ei, shift = geometry.radius_graph(pos, cfg["cutoff"], max_neighbors=cfg["max_neighbors"])
+    nl_ms = (time.perf_counter() - t0) * 1e3
+    se = geometry.csd_embedding(w, torch.tensor([0.0]), torch.tensor([1.0]), dataset=cfg["task"])
+    se = se.expand(len(Z), -1).contiguous()
+    return cfg, w, host, pos, Z, ei, se, nl_ms
+
+
+def cpu_baseline(torch):
+    """CPU oracle on a bounded sample of the C3 workload."""
+    from oracle import forces as OF
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    cfg, w, host, pos, Z, ei, se, _ = build_c3(torch, n_atoms=64, seed=301)
+    m = OF.Model(w, cfg, host)
+    OF.energy_and_forces(m, pos, Z, ei, se)                       # warm-up (threads, allocator)
+    # one step of a 512-atom same-density cluster; on a host fast enough for that to take under
+    # 3 s, one step of the full 2048-atom workload instead (the bounded sample stays ~10-30 s)
+    for n_atoms in (512, 2048):
+        cfg, w, host, pos, Z, ei, se, _ = build_c3(torch, n_atoms=n_atoms)
+        m = OF.Model(w, cfg, host)
+        t0 = time.perf_counter()
+        OF.energy_and_forces(m, pos, Z, ei, se)
+        dt = time.perf_counter() - t0
+        if dt > 3.0:
+            break
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(len(Z) / dt, 3), "unit": "atom-steps/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"CPU oracle (torch-CPU restatement of the reference path), C3 model on a "
+                       f"{len(Z)}-atom same-density cluster (E={ei.shape[1]}), 1 step after a "
+                       f"64-atom warm-up, {dt:.1f} s; {threads} threads on {model}")}
+
+
+def read_traffic():
+    if not TRAFFIC_FILE.exists():
+        return None
+    vals = {}
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if ":" in line and not line.startswith("#"):
+            k, v = line.split(":", 1)
+            vals[k.strip()] = v.strip()
+    try:
+        return float(vals["hbm_bytes_per_launch"])
+    except (KeyError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 256 MiB device copy (y = -x) for the HBM counter scale")
+    args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+        x = torch.randn(64 * 1024 * 1024, device="cuda")
+        y = torch.empty_like(x)
+        torch.cuda.synchronize()
+        torch.neg(x, out=y)                       # reads 256 MiB, writes 256 MiB
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": x.numel() * 4, "copy_bytes_written": y.numel() * 4}))
+        return
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is a "
+              "design note only)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from tt_atom import _native, geometry, model, trace
+
+    cfg, w, host, pos, Z, ei, se, nl_ms = build_c3(torch)
+    dev = torch.device("cuda:0")
+    bb = model.Backbone(w, dev, cfg)
+    geo = geometry.HostGeometry(w, cfg, host["to_m"], host["gauss_offset"], host["gauss_coeff"],
+                                device=dev)
+    eng = trace.TracedEngine(bb, geo, Z, ei, se)
+    pos_d = pos.to(dev)
+    for _ in range(args.warmup):
+        eng.run(pos_d)
+    torch.cuda.synchronize()
+    print(f"[bench] warm-up done: N={len(Z)} E={ei.shape[1]} energy={float(eng.energy_buf):.6f}",
+          file=sys.stderr, flush=True)
+
+    probe = GemmEvents(torch)
+    _native.set_gemm_probe(probe)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.run(pos_d)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    _native.set_gemm_probe(None)
+    energy = float(eng.energy_buf)
+    if not (energy == energy) or not bool(torch.isfinite(eng.forces).all()):
+        raise RuntimeError("non-finite energy or forces")
+    n_launch, flops, gemm_ms = probe.summary()
+    achieved = flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
+    traffic = read_traffic()
+    ms_step = dt / args.steps * 1e3
+    out = {
+        "metric": METRIC,
+        "value": round(len(Z) * args.steps / dt, 2),
+        "unit": "atom-steps/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random-init uma-s-1-architecture weights, seeded C3 cluster)",
+        "config": {"workload": "C3: uma-s-1 arch (4 eSCN-MD layers, C=H=128, lmax=mmax=2, 512 "
+                               "gaussians, spectral FF), 2048-atom H/C/N/O cluster in a 17 A ball, "
+                               "cutoff 6 A, cap 30, energy+forces, fixed topology",
+                   "atoms": len(Z), "edges": int(ei.shape[1]),
+                   "neighbor_list_host_ms": round(nl_ms, 1),
+                   "energy": energy},
+        "roofline": {"bound": "mfma", "kernel": "gemm_f32_kernel (all GEMMs of the step)",
+                     "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+                     "traffic": traffic, "launches": n_launch,
+                     "algorithmic_bytes_per_launch": round(probe.nbytes / max(1, n_launch)),
+                     "algorithmic_flops_per_launch": round(flops / max(1, n_launch)),
+                     "avg_launch_us": round(gemm_ms * 1e3 / max(1, n_launch), 2),
+                     "gemm_share_of_step": round(gemm_ms / (dt * 1e3), 4)},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -31,6 +31,7 @@ struct GemmArgs {
   int M, N, K;
   int64_t lda, ldb, ldc;
   int64_t sA, sB, sC, sBias;
+  int epi;
 };
 
 enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ACCUM = 2, EPI_PRE_SILU = 3, EPI_SILU_GRAD = 4 };
@@ -103,8 +104,11 @@ __device__ __forceinline__ void store_b(float (*Bs)[BN + PAD], int t, const floa
   }
 }
 
-template <int EPI, bool VEC>
+// The epilogue is a (wave-uniform) runtime switch so every GEMM of the step is one kernel
+// symbol; it runs once per output element and costs nothing next to the K loop.
+template <bool VEC>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
+  const int EPI = p.epi;
   __shared__ float As[2][BK][BM + PAD];
   __shared__ float Bs[2][BK][BN + PAD];
 
@@ -187,13 +191,12 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
   }
 }
 
-template <int EPI>
 int launch(const GemmArgs& p, int64_t batch, bool vec, hipStream_t s) {
   dim3 grid(tta_blocks(p.N, BN), tta_blocks(p.M, BM), (unsigned)batch);
   if (vec)
-    hipLaunchKernelGGL((gemm_f32_kernel<EPI, true>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_kernel<true>), grid, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_f32_kernel<EPI, false>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_kernel<false>), grid, dim3(256), 0, s, p);
   TTA_CHECK_LAUNCH("tta_gemm_f32");
   return tta::kOk;
 }
@@ -215,15 +218,10 @@ extern "C" int tta_gemm_f32(const float* A, const float* B, float* C, const floa
   if (M == 0 || N == 0 || batch == 0) return tta::kOk;
   TTA_CHECK_ARG(A && B && C, "tta_gemm_f32: null pointer");
   TTA_CHECK_ARG(lda >= K && ldb >= N && ldc >= N, "tta_gemm_f32: leading dimension too small");
-  GemmArgs p{A, B, C, bias, C2, aux, (int)M, (int)N, (int)K, lda, ldb, ldc, sA, sB, sC, sBias};
+  GemmArgs p{A, B, C, bias, C2, aux, (int)M, (int)N, (int)K, lda, ldb, ldc, sA, sB, sC, sBias,
+             epilogue};
   const bool vec = (K % 4 == 0) && (N % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                    (sA % 4 == 0) && (sB % 4 == 0) && ((uintptr_t)A % 16 == 0) &&
                    ((uintptr_t)B % 16 == 0);
-  switch (epilogue) {
-    case EPI_STORE: return launch<EPI_STORE>(p, batch, vec, stream);
-    case EPI_SILU: return launch<EPI_SILU>(p, batch, vec, stream);
-    case EPI_ACCUM: return launch<EPI_ACCUM>(p, batch, vec, stream);
-    case EPI_PRE_SILU: return launch<EPI_PRE_SILU>(p, batch, vec, stream);
-    default: return launch<EPI_SILU_GRAD>(p, batch, vec, stream);
-  }
+  return launch(p, batch, vec, stream);
 }

@@ -123,6 +123,17 @@ def _i32(t, numel=None, name="index"):
 # ----------------------------------------------------------------------------- GEMM
 EPI_STORE, EPI_SILU, EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD = 0, 1, 2, 3, 4
 
+# Optional measurement hook: when set, every GEMM launch is bracketed by
+# ``probe.before(flops, nbytes)`` and ``probe.after()`` (the benchmark records HIP events on the
+# launch stream there).  nbytes is the algorithmic traffic: A, B and C once (C twice when
+# accumulated, plus the second output / auxiliary input of epilogues 3 and 4).
+_gemm_probe = None
+
+
+def set_gemm_probe(probe):
+    global _gemm_probe
+    _gemm_probe = probe
+
 
 def gemm(A, B, C, *, M, N, K, lda, ldb, ldc, bias=None, epilogue=EPI_STORE, C2=None, aux=None,
          batch=1, sA=0, sB=0, sC=0, sBias=0):
@@ -131,10 +142,18 @@ def gemm(A, B, C, *, M, N, K, lda, ldb, ldc, bias=None, epilogue=EPI_STORE, C2=N
     for t, nm in ((A, "A"), (B, "B"), (C, "C")):
         if not t.is_cuda or t.dtype != torch.float32:
             raise RuntimeError(f"gemm: {nm} must be an fp32 device tensor")
+    probe = _gemm_probe
+    if probe is not None:
+        c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD))
+        nbytes = 4.0 * (M * K * (batch if sA else 1) + K * N * (batch if sB else 1)
+                        + c_passes * M * N * batch)
+        probe.before(2.0 * M * N * K * batch, nbytes)
     _call("tta_gemm_f32", A.data_ptr(), B.data_ptr(), C.data_ptr(),
           None if bias is None else bias.data_ptr(), None if C2 is None else C2.data_ptr(),
           None if aux is None else aux.data_ptr(), M, N, K, lda, ldb, ldc, batch, sA, sB, sC,
           sBias, epilogue, _stream())
+    if probe is not None:
+        probe.after()
 
 
 def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None):

@@ -1,0 +1,66 @@
+"""Host-side logic of the calculator front end (no GPU): Voigt conversion, bundle round trip,
+coverage check, neighbour-list cap and configuration generators."""
+import numpy as np
+import torch
+
+from tt_atom import calculator, geometry, synthetic, weights
+
+
+def test_voigt_order_matches_ase_convention():
+    s = np.arange(9, dtype=float).reshape(3, 3)
+    v = calculator.full_3x3_to_voigt_6(s)
+    assert np.allclose(v, [0, 4, 8, 0.5 * (5 + 7), 0.5 * (2 + 6), 0.5 * (1 + 3)])
+
+
+def test_bundle_round_trip_and_coverage(tmp_path):
+    cfg = dict(synthetic.CFG_UMA_S, sphere_channels=8, hidden_channels=8, edge_channels=8,
+               num_distance_basis=8, num_layers=1)
+    w, host = synthetic.random_uma_bundle(cfg, 5)
+    p = tmp_path / "b.npz"
+    weights.save_bundle(p, cfg, w, host, scale={"rmsd": 2.0, "mean": -1.0})
+    b = weights.WeightBundle.load(p)
+    ok, missing, _ = b.verify_coverage()
+    assert ok, missing
+    assert b.scale_rmsd == 2.0 and b.scale_mean == -1.0 and b.task == "omol"
+    assert torch.equal(b.weights["blocks.0.norm_1.affine_weight"], w["blocks.0.norm_1.affine_weight"])
+    assert torch.equal(b.to_m, host["to_m"])
+
+
+def test_jd_matches_fixture(golden):
+    jd = synthetic.jd_matrices()
+    for l in range(3):
+        assert (jd[l] - golden.w()[f"Jd_{l}"]).abs().max() < 1e-7
+
+
+def test_gaussian_buffers_match_fixture(golden):
+    off, coeff = synthetic.gaussian_buffers(32, 5.0)
+    assert (off - golden.host("gauss_offset")).abs().max() < 1e-6
+    assert abs(float(coeff) - float(golden.host("gauss_coeff"))) < 1e-4
+
+
+def test_product_neighbor_list_matches_oracle():
+    from oracle import geometry as OG
+    pos, Z = synthetic.c1_system()
+    pos = torch.from_numpy(pos)
+    for cap in (None, 6):
+        a = geometry.radius_graph(pos, 5.0, max_neighbors=cap)
+        b = OG.neighbor_list(pos, 5.0, max_neighbors=cap)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    p4, _, cell = synthetic.c4_system(reps=2)
+    p4, cell = torch.from_numpy(p4), torch.from_numpy(cell)
+    a = geometry.radius_graph(p4, 4.0, cell, [True] * 3, max_neighbors=10)
+    b = OG.neighbor_list(p4, 4.0, cell, [True] * 3, max_neighbors=10)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_generators_are_seeded_and_sized():
+    p1, Z1 = synthetic.c1_system()
+    p2, Z2 = synthetic.c1_system()
+    assert np.array_equal(p1, p2) and len(Z1) == 24 and set(Z1) <= {1, 6, 7, 8}
+    d = np.linalg.norm(p1[:, None] - p1[None], axis=-1) + np.eye(24) * 9
+    assert d.min() >= 0.9
+    p4, Z4, cell = synthetic.c4_system()
+    assert p4.shape == (2048, 3) and np.all(Z4 == 29) and np.allclose(np.diag(cell), 8 * 3.61)
+    ei, vec = synthetic.c2_graph()
+    assert ei.shape == (2, 204800) and np.all(ei[0] != ei[1]) and np.all(np.diff(ei[1]) >= 0)
+    assert np.allclose(np.linalg.norm(vec, axis=1).min(), 0.8, atol=1e-3)

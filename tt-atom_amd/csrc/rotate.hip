@@ -8,28 +8,62 @@
 // The inverse rotation is W^T (geometry.py:211), so one coefficient array serves both
 // directions.  Edge tensors are flat [E, 9, W] coefficient-major, W channels per coefficient.
 //
-// Work mapping: each edge (or node, for the segmented reductions) is owned by a group of G lanes
-// (G = min(64, W/4)); a lane handles QPL float4 channel quads.  Channel reductions (coefficient
-// adjoints, envelope adjoint) are butterfly sums inside the lane group, so every output is
-// written by exactly one lane with plain stores: no float atomics, deterministic results.
+// Work mapping: one wavefront per edge (per node for the segmented sums).  The edge index is
+// wave-uniform, so the 35 coefficients, the envelope and the src/tgt indices live in scalar
+// registers.  The 64 lanes cover one coefficient row of W channels with V-wide vectors
+// (V = 4, 2 or 1 so that W / V <= 64 where possible; wider rows loop).  Channel reductions
+// (coefficient adjoints, envelope adjoint) are DPP butterflies inside each 16-lane row followed by
+// a 4-entry LDS transpose; every output is written by exactly one lane with a plain store: no
+// float atomics, deterministic results.
 #include "common.h"
-
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
 constexpr int NSPH = 9;
 constexpr int NNZ = 35;
+constexpr int WAVES = 4;  // wavefronts per 256-thread block
 
-__device__ __forceinline__ floatx4 ld4(const float* p) { return *reinterpret_cast<const floatx4*>(p); }
-__device__ __forceinline__ void st4(float* p, floatx4 v) { *reinterpret_cast<floatx4*>(p) = v; }
-__device__ __forceinline__ floatx4 z4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
-__device__ __forceinline__ float dot4(floatx4 a, floatx4 b) {
-  return a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+template <int V>
+struct VecT;
+template <>
+struct VecT<1> {
+  typedef float T;
+};
+template <>
+struct VecT<2> {
+  typedef float T __attribute__((ext_vector_type(2)));
+};
+template <>
+struct VecT<4> {
+  typedef float T __attribute__((ext_vector_type(4)));
+};
+
+template <int V>
+__device__ __forceinline__ typename VecT<V>::T ldv(const float* p) {
+  return *reinterpret_cast<const typename VecT<V>::T*>(p);
+}
+template <int V>
+__device__ __forceinline__ void stv(float* p, typename VecT<V>::T v) {
+  *reinterpret_cast<typename VecT<V>::T*>(p) = v;
+}
+template <int V>
+__device__ __forceinline__ typename VecT<V>::T zv() {
+  return typename VecT<V>::T(0.f);
+}
+template <int V>
+__device__ __forceinline__ float hsum(typename VecT<V>::T v) {
+  if constexpr (V == 1) {
+    return v;
+  } else if constexpr (V == 2) {
+    return v[0] + v[1];
+  } else {
+    return (v[0] + v[1]) + (v[2] + v[3]);
+  }
 }
 
 // out[m] = sum_j W[m, j] in[j]   (node SH -> edge frame; also the adjoint of the inverse rotation)
-__device__ __forceinline__ void rot_fwd(const float* c, const floatx4* in, floatx4* out) {
+template <class T>
+__device__ __forceinline__ void rot_fwd(const float* c, const T* in, T* out) {
   out[0] = c[0] * in[0];
   const int m1[3] = {1, 3, 5}, k1[3] = {1, 9, 17};
 #pragma unroll
@@ -48,41 +82,42 @@ __device__ __forceinline__ void rot_fwd(const float* c, const floatx4* in, float
 
 // out[j] = sum_m W[m, j] in[m]   (edge frame -> node SH; also the adjoint of the forward rotation)
 // Only the first NIN m-primed inputs are non-zero (NIN = 3: the m = 0 block alone).
-template <int NIN>
-__device__ __forceinline__ void rot_inv(const float* c, const floatx4* in, floatx4* out) {
+template <int NIN, class T>
+__device__ __forceinline__ void rot_inv(const float* c, const T* in, T* out) {
   out[0] = c[0] * in[0];
 #pragma unroll
   for (int q = 0; q < 3; ++q) {
-    floatx4 v = c[1 + q] * in[1];
+    T v = c[1 + q] * in[1];
     if (NIN > 3) v = v + c[9 + q] * in[3] + c[17 + q] * in[5];
     out[1 + q] = v;
   }
 #pragma unroll
   for (int q = 0; q < 5; ++q) {
-    floatx4 v = c[4 + q] * in[2];
+    T v = c[4 + q] * in[2];
     if (NIN > 3) v = v + c[12 + q] * in[4] + c[20 + q] * in[6] + c[25 + q] * in[7] + c[30 + q] * in[8];
     out[4 + q] = v;
   }
 }
 
-// Coefficient adjoint partials: gc[k] += <a[m_k], b[j_k]> over one channel quad, where a is the
-// m-primed-side tensor and b the natural-side tensor.  Only k with m_k < NIN when NIN = 3.
-template <int NIN>
-__device__ __forceinline__ void coef_partials(const floatx4* a, const floatx4* b, float* gc) {
-  gc[0] += dot4(a[0], b[0]);
+// Coefficient adjoint partials: gc[k] += <a[m_k], b[j_k]> over this lane's channels, where a is
+// the m-primed-side tensor and b the natural-side tensor.  Only k with m_k < NIN.
+template <int NIN, int V>
+__device__ __forceinline__ void coef_partials(const typename VecT<V>::T* a,
+                                              const typename VecT<V>::T* b, float* gc) {
+  gc[0] += hsum<V>(a[0] * b[0]);
   const int m1[3] = {1, 3, 5}, k1[3] = {1, 9, 17};
 #pragma unroll
   for (int r = 0; r < 3; ++r) {
     if (m1[r] >= NIN) continue;
 #pragma unroll
-    for (int q = 0; q < 3; ++q) gc[k1[r] + q] += dot4(a[m1[r]], b[1 + q]);
+    for (int q = 0; q < 3; ++q) gc[k1[r] + q] += hsum<V>(a[m1[r]] * b[1 + q]);
   }
   const int m2[5] = {2, 4, 6, 7, 8}, k2[5] = {4, 12, 20, 25, 30};
 #pragma unroll
   for (int r = 0; r < 5; ++r) {
     if (m2[r] >= NIN) continue;
 #pragma unroll
-    for (int q = 0; q < 5; ++q) gc[k2[r] + q] += dot4(a[m2[r]], b[4 + q]);
+    for (int q = 0; q < 5; ++q) gc[k2[r] + q] += hsum<V>(a[m2[r]] * b[4 + q]);
   }
 }
 
@@ -94,63 +129,75 @@ __device__ __forceinline__ int rad_block(int m) {
   return rb[m];
 }
 
-struct Lanes {
-  int G;    // lanes per item
-  int QPL;  // channel quads per lane
-};
-
-static bool lanes_for(int64_t W, Lanes& l) {
-  if (W <= 0 || W % 4) return false;
-  const int64_t W4 = W / 4;
-  if (W4 <= 64) {
-    if (W4 & (W4 - 1)) return false;  // power of two so groups tile a wave
-    l.G = (int)W4;
-    l.QPL = 1;
-  } else {
-    if (W4 % 64) return false;
-    l.G = 64;
-    l.QPL = (int)(W4 / 64);
-  }
-  return true;
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
 }
 
-__device__ __forceinline__ void load_coef(const float* coef, int64_t e, float* c) {
+// Sums v[i] over the 64 lanes of the wave; afterwards lane i (< NV) holds total i.  DPP
+// butterflies (quad xor 1, quad xor 2, half-row mirror, row mirror) leave each 16-lane row's sum in
+// every lane of the row; the four row sums meet in a per-wave LDS slot `lds` [NV][4].
+template <int NV>
+__device__ __forceinline__ float wave_sums(float* v, float* lds, int lane) {
 #pragma unroll
-  for (int k = 0; k < NNZ; ++k) c[k] = coef[e * NNZ + k];
+  for (int i = 0; i < NV; ++i) {
+    float x = v[i];
+    x = dpp_add<0xB1>(x);   // quad_perm [1,0,3,2]
+    x = dpp_add<0x4E>(x);   // quad_perm [2,3,0,1]
+    x = dpp_add<0x141>(x);  // row_half_mirror
+    x = dpp_add<0x140>(x);  // row_mirror
+    v[i] = x;
+  }
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) lds[i * 4 + (lane >> 4)] = v[i];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float t = 0.f;
+  if (lane < NV) t = (lds[lane * 4] + lds[lane * 4 + 1]) + (lds[lane * 4 + 2] + lds[lane * 4 + 3]);
+  return t;
+}
+
+__device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ void load_coef(const float* __restrict__ coef, int64_t e, float* c) {
+  const float* p = coef + e * NNZ;
+#pragma unroll
+  for (int k = 0; k < NNZ; ++k) c[k] = p[k];
 }
 
 // -------------------------------------------------------------------------------------------
 // Forward: out[e, m, :] = (sum_j W[e,m,j] [x[src_e, j, :] | x[tgt_e, j, :]]) * rad[e, rb(m), :]
 // (edgewise.py:52-69 gather + interleave + rotate, so2.py:263-277 radial multiply).
-template <bool RAD>
+template <int V, bool RAD>
 __global__ __launch_bounds__(256) void k_gather_rotate(const float* __restrict__ x,
                                                        const int* __restrict__ src,
                                                        const int* __restrict__ tgt,
                                                        const float* __restrict__ coef,
                                                        const float* __restrict__ rad,
-                                                       float* __restrict__ out, int E, int C,
-                                                       Lanes ln) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t e = gid / ln.G;
-  const int gl = (int)(gid % ln.G);
+                                                       float* __restrict__ out, int E, int C) {
+  typedef typename VecT<V>::T T;
+  const int lane = threadIdx.x & 63;
+  const int e = wave_uniform(blockIdx.x * WAVES + (threadIdx.x >> 6));
   if (e >= E) return;
-  const int W = 2 * C, C4 = C / 4;
+  const int W = 2 * C, nq = W / V, cq = C / V;
   float c[NNZ];
   load_coef(coef, e, c);
-  const int64_t s = src[e], t = tgt[e];
-  for (int q = 0; q < ln.QPL; ++q) {
-    const int qd = gl + q * ln.G;
-    const float* row = qd < C4 ? x + s * NSPH * C + 4 * qd : x + t * NSPH * C + 4 * (qd - C4);
-    floatx4 in[NSPH], o[NSPH];
+  const int64_t s = wave_uniform(src[e]), t = wave_uniform(tgt[e]);
+  for (int q = lane; q < nq; q += 64) {
+    const float* row = q < cq ? x + s * NSPH * C + V * q : x + t * NSPH * C + V * (q - cq);
+    T in[NSPH], o[NSPH];
 #pragma unroll
-    for (int j = 0; j < NSPH; ++j) in[j] = ld4(row + j * C);
+    for (int j = 0; j < NSPH; ++j) in[j] = ldv<V>(row + j * C);
     rot_fwd(c, in, o);
-    float* orow = out + e * NSPH * W + 4 * qd;
+    float* orow = out + (int64_t)e * NSPH * W + V * q;
 #pragma unroll
     for (int m = 0; m < NSPH; ++m) {
-      floatx4 v = o[m];
-      if (RAD) v = v * ld4(rad + e * 6 * W + rad_block(m) * W + 4 * qd);
-      st4(orow + m * W, v);
+      T v = o[m];
+      if (RAD) v = v * ldv<V>(rad + (int64_t)e * 6 * W + rad_block(m) * W + V * q);
+      stv<V>(orow + m * W, v);
     }
   }
 }
@@ -161,56 +208,56 @@ __global__ __launch_bounds__(256) void k_gather_rotate(const float* __restrict__
 // nodes by k_node_gather_sum), g_rad [E, 6, 2C] (adjoint at the radial output, duplicate blocks
 // collapsed) and accumulates the coefficient adjoint g_coef[e, k] += <g_mrot[m_k], m_cat[j_k]>
 // (rotation.py:225-260 semantics).
-template <bool RAD>
+template <int V, bool RAD>
 __global__ __launch_bounds__(256) void k_gather_rotate_bw(
     const float* __restrict__ g_xf, const float* __restrict__ rad, const float* __restrict__ x,
     const int* __restrict__ src, const int* __restrict__ tgt, const float* __restrict__ coef,
     float* __restrict__ g_rad, float* __restrict__ g_mcat, float* __restrict__ g_coef, int E,
-    int C, Lanes ln) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t e = gid / ln.G;
-  const int gl = (int)(gid % ln.G);
-  if (e >= E) return;  // whole lane groups exit together (G divides the block size)
-  const int W = 2 * C, C4 = C / 4;
+    int C) {
+  typedef typename VecT<V>::T T;
+  __shared__ float red[WAVES][NNZ * 4];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int e = wave_uniform(blockIdx.x * WAVES + w);
+  if (e >= E) return;
+  const int W = 2 * C, nq = W / V, cq = C / V;
   float c[NNZ];
   load_coef(coef, e, c);
   float gc[NNZ];
 #pragma unroll
   for (int k = 0; k < NNZ; ++k) gc[k] = 0.f;
-  const int64_t s = src[e], t = tgt[e];
-  for (int q = 0; q < ln.QPL; ++q) {
-    const int qd = gl + q * ln.G;
-    const float* row = qd < C4 ? x + s * NSPH * C + 4 * qd : x + t * NSPH * C + 4 * (qd - C4);
-    floatx4 in[NSPH], gm[NSPH];
+  const int64_t s = wave_uniform(src[e]), t = wave_uniform(tgt[e]);
+  const int64_t eo = (int64_t)e * NSPH * W;
+  for (int q = lane; q < nq; q += 64) {
+    const float* row = q < cq ? x + s * NSPH * C + V * q : x + t * NSPH * C + V * (q - cq);
+    T in[NSPH], gm[NSPH];
 #pragma unroll
-    for (int j = 0; j < NSPH; ++j) in[j] = ld4(row + j * C);
+    for (int j = 0; j < NSPH; ++j) in[j] = ldv<V>(row + j * C);
 #pragma unroll
-    for (int m = 0; m < NSPH; ++m) gm[m] = ld4(g_xf + e * NSPH * W + m * W + 4 * qd);
+    for (int m = 0; m < NSPH; ++m) gm[m] = ldv<V>(g_xf + eo + m * W + V * q);
     if (RAD) {
-      floatx4 mr[NSPH];
+      const float* rr = rad + (int64_t)e * 6 * W + V * q;
+      float* gr = g_rad + (int64_t)e * 6 * W + V * q;
+      T mr[NSPH];
       rot_fwd(c, in, mr);
-      floatx4 gr[6];
+      // g_rad[b] = sum over the coefficients sharing radial block b (collapse the duplicates)
+      stv<V>(gr + 0 * W, gm[0] * mr[0]);
+      stv<V>(gr + 1 * W, gm[1] * mr[1]);
+      stv<V>(gr + 2 * W, gm[2] * mr[2]);
+      stv<V>(gr + 3 * W, gm[3] * mr[3] + gm[5] * mr[5]);
+      stv<V>(gr + 4 * W, gm[4] * mr[4] + gm[6] * mr[6]);
+      stv<V>(gr + 5 * W, gm[7] * mr[7] + gm[8] * mr[8]);
 #pragma unroll
-      for (int b = 0; b < 6; ++b) gr[b] = z4();
-#pragma unroll
-      for (int m = 0; m < NSPH; ++m) gr[rad_block(m)] = gr[rad_block(m)] + gm[m] * mr[m];
-#pragma unroll
-      for (int b = 0; b < 6; ++b) st4(g_rad + e * 6 * W + b * W + 4 * qd, gr[b]);
-#pragma unroll
-      for (int m = 0; m < NSPH; ++m) gm[m] = gm[m] * ld4(rad + e * 6 * W + rad_block(m) * W + 4 * qd);
+      for (int m = 0; m < NSPH; ++m) gm[m] = gm[m] * ldv<V>(rr + rad_block(m) * W);
     }
-    floatx4 gi[NSPH];
+    T gi[NSPH];
     rot_inv<9>(c, gm, gi);
 #pragma unroll
-    for (int j = 0; j < NSPH; ++j) st4(g_mcat + e * NSPH * W + j * W + 4 * qd, gi[j]);
-    coef_partials<9>(gm, in, gc);
+    for (int j = 0; j < NSPH; ++j) stv<V>(g_mcat + eo + j * W + V * q, gi[j]);
+    coef_partials<9, V>(gm, in, gc);
   }
-#pragma unroll
-  for (int k = 0; k < NNZ; ++k) gc[k] = tta_group_sum(gc[k], ln.G);
-  if (gl == 0) {
-#pragma unroll
-    for (int k = 0; k < NNZ; ++k) g_coef[e * NNZ + k] += gc[k];
-  }
+  const float tot = wave_sums<NNZ>(gc, red[w], lane);
+  if (lane < NNZ) g_coef[(int64_t)e * NNZ + lane] += tot;
 }
 
 // -------------------------------------------------------------------------------------------
@@ -219,49 +266,60 @@ __global__ __launch_bounds__(256) void k_gather_rotate_bw(
 // ENV_FIRST (edgewise.py:72-86):  contrib = W^T (m[e] * env[e])
 // otherwise (geometry.py:269-276, edge-degree init): contrib = ((W^T pad(m[e])) * env[e]) / div
 // Edges of a segment are summed in ascending order starting from zero, then the residual is
-// added: the order index_add_ followed by "+ x_res" uses.
-template <int NIN, bool ENV_FIRST>
+// added: the order index_add_ followed by "+ x_res" uses.  One wave per node; the next edge's
+// rows are loaded before the current edge is accumulated.
+template <int V, int NIN, bool ENV_FIRST>
 __global__ __launch_bounds__(256) void k_rotate_env_segsum(
     const float* __restrict__ m, const float* __restrict__ coef, const float* __restrict__ env,
     const int* __restrict__ ptr, const float* __restrict__ res, float* __restrict__ out, int N,
-    int C, float div, Lanes ln) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t n = gid / ln.G;
-  const int gl = (int)(gid % ln.G);
+    int C, float div) {
+  typedef typename VecT<V>::T T;
+  const int lane = threadIdx.x & 63;
+  const int n = wave_uniform(blockIdx.x * WAVES + (threadIdx.x >> 6));
   if (n >= N) return;
-  const int e0 = ptr[n], e1 = ptr[n + 1];
-  for (int q = 0; q < ln.QPL; ++q) {
-    const int qd = gl + q * ln.G;
-    floatx4 acc[NSPH];
+  const int e0 = wave_uniform(ptr[n]), e1 = wave_uniform(ptr[n + 1]);
+  const int nq = C / V;
+  for (int q = lane; q < nq; q += 64) {
+    T acc[NSPH];
 #pragma unroll
-    for (int j = 0; j < NSPH; ++j) acc[j] = z4();
+    for (int j = 0; j < NSPH; ++j) acc[j] = zv<V>();
+    T nxt[NIN];
+    if (e0 < e1) {
+#pragma unroll
+      for (int mm = 0; mm < NIN; ++mm) nxt[mm] = ldv<V>(m + (int64_t)e0 * NIN * C + mm * C + V * q);
+    }
     for (int e = e0; e < e1; ++e) {
+      T in[NSPH];
+#pragma unroll
+      for (int mm = 0; mm < NSPH; ++mm) in[mm] = zv<V>();
+#pragma unroll
+      for (int mm = 0; mm < NIN; ++mm) in[mm] = nxt[mm];
+      if (e + 1 < e1) {
+#pragma unroll
+        for (int mm = 0; mm < NIN; ++mm)
+          nxt[mm] = ldv<V>(m + (int64_t)(e + 1) * NIN * C + mm * C + V * q);
+      }
       float c[NNZ];
       load_coef(coef, e, c);
       const float ev = env[e];
-      floatx4 in[NSPH], o[NSPH];
+      if (ENV_FIRST) {
 #pragma unroll
-      for (int mm = 0; mm < NSPH; ++mm) {
-        if (mm < NIN) {
-          in[mm] = ld4(m + (int64_t)e * NIN * C + mm * C + 4 * qd);
-          if (ENV_FIRST) in[mm] = in[mm] * ev;
-        } else {
-          in[mm] = z4();
-        }
+        for (int mm = 0; mm < NIN; ++mm) in[mm] = in[mm] * ev;
       }
+      T o[NSPH];
       rot_inv<NIN>(c, in, o);
 #pragma unroll
       for (int j = 0; j < NSPH; ++j) {
-        floatx4 v = o[j];
+        T v = o[j];
         if (!ENV_FIRST) v = (v * ev) / div;
         acc[j] = acc[j] + v;
       }
     }
 #pragma unroll
     for (int j = 0; j < NSPH; ++j) {
-      floatx4 v = acc[j];
-      if (res) v = v + ld4(res + n * NSPH * C + j * C + 4 * qd);
-      st4(out + n * NSPH * C + j * C + 4 * qd, v);
+      T v = acc[j];
+      if (res) v = v + ldv<V>(res + (int64_t)n * NSPH * C + j * C + V * q);
+      stv<V>(out + (int64_t)n * NSPH * C + j * C + V * q, v);
     }
   }
 }
@@ -274,65 +332,61 @@ __global__ __launch_bounds__(256) void k_rotate_env_segsum(
 // otherwise (edge-degree, forward v = ((W^T pad(m)) * env) / div):
 //   g_v2 = g_node[tgt] / div; g_v1 = g_v2 * env; g_env += <g_v2, W^T pad(m)>;
 //   g_m = (W g_v1)[:NIN];  g_coef(m,j) += <g_v1[j], pad(m)[m]>
-template <int NIN, bool ENV_FIRST>
+template <int V, int NIN, bool ENV_FIRST>
 __global__ __launch_bounds__(256) void k_rotate_env_segsum_bw(
     const float* __restrict__ g_node, const int* __restrict__ tgt, const float* __restrict__ m,
     const float* __restrict__ coef, const float* __restrict__ env, float* __restrict__ g_m,
-    float* __restrict__ g_coef, float* __restrict__ g_env, int E, int C, float div, Lanes ln) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t e = gid / ln.G;
-  const int gl = (int)(gid % ln.G);
+    float* __restrict__ g_coef, float* __restrict__ g_env, int E, int C, float div) {
+  typedef typename VecT<V>::T T;
+  __shared__ float red[WAVES][(NNZ + 1) * 4];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int e = wave_uniform(blockIdx.x * WAVES + w);
   if (e >= E) return;
+  const int nq = C / V;
   float c[NNZ];
   load_coef(coef, e, c);
   const float ev = env[e];
-  const int64_t t = tgt[e];
-  float gc[NNZ];
+  const int64_t t = wave_uniform(tgt[e]);
+  float gc[NNZ + 1];  // 35 coefficient partials + the envelope partial
 #pragma unroll
-  for (int k = 0; k < NNZ; ++k) gc[k] = 0.f;
-  float genv = 0.f;
-  for (int q = 0; q < ln.QPL; ++q) {
-    const int qd = gl + q * ln.G;
-    floatx4 gb[NSPH], mi[NSPH];
+  for (int k = 0; k <= NNZ; ++k) gc[k] = 0.f;
+  for (int q = lane; q < nq; q += 64) {
+    T gb[NSPH], mi[NSPH];
 #pragma unroll
-    for (int j = 0; j < NSPH; ++j) gb[j] = ld4(g_node + t * NSPH * C + j * C + 4 * qd);
+    for (int j = 0; j < NSPH; ++j) gb[j] = ldv<V>(g_node + t * NSPH * C + j * C + V * q);
 #pragma unroll
     for (int mm = 0; mm < NSPH; ++mm)
-      mi[mm] = mm < NIN ? ld4(m + e * NIN * C + mm * C + 4 * qd) : z4();
+      mi[mm] = mm < NIN ? ldv<V>(m + (int64_t)e * NIN * C + mm * C + V * q) : zv<V>();
     if (ENV_FIRST) {
-      floatx4 gin[NSPH], me[NSPH];
+      T gin[NSPH], me[NSPH];
       rot_fwd(c, gb, gin);
 #pragma unroll
       for (int mm = 0; mm < NSPH; ++mm) {
         me[mm] = mi[mm] * ev;
         if (mm >= NIN) continue;
-        genv += dot4(gin[mm], mi[mm]);
-        st4(g_m + e * NIN * C + mm * C + 4 * qd, gin[mm] * ev);
+        gc[NNZ] += hsum<V>(gin[mm] * mi[mm]);
+        stv<V>(g_m + (int64_t)e * NIN * C + mm * C + V * q, gin[mm] * ev);
       }
-      coef_partials<NIN>(me, gb, gc);
+      coef_partials<NIN, V>(me, gb, gc);
     } else {
-      floatx4 v1[NSPH], g1[NSPH], gin[NSPH];
+      T v1[NSPH], g1[NSPH], gin[NSPH];
       rot_inv<NIN>(c, mi, v1);
 #pragma unroll
       for (int j = 0; j < NSPH; ++j) {
-        const floatx4 g2 = gb[j] / div;
-        genv += dot4(g2, v1[j]);
+        const T g2 = gb[j] / div;
+        gc[NNZ] += hsum<V>(g2 * v1[j]);
         g1[j] = g2 * ev;
       }
       rot_fwd(c, g1, gin);
 #pragma unroll
-      for (int mm = 0; mm < NIN; ++mm) st4(g_m + e * NIN * C + mm * C + 4 * qd, gin[mm]);
-      coef_partials<NIN>(mi, g1, gc);
+      for (int mm = 0; mm < NIN; ++mm) stv<V>(g_m + (int64_t)e * NIN * C + mm * C + V * q, gin[mm]);
+      coef_partials<NIN, V>(mi, g1, gc);
     }
   }
-#pragma unroll
-  for (int k = 0; k < NNZ; ++k) gc[k] = tta_group_sum(gc[k], ln.G);
-  genv = tta_group_sum(genv, ln.G);
-  if (gl == 0) {
-#pragma unroll
-    for (int k = 0; k < NNZ; ++k) g_coef[e * NNZ + k] += gc[k];
-    g_env[e] += genv;
-  }
+  const float tot = wave_sums<NNZ + 1>(gc, red[w], lane);
+  if (lane < NNZ) g_coef[(int64_t)e * NNZ + lane] += tot;
+  if (lane == NNZ) g_env[e] += tot;
 }
 
 // -------------------------------------------------------------------------------------------
@@ -340,57 +394,84 @@ __global__ __launch_bounds__(256) void k_rotate_env_segsum_bw(
 //   g_x[n] = sum_{edges with src = n} g_mcat[e, :, 0:C] + sum_{edges with tgt = n} g_mcat[e, :, C:2C]
 // src edges come through a src-sorted permutation (src_ptr / src_perm), tgt edges are the
 // contiguous destination segments.  Optional residual: out = (src sum + tgt sum) + res.
+template <int V>
 __global__ __launch_bounds__(256) void k_node_gather_sum(
     const float* __restrict__ g_mcat, const int* __restrict__ src_ptr,
     const int* __restrict__ src_perm, const int* __restrict__ tgt_ptr,
-    const float* __restrict__ res, float* __restrict__ out, int N, int C, Lanes ln) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t n = gid / ln.G;
-  const int gl = (int)(gid % ln.G);
+    const float* __restrict__ res, float* __restrict__ out, int N, int C) {
+  typedef typename VecT<V>::T T;
+  const int lane = threadIdx.x & 63;
+  const int n = wave_uniform(blockIdx.x * WAVES + (threadIdx.x >> 6));
   if (n >= N) return;
-  const int W = 2 * C;
-  for (int q = 0; q < ln.QPL; ++q) {
-    const int qd = gl + q * ln.G;
-    floatx4 a[NSPH], b[NSPH];
+  const int W = 2 * C, nq = C / V;
+  const int s0 = wave_uniform(src_ptr[n]), s1 = wave_uniform(src_ptr[n + 1]);
+  const int t0 = wave_uniform(tgt_ptr[n]), t1 = wave_uniform(tgt_ptr[n + 1]);
+  for (int q = lane; q < nq; q += 64) {
+    T a[NSPH], b[NSPH];
 #pragma unroll
-    for (int j = 0; j < NSPH; ++j) a[j] = b[j] = z4();
-    for (int k = src_ptr[n]; k < src_ptr[n + 1]; ++k) {
-      const int64_t e = src_perm[k];
+    for (int j = 0; j < NSPH; ++j) a[j] = b[j] = zv<V>();
+    for (int k = s0; k < s1; ++k) {
+      const int64_t e = wave_uniform(src_perm[k]);
 #pragma unroll
-      for (int j = 0; j < NSPH; ++j) a[j] = a[j] + ld4(g_mcat + e * NSPH * W + j * W + 4 * qd);
+      for (int j = 0; j < NSPH; ++j) a[j] = a[j] + ldv<V>(g_mcat + e * NSPH * W + j * W + V * q);
     }
-    for (int64_t e = tgt_ptr[n]; e < tgt_ptr[n + 1]; ++e) {
+    for (int64_t e = t0; e < t1; ++e) {
 #pragma unroll
-      for (int j = 0; j < NSPH; ++j) b[j] = b[j] + ld4(g_mcat + e * NSPH * W + j * W + C + 4 * qd);
+      for (int j = 0; j < NSPH; ++j) b[j] = b[j] + ldv<V>(g_mcat + e * NSPH * W + j * W + C + V * q);
     }
 #pragma unroll
     for (int j = 0; j < NSPH; ++j) {
-      floatx4 v = a[j] + b[j];
-      if (res) v = v + ld4(res + n * NSPH * C + j * C + 4 * qd);
-      st4(out + n * NSPH * C + j * C + 4 * qd, v);
+      T v = a[j] + b[j];
+      if (res) v = v + ldv<V>(res + (int64_t)n * NSPH * C + j * C + V * q);
+      stv<V>(out + (int64_t)n * NSPH * C + j * C + V * q, v);
     }
   }
 }
 
+// Vector width for a row of W channels (W a multiple of 4): the widest of 4, 2, 1 that still
+// gives every one of the 64 lanes a vector (narrow rows leave lanes idle; wide rows loop).
+int pick_v(int64_t W) {
+  if (W >= 256) return 4;
+  if (W >= 128) return 2;
+  return 1;
+}
+
+unsigned wave_blocks(int64_t items) { return (unsigned)((items + WAVES - 1) / WAVES); }
+
 }  // namespace
 
 // =========================================================================== C ABI
+#define TTA_V_DISPATCH(V, ...)       \
+  do {                               \
+    if (V == 4) {                    \
+      constexpr int VV = 4;          \
+      __VA_ARGS__;                   \
+    } else if (V == 2) {             \
+      constexpr int VV = 2;          \
+      __VA_ARGS__;                   \
+    } else {                         \
+      constexpr int VV = 1;          \
+      __VA_ARGS__;                   \
+    }                                \
+  } while (0)
+
 extern "C" int tta_gather_rotate(const float* x, const int* src, const int* tgt,
                                  const float* coef, const float* rad, float* out, int64_t N,
                                  int64_t E, int64_t C, hipStream_t stream) {
-  Lanes ln;
-  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && lanes_for(2 * C, ln),
+  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C <= 4096,
                 "tta_gather_rotate: unsupported channel count C=%lld", (long long)C);
   TTA_CHECK_ARG(E >= 0 && N >= 0 && E < (1ll << 31), "tta_gather_rotate: bad sizes");
   if (E == 0) return tta::kOk;
   TTA_CHECK_ARG(x && src && tgt && coef && out, "tta_gather_rotate: null pointer");
-  const unsigned blocks = tta_blocks(E * ln.G, 256);
-  if (rad)
-    hipLaunchKernelGGL(k_gather_rotate<true>, dim3(blocks), dim3(256), 0, stream, x, src, tgt,
-                       coef, rad, out, (int)E, (int)C, ln);
-  else
-    hipLaunchKernelGGL(k_gather_rotate<false>, dim3(blocks), dim3(256), 0, stream, x, src, tgt,
-                       coef, rad, out, (int)E, (int)C, ln);
+  const int V = pick_v(2 * C);  // divides C: C is a multiple of 4
+  TTA_V_DISPATCH(V, {
+    if (rad)
+      hipLaunchKernelGGL((k_gather_rotate<VV, true>), dim3(wave_blocks(E)), dim3(256), 0, stream,
+                         x, src, tgt, coef, rad, out, (int)E, (int)C);
+    else
+      hipLaunchKernelGGL((k_gather_rotate<VV, false>), dim3(wave_blocks(E)), dim3(256), 0,
+                         stream, x, src, tgt, coef, rad, out, (int)E, (int)C);
+  });
   TTA_CHECK_LAUNCH("tta_gather_rotate");
   return tta::kOk;
 }
@@ -399,21 +480,24 @@ extern "C" int tta_gather_rotate_bw(const float* g_xf, const float* rad, const f
                                     const int* src, const int* tgt, const float* coef,
                                     float* g_rad, float* g_mcat, float* g_coef, int64_t N,
                                     int64_t E, int64_t C, hipStream_t stream) {
-  Lanes ln;
-  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && lanes_for(2 * C, ln),
+  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C <= 4096,
                 "tta_gather_rotate_bw: unsupported channel count C=%lld", (long long)C);
   TTA_CHECK_ARG(E >= 0 && N >= 0 && E < (1ll << 31), "tta_gather_rotate_bw: bad sizes");
   if (E == 0) return tta::kOk;
   TTA_CHECK_ARG(g_xf && x && src && tgt && coef && g_mcat && g_coef,
                 "tta_gather_rotate_bw: null pointer");
   TTA_CHECK_ARG(!rad == !g_rad, "tta_gather_rotate_bw: rad and g_rad must be given together");
-  const unsigned blocks = tta_blocks(E * ln.G, 256);
-  if (rad)
-    hipLaunchKernelGGL(k_gather_rotate_bw<true>, dim3(blocks), dim3(256), 0, stream, g_xf, rad,
-                       x, src, tgt, coef, g_rad, g_mcat, g_coef, (int)E, (int)C, ln);
-  else
-    hipLaunchKernelGGL(k_gather_rotate_bw<false>, dim3(blocks), dim3(256), 0, stream, g_xf, rad,
-                       x, src, tgt, coef, g_rad, g_mcat, g_coef, (int)E, (int)C, ln);
+  const int V = pick_v(2 * C);
+  TTA_V_DISPATCH(V, {
+    if (rad)
+      hipLaunchKernelGGL((k_gather_rotate_bw<VV, true>), dim3(wave_blocks(E)), dim3(256), 0,
+                         stream, g_xf, rad, x, src, tgt, coef, g_rad, g_mcat, g_coef, (int)E,
+                         (int)C);
+    else
+      hipLaunchKernelGGL((k_gather_rotate_bw<VV, false>), dim3(wave_blocks(E)), dim3(256), 0,
+                         stream, g_xf, rad, x, src, tgt, coef, g_rad, g_mcat, g_coef, (int)E,
+                         (int)C);
+  });
   TTA_CHECK_LAUNCH("tta_gather_rotate_bw");
   return tta::kOk;
 }
@@ -422,8 +506,7 @@ extern "C" int tta_rotate_env_segsum(const float* m, const float* coef, const fl
                                      const int* tgt_ptr, const float* res, float* out,
                                      int64_t N, int64_t E, int64_t C, int64_t n_in,
                                      int env_first, float div, hipStream_t stream) {
-  Lanes ln;
-  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && lanes_for(C, ln),
+  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C <= 4096,
                 "tta_rotate_env_segsum: unsupported channel count C=%lld", (long long)C);
   TTA_CHECK_ARG(n_in == 9 || n_in == 3, "tta_rotate_env_segsum: n_in must be 9 or 3");
   TTA_CHECK_ARG(N >= 0 && E >= 0 && N < (1ll << 31) && E < (1ll << 31),
@@ -431,15 +514,21 @@ extern "C" int tta_rotate_env_segsum(const float* m, const float* coef, const fl
   TTA_CHECK_ARG(div != 0.f, "tta_rotate_env_segsum: zero divisor");
   if (N == 0) return tta::kOk;
   TTA_CHECK_ARG(coef && env && tgt_ptr && out && (m || E == 0), "tta_rotate_env_segsum: null pointer");
-  const unsigned blocks = tta_blocks(N * ln.G, 256);
-#define TTA_LAUNCH_SEG(NIN, EF)                                                                \
-  hipLaunchKernelGGL((k_rotate_env_segsum<NIN, EF>), dim3(blocks), dim3(256), 0, stream, m, coef, \
-                     env, tgt_ptr, res, out, (int)N, (int)C, div, ln)
-  if (n_in == 9 && env_first) TTA_LAUNCH_SEG(9, true);
-  else if (n_in == 9) TTA_LAUNCH_SEG(9, false);
-  else if (env_first) TTA_LAUNCH_SEG(3, true);
-  else TTA_LAUNCH_SEG(3, false);
-#undef TTA_LAUNCH_SEG
+  const int V = pick_v(C);
+  TTA_V_DISPATCH(V, {
+    if (n_in == 9 && env_first)
+      hipLaunchKernelGGL((k_rotate_env_segsum<VV, 9, true>), dim3(wave_blocks(N)), dim3(256), 0,
+                         stream, m, coef, env, tgt_ptr, res, out, (int)N, (int)C, div);
+    else if (n_in == 9)
+      hipLaunchKernelGGL((k_rotate_env_segsum<VV, 9, false>), dim3(wave_blocks(N)), dim3(256), 0,
+                         stream, m, coef, env, tgt_ptr, res, out, (int)N, (int)C, div);
+    else if (env_first)
+      hipLaunchKernelGGL((k_rotate_env_segsum<VV, 3, true>), dim3(wave_blocks(N)), dim3(256), 0,
+                         stream, m, coef, env, tgt_ptr, res, out, (int)N, (int)C, div);
+    else
+      hipLaunchKernelGGL((k_rotate_env_segsum<VV, 3, false>), dim3(wave_blocks(N)), dim3(256), 0,
+                         stream, m, coef, env, tgt_ptr, res, out, (int)N, (int)C, div);
+  });
   TTA_CHECK_LAUNCH("tta_rotate_env_segsum");
   return tta::kOk;
 }
@@ -449,8 +538,7 @@ extern "C" int tta_rotate_env_segsum_bw(const float* g_node, const int* tgt, con
                                         float* g_coef, float* g_env, int64_t N, int64_t E,
                                         int64_t C, int64_t n_in, int env_first, float div,
                                         hipStream_t stream) {
-  Lanes ln;
-  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && lanes_for(C, ln),
+  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C <= 4096,
                 "tta_rotate_env_segsum_bw: unsupported channel count C=%lld", (long long)C);
   TTA_CHECK_ARG(n_in == 9 || n_in == 3, "tta_rotate_env_segsum_bw: n_in must be 9 or 3");
   TTA_CHECK_ARG(E >= 0 && N >= 0 && E < (1ll << 31), "tta_rotate_env_segsum_bw: bad sizes");
@@ -458,15 +546,25 @@ extern "C" int tta_rotate_env_segsum_bw(const float* g_node, const int* tgt, con
   if (E == 0) return tta::kOk;
   TTA_CHECK_ARG(g_node && tgt && m && coef && env && g_m && g_coef && g_env,
                 "tta_rotate_env_segsum_bw: null pointer");
-  const unsigned blocks = tta_blocks(E * ln.G, 256);
-#define TTA_LAUNCH_SEGBW(NIN, EF)                                                               \
-  hipLaunchKernelGGL((k_rotate_env_segsum_bw<NIN, EF>), dim3(blocks), dim3(256), 0, stream,     \
-                     g_node, tgt, m, coef, env, g_m, g_coef, g_env, (int)E, (int)C, div, ln)
-  if (n_in == 9 && env_first) TTA_LAUNCH_SEGBW(9, true);
-  else if (n_in == 9) TTA_LAUNCH_SEGBW(9, false);
-  else if (env_first) TTA_LAUNCH_SEGBW(3, true);
-  else TTA_LAUNCH_SEGBW(3, false);
-#undef TTA_LAUNCH_SEGBW
+  const int V = pick_v(C);
+  TTA_V_DISPATCH(V, {
+    if (n_in == 9 && env_first)
+      hipLaunchKernelGGL((k_rotate_env_segsum_bw<VV, 9, true>), dim3(wave_blocks(E)), dim3(256),
+                         0, stream, g_node, tgt, m, coef, env, g_m, g_coef, g_env, (int)E, (int)C,
+                         div);
+    else if (n_in == 9)
+      hipLaunchKernelGGL((k_rotate_env_segsum_bw<VV, 9, false>), dim3(wave_blocks(E)), dim3(256),
+                         0, stream, g_node, tgt, m, coef, env, g_m, g_coef, g_env, (int)E, (int)C,
+                         div);
+    else if (env_first)
+      hipLaunchKernelGGL((k_rotate_env_segsum_bw<VV, 3, true>), dim3(wave_blocks(E)), dim3(256),
+                         0, stream, g_node, tgt, m, coef, env, g_m, g_coef, g_env, (int)E, (int)C,
+                         div);
+    else
+      hipLaunchKernelGGL((k_rotate_env_segsum_bw<VV, 3, false>), dim3(wave_blocks(E)), dim3(256),
+                         0, stream, g_node, tgt, m, coef, env, g_m, g_coef, g_env, (int)E, (int)C,
+                         div);
+  });
   TTA_CHECK_LAUNCH("tta_rotate_env_segsum_bw");
   return tta::kOk;
 }
@@ -474,16 +572,17 @@ extern "C" int tta_rotate_env_segsum_bw(const float* g_node, const int* tgt, con
 extern "C" int tta_node_gather_sum(const float* g_mcat, const int* src_ptr, const int* src_perm,
                                    const int* tgt_ptr, const float* res, float* out, int64_t N,
                                    int64_t E, int64_t C, hipStream_t stream) {
-  Lanes ln;
-  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && lanes_for(C, ln),
+  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C <= 4096,
                 "tta_node_gather_sum: unsupported channel count C=%lld", (long long)C);
   TTA_CHECK_ARG(N >= 0 && E >= 0 && N < (1ll << 31), "tta_node_gather_sum: bad sizes");
   if (N == 0) return tta::kOk;
   TTA_CHECK_ARG(src_ptr && src_perm && tgt_ptr && out && (g_mcat || E == 0),
                 "tta_node_gather_sum: null pointer");
-  const unsigned blocks = tta_blocks(N * ln.G, 256);
-  hipLaunchKernelGGL(k_node_gather_sum, dim3(blocks), dim3(256), 0, stream, g_mcat, src_ptr,
-                     src_perm, tgt_ptr, res, out, (int)N, (int)C, ln);
+  const int V = pick_v(C);
+  TTA_V_DISPATCH(V, {
+    hipLaunchKernelGGL((k_node_gather_sum<VV>), dim3(wave_blocks(N)), dim3(256), 0, stream,
+                       g_mcat, src_ptr, src_perm, tgt_ptr, res, out, (int)N, (int)C);
+  });
   TTA_CHECK_LAUNCH("tta_node_gather_sum");
   return tta::kOk;
 }

@@ -83,21 +83,25 @@ int tta_node_gather_sum(const float* g_mcat, const int* src_ptr, const int* src_
                         int64_t C, tta_stream_t stream);
 
 /* ---------------------------------------------------------------- element / row-wise
- * Gate: y[r,0] = silu(x[r,0]); y[r,c] = x[r,c] sigmoid(gating[r, idx8[c-1]]).  x, y [R,9,H],
- * gating [R, L*H].  activation.py:29-70 (m-primed idx), spectral.py:129-144 (natural idx);
- * backward forces.py:104-130 (and ttnn.experimental.fused_gate, fused_gate.hpp:14-21). */
+ * Gate: y[r,0] = silu(x[r,0]); y[r,c] = x[r,c] sigmoid(gating[r, idx8[c-1]]).  x [R,9,H] rows of
+ * stride ldx, gating [R, L*H] rows of stride ldg (column blocks of one GEMM output allowed),
+ * y / g_y contiguous [R,9,H]; g_x / g_gating share the strides of x / gating.
+ * activation.py:29-70 (m-primed idx), spectral.py:129-144 (natural idx); backward
+ * forces.py:104-130 (and ttnn.experimental.fused_gate, fused_gate.hpp:14-21). */
 int tta_gate_fwd(const float* x, const float* gating, float* y, int64_t R, int64_t H, int64_t L,
-                 const int* idx8, tta_stream_t stream);
+                 int64_t ldx, int64_t ldg, const int* idx8, tta_stream_t stream);
 int tta_gate_bwd(const float* g_y, const float* x, const float* gating, float* g_x,
-                 float* g_gating, int64_t R, int64_t H, int64_t L, const int* idx8,
-                 tta_stream_t stream);
+                 float* g_gating, int64_t R, int64_t H, int64_t L, int64_t ldx, int64_t ldg,
+                 const int* idx8, tta_stream_t stream);
 
 /* Radial MLP LayerNorm + SiLU: nrm = LN(a), s = silu(nrm) (so2.py:101-115) and its backward
- * g_a (so2.py:117-143; ttnn.experimental.fused_ln_bw, fused_ln_bw.hpp:14-21). */
+ * g_a (so2.py:117-143; ttnn.experimental.fused_ln_bw, fused_ln_bw.hpp:14-21).  Row strides:
+ * a / nrm lda, s lds, g ldg, g_a ldo. */
 int tta_ln_silu_fwd(const float* a, const float* gamma, const float* beta, float* nrm, float* s,
-                    int64_t R, int64_t n, float eps, tta_stream_t stream);
+                    int64_t R, int64_t n, int64_t lda, int64_t lds, float eps, tta_stream_t stream);
 int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm, const float* gamma,
-                    float* g_a, int64_t R, int64_t n, float eps, tta_stream_t stream);
+                    float* g_a, int64_t R, int64_t n, int64_t ldg, int64_t lda, int64_t ldo,
+                    float eps, tta_stream_t stream);
 
 /* RMSNormSH (norm.py:59-111) with an optional l=0 addend (the system embedding of
  * model.py:164-167); inv [N] kept for the backward (forces.py:49-98; res = residual adjoint). */

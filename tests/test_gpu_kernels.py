@@ -281,13 +281,23 @@ def test_gate_fwd_bwd(nat, natural):
     f = lambda t: t.float().to(DEV).contiguous()
     idx_t = torch.tensor(idx, dtype=torch.int32, device=DEV)
     yo = torch.empty(R, 9, H, device=DEV)
-    nat.gate_fwd(f(x), f(gat), yo, idx_t)
+    nat.gate_fwd(f(x), f(gat), yo, idx_t, R=R, H=H, L=2)
     gxo, ggo = torch.empty(R, 9, H, device=DEV), torch.empty(R, 2 * H, device=DEV)
-    nat.gate_bwd(f(gy), f(x), f(gat), gxo, ggo, idx_t)
+    nat.gate_bwd(f(gy), f(x), f(gat), gxo, ggo, idx_t, R=R, H=H, L=2)
     torch.cuda.synchronize()
     assert (yo.cpu().double() - y.detach()).abs().max() < 1e-5
     assert (gxo.cpu().double() - gx).abs().max() < 1e-5
     assert (ggo.cpu().double() - gg).abs().max() < 1e-5
+    # the combined row layout [gating | x] of the conv-1 GEMM output (row stride 11 H)
+    comb = torch.cat([gat, x.reshape(R, 9 * H)], 1).float().to(DEV).contiguous()
+    yo2 = torch.empty(R, 9, H, device=DEV)
+    nat.gate_fwd(comb[:, 2 * H:], comb, yo2, idx_t, R=R, H=H, L=2, ldx=11 * H, ldg=11 * H)
+    gcomb = torch.zeros(R, 11 * H, device=DEV)
+    nat.gate_bwd(f(gy), comb[:, 2 * H:], comb, gcomb[:, 2 * H:], gcomb, idx_t, R=R, H=H, L=2,
+                 ldx=11 * H, ldg=11 * H)
+    torch.cuda.synchronize()
+    assert torch.equal(yo2, yo)
+    assert torch.equal(gcomb[:, 2 * H:].reshape(R, 9, H), gxo) and torch.equal(gcomb[:, :2 * H], ggo)
 
 
 @pytest.mark.parametrize("n", [16, 128, 200])
@@ -304,12 +314,24 @@ def test_ln_silu_fwd_bwd(nat, n):
     (ga,) = torch.autograd.grad((s * gs).sum(), [ar])
     f = lambda t: t.float().to(DEV).contiguous()
     no, so, gao = (torch.empty(R, n, device=DEV) for _ in range(3))
-    nat.ln_silu_fwd(f(a), f(gam), f(bet), no, so)
-    nat.ln_silu_bwd(f(gs), f(a), no, f(gam), gao)
+    nat.ln_silu_fwd(f(a), f(gam), f(bet), no, so, R=R, n=n)
+    nat.ln_silu_bwd(f(gs), f(a), no, f(gam), gao, R=R, n=n)
     torch.cuda.synchronize()
     assert (no.cpu().double() - nrm.detach()).abs().max() < 1e-5
     assert (so.cpu().double() - s.detach()).abs().max() < 1e-5
     assert (gao.cpu().double() - ga).abs().max() < 1e-4
+    # strided rows: a / nrm / g_a as a column block of a wider buffer
+    wide = torch.zeros(R, 3 * n, device=DEV)
+    wide[:, n:2 * n] = f(a)
+    nw, gw = torch.zeros(R, 3 * n, device=DEV), torch.zeros(R, 3 * n, device=DEV)
+    so2 = torch.empty(R, n, device=DEV)
+    nat.ln_silu_fwd(wide[:, n:2 * n], f(gam), f(bet), nw[:, n:2 * n], so2, R=R, n=n, lda=3 * n,
+                    lds=n)
+    nat.ln_silu_bwd(f(gs), wide[:, n:2 * n], nw[:, n:2 * n], f(gam), gw[:, n:2 * n], R=R, n=n,
+                    ldg=n, lda=3 * n, ldo=3 * n)
+    torch.cuda.synchronize()
+    assert torch.equal(so2, so) and torch.equal(gw[:, n:2 * n], gao)
+    assert gw[:, :n].abs().max() == 0 and gw[:, 2 * n:].abs().max() == 0
 
 
 @pytest.mark.parametrize("C", [16, 128, 96])

@@ -6,10 +6,8 @@
 // Epilogues: 0 store; 1 store silu(v); 2 accumulate C += v; 3 store v to C and silu(v) to C2
 // (pre-activation kept for the backward); 4 store v * silu'(aux) (aux shares C's layout).
 //
-// Block tile 128x128x16, 256 threads = 4 waves in a 2x2 arrangement, each wave owns a 64x64
-// sub-tile = 4x4 MFMA tiles of 16x16 (16 fp32x4 accumulators).  A is staged k-major in LDS so
-// that the 16 lanes sharing a k read 16 consecutive rows; B is staged row-major.  Two LDS
-// buffers with register prefetch of the next k-slab give one barrier per k-step.
+// Block tiles 128x128, 64x128 or 32x64 (x16 in k), 256 threads = 4 waves in a 2x2 arrangement;
+// the largest tile whose grid still fills the chip is used (dispatch()).
 //
 // MFMA 16x16x4 f32 operand layout (one block): lane l supplies A[l%16][l/16] and B[l/16][l%16];
 // the result D[4*(l/16)+r][l%16], r=0..3, lands in accumulator element r of lane l.
@@ -19,7 +17,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 16, PAD = 4;
+constexpr int BK = 16, PAD = 4;
 
 struct GemmArgs {
   const float* A;
@@ -36,86 +34,108 @@ struct GemmArgs {
 
 enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ACCUM = 2, EPI_PRE_SILU = 3, EPI_SILU_GRAD = 4 };
 
-template <bool VEC>
+// Block tile BM x BN x BK with 4 waves in a WGM x WGN grid; each wave owns (BM/WGM) x (BN/WGN)
+// = TI x TJ MFMA tiles of 16 x 16.  Loads stage A k-major (the 16 lanes sharing a k read 16
+// consecutive rows) and B row-major in LDS; per-thread register prefetch of the next k-slab and
+// two LDS buffers give one barrier per k-step.
+template <int BM, int BN, int WGM, int WGN>
+struct Tile {
+  static constexpr int TI = BM / WGM / 16;
+  static constexpr int TJ = BN / WGN / 16;
+  static constexpr int A_VEC = BM * BK / 4;   // float4 loads of the A slab
+  static constexpr int B_VEC = BK * BN / 4;
+  static constexpr int A_PER_T = (A_VEC + 255) / 256;
+  static constexpr int B_PER_T = (B_VEC + 255) / 256;
+  static_assert(WGM * WGN == 4, "4 waves per block");
+  static_assert(TI >= 1 && TJ >= 1, "wave tile at least 16 x 16");
+};
+
+template <class TL, int BM, bool VEC>
 __device__ __forceinline__ void load_a(const GemmArgs& p, const float* A, int m0, int k0, int t,
-                                       float (&ra)[8]) {
-  const int kq = (t & 3) * 4;
+                                       float (&ra)[TL::A_PER_T * 4]) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int r = (t >> 2) + 64 * h;
-    const int row = m0 + r;
-    const int k = k0 + kq;
+  for (int h = 0; h < TL::A_PER_T; ++h) {
+    const int i = t + 256 * h;
+    const int row = m0 + i / (BK / 4);
+    const int k = k0 + (i % (BK / 4)) * 4;
+    const bool in = i < TL::A_VEC && row < p.M;
     if (VEC) {
       floatx4 v = {0.f, 0.f, 0.f, 0.f};
-      if (row < p.M && k < p.K) v = *reinterpret_cast<const floatx4*>(A + (int64_t)row * p.lda + k);
-      ra[4 * h + 0] = v[0];
-      ra[4 * h + 1] = v[1];
-      ra[4 * h + 2] = v[2];
-      ra[4 * h + 3] = v[3];
+      if (in && k < p.K) v = *reinterpret_cast<const floatx4*>(A + (int64_t)row * p.lda + k);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ra[4 * h + c] = v[c];
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        ra[4 * h + i] = (row < p.M && k + i < p.K) ? A[(int64_t)row * p.lda + k + i] : 0.f;
+      for (int c = 0; c < 4; ++c)
+        ra[4 * h + c] = (in && k + c < p.K) ? A[(int64_t)row * p.lda + k + c] : 0.f;
     }
   }
 }
 
-template <bool VEC>
+template <class TL, int BN, bool VEC>
 __device__ __forceinline__ void load_b(const GemmArgs& p, const float* B, int n0, int k0, int t,
-                                       float (&rb)[8]) {
-  const int nq = (t & 31) * 4;
+                                       float (&rb)[TL::B_PER_T * 4]) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int kr = (t >> 5) + 8 * h;
-    const int k = k0 + kr;
-    const int col = n0 + nq;
+  for (int h = 0; h < TL::B_PER_T; ++h) {
+    const int i = t + 256 * h;
+    const int k = k0 + i / (BN / 4);
+    const int col = n0 + (i % (BN / 4)) * 4;
+    const bool in = i < TL::B_VEC && k < p.K;
     if (VEC) {
       floatx4 v = {0.f, 0.f, 0.f, 0.f};
-      if (k < p.K && col < p.N) v = *reinterpret_cast<const floatx4*>(B + (int64_t)k * p.ldb + col);
-      rb[4 * h + 0] = v[0];
-      rb[4 * h + 1] = v[1];
-      rb[4 * h + 2] = v[2];
-      rb[4 * h + 3] = v[3];
+      if (in && col < p.N) v = *reinterpret_cast<const floatx4*>(B + (int64_t)k * p.ldb + col);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) rb[4 * h + c] = v[c];
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        rb[4 * h + i] = (k < p.K && col + i < p.N) ? B[(int64_t)k * p.ldb + col + i] : 0.f;
+      for (int c = 0; c < 4; ++c)
+        rb[4 * h + c] = (in && col + c < p.N) ? B[(int64_t)k * p.ldb + col + c] : 0.f;
     }
   }
 }
 
-__device__ __forceinline__ void store_a(float (*As)[BM + PAD], int t, const float (&ra)[8]) {
-  const int kq = (t & 3) * 4;
+template <class TL, int BM>
+__device__ __forceinline__ void store_a(float (*As)[BM + PAD], int t,
+                                        const float (&ra)[TL::A_PER_T * 4]) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int r = (t >> 2) + 64 * h;
+  for (int h = 0; h < TL::A_PER_T; ++h) {
+    const int i = t + 256 * h;
+    if (i >= TL::A_VEC) continue;
+    const int r = i / (BK / 4);
+    const int kq = (i % (BK / 4)) * 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) As[kq + i][r] = ra[4 * h + i];
+    for (int c = 0; c < 4; ++c) As[kq + c][r] = ra[4 * h + c];
   }
 }
 
-__device__ __forceinline__ void store_b(float (*Bs)[BN + PAD], int t, const float (&rb)[8]) {
-  const int nq = (t & 31) * 4;
+template <class TL, int BN>
+__device__ __forceinline__ void store_b(float (*Bs)[BN + PAD], int t,
+                                        const float (&rb)[TL::B_PER_T * 4]) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int kr = (t >> 5) + 8 * h;
+  for (int h = 0; h < TL::B_PER_T; ++h) {
+    const int i = t + 256 * h;
+    if (i >= TL::B_VEC) continue;
+    const int kr = i / (BN / 4);
+    const int nq = (i % (BN / 4)) * 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) Bs[kr][nq + i] = rb[4 * h + i];
+    for (int c = 0; c < 4; ++c) Bs[kr][nq + c] = rb[4 * h + c];
   }
 }
 
 // The epilogue is a (wave-uniform) runtime switch so every GEMM of the step is one kernel
-// symbol; it runs once per output element and costs nothing next to the K loop.
-template <bool VEC>
+// symbol per tile shape; it runs once per output element and costs nothing next to the K loop.
+template <int BM, int BN, int WGM, int WGN, bool VEC>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
-  const int EPI = p.epi;
+  typedef Tile<BM, BN, WGM, WGN> TL;
+  constexpr int TI = TL::TI, TJ = TL::TJ;
   __shared__ float As[2][BK][BM + PAD];
   __shared__ float Bs[2][BK][BN + PAD];
 
+  const int EPI = p.epi;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int n0 = blockIdx.x * BN;
   const int m0 = blockIdx.y * BM;
   const float* A = p.A + (int64_t)blockIdx.z * p.sA;
@@ -125,59 +145,60 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
   const float* aux = p.aux ? p.aux + (int64_t)blockIdx.z * p.sC : nullptr;
   const float* bias = p.bias ? p.bias + (int64_t)blockIdx.z * p.sBias : nullptr;
 
-  floatx4 acc[4][4];
+  floatx4 acc[TI][TJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  float ra[8], rb[8];
+  float ra[TL::A_PER_T * 4], rb[TL::B_PER_T * 4];
   const int nk = (p.K + BK - 1) / BK;
-  load_a<VEC>(p, A, m0, 0, t, ra);
-  load_b<VEC>(p, B, n0, 0, t, rb);
-  store_a(As[0], t, ra);
-  store_b(Bs[0], t, rb);
+  load_a<TL, BM, VEC>(p, A, m0, 0, t, ra);
+  load_b<TL, BN, VEC>(p, B, n0, 0, t, rb);
+  store_a<TL, BM>(As[0], t, ra);
+  store_b<TL, BN>(Bs[0], t, rb);
   __syncthreads();
 
   const int li = lane & 15;
   const int lk = lane >> 4;
+  const int rbase = wm * (BM / WGM), cbase = wn * (BN / WGN);
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < nk) {
-      load_a<VEC>(p, A, m0, (kt + 1) * BK, t, ra);
-      load_b<VEC>(p, B, n0, (kt + 1) * BK, t, rb);
+      load_a<TL, BM, VEC>(p, A, m0, (kt + 1) * BK, t, ra);
+      load_b<TL, BN, VEC>(p, B, n0, (kt + 1) * BK, t, rb);
     }
 #pragma unroll
     for (int kk = 0; kk < BK / 4; ++kk) {
       const int k = 4 * kk + lk;
-      float a[4], b[4];
+      float a[TI], b[TJ];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = As[buf][k][wm * 64 + i * 16 + li];
+      for (int i = 0; i < TI; ++i) a[i] = As[buf][k][rbase + i * 16 + li];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = Bs[buf][k][wn * 64 + j * 16 + li];
+      for (int j = 0; j < TJ; ++j) b[j] = Bs[buf][k][cbase + j * 16 + li];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < TJ; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
     }
     if (kt + 1 < nk) {
-      store_a(As[buf ^ 1], t, ra);
-      store_b(Bs[buf ^ 1], t, rb);
+      store_a<TL, BM>(As[buf ^ 1], t, ra);
+      store_b<TL, BN>(Bs[buf ^ 1], t, rb);
     }
     __syncthreads();
   }
 
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = n0 + wn * 64 + j * 16 + li;
+  for (int j = 0; j < TJ; ++j) {
+    const int col = n0 + cbase + j * 16 + li;
     if (col >= p.N) continue;
     const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < TI; ++i) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 64 + i * 16 + lk * 4 + r;
+        const int row = m0 + rbase + i * 16 + lk * 4 + r;
         if (row >= p.M) continue;
         float v = acc[i][j][r] + bv;
         const int64_t off = (int64_t)row * p.ldc + col;
@@ -191,14 +212,29 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
   }
 }
 
+template <int BM, int BN, int WGM, int WGN>
 int launch(const GemmArgs& p, int64_t batch, bool vec, hipStream_t s) {
   dim3 grid(tta_blocks(p.N, BN), tta_blocks(p.M, BM), (unsigned)batch);
+  if (grid.y > 65535) {
+    tta::set_error("tta_gemm_f32: grid too large");
+    return tta::kBadArgument;
+  }
   if (vec)
-    hipLaunchKernelGGL((gemm_f32_kernel<true>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, true>), grid, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_f32_kernel<false>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, false>), grid, dim3(256), 0, s, p);
   TTA_CHECK_LAUNCH("tta_gemm_f32");
   return tta::kOk;
+}
+
+// Tile shape per call: 128 x 128 when the grid already fills the chip (>= 960 blocks, about four
+// resident blocks per CU), 64 x 128 for mid-size grids, 32 x 64 for the small node-level GEMMs.
+int dispatch(const GemmArgs& p, int64_t batch, bool vec, hipStream_t s) {
+  const int64_t big = (int64_t)tta_blocks(p.M, 128) * tta_blocks(p.N, 128) * batch;
+  const int64_t mid = (int64_t)tta_blocks(p.M, 64) * tta_blocks(p.N, 128) * batch;
+  if (big >= 960) return launch<128, 128, 2, 2>(p, batch, vec, s);
+  if (mid >= 512) return launch<64, 128, 2, 2>(p, batch, vec, s);
+  return launch<32, 64, 2, 2>(p, batch, vec, s);
 }
 
 }  // namespace
@@ -211,7 +247,7 @@ extern "C" int tta_gemm_f32(const float* A, const float* B, float* C, const floa
   TTA_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tta_gemm_f32: negative size");
   TTA_CHECK_ARG(M < (int64_t)1 << 31 && N < (int64_t)1 << 31 && K < (int64_t)1 << 31,
                 "tta_gemm_f32: size exceeds int32");
-  TTA_CHECK_ARG(tta_blocks(M, BM) <= 65535 && batch <= 65535, "tta_gemm_f32: grid too large");
+  TTA_CHECK_ARG(tta_blocks(M, 32) <= 65535 && batch <= 65535, "tta_gemm_f32: grid too large");
   TTA_CHECK_ARG(epilogue >= 0 && epilogue <= 4, "tta_gemm_f32: bad epilogue %d", epilogue);
   TTA_CHECK_ARG(epilogue != EPI_PRE_SILU || C2, "tta_gemm_f32: epilogue 3 needs C2");
   TTA_CHECK_ARG(epilogue != EPI_SILU_GRAD || aux, "tta_gemm_f32: epilogue 4 needs aux");
@@ -223,5 +259,5 @@ extern "C" int tta_gemm_f32(const float* A, const float* B, float* C, const floa
   const bool vec = (K % 4 == 0) && (N % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
                    (sA % 4 == 0) && (sB % 4 == 0) && ((uintptr_t)A % 16 == 0) &&
                    ((uintptr_t)B % 16 == 0);
-  return launch(p, batch, vec, stream);
+  return dispatch(p, batch, vec, stream);
 }

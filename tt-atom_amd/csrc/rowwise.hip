@@ -12,40 +12,42 @@ struct GateIdx {
 
 // GateActivation (activation.py:29-70, spectral.py:129-144):
 //   y[r, 0, h] = silu(x[r, 0, h]);  y[r, c, h] = x[r, c, h] * sigmoid(gating[r, idx[c-1] * H + h])
+// x and gating rows have strides ldx / ldg (they may be column blocks of one GEMM output row).
 __global__ __launch_bounds__(256) void k_gate_fwd(const float* __restrict__ x,
                                                   const float* __restrict__ gating,
                                                   float* __restrict__ y, int64_t R, int H, int L,
-                                                  GateIdx idx) {
+                                                  int64_t ldx, int64_t ldg, GateIdx idx) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= R * H) return;
   const int64_t r = gid / H;
   const int h = (int)(gid % H);
-  const float* xr = x + r * 9 * H;
+  const float* xr = x + r * ldx;
   float* yr = y + r * 9 * H;
   float sg[8];
-  for (int t = 0; t < L; ++t) sg[t] = tta_sigmoid_acc(gating[r * L * H + t * H + h]);
+  for (int t = 0; t < L; ++t) sg[t] = tta_sigmoid_acc(gating[r * ldg + t * H + h]);
   yr[h] = tta_silu(xr[h]);
 #pragma unroll
   for (int c = 1; c < 9; ++c) yr[c * H + h] = xr[c * H + h] * sg[idx.v[c - 1]];
 }
 
 // Backward (forces.py:104-130): g_x and g_gating = sigmoid'(gating) * sum_c g_y[c] x[c].
+// g_x rows share x's stride ldx, g_gating rows share gating's stride ldg.
 __global__ __launch_bounds__(256) void k_gate_bwd(const float* __restrict__ g_y,
                                                   const float* __restrict__ x,
                                                   const float* __restrict__ gating,
                                                   float* __restrict__ g_x,
                                                   float* __restrict__ g_gating, int64_t R, int H,
-                                                  int L, GateIdx idx) {
+                                                  int L, int64_t ldx, int64_t ldg, GateIdx idx) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= R * H) return;
   const int64_t r = gid / H;
   const int h = (int)(gid % H);
-  const float* xr = x + r * 9 * H;
+  const float* xr = x + r * ldx;
   const float* gr = g_y + r * 9 * H;
-  float* gx = g_x + r * 9 * H;
+  float* gx = g_x + r * ldx;
   float sg[8], acc[8];
   for (int t = 0; t < L; ++t) {
-    sg[t] = tta_sigmoid_acc(gating[r * L * H + t * H + h]);
+    sg[t] = tta_sigmoid_acc(gating[r * ldg + t * H + h]);
     acc[t] = 0.f;
   }
   gx[h] = gr[h] * tta_silu_grad(xr[h]);
@@ -56,22 +58,23 @@ __global__ __launch_bounds__(256) void k_gate_bwd(const float* __restrict__ g_y,
     gx[c * H + h] = g * sg[t];
     acc[t] += g * xr[c * H + h];
   }
-  for (int t = 0; t < L; ++t) g_gating[r * L * H + t * H + h] = acc[t] * (sg[t] * (1.f - sg[t]));
+  for (int t = 0; t < L; ++t) g_gating[r * ldg + t * H + h] = acc[t] * (sg[t] * (1.f - sg[t]));
 }
 
 // ------------------------------------------------------------------ LayerNorm + SiLU (radial MLP)
 // One wave per row.  Forward (so2.py:101-115 / geometry.py:161-168):
 //   nrm = (a - mean) * rstd * gamma + beta,  s = silu(nrm)
+// a and nrm rows have stride lda, s rows stride lds.
 __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a,
                                                      const float* __restrict__ gamma,
                                                      const float* __restrict__ beta,
                                                      float* __restrict__ nrm,
                                                      float* __restrict__ s, int64_t R, int n,
-                                                     float eps) {
+                                                     int64_t lda, int64_t lds, float eps) {
   const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
   if (row >= R) return;
-  const float* ar = a + row * n;
+  const float* ar = a + row * lda;
   float sum = 0.f;
   for (int i = lane; i < n; i += 64) sum += ar[i];
   const float mean = tta_group_sum(sum, 64) / n;
@@ -84,24 +87,26 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
   const float rstd = 1.0f / sqrtf(var + eps);
   for (int i = lane; i < n; i += 64) {
     const float v = (ar[i] - mean) * rstd * gamma[i] + beta[i];
-    nrm[row * n + i] = v;
-    s[row * n + i] = tta_silu(v);
+    nrm[row * lda + i] = v;
+    s[row * lds + i] = tta_silu(v);
   }
 }
 
 // Backward of silu(layer_norm(a)) w.r.t. a (so2.py:117-143):
 //   gy = g * silu'(nrm) * gamma;  xhat = (a - mean) * rstd;
 //   g_a = rstd * (gy - mean(gy) - xhat * mean(gy * xhat))
+// g rows stride ldg, a / nrm rows stride lda, g_a rows stride ldo.
 __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g,
                                                      const float* __restrict__ a,
                                                      const float* __restrict__ nrm,
                                                      const float* __restrict__ gamma,
                                                      float* __restrict__ g_a, int64_t R, int n,
+                                                     int64_t ldg, int64_t lda, int64_t ldo,
                                                      float eps) {
   const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
   if (row >= R) return;
-  const float* ar = a + row * n;
+  const float* ar = a + row * lda;
   float sum = 0.f;
   for (int i = lane; i < n; i += 64) sum += ar[i];
   const float mean = tta_group_sum(sum, 64) / n;
@@ -113,7 +118,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   const float rstd = 1.0f / sqrtf(tta_group_sum(sq, 64) / n + eps);
   float m1 = 0.f, m2 = 0.f;
   for (int i = lane; i < n; i += 64) {
-    const float gy = g[row * n + i] * tta_silu_grad(nrm[row * n + i]) * gamma[i];
+    const float gy = g[row * ldg + i] * tta_silu_grad(nrm[row * lda + i]) * gamma[i];
     const float xh = (ar[i] - mean) * rstd;
     m1 += gy;
     m2 += gy * xh;
@@ -121,9 +126,9 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   m1 = tta_group_sum(m1, 64) / n;
   m2 = tta_group_sum(m2, 64) / n;
   for (int i = lane; i < n; i += 64) {
-    const float gy = g[row * n + i] * tta_silu_grad(nrm[row * n + i]) * gamma[i];
+    const float gy = g[row * ldg + i] * tta_silu_grad(nrm[row * lda + i]) * gamma[i];
     const float xh = (ar[i] - mean) * rstd;
-    g_a[row * n + i] = rstd * (gy - m1 - xh * m2);
+    g_a[row * ldo + i] = rstd * (gy - m1 - xh * m2);
   }
 }
 
@@ -260,8 +265,10 @@ __global__ __launch_bounds__(256) void k_fill(float* __restrict__ out, int64_t n
 }  // namespace
 
 extern "C" int tta_gate_fwd(const float* x, const float* gating, float* y, int64_t R, int64_t H,
-                            int64_t L, const int* idx8, hipStream_t stream) {
+                            int64_t L, int64_t ldx, int64_t ldg, const int* idx8,
+                            hipStream_t stream) {
   TTA_CHECK_ARG(R >= 0 && H > 0 && L >= 1 && L <= 8, "tta_gate_fwd: bad sizes");
+  TTA_CHECK_ARG(ldx >= 9 * H && ldg >= L * H, "tta_gate_fwd: row stride too small");
   TTA_CHECK_ARG(idx8, "tta_gate_fwd: null index table");
   GateIdx gi;
   for (int i = 0; i < 8; ++i) {
@@ -271,15 +278,16 @@ extern "C" int tta_gate_fwd(const float* x, const float* gating, float* y, int64
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(x && gating && y, "tta_gate_fwd: null pointer");
   hipLaunchKernelGGL(k_gate_fwd, dim3(tta_blocks(R * H, 256)), dim3(256), 0, stream, x, gating, y,
-                     R, (int)H, (int)L, gi);
+                     R, (int)H, (int)L, ldx, ldg, gi);
   TTA_CHECK_LAUNCH("tta_gate_fwd");
   return tta::kOk;
 }
 
 extern "C" int tta_gate_bwd(const float* g_y, const float* x, const float* gating, float* g_x,
-                            float* g_gating, int64_t R, int64_t H, int64_t L, const int* idx8,
-                            hipStream_t stream) {
+                            float* g_gating, int64_t R, int64_t H, int64_t L, int64_t ldx,
+                            int64_t ldg, const int* idx8, hipStream_t stream) {
   TTA_CHECK_ARG(R >= 0 && H > 0 && L >= 1 && L <= 8, "tta_gate_bwd: bad sizes");
+  TTA_CHECK_ARG(ldx >= 9 * H && ldg >= L * H, "tta_gate_bwd: row stride too small");
   TTA_CHECK_ARG(idx8, "tta_gate_bwd: null index table");
   GateIdx gi;
   for (int i = 0; i < 8; ++i) {
@@ -289,30 +297,31 @@ extern "C" int tta_gate_bwd(const float* g_y, const float* x, const float* gatin
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(g_y && x && gating && g_x && g_gating, "tta_gate_bwd: null pointer");
   hipLaunchKernelGGL(k_gate_bwd, dim3(tta_blocks(R * H, 256)), dim3(256), 0, stream, g_y, x,
-                     gating, g_x, g_gating, R, (int)H, (int)L, gi);
+                     gating, g_x, g_gating, R, (int)H, (int)L, ldx, ldg, gi);
   TTA_CHECK_LAUNCH("tta_gate_bwd");
   return tta::kOk;
 }
 
 extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* beta, float* nrm,
-                               float* s, int64_t R, int64_t n, float eps, hipStream_t stream) {
-  TTA_CHECK_ARG(R >= 0 && n > 0, "tta_ln_silu_fwd: bad sizes");
+                               float* s, int64_t R, int64_t n, int64_t lda, int64_t lds,
+                               float eps, hipStream_t stream) {
+  TTA_CHECK_ARG(R >= 0 && n > 0 && lda >= n && lds >= n, "tta_ln_silu_fwd: bad sizes");
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(a && gamma && beta && nrm && s, "tta_ln_silu_fwd: null pointer");
   hipLaunchKernelGGL(k_ln_silu_fwd, dim3(tta_blocks(R * 64, 256)), dim3(256), 0, stream, a, gamma,
-                     beta, nrm, s, R, (int)n, eps);
+                     beta, nrm, s, R, (int)n, lda, lds, eps);
   TTA_CHECK_LAUNCH("tta_ln_silu_fwd");
   return tta::kOk;
 }
 
 extern "C" int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm,
-                               const float* gamma, float* g_a, int64_t R, int64_t n, float eps,
-                               hipStream_t stream) {
-  TTA_CHECK_ARG(R >= 0 && n > 0, "tta_ln_silu_bwd: bad sizes");
+                               const float* gamma, float* g_a, int64_t R, int64_t n, int64_t ldg,
+                               int64_t lda, int64_t ldo, float eps, hipStream_t stream) {
+  TTA_CHECK_ARG(R >= 0 && n > 0 && ldg >= n && lda >= n && ldo >= n, "tta_ln_silu_bwd: bad sizes");
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(g && a && nrm && gamma && g_a, "tta_ln_silu_bwd: null pointer");
   hipLaunchKernelGGL(k_ln_silu_bwd, dim3(tta_blocks(R * 64, 256)), dim3(256), 0, stream, g, a, nrm,
-                     gamma, g_a, R, (int)n, eps);
+                     gamma, g_a, R, (int)n, ldg, lda, ldo, eps);
   TTA_CHECK_LAUNCH("tta_ln_silu_bwd");
   return tta::kOk;
 }

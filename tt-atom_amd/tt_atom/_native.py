@@ -33,10 +33,10 @@ _SIGS = {
     "tta_rotate_env_segsum_bw": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _F,
                                  _P],
     "tta_node_gather_sum": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
-    "tta_gate_fwd": [_P, _P, _P, _I64, _I64, _I64, _P, _P],
-    "tta_gate_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _P],
-    "tta_ln_silu_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _F, _P],
-    "tta_ln_silu_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _F, _P],
+    "tta_gate_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
+    "tta_gate_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
+    "tta_ln_silu_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P],
+    "tta_ln_silu_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "tta_rmsnorm_sh_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _P],
     "tta_rmsnorm_sh_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _P],
     "tta_silu_bwd": [_P, _P, _P, _I64, _P],
@@ -118,6 +118,19 @@ def _ptr(t, dtype=torch.float32, numel=None, name="tensor", contiguous=True):
 
 def _i32(t, numel=None, name="index"):
     return _ptr(t, torch.int32, numel, name)
+
+
+def _rows(t, rows, ld, width, name="tensor"):
+    """Pointer of a row-strided fp32 view; checks that rows x width at stride ld stay inside the
+    tensor's storage (the kernels index ptr[r * ld + c] for r < rows, c < width)."""
+    if not t.is_cuda or t.dtype != torch.float32:
+        raise RuntimeError(f"{name} must be an fp32 device tensor")
+    if rows == 0:
+        return t.data_ptr()
+    need = t.storage_offset() + (rows - 1) * ld + width
+    if ld < width or need * 4 > t.untyped_storage().nbytes():
+        raise RuntimeError(f"{name}: {rows} rows of {width} at stride {ld} exceed its storage")
+    return t.data_ptr()
 
 
 # ----------------------------------------------------------------------------- GEMM
@@ -231,36 +244,40 @@ def node_gather_sum(g_mcat, src_ptr, src_perm, tgt_ptr, res, out):
 
 
 # ----------------------------------------------------------------------------- row-wise
-def gate_fwd(x, gating, y, idx8):
-    R = x.shape[0]
-    H = x.numel() // (9 * R) if R else 0
-    L = gating.shape[1] // H if R else 1
-    _call("tta_gate_fwd", _ptr(x, name="x"), _ptr(gating, numel=R * L * H, name="gating"),
-          _ptr(y, numel=R * 9 * H, name="y"), R, H, L, _i32(idx8, 8, "idx8"), _stream())
+def gate_fwd(x, gating, y, idx8, *, R, H, L, ldx=None, ldg=None):
+    """x rows [9*H] at stride ldx, gating rows [L*H] at stride ldg, y contiguous [R, 9, H]."""
+    ldx = 9 * H if ldx is None else ldx
+    ldg = L * H if ldg is None else ldg
+    _call("tta_gate_fwd", _rows(x, R, ldx, 9 * H, "x"), _rows(gating, R, ldg, L * H, "gating"),
+          _ptr(y, numel=R * 9 * H, name="y"), R, H, L, ldx, ldg, _i32(idx8, 8, "idx8"),
+          _stream())
     return y
 
 
-def gate_bwd(g_y, x, gating, g_x, g_gating, idx8):
-    R = x.shape[0]
-    H = x.numel() // (9 * R) if R else 0
-    L = gating.shape[1] // H if R else 1
-    _call("tta_gate_bwd", _ptr(g_y, numel=R * 9 * H, name="g_y"), _ptr(x, name="x"),
-          _ptr(gating, numel=R * L * H, name="gating"), _ptr(g_x, numel=R * 9 * H, name="g_x"),
-          _ptr(g_gating, numel=R * L * H, name="g_gating"), R, H, L, _i32(idx8, 8, "idx8"),
-          _stream())
+def gate_bwd(g_y, x, gating, g_x, g_gating, idx8, *, R, H, L, ldx=None, ldg=None):
+    """g_x shares x's row stride, g_gating shares gating's."""
+    ldx = 9 * H if ldx is None else ldx
+    ldg = L * H if ldg is None else ldg
+    _call("tta_gate_bwd", _ptr(g_y, numel=R * 9 * H, name="g_y"), _rows(x, R, ldx, 9 * H, "x"),
+          _rows(gating, R, ldg, L * H, "gating"), _rows(g_x, R, ldx, 9 * H, "g_x"),
+          _rows(g_gating, R, ldg, L * H, "g_gating"), R, H, L, ldx, ldg,
+          _i32(idx8, 8, "idx8"), _stream())
 
 
-def ln_silu_fwd(a, gamma, beta, nrm, s, eps=1e-5):
-    R, n = a.shape
-    _call("tta_ln_silu_fwd", _ptr(a, name="a"), _ptr(gamma, numel=n), _ptr(beta, numel=n),
-          _ptr(nrm, numel=R * n), _ptr(s, numel=R * n), R, n, eps, _stream())
+def ln_silu_fwd(a, gamma, beta, nrm, s, *, R, n, lda=None, lds=None, eps=1e-5):
+    lda = n if lda is None else lda
+    lds = n if lds is None else lds
+    _call("tta_ln_silu_fwd", _rows(a, R, lda, n, "a"), _ptr(gamma, numel=n), _ptr(beta, numel=n),
+          _rows(nrm, R, lda, n, "nrm"), _rows(s, R, lds, n, "s"), R, n, lda, lds, eps, _stream())
 
 
-def ln_silu_bwd(g, a, nrm, gamma, g_a, eps=1e-5):
-    R, n = a.shape
-    _call("tta_ln_silu_bwd", _ptr(g, numel=R * n, name="g"), _ptr(a, name="a"),
-          _ptr(nrm, numel=R * n), _ptr(gamma, numel=n), _ptr(g_a, numel=R * n), R, n, eps,
-          _stream())
+def ln_silu_bwd(g, a, nrm, gamma, g_a, *, R, n, ldg=None, lda=None, ldo=None, eps=1e-5):
+    ldg = n if ldg is None else ldg
+    lda = n if lda is None else lda
+    ldo = n if ldo is None else ldo
+    _call("tta_ln_silu_bwd", _rows(g, R, ldg, n, "g"), _rows(a, R, lda, n, "a"),
+          _rows(nrm, R, lda, n, "nrm"), _ptr(gamma, numel=n), _rows(g_a, R, ldo, n, "g_a"), R, n,
+          ldg, lda, ldo, eps, _stream())
 
 
 def rmsnorm_sh_fwd(x, aw, ab, add0, y, inv, eps=1e-5):

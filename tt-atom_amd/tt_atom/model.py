@@ -79,12 +79,11 @@ class SO2Weights:
         bm0 = w[f"{prefix}.fc_m0.bias"]
         if wm0.shape != (extra + 3 * hout, 3 * cin):
             raise RuntimeError(_UNSUPPORTED.format(what=f"fc_m0 {tuple(wm0.shape)}"))
-        self.wg_t = _dev(wm0[:extra].T, device) if extra else None      # -> gating
-        self.bg = _dev(bm0[:extra], device) if extra else None
-        self.wc_t = _dev(wm0[extra:].T, device)                         # -> coefficients 0..2
-        self.bc = _dev(bm0[extra:], device)
-        self.wg = _dev(wm0[:extra], device) if extra else None          # adjoint operands
-        self.wc = _dev(wm0[extra:], device)
+        # one m = 0 GEMM yields [gating (extra) | coefficients 0..2 (3 hout)], the column order of
+        # the torch weight; its adjoint is one GEMM with the weight as stored
+        self.wm0_t = _dev(wm0.T, device)                                # [3 cin, extra + 3 hout]
+        self.bm0 = _dev(bm0, device)
+        self.wm0 = _dev(wm0, device)                                    # [extra + 3 hout, 3 cin]
         b1 = _so2_block(w[f"{prefix}.so2_m_conv.0.fc.weight"])          # [4 cin, 4 hout]
         b2 = _so2_block(w[f"{prefix}.so2_m_conv.1.fc.weight"])          # [2 cin, 2 hout]
         if b1.shape != (4 * cin, 4 * hout) or b2.shape != (2 * cin, 2 * hout):
@@ -190,6 +189,14 @@ class Backbone:
         self.eh_w_t = [_dev(x.T, dev) for x in eb]
         self.eh_w = [_dev(x, dev) for x in eb]
         self.eh_b = [_dev(w[f"energy_block.{i}.bias"], dev) for i in (0, 2, 4)]
+        # the first layers of all radial MLPs read the same x_edge: one GEMM for all of them, and one
+        # for the gaussian part of their input adjoints (order: edge-degree, then block 0..L-1)
+        self.radials = [self.edge_degree] + [b.so2_1.rad for b in self.blocks]
+        self.rad_w0t_all = torch.cat([r.w0t for r in self.radials], 1).contiguous()
+        self.rad_b0_all = torch.cat([r.b0 for r in self.radials]).contiguous()
+        self.rad_w0g_all = torch.cat([r.w0g for r in self.radials], 0).contiguous()
+        if len({r.hidden for r in self.radials}) != 1 or len({r.k_in for r in self.radials}) != 1:
+            raise RuntimeError(_UNSUPPORTED.format(what="radial MLPs of different widths"))
         self.gate_idx_mprime = torch.tensor(GATE_IDX_MPRIME, dtype=torch.int32, device=dev)
         self.gate_idx_natural = torch.tensor(GATE_IDX_NATURAL, dtype=torch.int32, device=dev)
 

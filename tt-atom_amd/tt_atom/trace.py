@@ -7,6 +7,13 @@ finish (geometry.py:226-280, forces.py:545-589) and the trace engine interface
 (trace.py:83-215: build once per topology, then ``engine(pos)`` per step).  Here the geometric
 terms and their VJP are kernels too, so a step is positions in, (E, F[, virial]) out, with no
 host round trip in between.  All buffers are allocated once per topology.
+
+Batching across the layer structure (same math, fewer and larger launches):
+* the first linear of every radial MLP (edge-degree + one per block) reads the same x_edge, so
+  it is one GEMM with the stacked weights; the gaussian part of their input adjoints is likewise
+  one GEMM over the stacked first-layer adjoints (no read-modify-write accumulation);
+* conv-1's m = 0 block produces [gating | coefficients 0..2] with one GEMM into a combined row
+  ``[gating (L*H) | out (9*H)]``; its adjoint is one GEMM on the same combined layout.
 """
 from __future__ import annotations
 
@@ -52,6 +59,9 @@ class TracedEngine:
         z = lambda *s: torch.zeros(*s, **f32)
         emp = lambda *s: torch.empty(*s, **f32)
         hid = bb.edge_degree.hidden
+        self.hid = hid
+        nrad = len(bb.radials)
+        self.nrad = nrad
         # pos-independent node init: sphere_emb[Z] + sys_emb on coefficient 0 (geometry.py:257-258)
         se = torch.as_tensor(sys_emb, dtype=torch.float32).reshape(N, C).to(dev)
         self.sys_emb = se.contiguous()
@@ -65,25 +75,28 @@ class TracedEngine:
         self.g_coef, self.g_env, self.g_gauss = emp(E, 35), emp(E), emp(E, nb)
         self.g_ev, self.forces = emp(E, 3), emp(N, 3)
         self.energy_buf, self.virial_buf, self.virial_work = emp(1), emp(9), emp(256 * 9)
+        # radial MLPs: stacked first layer (pre-LN a0 and LN output of every radial)
+        self.a0_all, self.nrm1_all, self.g_a0_all = (emp(E, nrad * hid) for _ in range(3))
         # shared edge temporaries
+        self.LHc = L * H + NSPH * H                      # combined conv-1 row [gating | out]
         self.xf, self.g_xf, self.g_mcat = emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C)
-        self.y, self.g_y, self.g_out1 = emp(E, NSPH, H), emp(E, NSPH, H), emp(E, NSPH, H)
+        self.y, self.g_y = emp(E, NSPH, H), emp(E, NSPH, H)
+        self.g1c = emp(E, self.LHc)
         self.g_mso2 = emp(E, NSPH, C)
-        self.g_gating = emp(E, L * H)
         self.g_rad = emp(E, 6 * 2 * C)
         self.s1, self.s2 = emp(E, hid), emp(E, hid)
         self.t1, self.t2 = emp(E, hid), emp(E, hid)
-        # edge-degree caches
-        self.ed = self._radial_cache(E, hid, 3 * C, dev)
+        # per-radial caches (second LN and the output)
+        self.ed = self._radial_cache(E, hid, 3 * C, dev, 0)
         self.g_edm = emp(E, 3 * C)
         # per-block caches
         self.blk = []
-        for b in bb.blocks:
+        for i, b in enumerate(bb.blocks):
             c = _Buf()
-            c.x_in, c.n1, c.x1, c.n2, c.x2 = (emp(N, NSPH, C) for _ in range(5))
+            c.x_in, c.n1, c.x1, c.n2 = (emp(N, NSPH, C) for _ in range(4))
             c.inv1, c.inv2 = emp(N), emp(N)
-            c.rad = self._radial_cache(E, hid, 6 * 2 * C, dev)
-            c.out1, c.gating, c.mso2 = emp(E, NSPH, H), emp(E, L * H), emp(E, NSPH, C)
+            c.rad = self._radial_cache(E, hid, 6 * 2 * C, dev, 1 + i)
+            c.o1c, c.mso2 = emp(E, self.LHc), emp(E, NSPH, C)
             if b.ff_type == "spectral":
                 c.a_s, c.gat, c.h, c.gout = emp(N, L * H), emp(N, L * H), emp(N, NSPH, H), emp(N, NSPH, H)
             else:
@@ -103,49 +116,52 @@ class TracedEngine:
         P = max([b.atom_wise.npts for b in bb.blocks if b.ff_type != "spectral"], default=0)
         self.gt1, self.gt2 = emp(N * P, C), emp(N * P, C)
 
-    @staticmethod
-    def _radial_cache(E, hid, n_out, dev):
+    def _radial_cache(self, E, hid, n_out, dev, r):
         c = _Buf()
         f32 = dict(device=dev, dtype=torch.float32)
-        c.a0, c.nrm1, c.a3, c.nrm4 = (torch.empty(E, hid, **f32) for _ in range(4))
+        c.r = r
+        c.a3, c.nrm4 = torch.empty(E, hid, **f32), torch.empty(E, hid, **f32)
         c.out = torch.empty(E, n_out, **f32)
         return c
 
     # ------------------------------------------------------------------ radial MLP
     def _radial_fwd(self, rw, c):
-        nat.linear(self.x_edge, rw.w0t, rw.b0, out=c.a0)
-        nat.ln_silu_fwd(c.a0, rw.ln1w, rw.ln1b, c.nrm1, self.s1)
+        E, hid, ld = self.E, self.hid, self.nrad * self.hid
+        sl = slice(c.r * hid, (c.r + 1) * hid)
+        nat.ln_silu_fwd(self.a0_all[:, sl], rw.ln1w, rw.ln1b, self.nrm1_all[:, sl], self.s1,
+                        R=E, n=hid, lda=ld, lds=hid)
         nat.linear(self.s1, rw.w3t, rw.b3, out=c.a3)
-        nat.ln_silu_fwd(c.a3, rw.ln4w, rw.ln4b, c.nrm4, self.s2)
+        nat.ln_silu_fwd(c.a3, rw.ln4w, rw.ln4b, c.nrm4, self.s2, R=E, n=hid)
         nat.linear(self.s2, rw.w6t, rw.b6, out=c.out)
 
-    def _radial_bwd(self, rw, c, g_out, first):
+    def _radial_bwd(self, rw, c, g_out):
+        E, hid, ld = self.E, self.hid, self.nrad * self.hid
+        sl = slice(c.r * hid, (c.r + 1) * hid)
         nat.linear(g_out, rw.w6, out=self.t1)
-        nat.ln_silu_bwd(self.t1, c.a3, c.nrm4, rw.ln4w, self.t2)
+        nat.ln_silu_bwd(self.t1, c.a3, c.nrm4, rw.ln4w, self.t2, R=E, n=hid)
         nat.linear(self.t2, rw.w3, out=self.t1)
-        nat.ln_silu_bwd(self.t1, c.a0, c.nrm1, rw.ln1w, self.t2)
-        nat.linear(self.t2, rw.w0g, out=self.g_gauss,
-                   epilogue=nat.EPI_STORE if first else nat.EPI_ACCUM)
+        nat.ln_silu_bwd(self.t1, self.a0_all[:, sl], self.nrm1_all[:, sl], rw.ln1w,
+                        self.g_a0_all[:, sl], R=E, n=hid, ldg=hid, lda=ld, ldo=ld)
 
     # ------------------------------------------------------------------ feed-forward
     def _spectral_fwd(self, aw, c, x, res, out):
-        N, C, H = self.N, self.C, self.H
+        N, C, H, L = self.N, self.C, self.H, self.L
         x2d = x.view(N, NSPH * C)
         nat.linear(x2d[:, :C], aw.ws_t, aw.bs, out=c.a_s, epilogue=nat.EPI_PRE_SILU, out2=c.gat)
         nat.gemm(x, aw.w1_t, c.h, bias=aw.b1, M=N, N=H, K=C, lda=NSPH * C, ldb=H, ldc=NSPH * H,
                  batch=NSPH, sA=C, sB=C * H, sC=H, sBias=H)
-        nat.gate_fwd(c.h, c.gat, c.gout, self.bb.gate_idx_natural)
+        nat.gate_fwd(c.h, c.gat, c.gout, self.bb.gate_idx_natural, R=N, H=H, L=L)
         out.copy_(res)
         nat.gemm(c.gout, aw.w2_t, out, bias=aw.b2, M=N, N=C, K=H, lda=NSPH * H, ldb=C,
                  ldc=NSPH * C, batch=NSPH, sA=H, sB=H * C, sC=C, sBias=C, epilogue=nat.EPI_ACCUM)
 
     def _spectral_bwd(self, aw, c, g, out):
-        N, C, H = self.N, self.C, self.H
+        N, C, H, L = self.N, self.C, self.H, self.L
         nat.gemm(g, aw.w2, self.gs_h, M=N, N=H, K=C, lda=NSPH * C, ldb=H, ldc=NSPH * H,
                  batch=NSPH, sA=C, sB=C * H, sC=H)
-        g_h = self.gs_h2
-        nat.gate_bwd(self.gs_h, c.h, c.gat, g_h, self.gs_g, self.bb.gate_idx_natural)
-        nat.gemm(g_h, aw.w1, out, M=N, N=C, K=H, lda=NSPH * H, ldb=C, ldc=NSPH * C,
+        nat.gate_bwd(self.gs_h, c.h, c.gat, self.gs_h2, self.gs_g, self.bb.gate_idx_natural,
+                     R=N, H=H, L=L)
+        nat.gemm(self.gs_h2, aw.w1, out, M=N, N=C, K=H, lda=NSPH * H, ldb=C, ldc=NSPH * C,
                  batch=NSPH, sA=H, sB=H * C, sC=C)
         nat.silu_bwd(self.gs_g, c.a_s, self.gs_a)
         nat.linear(self.gs_a, aw.ws, out=out.view(N, NSPH * C)[:, :C], epilogue=nat.EPI_ACCUM)
@@ -176,11 +192,13 @@ class TracedEngine:
     # ------------------------------------------------------------------ forward
     def _forward(self):
         bb, geo, g = self.bb, self.geo, self.g
-        E, N, C, H = self.E, self.N, self.C, self.H
+        E, N, C, H, L = self.E, self.N, self.C, self.H, self.L
+        LH, LHc = L * H, self.LHc
         nat.edge_wigner(self.pos, g.src, g.tgt, g.shift, geo.jd, geo.gamma, self.ev, self.dist,
                         self.coef)
         nat.edge_features(self.dist, g.zsrc, g.ztgt, bb.src_emb, bb.tgt_emb, geo.offset,
                           geo.coeff, geo.cutoff, self.nb, self.ec, self.x_edge, self.env)
+        nat.linear(self.x_edge, bb.rad_w0t_all, bb.rad_b0_all, out=self.a0_all)
         # edge-degree node init (geometry.py:268-276)
         self._radial_fwd(bb.edge_degree, self.ed)
         x = self.blk[0].x_in if self.blk else self.x_final
@@ -193,15 +211,15 @@ class TracedEngine:
             self._radial_fwd(s1w.rad, c.rad)
             nat.gather_rotate(c.n1, g.src, g.tgt, self.coef, c.rad.out, self.xf)
             xf = self.xf.view(E, NSPH * Cin)
-            o1 = c.out1.view(E, NSPH * H)
-            nat.linear(xf[:, :3 * Cin], s1w.wg_t, s1w.bg, out=c.gating)
-            nat.linear(xf[:, :3 * Cin], s1w.wc_t, s1w.bc, out=o1[:, :3 * H])
-            nat.linear(xf[:, 3 * Cin:7 * Cin], s1w.w1, out=o1[:, 3 * H:7 * H])
-            nat.linear(xf[:, 7 * Cin:], s1w.w2, out=o1[:, 7 * H:])
-            nat.gate_fwd(c.out1, c.gating, self.y, bb.gate_idx_mprime)
+            o1 = c.o1c
+            nat.linear(xf[:, :3 * Cin], s1w.wm0_t, s1w.bm0, out=o1[:, :LH + 3 * H])
+            nat.linear(xf[:, 3 * Cin:7 * Cin], s1w.w1, out=o1[:, LH + 3 * H:LH + 7 * H])
+            nat.linear(xf[:, 7 * Cin:], s1w.w2, out=o1[:, LH + 7 * H:])
+            nat.gate_fwd(o1[:, LH:], o1, self.y, bb.gate_idx_mprime, R=E, H=H, L=L, ldx=LHc,
+                         ldg=LHc)
             y = self.y.view(E, NSPH * H)
             ms = c.mso2.view(E, NSPH * C)
-            nat.linear(y[:, :3 * H], s2w.wc_t, s2w.bc, out=ms[:, :3 * C])
+            nat.linear(y[:, :3 * H], s2w.wm0_t, s2w.bm0, out=ms[:, :3 * C])
             nat.linear(y[:, 3 * H:7 * H], s2w.w1, out=ms[:, 3 * C:7 * C])
             nat.linear(y[:, 7 * H:], s2w.w2, out=ms[:, 7 * C:])
             nat.rotate_env_segsum(c.mso2, self.coef, self.env, g.tgt_ptr, c.x_in, c.x1, n_in=9,
@@ -225,7 +243,8 @@ class TracedEngine:
     # ------------------------------------------------------------------ reverse
     def _backward(self):
         bb, g = self.bb, self.g
-        E, N, C, H = self.E, self.N, self.C, self.H
+        E, N, C, H, L = self.E, self.N, self.C, self.H, self.L
+        LH, LHc = L * H, self.LHc
         Cin = 2 * C
         nat.fill(self.g_coef, 0.0)
         nat.fill(self.g_env, 0.0)
@@ -236,7 +255,6 @@ class TracedEngine:
         nat.linear(self.g_eh1, bb.eh_w[0], out=self.gn_a.view(N, NSPH * C)[:, :C])
         gcur = self.gn_b
         nat.rmsnorm_sh_bwd(self.gn_a, self.x_final, bb.final_norm.aw, self.inv_f, None, gcur)
-        first_rad = True
         for bw, c in zip(reversed(bb.blocks), reversed(self.blk)):
             s1w, s2w = bw.so2_1, bw.so2_2
             # x2 = ff(norm2(x1)) + x1
@@ -252,16 +270,16 @@ class TracedEngine:
                                      self.g_coef, self.g_env, n_in=9, env_first=True)
             gm = self.g_mso2.view(E, NSPH * C)
             gy = self.g_y.view(E, NSPH * H)
-            nat.linear(gm[:, :3 * C], s2w.wc, out=gy[:, :3 * H])
+            nat.linear(gm[:, :3 * C], s2w.wm0, out=gy[:, :3 * H])
             nat.linear(gm[:, 3 * C:7 * C], s2w.w1_t, out=gy[:, 3 * H:7 * H])
             nat.linear(gm[:, 7 * C:], s2w.w2_t, out=gy[:, 7 * H:])
-            nat.gate_bwd(self.g_y, c.out1, c.gating, self.g_out1, self.g_gating, bb.gate_idx_mprime)
-            go = self.g_out1.view(E, NSPH * H)
+            o1, g1 = c.o1c, self.g1c
+            nat.gate_bwd(self.g_y, o1[:, LH:], o1, g1[:, LH:], g1, bb.gate_idx_mprime, R=E, H=H,
+                         L=L, ldx=LHc, ldg=LHc)
             gx = self.g_xf.view(E, NSPH * Cin)
-            nat.linear(self.g_gating, s1w.wg, out=gx[:, :3 * Cin])
-            nat.linear(go[:, :3 * H], s1w.wc, out=gx[:, :3 * Cin], epilogue=nat.EPI_ACCUM)
-            nat.linear(go[:, 3 * H:7 * H], s1w.w1_t, out=gx[:, 3 * Cin:7 * Cin])
-            nat.linear(go[:, 7 * H:], s1w.w2_t, out=gx[:, 7 * Cin:])
+            nat.linear(g1[:, :LH + 3 * H], s1w.wm0, out=gx[:, :3 * Cin])
+            nat.linear(g1[:, LH + 3 * H:LH + 7 * H], s1w.w1_t, out=gx[:, 3 * Cin:7 * Cin])
+            nat.linear(g1[:, LH + 7 * H:], s1w.w2_t, out=gx[:, 7 * Cin:])
             nat.gather_rotate_bw(self.g_xf, c.rad.out, c.n1, g.src, g.tgt, self.coef, self.g_rad,
                                  self.g_mcat, self.g_coef)
             g_n1 = self.gn_a
@@ -269,13 +287,14 @@ class TracedEngine:
             g_in = self.gn_b
             nat.rmsnorm_sh_bwd(g_n1, c.x_in, bw.norm_1.aw, c.inv1, g_x1, g_in)
             gcur = g_in
-            self._radial_bwd(s1w.rad, c.rad, self.g_rad, first_rad)
-            first_rad = False
+            self._radial_bwd(s1w.rad, c.rad, self.g_rad)
         # edge-degree init backward (edge_degree.py:69-93)
         nat.rotate_env_segsum_bw(gcur, g.tgt, self.ed.out, self.coef, self.env, self.g_edm,
                                  self.g_coef, self.g_env, n_in=3, env_first=False,
                                  div=self.geo.rescale)
-        self._radial_bwd(bb.edge_degree, self.ed, self.g_edm, first_rad)
+        self._radial_bwd(bb.edge_degree, self.ed, self.g_edm)
+        # gaussian columns of x_edge: one GEMM over the stacked first-layer adjoints
+        nat.linear(self.g_a0_all, bb.rad_w0g_all, out=self.g_gauss)
         # geometry VJP -> forces (forces.py:580-589 in closed form)
         geo = self.geo
         nat.edge_geometry_bwd(self.ev, self.dist, self.g_coef, self.g_env, self.g_gauss, self.nb,

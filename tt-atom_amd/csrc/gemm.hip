@@ -136,8 +136,17 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
   const int lane = t & 63;
   const int wave = t >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
-  const int n0 = blockIdx.x * BN;
-  const int m0 = blockIdx.y * BM;
+  // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so workgroup b
+  // runs on XCD b % 8.  Give each XCD a contiguous run of row-major tiles; the column tiles of a
+  // row panel then share that XCD's L2 and the A panel is fetched once per XCD instead of once
+  // per column tile.
+  const int tn = (p.N + BN - 1) / BN;
+  const int ntiles = tn * ((p.M + BM - 1) / BM);
+  const int per_xcd = (ntiles + 7) / 8;
+  const int tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (tile >= ntiles) return;
+  const int n0 = (tile % tn) * BN;
+  const int m0 = (tile / tn) * BM;
   const float* A = p.A + (int64_t)blockIdx.z * p.sA;
   const float* B = p.B + (int64_t)blockIdx.z * p.sB;
   float* C = p.C + (int64_t)blockIdx.z * p.sC;
@@ -214,8 +223,10 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
 
 template <int BM, int BN, int WGM, int WGN>
 int launch(const GemmArgs& p, int64_t batch, bool vec, hipStream_t s) {
-  dim3 grid(tta_blocks(p.N, BN), tta_blocks(p.M, BM), (unsigned)batch);
-  if (grid.y > 65535) {
+  const int64_t ntiles = (int64_t)tta_blocks(p.N, BN) * tta_blocks(p.M, BM);
+  // one workgroup per tile, rounded up to a multiple of 8 so every XCD gets a full share
+  dim3 grid((unsigned)(((ntiles + 7) / 8) * 8), 1, (unsigned)batch);
+  if (ntiles > (1ll << 30)) {
     tta::set_error("tta_gemm_f32: grid too large");
     return tta::kBadArgument;
   }

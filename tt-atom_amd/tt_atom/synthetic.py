@@ -250,3 +250,72 @@ def random_uma_bundle(cfg, seed, grid_mats=None):
 
 def system_embedding_inputs(cfg, charge=0, spin=1):
     return torch.tensor([float(charge)]), torch.tensor([float(spin)])
+
+
+# ------------------------------------------------------------------------------ Orb-v3
+# Orb-v3-conservative architecture (orb_calculator.py:56-65; tools/export_orb_weights.py:49-62):
+# 5 attention message-passing layers, latent 256, MLP hidden 1024, 8 Bessel bases x 16 real SH
+# (lmax 3) = edge_embed_size 128, cutoff 6 A, cap 20.  ``mlp_hidden_dim`` and
+# ``head_hidden_dim`` are parameters here (the reference hard-codes 1024 and the checkpoint's 256)
+# so that the CPU parity configuration stays small.
+CFG_ORB_C5 = dict(latent_dim=256, num_message_passing_steps=5, edge_embed_size=128,
+                  node_embed_size=256, lmax=3, num_bases=8, outer_product_with_cutoff=True,
+                  checkpoint="random-init", task="omat", has_charge_spin_cond=False, cutoff=6.0,
+                  max_num_neighbors=20, mlp_hidden_dim=1024, head_hidden_dim=256)
+CFG_ORB_TINY = dict(CFG_ORB_C5, latent_dim=32, num_message_passing_steps=2, node_embed_size=24,
+                    mlp_hidden_dim=48, head_hidden_dim=16)
+
+
+def c5_systems(seed=SEEDS["C5"], K=256, n_min=20, n_max=60, side=7.0, dmin=0.9):
+    """K molecules, sizes uniform in {n_min..n_max}, H/C/N/O, uniform in a ``side`` A cube with
+    ``dmin`` rejection; one generator stream for sizes, elements and positions."""
+    rng = _rng(seed)
+    out = []
+    for _ in range(K):
+        n = int(rng.integers(n_min, n_max + 1))
+        Z = rng.choice(ELEMENTS, size=n, p=ELEMENT_P)
+        pos = _rejection_fill(rng, n, lambda: rng.uniform(0.0, side, size=3), dmin, dmin)
+        out.append((pos.astype(np.float32), Z.astype(np.int64)))
+    return out
+
+
+def random_orb_weights(cfg, seed):
+    """Random-init MoleculeGNS weights in the orb-models state-dict key layout
+    (tools/export_orb_weights.py:64-80): nn.Linear-style U(-1/sqrt(fan_in), 1/sqrt(fan_in))
+    linears, RMSNorm weights 1 + 0.1 N(0,1), N(0,1) atom embeddings, energy-head normaliser and a
+    per-element reference energy."""
+    gen = torch.Generator().manual_seed(int(seed))
+    C, Hd, He = cfg["latent_dim"], cfg.get("mlp_hidden_dim", 1024), cfg.get("head_hidden_dim", 256)
+    w = {}
+
+    def lin(name, n_in, n_out):
+        b = 1.0 / math.sqrt(n_in)
+        w[f"{name}.weight"] = (torch.rand(n_out, n_in, generator=gen) * 2 - 1) * b
+        w[f"{name}.bias"] = (torch.rand(n_out, generator=gen) * 2 - 1) * b
+
+    def mlp_norm(p, n_in):
+        lin(f"{p}.mlp.NN-0", n_in, Hd)
+        lin(f"{p}.mlp.NN-1", Hd, Hd)
+        lin(f"{p}.mlp.NN-2", Hd, C)
+        w[f"{p}.layer_norm.weight"] = 1.0 + 0.1 * torch.randn(C, generator=gen)
+
+    w["atom_emb.embeddings.weight"] = torch.randn(119, cfg["node_embed_size"], generator=gen)
+    mlp_norm("_encoder._node_fn", cfg["node_embed_size"])
+    mlp_norm("_encoder._edge_fn", cfg["edge_embed_size"])
+    for i in range(cfg["num_message_passing_steps"]):
+        p = f"gnn_stacks.{i}"
+        mlp_norm(f"{p}._edge_mlp", 3 * C)
+        mlp_norm(f"{p}._node_mlp", 3 * C)
+        lin(f"{p}._receive_attn", C, 1)
+        lin(f"{p}._send_attn", C, 1)
+        if cfg.get("has_charge_spin_cond", False):
+            lin(f"{p}._cond_node_proj", C, C)
+    if cfg.get("has_charge_spin_cond", False):
+        w["conditioner.charge_embedding.W"] = torch.randn(C // 4, generator=gen)
+        w["conditioner.spin_embedding.W"] = torch.randn(C // 4, generator=gen)
+    lin("energy_head.mlp.NN-0", C, He)
+    lin("energy_head.mlp.NN-1", He, 1)
+    w["energy_head.normalizer.bn.running_mean"] = torch.tensor(-1.5)
+    w["energy_head.normalizer.bn.running_var"] = torch.tensor(2.25)
+    w["energy_head.reference.linear.weight"] = -torch.rand(1, 119, generator=gen) * 10.0
+    return w

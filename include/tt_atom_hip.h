@@ -142,6 +142,74 @@ int tta_node_forces(const float* g_ev, const int* src_ptr, const int* src_perm,
 int tta_virial(const float* ev, const float* g_ev, int64_t E, float* work, float* out,
                tta_stream_t stream);
 
+/* ---------------------------------------------------------------- Orb-v3 edge MLP + scatter
+ * Internal edge order is sender-sorted (stable): sender segments are [send_ptr[n], send_ptr[n+1]),
+ * receiver segments go through (recv_ptr [N+1], recv_perm [E]).  Gates sig [E, 2] hold
+ * (sigmoid(receive_attn), sigmoid(send_attn)); the attention weights attn_w are [w_r | w_s]
+ * (2C floats) with attn_b [2]. */
+
+/* tta_gemm_f32 plus a row-gather term before the epilogue:
+ *   v += P[idx0[row], col] + P[idx1[row], off1 + col]   (P rows of stride ldp; every idx0/idx1
+ * entry must lie in [0, n_rows_p)).  The first edge-MLP layer on [e | n[send] | n[recv]]
+ * (orb_model.py:248-252, the concat + ttnn.linear of MLPNorm, orb_model.py:155-173) is evaluated as
+ * e @ W_e + (n @ W_s)[send] + (n @ W_r)[recv] with the node products precomputed. */
+int tta_gemm_f32_gather(const float* A, const float* B, float* C, const float* bias, float* C2,
+                        const float* aux, int64_t M, int64_t N, int64_t K, int64_t lda,
+                        int64_t ldb, int64_t ldc, const float* P, int64_t ldp, const int* idx0,
+                        const int* idx1, int64_t off1, int64_t n_rows_p, int epilogue,
+                        tta_stream_t stream);
+
+/* vec = pos[recv] - pos[send] + shift (shift may be NULL); feat [E, nb*16] = cut * rbf (x) sh;
+ * cut [E].  Replaces host_edge_features (orb_geometry.py:65-97) and host_cutoff
+ * (orb_model.py:69-82). */
+int tta_orb_edge_features(const float* pos, const int* send, const int* recv, const float* shift,
+                          float r_max, int64_t nb, float* vec, float* feat, float* cut, int64_t N,
+                          int64_t E, tta_stream_t stream);
+/* g_vec [E,3] from g_feat [E, nb*16] and g_cut [E]; nb a power of two.  Replaces the closed-form
+ * host_edge_features_vjp (orb_geometry.py:100-133) and the host torch.autograd.grad finish of
+ * orb_forces.py:303 / 374; forces then come from tta_node_forces (orb_geometry.py:135-139). */
+int tta_orb_edge_features_bwd(const float* vec, const float* g_feat, const float* g_cut,
+                              float r_max, int64_t nb, float* g_vec, int64_t E,
+                              tta_stream_t stream);
+
+/* Row-wise RMSNorm (eps) of h [R, C] with weight w, written to u (may be NULL), plus the residual
+ * x_new = x_old + u (x_old may be NULL), inv [R] kept for the backward, and optionally the next
+ * layer's attention gates on x_new into sig.  Replaces RMSNorm.__call__ (orb_model.py:107-112),
+ * the residual adds (orb_model.py:266) and the gate linears + sigmoid (orb_model.py:239-244). */
+int tta_rms_residual(const float* h, const float* w, const float* x_old, float* u, float* x_new,
+                     float* inv, const float* attn_w, const float* attn_b, float* sig, int64_t R,
+                     int64_t C, float eps, tta_stream_t stream);
+/* g_h = inv w g - inv^3 / C h sum(g w h)  (rmsnorm_bw, orb_forces.py:67-79). */
+int tta_rms_bwd(const float* g, const float* h, const float* w, const float* inv, float* g_h,
+                int64_t R, int64_t C, tta_stream_t stream);
+
+/* node_in [N, 3C] = [nodes | sum_recv ue sig_r cut | sum_send ue sig_s cut]: the attention-
+ * weighted messages and both segment sums of orb_model.py:245-259 (scatter.segment_sum,
+ * scatter.py:62-89). */
+int tta_orb_segsum(const float* ue, const float* sig, const float* cut, const int* send_ptr,
+                   const int* recv_ptr, const int* recv_perm, const float* nodes, float* node_in,
+                   int64_t N, int64_t E, int64_t C, tta_stream_t stream);
+/* Edge side of attn_layer_bw (orb_forces.py:107-147): g_h2 (written), g_cut (accumulated), g_e
+ * (updated in place with the attention adjoint); g_node_in [N, 3C] from the node-MLP backward. */
+int tta_orb_edge_bwd(float* g_e, const float* g_node_in, const float* ue, const float* sig,
+                     const float* cut, const float* h2, const float* inv, const float* wn,
+                     const float* attn_w, const int* send, const int* recv, float* g_h2,
+                     float* g_cut, int64_t N, int64_t E, int64_t C, tta_stream_t stream);
+/* out [N, 2H] = [sum_send x | sum_recv x] for x [E, H]: the gather adjoints of orb_forces.py:131-
+ * 133 moved in front of the (linear) first-layer weight product. */
+int tta_orb_node_segsum2(const float* x, const int* send_ptr, const int* recv_ptr,
+                         const int* recv_perm, float* out, int64_t N, int64_t E, int64_t H,
+                         tta_stream_t stream);
+/* Per-system mean of node rows over [ptr[k], ptr[k+1]) (EnergyHead.batch, orb_model.py:340-355)
+ * and its adjoint out[n] = g[batch[n]] / count (energy_bw_batch, orb_forces.py:207-229). */
+int tta_segment_mean(const float* x, const int* ptr, float* out, int64_t K, int64_t C,
+                     tta_stream_t stream);
+int tta_segment_mean_bwd(const float* g, const int* batch, const int* ptr, float* out, int64_t N,
+                         int64_t C, tta_stream_t stream);
+/* y[r, :C] += x[r, :C] (row strides ldx, ldy): the residual adjoint sums of orb_forces.py:145. */
+int tta_add_rows(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t R, int64_t C,
+                 tta_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,189 @@
+"""GPU parity of the Orb-v3 path (HIP kernels through the C ABI) against the CPU oracle."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import orb as O
+from tt_atom import orb as orb
+from tt_atom import synthetic as S
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def nat():
+    from tt_atom import _native
+    _native.load()
+    return _native
+
+
+def _edges(seed, n_nodes=40, n_edges=400, r_hi=6.5):
+    g = torch.Generator().manual_seed(seed)
+    pos = 3.0 * torch.randn(n_nodes, 3, generator=g)
+    s = torch.randint(n_nodes, (n_edges,), generator=g)
+    r = (s + torch.randint(1, n_nodes, (n_edges,), generator=g)) % n_nodes
+    d = torch.nn.functional.normalize(torch.randn(n_edges, 3, generator=g), dim=1)
+    length = 0.5 + (r_hi - 0.5) * torch.rand(n_edges, generator=g)
+    shift = d * length[:, None] - (pos[r] - pos[s])           # vectors of controlled length
+    return pos, s, r, shift
+
+
+def test_edge_features_and_vjp(nat):
+    pos, s, r, shift = _edges(3)
+    E = s.numel()
+    dev = "cuda"
+    vec, feat, cut = (torch.empty(E, 3, device=dev), torch.empty(E, 128, device=dev),
+                      torch.empty(E, device=dev))
+    i32 = lambda t: t.to(torch.int32).to(dev)
+    nat.orb_edge_features(pos.to(dev), i32(s), i32(r), shift.to(dev), 6.0, 8, vec, feat, cut)
+    p64 = pos.double().requires_grad_(True)
+    rf, rc, rv = O.edge_features(p64, s, r, shift.double())
+    # fp32 rounding of the sine argument n pi r / r_max (up to ~27) bounds the absolute error
+    # of the features (values up to ~6) at a few 1e-6
+    assert (feat.cpu().double() - rf).abs().max() < 1e-5
+    assert (cut.cpu().double() - rc[:, 0]).abs().max() < 1e-6
+    assert (vec.cpu().double() - rv).abs().max() < 2e-6
+    g = torch.Generator().manual_seed(5)
+    gf, gc = torch.randn(E, 128, generator=g), torch.randn(E, generator=g)
+    g_vec = torch.empty(E, 3, device=dev)
+    nat.orb_edge_features_bwd(vec, gf.to(dev), gc.to(dev), 6.0, 8, g_vec)
+    v64 = rv.detach().clone().requires_grad_(True)
+    r64 = torch.linalg.norm(v64, dim=1)
+    u64 = torch.nn.functional.normalize(v64, dim=1)
+    f64 = (O.envelope(r64)[:, None] * (O.bessel(r64)[:, :, None] * O.sph_l3(u64)[:, None, :])
+           .reshape(E, -1))
+    ref = torch.autograd.grad([f64, O.envelope(r64)], v64, [gf.double(), gc.double()])[0]
+    err = (g_vec.cpu().double() - ref).abs().max() / ref.abs().max()
+    assert err < 1e-5, err
+
+
+def test_row_kernels(nat):
+    g = torch.Generator().manual_seed(7)
+    R, C = 300, 256
+    dev = "cuda"
+    h, w, x = (torch.randn(R, C, generator=g), 1 + 0.1 * torch.randn(C, generator=g),
+               torch.randn(R, C, generator=g))
+    aw, ab = 0.1 * torch.randn(2 * C, generator=g), torch.randn(2, generator=g)
+    u, xn, inv, sig = (torch.empty(R, C, device=dev), torch.empty(R, C, device=dev),
+                       torch.empty(R, device=dev), torch.empty(R, 2, device=dev))
+    nat.rms_residual(h.to(dev), w.to(dev), x.to(dev), u, xn, inv, aw.to(dev), ab.to(dev), sig)
+    y = O.rmsnorm(h.double(), w.double())
+    assert (u.cpu().double() - y).abs().max() < 2e-6
+    assert (xn.cpu().double() - (x.double() + y)).abs().max() < 4e-6
+    xs = x.double() + y
+    sr = torch.sigmoid(xs @ aw[:C].double() + ab[0])
+    ss = torch.sigmoid(xs @ aw[C:].double() + ab[1])
+    assert (sig.cpu().double() - torch.stack([sr, ss], 1)).abs().max() < 2e-6
+    # RMSNorm backward vs autograd
+    gy = torch.randn(R, C, generator=g)
+    hd = h.double().requires_grad_(True)
+    ref = torch.autograd.grad(O.rmsnorm(hd, w.double()), hd, gy.double())[0]
+    gh = torch.empty(R, C, device=dev)
+    nat.rms_bwd(gy.to(dev), h.to(dev), w.to(dev), inv, gh)
+    assert (gh.cpu().double() - ref).abs().max() < 5e-6
+
+
+def _tiny_batch(K=3, seed=11, cfg=None, n_min=6, n_max=14, side=5.0):
+    cfg = dict(S.CFG_ORB_TINY if cfg is None else cfg)
+    w = S.random_orb_weights(cfg, seed + S.WEIGHT_SEED_OFFSET)
+    systems = S.c5_systems(seed, K=K, n_min=n_min, n_max=n_max, side=side)
+    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    return cfg, w, systems, bg
+
+
+def _oracle(cfg, w, bg, dtype=torch.float64, **kw):
+    return O.energy_and_forces(w, cfg, bg.pos.to(dtype), bg.Z, bg.senders, bg.receivers,
+                               bg.cell_shift.to(dtype), bg.batch, bg.natoms, **kw)
+
+
+def _check(cfg, w, bg, raw, F, tol_e=1e-6, tol_f=1e-4):
+    ref_raw, ref_F = _oracle(cfg, w, bg)
+    off = 0
+    for k, n in enumerate(bg.natoms):
+        e = float(orb.denormalize_energy(raw[k], bg.Z[off:off + n], n, w))
+        e_ref = float(O.denormalize_energy(ref_raw[k], bg.Z[off:off + n], n,
+                                           w["energy_head.normalizer.bn.running_mean"],
+                                           w["energy_head.normalizer.bn.running_var"],
+                                           w["energy_head.reference.linear.weight"]))
+        assert abs(e - e_ref) <= tol_e * max(1.0, abs(e_ref)), (k, e, e_ref)
+        f = orb.denormalize_forces(F[off:off + n], n, w)
+        f_ref = O.denormalize_forces(ref_F[off:off + n], n,
+                                     w["energy_head.normalizer.bn.running_var"])
+        assert (f - f_ref).abs().max() <= tol_f, (k, (f - f_ref).abs().max())
+        off += n
+
+
+def test_orb_tiny_batch_matches_oracle(nat):
+    cfg, w, _, bg = _tiny_batch()
+    model = orb.OrbModel(w, cfg)
+    raw, F = orb.energy_and_forces_batch(model, pos=bg.pos, senders=bg.senders,
+                                         receivers=bg.receivers, atomic_numbers=bg.Z,
+                                         natoms=bg.natoms, cell_shift=bg.cell_shift)
+    _check(cfg, w, bg, raw, F)
+
+
+def test_orb_conditioning_and_batch_consistency(nat):
+    cfg = dict(S.CFG_ORB_TINY, has_charge_spin_cond=True)
+    cfg, w, systems, bg = _tiny_batch(K=2, seed=12, cfg=cfg)
+    model = orb.OrbModel(w, cfg)
+    cond = torch.cat([model.charge_spin_embedding(1.0, 2.0, bg.natoms[0]),
+                      model.charge_spin_embedding(0.0, 1.0, bg.natoms[1])])
+    raw, F = orb.energy_and_forces_batch(model, pos=bg.pos, senders=bg.senders,
+                                         receivers=bg.receivers, atomic_numbers=bg.Z,
+                                         natoms=bg.natoms, cell_shift=bg.cell_shift,
+                                         cond_nodes=cond)
+    ref_raw, ref_F = _oracle(cfg, w, bg, cond_nodes=cond.double())
+    assert (raw - ref_raw).abs().max() < 1e-6 * max(1.0, ref_raw.abs().max().item())
+    assert (F.double() - ref_F).abs().max() < 2e-6
+    # each system alone gives the same result as inside the batch
+    off = 0
+    for k, sysk in enumerate(systems):
+        one = orb.assemble_orb([sysk], cfg["cutoff"], cfg["max_num_neighbors"])
+        n = bg.natoms[k]
+        r1, F1 = orb.energy_and_forces_batch(model, pos=one.pos, senders=one.senders,
+                                             receivers=one.receivers, atomic_numbers=one.Z,
+                                             natoms=one.natoms, cell_shift=one.cell_shift,
+                                             cond_nodes=cond[off:off + n])
+        assert abs(float(r1[0]) - float(raw[k])) < 1e-6 * max(1.0, abs(float(raw[k])))
+        assert (F1 - F[off:off + n]).abs().max() < 2e-6
+        off += n
+
+
+def test_orb_periodic_stress_matches_oracle(nat):
+    cfg = dict(S.CFG_ORB_TINY)
+    w = S.random_orb_weights(cfg, 99)
+    pos, Z, cell = S.c4_system(seed=4, reps=2, a=3.61, noise=0.05, Z=29)
+    bg = orb.assemble_orb([(pos, Z, cell, [True] * 3)], cfg["cutoff"], cfg["max_num_neighbors"])
+    model = orb.OrbModel(w, cfg)
+    raw, F, vir = orb.energy_and_forces(model, pos=bg.pos, senders=bg.senders,
+                                        receivers=bg.receivers, atomic_numbers=bg.Z,
+                                        cell_shift=bg.cell_shift, compute_stress=True)
+    r_raw, r_F, r_vir = _oracle(cfg, w, bg, compute_stress=True)
+    n = bg.natoms[0]
+    assert abs(raw - float(r_raw[0])) < 1e-6 * max(1.0, abs(float(r_raw[0])))
+    s = orb.denormalize_stress(vir, n, cell, w)
+    s_ref = orb.denormalize_stress(r_vir, n, cell, w)
+    assert (s - s_ref).abs().max() < 1e-5, (s, s_ref)
+    f = orb.denormalize_forces(F, n, w)
+    f_ref = orb.denormalize_forces(r_F, n, w)
+    assert (f - f_ref).abs().max() < 1e-4
+
+
+def test_orb_c5_architecture_reduced_batch(nat):
+    """C5 architecture (latent 256, hidden 1024, 5 layers, cap 20) on 8 of its molecules."""
+    cfg = dict(S.CFG_ORB_C5)
+    w = S.random_orb_weights(cfg, S.SEEDS["C5"] + S.WEIGHT_SEED_OFFSET)
+    systems = S.c5_systems()[:8]
+    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    model = orb.OrbModel(w, cfg)
+    raw, F = orb.energy_and_forces_batch(model, pos=bg.pos, senders=bg.senders,
+                                         receivers=bg.receivers, atomic_numbers=bg.Z,
+                                         natoms=bg.natoms, cell_shift=bg.cell_shift)
+    _check(cfg, w, bg, raw, F)
+    # a second call on the same engine inputs is bitwise identical (deterministic reductions)
+    raw2, F2 = orb.energy_and_forces_batch(model, pos=bg.pos, senders=bg.senders,
+                                           receivers=bg.receivers, atomic_numbers=bg.Z,
+                                           natoms=bg.natoms, cell_shift=bg.cell_shift)
+    assert torch.equal(raw, raw2) and torch.equal(F, F2)

@@ -5,6 +5,9 @@
 //
 // Epilogues: 0 store; 1 store silu(v); 2 accumulate C += v; 3 store v to C and silu(v) to C2
 // (pre-activation kept for the backward); 4 store v * silu'(aux) (aux shares C's layout).
+// Optional row-gather term (tta_gemm_f32_gather): before the epilogue,
+//   v += P[idx0[row], col] + P[idx1[row], off1 + col]        (P rows of stride ldp)
+// which adds per-row node-level partial products to an edge-level GEMM.
 //
 // Block tiles 128x128, 64x128 or 32x64 (x16 in k), 256 threads = 4 waves in a 2x2 arrangement;
 // the largest tile whose grid still fills the chip is used (dispatch()).
@@ -30,6 +33,10 @@ struct GemmArgs {
   int64_t lda, ldb, ldc;
   int64_t sA, sB, sC, sBias;
   int epi;
+  const float* P;  // optional row-gather table (batch 1 only)
+  const int* idx0;
+  const int* idx1;
+  int64_t ldp, off1;
 };
 
 enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ACCUM = 2, EPI_PRE_SILU = 3, EPI_SILU_GRAD = 4 };
@@ -210,6 +217,9 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
         const int row = m0 + rbase + i * 16 + lk * 4 + r;
         if (row >= p.M) continue;
         float v = acc[i][j][r] + bv;
+        if (p.P)
+          v += p.P[(int64_t)p.idx0[row] * p.ldp + col] +
+               p.P[(int64_t)p.idx1[row] * p.ldp + p.off1 + col];
         const int64_t off = (int64_t)row * p.ldc + col;
         if (EPI == EPI_SILU) v = tta_silu(v);
         if (EPI == EPI_ACCUM) v += C[off];
@@ -250,25 +260,50 @@ int dispatch(const GemmArgs& p, int64_t batch, bool vec, hipStream_t s) {
 
 }  // namespace
 
+namespace {
+
+int check_and_run(GemmArgs& p, int64_t M, int64_t N, int64_t K, int64_t batch,
+                  hipStream_t stream, const char* name) {
+  TTA_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "%s: negative size", name);
+  TTA_CHECK_ARG(M < (int64_t)1 << 31 && N < (int64_t)1 << 31 && K < (int64_t)1 << 31,
+                "%s: size exceeds int32", name);
+  TTA_CHECK_ARG(tta_blocks(M, 32) <= 65535 && batch <= 65535, "%s: grid too large", name);
+  TTA_CHECK_ARG(p.epi >= 0 && p.epi <= 4, "%s: bad epilogue %d", name, p.epi);
+  TTA_CHECK_ARG(p.epi != EPI_PRE_SILU || p.C2, "%s: epilogue 3 needs C2", name);
+  TTA_CHECK_ARG(p.epi != EPI_SILU_GRAD || p.aux, "%s: epilogue 4 needs aux", name);
+  if (M == 0 || N == 0 || batch == 0) return tta::kOk;
+  TTA_CHECK_ARG(p.A && p.B && p.C, "%s: null pointer", name);
+  TTA_CHECK_ARG(p.lda >= K && p.ldb >= N && p.ldc >= N, "%s: leading dimension too small", name);
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  const bool vec = (K % 4 == 0) && (N % 4 == 0) && (p.lda % 4 == 0) && (p.ldb % 4 == 0) &&
+                   (p.sA % 4 == 0) && (p.sB % 4 == 0) && ((uintptr_t)p.A % 16 == 0) &&
+                   ((uintptr_t)p.B % 16 == 0);
+  return dispatch(p, batch, vec, stream);
+}
+
+}  // namespace
+
 extern "C" int tta_gemm_f32(const float* A, const float* B, float* C, const float* bias,
                             float* C2, const float* aux, int64_t M, int64_t N, int64_t K,
                             int64_t lda, int64_t ldb, int64_t ldc, int64_t batch, int64_t sA,
                             int64_t sB, int64_t sC, int64_t sBias, int epilogue,
                             hipStream_t stream) {
-  TTA_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tta_gemm_f32: negative size");
-  TTA_CHECK_ARG(M < (int64_t)1 << 31 && N < (int64_t)1 << 31 && K < (int64_t)1 << 31,
-                "tta_gemm_f32: size exceeds int32");
-  TTA_CHECK_ARG(tta_blocks(M, 32) <= 65535 && batch <= 65535, "tta_gemm_f32: grid too large");
-  TTA_CHECK_ARG(epilogue >= 0 && epilogue <= 4, "tta_gemm_f32: bad epilogue %d", epilogue);
-  TTA_CHECK_ARG(epilogue != EPI_PRE_SILU || C2, "tta_gemm_f32: epilogue 3 needs C2");
-  TTA_CHECK_ARG(epilogue != EPI_SILU_GRAD || aux, "tta_gemm_f32: epilogue 4 needs aux");
-  if (M == 0 || N == 0 || batch == 0) return tta::kOk;
-  TTA_CHECK_ARG(A && B && C, "tta_gemm_f32: null pointer");
-  TTA_CHECK_ARG(lda >= K && ldb >= N && ldc >= N, "tta_gemm_f32: leading dimension too small");
-  GemmArgs p{A, B, C, bias, C2, aux, (int)M, (int)N, (int)K, lda, ldb, ldc, sA, sB, sC, sBias,
-             epilogue};
-  const bool vec = (K % 4 == 0) && (N % 4 == 0) && (lda % 4 == 0) && (ldb % 4 == 0) &&
-                   (sA % 4 == 0) && (sB % 4 == 0) && ((uintptr_t)A % 16 == 0) &&
-                   ((uintptr_t)B % 16 == 0);
-  return dispatch(p, batch, vec, stream);
+  GemmArgs p{A, B, C, bias, C2, aux, 0, 0, 0, lda, ldb, ldc, sA, sB, sC, sBias, epilogue,
+             nullptr, nullptr, nullptr, 0, 0};
+  return check_and_run(p, M, N, K, batch, stream, "tta_gemm_f32");
+}
+
+extern "C" int tta_gemm_f32_gather(const float* A, const float* B, float* C, const float* bias,
+                                   float* C2, const float* aux, int64_t M, int64_t N, int64_t K,
+                                   int64_t lda, int64_t ldb, int64_t ldc, const float* P,
+                                   int64_t ldp, const int* idx0, const int* idx1, int64_t off1,
+                                   int64_t n_rows_p, int epilogue, hipStream_t stream) {
+  TTA_CHECK_ARG(P && idx0 && idx1, "tta_gemm_f32_gather: null gather pointer");
+  TTA_CHECK_ARG(n_rows_p > 0 && ldp >= off1 + N && off1 >= 0,
+                "tta_gemm_f32_gather: gather table too narrow");
+  GemmArgs p{A, B, C, bias, C2, aux, 0, 0, 0, lda, ldb, ldc, 0, 0, 0, 0, epilogue,
+             P, idx0, idx1, ldp, off1};
+  return check_and_run(p, M, N, K, 1, stream, "tta_gemm_f32_gather");
 }

@@ -47,6 +47,19 @@ _SIGS = {
     "tta_edge_geometry_bwd": [_P, _P, _P, _P, _P, _I64, _P, _F, _F, _I64, _P, _F, _P, _I64, _P],
     "tta_node_forces": [_P, _P, _P, _P, _P, _I64, _I64, _P],
     "tta_virial": [_P, _P, _I64, _P, _P, _P],
+    "tta_gemm_f32_gather": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64,
+                            _P, _P, _I64, _I64, _I, _P],
+    "tta_orb_edge_features": [_P, _P, _P, _P, _F, _I64, _P, _P, _P, _I64, _I64, _P],
+    "tta_orb_edge_features_bwd": [_P, _P, _P, _F, _I64, _P, _I64, _P],
+    "tta_rms_residual": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _F, _P],
+    "tta_rms_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _P],
+    "tta_orb_segsum": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "tta_orb_edge_bwd": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
+                         _P],
+    "tta_orb_node_segsum2": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "tta_segment_mean": [_P, _P, _P, _I64, _I64, _P],
+    "tta_segment_mean_bwd": [_P, _P, _P, _P, _I64, _I64, _P],
+    "tta_add_rows": [_P, _I64, _P, _I64, _I64, _I64, _P],
 }
 _RESTYPE = {"tta_last_error": ctypes.c_char_p}
 
@@ -345,3 +358,111 @@ def virial(ev, g_ev, work, out):
     E = ev.shape[0]
     _call("tta_virial", _ptr(ev, numel=E * 3), _ptr(g_ev, numel=E * 3), E,
           _ptr(work, numel=256 * 9, name="work"), _ptr(out, numel=9), _stream())
+
+
+# ----------------------------------------------------------------------------- Orb-v3
+def linear_gather(x, w_t, bias, out, P, idx0, idx1, off1, *, epilogue=EPI_STORE, out2=None):
+    """out = epi(x @ w_t + bias + P[idx0, :N] + P[idx1, off1:off1+N]) (row-gathered node terms)."""
+    M, K = x.shape
+    K2, N = w_t.shape
+    if K != K2 or idx0.numel() != M or idx1.numel() != M:
+        raise RuntimeError("linear_gather: shape mismatch")
+    probe = _gemm_probe
+    if probe is not None:
+        c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD))
+        probe.before(2.0 * M * N * K, 4.0 * (M * K + K * N + (c_passes + 2) * M * N))
+    _call("tta_gemm_f32_gather", x.data_ptr(), w_t.data_ptr(), out.data_ptr(),
+          None if bias is None else _ptr(bias, numel=N, name="bias"),
+          None if out2 is None else out2.data_ptr(), None, M, N, K, _ld(x, "x"),
+          _ld(w_t, "w_t"), _ld(out, "out"), _ptr(P, name="P"), _ld(P, "P"),
+          _i32(idx0, M), _i32(idx1, M), off1, P.shape[0], epilogue, _stream())
+    if probe is not None:
+        probe.after()
+    return out
+
+
+def orb_edge_features(pos, send, recv, shift, r_max, nb, vec, feat, cut):
+    N = pos.shape[0]
+    E = send.numel()
+    _call("tta_orb_edge_features", _ptr(pos, numel=N * 3, name="pos"), _i32(send, E),
+          _i32(recv, E), None if shift is None else _ptr(shift, numel=E * 3, name="shift"),
+          float(r_max), nb, _ptr(vec, numel=E * 3), _ptr(feat, numel=E * nb * 16),
+          _ptr(cut, numel=E), N, E, _stream())
+
+
+def orb_edge_features_bwd(vec, g_feat, g_cut, r_max, nb, g_vec):
+    E = vec.shape[0]
+    _call("tta_orb_edge_features_bwd", _ptr(vec, numel=E * 3), _ptr(g_feat, numel=E * nb * 16),
+          _ptr(g_cut, numel=E), float(r_max), nb, _ptr(g_vec, numel=E * 3), E, _stream())
+
+
+def rms_residual(h, w, x_old, u, x_new, inv, attn_w=None, attn_b=None, sig=None, eps=1e-6):
+    R, C = h.shape
+    n = R * C
+    _call("tta_rms_residual", _ptr(h, numel=n, name="h"), _ptr(w, numel=C, name="w"),
+          None if x_old is None else _ptr(x_old, numel=n, name="x_old"),
+          None if u is None else _ptr(u, numel=n, name="u"),
+          None if x_new is None else _ptr(x_new, numel=n, name="x_new"),
+          None if inv is None else _ptr(inv, numel=R, name="inv"),
+          None if attn_w is None else _ptr(attn_w, numel=2 * C, name="attn_w"),
+          None if attn_b is None else _ptr(attn_b, numel=2, name="attn_b"),
+          None if sig is None else _ptr(sig, numel=2 * R, name="sig"), R, C, float(eps), _stream())
+
+
+def rms_bwd(g, h, w, inv, g_h):
+    R, C = h.shape
+    _call("tta_rms_bwd", _ptr(g, numel=R * C, name="g"), _ptr(h, numel=R * C, name="h"),
+          _ptr(w, numel=C, name="w"), _ptr(inv, numel=R, name="inv"),
+          _ptr(g_h, numel=R * C, name="g_h"), R, C, _stream())
+
+
+def orb_segsum(ue, sig, cut, send_ptr, recv_ptr, recv_perm, nodes, node_in):
+    N, C = nodes.shape
+    E = ue.shape[0]
+    _call("tta_orb_segsum", _ptr(ue, numel=E * C, name="ue"), _ptr(sig, numel=2 * E, name="sig"),
+          _ptr(cut, numel=E, name="cut"), _i32(send_ptr, N + 1), _i32(recv_ptr, N + 1),
+          _i32(recv_perm, E), _ptr(nodes, numel=N * C, name="nodes"),
+          _ptr(node_in, numel=N * 3 * C, name="node_in"), N, E, C, _stream())
+
+
+def orb_edge_bwd(g_e, g_node_in, ue, sig, cut, h2, inv, wn, attn_w, send, recv, g_h2, g_cut):
+    E, C = ue.shape
+    N = g_node_in.shape[0]
+    n = E * C
+    _call("tta_orb_edge_bwd", _ptr(g_e, numel=n, name="g_e"),
+          _ptr(g_node_in, numel=N * 3 * C, name="g_node_in"), _ptr(ue, numel=n),
+          _ptr(sig, numel=2 * E), _ptr(cut, numel=E), _ptr(h2, numel=n), _ptr(inv, numel=E),
+          _ptr(wn, numel=C), _ptr(attn_w, numel=2 * C), _i32(send, E), _i32(recv, E),
+          _ptr(g_h2, numel=n, name="g_h2"), _ptr(g_cut, numel=E, name="g_cut"), N, E, C,
+          _stream())
+
+
+def orb_node_segsum2(x, send_ptr, recv_ptr, recv_perm, out):
+    E, H = x.shape
+    N = out.shape[0]
+    _call("tta_orb_node_segsum2", _ptr(x, numel=E * H, name="x"), _i32(send_ptr, N + 1),
+          _i32(recv_ptr, N + 1), _i32(recv_perm, E), _ptr(out, numel=N * 2 * H, name="out"),
+          N, E, H, _stream())
+
+
+def segment_mean(x, ptr, out):
+    K, C = out.shape
+    _call("tta_segment_mean", _ptr(x, name="x"), _i32(ptr, K + 1), _ptr(out, numel=K * C), K, C,
+          _stream())
+
+
+def segment_mean_bwd(g, batch, ptr, out):
+    N, C = out.shape
+    K = ptr.numel() - 1
+    _call("tta_segment_mean_bwd", _ptr(g, numel=K * C, name="g"), _i32(batch, N), _i32(ptr, K + 1),
+          _ptr(out, numel=N * C), N, C, _stream())
+
+
+def add_rows(x, y):
+    """y += x for 2-D row-strided views of equal shape."""
+    R, C = y.shape
+    if tuple(x.shape) != (R, C):
+        raise RuntimeError("add_rows: shape mismatch")
+    ldx, ldy = _ld(x, "x"), _ld(y, "y")
+    _call("tta_add_rows", _rows(x, R, ldx, C, "x"), ldx, _rows(y, R, ldy, C, "y"), ldy, R, C,
+          _stream())

@@ -1,0 +1,471 @@
+"""Orb-v3 (MoleculeGNS, conservative) energy + forces on one MI355X.
+
+Host side of the Orb edge-MLP + scatter path: weight bundle, disjoint-union graph assembly,
+device weights, and an engine that runs one position -> (energy, forces[, virial]) step as a
+fixed sequence of HIP kernels from ``libttatom_hip.so``:
+
+* edge descriptor: Bessel(8) x real SH(l<=3) x polynomial cutoff, and its closed-form VJP, on the
+  device (reference: host torch, orb_geometry.py:65-139);
+* encoder / interaction-layer / node MLPs: MFMA GEMMs with fused bias + SiLU epilogues;
+  RMSNorm + residual + next-layer attention gates in one row kernel;
+* the first edge-MLP layer on ``[e | n[send] | n[recv]]`` is evaluated as
+  ``e @ W_e + (n @ W_s)[send] + (n @ W_r)[recv]`` -- the node products are node-level GEMMs and the
+  gathers are an epilogue term, which removes two thirds of that edge-level GEMM and the
+  ``[E, 3C]`` concat; its adjoint segment-sums ``g_a0`` to the nodes before the weight product;
+* sender / receiver segment sums over sender-sorted edges (deterministic, no atomics).
+
+Reference counterparts: orb_model.py (Encoder, AttentionInteractionLayer, EnergyHead.batch,
+OrbGraphContext), orb_forces.py (mlpnorm_bw, attn_layer_bw, backbone_bw(_batch),
+energy_and_forces(_batch)), disjoint.py:162-218 (assemble_orb), orb_weights.py (bundle).
+"""
+from __future__ import annotations
+
+import json
+import math
+import pathlib
+
+import numpy as np
+import torch
+
+from . import _native as nat
+from .geometry import radius_graph
+from .weights import NpzBundle
+
+HIDDEN_DIM = 1024  # the reference's fixed MLP width (orb_calculator.py:57)
+
+
+# ----------------------------------------------------------------------------- weights
+class OrbWeights(NpzBundle):
+    """``.npz`` bundle of MoleculeGNS parameters: ``config`` JSON + ``w@<state_dict key>``
+    (orb_weights.py:15-26; tools/export_orb_weights.py:51-82)."""
+
+    def activation(self, key):
+        return self._t(f"a@{key}").float()
+
+    def host(self, key):
+        return self._t(f"host@{key}").float()
+
+    def inp(self, key):
+        return self._t(f"in@{key}")
+
+    def out(self, key):
+        return self._t(f"out@{key}")
+
+
+def save_orb_bundle(path, cfg, weights):
+    out = {"config": np.frombuffer(json.dumps(cfg).encode(), dtype=np.uint8)}
+    for k, v in weights.items():
+        out[f"w@{k}"] = torch.as_tensor(v).detach().float().cpu().numpy()
+    np.savez(pathlib.Path(path), **out)
+
+
+# ----------------------------------------------------------------------------- graph
+class OrbBatchedGraph:
+    """Disjoint union of systems under Orb's edge convention (disjoint.py:162-218)."""
+
+    def __init__(self, pos, Z, senders, receivers, cell_shift, batch, natoms, charges=None,
+                 spins=None):
+        self.pos, self.Z = pos, Z
+        self.senders, self.receivers, self.cell_shift = senders, receivers, cell_shift
+        self.batch, self.natoms = batch, list(natoms)
+        self.charges = charges or [0.0] * len(natoms)
+        self.spins = spins or [0.0] * len(natoms)
+
+    @property
+    def K(self):
+        return len(self.natoms)
+
+    def segment_matrices(self):
+        """(seg, seg_mean) [K, Ntot] indicator / row-normalised (disjoint.py:109-120)."""
+        K, N = self.K, self.pos.shape[0]
+        seg = torch.zeros(K, N)
+        seg[self.batch, torch.arange(N)] = 1.0
+        return seg, seg / torch.tensor(self.natoms, dtype=seg.dtype)[:, None]
+
+
+def _fields(system):
+    if isinstance(system, dict):
+        return (system["positions"], system["numbers"], system.get("cell"), system.get("pbc"),
+                system.get("charge", 0.0), system.get("spin", 0.0))
+    if hasattr(system, "get_positions"):
+        info = getattr(system, "info", {}) or {}
+        cell = system.get_cell() if any(system.get_pbc()) else None
+        return (system.get_positions(), system.get_atomic_numbers(), cell, system.get_pbc(),
+                info.get("charge", 0.0), info.get("spin", 0.0))
+    pos, Z = system[0], system[1]
+    cell = system[2] if len(system) > 2 else None
+    pbc = system[3] if len(system) > 3 else None
+    return pos, Z, cell, pbc, 0.0, 0.0
+
+
+def assemble_orb(systems, r_max, max_num_neighbors):
+    """Block-diagonal graph of ``systems`` (ASE Atoms, dicts or (pos, Z[, cell, pbc]) tuples):
+    per-system neighbour list, senders = tgt and receivers = src (Orb's convention), node
+    offsets.  Departure from the reference, which refuses a system whose degree exceeds the cap
+    (disjoint.py:188-197): each sender keeps its ``max_num_neighbors`` nearest neighbours
+    (ordered by (d^2, neighbour, image)), the rule the eSCN-MD path uses."""
+    if len(systems) == 0:
+        raise ValueError("empty batch")
+    pos_all, Z_all, s_all, r_all, sh_all, b_all, natoms, q_all, s_spin = ([] for _ in range(9))
+    off = 0
+    for k, system in enumerate(systems):
+        pos, Z, cell, pbc, charge, spin = _fields(system)
+        pos = torch.as_tensor(np.asarray(pos), dtype=torch.float32)
+        Z = torch.as_tensor(np.asarray(Z), dtype=torch.int64)
+        ei, shift = radius_graph(pos, r_max, cell, pbc, max_num_neighbors)
+        if ei.shape[1] == 0:
+            raise ValueError(f"system {k} has no edges within cutoff -- too sparse for this model")
+        n = Z.shape[0]
+        pos_all.append(pos)
+        Z_all.append(Z)
+        s_all.append(ei[1] + off)
+        r_all.append(ei[0] + off)
+        sh_all.append(shift)
+        b_all.append(torch.full((n,), k, dtype=torch.long))
+        natoms.append(n)
+        q_all.append(float(charge))
+        s_spin.append(float(spin))
+        off += n
+    return OrbBatchedGraph(torch.cat(pos_all), torch.cat(Z_all), torch.cat(s_all),
+                           torch.cat(r_all), torch.cat(sh_all), torch.cat(b_all), natoms, q_all,
+                           s_spin)
+
+
+class OrbGraph:
+    """Device topology of one (batched) graph (orb_model.py:269-304).  The reference edge order
+    is kept at the API; internally edges are stably sorted by sender, so sender segments are
+    contiguous and the receiver segments go through a permutation."""
+
+    def __init__(self, device, *, senders, receivers, num_nodes, atomic_numbers,
+                 cell_shift=None, natoms=None):
+        s = torch.as_tensor(senders).to("cpu", torch.int64).numpy()
+        r = torch.as_tensor(receivers).to("cpu", torch.int64).numpy()
+        N, E = int(num_nodes), int(s.shape[0])
+        if r.shape[0] != E:
+            raise ValueError("senders / receivers length mismatch")
+        if E and (min(s.min(), r.min()) < 0 or max(s.max(), r.max()) >= N):
+            raise ValueError("edge index out of range")
+        if N >= 2 ** 31 or E >= 2 ** 31:
+            raise ValueError("graph too large for int32 indices")
+        natoms = [N] if natoms is None else [int(n) for n in natoms]
+        if sum(natoms) != N:
+            raise ValueError("natoms do not add up to the node count")
+        self.N, self.E, self.K = N, E, len(natoms)
+        order = np.argsort(s, kind="stable")
+        self.order = torch.from_numpy(order)
+        s_s, r_s = s[order], r[order]
+        send_ptr = np.zeros(N + 1, np.int64)
+        send_ptr[1:] = np.cumsum(np.bincount(s_s, minlength=N))
+        recv_perm = np.argsort(r_s, kind="stable")
+        recv_ptr = np.zeros(N + 1, np.int64)
+        recv_ptr[1:] = np.cumsum(np.bincount(r_s, minlength=N))
+        seg_ptr = np.zeros(self.K + 1, np.int64)
+        seg_ptr[1:] = np.cumsum(natoms)
+        batch = np.repeat(np.arange(self.K), natoms)
+        if E and (batch[s_s] != batch[r_s]).any():
+            raise ValueError("an edge joins two systems of the batch")
+        dev = torch.device(device)
+        i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(dev)
+        self.send, self.recv = i32(s_s), i32(r_s)
+        self.send_ptr, self.recv_ptr, self.recv_perm = i32(send_ptr), i32(recv_ptr), i32(recv_perm)
+        self.seg_ptr, self.batch = i32(seg_ptr), i32(batch)
+        self.natoms = natoms
+        self.Z = torch.as_tensor(atomic_numbers).to("cpu", torch.int64).to(dev)
+        self.shift = None
+        if cell_shift is not None:
+            sh = torch.as_tensor(cell_shift, dtype=torch.float32).cpu()[self.order]
+            self.shift = sh.contiguous().to(dev)
+
+
+# ----------------------------------------------------------------------------- device weights
+def _dev(t, device):
+    out = torch.empty(tuple(t.shape), dtype=torch.float32, device=device)
+    out.copy_(torch.as_tensor(t, dtype=torch.float32))
+    return out
+
+
+class _MLPNorm:
+    """One MLPNorm (orb_model.py:127-173): forward w_t [in, out] / bias, backward w [out, in],
+    RMSNorm weight."""
+
+    def __init__(self, w, prefix, device):
+        self.w_t, self.b, self.w = [], [], []
+        for i in range(3):
+            W = w[f"{prefix}.mlp.NN-{i}.weight"]
+            self.w_t.append(_dev(W.T.contiguous(), device))
+            self.w.append(_dev(W, device))
+            self.b.append(_dev(w[f"{prefix}.mlp.NN-{i}.bias"], device))
+        self.norm = _dev(w[f"{prefix}.layer_norm.weight"], device)
+        self.hidden = int(self.w_t[0].shape[1])
+        self.out_dim = int(self.w_t[2].shape[1])
+
+
+class _Layer:
+    """AttentionInteractionLayer weights (orb_model.py:203-223) with the first edge-MLP weight
+    split by input block: W0 = [W_e | W_s | W_r] over [e | n[send] | n[recv]]."""
+
+    def __init__(self, w, prefix, device, C):
+        self.edge = _MLPNorm(w, f"{prefix}._edge_mlp", device)
+        self.node = _MLPNorm(w, f"{prefix}._node_mlp", device)
+        W0 = w[f"{prefix}._edge_mlp.mlp.NN-0.weight"]            # [H, 3C]
+        if W0.shape[1] != 3 * C:
+            raise ValueError(f"{prefix}: edge MLP input is {W0.shape[1]}, expected {3 * C}")
+        We, Ws, Wr = W0[:, :C], W0[:, C:2 * C], W0[:, 2 * C:]
+        self.we_t = _dev(We.T.contiguous(), device)                    # [C, H]
+        self.wsr_t = _dev(torch.cat([Ws.T, Wr.T], 1).contiguous(), device)  # [C, 2H]
+        self.we = _dev(We.contiguous(), device)                        # [H, C]
+        self.wsr = _dev(torch.cat([Ws, Wr], 0).contiguous(), device)     # [2H, C]
+        self.attn_w = _dev(torch.cat([w[f"{prefix}._receive_attn.weight"].reshape(-1),
+                                      w[f"{prefix}._send_attn.weight"].reshape(-1)]), device)
+        self.attn_b = _dev(torch.cat([w[f"{prefix}._receive_attn.bias"].reshape(-1),
+                                      w[f"{prefix}._send_attn.bias"].reshape(-1)]), device)
+        self.cond_w_t = self.cond_b = None
+        if f"{prefix}._cond_node_proj.weight" in w:
+            self.cond_w_t = _dev(w[f"{prefix}._cond_node_proj.weight"].T.contiguous(), device)
+            self.cond_b = _dev(w[f"{prefix}._cond_node_proj.bias"], device)
+
+
+class OrbModel:
+    """Device-resident Orb-v3 weights, built once per checkpoint (orb_calculator.py:54-73)."""
+
+    def __init__(self, weights, cfg, device="cuda"):
+        nat.load()
+        w = {k: torch.as_tensor(v, dtype=torch.float32) for k, v in weights.items()}
+        self.cfg = dict(cfg)
+        self.device = torch.device(device)
+        self.C = int(cfg["latent_dim"])
+        self.nb = int(cfg["num_bases"])
+        self.r_max = float(cfg["cutoff"])
+        if int(cfg.get("lmax", 3)) != 3 or int(cfg["edge_embed_size"]) != 16 * self.nb:
+            raise RuntimeError("Orb path supports lmax=3 spherical harmonics with "
+                               "edge_embed_size = 16 * num_bases")
+        if self.C % 4 or self.C > 1024:
+            raise RuntimeError("latent_dim must be a multiple of 4 and at most 1024")
+        if "forces_head.mlp.NN-0.weight" in w:
+            raise RuntimeError("direct-force Orb checkpoints are not part of this build "
+                               "(conservative checkpoints only)")
+        dev = self.device
+        self.node_emb = w["atom_emb.embeddings.weight"]          # host table, gathered per graph
+        self.enc_node = _MLPNorm(w, "_encoder._node_fn", dev)
+        self.enc_edge = _MLPNorm(w, "_encoder._edge_fn", dev)
+        self.layers = [_Layer(w, f"gnn_stacks.{i}", dev, self.C)
+                       for i in range(int(cfg["num_message_passing_steps"]))]
+        self.H = self.layers[0].edge.hidden if self.layers else self.enc_edge.hidden
+        for L in self.layers:
+            if L.edge.hidden != self.H or L.node.hidden != self.H:
+                raise RuntimeError("all edge / node MLPs must share one hidden width")
+        self.eh_w_t = [_dev(w[f"energy_head.mlp.NN-{i}.weight"].T.contiguous(), dev) for i in (0, 1)]
+        self.eh_w = [_dev(w[f"energy_head.mlp.NN-{i}.weight"], dev) for i in (0, 1)]
+        self.eh_b = [_dev(w[f"energy_head.mlp.NN-{i}.bias"], dev) for i in (0, 1)]
+        self.has_cond = "conditioner.charge_embedding.W" in w
+        self.host_w = {k: v for k, v in w.items() if k.startswith(("energy_head.normalizer",
+                                                                   "energy_head.reference",
+                                                                   "conditioner."))}
+
+    def charge_spin_embedding(self, charge, spin, n):
+        """sin/cos charge/spin conditioning broadcast to n nodes (orb_model.py:32-56)."""
+        def emb(value, W, is_spin):
+            proj = float(value) * W * (2.0 * math.pi)
+            e = torch.cat([torch.sin(proj), torch.cos(proj)])
+            return torch.zeros_like(e) if (is_spin and value == 0) else e
+        c = torch.cat([emb(charge, self.host_w["conditioner.charge_embedding.W"], False),
+                       emb(spin, self.host_w["conditioner.spin_embedding.W"], True)])
+        if c.shape[0] != self.C:
+            raise RuntimeError("conditioning width does not match latent_dim")
+        return c[None].expand(n, -1)
+
+
+# ----------------------------------------------------------------------------- engine
+class OrbEngine:
+    """One fixed-topology energy + forces step: buffers are allocated once per graph and every
+    call is the same kernel sequence (the shape a hipGraph capture would replay)."""
+
+    def __init__(self, model, graph, cond_nodes=None):
+        self.m, self.g = model, graph
+        dev = model.device
+        N, E, K, C, H = graph.N, graph.E, graph.K, model.C, model.H
+        nb16 = 16 * model.nb
+        f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
+        self.x_node = _dev(model.node_emb[graph.Z.cpu()], dev)
+        self.cond = None if cond_nodes is None else _dev(cond_nodes, dev)
+        He = model.eh_w_t[0].shape[1]
+        L = len(model.layers)
+        # geometry
+        self.vec, self.feat, self.cut = f(E, 3), f(E, nb16), f(E)
+        # transient activations
+        self.h0, self.h1 = f(E, H), f(E, H)
+        self.P = f(N, 2 * H)
+        self.edges = [f(E, C), f(E, C)]
+        self.nodes = [f(N, C) for _ in range(L + 1)]
+        self.node_in = f(N, 3 * C)
+        self.hn0, self.hn1, self.hn_out = f(N, H), f(N, H), f(N, C)
+        self.enc_h0, self.enc_h1 = f(N, model.enc_node.hidden), f(N, model.enc_node.hidden)
+        # saved for the backward
+        self.ea0, self.ea1, self.eh2, self.einv = f(E, H), f(E, H), f(E, C), f(E)
+        self.a0 = [f(E, H) for _ in range(L)]
+        self.a1 = [f(E, H) for _ in range(L)]
+        self.h2 = [f(E, C) for _ in range(L)]
+        self.ue = [f(E, C) for _ in range(L)]
+        self.inv = [f(E) for _ in range(L)]
+        self.sig = [f(E, 2) for _ in range(L)]
+        self.an0 = [f(N, H) for _ in range(L)]
+        self.an1 = [f(N, H) for _ in range(L)]
+        self.hn2 = [f(N, C) for _ in range(L)]
+        self.ninv = [f(N) for _ in range(L)]
+        self.mean, self.ha, self.hh, self.raw = f(K, C), f(K, He), f(K, He), f(K, 1)
+        # backward
+        self.ones = torch.ones(K, 1, device=dev, dtype=torch.float32)
+        self.g_ha, self.g_mean = f(K, He), f(K, C)
+        self.g_n, self.g_e, self.g_cut = f(N, C), f(E, C), f(E)
+        self.g_hn2, self.g_an1, self.g_an0, self.g_node_in = f(N, C), f(N, H), f(N, H), f(N, 3 * C)
+        self.g_h2, self.G = f(E, C), f(N, 2 * H)
+        self.g_feat, self.g_vec = f(E, nb16), f(E, 3)
+        self.forces, self.virial_buf, self.work = f(N, 3), f(9), f(256 * 9)
+
+    # -- forward --------------------------------------------------------------------------
+    def _mlp3(self, mlp, x, a0, h0, a1, h1, h2):
+        nat.linear(x, mlp.w_t[0], mlp.b[0], out=a0, epilogue=nat.EPI_PRE_SILU, out2=h0)
+        nat.linear(h0, mlp.w_t[1], mlp.b[1], out=a1, epilogue=nat.EPI_PRE_SILU, out2=h1)
+        nat.linear(h1, mlp.w_t[2], mlp.b[2], out=h2)
+
+    def _forward(self, pos):
+        m, g = self.m, self.g
+        nat.orb_edge_features(pos, g.send, g.recv, g.shift, m.r_max, m.nb, self.vec, self.feat,
+                              self.cut)
+        # encoder: node path (position independent, not differentiated) and edge path
+        en = m.enc_node
+        nat.linear(self.x_node, en.w_t[0], en.b[0], out=self.enc_h0, epilogue=nat.EPI_SILU)
+        nat.linear(self.enc_h0, en.w_t[1], en.b[1], out=self.enc_h1, epilogue=nat.EPI_SILU)
+        nat.linear(self.enc_h1, en.w_t[2], en.b[2], out=self.hn_out)
+        nat.rms_residual(self.hn_out, en.norm, None, None, self.nodes[0], None)
+        ee = m.enc_edge
+        self._mlp3(ee, self.feat, self.ea0, self.h0, self.ea1, self.h1, self.eh2)
+        L0 = m.layers[0] if m.layers else None
+        nat.rms_residual(self.eh2, ee.norm, None, None, self.edges[0], self.einv,
+                         None if L0 is None else L0.attn_w, None if L0 is None else L0.attn_b,
+                         None if L0 is None else self.sig[0])
+        H = m.H
+        for l, lay in enumerate(m.layers):
+            n_l, e_l, e_next = self.nodes[l], self.edges[l % 2], self.edges[(l + 1) % 2]
+            if lay.cond_w_t is not None and self.cond is not None:
+                nat.linear(self.cond, lay.cond_w_t, lay.cond_b, out=n_l, epilogue=nat.EPI_ACCUM)
+            nat.linear(n_l, lay.wsr_t, out=self.P)
+            nat.linear_gather(e_l, lay.we_t, lay.edge.b[0], self.a0[l], self.P, g.send, g.recv, H,
+                              epilogue=nat.EPI_PRE_SILU, out2=self.h0)
+            nat.linear(self.h0, lay.edge.w_t[1], lay.edge.b[1], out=self.a1[l],
+                       epilogue=nat.EPI_PRE_SILU, out2=self.h1)
+            nat.linear(self.h1, lay.edge.w_t[2], lay.edge.b[2], out=self.h2[l])
+            nxt = m.layers[l + 1] if l + 1 < len(m.layers) else None
+            nat.rms_residual(self.h2[l], lay.edge.norm, e_l, self.ue[l], e_next, self.inv[l],
+                             None if nxt is None else nxt.attn_w,
+                             None if nxt is None else nxt.attn_b,
+                             None if nxt is None else self.sig[l + 1])
+            nat.orb_segsum(self.ue[l], self.sig[l], self.cut, g.send_ptr, g.recv_ptr, g.recv_perm,
+                           n_l, self.node_in)
+            self._mlp3(lay.node, self.node_in, self.an0[l], self.hn0, self.an1[l], self.hn1,
+                       self.hn2[l])
+            nat.rms_residual(self.hn2[l], lay.node.norm, n_l, None, self.nodes[l + 1],
+                             self.ninv[l])
+        nat.segment_mean(self.nodes[len(m.layers)], g.seg_ptr, self.mean)
+        nat.linear(self.mean, m.eh_w_t[0], m.eh_b[0], out=self.ha, epilogue=nat.EPI_PRE_SILU,
+                   out2=self.hh)
+        nat.linear(self.hh, m.eh_w_t[1], m.eh_b[1], out=self.raw)
+
+    # -- backward -------------------------------------------------------------------------
+    def _backward(self, compute_stress):
+        m, g = self.m, self.g
+        nat.linear(self.ones, m.eh_w[1], out=self.g_ha, epilogue=nat.EPI_SILU_GRAD, aux=self.ha)
+        nat.linear(self.g_ha, m.eh_w[0], out=self.g_mean)
+        nat.segment_mean_bwd(self.g_mean, g.batch, g.seg_ptr, self.g_n)
+        nat.fill(self.g_e, 0.0)
+        nat.fill(self.g_cut, 0.0)
+        C = m.C
+        for l in reversed(range(len(m.layers))):
+            lay = m.layers[l]
+            nat.rms_bwd(self.g_n, self.hn2[l], lay.node.norm, self.ninv[l], self.g_hn2)
+            nat.linear(self.g_hn2, lay.node.w[2], out=self.g_an1, epilogue=nat.EPI_SILU_GRAD,
+                       aux=self.an1[l])
+            nat.linear(self.g_an1, lay.node.w[1], out=self.g_an0, epilogue=nat.EPI_SILU_GRAD,
+                       aux=self.an0[l])
+            nat.linear(self.g_an0, lay.node.w[0], out=self.g_node_in)
+            nat.orb_edge_bwd(self.g_e, self.g_node_in, self.ue[l], self.sig[l], self.cut,
+                             self.h2[l], self.inv[l], lay.edge.norm, lay.attn_w, g.send, g.recv,
+                             self.g_h2, self.g_cut)
+            nat.linear(self.g_h2, lay.edge.w[2], out=self.h1, epilogue=nat.EPI_SILU_GRAD,
+                       aux=self.a1[l])
+            nat.linear(self.h1, lay.edge.w[1], out=self.h0, epilogue=nat.EPI_SILU_GRAD,
+                       aux=self.a0[l])
+            nat.linear(self.h0, lay.we, out=self.g_e, epilogue=nat.EPI_ACCUM)
+            nat.orb_node_segsum2(self.h0, g.send_ptr, g.recv_ptr, g.recv_perm, self.G)
+            nat.add_rows(self.g_node_in[:, :C], self.g_n)
+            nat.linear(self.G, lay.wsr, out=self.g_n, epilogue=nat.EPI_ACCUM)
+        ee = m.enc_edge
+        nat.rms_bwd(self.g_e, self.eh2, ee.norm, self.einv, self.g_h2)
+        nat.linear(self.g_h2, ee.w[2], out=self.h1, epilogue=nat.EPI_SILU_GRAD, aux=self.ea1)
+        nat.linear(self.h1, ee.w[1], out=self.h0, epilogue=nat.EPI_SILU_GRAD, aux=self.ea0)
+        nat.linear(self.h0, ee.w[0], out=self.g_feat)
+        nat.orb_edge_features_bwd(self.vec, self.g_feat, self.g_cut, m.r_max, m.nb, self.g_vec)
+        # vec = pos[recv] - pos[send]: F[n] = sum_{send=n} g_vec - sum_{recv=n} g_vec
+        nat.node_forces(self.g_vec, g.recv_ptr, g.recv_perm, g.send_ptr, self.forces)
+        if compute_stress:
+            nat.virial(self.vec, self.g_vec, self.work, self.virial_buf)
+
+    def run(self, pos, compute_stress=False):
+        """pos [N, 3] fp32 device tensor (node order of the graph) -> (raw energies [K] fp64 host,
+        raw forces [N, 3] device view, raw virial [3, 3] device view or None); raw = normalised
+        space, as orb_forces.energy_and_forces returns."""
+        self._forward(pos)
+        self._backward(compute_stress)
+        raw = self.raw.view(-1).double().cpu()
+        return raw, self.forces, (self.virial_buf.view(3, 3) if compute_stress else None)
+
+
+# ----------------------------------------------------------------------------- functional API
+def _prepare(model, pos, senders, receivers, atomic_numbers, cell_shift, natoms, cond_nodes):
+    dev = model.device
+    N = int(torch.as_tensor(atomic_numbers).shape[0])
+    graph = OrbGraph(dev, senders=senders, receivers=receivers, num_nodes=N,
+                     atomic_numbers=atomic_numbers, cell_shift=cell_shift, natoms=natoms)
+    eng = OrbEngine(model, graph, cond_nodes)
+    p = torch.as_tensor(pos, dtype=torch.float32).to(dev).contiguous()
+    return eng, p
+
+
+def energy_and_forces(model, *, pos, senders, receivers, atomic_numbers, cell_shift=None,
+                      compute_stress=False, cond_nodes=None):
+    """Single system (orb_forces.py:307-378): raw energy (float), raw forces [N, 3] (host fp32)
+    and, with ``compute_stress``, the raw virial dE/dstrain [3, 3]."""
+    eng, p = _prepare(model, pos, senders, receivers, atomic_numbers, cell_shift, None, cond_nodes)
+    raw, F, vir = eng.run(p, compute_stress)
+    out = (float(raw[0]), F.detach().cpu().clone())
+    return out if not compute_stress else out + (vir.detach().cpu().clone(),)
+
+
+def energy_and_forces_batch(model, *, pos, senders, receivers, atomic_numbers, natoms,
+                            cell_shift=None, cond_nodes=None):
+    """Disjoint-union batch (orb_forces.py:257-304): raw energies [K] (fp64) and raw forces."""
+    eng, p = _prepare(model, pos, senders, receivers, atomic_numbers, cell_shift, natoms,
+                      cond_nodes)
+    raw, F, _ = eng.run(p, False)
+    return raw, F.detach().cpu().clone()
+
+
+def denormalize_energy(raw, Z, n, w):
+    """(raw sigma + mu) n + sum ref[Z] (orb_model.py:588-600)."""
+    sigma = w["energy_head.normalizer.bn.running_var"].double().sqrt()
+    mu = w["energy_head.normalizer.bn.running_mean"].double()
+    ref = w["energy_head.reference.linear.weight"].double().reshape(-1)
+    return (torch.as_tensor(raw).double() * sigma + mu) * n + ref[torch.as_tensor(Z).long()].sum()
+
+
+def denormalize_forces(raw_f, n, w):
+    """raw forces * sigma * n (orb_model.py:459-469)."""
+    return raw_f.double() * w["energy_head.normalizer.bn.running_var"].double().sqrt() * n
+
+
+def denormalize_stress(virial, n, cell, w):
+    """virial * sigma * n / volume -> Voigt [xx, yy, zz, yz, xz, xy] (orb_model.py:472-488)."""
+    sigma = w["energy_head.normalizer.bn.running_var"].double().sqrt()
+    s = virial.double() * sigma * n / torch.linalg.det(torch.as_tensor(cell).double()).abs()
+    return torch.stack([s[0, 0], s[1, 1], s[2, 2], 0.5 * (s[1, 2] + s[2, 1]),
+                        0.5 * (s[0, 2] + s[2, 0]), 0.5 * (s[0, 1] + s[1, 0])])

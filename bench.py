@@ -2,6 +2,10 @@
 """Headline benchmark: energy + conservative forces of the uma-s-1-architecture eSCN-MD model
 (random-init weights) on the 2,048-atom C3 cluster, one MI355X, fp32.
 
+``--workload c4`` runs the same model on the periodic FCC Cu supercell with stress and
+``--workload c5`` the Orb-v3 architecture on the 256-molecule batch; the default line (C3) is the
+headline metric, the others are secondary measurements.
+
 A step is positions -> (energy, forces) with a fixed topology (the neighbour list is built once,
 as in the reference's traced-MD convention): Wigner/edge geometry, edge-degree init, 4 eSCN-MD
 blocks, energy head, the full reverse pass and the geometric VJP, all in HIP kernels.
@@ -80,6 +84,50 @@ def build_c3(torch, n_atoms=2048, seed=None):
     return cfg, w, host, pos, Z, ei, se, nl_ms
 
 
+def build_c4(torch):
+    from tt_atom import geometry, synthetic
+    cfg = dict(synthetic.CFG_UMA_S, task="omat")
+    w, host = synthetic.random_uma_bundle(cfg, synthetic.SEEDS["C3"] + synthetic.WEIGHT_SEED_OFFSET)
+    pos, Z, cell = synthetic.c4_system()
+    pos, Z = torch.from_numpy(pos), torch.from_numpy(Z)
+    t0 = time.perf_counter()
+    ei, shift = geometry.radius_graph(pos, cfg["cutoff"], cell, [True] * 3,
+                                      max_neighbors=cfg["max_neighbors"])
+    nl_ms = (time.perf_counter() - t0) * 1e3
+    se = geometry.csd_embedding(w, torch.tensor([0.0]), torch.tensor([0.0]), dataset=cfg["task"])
+    se = se.expand(len(Z), -1).contiguous()
+    return cfg, w, host, pos, Z, ei, shift, se, cell, nl_ms
+
+
+def build_c5(torch, K=256):
+    from tt_atom import orb, synthetic
+    cfg = dict(synthetic.CFG_ORB_C5)
+    w = synthetic.random_orb_weights(cfg, synthetic.SEEDS["C5"] + synthetic.WEIGHT_SEED_OFFSET)
+    systems = synthetic.c5_systems(K=K)
+    t0 = time.perf_counter()
+    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    nl_ms = (time.perf_counter() - t0) * 1e3
+    return cfg, w, bg, nl_ms
+
+
+def cpu_baseline_c5(torch):
+    """Orb CPU oracle on a bounded sample of C5: the first 32 molecules of the batch."""
+    from oracle import orb as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    cfg, w, bg, _ = build_c5(torch, K=32)
+    args = (w, cfg, bg.pos, bg.Z, bg.senders, bg.receivers, bg.cell_shift, bg.batch, bg.natoms)
+    O.energy_and_forces(*args)                                   # warm-up
+    t0 = time.perf_counter()
+    O.energy_and_forces(*args)
+    dt = time.perf_counter() - t0
+    n = int(bg.pos.shape[0])
+    return {"value": round(n / dt, 3), "unit": "atom-steps/s", "cores": threads, "kind": "port",
+            "sample": (f"Orb CPU oracle (torch-CPU fp32), first 32 C5 molecules ({n} atoms, "
+                       f"E={int(bg.senders.numel())}), 1 step after a warm-up step, {dt:.1f} s; "
+                       f"{threads} threads")}
+
+
 def cpu_baseline(torch):
     """CPU oracle on a bounded sample of the C3 workload."""
     from oracle import forces as OF
@@ -133,6 +181,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=("c3", "c4", "c5"), default="c3",
+                    help="c3 (headline), c4 (periodic + stress) or c5 (Orb-v3 batch)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (y = -x) for the HBM counter scale")
     args = ap.parse_args()
@@ -151,19 +201,47 @@ def main():
         sys.exit(2)
 
     import torch
-    from tt_atom import _native, geometry, model, trace
+    from tt_atom import _native
 
-    cfg, w, host, pos, Z, ei, se, nl_ms = build_c3(torch)
-    dev = torch.device("cuda:0")
-    bb = model.Backbone(w, dev, cfg)
-    geo = geometry.HostGeometry(w, cfg, host["to_m"], host["gauss_offset"], host["gauss_coeff"],
-                                device=dev)
-    eng = trace.TracedEngine(bb, geo, Z, ei, se)
-    pos_d = pos.to(dev)
+    wl = args.workload
+    if wl in ("c3", "c4"):
+        from tt_atom import geometry, model, trace
+        if wl == "c3":
+            cfg, w, host, pos, Z, ei, se, nl_ms = build_c3(torch)
+            shift, cell = None, None
+        else:
+            cfg, w, host, pos, Z, ei, shift, se, cell, nl_ms = build_c4(torch)
+        dev = torch.device("cuda:0")
+        bb = model.Backbone(w, dev, cfg)
+        geo = geometry.HostGeometry(w, cfg, host["to_m"], host["gauss_offset"],
+                                    host["gauss_coeff"], device=dev)
+        eng = trace.TracedEngine(bb, geo, Z, ei, se, edge_cell_shift=shift)
+        pos_d = pos.to(dev)
+        stress = wl == "c4"
+        step = lambda: eng.run(pos_d, compute_stress=stress)
+        n_atoms, n_edges = len(Z), int(ei.shape[1])
+        energy_of = lambda: float(eng.energy_buf)
+        forces_of = lambda: eng.forces
+    else:
+        from tt_atom import orb
+        cfg, w, bg, nl_ms = build_c5(torch)
+        mdl = orb.OrbModel(w, cfg)
+        graph = orb.OrbGraph(mdl.device, senders=bg.senders, receivers=bg.receivers,
+                             num_nodes=bg.pos.shape[0], atomic_numbers=bg.Z,
+                             cell_shift=bg.cell_shift, natoms=bg.natoms)
+        eng = orb.OrbEngine(mdl, graph)
+        pos_d = bg.pos.to(mdl.device)
+
+        def step():
+            eng._forward(pos_d)
+            eng._backward(False)
+        n_atoms, n_edges = int(bg.pos.shape[0]), int(bg.senders.numel())
+        energy_of = lambda: float(eng.raw.sum())
+        forces_of = lambda: eng.forces
     for _ in range(args.warmup):
-        eng.run(pos_d)
+        step()
     torch.cuda.synchronize()
-    print(f"[bench] warm-up done: N={len(Z)} E={ei.shape[1]} energy={float(eng.energy_buf):.6f}",
+    print(f"[bench] {wl} warm-up done: N={n_atoms} E={n_edges} energy={energy_of():.6f}",
           file=sys.stderr, flush=True)
 
     probe = GemmEvents(torch)
@@ -171,20 +249,35 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        eng.run(pos_d)
+        step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     _native.set_gemm_probe(None)
-    energy = float(eng.energy_buf)
-    if not (energy == energy) or not bool(torch.isfinite(eng.forces).all()):
+    energy = energy_of()
+    if not (energy == energy) or not bool(torch.isfinite(forces_of()).all()):
         raise RuntimeError("non-finite energy or forces")
     n_launch, flops, gemm_ms = probe.summary()
     achieved = flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
-    traffic = read_traffic()
+    traffic = read_traffic() if wl == "c3" else None
     ms_step = dt / args.steps * 1e3
+    if wl == "c5":
+        metric = "atom-steps/s (energy+forces), Orb-v3-conservative arch, 256 molecules (C5)"
+        workload = ("C5: Orb-v3-conservative arch (5 layers, latent 256, MLP hidden 1024, 8 "
+                    "Bessel x SH l<=3), 256 H/C/N/O molecules of 20-60 atoms in 7 A cubes, "
+                    "cutoff 6 A, cap 20, energy+forces, fixed topology")
+        data = "synthetic (random-init Orb-v3-conservative-architecture weights, seeded C5 batch)"
+    else:
+        metric = METRIC
+        workload = ("C3: uma-s-1 arch (4 eSCN-MD layers, C=H=128, lmax=mmax=2, 512 gaussians, "
+                    "spectral FF), 2048-atom H/C/N/O cluster in a 17 A ball, cutoff 6 A, cap 30, "
+                    "energy+forces, fixed topology") if wl == "c3" else (
+                    "C4: C3 weights (task omat) on FCC Cu 8x8x8 (a=3.61 A, N(0,0.05) noise), "
+                    "PBC, cutoff 6 A, cap 30, energy+forces+stress, fixed topology")
+        data = ("synthetic (random-init uma-s-1-architecture weights, seeded "
+                f"{wl.upper()} system)")
     out = {
-        "metric": METRIC,
-        "value": round(len(Z) * args.steps / dt, 2),
+        "metric": metric,
+        "value": round(n_atoms * args.steps / dt, 2),
         "unit": "atom-steps/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -194,13 +287,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (random-init uma-s-1-architecture weights, seeded C3 cluster)",
-        "config": {"workload": "C3: uma-s-1 arch (4 eSCN-MD layers, C=H=128, lmax=mmax=2, 512 "
-                               "gaussians, spectral FF), 2048-atom H/C/N/O cluster in a 17 A ball, "
-                               "cutoff 6 A, cap 30, energy+forces, fixed topology",
-                   "atoms": len(Z), "edges": int(ei.shape[1]),
-                   "neighbor_list_host_ms": round(nl_ms, 1),
-                   "energy": energy},
+        "data": data,
+        "config": {"workload": workload, "atoms": n_atoms, "edges": n_edges,
+                   "neighbor_list_host_ms": round(nl_ms, 1), "energy": energy},
         "roofline": {"bound": "mfma", "kernel": "gemm_f32_kernel (all GEMMs of the step)",
                      "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
@@ -211,7 +300,7 @@ def main():
                      "gemm_share_of_step": round(gemm_ms / (dt * 1e3), 4)},
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(torch)
+        out["cpu_baseline"] = cpu_baseline_c5(torch) if wl == "c5" else cpu_baseline(torch)
     print(json.dumps(out), flush=True)
 
 

@@ -43,6 +43,22 @@ int tta_gemm_f32(const float* A, const float* B, float* C, const float* bias, fl
                  int64_t ldc, int64_t batch, int64_t sA, int64_t sB, int64_t sC, int64_t sBias,
                  int epilogue, tta_stream_t stream);
 
+/* Split-bf16 GEMM on the bf16 matrix cores (same contractions as tta_gemm_f32, same epilogues,
+ * plus the optional row-gather term of tta_gemm_f32_gather when P is non-NULL).  The fp32 A
+ * operand is split on the fly into bf16 planes a = a0 + a1 + a2 (round-to-nearest residuals); the
+ * constant B operand is packed once by tta_pack_b.  mode 6: planes 3 x 3, products
+ * a0b0 + a0b1 + a1b0 + a0b2 + a2b0 + a1b1 -- fp32 GEMM accuracy; mode 3: 2 x 2 planes, 3 products
+ * (~2^-16 relative); mode 1: bf16 operands.  A needs K, lda multiples of 4 and 16-byte alignment.
+ * Replaces the same ttnn.linear / ttnn.matmul call sites as tta_gemm_f32 (the reference runs
+ * them in bf16 / bf8 with fp32 accumulation: compute_kernel_config, device.py). */
+int64_t tta_pack_b_elems(int64_t K, int64_t N, int mode);
+int tta_pack_b(const float* B, int64_t K, int64_t N, int64_t ldb, int mode, void* out,
+               int64_t out_elems, tta_stream_t stream);
+int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const float* bias, float* C2,
+                   const float* aux, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc,
+                   int mode, const float* P, int64_t ldp, const int* idx0, const int* idx1,
+                   int64_t off1, int64_t n_rows_p, int epilogue, tta_stream_t stream);
+
 /* ---------------------------------------------------------------- edge-frame rotation
  * out[e, m, :] = (sum_j W[e,m,j] [x[src_e, j, :] | x[tgt_e, j, :]]) * rad[e, rb(m), :]
  * x [N,9,C], out [E,9,2C], rad [E,6,2C] or NULL.  Fuses the src/tgt gather + interleave of

@@ -10,7 +10,7 @@ HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "tt_atom_hip.
 
 def _declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const char\*|int)\s+(tta_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const char\*|int64_t|int)\s+(tta_\w+)\(", text, re.M)))
 
 
 def test_header_and_bindings_agree():

@@ -103,6 +103,59 @@ def test_gemm_batched_strided(nat):
     assert (out.cpu().double() - ref).abs().max() < 1e-4
 
 
+@pytest.mark.parametrize("M,N,K", [(4100, 200, 196), (8192, 640, 768), (5000, 16, 1000)])
+@pytest.mark.parametrize("epi", [0, 2, 3, 4])
+def test_split_bf16_gemm_fp32_accuracy(nat, M, N, K, epi):
+    """Mode 6 (three bf16 planes, six products) has the accuracy of an fp32 GEMM: its error
+    relative to |A| |B| stays within the fp32 kernel's, on ragged M / N / K tails too."""
+    g = torch.Generator().manual_seed(M + N + K)
+    A = torch.randn(M, K, generator=g)
+    B = torch.randn(K, N, generator=g) / math.sqrt(K)
+    bias = torch.randn(N, generator=g)
+    C0 = torch.randn(M, N, generator=g)
+    aux = torch.randn(M, N, generator=g)
+    ref = (A.double() @ B.double()) + bias.double()
+    scale = A.double().abs() @ B.double().abs() + 1.0
+    if epi == 2:
+        ref = ref + C0.double()
+    elif epi == 4:
+        s = torch.sigmoid(aux.double())
+        ref = ref * (s * (1 + aux.double() * (1 - s)))
+        scale = scale * 1.2
+    pw = nat.PackedWeight(B.to(DEV), nat.SPLIT_F32)
+    outs = {}
+    for name, w in (("split", pw), ("f32", B.to(DEV))):
+        Cd = C0.clone().to(DEV)
+        C2 = torch.zeros(M, N, device=DEV)
+        nat.linear(A.to(DEV), w, bias.to(DEV), out=Cd, epilogue=epi, out2=C2, aux=aux.to(DEV))
+        outs[name] = ((Cd.cpu().double() - ref).abs() / scale).max().item(), C2.cpu().double()
+    assert outs["split"][0] < max(2.0 * outs["f32"][0], 1e-6), outs
+    if epi == 3:
+        assert (outs["split"][1] - torch.nn.functional.silu(ref)).abs().max() < 1e-5 * float(
+            scale.max())
+
+
+def test_split_bf16_gemm_modes_and_gather(nat):
+    g = torch.Generator().manual_seed(3)
+    M, N, K, Nn = 6000, 256, 512, 300
+    A = torch.randn(M, K, generator=g)
+    B = torch.randn(K, N, generator=g) / math.sqrt(K)
+    P = torch.randn(Nn, 2 * N, generator=g)
+    i0 = torch.randint(Nn, (M,), generator=g)
+    i1 = torch.randint(Nn, (M,), generator=g)
+    ref = A.double() @ B.double() + P.double()[i0, :N] + P.double()[i1, N:]
+    scale = (A.double().abs() @ B.double().abs()).max().item()
+    errs = {}
+    for mode in (nat.SPLIT_F32, nat.SPLIT_3, nat.SPLIT_BF16):
+        pw = nat.PackedWeight(B.to(DEV), mode)
+        out = torch.empty(M, N, device=DEV)
+        nat.linear_gather(A.to(DEV), pw, None, out, P.to(DEV), _i32(i0), _i32(i1), N)
+        errs[mode] = (out.cpu().double() - ref).abs().max().item() / scale
+    # bf16 operands: ~2^-8 relative; two planes: ~2^-16; three planes: fp32 level
+    assert errs[nat.SPLIT_BF16] < 2e-2 and errs[nat.SPLIT_3] < 2e-5 and errs[nat.SPLIT_F32] < 2e-6, errs
+    assert errs[nat.SPLIT_F32] < errs[nat.SPLIT_3] < errs[nat.SPLIT_BF16]
+
+
 # ------------------------------------------------------------------------------ geometry
 def _oracle_wig(ev, jd):
     eul = OG.euler_angles(ev)

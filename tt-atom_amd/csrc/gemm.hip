@@ -14,32 +14,13 @@
 //
 // MFMA 16x16x4 f32 operand layout (one block): lane l supplies A[l%16][l/16] and B[l/16][l%16];
 // the result D[4*(l/16)+r][l%16], r=0..3, lands in accumulator element r of lane l.
-#include "common.h"
-
-typedef float floatx4 __attribute__((ext_vector_type(4)));
+#include "gemm_common.h"
 
 namespace {
 
+using namespace tta_gemm;
+
 constexpr int BK = 16, PAD = 4;
-
-struct GemmArgs {
-  const float* A;
-  const float* B;
-  float* C;
-  const float* bias;
-  float* C2;
-  const float* aux;
-  int M, N, K;
-  int64_t lda, ldb, ldc;
-  int64_t sA, sB, sC, sBias;
-  int epi;
-  const float* P;  // optional row-gather table (batch 1 only)
-  const int* idx0;
-  const int* idx1;
-  int64_t ldp, off1;
-};
-
-enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ACCUM = 2, EPI_PRE_SILU = 3, EPI_SILU_GRAD = 4 };
 
 // Block tile BM x BN x BK with 4 waves in a WGM x WGN grid; each wave owns (BM/WGM) x (BN/WGN)
 // = TI x TJ MFMA tiles of 16 x 16.  Loads stage A k-major (the 16 lanes sharing a k read 16
@@ -138,24 +119,18 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
   __shared__ float As[2][BK][BM + PAD];
   __shared__ float Bs[2][BK][BN + PAD];
 
-  const int EPI = p.epi;
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
-  // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so workgroup b
-  // runs on XCD b % 8.  Give each XCD a contiguous run of row-major tiles; the column tiles of a
-  // row panel then share that XCD's L2 and the A panel is fetched once per XCD instead of once
-  // per column tile.
   const int tn = (p.N + BN - 1) / BN;
   const int ntiles = tn * ((p.M + BM - 1) / BM);
-  const int per_xcd = (ntiles + 7) / 8;
-  const int tile = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  const int tile = xcd_tile(ntiles);
   if (tile >= ntiles) return;
   const int n0 = (tile % tn) * BN;
   const int m0 = (tile / tn) * BM;
   const float* A = p.A + (int64_t)blockIdx.z * p.sA;
-  const float* B = p.B + (int64_t)blockIdx.z * p.sB;
+  const float* B = static_cast<const float*>(p.B) + (int64_t)blockIdx.z * p.sB;
   float* C = p.C + (int64_t)blockIdx.z * p.sC;
   float* C2 = p.C2 ? p.C2 + (int64_t)blockIdx.z * p.sC : nullptr;
   const float* aux = p.aux ? p.aux + (int64_t)blockIdx.z * p.sC : nullptr;
@@ -205,30 +180,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
     __syncthreads();
   }
 
-#pragma unroll
-  for (int j = 0; j < TJ; ++j) {
-    const int col = n0 + cbase + j * 16 + li;
-    if (col >= p.N) continue;
-    const float bv = bias ? bias[col] : 0.f;
-#pragma unroll
-    for (int i = 0; i < TI; ++i) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + rbase + i * 16 + lk * 4 + r;
-        if (row >= p.M) continue;
-        float v = acc[i][j][r] + bv;
-        if (p.P)
-          v += p.P[(int64_t)p.idx0[row] * p.ldp + col] +
-               p.P[(int64_t)p.idx1[row] * p.ldp + p.off1 + col];
-        const int64_t off = (int64_t)row * p.ldc + col;
-        if (EPI == EPI_SILU) v = tta_silu(v);
-        if (EPI == EPI_ACCUM) v += C[off];
-        if (EPI == EPI_PRE_SILU) C2[off] = tta_silu(v);
-        if (EPI == EPI_SILU_GRAD) v = v * tta_silu_grad(aux[off]);
-        C[off] = v;
-      }
-    }
-  }
+  store_tiles<TI, TJ>(p, acc, m0 + rbase, n0 + cbase, li, lk, C, C2, aux, bias);
 }
 
 template <int BM, int BN, int WGM, int WGN>

@@ -1,0 +1,71 @@
+// Shared pieces of the MFMA GEMM kernels: argument block, epilogue codes and the epilogue that
+// writes one wave's 16x16 accumulator tiles.
+#pragma once
+
+#include "common.h"
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+namespace tta_gemm {
+
+enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ACCUM = 2, EPI_PRE_SILU = 3, EPI_SILU_GRAD = 4 };
+
+struct GemmArgs {
+  const float* A;
+  const void* B;  // fp32 [K, N] (fp32 kernel) or packed bf16 planes (split-bf16 kernel)
+  float* C;
+  const float* bias;
+  float* C2;
+  const float* aux;
+  int M, N, K;
+  int64_t lda, ldb, ldc;
+  int64_t sA, sB, sC, sBias;
+  int epi;
+  const float* P;  // optional row-gather table (batch 1 only)
+  const int* idx0;
+  const int* idx1;
+  int64_t ldp, off1;
+};
+
+// Accumulator layout of v_mfma_f32_16x16x{4f32,32bf16}: lane l holds D[4*(l/16)+r][l%16] in
+// element r.  The epilogue is a (wave-uniform) runtime switch: one kernel symbol per tile shape.
+template <int TI, int TJ>
+__device__ __forceinline__ void store_tiles(const GemmArgs& p, const floatx4 (&acc)[TI][TJ],
+                                            int m0, int n0, int li, int lk, float* C, float* C2,
+                                            const float* aux, const float* bias) {
+  const int EPI = p.epi;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int col = n0 + j * 16 + li;
+    if (col >= p.N) continue;
+    const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + i * 16 + lk * 4 + r;
+        if (row >= p.M) continue;
+        float v = acc[i][j][r] + bv;
+        if (p.P)
+          v += p.P[(int64_t)p.idx0[row] * p.ldp + col] +
+               p.P[(int64_t)p.idx1[row] * p.ldp + p.off1 + col];
+        const int64_t off = (int64_t)row * p.ldc + col;
+        if (EPI == EPI_SILU) v = tta_silu(v);
+        if (EPI == EPI_ACCUM) v += C[off];
+        if (EPI == EPI_PRE_SILU) C2[off] = tta_silu(v);
+        if (EPI == EPI_SILU_GRAD) v = v * tta_silu_grad(aux[off]);
+        C[off] = v;
+      }
+    }
+  }
+}
+
+// XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so workgroup b
+// runs on XCD b % 8.  Each XCD gets a contiguous run of row-major tiles, so the column tiles of a
+// row panel share that XCD's L2 and the A panel is fetched once per XCD.
+__device__ __forceinline__ int xcd_tile(int ntiles) {
+  const int per_xcd = (ntiles + 7) / 8;
+  return (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+}
+
+}  // namespace tta_gemm

@@ -60,8 +60,12 @@ _SIGS = {
     "tta_segment_mean": [_P, _P, _P, _I64, _I64, _P],
     "tta_segment_mean_bwd": [_P, _P, _P, _P, _I64, _I64, _P],
     "tta_add_rows": [_P, _I64, _P, _I64, _I64, _I64, _P],
+    "tta_pack_b_elems": [_I64, _I64, _I],
+    "tta_pack_b": [_P, _I64, _I64, _I64, _I, _P, _I64, _P],
+    "tta_gemm_bf16x": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _P,
+                       _I64, _I64, _I, _P],
 }
-_RESTYPE = {"tta_last_error": ctypes.c_char_p}
+_RESTYPE = {"tta_last_error": ctypes.c_char_p, "tta_pack_b_elems": ctypes.c_int64}
 
 EXPORTS = tuple(_SIGS)
 
@@ -182,14 +186,74 @@ def gemm(A, B, C, *, M, N, K, lda, ldb, ldc, bias=None, epilogue=EPI_STORE, C2=N
         probe.after()
 
 
+# Split-bf16 MFMA GEMM modes (tta_gemm_bf16x): 6 = fp32-accurate (three bf16 planes per
+# operand, six products), 3 = two planes / three products, 1 = bf16 operands.
+SPLIT_F32, SPLIT_3, SPLIT_BF16 = 6, 3, 1
+
+
+class PackedWeight:
+    """A constant GEMM operand w_t [K, N] (fp32, row-major) plus its bf16-plane packing for the
+    split-bf16 kernel (``mode`` 6, 3 or 1; None keeps only the fp32 matrix for the fp32-MFMA
+    kernel).  ``shape`` / ``T``-free: it stands wherever a [K, N] weight is passed to linear()."""
+
+    def __init__(self, w_t, mode=SPLIT_F32):
+        if w_t.dim() != 2 or w_t.dtype != torch.float32 or not w_t.is_cuda:
+            raise RuntimeError("PackedWeight: w_t must be a 2-D fp32 device tensor")
+        self.w_t = w_t
+        self.mode = mode
+        self.packed = None
+        K, N = w_t.shape
+        if mode is not None and K % 4 == 0:
+            n = load().tta_pack_b_elems(K, N, mode)
+            self.packed = torch.empty(n, dtype=torch.int16, device=w_t.device)
+            _call("tta_pack_b", _ptr(w_t, name="w_t", contiguous=False), K, N, _ld(w_t, "w_t"),
+                  mode, self.packed.data_ptr(), n, _stream())
+
+    @property
+    def shape(self):
+        return self.w_t.shape
+
+
+def _gemm_bf16x(x, pw, out, bias, epilogue, out2, aux, P=None, idx0=None, idx1=None, off1=0):
+    M, K = x.shape
+    N = pw.w_t.shape[1]
+    probe = _gemm_probe
+    if probe is not None:
+        c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD)) + (2 if P is not None else 0)
+        probe.before(2.0 * M * N * K, 4.0 * (M * K + K * N + c_passes * M * N))
+    _call("tta_gemm_bf16x", x.data_ptr(), pw.packed.data_ptr(), out.data_ptr(),
+          None if bias is None else _ptr(bias, numel=N, name="bias"),
+          None if out2 is None else out2.data_ptr(), None if aux is None else aux.data_ptr(),
+          M, N, K, _ld(x, "x"), _ld(out, "out"), pw.mode,
+          None if P is None else _ptr(P, name="P"), 0 if P is None else _ld(P, "P"),
+          None if idx0 is None else _i32(idx0, M), None if idx1 is None else _i32(idx1, M),
+          off1, 0 if P is None else P.shape[0], epilogue, _stream())
+    if probe is not None:
+        probe.after()
+
+
+def _split_ok(x, pw):
+    """The split-bf16 kernel (128 x 128 x 32 tiles) runs edge-level GEMMs; short-K or small-M
+    products stay on the fp32 MFMA kernel, whose smaller tiles fill the chip better there."""
+    M, K = x.shape
+    return (isinstance(pw, PackedWeight) and pw.packed is not None and M >= 4096 and K >= 192
+            and x.data_ptr() % 16 == 0 and _ld(x, "x") % 4 == 0)
+
+
 def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None):
-    """y = x @ w_t (+ bias) for 2-D row-major x [M, K] (any row stride) and w_t [K, N]."""
+    """y = x @ w_t (+ bias) for 2-D row-major x [M, K] (any row stride) and w_t [K, N] (a tensor
+    or a PackedWeight; a packed weight runs on the split-bf16 kernel when the shapes allow)."""
     M, K = x.shape
     K2, N = w_t.shape
     if K != K2:
         raise RuntimeError(f"linear: inner dims {K} vs {K2}")
     if out is None:
         out = torch.empty(M, N, device=x.device, dtype=torch.float32)
+    if isinstance(w_t, PackedWeight):
+        if _split_ok(x, w_t):
+            _gemm_bf16x(x, w_t, out, bias, epilogue, out2, aux)
+            return out
+        w_t = w_t.w_t
     gemm(x, w_t, out, M=M, N=N, K=K, lda=_ld(x, "x"), ldb=_ld(w_t, "w_t"), ldc=_ld(out, "out"),
          bias=bias, epilogue=epilogue, C2=out2, aux=aux)
     return out
@@ -367,6 +431,11 @@ def linear_gather(x, w_t, bias, out, P, idx0, idx1, off1, *, epilogue=EPI_STORE,
     K2, N = w_t.shape
     if K != K2 or idx0.numel() != M or idx1.numel() != M:
         raise RuntimeError("linear_gather: shape mismatch")
+    if isinstance(w_t, PackedWeight):
+        if _split_ok(x, w_t):
+            _gemm_bf16x(x, w_t, out, bias, epilogue, out2, None, P, idx0, idx1, off1)
+            return out
+        w_t = w_t.w_t
     probe = _gemm_probe
     if probe is not None:
         c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD))

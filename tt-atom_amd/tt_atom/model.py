@@ -15,6 +15,8 @@ from __future__ import annotations
 import numpy as np
 import torch
 
+from . import _native as nat
+
 NSPH = 9
 # m-primed gate row per vector coefficient (activation.py:19-26 for lmax = mmax = 2) and the
 # natural-order one of the spectral feed-forward (spectral.py:77-88)
@@ -35,10 +37,21 @@ def _dev(t, device):
     return out
 
 
+# GEMM arithmetic per precision setting: "f32" = split-bf16 MFMA with six plane products (fp32
+# GEMM accuracy), "f32-mfma" = the fp32 MFMA kernel only, "bf16" = bf16 operands, fp32 accumulate.
+PRECISIONS = {"f32": nat.SPLIT_F32, "f32-mfma": None, "bf16": nat.SPLIT_BF16}
+
+
+def _gw(t, device, mode):
+    """A GEMM weight operand [K, N]: packed for the split-bf16 kernel unless mode is None."""
+    d = t if (isinstance(t, torch.Tensor) and t.is_cuda) else _dev(t, device)
+    return nat.PackedWeight(d, mode) if mode is not None else d
+
+
 class RadialWeights:
     """Linear -> LN -> SiLU -> Linear -> LN -> SiLU -> Linear (so2.py:54-163)."""
 
-    def __init__(self, w, prefix, device, n_gauss):
+    def __init__(self, w, prefix, device, n_gauss, mode=None):
         g = lambda k: w[f"{prefix}.{k}"]
         self.k_in = g("net.0.weight").shape[1]
         self.hidden = g("net.0.weight").shape[0]
@@ -46,15 +59,15 @@ class RadialWeights:
         self.w0t = _dev(g("net.0.weight").T, device)
         self.b0 = _dev(g("net.0.bias"), device)
         self.ln1w, self.ln1b = _dev(g("net.1.weight"), device), _dev(g("net.1.bias"), device)
-        self.w3t = _dev(g("net.3.weight").T, device)
+        self.w3t = _gw(g("net.3.weight").T, device, mode)
         self.b3 = _dev(g("net.3.bias"), device)
         self.ln4w, self.ln4b = _dev(g("net.4.weight"), device), _dev(g("net.4.bias"), device)
-        self.w6t = _dev(g("net.6.weight").T, device)
+        self.w6t = _gw(g("net.6.weight").T, device, mode)
         self.b6 = _dev(g("net.6.bias"), device)
         # adjoint operands: g @ W for each Linear; only the gaussian columns of net.0 matter for
         # the force (the element-embedding columns of x_edge do not depend on positions)
-        self.w6 = _dev(g("net.6.weight"), device)
-        self.w3 = _dev(g("net.3.weight"), device)
+        self.w6 = _gw(g("net.6.weight"), device, mode)
+        self.w3 = _gw(g("net.3.weight"), device, mode)
         self.w0g = _dev(g("net.0.weight")[:, :n_gauss], device)
 
 
@@ -73,7 +86,7 @@ def _so2_block(wm):
 class SO2Weights:
     """SO2Convolution (so2.py:166-330) for lmax = mmax = 2."""
 
-    def __init__(self, w, prefix, device, cin, hout, extra, n_gauss):
+    def __init__(self, w, prefix, device, cin, hout, extra, n_gauss, mode=None):
         self.cin, self.hout, self.extra = cin, hout, extra
         wm0 = w[f"{prefix}.fc_m0.weight"]            # [extra + 3 hout, 3 cin]
         bm0 = w[f"{prefix}.fc_m0.bias"]
@@ -81,16 +94,16 @@ class SO2Weights:
             raise RuntimeError(_UNSUPPORTED.format(what=f"fc_m0 {tuple(wm0.shape)}"))
         # one m = 0 GEMM yields [gating (extra) | coefficients 0..2 (3 hout)], the column order of
         # the torch weight; its adjoint is one GEMM with the weight as stored
-        self.wm0_t = _dev(wm0.T, device)                                # [3 cin, extra + 3 hout]
+        self.wm0_t = _gw(wm0.T, device, mode)                           # [3 cin, extra + 3 hout]
         self.bm0 = _dev(bm0, device)
-        self.wm0 = _dev(wm0, device)                                    # [extra + 3 hout, 3 cin]
+        self.wm0 = _gw(wm0, device, mode)                               # [extra + 3 hout, 3 cin]
         b1 = _so2_block(w[f"{prefix}.so2_m_conv.0.fc.weight"])          # [4 cin, 4 hout]
         b2 = _so2_block(w[f"{prefix}.so2_m_conv.1.fc.weight"])          # [2 cin, 2 hout]
         if b1.shape != (4 * cin, 4 * hout) or b2.shape != (2 * cin, 2 * hout):
             raise RuntimeError(_UNSUPPORTED.format(what="SO(2) m>0 weight shapes"))
-        self.w1, self.w1_t = _dev(b1, device), _dev(b1.T, device)
-        self.w2, self.w2_t = _dev(b2, device), _dev(b2.T, device)
-        self.rad = (RadialWeights(w, f"{prefix}.rad_func", device, n_gauss)
+        self.w1, self.w1_t = _gw(b1, device, mode), _gw(b1.T, device, mode)
+        self.w2, self.w2_t = _gw(b2, device, mode), _gw(b2.T, device, mode)
+        self.rad = (RadialWeights(w, f"{prefix}.rad_func", device, n_gauss, mode)
                     if f"{prefix}.rad_func.net.0.weight" in w else None)
 
 
@@ -143,12 +156,14 @@ class GridWeights:
 
 
 class BlockWeights:
-    def __init__(self, w, prefix, device, cfg, to_grid, from_grid, n_gauss):
+    def __init__(self, w, prefix, device, cfg, to_grid, from_grid, n_gauss, mode=None):
         C, H, L = cfg["sphere_channels"], cfg["hidden_channels"], cfg["lmax"]
         self.norm_1 = NormWeights(w, f"{prefix}.norm_1", device)
         self.norm_2 = NormWeights(w, f"{prefix}.norm_2", device)
-        self.so2_1 = SO2Weights(w, f"{prefix}.edge_wise.so2_conv_1", device, 2 * C, H, L * H, n_gauss)
-        self.so2_2 = SO2Weights(w, f"{prefix}.edge_wise.so2_conv_2", device, H, C, 0, n_gauss)
+        self.so2_1 = SO2Weights(w, f"{prefix}.edge_wise.so2_conv_1", device, 2 * C, H, L * H,
+                                n_gauss, mode)
+        self.so2_2 = SO2Weights(w, f"{prefix}.edge_wise.so2_conv_2", device, H, C, 0, n_gauss,
+                                mode)
         if self.so2_1.rad is None:
             raise RuntimeError(_UNSUPPORTED.format(what="so2_conv_1 without a radial MLP"))
         self.ff_type = cfg.get("ff_type", "grid")
@@ -162,9 +177,13 @@ class Backbone:
     """eSCN-MD backbone + energy head weights on the device (reference model.py:175-247)."""
 
     def __init__(self, weights, device, cfg, to_grid_mat=None, from_grid_mat=None, *, fast=False,
-                 n_gauss=None):
+                 n_gauss=None, precision="f32"):
         if fast:
             raise RuntimeError("fast (reduced-precision) mode is not part of this fp32 build")
+        if precision not in PRECISIONS:
+            raise RuntimeError(f"precision must be one of {sorted(PRECISIONS)}")
+        self.precision = precision
+        mode = PRECISIONS[precision]
         lmax, mmax = cfg["lmax"], cfg.get("mmax", cfg["lmax"])
         if lmax != 2 or mmax != 2:
             raise RuntimeError(_UNSUPPORTED.format(what=f"lmax={lmax}, mmax={mmax}"))
@@ -177,10 +196,10 @@ class Backbone:
         self.n_gauss = nb
         w = weights
         dev = self.device
-        self.blocks = [BlockWeights(w, f"blocks.{i}", dev, cfg, to_grid_mat, from_grid_mat, nb)
+        self.blocks = [BlockWeights(w, f"blocks.{i}", dev, cfg, to_grid_mat, from_grid_mat, nb, mode)
                        for i in range(cfg["num_layers"])]
         self.final_norm = NormWeights(w, "norm", dev)
-        self.edge_degree = RadialWeights(w, "edge_degree_embedding.rad_func", dev, nb)
+        self.edge_degree = RadialWeights(w, "edge_degree_embedding.rad_func", dev, nb, mode)
         self.sphere_emb = _dev(w["sphere_embedding.weight"], dev)
         self.src_emb = _dev(w["source_embedding.weight"], dev)
         self.tgt_emb = _dev(w["target_embedding.weight"], dev)
@@ -192,9 +211,9 @@ class Backbone:
         # the first layers of all radial MLPs read the same x_edge: one GEMM for all of them, and one
         # for the gaussian part of their input adjoints (order: edge-degree, then block 0..L-1)
         self.radials = [self.edge_degree] + [b.so2_1.rad for b in self.blocks]
-        self.rad_w0t_all = torch.cat([r.w0t for r in self.radials], 1).contiguous()
+        self.rad_w0t_all = _gw(torch.cat([r.w0t for r in self.radials], 1).contiguous(), dev, mode)
         self.rad_b0_all = torch.cat([r.b0 for r in self.radials]).contiguous()
-        self.rad_w0g_all = torch.cat([r.w0g for r in self.radials], 0).contiguous()
+        self.rad_w0g_all = _gw(torch.cat([r.w0g for r in self.radials], 0).contiguous(), dev, mode)
         if len({r.hidden for r in self.radials}) != 1 or len({r.k_in for r in self.radials}) != 1:
             raise RuntimeError(_UNSUPPORTED.format(what="radial MLPs of different widths"))
         self.gate_idx_mprime = torch.tensor(GATE_IDX_MPRIME, dtype=torch.int32, device=dev)

@@ -29,6 +29,7 @@ import torch
 
 from . import _native as nat
 from .geometry import radius_graph
+from .model import PRECISIONS, _gw
 from .weights import NpzBundle
 
 HIDDEN_DIM = 1024  # the reference's fixed MLP width (orb_calculator.py:57)
@@ -188,12 +189,12 @@ class _MLPNorm:
     """One MLPNorm (orb_model.py:127-173): forward w_t [in, out] / bias, backward w [out, in],
     RMSNorm weight."""
 
-    def __init__(self, w, prefix, device):
+    def __init__(self, w, prefix, device, mode=None):
         self.w_t, self.b, self.w = [], [], []
         for i in range(3):
             W = w[f"{prefix}.mlp.NN-{i}.weight"]
-            self.w_t.append(_dev(W.T.contiguous(), device))
-            self.w.append(_dev(W, device))
+            self.w_t.append(_gw(W.T.contiguous(), device, mode))
+            self.w.append(_gw(W, device, mode))
             self.b.append(_dev(w[f"{prefix}.mlp.NN-{i}.bias"], device))
         self.norm = _dev(w[f"{prefix}.layer_norm.weight"], device)
         self.hidden = int(self.w_t[0].shape[1])
@@ -204,17 +205,17 @@ class _Layer:
     """AttentionInteractionLayer weights (orb_model.py:203-223) with the first edge-MLP weight
     split by input block: W0 = [W_e | W_s | W_r] over [e | n[send] | n[recv]]."""
 
-    def __init__(self, w, prefix, device, C):
-        self.edge = _MLPNorm(w, f"{prefix}._edge_mlp", device)
-        self.node = _MLPNorm(w, f"{prefix}._node_mlp", device)
+    def __init__(self, w, prefix, device, C, mode=None):
+        self.edge = _MLPNorm(w, f"{prefix}._edge_mlp", device, mode)
+        self.node = _MLPNorm(w, f"{prefix}._node_mlp", device, mode)
         W0 = w[f"{prefix}._edge_mlp.mlp.NN-0.weight"]            # [H, 3C]
         if W0.shape[1] != 3 * C:
             raise ValueError(f"{prefix}: edge MLP input is {W0.shape[1]}, expected {3 * C}")
         We, Ws, Wr = W0[:, :C], W0[:, C:2 * C], W0[:, 2 * C:]
-        self.we_t = _dev(We.T.contiguous(), device)                    # [C, H]
-        self.wsr_t = _dev(torch.cat([Ws.T, Wr.T], 1).contiguous(), device)  # [C, 2H]
-        self.we = _dev(We.contiguous(), device)                        # [H, C]
-        self.wsr = _dev(torch.cat([Ws, Wr], 0).contiguous(), device)     # [2H, C]
+        self.we_t = _gw(We.T.contiguous(), device, mode)                    # [C, H]
+        self.wsr_t = _gw(torch.cat([Ws.T, Wr.T], 1).contiguous(), device, mode)  # [C, 2H]
+        self.we = _gw(We.contiguous(), device, mode)                        # [H, C]
+        self.wsr = _gw(torch.cat([Ws, Wr], 0).contiguous(), device, mode)     # [2H, C]
         self.attn_w = _dev(torch.cat([w[f"{prefix}._receive_attn.weight"].reshape(-1),
                                       w[f"{prefix}._send_attn.weight"].reshape(-1)]), device)
         self.attn_b = _dev(torch.cat([w[f"{prefix}._receive_attn.bias"].reshape(-1),
@@ -228,8 +229,12 @@ class _Layer:
 class OrbModel:
     """Device-resident Orb-v3 weights, built once per checkpoint (orb_calculator.py:54-73)."""
 
-    def __init__(self, weights, cfg, device="cuda"):
+    def __init__(self, weights, cfg, device="cuda", precision="f32"):
         nat.load()
+        if precision not in PRECISIONS:
+            raise RuntimeError(f"precision must be one of {sorted(PRECISIONS)}")
+        self.precision = precision
+        mode = PRECISIONS[precision]
         w = {k: torch.as_tensor(v, dtype=torch.float32) for k, v in weights.items()}
         self.cfg = dict(cfg)
         self.device = torch.device(device)
@@ -246,9 +251,9 @@ class OrbModel:
                                "(conservative checkpoints only)")
         dev = self.device
         self.node_emb = w["atom_emb.embeddings.weight"]          # host table, gathered per graph
-        self.enc_node = _MLPNorm(w, "_encoder._node_fn", dev)
-        self.enc_edge = _MLPNorm(w, "_encoder._edge_fn", dev)
-        self.layers = [_Layer(w, f"gnn_stacks.{i}", dev, self.C)
+        self.enc_node = _MLPNorm(w, "_encoder._node_fn", dev, mode)
+        self.enc_edge = _MLPNorm(w, "_encoder._edge_fn", dev, mode)
+        self.layers = [_Layer(w, f"gnn_stacks.{i}", dev, self.C, mode)
                        for i in range(int(cfg["num_message_passing_steps"]))]
         self.H = self.layers[0].edge.hidden if self.layers else self.enc_edge.hidden
         for L in self.layers:

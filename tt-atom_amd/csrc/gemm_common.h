@@ -5,6 +5,7 @@
 #include "common.h"
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 namespace tta_gemm {
 
@@ -44,6 +45,40 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& p, const floatx4 (&a
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = m0 + i * 16 + lk * 4 + r;
+        if (row >= p.M) continue;
+        float v = acc[i][j][r] + bv;
+        if (p.P)
+          v += p.P[(int64_t)p.idx0[row] * p.ldp + col] +
+               p.P[(int64_t)p.idx1[row] * p.ldp + p.off1 + col];
+        const int64_t off = (int64_t)row * p.ldc + col;
+        if (EPI == EPI_SILU) v = tta_silu(v);
+        if (EPI == EPI_ACCUM) v += C[off];
+        if (EPI == EPI_PRE_SILU) C2[off] = tta_silu(v);
+        if (EPI == EPI_SILU_GRAD) v = v * tta_silu_grad(aux[off]);
+        C[off] = v;
+      }
+    }
+  }
+}
+
+// Accumulator layout of v_mfma_f32_32x32x16_bf16: lane l holds, in element r = 0..15,
+// D[8*(r/4) + 4*(l/32) + r%4][l%32].
+template <int TI, int TJ>
+__device__ __forceinline__ void store_tiles32(const GemmArgs& p,
+                                              const floatx16 (&acc)[TI][TJ], int m0,
+                                              int n0, int l32, int lh, float* C, float* C2,
+                                              const float* aux, const float* bias) {
+  const int EPI = p.epi;
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) {
+    const int col = n0 + j * 32 + l32;
+    if (col >= p.N) continue;
+    const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (row >= p.M) continue;
         float v = acc[i][j][r] + bv;
         if (p.P)

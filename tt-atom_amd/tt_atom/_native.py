@@ -236,7 +236,7 @@ def _split_ok(x, pw):
     """The split-bf16 kernel (128 x 128 x 32 tiles) runs edge-level GEMMs; short-K or small-M
     products stay on the fp32 MFMA kernel, whose smaller tiles fill the chip better there."""
     M, K = x.shape
-    return (isinstance(pw, PackedWeight) and pw.packed is not None and M >= 4096 and K >= 192
+    return (isinstance(pw, PackedWeight) and pw.packed is not None and M >= 4096 and K >= 128
             and x.data_ptr() % 16 == 0 and _ld(x, "x") % 4 == 0)
 
 

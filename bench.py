@@ -12,11 +12,14 @@ blocks, energy head, the full reverse pass and the geometric VJP, all in HIP ker
 ``value`` = atoms * steps / wall time of the timed steps (atom-steps/s).
 
 Also reported on the same JSON line:
-  roofline      the dominant kernel (the fp32 MFMA GEMM, one kernel symbol for every GEMM of the
-                step): algorithmic FLOPs of its launches in the timed region / their HIP-event
-                durations (recorded on the launch stream), against the 157.3 TFLOP/s fp32 MFMA
-                peak; ``traffic`` = HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE
-                when profiles/gemm_f32_traffic_c3.txt holds them, else null.
+  roofline      the dominant kernel (the split-bf16 MFMA GEMM that runs the edge-level
+                contractions at fp32 accuracy): algorithmic FLOPs (2MNK) of its launches in the
+                timed region / their HIP-event durations (recorded on the launch stream), against
+                the ceiling of its arithmetic (bf16 dense MFMA peak 2.5 PFLOP/s / 6 plane
+                products); ``traffic`` = HBM bytes per launch from rocprofv3 FETCH_SIZE +
+                WRITE_SIZE when profiles/gemm_bf16x6_traffic_c3.txt holds them, else null.  The
+                other GEMM kernel family (fp32 MFMA, node-level and short-K products) is listed
+                under ``gemm_families``.
   cpu_baseline  the CPU oracle (PyTorch-CPU restatement of the reference path) on a bounded sample
                 of the same workload: the C3 model on a 512-atom cluster of the same density
                 (one step after a small warm-up), in atom-steps/s.
@@ -36,36 +39,47 @@ for p in (ROOT, ROOT / "tt-atom_amd"):
         sys.path.insert(0, str(p))
 
 METRIC = "atom-steps/s (energy+forces), uma-s-1 arch 2,048 atoms; % HBM/MFMA roofline"
-PEAK_FP32_MFMA_TFLOPS = 157.3
-TRAFFIC_FILE = ROOT / "profiles" / "gemm_f32_traffic_c3.txt"
+# MI355X published dense peaks (TFLOP/s).  The split-bf16 GEMM computes an fp32-accurate product
+# with 6 bf16 plane products (mode 6): its fp32-equivalent ceiling is the bf16 peak / 6.
+PEAK_FP32_MFMA = 157.3
+PEAK_BF16_MFMA = 2500.0
+PEAKS = {"f32": PEAK_FP32_MFMA, "bf16x6": PEAK_BF16_MFMA / 6, "bf16x3": PEAK_BF16_MFMA / 3,
+         "bf16x1": PEAK_BF16_MFMA}
+KERNELS = {"f32": "gemm_f32_kernel (fp32 MFMA 16x16x4)",
+           "bf16x6": "gemm_bf16x_kernel<4,6> (split-bf16, 3x3 planes / 6 products, fp32-accurate)",
+           "bf16x3": "gemm_bf16x_kernel<4,3> (split-bf16, 2x2 planes / 3 products)",
+           "bf16x1": "gemm_bf16x_kernel<2,1> (bf16 operands)"}
+TRAFFIC_FILE = ROOT / "profiles" / "gemm_bf16x6_traffic_c3.txt"
 
 
 class GemmEvents:
-    """HIP events around every GEMM launch (same stream as the launch)."""
+    """HIP events around every GEMM launch (same stream as the launch), per kernel family."""
 
     def __init__(self, torch):
         self.torch = torch
-        self.pairs = []
-        self.flops = 0.0
-        self.nbytes = 0.0
+        self.kinds = {}
         self._cur = None
 
-    def before(self, flops, nbytes):
+    def before(self, flops, nbytes, kind="f32"):
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
-        self._cur = e
-        self.flops += flops
-        self.nbytes += nbytes
+        self._cur = (e, kind)
+        k = self.kinds.setdefault(kind, {"pairs": [], "flops": 0.0, "nbytes": 0.0})
+        k["flops"] += flops
+        k["nbytes"] += nbytes
 
     def after(self):
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
-        self.pairs.append((self._cur, e))
+        start, kind = self._cur
+        self.kinds[kind]["pairs"].append((start, e))
 
     def summary(self):
-        ms = sum(a.elapsed_time(b) for a, b in self.pairs)
-        n = len(self.pairs)
-        return n, self.flops, ms
+        out = {}
+        for kind, k in self.kinds.items():
+            ms = sum(a.elapsed_time(b) for a, b in k["pairs"])
+            out[kind] = dict(n=len(k["pairs"]), flops=k["flops"], nbytes=k["nbytes"], ms=ms)
+        return out
 
 
 def build_c3(torch, n_atoms=2048, seed=None):
@@ -256,10 +270,17 @@ def main():
     energy = energy_of()
     if not (energy == energy) or not bool(torch.isfinite(forces_of()).all()):
         raise RuntimeError("non-finite energy or forces")
-    n_launch, flops, gemm_ms = probe.summary()
-    achieved = flops / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
-    traffic = read_traffic() if wl == "c3" else None
+    fam = probe.summary()
+    gemm_ms = sum(v["ms"] for v in fam.values())
+    dom = max(fam, key=lambda k: fam[k]["ms"])
+    d = fam[dom]
+    achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12 if d["ms"] > 0 else 0.0
+    traffic = read_traffic() if (wl == "c3" and dom == "bf16x6") else None
     ms_step = dt / args.steps * 1e3
+    others = {k: {"launches": v["n"], "avg_launch_us": round(v["ms"] * 1e3 / max(1, v["n"]), 2),
+                  "achieved_tflops": round(v["flops"] / max(1e-12, v["ms"] * 1e-3) / 1e12, 2),
+                  "peak_tflops": round(PEAKS[k], 1), "share_of_step": round(v["ms"] / (dt * 1e3), 4)}
+              for k, v in fam.items()}
     if wl == "c5":
         metric = "atom-steps/s (energy+forces), Orb-v3-conservative arch, 256 molecules (C5)"
         workload = ("C5: Orb-v3-conservative arch (5 layers, latent 256, MLP hidden 1024, 8 "
@@ -290,14 +311,18 @@ def main():
         "data": data,
         "config": {"workload": workload, "atoms": n_atoms, "edges": n_edges,
                    "neighbor_list_host_ms": round(nl_ms, 1), "energy": energy},
-        "roofline": {"bound": "mfma", "kernel": "gemm_f32_kernel (all GEMMs of the step)",
-                     "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-                     "traffic": traffic, "launches": n_launch,
-                     "algorithmic_bytes_per_launch": round(probe.nbytes / max(1, n_launch)),
-                     "algorithmic_flops_per_launch": round(flops / max(1, n_launch)),
-                     "avg_launch_us": round(gemm_ms * 1e3 / max(1, n_launch), 2),
-                     "gemm_share_of_step": round(gemm_ms / (dt * 1e3), 4)},
+        "roofline": {"bound": "mfma", "kernel": KERNELS[dom],
+                     "achieved": round(achieved, 3), "peak": round(PEAKS[dom], 2),
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAKS[dom], 4),
+                     "traffic": traffic, "launches": d["n"],
+                     "algorithmic_bytes_per_launch": round(d["nbytes"] / max(1, d["n"])),
+                     "algorithmic_flops_per_launch": round(d["flops"] / max(1, d["n"])),
+                     "avg_launch_us": round(d["ms"] * 1e3 / max(1, d["n"]), 2),
+                     "peak_note": ("algorithmic fp32 GEMM flops (2MNK) against the ceiling of "
+                                   "the kernel's arithmetic: fp32 MFMA 157.3, or the bf16 dense "
+                                   "MFMA 2500 / number of plane products"),
+                     "gemm_share_of_step": round(gemm_ms / (dt * 1e3), 4),
+                     "gemm_families": others},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline_c5(torch) if wl == "c5" else cpu_baseline(torch)

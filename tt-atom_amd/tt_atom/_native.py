@@ -154,9 +154,10 @@ def _rows(t, rows, ld, width, name="tensor"):
 EPI_STORE, EPI_SILU, EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD = 0, 1, 2, 3, 4
 
 # Optional measurement hook: when set, every GEMM launch is bracketed by
-# ``probe.before(flops, nbytes)`` and ``probe.after()`` (the benchmark records HIP events on the
-# launch stream there).  nbytes is the algorithmic traffic: A, B and C once (C twice when
-# accumulated, plus the second output / auxiliary input of epilogues 3 and 4).
+# ``probe.before(flops, nbytes, kind)`` and ``probe.after()`` (the benchmark records HIP events on
+# the launch stream there).  nbytes is the algorithmic traffic: A, B and C once (C twice when
+# accumulated, plus the second output / auxiliary input of epilogues 3 and 4); kind is "f32" for
+# the fp32 MFMA kernel and "bf16x<mode>" for the split-bf16 kernel.
 _gemm_probe = None
 
 
@@ -177,7 +178,7 @@ def gemm(A, B, C, *, M, N, K, lda, ldb, ldc, bias=None, epilogue=EPI_STORE, C2=N
         c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD))
         nbytes = 4.0 * (M * K * (batch if sA else 1) + K * N * (batch if sB else 1)
                         + c_passes * M * N * batch)
-        probe.before(2.0 * M * N * K * batch, nbytes)
+        probe.before(2.0 * M * N * K * batch, nbytes, "f32")
     _call("tta_gemm_f32", A.data_ptr(), B.data_ptr(), C.data_ptr(),
           None if bias is None else bias.data_ptr(), None if C2 is None else C2.data_ptr(),
           None if aux is None else aux.data_ptr(), M, N, K, lda, ldb, ldc, batch, sA, sB, sC,
@@ -220,7 +221,8 @@ def _gemm_bf16x(x, pw, out, bias, epilogue, out2, aux, P=None, idx0=None, idx1=N
     probe = _gemm_probe
     if probe is not None:
         c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD)) + (2 if P is not None else 0)
-        probe.before(2.0 * M * N * K, 4.0 * (M * K + K * N + c_passes * M * N))
+        probe.before(2.0 * M * N * K, 4.0 * (M * K + K * N + c_passes * M * N),
+                     f"bf16x{pw.mode}")
     _call("tta_gemm_bf16x", x.data_ptr(), pw.packed.data_ptr(), out.data_ptr(),
           None if bias is None else _ptr(bias, numel=N, name="bias"),
           None if out2 is None else out2.data_ptr(), None if aux is None else aux.data_ptr(),
@@ -439,7 +441,7 @@ def linear_gather(x, w_t, bias, out, P, idx0, idx1, off1, *, epilogue=EPI_STORE,
     probe = _gemm_probe
     if probe is not None:
         c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD))
-        probe.before(2.0 * M * N * K, 4.0 * (M * K + K * N + (c_passes + 2) * M * N))
+        probe.before(2.0 * M * N * K, 4.0 * (M * K + K * N + (c_passes + 2) * M * N), "f32")
     _call("tta_gemm_f32_gather", x.data_ptr(), w_t.data_ptr(), out.data_ptr(),
           None if bias is None else _ptr(bias, numel=N, name="bias"),
           None if out2 is None else out2.data_ptr(), None, M, N, K, _ld(x, "x"),

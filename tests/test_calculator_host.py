@@ -64,3 +64,39 @@ def test_generators_are_seeded_and_sized():
     ei, vec = synthetic.c2_graph()
     assert ei.shape == (2, 204800) and np.all(ei[0] != ei[1]) and np.all(np.diff(ei[1]) >= 0)
     assert np.allclose(np.linalg.norm(vec, axis=1).min(), 0.8, atol=1e-3)
+
+
+def test_orb_zbl_forces_and_stress_are_derivatives_of_its_energy():
+    """Host ZBL pair repulsion: forces = -dE/dpos and stress = dE/dstrain / V by fp64 finite
+    differences (orb_model.py:491-585), on a short-contact periodic pair system."""
+    import numpy as np
+    import torch
+    from tt_atom import orb_calculator as OC
+    from tt_atom import orb
+    radii = np.full(120, 1.1)
+    pos = np.array([[0.0, 0.0, 0.0], [1.3, 0.2, 0.1], [0.4, 1.5, 0.3]])
+    Z = np.array([6, 8, 1])
+    cell = np.eye(3) * 4.0
+    bg = orb.assemble_orb([(pos, Z, cell, [True] * 3)], 3.0, 20)
+    args = (bg.Z, bg.senders, bg.receivers)
+    e, F, s = OC.zbl_energy_forces_stress(*args, bg.pos.double(), bg.cell_shift, radii, cell)
+    assert e > 0
+    h = 1e-6
+    for a, k in ((0, 0), (1, 2), (2, 1)):
+        p1, p2 = bg.pos.double().clone(), bg.pos.double().clone()
+        p1[a, k] += h
+        p2[a, k] -= h
+        e1 = OC.zbl_energy_forces_stress(*args, p1, bg.cell_shift, radii)[0]
+        e2 = OC.zbl_energy_forces_stress(*args, p2, bg.cell_shift, radii)[0]
+        assert abs(-(e1 - e2) / (2 * h) - F[a, k]) < 1e-6 * max(1.0, abs(F[a, k]))
+    # stress: strain the positions, the cell and therefore the image shifts together
+    eps = np.zeros((3, 3))
+    eps[0, 1] = eps[1, 0] = h
+    vals = []
+    for sgn in (1, -1):
+        M = np.eye(3) + sgn * eps
+        vals.append(OC.zbl_energy_forces_stress(*args, bg.pos.double() @ torch.tensor(M),
+                                                bg.cell_shift.double() @ torch.tensor(M),
+                                                radii)[0])
+    fd = (vals[0] - vals[1]) / (2 * h) / 2 / 64.0          # d/d eps_01 of a symmetric strain / V
+    assert abs(fd - s[5]) < 1e-6 * max(1.0, abs(s[5]))

@@ -187,3 +187,36 @@ def test_orb_c5_architecture_reduced_batch(nat):
                                            receivers=bg.receivers, atomic_numbers=bg.Z,
                                            natoms=bg.natoms, cell_shift=bg.cell_shift)
     assert torch.equal(raw, raw2) and torch.equal(F, F2)
+
+
+def test_orb_session_single_and_batch(nat, tmp_path):
+    """OrbSession (the array-level core of OrbCalculator): a saved bundle round trip, one system
+    against the oracle, and evaluate_batch == per-system evaluate (ZBL on, with a synthetic
+    covalent-radius table, since ase is absent)."""
+    from tt_atom import orb_calculator as OC
+    cfg = dict(S.CFG_ORB_TINY)
+    w = S.random_orb_weights(cfg, 31)
+    path = tmp_path / "orb.npz"
+    orb.save_orb_bundle(path, cfg, w)
+    systems = S.c5_systems(13, K=3, n_min=6, n_max=12, side=5.0)
+    radii = np.full(120, 0.45)
+    sess = OC.OrbSession(str(path), pair_repulsion=True, covalent_radii=radii)
+    res = [sess.evaluate(p, z) for p, z in systems]
+    # oracle: raw GNN energy / forces + the same host ZBL
+    for (p, z), r in zip(systems, res):
+        bg = orb.assemble_orb([(p, z)], cfg["cutoff"], cfg["max_num_neighbors"])
+        raw, F = _oracle(cfg, w, bg)
+        n = bg.natoms[0]
+        e_z, f_z, _ = OC.zbl_energy_forces_stress(bg.Z, bg.senders, bg.receivers, bg.pos,
+                                                  bg.cell_shift, radii)
+        e_ref = float(O.denormalize_energy(raw[0], bg.Z, n,
+                                           w["energy_head.normalizer.bn.running_mean"],
+                                           w["energy_head.normalizer.bn.running_var"],
+                                           w["energy_head.reference.linear.weight"])) + e_z
+        f_ref = O.denormalize_forces(F, n, w["energy_head.normalizer.bn.running_var"]).numpy() + f_z
+        assert abs(r["energy"] - e_ref) <= 1e-6 * max(1.0, abs(e_ref))
+        assert np.abs(r["forces"] - f_ref).max() <= 1e-4
+    batch = sess.evaluate_batch(systems)
+    for k, r in enumerate(res):
+        assert abs(batch["energy"][k] - r["energy"]) <= 1e-6 * max(1.0, abs(r["energy"]))
+        assert np.abs(batch["forces"][k] - r["forces"]).max() <= 2e-5

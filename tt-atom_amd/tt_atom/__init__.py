@@ -1,10 +1,12 @@
-"""tt_atom -- MI355X (gfx950) build of the eSCN-MD (UMA) edgewise hot path.
+"""tt_atom -- MI355X (gfx950) build of the eSCN-MD (UMA) and Orb-v3 edgewise hot paths.
 
 Same module and class names as the reference package for the path it covers
 (``geometry.HostGeometry``, ``geometry.radius_graph``, ``geometry.csd_embedding``,
 ``model.Backbone``, ``model.GraphContext``, ``forces.energy_and_forces``,
-``trace.TracedEngine``, ``weights.WeightBundle``, ``calculator.TTAtomCalculator``); the compute
+``trace.TracedEngine``, ``weights.WeightBundle``, ``calculator.TTAtomCalculator``,
+``orb.OrbWeights`` / ``orb.energy_and_forces(_batch)``, ``orb_calculator.OrbCalculator``); the compute
 runs in hand-written HIP kernels behind the C ABI of ``include/tt_atom_hip.h``.
 """
-__all__ = ["geometry", "model", "forces", "trace", "weights", "synthetic", "calculator"]
+__all__ = ["geometry", "model", "forces", "trace", "weights", "synthetic", "calculator", "orb",
+           "orb_calculator"]
 __version__ = "0.1.0"

@@ -1,0 +1,227 @@
+"""``OrbCalculator`` -- ASE calculator over the MI355X Orb-v3 step (reference orb_calculator.py:25-327).
+
+``OrbSession`` holds one Orb-v3 conservative checkpoint on one GPU and evaluates arrays (one
+system, ``evaluate``) or a disjoint-union batch (``evaluate_batch``) as the reference's
+``calculate`` / ``evaluate_batch`` do: neighbour list (senders = tgt, receivers = src), node
+embedding and optional charge/spin conditioning, one device forward + backward, then the energy
+normaliser ``E = (raw sigma + mu) n + sum ref[Z]``, ``F = raw_F sigma n`` and
+``stress = virial sigma n / V`` (orb_model.py:459-600), plus the ZBL pair repulsion
+(orb_model.py:491-585) when enabled.  The step engine is kept while the graph is unchanged.
+``OrbCalculator`` adapts it to ASE; ``ase`` is optional and only that class (and the default ZBL
+radius table) needs it.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import orb
+from .calculator import full_3x3_to_voigt_6
+
+try:  # ASE is optional
+    from ase.calculators.calculator import Calculator as _AseCalculator
+    from ase.calculators.calculator import all_changes as _all_changes
+    HAVE_ASE = True
+except ImportError:  # pragma: no cover - exercised where ase is absent
+    _AseCalculator = object
+    _all_changes = ()
+    HAVE_ASE = False
+
+
+# ----------------------------------------------------------------------------- ZBL (host)
+# Universal ZBL screening function and the Orb pair-repulsion envelope (orb_model.py:491-538);
+# the constants are the physical ones and are kept as published.
+_ZBL_C = (0.1818, 0.5099, 0.2802, 0.02817)
+_ZBL_D = (3.2, 0.9423, 0.4028, 0.2016)
+_ZBL_A_EXP, _ZBL_A_PRE, _BOHR, _COULOMB = 0.300, 0.4543, 0.529, 14.3996
+
+
+def zbl_energy(Z, senders, receivers, vectors, covalent_radii, p=6, aggregation="mean"):
+    """Pair repulsion of one system (fp64, differentiable in ``vectors``).  Orb's atomic-number
+    embedding is indexed by the stored number and its ZBL basis adds one to it
+    (orb_model.py:507-510); that convention is kept."""
+    Zu = Z[senders].double() + 1
+    Zv = Z[receivers].double() + 1
+    a = _ZBL_A_PRE * _BOHR / (Zu ** _ZBL_A_EXP + Zv ** _ZBL_A_EXP)
+    x = torch.linalg.norm(vectors.double(), dim=1)
+    phi = sum(c * torch.exp(-d * x / a) for c, d in zip(_ZBL_C, _ZBL_D))
+    rad = torch.as_tensor(covalent_radii, dtype=torch.float64)
+    r_max = rad[Zu.long()] + rad[Zv.long()]
+    q = x / r_max
+    env = (1.0 - (p + 1) * (p + 2) / 2.0 * q ** p + p * (p + 2) * q ** (p + 1)
+           - p * (p + 1) / 2.0 * q ** (p + 2)) * (x < r_max).double()
+    v = 0.5 * _COULOMB * Zu * Zv / x * phi * env
+    per_node = torch.zeros(Z.shape[0], dtype=torch.float64).index_add_(0, senders, v)
+    if aggregation == "mean":
+        return per_node.mean()
+    if aggregation == "sum":
+        return per_node.sum()
+    raise ValueError(f"aggregation must be 'mean' or 'sum', got {aggregation!r}")
+
+
+def zbl_energy_forces_stress(Z, senders, receivers, pos, shift, covalent_radii, cell=None,
+                             aggregation="mean"):
+    """(energy, forces [N,3], Voigt stress or None) of the pair repulsion by host autograd
+    (orb_model.py:541-585)."""
+    pos = torch.as_tensor(pos, dtype=torch.float64).detach().clone().requires_grad_(True)
+    strain = torch.zeros(3, 3, dtype=torch.float64, requires_grad=cell is not None)
+    v = pos[receivers] - pos[senders]
+    if shift is not None:
+        v = v + torch.as_tensor(shift, dtype=torch.float64)
+    if cell is not None:
+        v = v @ (torch.eye(3, dtype=torch.float64) + 0.5 * (strain + strain.T))
+    e = zbl_energy(Z, senders, receivers, v, covalent_radii, aggregation=aggregation)
+    ins = [pos] if cell is None else [pos, strain]
+    g = torch.autograd.grad(e, ins)
+    stress = None
+    if cell is not None:
+        vol = abs(float(np.linalg.det(np.asarray(cell, dtype=np.float64).reshape(3, 3))))
+        stress = full_3x3_to_voigt_6(g[1].numpy() / vol)
+    return float(e.detach()), (-g[0]).numpy(), stress
+
+
+def _default_radii():
+    try:
+        from ase.data import covalent_radii
+    except ImportError as exc:  # pragma: no cover
+        raise RuntimeError("the ZBL pair repulsion needs a covalent-radius table: install ase, "
+                           "pass covalent_radii=..., or pair_repulsion=False") from exc
+    return np.asarray(covalent_radii, dtype=np.float64)
+
+
+# ----------------------------------------------------------------------------- session
+class OrbSession:
+    """One Orb-v3 conservative checkpoint on one GPU (orb_calculator.py:26-73)."""
+
+    def __init__(self, weights, device=None, device_id=0, precision="f32", pair_repulsion=True,
+                 covalent_radii=None):
+        if isinstance(weights, str):
+            weights = orb.OrbWeights.load(weights)
+        self.cfg = dict(weights.config)
+        self._w = weights.weights
+        dev = torch.device(device) if device is not None else torch.device(f"cuda:{device_id}")
+        self.model = orb.OrbModel(self._w, self.cfg, dev, precision=precision)
+        self.r_max = float(self.cfg["cutoff"])
+        self.max_num_neighbors = int(self.cfg["max_num_neighbors"])
+        self.task = self.task_name = self.cfg.get("task", "omat")
+        self.pair_repulsion = pair_repulsion
+        self._radii = covalent_radii
+        self._engine, self._key = None, None
+
+    def _radii_table(self):
+        if self._radii is None:
+            self._radii = _default_radii()
+        return self._radii
+
+    def _run(self, bg, compute_stress):
+        N = int(bg.pos.shape[0])
+        key = (bg.senders.numel(), tuple(bg.natoms))
+        same = (self._engine is not None and self._key[0] == key
+                and torch.equal(self._key[1], bg.senders) and torch.equal(self._key[2], bg.receivers)
+                and torch.equal(self._key[3], bg.cell_shift) and torch.equal(self._key[4], bg.Z)
+                and torch.equal(self._key[5], self._cond(bg)))
+        if not same:
+            graph = orb.OrbGraph(self.model.device, senders=bg.senders, receivers=bg.receivers,
+                                 num_nodes=N, atomic_numbers=bg.Z, cell_shift=bg.cell_shift,
+                                 natoms=bg.natoms)
+            cond = self._cond(bg) if self.model.has_cond else None
+            self._engine = orb.OrbEngine(self.model, graph, cond)
+            self._key = (key, bg.senders.clone(), bg.receivers.clone(), bg.cell_shift.clone(),
+                         bg.Z.clone(), self._cond(bg))
+        p = torch.as_tensor(bg.pos, dtype=torch.float32).to(self.model.device)
+        raw, F, vir = self._engine.run(p, compute_stress)
+        return raw, F.detach().cpu().double(), (None if vir is None else vir.detach().cpu().double())
+
+    def _cond(self, bg):
+        if not self.model.has_cond:
+            return torch.zeros(0)
+        return torch.cat([self.model.charge_spin_embedding(q, s, n)
+                          for q, s, n in zip(bg.charges, bg.spins, bg.natoms)])
+
+    def evaluate(self, positions, numbers, cell=None, pbc=None, charge=0.0, spin=0.0,
+                 properties=("energy", "forces")):
+        """One system (orb_calculator.py:89-215): energy, free_energy, forces[, stress]."""
+        pbc_a = np.zeros(3, bool) if pbc is None else np.asarray(pbc, dtype=bool).reshape(-1)
+        if pbc_a.size == 1:
+            pbc_a = np.repeat(pbc_a, 3)
+        cell_a = np.asarray(cell, dtype=np.float64).reshape(3, 3) \
+            if (cell is not None and pbc_a.any()) else None
+        system = dict(positions=positions, numbers=numbers, cell=cell_a,
+                      pbc=pbc_a if cell_a is not None else None, charge=charge, spin=spin)
+        bg = orb.assemble_orb([system], self.r_max, self.max_num_neighbors)
+        want_stress = cell_a is not None and ("stress" in properties or bool(pbc_a.all()))
+        raw, F_raw, vir = self._run(bg, want_stress)
+        n = bg.natoms[0]
+        E = float(orb.denormalize_energy(raw[0], bg.Z, n, self._w))
+        F = orb.denormalize_forces(F_raw, n, self._w).numpy()
+        stress = None
+        if want_stress:
+            stress = orb.denormalize_stress(vir, n, torch.as_tensor(cell_a), self._w).numpy()
+        if self.pair_repulsion:
+            e_z, f_z, s_z = zbl_energy_forces_stress(bg.Z, bg.senders, bg.receivers, bg.pos,
+                                                     bg.cell_shift, self._radii_table(),
+                                                     cell_a if want_stress else None)
+            E, F = E + e_z, F + f_z
+            if stress is not None:
+                stress = stress + s_z
+        res = {"energy": E, "free_energy": E, "forces": F}
+        if stress is not None:
+            res["stress"] = stress
+        return res
+
+    def evaluate_batch(self, systems, properties=("energy", "forces")):
+        """Disjoint-union batch in one device step (orb_calculator.py:217-327):
+        ``dict(energy=ndarray[K], forces=list[ndarray[N_k, 3]] or None)``."""
+        want_forces = "forces" in properties
+        bg = orb.assemble_orb(systems, self.r_max, self.max_num_neighbors)
+        raw, F_raw, _ = self._run(bg, False)
+        energies, forces, off = [], [], 0
+        for k, n in enumerate(bg.natoms):
+            sl = slice(off, off + n)
+            E_k = float(orb.denormalize_energy(raw[k], bg.Z[sl], n, self._w))
+            F_k = orb.denormalize_forces(F_raw[sl], n, self._w).numpy()
+            if self.pair_repulsion:
+                m = (bg.senders >= off) & (bg.senders < off + n)
+                e_z, f_z, _ = zbl_energy_forces_stress(
+                    bg.Z[sl], bg.senders[m] - off, bg.receivers[m] - off, bg.pos[sl],
+                    bg.cell_shift[m], self._radii_table())
+                E_k, F_k = E_k + e_z, F_k + f_z
+            energies.append(E_k)
+            forces.append(F_k)
+            off += n
+        return dict(energy=np.array(energies), forces=forces if want_forces else None)
+
+
+class OrbCalculator(_AseCalculator):
+    """ASE calculator (orb_calculator.py:25-215)."""
+
+    implemented_properties = ["energy", "free_energy", "forces", "stress"]
+
+    def __init__(self, weights, device=None, device_id=0, fast=False, bucketing=False,
+                 precision="f32", **kwargs):
+        if not HAVE_ASE:
+            raise ImportError("OrbCalculator needs ase; tt_atom.orb_calculator.OrbSession "
+                              "evaluates arrays without it")
+        if fast:
+            raise RuntimeError("fast (bf8) weights are not part of this build; use "
+                               "precision='bf16' for bf16 GEMM operands")
+        super().__init__(**kwargs)
+        # bucketing pads edge counts so ttnn reuses compiled shapes; the HIP kernels are shape-
+        # generic, so it changes nothing here
+        self.session = OrbSession(weights, device=device, device_id=device_id,
+                                  precision=precision)
+        self.task = self.task_name = self.session.task
+
+    def calculate(self, atoms=None, properties=("energy", "forces"),
+                  system_changes=_all_changes):
+        super().calculate(atoms, properties, system_changes)
+        pbc = np.asarray(atoms.get_pbc())
+        res = self.session.evaluate(atoms.get_positions(), atoms.get_atomic_numbers(),
+                                    cell=np.asarray(atoms.get_cell()) if pbc.any() else None,
+                                    pbc=pbc, charge=float(atoms.info.get("charge", 0.0)),
+                                    spin=float(atoms.info.get("spin", 0.0)),
+                                    properties=properties)
+        self.results.update(res)
+
+    def evaluate_batch(self, systems, properties=("energy", "forces")):
+        return self.session.evaluate_batch(systems, properties)

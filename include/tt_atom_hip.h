@@ -76,6 +76,16 @@ int tta_gather_rotate_bw(const float* g_xf, const float* rad, const float* x, co
                          const int* tgt, const float* coef, float* g_rad, float* g_mcat,
                          float* g_coef, int64_t N, int64_t E, int64_t C, tta_stream_t stream);
 
+/* Source-only variant: out[e, m, :] = sum_j W[e,m,j] x[src_e, j, :], out [E, 9, C] m-primed --
+ * rotation.rotate (rotation.py:211-222) applied to source features gathered by edge (the C2
+ * isolated-edgewise pipeline).  Its backward writes g_in[e] = W[e]^T g_out[e] (skipped when g_in
+ * is NULL) and accumulates g_coef[e, k] += <g_out[e, m_k], x[src_e, j_k]> (rotation.py:225-260). */
+int tta_gather_rotate_src(const float* x, const int* src, const float* coef, float* out, int64_t N,
+                          int64_t E, int64_t C, tta_stream_t stream);
+int tta_gather_rotate_src_bw(const float* g_out, const float* x, const int* src, const float* coef,
+                             float* g_in, float* g_coef, int64_t N, int64_t E, int64_t C,
+                             tta_stream_t stream);
+
 /* out[n] = res[n] + sum_{e in dst segment n} contrib_e, contrib = W^T (m[e] env[e]) when
  * env_first, else ((W^T pad(m[e])) env[e]) / div.  m [E, n_in, C] with n_in 9 or 3 (the m = 0
  * block only).  Deterministic (ascending edge order, no atomics).  Replaces the inverse rotate +

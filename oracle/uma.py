@@ -175,3 +175,17 @@ def node_energy(node_emb, w):
 
 def energy(node_emb, w):
     return node_energy(node_emb, w).sum()
+
+
+def isolated_edgewise(x, ev, src, tgt, w, p, Jd, N):
+    """The isolated edgewise map (gather source features, rotate into the edge frame, SO(2)
+    convolution, rotate back, segment-sum to destinations; edgewise.py:52-86 without radial, gate
+    and envelope) as a differentiable function of the edge vectors ``ev``."""
+    from .geometry import euler_angles, eulers_to_wigner
+    C = x.shape[2]
+    perm = torch.tensor([0, 2, 6, 3, 7, 1, 5, 8, 4])
+    W = eulers_to_wigner(euler_angles(ev, 0.0), 2, [j.to(ev.dtype) for j in Jd]).index_select(1, perm)
+    xe = torch.bmm(W, x[src])
+    m = so2(xe, None, w, p, 2, 2, C, C, 0)
+    back = torch.bmm(W.transpose(1, 2), m)
+    return torch.zeros(N, 9, C, dtype=x.dtype).index_add_(0, tgt, back)

@@ -171,7 +171,8 @@ __device__ __forceinline__ void load_coef(const float* __restrict__ coef, int64_
 // -------------------------------------------------------------------------------------------
 // Forward: out[e, m, :] = (sum_j W[e,m,j] [x[src_e, j, :] | x[tgt_e, j, :]]) * rad[e, rb(m), :]
 // (edgewise.py:52-69 gather + interleave + rotate, so2.py:263-277 radial multiply).
-template <int V, bool RAD>
+// HALVES = 1 gathers x[src_e] alone (row width C): a plain rotation of gathered source features.
+template <int V, bool RAD, int HALVES = 2>
 __global__ __launch_bounds__(256) void k_gather_rotate(const float* __restrict__ x,
                                                        const int* __restrict__ src,
                                                        const int* __restrict__ tgt,
@@ -182,12 +183,13 @@ __global__ __launch_bounds__(256) void k_gather_rotate(const float* __restrict__
   const int lane = threadIdx.x & 63;
   const int e = wave_uniform(blockIdx.x * WAVES + (threadIdx.x >> 6));
   if (e >= E) return;
-  const int W = 2 * C, nq = W / V, cq = C / V;
+  const int W = HALVES * C, nq = W / V, cq = C / V;
   float c[NNZ];
   load_coef(coef, e, c);
-  const int64_t s = wave_uniform(src[e]), t = wave_uniform(tgt[e]);
+  const int64_t s = wave_uniform(src[e]), t = HALVES == 2 ? wave_uniform(tgt[e]) : 0;
   for (int q = lane; q < nq; q += 64) {
-    const float* row = q < cq ? x + s * NSPH * C + V * q : x + t * NSPH * C + V * (q - cq);
+    const float* row = (HALVES == 1 || q < cq) ? x + s * NSPH * C + V * q
+                                               : x + t * NSPH * C + V * (q - cq);
     T in[NSPH], o[NSPH];
 #pragma unroll
     for (int j = 0; j < NSPH; ++j) in[j] = ldv<V>(row + j * C);
@@ -207,8 +209,9 @@ __global__ __launch_bounds__(256) void k_gather_rotate(const float* __restrict__
 // storing them.  Writes g_mcat [E, 9, 2C] (adjoint of the interleaved gather, scattered to
 // nodes by k_node_gather_sum), g_rad [E, 6, 2C] (adjoint at the radial output, duplicate blocks
 // collapsed) and accumulates the coefficient adjoint g_coef[e, k] += <g_mrot[m_k], m_cat[j_k]>
-// (rotation.py:225-260 semantics).
-template <int V, bool RAD>
+// (rotation.py:225-260 semantics).  HALVES = 1: source-only gather of row width C; g_mcat may then
+// be NULL (only the coefficient adjoint is wanted).
+template <int V, bool RAD, int HALVES = 2>
 __global__ __launch_bounds__(256) void k_gather_rotate_bw(
     const float* __restrict__ g_xf, const float* __restrict__ rad, const float* __restrict__ x,
     const int* __restrict__ src, const int* __restrict__ tgt, const float* __restrict__ coef,
@@ -220,16 +223,17 @@ __global__ __launch_bounds__(256) void k_gather_rotate_bw(
   const int w = threadIdx.x >> 6;
   const int e = wave_uniform(blockIdx.x * WAVES + w);
   if (e >= E) return;
-  const int W = 2 * C, nq = W / V, cq = C / V;
+  const int W = HALVES * C, nq = W / V, cq = C / V;
   float c[NNZ];
   load_coef(coef, e, c);
   float gc[NNZ];
 #pragma unroll
   for (int k = 0; k < NNZ; ++k) gc[k] = 0.f;
-  const int64_t s = wave_uniform(src[e]), t = wave_uniform(tgt[e]);
+  const int64_t s = wave_uniform(src[e]), t = HALVES == 2 ? wave_uniform(tgt[e]) : 0;
   const int64_t eo = (int64_t)e * NSPH * W;
   for (int q = lane; q < nq; q += 64) {
-    const float* row = q < cq ? x + s * NSPH * C + V * q : x + t * NSPH * C + V * (q - cq);
+    const float* row = (HALVES == 1 || q < cq) ? x + s * NSPH * C + V * q
+                                               : x + t * NSPH * C + V * (q - cq);
     T in[NSPH], gm[NSPH];
 #pragma unroll
     for (int j = 0; j < NSPH; ++j) in[j] = ldv<V>(row + j * C);
@@ -250,10 +254,12 @@ __global__ __launch_bounds__(256) void k_gather_rotate_bw(
 #pragma unroll
       for (int m = 0; m < NSPH; ++m) gm[m] = gm[m] * ldv<V>(rr + rad_block(m) * W);
     }
-    T gi[NSPH];
-    rot_inv<9>(c, gm, gi);
+    if (g_mcat) {
+      T gi[NSPH];
+      rot_inv<9>(c, gm, gi);
 #pragma unroll
-    for (int j = 0; j < NSPH; ++j) stv<V>(g_mcat + eo + j * W + V * q, gi[j]);
+      for (int j = 0; j < NSPH; ++j) stv<V>(g_mcat + eo + j * W + V * q, gi[j]);
+    }
     coef_partials<9, V>(gm, in, gc);
   }
   const float tot = wave_sums<NNZ>(gc, red[w], lane);
@@ -499,6 +505,41 @@ extern "C" int tta_gather_rotate_bw(const float* g_xf, const float* rad, const f
                          (int)C);
   });
   TTA_CHECK_LAUNCH("tta_gather_rotate_bw");
+  return tta::kOk;
+}
+
+extern "C" int tta_gather_rotate_src(const float* x, const int* src, const float* coef,
+                                     float* out, int64_t N, int64_t E, int64_t C,
+                                     hipStream_t stream) {
+  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C <= 4096,
+                "tta_gather_rotate_src: unsupported channel count C=%lld", (long long)C);
+  TTA_CHECK_ARG(E >= 0 && N >= 0 && E < (1ll << 31), "tta_gather_rotate_src: bad sizes");
+  if (E == 0) return tta::kOk;
+  TTA_CHECK_ARG(x && src && coef && out, "tta_gather_rotate_src: null pointer");
+  const int V = pick_v(C);
+  TTA_V_DISPATCH(V, {
+    hipLaunchKernelGGL((k_gather_rotate<VV, false, 1>), dim3(wave_blocks(E)), dim3(256), 0,
+                       stream, x, src, nullptr, coef, nullptr, out, (int)E, (int)C);
+  });
+  TTA_CHECK_LAUNCH("tta_gather_rotate_src");
+  return tta::kOk;
+}
+
+extern "C" int tta_gather_rotate_src_bw(const float* g_out, const float* x, const int* src,
+                                        const float* coef, float* g_in, float* g_coef,
+                                        int64_t N, int64_t E, int64_t C, hipStream_t stream) {
+  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C <= 4096,
+                "tta_gather_rotate_src_bw: unsupported channel count C=%lld", (long long)C);
+  TTA_CHECK_ARG(E >= 0 && N >= 0 && E < (1ll << 31), "tta_gather_rotate_src_bw: bad sizes");
+  if (E == 0) return tta::kOk;
+  TTA_CHECK_ARG(g_out && x && src && coef && g_coef, "tta_gather_rotate_src_bw: null pointer");
+  const int V = pick_v(C);
+  TTA_V_DISPATCH(V, {
+    hipLaunchKernelGGL((k_gather_rotate_bw<VV, false, 1>), dim3(wave_blocks(E)), dim3(256), 0,
+                       stream, g_out, nullptr, x, src, nullptr, coef, nullptr, g_in, g_coef,
+                       (int)E, (int)C);
+  });
+  TTA_CHECK_LAUNCH("tta_gather_rotate_src_bw");
   return tta::kOk;
 }
 

@@ -60,6 +60,8 @@ _SIGS = {
     "tta_segment_mean": [_P, _P, _P, _I64, _I64, _P],
     "tta_segment_mean_bwd": [_P, _P, _P, _P, _I64, _I64, _P],
     "tta_add_rows": [_P, _I64, _P, _I64, _I64, _I64, _P],
+    "tta_gather_rotate_src": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "tta_gather_rotate_src_bw": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_pack_b_elems": [_I64, _I64, _I],
     "tta_pack_b": [_P, _I64, _I64, _I64, _I, _P, _I64, _P],
     "tta_gemm_bf16x": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _P,
@@ -278,6 +280,24 @@ def gather_rotate(x, src, tgt, coef, rad, out):
           _ptr(coef, numel=E * 35, name="coef"), _ptr(rad, numel=E * 12 * C, name="rad"),
           _ptr(out, numel=E * 18 * C, name="out"), N, E, C, _stream())
     return out
+
+
+def gather_rotate_src(x, src, coef, out):
+    N, _, C = x.shape
+    E = src.numel()
+    _call("tta_gather_rotate_src", _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E),
+          _ptr(coef, numel=E * 35, name="coef"), _ptr(out, numel=E * 9 * C, name="out"), N, E, C,
+          _stream())
+    return out
+
+
+def gather_rotate_src_bw(g_out, x, src, coef, g_in, g_coef):
+    N, _, C = x.shape
+    E = src.numel()
+    _call("tta_gather_rotate_src_bw", _ptr(g_out, numel=E * 9 * C, name="g_out"),
+          _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E), _ptr(coef, numel=E * 35, name="coef"),
+          None if g_in is None else _ptr(g_in, numel=E * 9 * C, name="g_in"),
+          _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream())
 
 
 def gather_rotate_bw(g_xf, rad, x, src, tgt, coef, g_rad, g_mcat, g_coef):

@@ -319,3 +319,28 @@ def random_orb_weights(cfg, seed):
     w["energy_head.normalizer.bn.running_var"] = torch.tensor(2.25)
     w["energy_head.reference.linear.weight"] = -torch.rand(1, 119, generator=gen) * 10.0
     return w
+
+
+# ------------------------------------------------------------------------------ C2
+def c2_weights(seed=SEEDS["C2"] + WEIGHT_SEED_OFFSET, C=128, prefix="c2"):
+    """SO(2) convolution weights of the isolated edgewise workload, N(0, 1/sqrt(fan_in)), m = 0
+    bias 0, in the reference key layout: fc_m0 [3C, 3C], so2_m_conv.0.fc [4C, 2C],
+    so2_m_conv.1.fc [2C, C] (torch [out, in])."""
+    gen = torch.Generator().manual_seed(int(seed))
+    w = {}
+    for name, (n_out, n_in) in (("fc_m0", (3 * C, 3 * C)), ("so2_m_conv.0.fc", (4 * C, 2 * C)),
+                                ("so2_m_conv.1.fc", (2 * C, C))):
+        w[f"{prefix}.{name}.weight"] = torch.randn(n_out, n_in, generator=gen) / math.sqrt(n_in)
+    w[f"{prefix}.fc_m0.bias"] = torch.zeros(3 * C)
+    return w
+
+
+def c2_tensors(seed=SEEDS["C2"], N=8192, deg=25, C=128):
+    """(edge_index [2, E], edge vectors [E, 3], node features [N, 9, C] ~ N(0,1), upstream adjoint
+    of the scattered output [N, 9, C] ~ N(0,1)); the graph from ``c2_graph(seed)``, the features
+    from the generator seeded ``seed + 1``."""
+    ei, vec = c2_graph(seed, N, deg)
+    rng = _rng(seed + 1)
+    x = rng.standard_normal((N, 9, C)).astype(np.float32)
+    g = rng.standard_normal((N, 9, C)).astype(np.float32)
+    return ei, vec, x, g

@@ -13,13 +13,15 @@ blocks, energy head, the full reverse pass and the geometric VJP, all in HIP ker
 
 Also reported on the same JSON line:
   roofline      the dominant kernel (the split-bf16 MFMA GEMM that runs the edge-level
-                contractions at fp32 accuracy): algorithmic FLOPs (2MNK) of its launches in the
-                timed region / their HIP-event durations (recorded on the launch stream), against
+                contractions at fp32 accuracy): algorithmic FLOPs (2MNK) of its launches / their
+                HIP-event durations (recorded on the launch stream during a second pass of the
+                same K steps, so that the timed pass carries no instrumentation), against
                 the ceiling of its arithmetic (bf16 dense MFMA peak 2.5 PFLOP/s / 6 plane
                 products); ``traffic`` = HBM bytes per launch from rocprofv3 FETCH_SIZE +
                 WRITE_SIZE when profiles/gemm_bf16x6_traffic_c3.txt holds them, else null.  The
                 other GEMM kernel family (fp32 MFMA, node-level and short-K products) is listed
-                under ``gemm_families``.
+                under ``gemm_families``; ``hbm_kernels`` gives the same for the HBM-bound edge
+                kernels (rotation, segment sums) against the 8 TB/s HBM peak.
   cpu_baseline  the CPU oracle (PyTorch-CPU restatement of the reference path) on a bounded sample
                 of the same workload: the C3 model on a 512-atom cluster of the same density
                 (one step after a small warm-up), in atom-steps/s.
@@ -42,6 +44,7 @@ METRIC = "atom-steps/s (energy+forces), uma-s-1 arch 2,048 atoms; % HBM/MFMA roo
 # MI355X published dense peaks (TFLOP/s).  The split-bf16 GEMM computes an fp32-accurate product
 # with 6 bf16 plane products (mode 6): its fp32-equivalent ceiling is the bf16 peak / 6.
 PEAK_FP32_MFMA = 157.3
+PEAK_HBM_GBPS = 8000.0
 PEAK_BF16_MFMA = 2500.0
 PEAKS = {"f32": PEAK_FP32_MFMA, "bf16x6": PEAK_BF16_MFMA / 6, "bf16x3": PEAK_BF16_MFMA / 3,
          "bf16x1": PEAK_BF16_MFMA}
@@ -80,6 +83,68 @@ class GemmEvents:
             ms = sum(a.elapsed_time(b) for a, b in k["pairs"])
             out[kind] = dict(n=len(k["pairs"]), flops=k["flops"], nbytes=k["nbytes"], ms=ms)
         return out
+
+
+class HbmEvents:
+    """HIP events around every HBM-bound edge kernel launch (rotation / segment kernels)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.k = {}
+        self._cur = None
+
+    def before(self, kernel, nbytes):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        self._cur = (e, kernel)
+        d = self.k.setdefault(kernel, {"pairs": [], "nbytes": 0.0})
+        d["nbytes"] += nbytes
+
+    def after(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        start, kernel = self._cur
+        self.k[kernel]["pairs"].append((start, e))
+
+    def summary(self):
+        out = {}
+        for name, d in self.k.items():
+            ms = sum(a.elapsed_time(b) for a, b in d["pairs"])
+            n = len(d["pairs"])
+            gbs = d["nbytes"] / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+            out[name] = {"launches": n, "avg_launch_us": round(ms * 1e3 / max(1, n), 2),
+                         "algorithmic_bytes_per_launch": round(d["nbytes"] / max(1, n)),
+                         "achieved_GBps": round(gbs, 1), "peak_GBps": PEAK_HBM_GBPS,
+                         "frac": round(gbs / PEAK_HBM_GBPS, 4)}
+        return out
+
+
+def build_c2(torch, N=8192):
+    from tt_atom import synthetic
+    ei, vec, x, g = synthetic.c2_tensors(N=N)
+    return ei, vec, x, g, synthetic.c2_weights(), synthetic.jd_matrices()
+
+
+def cpu_baseline_c2(torch):
+    """Oracle on a bounded sample of C2: the same pipeline on N = 2048 nodes (E = 51,200)."""
+    from oracle import uma as U
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    ei, vec, x, g, w, jd = build_c2(torch, N=2048)
+
+    def run():
+        ev = torch.from_numpy(vec).requires_grad_(True)
+        out = U.isolated_edgewise(torch.from_numpy(x), ev, torch.from_numpy(ei[0]),
+                                  torch.from_numpy(ei[1]), w, "c2", jd, 2048)
+        torch.autograd.grad((out * torch.from_numpy(g)).sum(), ev)
+    run()
+    t0 = time.perf_counter()
+    run()
+    dt = time.perf_counter() - t0
+    E = int(ei.shape[1])
+    return {"value": round(E / dt, 1), "unit": "edge-steps/s", "cores": threads, "kind": "port",
+            "sample": (f"CPU oracle (torch-CPU fp32) of the C2 pipeline on N=2048 nodes "
+                       f"(E={E}), 1 step after a warm-up step, {dt:.2f} s; {threads} threads")}
 
 
 def build_c3(torch, n_atoms=2048, seed=None):
@@ -195,8 +260,12 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("c3", "c4", "c5"), default="c3",
-                    help="c3 (headline), c4 (periodic + stress) or c5 (Orb-v3 batch)")
+    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c3",
+                    help="c3 (headline), c2 (isolated edgewise kernel), c4 (periodic + stress) "
+                         "or c5 (Orb-v3 batch)")
+    ap.add_argument("--precision", choices=("f32", "f32-mfma", "bf16"), default="f32",
+                    help="GEMM arithmetic: f32 (split-bf16, fp32-accurate), f32-mfma, or bf16 "
+                         "operands (the bf16 variants of C2 / C5)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (y = -x) for the HBM counter scale")
     args = ap.parse_args()
@@ -218,7 +287,22 @@ def main():
     from tt_atom import _native
 
     wl = args.workload
-    if wl in ("c3", "c4"):
+    if wl == "c2":
+        from tt_atom.edgewise import EdgewiseStep
+        ei, vec, x, g, w, jd = build_c2(torch)
+        nl_ms = 0.0
+        st = EdgewiseStep(w, "c2", jd, ei[0], ei[1], 8192, precision=args.precision)
+        x_d = torch.from_numpy(x).cuda()
+        ev_d = torch.from_numpy(vec).cuda()[st.order].contiguous()
+        g_d = torch.from_numpy(g).cuda()
+
+        def step():
+            st.forward(x_d, ev_d)
+            st.backward(x_d, g_d)
+        n_atoms, n_edges = 8192, int(ei.shape[1])
+        energy_of = lambda: float(st.out.abs().sum())
+        forces_of = lambda: st.g_ev
+    elif wl in ("c3", "c4"):
         from tt_atom import geometry, model, trace
         if wl == "c3":
             cfg, w, host, pos, Z, ei, se, nl_ms = build_c3(torch)
@@ -226,7 +310,7 @@ def main():
         else:
             cfg, w, host, pos, Z, ei, shift, se, cell, nl_ms = build_c4(torch)
         dev = torch.device("cuda:0")
-        bb = model.Backbone(w, dev, cfg)
+        bb = model.Backbone(w, dev, cfg, precision=args.precision)
         geo = geometry.HostGeometry(w, cfg, host["to_m"], host["gauss_offset"],
                                     host["gauss_coeff"], device=dev)
         eng = trace.TracedEngine(bb, geo, Z, ei, se, edge_cell_shift=shift)
@@ -239,7 +323,7 @@ def main():
     else:
         from tt_atom import orb
         cfg, w, bg, nl_ms = build_c5(torch)
-        mdl = orb.OrbModel(w, cfg)
+        mdl = orb.OrbModel(w, cfg, precision=args.precision)
         graph = orb.OrbGraph(mdl.device, senders=bg.senders, receivers=bg.receivers,
                              num_nodes=bg.pos.shape[0], atomic_numbers=bg.Z,
                              cell_shift=bg.cell_shift, natoms=bg.natoms)
@@ -258,15 +342,25 @@ def main():
     print(f"[bench] {wl} warm-up done: N={n_atoms} E={n_edges} energy={energy_of():.6f}",
           file=sys.stderr, flush=True)
 
-    probe = GemmEvents(torch)
-    _native.set_gemm_probe(probe)
+    # timed region: K steps between two device synchronisations, no instrumentation
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    # the same K steps again with HIP events recorded around every GEMM and HBM-bound edge-kernel
+    # launch on the launch stream (kernel durations for the roofline; the extra host calls of
+    # the events would otherwise inflate the timed step)
+    probe = GemmEvents(torch)
+    hbm = HbmEvents(torch)
+    _native.set_gemm_probe(probe)
+    _native.set_hbm_probe(hbm)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
     _native.set_gemm_probe(None)
+    _native.set_hbm_probe(None)
     energy = energy_of()
     if not (energy == energy) or not bool(torch.isfinite(forces_of()).all()):
         raise RuntimeError("non-finite energy or forces")
@@ -275,13 +369,22 @@ def main():
     dom = max(fam, key=lambda k: fam[k]["ms"])
     d = fam[dom]
     achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12 if d["ms"] > 0 else 0.0
-    traffic = read_traffic() if (wl == "c3" and dom == "bf16x6") else None
+    traffic = read_traffic() if (wl == "c3" and dom == "bf16x6" and args.precision == "f32") \
+        else None
     ms_step = dt / args.steps * 1e3
     others = {k: {"launches": v["n"], "avg_launch_us": round(v["ms"] * 1e3 / max(1, v["n"]), 2),
                   "achieved_tflops": round(v["flops"] / max(1e-12, v["ms"] * 1e-3) / 1e12, 2),
                   "peak_tflops": round(PEAKS[k], 1), "share_of_step": round(v["ms"] / (dt * 1e3), 4)}
               for k, v in fam.items()}
-    if wl == "c5":
+    unit = "atom-steps/s"
+    if wl == "c2":
+        metric = "edge-steps/s (forward + edge-vector VJP), isolated edgewise kernel (C2)"
+        unit = "edge-steps/s"
+        workload = ("C2: isolated edgewise step, N=8192 nodes, E=204800 (in-degree 25, dst-sorted, "
+                    "src uniform), lmax=2, 128 channels: gather(src) -> rotate -> SO(2) conv -> "
+                    "rotate back -> scatter-add, plus the VJP w.r.t. edge vectors")
+        data = "synthetic (seeded C2 graph, N(0,1) features / adjoint, N(0,1/sqrt(fan_in)) weights)"
+    elif wl == "c5":
         metric = "atom-steps/s (energy+forces), Orb-v3-conservative arch, 256 molecules (C5)"
         workload = ("C5: Orb-v3-conservative arch (5 layers, latent 256, MLP hidden 1024, 8 "
                     "Bessel x SH l<=3), 256 H/C/N/O molecules of 20-60 atoms in 7 A cubes, "
@@ -298,8 +401,8 @@ def main():
                 f"{wl.upper()} system)")
     out = {
         "metric": metric,
-        "value": round(n_atoms * args.steps / dt, 2),
-        "unit": "atom-steps/s",
+        "value": round((n_edges if wl == "c2" else n_atoms) * args.steps / dt, 2),
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -307,9 +410,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16" if args.precision == "bf16" else "f32",
         "data": data,
-        "config": {"workload": workload, "atoms": n_atoms, "edges": n_edges,
+        "config": {"workload": workload, "precision": args.precision,
+                   "atoms" if wl != "c2" else "nodes": n_atoms, "edges": n_edges,
                    "neighbor_list_host_ms": round(nl_ms, 1), "energy": energy},
         "roofline": {"bound": "mfma", "kernel": KERNELS[dom],
                      "achieved": round(achieved, 3), "peak": round(PEAKS[dom], 2),
@@ -322,10 +426,14 @@ def main():
                                    "the kernel's arithmetic: fp32 MFMA 157.3, or the bf16 dense "
                                    "MFMA 2500 / number of plane products"),
                      "gemm_share_of_step": round(gemm_ms / (dt * 1e3), 4),
+                     "measured": ("HIP events around each launch, on the launch stream, over a "
+                                  "second pass of the same steps"),
                      "gemm_families": others},
+        "hbm_kernels": hbm.summary(),
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_c5(torch) if wl == "c5" else cpu_baseline(torch)
+        out["cpu_baseline"] = (cpu_baseline_c5(torch) if wl == "c5" else
+                               cpu_baseline_c2(torch) if wl == "c2" else cpu_baseline(torch))
     print(json.dumps(out), flush=True)
 
 

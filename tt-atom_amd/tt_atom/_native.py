@@ -273,51 +273,81 @@ def _ld(t, name):
 
 
 # ----------------------------------------------------------------------------- rotation
+# Optional measurement hook for the HBM-bound edge kernels: ``probe.before(kernel, nbytes)`` /
+# ``probe.after()`` around each launch, nbytes = algorithmic bytes (every operand read or written
+# once per use; gathered node rows count once per edge).
+_hbm_probe = None
+
+
+def set_hbm_probe(probe):
+    global _hbm_probe
+    _hbm_probe = probe
+
+
+def _hbm_call(kernel, nbytes, name, *args):
+    probe = _hbm_probe
+    if probe is not None:
+        probe.before(kernel, float(nbytes))
+    _call(name, *args)
+    if probe is not None:
+        probe.after()
+
+
 def gather_rotate(x, src, tgt, coef, rad, out):
     N, nsph, C = x.shape
     E = src.numel()
-    _call("tta_gather_rotate", _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E), _i32(tgt, E),
-          _ptr(coef, numel=E * 35, name="coef"), _ptr(rad, numel=E * 12 * C, name="rad"),
-          _ptr(out, numel=E * 18 * C, name="out"), N, E, C, _stream())
+    nbytes = E * (4 * (9 * C + 9 * C + 35 + (12 * C if rad is not None else 0) + 18 * C) + 8)
+    _hbm_call("k_gather_rotate", nbytes, "tta_gather_rotate", _ptr(x, numel=N * 9 * C, name="x"),
+              _i32(src, E), _i32(tgt, E),
+              _ptr(coef, numel=E * 35, name="coef"), _ptr(rad, numel=E * 12 * C, name="rad"),
+              _ptr(out, numel=E * 18 * C, name="out"), N, E, C, _stream())
     return out
 
 
 def gather_rotate_src(x, src, coef, out):
     N, _, C = x.shape
     E = src.numel()
-    _call("tta_gather_rotate_src", _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E),
-          _ptr(coef, numel=E * 35, name="coef"), _ptr(out, numel=E * 9 * C, name="out"), N, E, C,
-          _stream())
+    _hbm_call("k_gather_rotate_src", E * (4 * (9 * C + 35 + 9 * C) + 4), "tta_gather_rotate_src",
+              _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E),
+              _ptr(coef, numel=E * 35, name="coef"), _ptr(out, numel=E * 9 * C, name="out"), N, E, C,
+              _stream())
     return out
 
 
 def gather_rotate_src_bw(g_out, x, src, coef, g_in, g_coef):
     N, _, C = x.shape
     E = src.numel()
-    _call("tta_gather_rotate_src_bw", _ptr(g_out, numel=E * 9 * C, name="g_out"),
-          _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E), _ptr(coef, numel=E * 35, name="coef"),
-          None if g_in is None else _ptr(g_in, numel=E * 9 * C, name="g_in"),
-          _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream())
+    nbytes = E * (4 * (9 * C + 9 * C + 35 + 70 + (9 * C if g_in is not None else 0)) + 4)
+    _hbm_call("k_gather_rotate_src_bw", nbytes, "tta_gather_rotate_src_bw",
+              _ptr(g_out, numel=E * 9 * C, name="g_out"),
+              _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E), _ptr(coef, numel=E * 35, name="coef"),
+              None if g_in is None else _ptr(g_in, numel=E * 9 * C, name="g_in"),
+              _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream())
 
 
 def gather_rotate_bw(g_xf, rad, x, src, tgt, coef, g_rad, g_mcat, g_coef):
     N, _, C = x.shape
     E = src.numel()
-    _call("tta_gather_rotate_bw", _ptr(g_xf, numel=E * 18 * C, name="g_xf"),
-          _ptr(rad, numel=E * 12 * C, name="rad"), _ptr(x, numel=N * 9 * C, name="x"),
-          _i32(src, E), _i32(tgt, E), _ptr(coef, numel=E * 35, name="coef"),
-          _ptr(g_rad, numel=E * 12 * C, name="g_rad"), _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
-          _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream())
+    nbytes = E * (4 * (18 * C + (24 * C if rad is not None else 0) + 18 * C + 35 + 70 + 18 * C)
+                  + 8)
+    _hbm_call("k_gather_rotate_bw", nbytes, "tta_gather_rotate_bw",
+              _ptr(g_xf, numel=E * 18 * C, name="g_xf"),
+              _ptr(rad, numel=E * 12 * C, name="rad"), _ptr(x, numel=N * 9 * C, name="x"),
+              _i32(src, E), _i32(tgt, E), _ptr(coef, numel=E * 35, name="coef"),
+              _ptr(g_rad, numel=E * 12 * C, name="g_rad"), _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
+              _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream())
 
 
 def rotate_env_segsum(m, coef, env, tgt_ptr, res, out, *, n_in, env_first, div=1.0):
     N, _, C = out.shape
     E = coef.shape[0]
-    _call("tta_rotate_env_segsum", _ptr(m, numel=E * n_in * C, name="m"),
-          _ptr(coef, numel=E * 35, name="coef"), _ptr(env, numel=E, name="env"),
-          _i32(tgt_ptr, N + 1, "tgt_ptr"), _ptr(res, numel=N * 9 * C, name="res"),
-          _ptr(out, numel=N * 9 * C, name="out"), N, E, C, n_in, int(env_first), float(div),
-          _stream())
+    nbytes = 4 * (E * (n_in * C + 36) + (N + 1) + N * 9 * C * (1 + (res is not None)))
+    _hbm_call("k_rotate_env_segsum", nbytes, "tta_rotate_env_segsum",
+              _ptr(m, numel=E * n_in * C, name="m"),
+              _ptr(coef, numel=E * 35, name="coef"), _ptr(env, numel=E, name="env"),
+              _i32(tgt_ptr, N + 1, "tgt_ptr"), _ptr(res, numel=N * 9 * C, name="res"),
+              _ptr(out, numel=N * 9 * C, name="out"), N, E, C, n_in, int(env_first), float(div),
+              _stream())
     return out
 
 
@@ -325,20 +355,24 @@ def rotate_env_segsum_bw(g_node, tgt, m, coef, env, g_m, g_coef, g_env, *, n_in,
                          div=1.0):
     N, _, C = g_node.shape
     E = tgt.numel()
-    _call("tta_rotate_env_segsum_bw", _ptr(g_node, numel=N * 9 * C, name="g_node"), _i32(tgt, E),
-          _ptr(m, numel=E * n_in * C, name="m"), _ptr(coef, numel=E * 35, name="coef"),
-          _ptr(env, numel=E, name="env"), _ptr(g_m, numel=E * n_in * C, name="g_m"),
-          _ptr(g_coef, numel=E * 35, name="g_coef"), _ptr(g_env, numel=E, name="g_env"), N, E, C,
-          n_in, int(env_first), float(div), _stream())
+    nbytes = 4 * E * (9 * C + 1 + 2 * n_in * C + 35 + 1 + 70 + 2)
+    _hbm_call("k_rotate_env_segsum_bw", nbytes, "tta_rotate_env_segsum_bw",
+              _ptr(g_node, numel=N * 9 * C, name="g_node"), _i32(tgt, E),
+              _ptr(m, numel=E * n_in * C, name="m"), _ptr(coef, numel=E * 35, name="coef"),
+              _ptr(env, numel=E, name="env"), _ptr(g_m, numel=E * n_in * C, name="g_m"),
+              _ptr(g_coef, numel=E * 35, name="g_coef"), _ptr(g_env, numel=E, name="g_env"), N, E, C,
+              n_in, int(env_first), float(div), _stream())
 
 
 def node_gather_sum(g_mcat, src_ptr, src_perm, tgt_ptr, res, out):
     N, _, C = out.shape
     E = src_perm.numel()
-    _call("tta_node_gather_sum", _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
-          _i32(src_ptr, N + 1, "src_ptr"), _i32(src_perm, E, "src_perm"),
-          _i32(tgt_ptr, N + 1, "tgt_ptr"), _ptr(res, numel=N * 9 * C, name="res"),
-          _ptr(out, numel=N * 9 * C, name="out"), N, E, C, _stream())
+    nbytes = 4 * (E * 18 * C + 2 * (N + 1) + E + N * 9 * C * (1 + (res is not None)))
+    _hbm_call("k_node_gather_sum", nbytes, "tta_node_gather_sum",
+              _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
+              _i32(src_ptr, N + 1, "src_ptr"), _i32(src_perm, E, "src_perm"),
+              _i32(tgt_ptr, N + 1, "tgt_ptr"), _ptr(res, numel=N * 9 * C, name="res"),
+              _ptr(out, numel=N * 9 * C, name="out"), N, E, C, _stream())
     return out
 
 

@@ -16,19 +16,23 @@
 // 16x16x32 (which issues at half rate).  Operand layout: lane l supplies A[l%32][8*(l/32) + e] and
 // B[8*(l/32) + e][l%32], e = 0..7, of a 32 x 16 / 16 x 32 block.
 //
-// Packed B layout (tta_pack_b): bf16 [KT][planes][NT32][2][64 lanes][8] with KT = ceil(K/32),
-// NT32 = ceil(N/32): one 16(k) x 32(n) fragment is 1 KB, lane l holding
+// Packed B layout (tta_pack_b): bf16 [KT][planes][NT32][2][64 lanes][8] with KT = ceil(K/32) and
+// NT32 padded to whole 128-column tiles: one 16(k) x 32(n) fragment is 1 KB, lane l holding
 // B[kt*32 + ks*16 + 8*(l/32) + e][n32*32 + l%32] (zero beyond K, N).
 //
-// Block tile (64 WM) x 128 x 32: WM x 2 waves, each 64 x 64 (2 x 2 MFMA tiles of 32 x 32).  The
-// A slab is split while it is written to LDS (one bf16 plane array per plane, 16-byte chunks
-// XOR-swizzled over 16 rows so that neither the fragment reads nor the writes conflict); the B
-// slab is copied as packed.  Register prefetch of the next slab and double-buffered LDS give one
-// barrier per k-step.  WM = 4 (256 x 128, 512 threads) for the split modes, WM = 2 for bf16.
+// Block tile (64 WM) x 128 x 32: WM x 2 waves, each 64 x 64 (2 x 2 MFMA tiles of 32 x 32).  Both
+// slabs of a k-step reach LDS by direct copies (buffer/global_load ... lds: lane i of a wave
+// writes 16 bytes at the wave's LDS base + 16 i), with no register round trip: A as raw fp32 rows
+// (16-byte chunks XOR-swizzled so that the fragment reads are conflict-free), B as packed.  The
+// copies of slab kt+2 go into the stage slab kt leaves, right after the barrier that retires it,
+// so they have a whole k-step to land.  Each wave reads its A fragment as fp32 and splits it into
+// planes in registers, one 16-wide k half ahead of the MFMAs that consume it.  WM = 4 (256 x 128,
+// 512 threads, 112 KB LDS) for the split modes, WM = 2 (two blocks per CU) for bf16.
 #include "gemm_common.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef __attribute__((address_space(1))) void* gbl_ptr;
 
 namespace {
 
@@ -56,26 +60,8 @@ struct Split<6> {
   static constexpr int pb[6] = {1, 2, 0, 1, 0, 0};
 };
 
-template <int NPL, int L>
-__device__ __forceinline__ void split_planes(const float* v, __bf16 (&out)[NPL][L]) {
-#pragma unroll
-  for (int i = 0; i < L; ++i) {
-    float r = v[i];
-#pragma unroll
-    for (int q = 0; q < NPL; ++q) {
-      const __bf16 h = (__bf16)r;
-      out[q][i] = h;
-      if (q + 1 < NPL) r = r - (float)h;
-    }
-  }
-}
-
 constexpr int BN = 128, BK = 32;
 constexpr int NF = (BN / 32) * 2;  // B fragments per plane per k-step: n32 tiles x k16 halves
-
-// 16-byte chunk swizzle of a 64-byte bf16 row: conflict-free for any 16 consecutive rows read
-// at one logical chunk (and for 8-row groups).
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 2)) & 3; }
 
 __device__ __forceinline__ float epi_one(const GemmArgs& p, float v, int row, int col) {
   if (p.bias) v += p.bias[col];
@@ -127,6 +113,28 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
   }
 }
 
+// Split 8 fp32 values into NPL bf16 planes (round-to-nearest residuals), pairs at a time.
+template <int NPL>
+__device__ __forceinline__ void split8(const floatx4& x0, const floatx4& x1, bf16x8 (&out)[NPL]) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+  f2 r[4] = {f2{x0[0], x0[1]}, f2{x0[2], x0[3]}, f2{x1[0], x1[1]}, f2{x1[2], x1[3]}};
+#pragma unroll
+  for (int q = 0; q < NPL; ++q) {
+    h2 h[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[i] = __builtin_convertvector(r[i], h2);
+      if (q + 1 < NPL) r[i] = r[i] - __builtin_convertvector(h[i], f2);
+    }
+    out[q] = bf16x8{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+  }
+}
+
+// A (fp32) tile row: 8 chunks of 16 B per 32-wide k slab, chunk c of row r stored at c ^ aswz(r):
+// 16 consecutive rows at one logical chunk then cover all 64 banks.
+__device__ __forceinline__ int aswz(int row) { return (row >> 1) & 7; }
+
 template <int WM, int MODE>
 __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(GemmArgs p,
                                                                                int NT32,
@@ -134,14 +142,10 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   typedef Split<MODE> S;
   constexpr int NA = S::NA, NB = S::NB;
   constexpr int BM = 64 * WM, NTH = 128 * WM;
-  constexpr int BPT = NB * NF * 64 / NTH;  // B slab chunks per thread
-  static_assert(BPT * NTH == NB * NF * 64, "B slab must split evenly over the threads");
-  constexpr int A_SLAB = NA * BM * 4, B_SLAB = NB * NF * 64;  // in 16-byte chunks
-  // [A slab x 2 | B slab x 2]; plane q of an A slab: BM rows x 4 chunks of 16 B (32 bf16).
-  // After the k-loop the same memory stages the output tile for the epilogue.
-  __shared__ uint4 smem[2 * (A_SLAB + B_SLAB)];
-  auto As = [&](int b) { return smem + b * A_SLAB; };
-  auto Bs = [&](int b) { return smem + 2 * A_SLAB + b * B_SLAB; };
+  constexpr int A_CH = BM * 8, B_CH = NB * NF * 64, STG = A_CH + B_CH;  // 16-byte chunks
+  constexpr int APT = A_CH / NTH, BPT = B_CH / NTH;                      // copies per thread
+  static_assert(APT * NTH == A_CH && BPT * NTH == B_CH, "slabs must split evenly");
+  __shared__ uint4 smem[2 * STG];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -155,6 +159,40 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   const int m0 = (tile / tn) * BM;
   const int nt0 = n0 / 32;
   const uint4* Bp = static_cast<const uint4*>(p.B);
+  // A through a buffer resource based at the tile's first row: an out-of-range chunk (row >= M or
+  // k >= K) gets an offset past num_records and is copied as zeros.
+  const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.A + (int64_t)m0 * p.lda), (short)0, 0x7ffffffe, 0x00020000);
+  int arow[APT], acol[APT];
+#pragma unroll
+  for (int h = 0; h < APT; ++h) {
+    const int L = t + NTH * h;  // LDS chunk this lane fills
+    const int row = L >> 3;
+    arow[h] = row;
+    acol[h] = 4 * ((L & 7) ^ aswz(row));
+  }
+  const int rows_left = p.M - m0;
+
+  auto issue = [&](int kt, int stg) {
+    uint4* base = smem + stg * STG;
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int h = 0; h < APT; ++h) {
+      const int k = k0 + acol[h];
+      const int o = (arow[h] * (int)p.lda + k) * 4;
+      const int off = ((arow[h] < rows_left) & (k < p.K)) ? o : (int)0x7fffffff;
+      const int L = t + NTH * h;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_ptr)(base + (L - lane)), 16, off, 0, 0,
+                                               0);
+    }
+#pragma unroll
+    for (int h = 0; h < BPT; ++h) {
+      const int c = t + NTH * h;
+      const int pl = c / (NF * 64), f = (c / 64) % NF, l = c % 64;
+      const uint4* g = Bp + ((((int64_t)kt * NB + pl) * NT32 + nt0 + (f >> 1)) * 2 + (f & 1)) * 64 + l;
+      __builtin_amdgcn_global_load_lds((gbl_ptr)g, (lds_ptr)(base + A_CH + (c - l)), 16, 0, 0);
+    }
+  };
 
   floatx16 acc[2][2];
 #pragma unroll
@@ -164,90 +202,71 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  floatx4 ra[4];
-  uint4 rb[BPT];
-  auto load = [&](int kt) {
-    const int k0 = kt * BK;
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int c = t + NTH * h;
-      const int row = m0 + (c >> 3), k = k0 + ((c & 7) << 2);
-      ra[h] = (row < p.M && k < p.K)
-                  ? *reinterpret_cast<const floatx4*>(p.A + (int64_t)row * p.lda + k)
-                  : floatx4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int h = 0; h < BPT; ++h) {
-      const int c = t + NTH * h;  // slab chunk: plane, fragment (n32 * 2 + k16 half), lane
-      const int pl = c / (NF * 64), f = (c / 64) % NF, l = c % 64;
-      rb[h] = (nt0 + (f >> 1) < NT32)
-                  ? Bp[((((int64_t)kt * NB + pl) * NT32 + nt0 + (f >> 1)) * 2 + (f & 1)) * 64 + l]
-                  : uint4{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store = [&](int buf) {
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      const int c = t + NTH * h;
-      const int row = c >> 3, kq = c & 7;
-      const float v[4] = {ra[h][0], ra[h][1], ra[h][2], ra[h][3]};
-      __bf16 pl[NA][4];
-      split_planes<NA, 4>(v, pl);
-      const int ch = (kq >> 1) ^ swz(row);
-#pragma unroll
-      for (int q = 0; q < NA; ++q) {
-        const bf16x4 w = {pl[q][0], pl[q][1], pl[q][2], pl[q][3]};
-        *reinterpret_cast<bf16x4*>(reinterpret_cast<char*>(&As(buf)[(q * BM + row) * 4 + ch]) +
-                                   (kq & 1) * 8) = w;
-      }
-    }
-#pragma unroll
-    for (int h = 0; h < BPT; ++h) Bs(buf)[t + NTH * h] = rb[h];
-  };
-
-  const int nk = (p.K + BK - 1) / BK;
-  load(0);
-  store(0);
-  __syncthreads();
-
   const int l32 = lane & 31, lh = lane >> 5;
   const int rbase = wm * 64, cbase = wn * 64;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load(kt + 1);
+  // Fragment reads of one 16-wide k half: raw fp32 A (split later) and the packed B planes.
+  auto rd = [&](int stg, int ks, floatx4 (&x)[2][2], bf16x8 (&b)[2][NB]) {
+    const uint4* As = smem + stg * STG;
+    const uint4* Bs = As + A_CH;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 b[2][NB], a[2][NA];
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int q = 0; q < NB; ++q)
+        b[j][q] = __builtin_bit_cast(bf16x8, Bs[(q * NF + (wn * 2 + j) * 2 + ks) * 64 + lane]);
 #pragma unroll
-        for (int q = 0; q < NB; ++q)
-          b[j][q] = __builtin_bit_cast(bf16x8,
-                                       Bs(buf)[(q * NF + (wn * 2 + j) * 2 + ks) * 64 + lane]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int row = rbase + i * 32 + l32;
-        const int ch = (2 * ks + lh) ^ swz(row);
-#pragma unroll
-        for (int q = 0; q < NA; ++q)
-          a[i][q] = __builtin_bit_cast(bf16x8, As(buf)[(q * BM + row) * 4 + ch]);
-      }
-#pragma unroll
-      for (int q = 0; q < S::NP; ++q)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][S::pa[q]], b[j][S::pb[q]],
-                                                                acc[i][j], 0, 0, 0);
+    for (int i = 0; i < 2; ++i) {
+      const int row = rbase + i * 32 + l32;
+      const int c0 = 4 * ks + 2 * lh;
+      x[i][0] = __builtin_bit_cast(floatx4, As[row * 8 + (c0 ^ aswz(row))]);
+      x[i][1] = __builtin_bit_cast(floatx4, As[row * 8 + ((c0 + 1) ^ aswz(row))]);
     }
-    if (kt + 1 < nk) store(buf ^ 1);
-    __syncthreads();
+  };
+  auto sp = [&](const floatx4 (&x)[2][2], bf16x8 (&a)[2][NA]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) split8<NA>(x[i][0], x[i][1], a[i]);
+  };
+  auto mm = [&](const bf16x8 (&a)[2][NA], const bf16x8 (&b)[2][NB]) {
+#pragma unroll
+    for (int q = 0; q < S::NP; ++q)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][S::pa[q]], b[j][S::pb[q]],
+                                                              acc[i][j], 0, 0, 0);
+  };
+
+  // Software pipeline: the fragments of the next k half are read (and A split) while the MFMAs of
+  // the current one run.  One barrier per slab: each wave arrives with its copies of slab kt+1
+  // landed and its reads of slab kt returned, so after it slab kt+1 is visible to all and slab kt's
+  // stage takes the copies of slab kt+2.  Slab indices past the end are clamped (harmless
+  // re-copies, never read) so every step issues the same copies.
+  const int nk = (p.K + BK - 1) / BK;
+  if (nk > 0) {
+    issue(0, 0);
+    issue(min(1, nk - 1), 1);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(APT + BPT) : "memory");
+    floatx4 cx[2][2], nx[2][2];
+    bf16x8 ca[2][NA], cb[2][NB], na[2][NA], nb[2][NB];
+    rd(0, 0, cx, cb);
+    sp(cx, ca);
+    for (int kt = 0; kt < nk; ++kt) {
+      const int stg = kt & 1;
+      rd(stg, 1, nx, nb);
+      mm(ca, cb);
+      sp(nx, na);
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      issue(min(kt + 2, nk - 1), stg);
+      rd(stg ^ 1, 0, cx, cb);
+      mm(na, nb);
+      sp(cx, ca);
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
   // Epilogue: stage the accumulators through LDS in row passes, then each thread applies the
   // epilogue to whole float4 column groups and writes coalesced rows.
-  constexpr int LDT = BN + 8;  // row stride (floats): lanes 32..63 (rows +4) land 32 banks away
-  constexpr int SMEM_F = 2 * (A_SLAB + B_SLAB) * 4;
+  constexpr int LDT = BN + 8;
+  constexpr int SMEM_F = 2 * STG * 4;
   constexpr int RP = (BM * LDT <= SMEM_F) ? BM : (BM / 2 * LDT <= SMEM_F) ? BM / 2
                    : (BM / 4 * LDT <= SMEM_F) ? BM / 4 : 32;
   static_assert(RP % 32 == 0 && RP * LDT <= SMEM_F, "epilogue staging must fit the LDS buffer");
@@ -255,7 +274,7 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   for (int r0 = 0; r0 < BM; r0 += RP) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int rt = rbase + i * 32 - r0;  // row tile start inside this pass
+      const int rt = rbase + i * 32 - r0;
       if (rt < 0 || rt >= RP) continue;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -318,10 +337,14 @@ int planes_of(int mode) { return mode == 1 ? 1 : mode == 3 ? 2 : mode == 6 ? 3 :
 
 }  // namespace
 
+// n32 tiles of the packed B, padded with zero columns to whole 128-column block tiles so that
+// every fragment a block copies exists.
+static int64_t nt32_padded(int64_t N) { return ((N + BN - 1) / BN) * (BN / 32); }
+
 extern "C" int64_t tta_pack_b_elems(int64_t K, int64_t N, int mode) {
   const int pl = planes_of(mode);
   if (pl == 0 || K <= 0 || N <= 0) return -1;
-  return ((K + 31) / 32) * ((N + 31) / 32) * 1024 * pl;
+  return ((K + 31) / 32) * nt32_padded(N) * 1024 * pl;
 }
 
 extern "C" int tta_pack_b(const float* B, int64_t K, int64_t N, int64_t ldb, int mode,
@@ -333,7 +356,7 @@ extern "C" int tta_pack_b(const float* B, int64_t K, int64_t N, int64_t ldb, int
   TTA_CHECK_ARG(out_elems == tta_pack_b_elems(K, N, mode), "tta_pack_b: output has %lld bf16, "
                 "expected %lld", (long long)out_elems, (long long)tta_pack_b_elems(K, N, mode));
   TTA_CHECK_ARG(B && out && ((uintptr_t)out % 16 == 0), "tta_pack_b: null or misaligned pointer");
-  const int KT = (int)((K + 31) / 32), NT32 = (int)((N + 31) / 32);
+  const int KT = (int)((K + 31) / 32), NT32 = (int)nt32_padded(N);
   hipLaunchKernelGGL(k_pack_b, dim3(tta_blocks((int64_t)KT * NT32 * 128, 256)), dim3(256), 0,
                      stream, B, (int)K, (int)N, ldb, pl, KT, NT32, static_cast<uint4*>(out));
   TTA_CHECK_LAUNCH("tta_pack_b");
@@ -359,10 +382,12 @@ extern "C" int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const fl
   TTA_CHECK_ARG(K % 4 == 0 && lda % 4 == 0 && (uintptr_t)A % 16 == 0,
                 "tta_gemm_bf16x: A needs K, lda multiples of 4 and 16-byte alignment");
   TTA_CHECK_ARG(lda >= K && ldc >= N, "tta_gemm_bf16x: leading dimension too small");
+  TTA_CHECK_ARG(lda < ((int64_t)1 << 21), "tta_gemm_bf16x: lda must be below 2^21 (32-bit "
+                "offsets inside a 256-row tile)");
   TTA_CHECK_ARG((uintptr_t)Bp % 16 == 0, "tta_gemm_bf16x: packed B must be 16-byte aligned");
   GemmArgs p{A, Bp, C, bias, C2, aux, (int)M, (int)N, (int)K, lda, 0, ldc, 0, 0, 0, 0, epilogue,
              P, idx0, idx1, ldp, off1};
-  const int NT32 = (int)((N + 31) / 32);
+  const int NT32 = (int)nt32_padded(N);
   switch (mode) {
     case 1: return launch_bf16x<2, 1>(p, NT32, stream);
     case 3: return launch_bf16x<4, 3>(p, NT32, stream);

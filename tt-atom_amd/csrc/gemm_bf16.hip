@@ -26,8 +26,10 @@
 // (16-byte chunks XOR-swizzled so that the fragment reads are conflict-free), B as packed.  The
 // copies of slab kt+2 go into the stage slab kt leaves, right after the barrier that retires it,
 // so they have a whole k-step to land.  Each wave reads its A fragment as fp32 and splits it into
-// planes in registers, one 16-wide k half ahead of the MFMAs that consume it.  WM = 4 (256 x 128,
-// 512 threads, 112 KB LDS) for the split modes, WM = 2 (two blocks per CU) for bf16.
+// planes in registers, one 16-wide k half ahead of the MFMAs that consume it.  All modes run
+// WM = 2: 128 x 128 tiles, 256 threads, 80 KB LDS (mode 6), so two blocks share a CU and one's
+// epilogue, prologue and barriers overlap the other's MFMAs (measured faster than 256 x 128 tiles
+// with one block per CU on every edge- and node-level shape of the two models).
 #include "gemm_common.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -390,7 +392,7 @@ extern "C" int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const fl
   const int NT32 = (int)nt32_padded(N);
   switch (mode) {
     case 1: return launch_bf16x<2, 1>(p, NT32, stream);
-    case 3: return launch_bf16x<4, 3>(p, NT32, stream);
-    default: return launch_bf16x<4, 6>(p, NT32, stream);
+    case 3: return launch_bf16x<2, 3>(p, NT32, stream);
+    default: return launch_bf16x<2, 6>(p, NT32, stream);
   }
 }

@@ -381,9 +381,10 @@ def gate_fwd(x, gating, y, idx8, *, R, H, L, ldx=None, ldg=None):
     """x rows [9*H] at stride ldx, gating rows [L*H] at stride ldg, y contiguous [R, 9, H]."""
     ldx = 9 * H if ldx is None else ldx
     ldg = L * H if ldg is None else ldg
-    _call("tta_gate_fwd", _rows(x, R, ldx, 9 * H, "x"), _rows(gating, R, ldg, L * H, "gating"),
-          _ptr(y, numel=R * 9 * H, name="y"), R, H, L, ldx, ldg, _i32(idx8, 8, "idx8"),
-          _stream())
+    _hbm_call("k_gate_fwd", 4 * R * H * (18 + L), "tta_gate_fwd",
+              _rows(x, R, ldx, 9 * H, "x"), _rows(gating, R, ldg, L * H, "gating"),
+              _ptr(y, numel=R * 9 * H, name="y"), R, H, L, ldx, ldg, _i32(idx8, 8, "idx8"),
+              _stream())
     return y
 
 
@@ -391,26 +392,30 @@ def gate_bwd(g_y, x, gating, g_x, g_gating, idx8, *, R, H, L, ldx=None, ldg=None
     """g_x shares x's row stride, g_gating shares gating's."""
     ldx = 9 * H if ldx is None else ldx
     ldg = L * H if ldg is None else ldg
-    _call("tta_gate_bwd", _ptr(g_y, numel=R * 9 * H, name="g_y"), _rows(x, R, ldx, 9 * H, "x"),
-          _rows(gating, R, ldg, L * H, "gating"), _rows(g_x, R, ldx, 9 * H, "g_x"),
-          _rows(g_gating, R, ldg, L * H, "g_gating"), R, H, L, ldx, ldg,
-          _i32(idx8, 8, "idx8"), _stream())
+    _hbm_call("k_gate_bwd", 4 * R * H * (27 + 2 * L), "tta_gate_bwd",
+              _ptr(g_y, numel=R * 9 * H, name="g_y"), _rows(x, R, ldx, 9 * H, "x"),
+              _rows(gating, R, ldg, L * H, "gating"), _rows(g_x, R, ldx, 9 * H, "g_x"),
+              _rows(g_gating, R, ldg, L * H, "g_gating"), R, H, L, ldx, ldg,
+              _i32(idx8, 8, "idx8"), _stream())
 
 
 def ln_silu_fwd(a, gamma, beta, nrm, s, *, R, n, lda=None, lds=None, eps=1e-5):
     lda = n if lda is None else lda
     lds = n if lds is None else lds
-    _call("tta_ln_silu_fwd", _rows(a, R, lda, n, "a"), _ptr(gamma, numel=n), _ptr(beta, numel=n),
-          _rows(nrm, R, lda, n, "nrm"), _rows(s, R, lds, n, "s"), R, n, lda, lds, eps, _stream())
+    _hbm_call("k_ln_silu_fwd", 4 * (3 * R * n + 2 * n), "tta_ln_silu_fwd",
+              _rows(a, R, lda, n, "a"), _ptr(gamma, numel=n), _ptr(beta, numel=n),
+              _rows(nrm, R, lda, n, "nrm"), _rows(s, R, lds, n, "s"), R, n, lda, lds, eps,
+              _stream())
 
 
 def ln_silu_bwd(g, a, nrm, gamma, g_a, *, R, n, ldg=None, lda=None, ldo=None, eps=1e-5):
     ldg = n if ldg is None else ldg
     lda = n if lda is None else lda
     ldo = n if ldo is None else ldo
-    _call("tta_ln_silu_bwd", _rows(g, R, ldg, n, "g"), _rows(a, R, lda, n, "a"),
-          _rows(nrm, R, lda, n, "nrm"), _ptr(gamma, numel=n), _rows(g_a, R, ldo, n, "g_a"), R, n,
-          ldg, lda, ldo, eps, _stream())
+    _hbm_call("k_ln_silu_bwd", 4 * (4 * R * n + n), "tta_ln_silu_bwd",
+              _rows(g, R, ldg, n, "g"), _rows(a, R, lda, n, "a"), _rows(nrm, R, lda, n, "nrm"),
+              _ptr(gamma, numel=n), _rows(g_a, R, ldo, n, "g_a"), R, n, ldg, lda, ldo, eps,
+              _stream())
 
 
 def rmsnorm_sh_fwd(x, aw, ab, add0, y, inv, eps=1e-5):
@@ -524,50 +529,61 @@ def orb_edge_features_bwd(vec, g_feat, g_cut, r_max, nb, g_vec):
 def rms_residual(h, w, x_old, u, x_new, inv, attn_w=None, attn_b=None, sig=None, eps=1e-6):
     R, C = h.shape
     n = R * C
-    _call("tta_rms_residual", _ptr(h, numel=n, name="h"), _ptr(w, numel=C, name="w"),
-          None if x_old is None else _ptr(x_old, numel=n, name="x_old"),
-          None if u is None else _ptr(u, numel=n, name="u"),
-          None if x_new is None else _ptr(x_new, numel=n, name="x_new"),
-          None if inv is None else _ptr(inv, numel=R, name="inv"),
-          None if attn_w is None else _ptr(attn_w, numel=2 * C, name="attn_w"),
-          None if attn_b is None else _ptr(attn_b, numel=2, name="attn_b"),
-          None if sig is None else _ptr(sig, numel=2 * R, name="sig"), R, C, float(eps), _stream())
+    nbytes = 4 * (n * (1 + (x_old is not None) + (u is not None) + (x_new is not None)) + C
+                  + R * ((inv is not None) + 2 * (sig is not None)))
+    _hbm_call("k_rms_residual", nbytes, "tta_rms_residual", _ptr(h, numel=n, name="h"),
+              _ptr(w, numel=C, name="w"),
+              None if x_old is None else _ptr(x_old, numel=n, name="x_old"),
+              None if u is None else _ptr(u, numel=n, name="u"),
+              None if x_new is None else _ptr(x_new, numel=n, name="x_new"),
+              None if inv is None else _ptr(inv, numel=R, name="inv"),
+              None if attn_w is None else _ptr(attn_w, numel=2 * C, name="attn_w"),
+              None if attn_b is None else _ptr(attn_b, numel=2, name="attn_b"),
+              None if sig is None else _ptr(sig, numel=2 * R, name="sig"), R, C, float(eps),
+              _stream())
 
 
 def rms_bwd(g, h, w, inv, g_h):
     R, C = h.shape
-    _call("tta_rms_bwd", _ptr(g, numel=R * C, name="g"), _ptr(h, numel=R * C, name="h"),
-          _ptr(w, numel=C, name="w"), _ptr(inv, numel=R, name="inv"),
-          _ptr(g_h, numel=R * C, name="g_h"), R, C, _stream())
+    _hbm_call("k_rms_bwd", 4 * (3 * R * C + R + C), "tta_rms_bwd",
+              _ptr(g, numel=R * C, name="g"), _ptr(h, numel=R * C, name="h"),
+              _ptr(w, numel=C, name="w"), _ptr(inv, numel=R, name="inv"),
+              _ptr(g_h, numel=R * C, name="g_h"), R, C, _stream())
 
 
 def orb_segsum(ue, sig, cut, send_ptr, recv_ptr, recv_perm, nodes, node_in):
     N, C = nodes.shape
     E = ue.shape[0]
-    _call("tta_orb_segsum", _ptr(ue, numel=E * C, name="ue"), _ptr(sig, numel=2 * E, name="sig"),
-          _ptr(cut, numel=E, name="cut"), _i32(send_ptr, N + 1), _i32(recv_ptr, N + 1),
-          _i32(recv_perm, E), _ptr(nodes, numel=N * C, name="nodes"),
-          _ptr(node_in, numel=N * 3 * C, name="node_in"), N, E, C, _stream())
+    # each edge row feeds two sums (sender order, then receiver order through recv_perm)
+    nbytes = 4 * (2 * E * C + 5 * E + 2 * (N + 1) + 4 * N * C)
+    _hbm_call("k_segsum", nbytes, "tta_orb_segsum", _ptr(ue, numel=E * C, name="ue"),
+              _ptr(sig, numel=2 * E, name="sig"), _ptr(cut, numel=E, name="cut"),
+              _i32(send_ptr, N + 1), _i32(recv_ptr, N + 1), _i32(recv_perm, E),
+              _ptr(nodes, numel=N * C, name="nodes"),
+              _ptr(node_in, numel=N * 3 * C, name="node_in"), N, E, C, _stream())
 
 
 def orb_edge_bwd(g_e, g_node_in, ue, sig, cut, h2, inv, wn, attn_w, send, recv, g_h2, g_cut):
     E, C = ue.shape
     N = g_node_in.shape[0]
     n = E * C
-    _call("tta_orb_edge_bwd", _ptr(g_e, numel=n, name="g_e"),
-          _ptr(g_node_in, numel=N * 3 * C, name="g_node_in"), _ptr(ue, numel=n),
-          _ptr(sig, numel=2 * E), _ptr(cut, numel=E), _ptr(h2, numel=n), _ptr(inv, numel=E),
-          _ptr(wn, numel=C), _ptr(attn_w, numel=2 * C), _i32(send, E), _i32(recv, E),
-          _ptr(g_h2, numel=n, name="g_h2"), _ptr(g_cut, numel=E, name="g_cut"), N, E, C,
-          _stream())
+    # g_e read and rewritten, two gathered node-row slices per edge, ue, h2, g_h2
+    nbytes = 4 * (7 * n + 8 * E + 3 * C)
+    _hbm_call("k_edge_bwd", nbytes, "tta_orb_edge_bwd", _ptr(g_e, numel=n, name="g_e"),
+              _ptr(g_node_in, numel=N * 3 * C, name="g_node_in"), _ptr(ue, numel=n),
+              _ptr(sig, numel=2 * E), _ptr(cut, numel=E), _ptr(h2, numel=n),
+              _ptr(inv, numel=E), _ptr(wn, numel=C), _ptr(attn_w, numel=2 * C), _i32(send, E),
+              _i32(recv, E), _ptr(g_h2, numel=n, name="g_h2"),
+              _ptr(g_cut, numel=E, name="g_cut"), N, E, C, _stream())
 
 
 def orb_node_segsum2(x, send_ptr, recv_ptr, recv_perm, out):
     E, H = x.shape
     N = out.shape[0]
-    _call("tta_orb_node_segsum2", _ptr(x, numel=E * H, name="x"), _i32(send_ptr, N + 1),
-          _i32(recv_ptr, N + 1), _i32(recv_perm, E), _ptr(out, numel=N * 2 * H, name="out"),
-          N, E, H, _stream())
+    nbytes = 4 * (2 * E * H + E + 2 * (N + 1) + 2 * N * H)
+    _hbm_call("k_node_segsum2", nbytes, "tta_orb_node_segsum2", _ptr(x, numel=E * H, name="x"),
+              _i32(send_ptr, N + 1), _i32(recv_ptr, N + 1), _i32(recv_perm, E),
+              _ptr(out, numel=N * 2 * H, name="out"), N, E, H, _stream())
 
 
 def segment_mean(x, ptr, out):

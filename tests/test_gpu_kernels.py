@@ -353,7 +353,7 @@ def test_gate_fwd_bwd(nat, natural):
     assert torch.equal(gcomb[:, 2 * H:].reshape(R, 9, H), gxo) and torch.equal(gcomb[:, :2 * H], ggo)
 
 
-@pytest.mark.parametrize("n", [16, 128, 200])
+@pytest.mark.parametrize("n", [16, 128, 200, 512])
 def test_ln_silu_fwd_bwd(nat, n):
     R = 300
     g = torch.Generator().manual_seed(n)

@@ -208,6 +208,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 constexpr int kMaxQ = 4;  // row width up to 64 lanes x 4 x kMaxQ = 1024 floats
+constexpr int kU = 4;     // edge rows in flight per lane in the segment sums
 
 // y = h * rsqrt(mean(h^2) + eps) * w (RMSNorm, orb_model.py:92-112); u = y; x_new = x_old + y
 // (residual, orb_model.py:266); optionally the next layer's attention gates on x_new:
@@ -311,21 +312,58 @@ __global__ __launch_bounds__(256) void k_segsum(const float* __restrict__ ue,
   floatx4 sr[kMaxQ], ssn[kMaxQ];
 #pragma unroll
   for (int k = 0; k < kMaxQ; ++k) sr[k] = ssn[k] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int j = recv_ptr[n]; j < recv_ptr[n + 1]; ++j) {
-    const int e = recv_perm[j];
-    const float a = sig[2 * e + 0] * cut[e];
+  // Up to 64 edges of a segment at a time: lane i fetches edge i's index and weight (one load
+  // each for the wave), then the rows of kU edges at a time are all in flight before any is added;
+  // the additions keep the plain loop's edge order.
+  const int r0 = recv_ptr[n], r1 = recv_ptr[n + 1];
+  for (int j0 = r0; j0 < r1; j0 += 64) {
+    const int cnt = min(64, r1 - j0);
+    const int my_e = lane < cnt ? recv_perm[j0 + lane] : 0;
+    const float my_w = lane < cnt ? sig[2 * my_e + 0] * cut[my_e] : 0.f;
+    for (int u0 = 0; u0 < cnt; u0 += kU) {
+      floatx4 v[kU][kMaxQ];
 #pragma unroll
-    for (int k = 0; k < kMaxQ; ++k) {
-      const int q = lane + 64 * k;
-      if (q < nq) sr[k] += reinterpret_cast<const floatx4*>(ue + (int64_t)e * C)[q] * a;
+      for (int u = 0; u < kU; ++u) {
+        const int e = __shfl(my_e, u0 + u, 64);
+#pragma unroll
+        for (int k = 0; k < kMaxQ; ++k) {
+          const int q = lane + 64 * k;
+          v[u][k] = (u0 + u < cnt && q < nq)
+                        ? reinterpret_cast<const floatx4*>(ue + (int64_t)e * C)[q]
+                        : floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const float w = __shfl(my_w, u0 + u, 64);
+        if (u0 + u < cnt)
+#pragma unroll
+          for (int k = 0; k < kMaxQ; ++k) sr[k] += v[u][k] * w;
+      }
     }
   }
-  for (int e = send_ptr[n]; e < send_ptr[n + 1]; ++e) {
-    const float a = sig[2 * e + 1] * cut[e];
+  const int s0 = send_ptr[n], s1 = send_ptr[n + 1];
+  for (int j0 = s0; j0 < s1; j0 += 64) {
+    const int cnt = min(64, s1 - j0);
+    const float my_w = lane < cnt ? sig[2 * (j0 + lane) + 1] * cut[j0 + lane] : 0.f;
+    for (int u0 = 0; u0 < cnt; u0 += kU) {
+      floatx4 v[kU][kMaxQ];
 #pragma unroll
-    for (int k = 0; k < kMaxQ; ++k) {
-      const int q = lane + 64 * k;
-      if (q < nq) ssn[k] += reinterpret_cast<const floatx4*>(ue + (int64_t)e * C)[q] * a;
+      for (int u = 0; u < kU; ++u)
+#pragma unroll
+        for (int k = 0; k < kMaxQ; ++k) {
+          const int q = lane + 64 * k;
+          v[u][k] = (u0 + u < cnt && q < nq)
+                        ? reinterpret_cast<const floatx4*>(ue + (int64_t)(j0 + u0 + u) * C)[q]
+                        : floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const float w = __shfl(my_w, u0 + u, 64);
+        if (u0 + u < cnt)
+#pragma unroll
+          for (int k = 0; k < kMaxQ; ++k) ssn[k] += v[u][k] * w;
+      }
     }
   }
   floatx4* out = reinterpret_cast<floatx4*>(node_in + n * 3 * C);
@@ -413,13 +451,59 @@ __global__ __launch_bounds__(256) void k_node_segsum2(const float* __restrict__ 
   const int nq = H / 4;
   floatx4* o = reinterpret_cast<floatx4*>(out + n * 2 * H);
   const int s0 = send_ptr[n], s1 = send_ptr[n + 1], r0 = recv_ptr[n], r1 = recv_ptr[n + 1];
-  for (int q = lane; q < nq; q += 64) {
-    floatx4 a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
-    for (int e = s0; e < s1; ++e) a += reinterpret_cast<const floatx4*>(x + (int64_t)e * H)[q];
-    for (int j = r0; j < r1; ++j)
-      b += reinterpret_cast<const floatx4*>(x + (int64_t)recv_perm[j] * H)[q];
-    o[q] = a;
-    o[nq + q] = b;
+  // Column blocks of 64 lanes x kMaxQ float4; within a block, edges in groups of kU whose rows
+  // are all loaded before the (edge-ordered) additions.
+  for (int qb = 0; qb < nq; qb += 64 * kMaxQ) {
+    floatx4 a[kMaxQ], b[kMaxQ];
+#pragma unroll
+    for (int k = 0; k < kMaxQ; ++k) a[k] = b[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int e0 = s0; e0 < s1; e0 += kU) {
+      floatx4 v[kU][kMaxQ];
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+#pragma unroll
+        for (int k = 0; k < kMaxQ; ++k) {
+          const int q = qb + lane + 64 * k;
+          v[u][k] = (e0 + u < s1 && q < nq)
+                        ? reinterpret_cast<const floatx4*>(x + (int64_t)(e0 + u) * H)[q]
+                        : floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (e0 + u < s1)
+#pragma unroll
+          for (int k = 0; k < kMaxQ; ++k) a[k] += v[u][k];
+    }
+    for (int j0 = r0; j0 < r1; j0 += 64) {
+      const int cnt = min(64, r1 - j0);
+      const int my_e = lane < cnt ? recv_perm[j0 + lane] : 0;
+      for (int u0 = 0; u0 < cnt; u0 += kU) {
+        floatx4 v[kU][kMaxQ];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+          const int e = __shfl(my_e, u0 + u, 64);
+#pragma unroll
+          for (int k = 0; k < kMaxQ; ++k) {
+            const int q = qb + lane + 64 * k;
+            v[u][k] = (u0 + u < cnt && q < nq)
+                          ? reinterpret_cast<const floatx4*>(x + (int64_t)e * H)[q]
+                          : floatx4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+          if (u0 + u < cnt)
+#pragma unroll
+            for (int k = 0; k < kMaxQ; ++k) b[k] += v[u][k];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kMaxQ; ++k) {
+      const int q = qb + lane + 64 * k;
+      if (q >= nq) continue;
+      o[q] = a[k];
+      o[nq + q] = b[k];
+    }
   }
 }
 

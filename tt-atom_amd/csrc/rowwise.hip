@@ -62,9 +62,12 @@ __global__ __launch_bounds__(256) void k_gate_bwd(const float* __restrict__ g_y,
 }
 
 // ------------------------------------------------------------------ LayerNorm + SiLU (radial MLP)
-// One wave per row.  Forward (so2.py:101-115 / geometry.py:161-168):
+// One wave per row; the row stays in registers (element lane + 64 k in slot k, NPL = ceil(n / 64)
+// slots) so that each operand crosses HBM once.  The per-lane partial sums run over k in order, as
+// a strided loop would.  Forward (so2.py:101-115 / geometry.py:161-168):
 //   nrm = (a - mean) * rstd * gamma + beta,  s = silu(nrm)
 // a and nrm rows have stride lda, s rows stride lds.
+template <int NPL>
 __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a,
                                                      const float* __restrict__ gamma,
                                                      const float* __restrict__ beta,
@@ -75,20 +78,30 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
   const int lane = threadIdx.x & 63;
   if (row >= R) return;
   const float* ar = a + row * lda;
+  float v[NPL];
   float sum = 0.f;
-  for (int i = lane; i < n; i += 64) sum += ar[i];
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const int i = lane + 64 * k;
+    v[k] = i < n ? ar[i] : 0.f;
+    sum += v[k];
+  }
   const float mean = tta_group_sum(sum, 64) / n;
   float sq = 0.f;
-  for (int i = lane; i < n; i += 64) {
-    const float d = ar[i] - mean;
-    sq += d * d;
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const float d = v[k] - mean;
+    if (lane + 64 * k < n) sq += d * d;
   }
   const float var = tta_group_sum(sq, 64) / n;
   const float rstd = 1.0f / sqrtf(var + eps);
-  for (int i = lane; i < n; i += 64) {
-    const float v = (ar[i] - mean) * rstd * gamma[i] + beta[i];
-    nrm[row * lda + i] = v;
-    s[row * lds + i] = tta_silu(v);
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const int i = lane + 64 * k;
+    if (i >= n) continue;
+    const float y = (v[k] - mean) * rstd * gamma[i] + beta[i];
+    nrm[row * lda + i] = y;
+    s[row * lds + i] = tta_silu(y);
   }
 }
 
@@ -96,6 +109,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
 //   gy = g * silu'(nrm) * gamma;  xhat = (a - mean) * rstd;
 //   g_a = rstd * (gy - mean(gy) - xhat * mean(gy * xhat))
 // g rows stride ldg, a / nrm rows stride lda, g_a rows stride ldo.
+template <int NPL>
 __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g,
                                                      const float* __restrict__ a,
                                                      const float* __restrict__ nrm,
@@ -107,28 +121,38 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   const int lane = threadIdx.x & 63;
   if (row >= R) return;
   const float* ar = a + row * lda;
+  float av[NPL], gy[NPL];
   float sum = 0.f;
-  for (int i = lane; i < n; i += 64) sum += ar[i];
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const int i = lane + 64 * k;
+    const bool in = i < n;
+    av[k] = in ? ar[i] : 0.f;
+    gy[k] = in ? g[row * ldg + i] * tta_silu_grad(nrm[row * lda + i]) * gamma[i] : 0.f;
+    sum += av[k];
+  }
   const float mean = tta_group_sum(sum, 64) / n;
   float sq = 0.f;
-  for (int i = lane; i < n; i += 64) {
-    const float d = ar[i] - mean;
-    sq += d * d;
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const float d = av[k] - mean;
+    if (lane + 64 * k < n) sq += d * d;
   }
   const float rstd = 1.0f / sqrtf(tta_group_sum(sq, 64) / n + eps);
   float m1 = 0.f, m2 = 0.f;
-  for (int i = lane; i < n; i += 64) {
-    const float gy = g[row * ldg + i] * tta_silu_grad(nrm[row * lda + i]) * gamma[i];
-    const float xh = (ar[i] - mean) * rstd;
-    m1 += gy;
-    m2 += gy * xh;
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    m1 += gy[k];
+    m2 += gy[k] * ((av[k] - mean) * rstd);
   }
   m1 = tta_group_sum(m1, 64) / n;
   m2 = tta_group_sum(m2, 64) / n;
-  for (int i = lane; i < n; i += 64) {
-    const float gy = g[row * ldg + i] * tta_silu_grad(nrm[row * lda + i]) * gamma[i];
-    const float xh = (ar[i] - mean) * rstd;
-    g_a[row * ldo + i] = rstd * (gy - m1 - xh * m2);
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const int i = lane + 64 * k;
+    if (i >= n) continue;
+    const float xh = (av[k] - mean) * rstd;
+    g_a[row * ldo + i] = rstd * (gy[k] - m1 - xh * m2);
   }
 }
 
@@ -305,11 +329,23 @@ extern "C" int tta_gate_bwd(const float* g_y, const float* x, const float* gatin
 extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* beta, float* nrm,
                                float* s, int64_t R, int64_t n, int64_t lda, int64_t lds,
                                float eps, hipStream_t stream) {
-  TTA_CHECK_ARG(R >= 0 && n > 0 && lda >= n && lds >= n, "tta_ln_silu_fwd: bad sizes");
+  TTA_CHECK_ARG(R >= 0 && n > 0 && n <= 512 && lda >= n && lds >= n,
+                "tta_ln_silu_fwd: bad sizes (row width 1..512)");
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(a && gamma && beta && nrm && s, "tta_ln_silu_fwd: null pointer");
-  hipLaunchKernelGGL(k_ln_silu_fwd, dim3(tta_blocks(R * 64, 256)), dim3(256), 0, stream, a, gamma,
-                     beta, nrm, s, R, (int)n, lda, lds, eps);
+  const dim3 grid(tta_blocks(R * 64, 256));
+  if (n <= 64)
+    hipLaunchKernelGGL(k_ln_silu_fwd<1>, grid, dim3(256), 0, stream, a, gamma, beta, nrm, s, R,
+                       (int)n, lda, lds, eps);
+  else if (n <= 128)
+    hipLaunchKernelGGL(k_ln_silu_fwd<2>, grid, dim3(256), 0, stream, a, gamma, beta, nrm, s, R,
+                       (int)n, lda, lds, eps);
+  else if (n <= 256)
+    hipLaunchKernelGGL(k_ln_silu_fwd<4>, grid, dim3(256), 0, stream, a, gamma, beta, nrm, s, R,
+                       (int)n, lda, lds, eps);
+  else
+    hipLaunchKernelGGL(k_ln_silu_fwd<8>, grid, dim3(256), 0, stream, a, gamma, beta, nrm, s, R,
+                       (int)n, lda, lds, eps);
   TTA_CHECK_LAUNCH("tta_ln_silu_fwd");
   return tta::kOk;
 }
@@ -317,11 +353,23 @@ extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* 
 extern "C" int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm,
                                const float* gamma, float* g_a, int64_t R, int64_t n, int64_t ldg,
                                int64_t lda, int64_t ldo, float eps, hipStream_t stream) {
-  TTA_CHECK_ARG(R >= 0 && n > 0 && ldg >= n && lda >= n && ldo >= n, "tta_ln_silu_bwd: bad sizes");
+  TTA_CHECK_ARG(R >= 0 && n > 0 && n <= 512 && ldg >= n && lda >= n && ldo >= n,
+                "tta_ln_silu_bwd: bad sizes (row width 1..512)");
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(g && a && nrm && gamma && g_a, "tta_ln_silu_bwd: null pointer");
-  hipLaunchKernelGGL(k_ln_silu_bwd, dim3(tta_blocks(R * 64, 256)), dim3(256), 0, stream, g, a, nrm,
-                     gamma, g_a, R, (int)n, ldg, lda, ldo, eps);
+  const dim3 grid(tta_blocks(R * 64, 256));
+  if (n <= 64)
+    hipLaunchKernelGGL(k_ln_silu_bwd<1>, grid, dim3(256), 0, stream, g, a, nrm, gamma, g_a, R,
+                       (int)n, ldg, lda, ldo, eps);
+  else if (n <= 128)
+    hipLaunchKernelGGL(k_ln_silu_bwd<2>, grid, dim3(256), 0, stream, g, a, nrm, gamma, g_a, R,
+                       (int)n, ldg, lda, ldo, eps);
+  else if (n <= 256)
+    hipLaunchKernelGGL(k_ln_silu_bwd<4>, grid, dim3(256), 0, stream, g, a, nrm, gamma, g_a, R,
+                       (int)n, ldg, lda, ldo, eps);
+  else
+    hipLaunchKernelGGL(k_ln_silu_bwd<8>, grid, dim3(256), 0, stream, g, a, nrm, gamma, g_a, R,
+                       (int)n, ldg, lda, ldo, eps);
   TTA_CHECK_LAUNCH("tta_ln_silu_bwd");
   return tta::kOk;
 }

@@ -299,6 +299,7 @@ def main():
         def step():
             st.forward(x_d, ev_d)
             st.backward(x_d, g_d)
+        step_eager = step
         n_atoms, n_edges = 8192, int(ei.shape[1])
         energy_of = lambda: float(st.out.abs().sum())
         forces_of = lambda: st.g_ev
@@ -317,6 +318,7 @@ def main():
         pos_d = pos.to(dev)
         stress = wl == "c4"
         step = lambda: eng.run(pos_d, compute_stress=stress)
+        step_eager = lambda: eng.run(pos_d, compute_stress=stress, eager=True)
         n_atoms, n_edges = len(Z), int(ei.shape[1])
         energy_of = lambda: float(eng.energy_buf)
         forces_of = lambda: eng.forces
@@ -330,9 +332,8 @@ def main():
         eng = orb.OrbEngine(mdl, graph)
         pos_d = bg.pos.to(mdl.device)
 
-        def step():
-            eng._forward(pos_d)
-            eng._backward(False)
+        step = lambda: eng.step(pos_d)
+        step_eager = lambda: eng.step(pos_d, eager=True)
         n_atoms, n_edges = int(bg.pos.shape[0]), int(bg.senders.numel())
         energy_of = lambda: float(eng.raw.sum())
         forces_of = lambda: eng.forces
@@ -349,15 +350,16 @@ def main():
         step()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    # the same K steps again with HIP events recorded around every GEMM and HBM-bound edge-kernel
-    # launch on the launch stream (kernel durations for the roofline; the extra host calls of
-    # the events would otherwise inflate the timed step)
+    # the same K steps again, launched kernel by kernel (not through the step graph) with HIP
+    # events recorded around every GEMM and HBM-bound edge-kernel launch on the launch stream
+    # (kernel durations for the roofline; the extra host calls of the events would otherwise
+    # inflate the timed step)
     probe = GemmEvents(torch)
     hbm = HbmEvents(torch)
     _native.set_gemm_probe(probe)
     _native.set_hbm_probe(hbm)
     for _ in range(args.steps):
-        step()
+        step_eager()
     torch.cuda.synchronize()
     _native.set_gemm_probe(None)
     _native.set_hbm_probe(None)
@@ -413,6 +415,7 @@ def main():
         "dtype": "bf16" if args.precision == "bf16" else "f32",
         "data": data,
         "config": {"workload": workload, "precision": args.precision,
+                   "step_launch": "kernel sequence" if wl == "c2" else "HIP graph replay",
                    "atoms" if wl != "c2" else "nodes": n_atoms, "edges": n_edges,
                    "neighbor_list_host_ms": round(nl_ms, 1), "energy": energy},
         "roofline": {"bound": "mfma", "kernel": KERNELS[dom],

@@ -220,3 +220,33 @@ def test_orb_session_single_and_batch(nat, tmp_path):
     for k, r in enumerate(res):
         assert abs(batch["energy"][k] - r["energy"]) <= 1e-6 * max(1.0, abs(r["energy"]))
         assert np.abs(batch["forces"][k] - r["forces"]).max() <= 2e-5
+
+
+def test_orb_step_graph_replays_match_eager():
+    """OrbEngine: graph replays equal the eager kernel sequence bit for bit, across eager work in
+    between and after a change of positions."""
+    from tt_atom import orb, synthetic
+    cfg = dict(synthetic.CFG_ORB_TINY)
+    w = synthetic.random_orb_weights(cfg, 7)
+    systems = synthetic.c5_systems(K=4)
+    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    model = orb.OrbModel(w, cfg)
+    graph = orb.OrbGraph(model.device, senders=bg.senders, receivers=bg.receivers,
+                         num_nodes=bg.pos.shape[0], atomic_numbers=bg.Z, cell_shift=bg.cell_shift,
+                         natoms=bg.natoms)
+    eng = orb.OrbEngine(model, graph)
+    p0 = bg.pos.to(model.device)
+    eng.step(p0, eager=True)
+    raw0, F0 = eng.raw.clone(), eng.forces.clone()
+    for _ in range(3):
+        eng.step(p0)
+        torch.cuda.synchronize()
+        assert torch.equal(eng.raw, raw0) and torch.equal(eng.forces, F0)
+        torch.randn(1 << 20, device=model.device).mul_(3.0).sum().item()
+    p1 = p0 + 0.01 * torch.randn_like(p0)
+    eng.step(p1, eager=True)
+    raw1, F1 = eng.raw.clone(), eng.forces.clone()
+    eng.step(p1)
+    torch.cuda.synchronize()
+    assert torch.equal(eng.raw, raw1) and torch.equal(eng.forces, F1)
+    assert not torch.equal(raw1, raw0)

@@ -114,3 +114,47 @@ def test_c4_reduced_periodic_stress():
                              max_neighbors=cfg["max_neighbors"])
     _check(w, cfg, host, pos, Z, ei, _system_embedding(w, cfg, len(Z)), shift, cell=cell,
            label="C4-256")
+
+
+def _graph_engine():
+    """C4 weights on FCC Cu 3x3x3 (108 atoms, PBC): a small engine with both step variants."""
+    from tt_atom import synthetic
+    from tt_atom.geometry import radius_graph
+    cfg = dict(synthetic.CFG_UMA_S, task="omat")
+    w, host = synthetic.random_uma_bundle(cfg, synthetic.SEEDS["C4"] + 100)
+    pos, Z, cell = synthetic.c4_system(reps=3)
+    pos, Z, cell = torch.from_numpy(pos), torch.from_numpy(Z), torch.from_numpy(cell)
+    ei, shift = radius_graph(pos, cfg["cutoff"], cell, [True] * 3,
+                             max_neighbors=cfg["max_neighbors"])
+    eng = _engine(w, cfg, host, Z, ei, _system_embedding(w, cfg, len(Z)), shift)
+    return eng, pos.float(), Z, ei
+
+
+def test_step_graph_replays_match_eager():
+    """The captured step graph reproduces the eager kernel sequence bit for bit, on every replay,
+    with eager work and synchronisations between replays, and follows new positions."""
+    eng, pos, Z, ei = _graph_engine()
+    dev = eng.device
+    p0 = pos.to(dev)
+    eng.run(p0, eager=True)
+    E_ref, F_ref = eng.energy_buf.clone(), eng.forces.clone()
+    for _ in range(3):
+        eng.run(p0)                                     # graph (captured on the first call)
+        torch.cuda.synchronize()
+        assert torch.equal(eng.energy_buf, E_ref) and torch.equal(eng.forces, F_ref)
+        scratch = torch.randn(1 << 20, device=dev)      # unrelated eager work in between
+        scratch.mul_(2.0).sum().item()
+    p1 = p0 + 0.01 * torch.randn_like(p0)
+    eng.run(p1, eager=True)
+    E1, F1 = eng.energy_buf.clone(), eng.forces.clone()
+    eng.run(p1)
+    torch.cuda.synchronize()
+    assert torch.equal(eng.energy_buf, E1) and torch.equal(eng.forces, F1)
+    assert not torch.equal(E1, E_ref)
+    # stress variant: its own graph
+    eng.run(p1, compute_stress=True, eager=True)
+    V_ref = eng.virial_buf.clone()
+    for _ in range(2):
+        eng.run(p1, compute_stress=True)
+        torch.cuda.synchronize()
+        assert torch.equal(eng.virial_buf, V_ref) and torch.equal(eng.forces, F1)

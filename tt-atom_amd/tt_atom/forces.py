@@ -13,6 +13,7 @@ from .trace import TracedEngine
 
 def energy_and_forces(bb, geo, pos, atomic_numbers, edge_index, sys_node_embedding,
                       edge_cell_shift=None, compute_stress=False):
+    # one step per engine: launched eagerly (a graph pays off from the second step on)
     eng = TracedEngine(bb, geo, atomic_numbers, edge_index, sys_node_embedding,
-                       edge_cell_shift=edge_cell_shift)
+                       edge_cell_shift=edge_cell_shift, use_graph=False)
     return eng(pos, compute_stress=compute_stress)

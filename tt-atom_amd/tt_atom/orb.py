@@ -28,6 +28,7 @@ import numpy as np
 import torch
 
 from . import _native as nat
+from .graphs import StepGraphs
 from .geometry import radius_graph
 from .model import PRECISIONS, _gw
 from .weights import NpzBundle
@@ -283,14 +284,18 @@ class OrbModel:
 # ----------------------------------------------------------------------------- engine
 class OrbEngine:
     """One fixed-topology energy + forces step: buffers are allocated once per graph and every
-    call is the same kernel sequence (the shape a hipGraph capture would replay)."""
+    call is the same kernel sequence, captured as a HIP graph on the first call of each variant
+    (with / without stress) and replayed afterwards unless ``use_graph`` is False."""
 
-    def __init__(self, model, graph, cond_nodes=None):
+    def __init__(self, model, graph, cond_nodes=None, use_graph=True):
         self.m, self.g = model, graph
         dev = model.device
         N, E, K, C, H = graph.N, graph.E, graph.K, model.C, model.H
         nb16 = 16 * model.nb
         f = lambda *s: torch.empty(*s, device=dev, dtype=torch.float32)
+        self.use_graph = use_graph
+        self._graphs = StepGraphs(self._step)
+        self.pos = f(N, 3)
         self.x_node = _dev(model.node_emb[graph.Z.cpu()], dev)
         self.cond = None if cond_nodes is None else _dev(cond_nodes, dev)
         He = model.eh_w_t[0].shape[1]
@@ -415,12 +420,26 @@ class OrbEngine:
         if compute_stress:
             nat.virial(self.vec, self.g_vec, self.work, self.virial_buf)
 
-    def run(self, pos, compute_stress=False):
-        """pos [N, 3] fp32 device tensor (node order of the graph) -> (raw energies [K] fp64 host,
-        raw forces [N, 3] device view, raw virial [3, 3] device view or None); raw = normalised
-        space, as orb_forces.energy_and_forces returns."""
-        self._forward(pos)
+    def _step(self, compute_stress):
+        self._forward(self.pos)
         self._backward(compute_stress)
+
+    def step(self, pos, compute_stress=False, eager=False):
+        """Enqueue one step on the current stream; results stay in the device buffers (raw,
+        forces, virial_buf).  Without ``eager`` (and with ``use_graph``) it replays a HIP graph
+        captured on the first call of each variant."""
+        self.pos.copy_(torch.as_tensor(pos, dtype=torch.float32).reshape(-1, 3),
+                       non_blocking=True)
+        if self.use_graph and not eager:
+            self._graphs.run(bool(compute_stress))
+        else:
+            self._step(compute_stress)
+
+    def run(self, pos, compute_stress=False, eager=False):
+        """pos [N, 3] fp32 (node order of the graph) -> (raw energies [K] fp64 host, raw forces
+        [N, 3] device view, raw virial [3, 3] device view or None); raw = normalised space, as
+        orb_forces.energy_and_forces returns."""
+        self.step(pos, compute_stress, eager)
         raw = self.raw.view(-1).double().cpu()
         return raw, self.forces, (self.virial_buf.view(3, 3) if compute_stress else None)
 
@@ -431,7 +450,8 @@ def _prepare(model, pos, senders, receivers, atomic_numbers, cell_shift, natoms,
     N = int(torch.as_tensor(atomic_numbers).shape[0])
     graph = OrbGraph(dev, senders=senders, receivers=receivers, num_nodes=N,
                      atomic_numbers=atomic_numbers, cell_shift=cell_shift, natoms=natoms)
-    eng = OrbEngine(model, graph, cond_nodes)
+    # one step per engine: launched eagerly (a graph pays off from the second step on)
+    eng = OrbEngine(model, graph, cond_nodes, use_graph=False)
     p = torch.as_tensor(pos, dtype=torch.float32).to(dev).contiguous()
     return eng, p
 

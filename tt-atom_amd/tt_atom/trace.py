@@ -20,6 +20,7 @@ from __future__ import annotations
 import torch
 
 from . import _native as nat
+from .graphs import StepGraphs
 from .model import GraphContext, NSPH
 
 
@@ -31,10 +32,15 @@ class TracedEngine:
     """``engine = TracedEngine(bb, geo, Z, edge_index, sys_emb, edge_cell_shift=None)``;
     ``E, F = engine(pos)`` or ``E, F, virial = engine(pos, compute_stress=True)``.
 
-    ``pos`` may be a host or device tensor; returned forces live on the device of ``pos``."""
+    ``pos`` may be a host or device tensor; returned forces live on the device of ``pos``.
+    With ``use_graph`` (default) the step is a HIP graph captured on the first call of each
+    variant (with / without stress) and replayed afterwards, as the reference replays its trace."""
 
-    def __init__(self, bb, geo, atomic_numbers, edge_index, sys_emb, edge_cell_shift=None):
+    def __init__(self, bb, geo, atomic_numbers, edge_index, sys_emb, edge_cell_shift=None,
+                 use_graph=True):
         nat.load()
+        self.use_graph = use_graph
+        self._graphs = StepGraphs(self._step)
         self.bb, self.geo = bb, geo
         dev = bb.device
         self.device = dev
@@ -303,14 +309,21 @@ class TracedEngine:
         nat.node_forces(self.g_ev, g.src_ptr, g.src_perm, g.tgt_ptr, self.forces)
 
     # ------------------------------------------------------------------ step
-    def run(self, pos, compute_stress=False):
-        """Enqueue one step; results stay on the device (energy_buf, forces, virial_buf)."""
-        self.pos.copy_(torch.as_tensor(pos, dtype=torch.float32).reshape(self.N, 3),
-                       non_blocking=True)
+    def _step(self, compute_stress):
         self._forward()
         self._backward()
         if compute_stress:
             nat.virial(self.ev, self.g_ev, self.virial_work, self.virial_buf)
+
+    def run(self, pos, compute_stress=False, eager=False):
+        """Enqueue one step; results stay on the device (energy_buf, forces, virial_buf).
+        ``eager`` launches the kernels one by one instead of replaying the graph."""
+        self.pos.copy_(torch.as_tensor(pos, dtype=torch.float32).reshape(self.N, 3),
+                       non_blocking=True)
+        if self.use_graph and not eager:
+            self._graphs.run(bool(compute_stress))
+        else:
+            self._step(compute_stress)
 
     def __call__(self, pos, compute_stress=False):
         self.run(pos, compute_stress)

@@ -49,8 +49,8 @@ PEAK_BF16_MFMA = 2500.0
 PEAKS = {"f32": PEAK_FP32_MFMA, "bf16x6": PEAK_BF16_MFMA / 6, "bf16x3": PEAK_BF16_MFMA / 3,
          "bf16x1": PEAK_BF16_MFMA}
 KERNELS = {"f32": "gemm_f32_kernel (fp32 MFMA 16x16x4)",
-           "bf16x6": "gemm_bf16x_kernel<4,6> (split-bf16, 3x3 planes / 6 products, fp32-accurate)",
-           "bf16x3": "gemm_bf16x_kernel<4,3> (split-bf16, 2x2 planes / 3 products)",
+           "bf16x6": "gemm_bf16x_kernel<2,6> (split-bf16, 3x3 planes / 6 products, fp32-accurate)",
+           "bf16x3": "gemm_bf16x_kernel<2,3> (split-bf16, 2x2 planes / 3 products)",
            "bf16x1": "gemm_bf16x_kernel<2,1> (bf16 operands)"}
 TRAFFIC_FILE = ROOT / "profiles" / "gemm_bf16x6_traffic_c3.txt"
 
@@ -266,6 +266,9 @@ def main():
     ap.add_argument("--precision", choices=("f32", "f32-mfma", "bf16"), default="f32",
                     help="GEMM arithmetic: f32 (split-bf16, fp32-accurate), f32-mfma, or bf16 "
                          "operands (the bf16 variants of C2 / C5)")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the step kernel by kernel instead of replaying its HIP graph "
+                         "(for profilers)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (y = -x) for the HBM counter scale")
     args = ap.parse_args()
@@ -317,7 +320,7 @@ def main():
         eng = trace.TracedEngine(bb, geo, Z, ei, se, edge_cell_shift=shift)
         pos_d = pos.to(dev)
         stress = wl == "c4"
-        step = lambda: eng.run(pos_d, compute_stress=stress)
+        step = lambda: eng.run(pos_d, compute_stress=stress, eager=args.eager)
         step_eager = lambda: eng.run(pos_d, compute_stress=stress, eager=True)
         n_atoms, n_edges = len(Z), int(ei.shape[1])
         energy_of = lambda: float(eng.energy_buf)
@@ -332,7 +335,7 @@ def main():
         eng = orb.OrbEngine(mdl, graph)
         pos_d = bg.pos.to(mdl.device)
 
-        step = lambda: eng.step(pos_d)
+        step = lambda: eng.step(pos_d, eager=args.eager)
         step_eager = lambda: eng.step(pos_d, eager=True)
         n_atoms, n_edges = int(bg.pos.shape[0]), int(bg.senders.numel())
         energy_of = lambda: float(eng.raw.sum())
@@ -415,7 +418,8 @@ def main():
         "dtype": "bf16" if args.precision == "bf16" else "f32",
         "data": data,
         "config": {"workload": workload, "precision": args.precision,
-                   "step_launch": "kernel sequence" if wl == "c2" else "HIP graph replay",
+                   "step_launch": ("kernel sequence" if wl == "c2" or args.eager
+                                   else "HIP graph replay"),
                    "atoms" if wl != "c2" else "nodes": n_atoms, "edges": n_edges,
                    "neighbor_list_host_ms": round(nl_ms, 1), "energy": energy},
         "roofline": {"bound": "mfma", "kernel": KERNELS[dom],

@@ -236,6 +236,31 @@ int tta_segment_mean_bwd(const float* g, const int* batch, const int* ptr, float
 int tta_add_rows(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t R, int64_t C,
                  tta_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------
+ * Neighbour list.  Replaces the host brute force geometry.radius_graph (geometry.py:48-81) plus
+ * the per-receiver max-neighbour cap, on the device and edge for edge equal to it (same indices,
+ * order and image cells).  Rows: aperiodic -> sources i (columns j ascending, edge (i, j)),
+ * periodic -> receivers t (columns (j, cell) lexicographic, edge (j, t, cell)).  lo / hi
+ * (nullable) bound every row's candidates to its own system of a batch.  Aperiodic keep:
+ * 0 < s < mid2 with s the fp32 fma-chain norm^2 and mid2 the square of the midpoint below
+ * fp32(cutoff); periodic keep: min2 < d2 <= cut2 over the image shifts [n_cells, 3].
+ * thresholds: the k-th smallest cap key (d2, src, cell) of every receiver (err[0] = 1 when a
+ * receiver has over 1024 candidates); count: kept entries per row (thresholds null = no cap);
+ * write: edges at the caller's exclusive int64 row offsets (edge_cell for periodic graphs). */
+int tta_radius_graph_thresholds(const float* pos, int64_t N, const int* lo, const int* hi,
+                                const float* shifts, int64_t n_cells, int periodic, double mid2,
+                                float cut2, float min2, int k, float* thr_d2, int* thr_src,
+                                int* thr_cell, int* err, tta_stream_t stream);
+int tta_radius_graph_count(const float* pos, int64_t N, const int* lo, const int* hi,
+                           const float* shifts, int64_t n_cells, int periodic, double mid2,
+                           float cut2, float min2, const float* thr_d2, const int* thr_src,
+                           const int* thr_cell, int* counts, tta_stream_t stream);
+int tta_radius_graph_write(const float* pos, int64_t N, const int* lo, const int* hi,
+                           const float* shifts, int64_t n_cells, int periodic, double mid2,
+                           float cut2, float min2, const float* thr_d2, const int* thr_src,
+                           const int* thr_cell, const int64_t* offsets, int64_t* edge_src,
+                           int64_t* edge_tgt, int* edge_cell, tta_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

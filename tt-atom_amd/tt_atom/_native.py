@@ -19,6 +19,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _I = ctypes.c_int
 _F = ctypes.c_float
+_D = ctypes.c_double
 
 # name -> argtypes (all return int status unless listed in _RESTYPE)
 _SIGS = {
@@ -66,6 +67,11 @@ _SIGS = {
     "tta_pack_b": [_P, _I64, _I64, _I64, _I, _P, _I64, _P],
     "tta_gemm_bf16x": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _P,
                        _I64, _I64, _I, _P],
+    "tta_radius_graph_thresholds": [_P, _I64, _P, _P, _P, _I64, _I, _D, _F, _F, _I, _P, _P, _P,
+                                    _P, _P],
+    "tta_radius_graph_count": [_P, _I64, _P, _P, _P, _I64, _I, _D, _F, _F, _P, _P, _P, _P, _P],
+    "tta_radius_graph_write": [_P, _I64, _P, _P, _P, _I64, _I, _D, _F, _F, _P, _P, _P, _P, _P,
+                               _P, _P, _P],
 }
 _RESTYPE = {"tta_last_error": ctypes.c_char_p, "tta_pack_b_elems": ctypes.c_int64}
 
@@ -483,6 +489,45 @@ def virial(ev, g_ev, work, out):
     E = ev.shape[0]
     _call("tta_virial", _ptr(ev, numel=E * 3), _ptr(g_ev, numel=E * 3), E,
           _ptr(work, numel=256 * 9, name="work"), _ptr(out, numel=9), _stream())
+
+
+# ----------------------------------------------------------------------------- neighbour list
+def radius_graph_passes(pos, lo, hi, shifts, periodic, mid2, cut2, min2, k):
+    """The three device passes of the radius graph (thresholds with a cap, per-row counts,
+    ordered write); returns (src int64 [E], tgt int64 [E], cell int32 [E] or None)."""
+    N = pos.shape[0]
+    dev = pos.device
+    n_cells = shifts.shape[0] if periodic else 0
+    lo_p = None if lo is None else _i32(lo, N, "lo")
+    hi_p = None if hi is None else _i32(hi, N, "hi")
+    sh_p = _ptr(shifts, numel=3 * n_cells, name="shifts") if periodic else None
+    common = (_ptr(pos, numel=N * 3, name="pos"), N, lo_p, hi_p, sh_p, n_cells, int(periodic),
+              float(mid2), float(cut2), float(min2))
+    thr = (None, None, None)
+    if k:
+        td = torch.empty(N, device=dev, dtype=torch.float32)
+        ta = torch.empty(N, device=dev, dtype=torch.int32)
+        tc = torch.empty(N, device=dev, dtype=torch.int32)
+        err = torch.zeros(1, device=dev, dtype=torch.int32)
+        _call("tta_radius_graph_thresholds", *common, int(k), td.data_ptr(), ta.data_ptr(),
+              tc.data_ptr(), err.data_ptr(), _stream())
+        if int(err.item()):
+            raise RuntimeError("radius graph: a receiver has more than 1024 neighbours within "
+                               "the cutoff (the capped device neighbour list holds at most 1024)")
+        thr = (td.data_ptr(), ta.data_ptr(), tc.data_ptr())
+    counts = torch.empty(N, device=dev, dtype=torch.int32)
+    _call("tta_radius_graph_count", *common, *thr, counts.data_ptr(), _stream())
+    c64 = counts.to(torch.int64)
+    ends = torch.cumsum(c64, 0)
+    offsets = ends - c64
+    E = int(ends[-1]) if N else 0
+    src = torch.empty(E, device=dev, dtype=torch.int64)
+    tgt = torch.empty(E, device=dev, dtype=torch.int64)
+    cell = torch.empty(E, device=dev, dtype=torch.int32) if periodic else None
+    if E:
+        _call("tta_radius_graph_write", *common, *thr, offsets.data_ptr(), src.data_ptr(),
+              tgt.data_ptr(), None if cell is None else cell.data_ptr(), _stream())
+    return src, tgt, cell
 
 
 # ----------------------------------------------------------------------------- Orb-v3

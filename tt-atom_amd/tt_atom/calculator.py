@@ -37,7 +37,11 @@ def full_3x3_to_voigt_6(s):
 class Session:
     """One bundle on one GPU; evaluates systems given as arrays."""
 
-    def __init__(self, bundle, task_name=None, device=None, gamma=0.0, max_neighbors=None):
+    def __init__(self, bundle, task_name=None, device=None, gamma=0.0, max_neighbors=None,
+                 neighbor_list="device"):
+        if neighbor_list not in ("host", "device"):
+            raise ValueError("neighbor_list must be 'host' or 'device'")
+        self.neighbor_list = neighbor_list
         if isinstance(bundle, str):
             bundle = WeightBundle.load(bundle)
         self.bundle = bundle
@@ -87,9 +91,11 @@ class Session:
             pbc = np.repeat(pbc, 3)
         cell_t = torch.as_tensor(np.asarray(cell), dtype=torch.float32).reshape(3, 3) \
             if (cell is not None and pbc.any()) else None
-        ei, shift = geometry.radius_graph(pos, self.cfg["cutoff"], cell=cell_t,
-                                          pbc=pbc if cell_t is not None else None,
-                                          max_neighbors=self.max_neighbors)
+        nl = geometry.radius_graph_device if self.neighbor_list == "device" else \
+            geometry.radius_graph
+        ei, shift = nl(pos, self.cfg["cutoff"], cell=cell_t,
+                       pbc=pbc if cell_t is not None else None, max_neighbors=self.max_neighbors)
+        ei, shift = ei.cpu(), shift.cpu()
         if ei.shape[1] == 0:
             raise ValueError("no edges within cutoff -- system too sparse for this model")
         sys_emb = geometry.csd_embedding(self._w, torch.tensor([float(charge)]),

@@ -11,6 +11,8 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
+
 import torch
 import torch.nn.functional as F
 
@@ -76,6 +78,55 @@ def radius_graph(pos, cutoff, cell=None, pbc=None, max_neighbors=None):
     if max_neighbors is not None and ei.shape[1]:
         keep = _cap(pos, ei, shift, int(max_neighbors))
         ei, shift = ei[:, keep], shift[keep]
+    return ei, shift
+
+
+def _image_shifts(pos, cutoff, cell, pbc):
+    """Cartesian image shifts of the periodic branch (reference geometry.py:70-77)."""
+    cell = torch.as_tensor(cell, dtype=pos.dtype).reshape(3, 3)
+    pbc = torch.as_tensor(pbc, dtype=torch.bool).reshape(-1).expand(3)
+    recip = torch.linalg.inv(cell).transpose(0, 1)
+    reps = [int(math.ceil(float(cutoff * torch.linalg.norm(recip[k])))) if bool(pbc[k]) else 0
+            for k in range(3)]
+    cells = torch.cartesian_prod(*[torch.arange(-r, r + 1, dtype=pos.dtype) for r in reps])
+    return cells.reshape(-1, 3) @ cell
+
+
+def radius_graph_device(pos, cutoff, cell=None, pbc=None, max_neighbors=None, *,
+                        node_ranges=None, device=None):
+    """``radius_graph`` computed on the GPU: the same edges in the same order with the same
+    ``cell_shift`` values (device tensors).  ``node_ranges`` ([N] lo, [N] hi) restricts every
+    node's candidates to its own system in a batch of disjoint aperiodic systems (the
+    concatenation of the per-system graphs, node indices global)."""
+    dev = torch.device(device) if device is not None else (
+        pos.device if torch.is_tensor(pos) and pos.is_cuda else torch.device("cuda"))
+    pos_h = torch.as_tensor(pos, dtype=torch.float32).detach().cpu()
+    N = pos_h.shape[0]
+    periodic = cell is not None and pbc is not None and bool(torch.as_tensor(pbc).any())
+    if periodic and node_ranges is not None:
+        raise ValueError("node_ranges applies to aperiodic batches only")
+    mid2, cut2, min2 = 0.0, 0.0, 0.0
+    if periodic:
+        shifts = _image_shifts(pos_h, cutoff, cell, pbc)
+        cut2 = float(np.float32(cutoff * cutoff))      # the fp32 of the host's d2 <= cutoff^2
+        min2 = float(np.float32(1e-8))
+    else:
+        shifts = pos_h.new_zeros(1, 3)
+        # d < fp32(cutoff) with d = fp32 sqrt(s)  <=>  s < m^2, m the midpoint below fp32(cutoff)
+        c32 = np.float32(cutoff)
+        m = (float(np.nextafter(c32, np.float32(-np.inf))) + float(c32)) / 2.0
+        mid2 = m * m
+    lo = hi = None
+    if node_ranges is not None:
+        lo = torch.as_tensor(node_ranges[0]).to(dev, torch.int32).contiguous()
+        hi = torch.as_tensor(node_ranges[1]).to(dev, torch.int32).contiguous()
+    from . import _native as nat
+    k = int(max_neighbors) if max_neighbors is not None else 0
+    sh_d = shifts.to(dev).contiguous()
+    src, tgt, c = nat.radius_graph_passes(pos_h.to(dev).contiguous(), lo, hi, sh_d, periodic,
+                                          mid2, cut2, min2, k)
+    ei = torch.stack([src, tgt], 0)
+    shift = sh_d[c.long()] if periodic else torch.zeros(src.shape[0], 3, device=dev)
     return ei, shift
 
 

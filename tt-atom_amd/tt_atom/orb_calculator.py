@@ -94,7 +94,7 @@ class OrbSession:
     """One Orb-v3 conservative checkpoint on one GPU (orb_calculator.py:26-73)."""
 
     def __init__(self, weights, device=None, device_id=0, precision="f32", pair_repulsion=True,
-                 covalent_radii=None):
+                 covalent_radii=None, neighbor_list="device"):
         if isinstance(weights, str):
             weights = orb.OrbWeights.load(weights)
         self.cfg = dict(weights.config)
@@ -106,6 +106,7 @@ class OrbSession:
         self.task = self.task_name = self.cfg.get("task", "omat")
         self.pair_repulsion = pair_repulsion
         self._radii = covalent_radii
+        self.neighbor_list = neighbor_list
         self._engine, self._key = None, None
 
     def _radii_table(self):
@@ -148,7 +149,7 @@ class OrbSession:
             if (cell is not None and pbc_a.any()) else None
         system = dict(positions=positions, numbers=numbers, cell=cell_a,
                       pbc=pbc_a if cell_a is not None else None, charge=charge, spin=spin)
-        bg = orb.assemble_orb([system], self.r_max, self.max_num_neighbors)
+        bg = orb.assemble_orb([system], self.r_max, self.max_num_neighbors, self.neighbor_list)
         want_stress = cell_a is not None and ("stress" in properties or bool(pbc_a.all()))
         raw, F_raw, vir = self._run(bg, want_stress)
         n = bg.natoms[0]
@@ -173,7 +174,7 @@ class OrbSession:
         """Disjoint-union batch in one device step (orb_calculator.py:217-327):
         ``dict(energy=ndarray[K], forces=list[ndarray[N_k, 3]] or None)``."""
         want_forces = "forces" in properties
-        bg = orb.assemble_orb(systems, self.r_max, self.max_num_neighbors)
+        bg = orb.assemble_orb(systems, self.r_max, self.max_num_neighbors, self.neighbor_list)
         raw, F_raw, _ = self._run(bg, False)
         energies, forces, off = [], [], 0
         for k, n in enumerate(bg.natoms):

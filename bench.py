@@ -189,6 +189,22 @@ def build_c5(torch, K=256):
     return cfg, w, bg, nl_ms
 
 
+def device_nl_ms(torch, fn, ref):
+    """Median wall time of the device neighbour list (after one warm-up call), and whether it
+    reproduced the host graph ``ref`` = (edge_index, shift) exactly."""
+    out = fn()
+    same = torch.equal(out[0].cpu(), ref[0]) and torch.equal(out[1].cpu().float(),
+                                                               ref[1].float())
+    ts = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return round(sorted(ts)[2], 3), same
+
+
 def cpu_baseline_c5(torch):
     """Orb CPU oracle on a bounded sample of C5: the first 32 molecules of the batch."""
     from oracle import orb as O
@@ -294,6 +310,7 @@ def main():
         from tt_atom.edgewise import EdgewiseStep
         ei, vec, x, g, w, jd = build_c2(torch)
         nl_ms = 0.0
+        nl_dev = None
         st = EdgewiseStep(w, "c2", jd, ei[0], ei[1], 8192, precision=args.precision)
         x_d = torch.from_numpy(x).cuda()
         ev_d = torch.from_numpy(vec).cuda()[st.order].contiguous()
@@ -318,6 +335,10 @@ def main():
         geo = geometry.HostGeometry(w, cfg, host["to_m"], host["gauss_offset"],
                                     host["gauss_coeff"], device=dev)
         eng = trace.TracedEngine(bb, geo, Z, ei, se, edge_cell_shift=shift)
+        nl_dev = device_nl_ms(torch, lambda: geometry.radius_graph_device(
+            pos, cfg["cutoff"], cell, None if cell is None else [True] * 3,
+            max_neighbors=cfg["max_neighbors"]),
+            (ei, shift if shift is not None else torch.zeros(ei.shape[1], 3)))
         pos_d = pos.to(dev)
         stress = wl == "c4"
         step = lambda: eng.run(pos_d, compute_stress=stress, eager=args.eager)
@@ -333,6 +354,13 @@ def main():
                              num_nodes=bg.pos.shape[0], atomic_numbers=bg.Z,
                              cell_shift=bg.cell_shift, natoms=bg.natoms)
         eng = orb.OrbEngine(mdl, graph)
+        from tt_atom import synthetic as syn
+        systems = syn.c5_systems(K=256)
+        ref_bg = bg
+        nl_dev = device_nl_ms(torch, lambda: (lambda g: (torch.stack([g.receivers, g.senders]),
+                                                         g.cell_shift))(
+            orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"], "device")),
+            (torch.stack([ref_bg.receivers, ref_bg.senders]), ref_bg.cell_shift))
         pos_d = bg.pos.to(mdl.device)
 
         step = lambda: eng.step(pos_d, eager=args.eager)
@@ -421,7 +449,10 @@ def main():
                    "step_launch": ("kernel sequence" if wl == "c2" or args.eager
                                    else "HIP graph replay"),
                    "atoms" if wl != "c2" else "nodes": n_atoms, "edges": n_edges,
-                   "neighbor_list_host_ms": round(nl_ms, 1), "energy": energy},
+                   "neighbor_list_host_ms": round(nl_ms, 1),
+                   "neighbor_list_device_ms": None if nl_dev is None else nl_dev[0],
+                   "neighbor_list_device_equals_host": None if nl_dev is None else nl_dev[1],
+                   "energy": energy},
         "roofline": {"bound": "mfma", "kernel": KERNELS[dom],
                      "achieved": round(achieved, 3), "peak": round(PEAKS[dom], 2),
                      "unit": "TFLOP/s", "frac": round(achieved / PEAKS[dom], 4),

@@ -98,8 +98,9 @@ def _oracle(cfg, w, bg, dtype=torch.float64, **kw):
                                bg.cell_shift.to(dtype), bg.batch, bg.natoms, **kw)
 
 
-def _check(cfg, w, bg, raw, F, tol_e=1e-6, tol_f=1e-4):
-    ref_raw, ref_F = _oracle(cfg, w, bg)
+def _check(cfg, w, bg, raw, F, tol_e=1e-6, tol_f=1e-4, oracle_dtype=torch.float64):
+    ref_raw, ref_F = _oracle(cfg, w, bg, dtype=oracle_dtype)
+    ref_raw, ref_F = ref_raw.double(), ref_F.double()
     off = 0
     for k, n in enumerate(bg.natoms):
         e = float(orb.denormalize_energy(raw[k], bg.Z[off:off + n], n, w))
@@ -187,6 +188,19 @@ def test_orb_c5_architecture_reduced_batch(nat):
                                            receivers=bg.receivers, atomic_numbers=bg.Z,
                                            natoms=bg.natoms, cell_shift=bg.cell_shift)
     assert torch.equal(raw, raw2) and torch.equal(F, F2)
+
+
+def test_orb_c5_full_batch(nat):
+    """The full C5 workload (256 molecules, 10,150 atoms, E = 196,555) against the fp32 oracle."""
+    cfg = dict(S.CFG_ORB_C5)
+    w = S.random_orb_weights(cfg, S.SEEDS["C5"] + S.WEIGHT_SEED_OFFSET)
+    bg = orb.assemble_orb(S.c5_systems(), cfg["cutoff"], cfg["max_num_neighbors"])
+    model = orb.OrbModel(w, cfg)
+    raw, F = orb.energy_and_forces_batch(model, pos=bg.pos, senders=bg.senders,
+                                         receivers=bg.receivers, atomic_numbers=bg.Z,
+                                         natoms=bg.natoms, cell_shift=bg.cell_shift)
+    # the fp64 oracle of the whole batch would hold ~50 GB of saved activations
+    _check(cfg, w, bg, raw, F, oracle_dtype=torch.float32)
 
 
 def test_orb_session_single_and_batch(nat, tmp_path):

@@ -158,3 +158,29 @@ def test_step_graph_replays_match_eager():
         eng.run(p1, compute_stress=True)
         torch.cuda.synchronize()
         assert torch.equal(eng.virial_buf, V_ref) and torch.equal(eng.forces, F1)
+
+
+def test_c3_full_size():
+    """The headline C3 workload itself: 2048 atoms, uma-s-1 widths, cap 30 (E = 61,440)."""
+    from tt_atom import synthetic
+    from tt_atom.geometry import radius_graph
+    cfg = dict(synthetic.CFG_UMA_S)
+    w, host = synthetic.random_uma_bundle(cfg, synthetic.SEEDS["C3"] + 100)
+    pos, Z = synthetic.c3_system()
+    pos, Z = torch.from_numpy(pos), torch.from_numpy(Z)
+    ei, _ = radius_graph(pos, cfg["cutoff"], max_neighbors=cfg["max_neighbors"])
+    _check(w, cfg, host, pos, Z, ei, _system_embedding(w, cfg, len(Z)), label="C3-2048")
+
+
+def test_c4_full_size_stress():
+    """C4: FCC Cu 8x8x8 (2048 atoms, PBC), energy, forces and the full stress."""
+    from tt_atom import synthetic
+    from tt_atom.geometry import radius_graph
+    cfg = dict(synthetic.CFG_UMA_S, task="omat")
+    w, host = synthetic.random_uma_bundle(cfg, synthetic.SEEDS["C4"] + 100)
+    pos, Z, cell = synthetic.c4_system()
+    pos, Z, cell = torch.from_numpy(pos), torch.from_numpy(Z), torch.from_numpy(cell)
+    ei, shift = radius_graph(pos, cfg["cutoff"], cell, [True] * 3,
+                             max_neighbors=cfg["max_neighbors"])
+    _check(w, cfg, host, pos, Z, ei, _system_embedding(w, cfg, len(Z)), shift, cell=cell,
+           label="C4-2048")

@@ -58,3 +58,31 @@ def test_edgewise_step_full_size_vjp_is_linear(nat):
     assert torch.equal(o1, o2) and torch.equal(o1, o3)
     err = (v3 - (v1 + 2 * v2)).abs().max().item() / v3.abs().max().item()
     assert err < 1e-5, err
+
+
+def _ref32(ei, vec, x, g, w, N):
+    ev = torch.from_numpy(vec).float().requires_grad_(True)
+    out = U.isolated_edgewise(torch.from_numpy(x).float(), ev, torch.from_numpy(ei[0]),
+                              torch.from_numpy(ei[1]), {k: v.float() for k, v in w.items()}, "c2",
+                              S.jd_matrices(), N)
+    g_ev = torch.autograd.grad((out * torch.from_numpy(g).float()).sum(), ev)[0]
+    return out.detach(), g_ev
+
+
+def test_edgewise_full_size_matches_oracle(nat):
+    """The full C2 workload (N = 8192, E = 204,800, C = 128) against the fp64 oracle: output and
+    edge-vector VJP errors (relative to the largest magnitude) within twice those of the fp32
+    CPU oracle on the same inputs, or within the reduced test's bounds (2e-6 / 2e-4)."""
+    from tt_atom.edgewise import EdgewiseStep
+    ei, vec, x, g = S.c2_tensors()
+    w = S.c2_weights()
+    step = EdgewiseStep(w, "c2", S.jd_matrices(), ei[0], ei[1], 8192)
+    out, g_ev = step(x, vec, g)
+    r_out, r_gev = _ref(ei, vec, x, g, w, 8192)
+    f_out, f_gev = _ref32(ei, vec, x, g, w, 8192)
+    rel = lambda a, b: (a.cpu().double() - b).abs().max().item() / b.abs().max().item()
+    e_out, e_gev = rel(out, r_out), rel(g_ev, r_gev)
+    b_out, b_gev = rel(f_out, r_out), rel(f_gev, r_gev)
+    print(f"C2 full: GPU out {e_out:.2e}, g_ev {e_gev:.2e}; fp32 oracle out {b_out:.2e}, "
+          f"g_ev {b_gev:.2e}", flush=True)
+    assert e_out < max(2e-6, 2 * b_out) and e_gev < max(2e-4, 2 * b_gev), (e_out, e_gev)

@@ -117,6 +117,32 @@ class Session:
         return res
 
 
+    def evaluate_batch(self, systems, properties=("energy", "forces")):
+        """K systems in one device step (calculator.py:168-236): ``dict(energy=ndarray[K],
+        forces=list[ndarray[N_k, 3]] or None)`` with the per-system energy normaliser applied.
+        The step engine (and its HIP graph) is kept while the batch topology is unchanged."""
+        from . import disjoint
+        bg = disjoint.assemble(systems, self.cfg["cutoff"], self._w, self.C, task=self.task,
+                               max_neighbors=self.max_neighbors, neighbor_list=self.neighbor_list)
+        periodic = bool(bg.cell_shift.abs().sum() > 0)
+        eng = self._engine_for(bg.Z, bg.edge_index, bg.cell_shift if periodic else None,
+                               bg.sys_emb)
+        eng.run(bg.pos)
+        E_raw = eng.segment_energies(bg.natoms).cpu().double()
+        want_forces = "forces" in properties
+        F_all = eng.forces.detach().cpu().double() if want_forces else None
+        energies, forces, off = [], [], 0
+        for k, n in enumerate(bg.natoms):
+            Ek = self.scale_rmsd * float(E_raw[k]) + self.scale_mean
+            if self.elem_refs is not None:
+                Ek += float(self.elem_refs[bg.Z[off:off + n]].sum())
+            energies.append(Ek)
+            if want_forces:
+                forces.append((self.scale_rmsd * F_all[off:off + n]).numpy())
+            off += n
+        return dict(energy=np.array(energies), forces=forces if want_forces else None)
+
+
 class TTAtomCalculator(_AseCalculator):
     """ASE calculator (reference calculator.py:22-166)."""
 
@@ -145,3 +171,6 @@ class TTAtomCalculator(_AseCalculator):
                                     spin=float(atoms.info.get("spin", 0.0)),
                                     properties=properties)
         self.results.update(res)
+
+    def evaluate_batch(self, systems, properties=("energy", "forces")):
+        return self.session.evaluate_batch(systems, properties)

@@ -130,6 +130,42 @@ def radius_graph_device(pos, cutoff, cell=None, pbc=None, max_neighbors=None, *,
     return ei, shift
 
 
+def system_graphs(systems, cutoff, max_neighbors=None, neighbor_list="host"):
+    """Per-system neighbour lists of a disjoint batch: ``systems`` = [(pos [n,3], cell or None,
+    pbc or None)], result [(edge_index [2,E_k] int64, cell_shift [E_k,3])] on the host, each in
+    its system's own node numbering.  ``neighbor_list="device"`` builds all aperiodic systems in
+    one batched GPU pass and periodic ones one by one; the graphs are identical to the host's."""
+    if neighbor_list not in ("host", "device"):
+        raise ValueError("neighbor_list must be 'host' or 'device'")
+    out = [None] * len(systems)
+    periodic = [c is not None and p is not None and bool(np.asarray(p).any())
+                for (_, c, p) in systems]
+    if neighbor_list == "device":
+        ap = [k for k in range(len(systems)) if not periodic[k]]
+        if ap:
+            sizes = [int(systems[k][0].shape[0]) for k in ap]
+            starts = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+            lo = np.repeat(starts, sizes)
+            hi = np.repeat(starts + np.asarray(sizes, np.int64), sizes)
+            ei, _ = radius_graph_device(
+                torch.cat([torch.as_tensor(systems[k][0], dtype=torch.float32) for k in ap]),
+                cutoff, max_neighbors=max_neighbors,
+                node_ranges=(torch.from_numpy(lo), torch.from_numpy(hi)))
+            ei = ei.cpu()
+            bounds = np.searchsorted(ei[0].numpy(), np.concatenate([starts, [lo.size]]))
+            for q, k in enumerate(ap):
+                part = ei[:, bounds[q]:bounds[q + 1]] - int(starts[q])
+                out[k] = (part, torch.zeros(part.shape[1], 3))
+        for k, (pos, cell, pbc) in enumerate(systems):
+            if periodic[k]:
+                ei, sh = radius_graph_device(pos, cutoff, cell, pbc, max_neighbors)
+                out[k] = (ei.cpu(), sh.cpu())
+    for k, (pos, cell, pbc) in enumerate(systems):
+        if out[k] is None:
+            out[k] = radius_graph(pos, cutoff, cell, pbc if periodic[k] else None, max_neighbors)
+    return out
+
+
 def _cap(pos, ei, shift, k):
     src, tgt = ei[0], ei[1]
     ev = pos[src] - pos[tgt] + shift

@@ -29,7 +29,7 @@ import torch
 
 from . import _native as nat
 from .graphs import StepGraphs
-from .geometry import radius_graph
+from .geometry import system_graphs
 from .model import PRECISIONS, _gw
 from .weights import NpzBundle
 
@@ -110,42 +110,16 @@ def assemble_orb(systems, r_max, max_num_neighbors, neighbor_list="host"):
     batched pass, periodic ones one by one); the result is identical edge for edge."""
     if len(systems) == 0:
         raise ValueError("empty batch")
-    if neighbor_list not in ("host", "device"):
-        raise ValueError("neighbor_list must be 'host' or 'device'")
     fields = []
     for system in systems:
         pos, Z, cell, pbc, charge, spin = _fields(system)
         fields.append((torch.as_tensor(np.asarray(pos), dtype=torch.float32),
                        torch.as_tensor(np.asarray(Z), dtype=torch.int64), cell, pbc, charge, spin))
-    periodic = [c is not None and p is not None and bool(np.asarray(p).any())
-                for (_, _, c, p, _, _) in fields]
-    graphs = [None] * len(fields)
-    if neighbor_list == "device":
-        from .geometry import radius_graph_device
-        ap = [k for k in range(len(fields)) if not periodic[k]]
-        if ap:
-            sizes = [fields[k][0].shape[0] for k in ap]
-            starts = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
-            lo = np.repeat(starts, sizes)
-            hi = np.repeat(starts + np.asarray(sizes), sizes)
-            ei, _ = radius_graph_device(torch.cat([fields[k][0] for k in ap]), r_max,
-                                        max_neighbors=max_num_neighbors,
-                                        node_ranges=(torch.from_numpy(lo), torch.from_numpy(hi)))
-            ei = ei.cpu()
-            bounds = np.searchsorted(ei[0].numpy(), np.concatenate([starts, [lo.size]]))
-            for q, k in enumerate(ap):
-                part = ei[:, bounds[q]:bounds[q + 1]] - int(starts[q])
-                graphs[k] = (part, torch.zeros(part.shape[1], 3))
-        for k in range(len(fields)):
-            if periodic[k]:
-                pos, _, cell, pbc, _, _ = fields[k]
-                ei, sh = radius_graph_device(pos, r_max, cell, pbc, max_num_neighbors)
-                graphs[k] = (ei.cpu(), sh.cpu())
+    graphs = system_graphs([(f[0], f[2], f[3]) for f in fields], r_max, max_num_neighbors,
+                           neighbor_list)
     pos_all, Z_all, s_all, r_all, sh_all, b_all, natoms, q_all, s_spin = ([] for _ in range(9))
     off = 0
     for k, (pos, Z, cell, pbc, charge, spin) in enumerate(fields):
-        if graphs[k] is None:
-            graphs[k] = radius_graph(pos, r_max, cell, pbc, max_num_neighbors)
         ei, shift = graphs[k]
         if ei.shape[1] == 0:
             raise ValueError(f"system {k} has no edges within cutoff -- too sparse for this model")

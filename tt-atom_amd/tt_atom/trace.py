@@ -325,6 +325,19 @@ class TracedEngine:
         else:
             self._step(compute_stress)
 
+    def segment_energies(self, natoms):
+        """Raw energies of the systems of a disjoint batch (contiguous node ranges of sizes
+        ``natoms``), each the same device sum over its nodes as a single system's energy
+        (Backbone.energy_batch, model.py:241-247); call after ``run``."""
+        if sum(natoms) != self.N:
+            raise ValueError("natoms do not add up to the node count")
+        out = torch.empty(len(natoms), device=self.device, dtype=torch.float32)
+        off = 0
+        for k, n in enumerate(natoms):
+            nat.reduce_sum(self.node_e[off:off + n], n, 1, out[k:k + 1])
+            off += n
+        return out
+
     def __call__(self, pos, compute_stress=False):
         self.run(pos, compute_stress)
         E = float(self.energy_buf.item())

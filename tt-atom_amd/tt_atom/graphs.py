@@ -13,18 +13,22 @@ import torch
 
 
 class StepGraphs:
-    """``graphs = StepGraphs(fn)``; ``graphs.run(key)`` runs ``fn(key)`` through a graph captured
-    on the first call for that key (the first call also runs ``fn(key)`` once eagerly, so that
-    lazily initialised state exists before capture)."""
+    """``graphs = StepGraphs(fn)``; ``graphs.run(key)`` runs ``fn(key)``: eagerly on the first
+    call for that key, through a graph captured on the second, by replay afterwards.  An engine
+    used once (a topology that changes every step) thus never pays for a capture."""
 
     def __init__(self, fn):
         self._fn = fn
         self._graphs = {}
+        self._seen = set()
 
     def run(self, key):
         g = self._graphs.get(key)
         if g is None:
-            self._fn(key)
+            if key not in self._seen:
+                self._seen.add(key)
+                self._fn(key)
+                return
             torch.cuda.current_stream().synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
@@ -34,3 +38,4 @@ class StepGraphs:
 
     def reset(self):
         self._graphs.clear()
+        self._seen.clear()

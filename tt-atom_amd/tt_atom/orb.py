@@ -290,7 +290,7 @@ class OrbModel:
 # ----------------------------------------------------------------------------- engine
 class OrbEngine:
     """One fixed-topology energy + forces step: buffers are allocated once per graph and every
-    call is the same kernel sequence, captured as a HIP graph on the first call of each variant
+    call is the same kernel sequence, captured as a HIP graph on the second call of each variant
     (with / without stress) and replayed afterwards unless ``use_graph`` is False."""
 
     def __init__(self, model, graph, cond_nodes=None, use_graph=True):
@@ -433,7 +433,7 @@ class OrbEngine:
     def step(self, pos, compute_stress=False, eager=False):
         """Enqueue one step on the current stream; results stay in the device buffers (raw,
         forces, virial_buf).  Without ``eager`` (and with ``use_graph``) it replays a HIP graph
-        captured on the first call of each variant."""
+        captured on the second call of each variant (the first runs eagerly)."""
         self.pos.copy_(torch.as_tensor(pos, dtype=torch.float32).reshape(-1, 3),
                        non_blocking=True)
         if self.use_graph and not eager:

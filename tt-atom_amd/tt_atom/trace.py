@@ -33,7 +33,7 @@ class TracedEngine:
     ``E, F = engine(pos)`` or ``E, F, virial = engine(pos, compute_stress=True)``.
 
     ``pos`` may be a host or device tensor; returned forces live on the device of ``pos``.
-    With ``use_graph`` (default) the step is a HIP graph captured on the first call of each
+    With ``use_graph`` (default) the step is a HIP graph captured on the second call of each
     variant (with / without stress) and replayed afterwards, as the reference replays its trace."""
 
     def __init__(self, bb, geo, atomic_numbers, edge_index, sys_emb, edge_cell_shift=None,

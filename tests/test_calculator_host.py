@@ -100,3 +100,32 @@ def test_orb_zbl_forces_and_stress_are_derivatives_of_its_energy():
                                                 radii)[0])
     fd = (vals[0] - vals[1]) / (2 * h) / 2 / 64.0          # d/d eps_01 of a symmetric strain / V
     assert abs(fd - s[5]) < 1e-6 * max(1.0, abs(s[5]))
+
+
+def test_disjoint_assemble_block_diagonal():
+    """disjoint.assemble (disjoint.py:123-159): every edge stays inside its system, edges are the
+    per-system graphs offset by the node count, and sys_emb rows follow each system's charge /
+    spin."""
+    from tt_atom import disjoint
+    cfg = dict(synthetic.CFG_UMA_S, sphere_channels=8, hidden_channels=8, edge_channels=8,
+               num_distance_basis=8, num_layers=1)
+    w, _ = synthetic.random_uma_bundle(cfg, 5)
+    mols = [synthetic.c3_system(seed=50 + k, n=n, radius=4.0 + k) for k, n in enumerate((9, 14, 11))]
+    systems = [dict(positions=p, numbers=z, charge=float(k), spin=1.0)
+               for k, (p, z) in enumerate(mols)]
+    bg = disjoint.assemble(systems, 5.0, w, 8, task="omol")
+    assert bg.K == 3 and bg.natoms == [9, 14, 11]
+    off = 0
+    for k, (p, z) in enumerate(mols):
+        n = len(z)
+        ei, _ = geometry.radius_graph(torch.from_numpy(p).float(), 5.0)
+        m = (bg.edge_index[1] >= off) & (bg.edge_index[1] < off + n)
+        assert torch.equal(bg.edge_index[:, m], ei + off)
+        assert bool(((bg.edge_index[0, m] >= off) & (bg.edge_index[0, m] < off + n)).all())
+        se = geometry.csd_embedding(w, torch.tensor([float(k)]), torch.tensor([1.0]), 8,
+                                    dataset="omol")
+        assert torch.equal(bg.sys_emb[off:off + n], se.expand(n, -1))
+        assert bool((bg.batch[off:off + n] == k).all())
+        off += n
+    seg = bg.segment_matrix()
+    assert torch.equal(seg.sum(0), torch.ones(off)) and seg.sum(1).tolist() == [9.0, 14.0, 11.0]

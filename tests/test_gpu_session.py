@@ -57,3 +57,28 @@ def test_session_evaluate_batch_equals_per_system(session):
     again = sess.evaluate_batch(systems)
     assert np.array_equal(again["energy"], out["energy"])
     assert all(np.array_equal(a, b) for a, b in zip(again["forces"], out["forces"]))
+
+
+def test_session_batch_of_identical_copies(session):
+    """K copies of one molecule give K identical energies and force blocks (reference
+    test_batch.py::test_batched_identical_copies)."""
+    cfg, w, host, sess = session
+    pos, Z = _molecules()[1]
+    out = sess.evaluate_batch([dict(positions=pos, numbers=Z)] * 5)
+    assert np.all(out["energy"] == out["energy"][0])
+    assert all(np.array_equal(f, out["forces"][0]) for f in out["forces"])
+
+
+def test_session_new_engine_on_cell_change(session):
+    """Same atoms, same edge set, a strained cell: the image shifts change, so the kept engine
+    must not be reused (reference test_trace.py::test_traced_recaptures_on_cell_shift_change);
+    the result equals a fresh session's."""
+    cfg, w, host, sess = session
+    pos, Z, cell = synthetic.c4_system(seed=4, reps=2)
+    r1 = sess.evaluate(pos, Z, cell=cell, pbc=[True] * 3)
+    cell2 = cell * 1.01
+    r2 = sess.evaluate(pos, Z, cell=cell2, pbc=[True] * 3)
+    assert r1["energy"] != r2["energy"]
+    fresh = calculator.Session(sess.bundle).evaluate(pos, Z, cell=cell2, pbc=[True] * 3)
+    assert r2["energy"] == fresh["energy"] and np.array_equal(r2["forces"], fresh["forces"])
+    assert np.array_equal(r2["stress"], fresh["stress"])

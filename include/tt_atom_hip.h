@@ -48,7 +48,8 @@ int tta_gemm_f32(const float* A, const float* B, float* C, const float* bias, fl
  * operand is split on the fly into bf16 planes a = a0 + a1 + a2 (round-to-nearest residuals); the
  * constant B operand is packed once by tta_pack_b.  mode 6: planes 3 x 3, products
  * a0b0 + a0b1 + a1b0 + a0b2 + a2b0 + a1b1 -- fp32 GEMM accuracy; mode 3: 2 x 2 planes, 3 products
- * (~2^-16 relative); mode 1: bf16 operands.  A needs K, lda multiples of 4 and 16-byte alignment.
+ * (~2^-16 relative); mode 1: bf16 operands.  A needs K, lda multiples of 4, lda < 2^21 and
+ * 16-byte alignment.
  * Replaces the same ttnn.linear / ttnn.matmul call sites as tta_gemm_f32 (the reference runs
  * them in bf16 / bf8 with fp32 accumulation: compute_kernel_config, device.py). */
 int64_t tta_pack_b_elems(int64_t K, int64_t N, int mode);

@@ -129,3 +129,70 @@ def test_disjoint_assemble_block_diagonal():
         off += n
     seg = bg.segment_matrix()
     assert torch.equal(seg.sum(0), torch.ones(off)) and seg.sum(1).tolist() == [9.0, 14.0, 11.0]
+
+
+def _np_csr(keys, n):
+    ptr = np.zeros(n + 1, np.int64)
+    ptr[1:] = np.cumsum(np.bincount(keys, minlength=n))
+    return ptr
+
+
+def test_graph_context_topology_matches_numpy():
+    """Destination-sorted edge order, CSR offsets and the src permutation (built with torch on
+    the engine's device) equal numpy's stable sorts; malformed edge lists raise."""
+    import pytest
+    from tt_atom.model import GraphContext
+    rng = np.random.default_rng(4)
+    N, E = 37, 500
+    ei = rng.integers(0, N, size=(2, E))
+    ei[:, :60] = 5                                                # repeated keys: stability matters
+    Z = rng.integers(1, 9, size=N)
+    shift = rng.normal(size=(E, 3)).astype(np.float32)
+    g = GraphContext("cpu", edge_index=torch.from_numpy(ei), num_nodes=N,
+                     atomic_numbers=torch.from_numpy(Z), edge_cell_shift=torch.from_numpy(shift))
+    order = np.argsort(ei[1], kind="stable")
+    s, t = ei[0][order], ei[1][order]
+    assert np.array_equal(g.order.numpy(), order)
+    assert np.array_equal(g.src.numpy(), s) and np.array_equal(g.tgt.numpy(), t)
+    assert np.array_equal(g.tgt_ptr.numpy(), _np_csr(t, N))
+    assert np.array_equal(g.src_ptr.numpy(), _np_csr(s, N))
+    assert np.array_equal(g.src_perm.numpy(), np.argsort(s, kind="stable"))
+    assert np.array_equal(g.zsrc.numpy(), Z[s]) and np.array_equal(g.ztgt.numpy(), Z[t])
+    assert np.array_equal(g.shift.numpy(), shift[order])
+    assert g.max_in_degree == int(np.bincount(t, minlength=N).max())
+    assert g.src.dtype == torch.int32 and g.src_perm.dtype == torch.int32
+    for bad in (np.array([[0, N], [1, 2]]), np.array([[0, -1], [1, 2]])):
+        with pytest.raises(ValueError):
+            GraphContext("cpu", edge_index=torch.from_numpy(bad), num_nodes=N,
+                         atomic_numbers=torch.from_numpy(Z))
+
+
+def test_orb_graph_topology_matches_numpy():
+    import pytest
+    from tt_atom.orb import OrbGraph
+    rng = np.random.default_rng(5)
+    natoms = [7, 12, 5]
+    N = sum(natoms)
+    off = np.concatenate([[0], np.cumsum(natoms)])
+    snd, rcv = [], []
+    for k, n in enumerate(natoms):                                  # edges inside each system
+        snd.append(rng.integers(0, n, 40) + off[k])
+        rcv.append(rng.integers(0, n, 40) + off[k])
+    s, r = np.concatenate(snd), np.concatenate(rcv)
+    g = OrbGraph("cpu", senders=torch.from_numpy(s), receivers=torch.from_numpy(r), num_nodes=N,
+                 atomic_numbers=torch.ones(N, dtype=torch.long), natoms=natoms)
+    order = np.argsort(s, kind="stable")
+    s_s, r_s = s[order], r[order]
+    assert np.array_equal(g.order.numpy(), order)
+    assert np.array_equal(g.send.numpy(), s_s) and np.array_equal(g.recv.numpy(), r_s)
+    assert np.array_equal(g.send_ptr.numpy(), _np_csr(s_s, N))
+    assert np.array_equal(g.recv_ptr.numpy(), _np_csr(r_s, N))
+    assert np.array_equal(g.recv_perm.numpy(), np.argsort(r_s, kind="stable"))
+    assert np.array_equal(g.batch.numpy(), np.repeat(np.arange(3), natoms))
+    assert np.array_equal(g.seg_ptr.numpy(), off)
+    with pytest.raises(ValueError, match="joins two systems"):
+        OrbGraph("cpu", senders=torch.tensor([0]), receivers=torch.tensor([8]), num_nodes=N,
+                 atomic_numbers=torch.ones(N, dtype=torch.long), natoms=natoms)
+    with pytest.raises(ValueError, match="out of range"):
+        OrbGraph("cpu", senders=torch.tensor([0]), receivers=torch.tensor([N]), num_nodes=N,
+                 atomic_numbers=torch.ones(N, dtype=torch.long), natoms=natoms)

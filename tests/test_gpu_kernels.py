@@ -281,6 +281,42 @@ def test_gather_rotate_fwd_bwd(nat, C):
     assert (gn.cpu().double() - gx).abs().max() < 1e-3
 
 
+@pytest.mark.parametrize("C", [16, 128, 256, 1024])
+def test_node_gather_sum_order_and_hubs(nat, C):
+    """Every node's sum is bit-equal to a plain fp32 loop in edge order (src edges in the
+    src-sorted order, then tgt edges, then src + tgt + res): hubs with more than 64 src and tgt
+    edges, isolated nodes and degrees that are not multiples of the unroll."""
+    N = 24
+    g = torch.Generator().manual_seed(C)
+    src = torch.randint(0, N, (400,), generator=g)
+    src[:150] = 3                                                  # src hub
+    tgt = torch.randint(0, N, (400,), generator=g)
+    tgt[150:230] = 5                                               # tgt hub
+    tgt[(src == 7) | (tgt == 7)] = 8
+    src[src == 7] = 9                                              # node 7 has no edges
+    tgt = torch.sort(tgt).values
+    E = src.numel()
+    gm = torch.randn(E, 9, 2 * C, generator=g).float()
+    res = torch.randn(N, 9, C, generator=g).float()
+    perm = torch.argsort(src, stable=True)
+    sptr, tptr = _csr(src, N), _csr(tgt, N)
+    gmn = gm.numpy()
+    want = np.empty((N, 9, C), np.float32)
+    for n in range(N):
+        a = np.zeros((9, C), np.float32)
+        for k in range(int(sptr[n]), int(sptr[n + 1])):
+            a = a + gmn[int(perm[k]), :, :C]
+        b = np.zeros((9, C), np.float32)
+        for e in range(int(tptr[n]), int(tptr[n + 1])):
+            b = b + gmn[e, :, C:]
+        want[n] = (a + b) + res[n].numpy()
+    out = torch.empty(N, 9, C, device=DEV)
+    nat.node_gather_sum(gm.to(DEV), _i32(sptr), _i32(perm), _i32(tptr), res.to(DEV), out)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), want)
+    assert int(sptr[8] - sptr[7]) == 0 and int(tptr[8] - tptr[7]) == 0
+
+
 @pytest.mark.parametrize("n_in,env_first", [(9, True), (3, False)])
 def test_rotate_env_segsum_fwd_bwd(nat, n_in, env_first):
     N, E, C = 30, 250, 32

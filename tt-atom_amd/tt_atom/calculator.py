@@ -95,7 +95,6 @@ class Session:
             geometry.radius_graph
         ei, shift = nl(pos, self.cfg["cutoff"], cell=cell_t,
                        pbc=pbc if cell_t is not None else None, max_neighbors=self.max_neighbors)
-        ei, shift = ei.cpu(), shift.cpu()
         if ei.shape[1] == 0:
             raise ValueError("no edges within cutoff -- system too sparse for this model")
         sys_emb = geometry.csd_embedding(self._w, torch.tensor([float(charge)]),

@@ -228,34 +228,37 @@ class GraphContext:
     a deterministic segmented sum in the same per-node order as ``index_add_``."""
 
     def __init__(self, device, *, edge_index, num_nodes, atomic_numbers, edge_cell_shift=None):
-        ei = torch.as_tensor(edge_index).to("cpu", torch.int64)
+        # The sort and the CSR offsets are built where the engine runs (an edge list from the
+        # device neighbour search never leaves the device); two host synchronisations remain,
+        # for the range check and the maximum in-degree.
+        dev = torch.device(device)
+        ei = torch.as_tensor(edge_index)
         if ei.dim() != 2 or ei.shape[0] != 2:
             raise ValueError("edge_index must be [2, E]")
+        ei = ei.to(dev, torch.int64)
         N = int(num_nodes)
         E = int(ei.shape[1])
-        if E and (int(ei.min()) < 0 or int(ei.max()) >= N):
-            raise ValueError("edge_index out of range")
         if N >= 2 ** 31 or E >= 2 ** 31:
             raise ValueError("graph too large for int32 indices")
+        if E and (N == 0 or not bool(((ei >= 0) & (ei < N)).all())):
+            raise ValueError("edge_index out of range")
         self.N, self.E = N, E
-        src_np, tgt_np = ei[0].numpy(), ei[1].numpy()
-        order = np.argsort(tgt_np, kind="stable")                # reference order -> dst-sorted
-        self.order = torch.from_numpy(order)
-        src_s, tgt_s = src_np[order], tgt_np[order]
-        tgt_ptr = np.zeros(N + 1, np.int64)
-        tgt_ptr[1:] = np.cumsum(np.bincount(tgt_s, minlength=N))
-        src_perm = np.argsort(src_s, kind="stable")              # dst-order edge ids by src
-        src_ptr = np.zeros(N + 1, np.int64)
-        src_ptr[1:] = np.cumsum(np.bincount(src_s, minlength=N))
-        dev = torch.device(device)
-        i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(dev)
+        order = torch.argsort(ei[1], stable=True)                 # reference order -> dst-sorted
+        self.order = order
+        src_s, tgt_s = ei[0][order], ei[1][order]
+        t_cnt = torch.bincount(tgt_s, minlength=N)
+        tgt_ptr = torch.zeros(N + 1, dtype=torch.int64, device=dev)
+        tgt_ptr[1:] = torch.cumsum(t_cnt, 0)
+        src_perm = torch.argsort(src_s, stable=True)              # dst-order edge ids by src
+        src_ptr = torch.zeros(N + 1, dtype=torch.int64, device=dev)
+        src_ptr[1:] = torch.cumsum(torch.bincount(src_s, minlength=N), 0)
+        i32 = lambda a: a.to(torch.int32).contiguous()
         self.src, self.tgt = i32(src_s), i32(tgt_s)
         self.tgt_ptr, self.src_ptr, self.src_perm = i32(tgt_ptr), i32(src_ptr), i32(src_perm)
-        Z = torch.as_tensor(atomic_numbers).to("cpu", torch.int64).numpy()
-        self.Z = torch.from_numpy(Z.astype(np.int64)).to(dev)
-        self.zsrc, self.ztgt = i32(Z[src_s]), i32(Z[tgt_s])
+        self.Z = torch.as_tensor(atomic_numbers).to(dev, torch.int64)
+        self.zsrc, self.ztgt = i32(self.Z[src_s]), i32(self.Z[tgt_s])
         self.shift = None
         if edge_cell_shift is not None:
-            sh = torch.as_tensor(edge_cell_shift, dtype=torch.float32).cpu()[self.order]
-            self.shift = sh.contiguous().to(dev)
-        self.max_in_degree = int(np.diff(tgt_ptr).max()) if N else 0
+            sh = torch.as_tensor(edge_cell_shift, dtype=torch.float32).to(dev)[order]
+            self.shift = sh.contiguous()
+        self.max_in_degree = int(t_cnt.max()) if N else 0

@@ -146,43 +146,47 @@ class OrbGraph:
 
     def __init__(self, device, *, senders, receivers, num_nodes, atomic_numbers,
                  cell_shift=None, natoms=None):
-        s = torch.as_tensor(senders).to("cpu", torch.int64).numpy()
-        r = torch.as_tensor(receivers).to("cpu", torch.int64).numpy()
+        # Sorted on the device the engine runs on (see GraphContext); one host synchronisation
+        # for the checks.
+        dev = torch.device(device)
+        s = torch.as_tensor(senders).to(dev, torch.int64).reshape(-1)
+        r = torch.as_tensor(receivers).to(dev, torch.int64).reshape(-1)
         N, E = int(num_nodes), int(s.shape[0])
         if r.shape[0] != E:
             raise ValueError("senders / receivers length mismatch")
-        if E and (min(s.min(), r.min()) < 0 or max(s.max(), r.max()) >= N):
-            raise ValueError("edge index out of range")
         if N >= 2 ** 31 or E >= 2 ** 31:
             raise ValueError("graph too large for int32 indices")
         natoms = [N] if natoms is None else [int(n) for n in natoms]
         if sum(natoms) != N:
             raise ValueError("natoms do not add up to the node count")
         self.N, self.E, self.K = N, E, len(natoms)
-        order = np.argsort(s, kind="stable")
-        self.order = torch.from_numpy(order)
+        if E and (N == 0 or not bool(((s >= 0) & (s < N) & (r >= 0) & (r < N)).all())):
+            raise ValueError("edge index out of range")
+        order = torch.argsort(s, stable=True)
+        self.order = order
         s_s, r_s = s[order], r[order]
-        send_ptr = np.zeros(N + 1, np.int64)
-        send_ptr[1:] = np.cumsum(np.bincount(s_s, minlength=N))
-        recv_perm = np.argsort(r_s, kind="stable")
-        recv_ptr = np.zeros(N + 1, np.int64)
-        recv_ptr[1:] = np.cumsum(np.bincount(r_s, minlength=N))
+        send_ptr = torch.zeros(N + 1, dtype=torch.int64, device=dev)
+        send_ptr[1:] = torch.cumsum(torch.bincount(s_s, minlength=N), 0)
+        recv_perm = torch.argsort(r_s, stable=True)
+        recv_ptr = torch.zeros(N + 1, dtype=torch.int64, device=dev)
+        recv_ptr[1:] = torch.cumsum(torch.bincount(r_s, minlength=N), 0)
         seg_ptr = np.zeros(self.K + 1, np.int64)
         seg_ptr[1:] = np.cumsum(natoms)
-        batch = np.repeat(np.arange(self.K), natoms)
-        if E and (batch[s_s] != batch[r_s]).any():
+        nat_t = torch.tensor(natoms, dtype=torch.int64, device=dev)
+        batch = torch.repeat_interleave(torch.arange(self.K, device=dev), nat_t, output_size=N)
+        if E and bool((batch[s_s] != batch[r_s]).any()):
             raise ValueError("an edge joins two systems of the batch")
-        dev = torch.device(device)
-        i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(dev)
+        i32 = lambda a: a.to(torch.int32).contiguous()
         self.send, self.recv = i32(s_s), i32(r_s)
         self.send_ptr, self.recv_ptr, self.recv_perm = i32(send_ptr), i32(recv_ptr), i32(recv_perm)
-        self.seg_ptr, self.batch = i32(seg_ptr), i32(batch)
+        self.seg_ptr = torch.from_numpy(seg_ptr.astype(np.int32)).to(dev)
+        self.batch = i32(batch)
         self.natoms = natoms
-        self.Z = torch.as_tensor(atomic_numbers).to("cpu", torch.int64).to(dev)
+        self.Z = torch.as_tensor(atomic_numbers).to(dev, torch.int64)
         self.shift = None
         if cell_shift is not None:
-            sh = torch.as_tensor(cell_shift, dtype=torch.float32).cpu()[self.order]
-            self.shift = sh.contiguous().to(dev)
+            sh = torch.as_tensor(cell_shift, dtype=torch.float32).to(dev)[order]
+            self.shift = sh.contiguous()
 
 
 # ----------------------------------------------------------------------------- device weights

@@ -233,6 +233,11 @@ int tta_segment_mean(const float* x, const int* ptr, float* out, int64_t K, int6
                      tta_stream_t stream);
 int tta_segment_mean_bwd(const float* g, const int* batch, const int* ptr, float* out, int64_t N,
                          int64_t C, tta_stream_t stream);
+/* out[n, :] = x[n, :] - (mean of x over the rows [ptr[k], ptr[k+1]) of n's system k), 1 <= C <= 16:
+ * the direct ForceHead's net-force removal (orb_model.py:387-388; per system as ForceHead.batch,
+ * orb_model.py:401-404).  out may alias x only if it is x itself. */
+int tta_segment_center(const float* x, const int* ptr, float* out, int64_t K, int64_t C,
+                       tta_stream_t stream);
 /* y[r, :C] += x[r, :C] (row strides ldx, ldy): the residual adjoint sums of orb_forces.py:145. */
 int tta_add_rows(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t R, int64_t C,
                  tta_stream_t stream);

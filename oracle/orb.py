@@ -14,6 +14,9 @@ Pins (tests/test_oracle_orb.py):
   * backbone: fp64 finite differences of energy and stress, translation invariance, atom
     permutation invariance, disjoint-union batching == per-system evaluation, segment sums vs
     dense one-hot products.
+  * direct heads: per-system net force exactly zero, atom-permutation equivariance of the forces
+    and invariance of the stress head, batch == per-system, the normaliser split of the six
+    stress components on known values.
 The MLP/attention/head arithmetic has no upstream vector (every Orb golden of the reference is
 gated and uncommitted): against orb-models itself this part is "parity unpinned"; it is pinned by
 the invariants above only.
@@ -134,13 +137,57 @@ def node_features(w, Z):
     return w["atom_emb.embeddings.weight"][Z]
 
 
-def backbone(w, cfg, Z, edge_feat, cut, senders, receivers, batch, natoms, cond_nodes=None):
+def force_head(nodes, batch, natoms, w):
+    """Direct ForceHead (orb_model.py:381-404): per-node Linear-SiLU-Linear -> [N, 3], then each
+    system's mean predicted force is subtracted (net-force removal per system, as the batched
+    form does; one system = the single-system form)."""
+    h = F.silu(_lin(nodes, w, "forces_head.mlp.NN-0"))
+    pred = _lin(h, w, "forces_head.mlp.NN-1")
+    K = len(natoms)
+    mean = torch.zeros(K, pred.shape[1], dtype=pred.dtype).index_add_(0, batch, pred)
+    mean = mean / torch.as_tensor(natoms, dtype=pred.dtype)[:, None]
+    return pred - mean[batch]
+
+
+def stress_head(nodes, batch, natoms, w):
+    """Direct StressHead (orb_model.py:429-435): per-system mean of node features, then
+    Linear-SiLU-Linear -> raw Voigt [K, 6] ([xx, yy, zz, yz, xz, xy])."""
+    K = len(natoms)
+    mean = torch.zeros(K, nodes.shape[1], dtype=nodes.dtype).index_add_(0, batch, nodes)
+    mean = mean / torch.as_tensor(natoms, dtype=nodes.dtype)[:, None]
+    h = F.silu(_lin(mean, w, "stress_head.mlp.NN-0"))
+    return _lin(h, w, "stress_head.mlp.NN-1")
+
+
+def node_embedding(w, cfg, Z, edge_feat, cut, senders, receivers, cond_nodes=None):
+    """Encoder and the message-passing layers -> final node features [N, latent]."""
     nodes = mlp_norm(node_features(w, Z), w, "_encoder._node_fn")
     edges = mlp_norm(edge_feat, w, "_encoder._edge_fn")
     for i in range(cfg["num_message_passing_steps"]):
         nodes, edges = attention_layer(nodes, edges, senders, receivers, cut, w,
                                        f"gnn_stacks.{i}", cond_nodes)
+    return nodes
+
+
+def backbone(w, cfg, Z, edge_feat, cut, senders, receivers, batch, natoms, cond_nodes=None):
+    nodes = node_embedding(w, cfg, Z, edge_feat, cut, senders, receivers, cond_nodes)
     return energy_head(nodes, batch, natoms, w)
+
+
+def direct_forward(w, cfg, pos, Z, senders, receivers, shift, batch, natoms, *,
+                   compute_stress=False, cond_nodes=None):
+    """Direct checkpoint, forward only (orb_calculator.py:141-185, 266-277): raw energies [K],
+    raw forces from the ForceHead [N, 3] and, with ``compute_stress``, the raw StressHead Voigt
+    vectors [K, 6]."""
+    dt = pos.dtype
+    w = {k: v.to(dt) for k, v in w.items()}
+    feat, cut, _ = edge_features(pos, senders, receivers, shift, cfg["cutoff"], cfg["num_bases"])
+    nodes = node_embedding(w, cfg, Z, feat, cut, senders, receivers,
+                           None if cond_nodes is None else cond_nodes.to(dt))
+    raw_e = energy_head(nodes, batch, natoms, w)
+    raw_f = force_head(nodes, batch, natoms, w)
+    raw_s = stress_head(nodes, batch, natoms, w) if compute_stress else None
+    return raw_e, raw_f, raw_s
 
 
 def energy_and_forces(w, cfg, pos, Z, senders, receivers, shift, batch, natoms, *,
@@ -211,3 +258,17 @@ def denormalize_energy(raw, Z, n, running_mean, running_var, ref_weight):
 def denormalize_forces(raw_f, n, running_var):
     """raw forces * sigma * n (orb_model.py:459-469)."""
     return raw_f.double() * running_var.double().sqrt() * n
+
+
+def denormalize_direct_forces(raw_f, running_mean, running_var):
+    """ForceHead's scalar normaliser inverse raw sigma + mu (orb_model.py:438-442)."""
+    return raw_f.double() * running_var.double().sqrt() + running_mean.double()
+
+
+def denormalize_direct_stress(raw_s, diag_mean, diag_var, offdiag_mean, offdiag_var):
+    """StressHead's two normalisers: components 0..2 and 3..5 each raw sigma + mu, no volume
+    division (orb_model.py:445-457)."""
+    raw = raw_s.double().reshape(-1, 6)
+    diag = raw[:, :3] * diag_var.double().sqrt() + diag_mean.double()
+    off = raw[:, 3:] * offdiag_var.double().sqrt() + offdiag_mean.double()
+    return torch.cat([diag, off], dim=1).reshape(raw_s.shape)

@@ -264,3 +264,133 @@ def test_orb_step_graph_replays_match_eager():
     torch.cuda.synchronize()
     assert torch.equal(eng.raw, raw1) and torch.equal(eng.forces, F1)
     assert not torch.equal(raw1, raw0)
+
+
+# ----------------------------------------------------------------------------- direct heads
+def _direct_check(cfg, w, bg, raw, F, S_raw, oracle_dtype=torch.float64):
+    """Denormalised energies within 1e-6 relative, forces within 1e-4 eV/A and the stress head
+    within 1e-5 eV/A^3 of the oracle; every system's net force is zero."""
+    ref_e, ref_f, ref_s = O.direct_forward(w, cfg, bg.pos.to(oracle_dtype), bg.Z, bg.senders,
+                                           bg.receivers, bg.cell_shift.to(oracle_dtype),
+                                           bg.batch, bg.natoms,
+                                           compute_stress=S_raw is not None)
+    off = 0
+    for k, n in enumerate(bg.natoms):
+        e = float(orb.denormalize_energy(raw[k], bg.Z[off:off + n], n, w))
+        e_ref = float(orb.denormalize_energy(ref_e[k].double(), bg.Z[off:off + n], n, w))
+        assert abs(e - e_ref) <= 1e-6 * max(1.0, abs(e_ref)), (k, e, e_ref)
+        f = orb.denormalize_direct_forces(F[off:off + n].double(), w)
+        f_ref = O.denormalize_direct_forces(ref_f[off:off + n],
+                                            w["forces_head.normalizer.bn.running_mean"],
+                                            w["forces_head.normalizer.bn.running_var"])
+        assert (f - f_ref).abs().max() <= 1e-4, (k, (f - f_ref).abs().max())
+        assert F[off:off + n].double().sum(0).abs().max() < 1e-5
+        off += n
+    if S_raw is not None:
+        s = orb.denormalize_direct_stress(S_raw.double(), w)
+        s_ref = O.denormalize_direct_stress(
+            ref_s, w["stress_head.diag_normalizer.bn.running_mean"],
+            w["stress_head.diag_normalizer.bn.running_var"],
+            w["stress_head.offdiag_normalizer.bn.running_mean"],
+            w["stress_head.offdiag_normalizer.bn.running_var"])
+        assert (s - s_ref).abs().max() <= 1e-5, (s - s_ref).abs().max()
+
+
+def _direct_engine(cfg, w, bg, use_graph=True):
+    model = orb.OrbModel(w, cfg)
+    graph = orb.OrbGraph(model.device, senders=bg.senders, receivers=bg.receivers,
+                         num_nodes=bg.pos.shape[0], atomic_numbers=bg.Z, cell_shift=bg.cell_shift,
+                         natoms=bg.natoms)
+    return model, orb.OrbEngine(model, graph, use_graph=use_graph)
+
+
+@pytest.mark.parametrize("arch", ["tiny", "c5"])
+def test_orb_direct_heads_match_oracle(nat, arch):
+    """Direct checkpoint: forward + ForceHead (per-system net-force removal) + StressHead on a
+    batch, against the fp64 oracle; graph replays equal the eager step bit for bit."""
+    if arch == "tiny":
+        cfg = dict(S.CFG_ORB_TINY)
+        systems = S.c5_systems(21, K=3, n_min=6, n_max=14, side=5.0)
+    else:
+        cfg = dict(S.CFG_ORB_C5)
+        systems = S.c5_systems()[:8]
+    w = S.random_orb_weights(cfg, 41, direct=True)
+    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    model, eng = _direct_engine(cfg, w, bg)
+    assert model.is_direct and model.has_stress_head
+    p = bg.pos.to(model.device)
+    raw, F, S_raw = eng.run(p, compute_stress=True, eager=True)
+    F, S_raw = F.detach().cpu().clone(), S_raw.detach().cpu().clone()
+    _direct_check(cfg, w, bg, raw, F, S_raw)
+    for _ in range(3):                                   # capture, then replays
+        raw2, F2, S2 = eng.run(p, compute_stress=True)
+        torch.cuda.synchronize()
+        assert torch.equal(raw2, raw) and torch.equal(F2.cpu(), F) and torch.equal(S2.cpu(), S_raw)
+    raw3, F3, none = eng.run(p)                          # the variant without the stress head
+    assert none is None and torch.equal(raw3, raw) and torch.equal(F3.cpu(), F)
+
+
+def test_orb_direct_session(nat, tmp_path):
+    """OrbSession on a direct bundle: periodic crystal with stress (ZBL sum-aggregated) against
+    the oracle, evaluate_batch == evaluate per system, and a direct checkpoint without a stress
+    head refuses an explicit stress request."""
+    from tt_atom import orb_calculator as OC
+    cfg = dict(S.CFG_ORB_TINY)
+    w = S.random_orb_weights(cfg, 43, direct=True)
+    path = tmp_path / "orb_direct.npz"
+    orb.save_orb_bundle(path, cfg, w)
+    radii = np.full(120, 0.6)
+    sess = OC.OrbSession(str(path), pair_repulsion=True, covalent_radii=radii)
+    assert sess.is_direct and sess.zbl_aggregation == "sum"
+    pos, Z, cell = S.c4_system(seed=4, reps=2, a=3.61, noise=0.05, Z=29)
+    r = sess.evaluate(pos, Z, cell=cell, pbc=[True] * 3, properties=("energy", "forces", "stress"))
+    bg = orb.assemble_orb([(pos, Z, cell, [True] * 3)], cfg["cutoff"], cfg["max_num_neighbors"])
+    e_raw, f_raw, s_raw = O.direct_forward(w, cfg, bg.pos.double(), bg.Z, bg.senders,
+                                           bg.receivers, bg.cell_shift.double(), bg.batch,
+                                           bg.natoms, compute_stress=True)
+    n = bg.natoms[0]
+    e_z, f_z, s_z = OC.zbl_energy_forces_stress(bg.Z, bg.senders, bg.receivers, bg.pos,
+                                                bg.cell_shift, radii, cell, aggregation="sum")
+    e_ref = float(orb.denormalize_energy(e_raw[0], bg.Z, n, w)) + e_z
+    f_ref = O.denormalize_direct_forces(f_raw, w["forces_head.normalizer.bn.running_mean"],
+                                        w["forces_head.normalizer.bn.running_var"]).numpy() + f_z
+    s_ref = O.denormalize_direct_stress(
+        s_raw[0], w["stress_head.diag_normalizer.bn.running_mean"],
+        w["stress_head.diag_normalizer.bn.running_var"],
+        w["stress_head.offdiag_normalizer.bn.running_mean"],
+        w["stress_head.offdiag_normalizer.bn.running_var"]).numpy() + s_z
+    assert abs(r["energy"] - e_ref) <= 1e-6 * max(1.0, abs(e_ref))
+    assert np.abs(r["forces"] - f_ref).max() <= 1e-4
+    assert np.abs(r["stress"] - s_ref).max() <= 1e-5
+    systems = S.c5_systems(17, K=3, n_min=6, n_max=12, side=5.0)
+    res = [sess.evaluate(p, z) for p, z in systems]
+    batch = sess.evaluate_batch(systems)
+    for k, rk in enumerate(res):
+        assert abs(batch["energy"][k] - rk["energy"]) <= 1e-6 * max(1.0, abs(rk["energy"]))
+        assert np.abs(batch["forces"][k] - rk["forces"]).max() <= 2e-5
+    w_ns = {k: v for k, v in w.items() if not k.startswith("stress_head.")}
+    path2 = tmp_path / "orb_direct_nostress.npz"
+    orb.save_orb_bundle(path2, cfg, w_ns)
+    sess2 = OC.OrbSession(str(path2), pair_repulsion=False)
+    with pytest.raises(ValueError, match="stress_head"):
+        sess2.evaluate(pos, Z, cell=cell, pbc=[True] * 3, properties=("energy", "stress"))
+    r2 = sess2.evaluate(pos, Z, cell=cell, pbc=[True] * 3)     # implicit stress: left out
+    assert "stress" not in r2
+
+
+def test_segment_center(nat):
+    """Per-system centring kernel: ragged systems, a one-row system, C = 3 and C = 16."""
+    g = torch.Generator().manual_seed(3)
+    sizes = [1, 5, 64, 65, 130, 7]
+    ptr = torch.tensor([0] + list(np.cumsum(sizes)), dtype=torch.int32)
+    N = int(ptr[-1])
+    for C in (3, 16):
+        x = torch.randn(N, C, generator=g)
+        out = torch.empty(N, C, device="cuda")
+        nat.segment_center(x.cuda(), ptr.cuda(), out)
+        torch.cuda.synchronize()
+        ref = torch.cat([xs - xs.double().mean(0).float() for xs in torch.split(x, sizes)])
+        assert (out.cpu() - ref).abs().max() < 1e-6
+        xi = x.cuda()
+        nat.segment_center(xi, ptr.cuda(), xi)                  # in place
+        assert torch.equal(xi, out)

@@ -182,3 +182,70 @@ def test_assemble_cap_and_convention():
     assert int(bg["batch"][bg["senders"]].ne(bg["batch"][bg["receivers"]]).sum()) == 0
     v = bg["pos"][bg["receivers"]] - bg["pos"][bg["senders"]]
     assert (torch.linalg.norm(v, dim=1) < cfg["cutoff"]).all()
+
+
+def test_direct_heads_invariants_and_batching():
+    """Direct checkpoint (ForceHead / StressHead): per-system net force zero, the shared weights
+    and energy equal to the conservative draw, batch == per-system (which a whole-batch mean
+    removal would break: the systems' mean predictions differ), atom relabelling permutes forces
+    and leaves energies and stress unchanged."""
+    seed = 11
+    cfg = dict(S.CFG_ORB_TINY)
+    w = S.random_orb_weights(cfg, seed + S.WEIGHT_SEED_OFFSET, direct=True)
+    wc = S.random_orb_weights(cfg, seed + S.WEIGHT_SEED_OFFSET)
+    assert all(torch.equal(wc[k], w[k]) for k in wc)
+    systems = [(torch.from_numpy(p).double(), torch.from_numpy(z))
+               for p, z in S.c5_systems(seed, K=3, n_min=6, n_max=12, side=5.0)]
+    bg = O.assemble(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    args = (bg["pos"], bg["Z"], bg["senders"], bg["receivers"], bg["shift"], bg["batch"],
+            bg["natoms"])
+    e, f, s = O.direct_forward(w, cfg, *args, compute_stress=True)
+    assert f.shape == (bg["pos"].shape[0], 3) and s.shape == (3, 6)
+    torch.testing.assert_close(e, _eval(cfg, wc, bg)[0], rtol=1e-12, atol=1e-12)
+    for k in range(3):
+        assert f[bg["batch"] == k].sum(0).abs().max() < 1e-12
+    assert f.abs().max() > 1e-3 and s.abs().max() > 1e-3
+    # the systems' mean raw predictions differ, so a whole-batch mean would change the forces
+    wd = {k: v.double() for k, v in w.items()}
+    feat, cut, _ = O.edge_features(bg["pos"], bg["senders"], bg["receivers"], bg["shift"],
+                                   cfg["cutoff"], cfg["num_bases"])
+    nodes = O.node_embedding(wd, cfg, bg["Z"], feat, cut, bg["senders"], bg["receivers"])
+    pred = O._lin(torch.nn.functional.silu(O._lin(nodes, wd, "forces_head.mlp.NN-0")), wd,
+                  "forces_head.mlp.NN-1")
+    means = torch.stack([pred[bg["batch"] == k].mean(0) for k in range(3)])
+    assert (means[0] - means[1]).abs().max() > 1e-4 and (means[1] - means[2]).abs().max() > 1e-4
+    # batch == per system
+    off = 0
+    for k, (p, z) in enumerate(systems):
+        one = O.assemble([(p, z)], cfg["cutoff"], cfg["max_num_neighbors"])
+        ek, fk, sk = O.direct_forward(w, cfg, one["pos"], one["Z"], one["senders"],
+                                      one["receivers"], one["shift"], one["batch"], one["natoms"],
+                                      compute_stress=True)
+        n = z.shape[0]
+        torch.testing.assert_close(ek[0], e[k], rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(fk, f[off:off + n], rtol=1e-10, atol=1e-12)
+        torch.testing.assert_close(sk[0], s[k], rtol=1e-10, atol=1e-12)
+        off += n
+    # relabelling atoms
+    perm = torch.randperm(bg["pos"].shape[0], generator=torch.Generator().manual_seed(1))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    e3, f3, s3 = O.direct_forward(w, cfg, bg["pos"][perm], bg["Z"][perm], inv[bg["senders"]],
+                                  inv[bg["receivers"]], bg["shift"], bg["batch"][perm],
+                                  bg["natoms"], compute_stress=True)
+    torch.testing.assert_close(e3, e, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(f3, f[perm], rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(s3, s, rtol=1e-10, atol=1e-12)
+
+
+def test_direct_denormalisers_known_values():
+    """x sigma + mu with sigma = sqrt(var); the stress's first three components take the diagonal
+    normaliser and the last three the off-diagonal one (distinct values catch a swap)."""
+    f = O.denormalize_direct_forces(torch.tensor([[1.0, -2.0, 0.0]]), torch.tensor(0.5),
+                                    torch.tensor(0.25))
+    torch.testing.assert_close(f, torch.tensor([[1.0, -0.5, 0.5]], dtype=torch.float64))
+    s = O.denormalize_direct_stress(torch.tensor([1.0, 2.0, 3.0, 1.0, 2.0, 3.0]),
+                                    torch.tensor(0.1), torch.tensor(4.0),
+                                    torch.tensor(-1.0), torch.tensor(9.0))
+    torch.testing.assert_close(s, torch.tensor([2.1, 4.1, 6.1, 2.0, 5.0, 8.0],
+                                               dtype=torch.float64))

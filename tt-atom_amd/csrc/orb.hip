@@ -534,6 +534,38 @@ __global__ __launch_bounds__(256) void k_segment_mean_bwd(const float* __restric
   out[gid] = g[(int64_t)k * C + c] / (float)(ptr[k + 1] - ptr[k]);
 }
 
+// out[n, :] = x[n, :] - mean of x over n's system (ForceHead net-force removal,
+// orb_model.py:387-388, per system as in the batched form 401-404).  One wavefront per system:
+// lane j sums rows j, j + 64, ... in order, then a fixed butterfly over the lanes, so the result
+// does not depend on scheduling.  C <= kCenterMaxC columns.
+constexpr int kCenterMaxC = 16;
+// x and out are not __restrict__: the entry point allows out == x.
+__global__ __launch_bounds__(256) void k_segment_center(const float* x,
+                                                        const int* __restrict__ ptr, float* out,
+                                                        int64_t K, int C) {
+  const int lane = threadIdx.x & 63;
+  const int64_t k = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (k >= K) return;
+  const int n0 = ptr[k], n1 = ptr[k + 1];
+  float acc[kCenterMaxC];
+#pragma unroll
+  for (int c = 0; c < kCenterMaxC; ++c) acc[c] = 0.f;
+  for (int n = n0 + lane; n < n1; n += 64) {
+#pragma unroll
+    for (int c = 0; c < kCenterMaxC; ++c)
+      if (c < C) acc[c] += x[(int64_t)n * C + c];
+  }
+  const float inv_cnt = 1.f / (float)max(n1 - n0, 1);
+#pragma unroll
+  for (int c = 0; c < kCenterMaxC; ++c)
+    if (c < C) acc[c] = wave_sum(acc[c]) * inv_cnt;
+  for (int n = n0 + lane; n < n1; n += 64) {
+#pragma unroll
+    for (int c = 0; c < kCenterMaxC; ++c)
+      if (c < C) out[(int64_t)n * C + c] = x[(int64_t)n * C + c] - acc[c];
+  }
+}
+
 // y[r, :C] += x[r, :C] with row strides ldx, ldy.
 __global__ __launch_bounds__(256) void k_add_rows(const float* __restrict__ x, int64_t ldx,
                                                   float* __restrict__ y, int64_t ldy, int64_t R,
@@ -663,6 +695,18 @@ extern "C" int tta_segment_mean_bwd(const float* g, const int* batch, const int*
   hipLaunchKernelGGL(k_segment_mean_bwd, dim3(tta_blocks(N * C, 256)), dim3(256), 0, stream, g,
                      batch, ptr, out, N, (int)C);
   TTA_CHECK_LAUNCH("tta_segment_mean_bwd");
+  return tta::kOk;
+}
+
+extern "C" int tta_segment_center(const float* x, const int* ptr, float* out, int64_t K,
+                                  int64_t C, hipStream_t stream) {
+  TTA_CHECK_ARG(K >= 0 && C > 0 && C <= kCenterMaxC,
+                "tta_segment_center: bad sizes (1 <= C <= 16)");
+  if (K == 0) return tta::kOk;
+  TTA_CHECK_ARG(x && ptr && out, "tta_segment_center: null pointer");
+  hipLaunchKernelGGL(k_segment_center, dim3((unsigned)((K + 3) / 4)), dim3(256), 0, stream, x, ptr,
+                     out, K, (int)C);
+  TTA_CHECK_LAUNCH("tta_segment_center");
   return tta::kOk;
 }
 

@@ -60,6 +60,7 @@ _SIGS = {
     "tta_orb_node_segsum2": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_segment_mean": [_P, _P, _P, _I64, _I64, _P],
     "tta_segment_mean_bwd": [_P, _P, _P, _P, _I64, _I64, _P],
+    "tta_segment_center": [_P, _P, _P, _I64, _I64, _P],
     "tta_add_rows": [_P, _I64, _P, _I64, _I64, _I64, _P],
     "tta_gather_rotate_src": [_P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_gather_rotate_src_bw": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
@@ -642,6 +643,16 @@ def segment_mean_bwd(g, batch, ptr, out):
     K = ptr.numel() - 1
     _call("tta_segment_mean_bwd", _ptr(g, numel=K * C, name="g"), _i32(batch, N), _i32(ptr, K + 1),
           _ptr(out, numel=N * C), N, C, _stream())
+
+
+def segment_center(x, ptr, out):
+    """out[n] = x[n] - mean of x over n's system, systems the row ranges [ptr[k], ptr[k+1])
+    (ptr[K] must equal the row count); out may be x itself."""
+    N, C = out.shape
+    K = ptr.numel() - 1
+    _call("tta_segment_center", _ptr(x, numel=N * C, name="x"), _i32(ptr, K + 1),
+          _ptr(out, numel=N * C, name="out"), K, C, _stream())
+    return out
 
 
 def add_rows(x, y):

@@ -257,9 +257,6 @@ class OrbModel:
                                "edge_embed_size = 16 * num_bases")
         if self.C % 4 or self.C > 1024:
             raise RuntimeError("latent_dim must be a multiple of 4 and at most 1024")
-        if "forces_head.mlp.NN-0.weight" in w:
-            raise RuntimeError("direct-force Orb checkpoints are not part of this build "
-                               "(conservative checkpoints only)")
         dev = self.device
         self.node_emb = w["atom_emb.embeddings.weight"]          # host table, gathered per graph
         self.enc_node = _MLPNorm(w, "_encoder._node_fn", dev, mode)
@@ -273,9 +270,29 @@ class OrbModel:
         self.eh_w_t = [_dev(w[f"energy_head.mlp.NN-{i}.weight"].T.contiguous(), dev) for i in (0, 1)]
         self.eh_w = [_dev(w[f"energy_head.mlp.NN-{i}.weight"], dev) for i in (0, 1)]
         self.eh_b = [_dev(w[f"energy_head.mlp.NN-{i}.bias"], dev) for i in (0, 1)]
+        # direct checkpoints carry a force head (and usually a stress head) and are evaluated by
+        # the forward alone (orb_calculator.py:66-72, 141-185)
+        self.is_direct = "forces_head.mlp.NN-0.weight" in w
+        self.has_stress_head = "stress_head.mlp.NN-0.weight" in w
+        self.fh_w_t = self.fh_b = self.sh_w_t = self.sh_b = None
+        if self.is_direct:
+            self.fh_w_t = [_dev(w[f"forces_head.mlp.NN-{i}.weight"].T.contiguous(), dev)
+                           for i in (0, 1)]
+            self.fh_b = [_dev(w[f"forces_head.mlp.NN-{i}.bias"], dev) for i in (0, 1)]
+            if self.fh_w_t[1].shape[1] != 3:
+                raise RuntimeError("the force head must have 3 outputs")
+        if self.has_stress_head:
+            self.sh_w_t = [_dev(w[f"stress_head.mlp.NN-{i}.weight"].T.contiguous(), dev)
+                           for i in (0, 1)]
+            self.sh_b = [_dev(w[f"stress_head.mlp.NN-{i}.bias"], dev) for i in (0, 1)]
+            if self.sh_w_t[1].shape[1] != 6:
+                raise RuntimeError("the stress head must have 6 outputs")
         self.has_cond = "conditioner.charge_embedding.W" in w
         self.host_w = {k: v for k, v in w.items() if k.startswith(("energy_head.normalizer",
                                                                    "energy_head.reference",
+                                                                   "forces_head.normalizer",
+                                                                   "stress_head.diag_normalizer",
+                                                                   "stress_head.offdiag_normalizer",
                                                                    "conditioner."))}
 
     def charge_spin_embedding(self, charge, spin, n):
@@ -295,7 +312,9 @@ class OrbModel:
 class OrbEngine:
     """One fixed-topology energy + forces step: buffers are allocated once per graph and every
     call is the same kernel sequence, captured as a HIP graph on the second call of each variant
-    (with / without stress) and replayed afterwards unless ``use_graph`` is False."""
+    (with / without stress) and replayed afterwards unless ``use_graph`` is False.  For a direct
+    checkpoint the step is the forward and the force / stress heads; otherwise the forward and
+    the analytic backward."""
 
     def __init__(self, model, graph, cond_nodes=None, use_graph=True):
         self.m, self.g = model, graph
@@ -341,6 +360,11 @@ class OrbEngine:
         self.g_h2, self.G = f(E, C), f(N, 2 * H)
         self.g_feat, self.g_vec = f(E, nb16), f(E, 3)
         self.forces, self.virial_buf, self.work = f(N, 3), f(9), f(256 * 9)
+        # direct heads
+        if model.is_direct:
+            self.fa, self.fpred = f(N, model.fh_w_t[0].shape[1]), f(N, 3)
+        if model.has_stress_head:
+            self.sa, self.raw_s = f(K, model.sh_w_t[0].shape[1]), f(K, 6)
 
     # -- forward --------------------------------------------------------------------------
     def _mlp3(self, mlp, x, a0, h0, a1, h1, h2):
@@ -430,14 +454,31 @@ class OrbEngine:
         if compute_stress:
             nat.virial(self.vec, self.g_vec, self.work, self.virial_buf)
 
+    # -- direct heads (orb_model.py:381-435) ------------------------------------------------
+    def _direct_heads(self, compute_stress):
+        m, g = self.m, self.g
+        nodes = self.nodes[len(m.layers)]
+        nat.linear(nodes, m.fh_w_t[0], m.fh_b[0], out=self.fa, epilogue=nat.EPI_SILU)
+        nat.linear(self.fa, m.fh_w_t[1], m.fh_b[1], out=self.fpred)
+        nat.segment_center(self.fpred, g.seg_ptr, self.forces)     # per-system net force removal
+        if compute_stress:                                          # on the energy head's mean
+            nat.linear(self.mean, m.sh_w_t[0], m.sh_b[0], out=self.sa, epilogue=nat.EPI_SILU)
+            nat.linear(self.sa, m.sh_w_t[1], m.sh_b[1], out=self.raw_s)
+
     def _step(self, compute_stress):
         self._forward(self.pos)
-        self._backward(compute_stress)
+        if self.m.is_direct:
+            self._direct_heads(compute_stress)
+        else:
+            self._backward(compute_stress)
 
     def step(self, pos, compute_stress=False, eager=False):
         """Enqueue one step on the current stream; results stay in the device buffers (raw,
         forces, virial_buf).  Without ``eager`` (and with ``use_graph``) it replays a HIP graph
         captured on the second call of each variant (the first runs eagerly)."""
+        if compute_stress and self.m.is_direct and not self.m.has_stress_head:
+            raise ValueError("stress requested but this direct checkpoint carries no "
+                             "stress_head weights")
         self.pos.copy_(torch.as_tensor(pos, dtype=torch.float32).reshape(-1, 3),
                        non_blocking=True)
         if self.use_graph and not eager:
@@ -447,11 +488,15 @@ class OrbEngine:
 
     def run(self, pos, compute_stress=False, eager=False):
         """pos [N, 3] fp32 (node order of the graph) -> (raw energies [K] fp64 host, raw forces
-        [N, 3] device view, raw virial [3, 3] device view or None); raw = normalised space, as
-        orb_forces.energy_and_forces returns."""
+        [N, 3] device view, stress term or None); raw = normalised space, as
+        orb_forces.energy_and_forces returns.  The stress term is the raw virial dE/dstrain
+        [3, 3] (device view) for a conservative checkpoint and the StressHead's raw Voigt
+        vectors [K, 6] for a direct one."""
         self.step(pos, compute_stress, eager)
         raw = self.raw.view(-1).double().cpu()
-        return raw, self.forces, (self.virial_buf.view(3, 3) if compute_stress else None)
+        if not compute_stress:
+            return raw, self.forces, None
+        return raw, self.forces, (self.raw_s if self.m.is_direct else self.virial_buf.view(3, 3))
 
 
 # ----------------------------------------------------------------------------- functional API
@@ -504,3 +549,20 @@ def denormalize_stress(virial, n, cell, w):
     s = virial.double() * sigma * n / torch.linalg.det(torch.as_tensor(cell).double()).abs()
     return torch.stack([s[0, 0], s[1, 1], s[2, 2], 0.5 * (s[1, 2] + s[2, 1]),
                         0.5 * (s[0, 2] + s[2, 0]), 0.5 * (s[0, 1] + s[1, 0])])
+
+
+def denormalize_direct_forces(raw_f, w):
+    """Direct ForceHead output raw sigma + mu (orb_model.py:438-442)."""
+    sigma = w["forces_head.normalizer.bn.running_var"].double().sqrt()
+    return raw_f.double() * sigma + w["forces_head.normalizer.bn.running_mean"].double()
+
+
+def denormalize_direct_stress(raw_s, w):
+    """Direct StressHead Voigt vector: components 0..2 through the diagonal normaliser, 3..5
+    through the off-diagonal one, no volume division (orb_model.py:445-457)."""
+    raw = raw_s.double().reshape(-1, 6)
+    p = "stress_head.diag_normalizer.bn."
+    q = "stress_head.offdiag_normalizer.bn."
+    diag = raw[:, :3] * w[p + "running_var"].double().sqrt() + w[p + "running_mean"].double()
+    off = raw[:, 3:] * w[q + "running_var"].double().sqrt() + w[q + "running_mean"].double()
+    return torch.cat([diag, off], dim=1).reshape(raw_s.shape)

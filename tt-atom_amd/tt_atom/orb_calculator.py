@@ -1,12 +1,17 @@
 """``OrbCalculator`` -- ASE calculator over the MI355X Orb-v3 step (reference orb_calculator.py:25-327).
 
-``OrbSession`` holds one Orb-v3 conservative checkpoint on one GPU and evaluates arrays (one
-system, ``evaluate``) or a disjoint-union batch (``evaluate_batch``) as the reference's
-``calculate`` / ``evaluate_batch`` do: neighbour list (senders = tgt, receivers = src), node
-embedding and optional charge/spin conditioning, one device forward + backward, then the energy
-normaliser ``E = (raw sigma + mu) n + sum ref[Z]``, ``F = raw_F sigma n`` and
-``stress = virial sigma n / V`` (orb_model.py:459-600), plus the ZBL pair repulsion
-(orb_model.py:491-585) when enabled.  The step engine is kept while the graph is unchanged.
+``OrbSession`` holds one Orb-v3 checkpoint on one GPU and evaluates arrays (one system,
+``evaluate``) or a disjoint-union batch (``evaluate_batch``) as the reference's ``calculate`` /
+``evaluate_batch`` do: neighbour list (senders = tgt, receivers = src), node embedding and
+optional charge/spin conditioning, then
+  * conservative checkpoints: one device forward + backward, the energy normaliser
+    ``E = (raw sigma + mu) n + sum ref[Z]``, ``F = raw_F sigma n`` and
+    ``stress = virial sigma n / V`` (orb_model.py:459-600), ZBL mean-aggregated;
+  * direct checkpoints (a ``forces_head`` in the weights): the device forward and the force /
+    stress heads, ``F = raw_F sigma_F + mu_F`` and the two-normaliser Voigt stress
+    (orb_model.py:438-457), ZBL sum-aggregated (orb_calculator.py:124-185);
+plus the ZBL pair repulsion (orb_model.py:491-585) when enabled.  The step engine is kept while
+the graph is unchanged.
 ``OrbCalculator`` adapts it to ASE; ``ase`` is optional and only that class (and the default ZBL
 radius table) needs it.
 """
@@ -91,7 +96,7 @@ def _default_radii():
 
 # ----------------------------------------------------------------------------- session
 class OrbSession:
-    """One Orb-v3 conservative checkpoint on one GPU (orb_calculator.py:26-73)."""
+    """One Orb-v3 checkpoint, conservative or direct, on one GPU (orb_calculator.py:26-73)."""
 
     def __init__(self, weights, device=None, device_id=0, precision="f32", pair_repulsion=True,
                  covalent_radii=None, neighbor_list="device"):
@@ -107,6 +112,8 @@ class OrbSession:
         self.pair_repulsion = pair_repulsion
         self._radii = covalent_radii
         self.neighbor_list = neighbor_list
+        self.is_direct = self.model.is_direct
+        self.zbl_aggregation = "sum" if self.is_direct else "mean"
         self._engine, self._key = None, None
 
     def _radii_table(self):
@@ -150,18 +157,31 @@ class OrbSession:
         system = dict(positions=positions, numbers=numbers, cell=cell_a,
                       pbc=pbc_a if cell_a is not None else None, charge=charge, spin=spin)
         bg = orb.assemble_orb([system], self.r_max, self.max_num_neighbors, self.neighbor_list)
-        want_stress = cell_a is not None and ("stress" in properties or bool(pbc_a.all()))
-        raw, F_raw, vir = self._run(bg, want_stress)
+        explicit_stress = "stress" in properties
+        want_stress = cell_a is not None and (explicit_stress or bool(pbc_a.all()))
+        if self.is_direct and not self.model.has_stress_head:
+            if explicit_stress:
+                raise ValueError("stress requested but this direct checkpoint carries no "
+                                 "stress_head weights")
+            want_stress = False          # a periodic system that did not ask for stress
+        raw, F_raw, s_raw = self._run(bg, want_stress)
         n = bg.natoms[0]
         E = float(orb.denormalize_energy(raw[0], bg.Z, n, self._w))
-        F = orb.denormalize_forces(F_raw, n, self._w).numpy()
         stress = None
-        if want_stress:
-            stress = orb.denormalize_stress(vir, n, torch.as_tensor(cell_a), self._w).numpy()
+        if self.is_direct:
+            F = orb.denormalize_direct_forces(F_raw, self._w).numpy()
+            if want_stress:
+                stress = orb.denormalize_direct_stress(s_raw[0], self._w).numpy()
+        else:
+            F = orb.denormalize_forces(F_raw, n, self._w).numpy()
+            if want_stress:
+                stress = orb.denormalize_stress(s_raw, n, torch.as_tensor(cell_a),
+                                                self._w).numpy()
         if self.pair_repulsion:
             e_z, f_z, s_z = zbl_energy_forces_stress(bg.Z, bg.senders, bg.receivers, bg.pos,
                                                      bg.cell_shift, self._radii_table(),
-                                                     cell_a if want_stress else None)
+                                                     cell_a if want_stress else None,
+                                                     aggregation=self.zbl_aggregation)
             E, F = E + e_z, F + f_z
             if stress is not None:
                 stress = stress + s_z
@@ -180,12 +200,15 @@ class OrbSession:
         for k, n in enumerate(bg.natoms):
             sl = slice(off, off + n)
             E_k = float(orb.denormalize_energy(raw[k], bg.Z[sl], n, self._w))
-            F_k = orb.denormalize_forces(F_raw[sl], n, self._w).numpy()
+            if self.is_direct:
+                F_k = orb.denormalize_direct_forces(F_raw[sl], self._w).numpy()
+            else:
+                F_k = orb.denormalize_forces(F_raw[sl], n, self._w).numpy()
             if self.pair_repulsion:
                 m = (bg.senders >= off) & (bg.senders < off + n)
                 e_z, f_z, _ = zbl_energy_forces_stress(
                     bg.Z[sl], bg.senders[m] - off, bg.receivers[m] - off, bg.pos[sl],
-                    bg.cell_shift[m], self._radii_table())
+                    bg.cell_shift[m], self._radii_table(), aggregation=self.zbl_aggregation)
                 E_k, F_k = E_k + e_z, F_k + f_z
             energies.append(E_k)
             forces.append(F_k)

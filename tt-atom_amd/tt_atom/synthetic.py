@@ -279,11 +279,13 @@ def c5_systems(seed=SEEDS["C5"], K=256, n_min=20, n_max=60, side=7.0, dmin=0.9):
     return out
 
 
-def random_orb_weights(cfg, seed):
+def random_orb_weights(cfg, seed, direct=False):
     """Random-init MoleculeGNS weights in the orb-models state-dict key layout
     (tools/export_orb_weights.py:64-80): nn.Linear-style U(-1/sqrt(fan_in), 1/sqrt(fan_in))
     linears, RMSNorm weights 1 + 0.1 N(0,1), N(0,1) atom embeddings, energy-head normaliser and a
-    per-element reference energy."""
+    per-element reference energy.  ``direct`` adds the direct checkpoint's force head (3 outputs)
+    and stress head (6 outputs) with their normalisers (orb_model.py:358-457), drawn after every
+    conservative weight so the shared weights are the same either way."""
     gen = torch.Generator().manual_seed(int(seed))
     C, Hd, He = cfg["latent_dim"], cfg.get("mlp_hidden_dim", 1024), cfg.get("head_hidden_dim", 256)
     w = {}
@@ -318,6 +320,17 @@ def random_orb_weights(cfg, seed):
     w["energy_head.normalizer.bn.running_mean"] = torch.tensor(-1.5)
     w["energy_head.normalizer.bn.running_var"] = torch.tensor(2.25)
     w["energy_head.reference.linear.weight"] = -torch.rand(1, 119, generator=gen) * 10.0
+    if direct:
+        lin("forces_head.mlp.NN-0", C, He)
+        lin("forces_head.mlp.NN-1", He, 3)
+        w["forces_head.normalizer.bn.running_mean"] = torch.tensor(0.02)
+        w["forces_head.normalizer.bn.running_var"] = torch.tensor(0.64)
+        lin("stress_head.mlp.NN-0", C, He)
+        lin("stress_head.mlp.NN-1", He, 6)
+        w["stress_head.diag_normalizer.bn.running_mean"] = torch.tensor(-0.003)
+        w["stress_head.diag_normalizer.bn.running_var"] = torch.tensor(4e-4)
+        w["stress_head.offdiag_normalizer.bn.running_mean"] = torch.tensor(0.001)
+        w["stress_head.offdiag_normalizer.bn.running_var"] = torch.tensor(1e-4)
     return w
 
 

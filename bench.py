@@ -189,6 +189,28 @@ def build_c5(torch, K=256):
     return cfg, w, bg, nl_ms
 
 
+def direct_c5_ms(torch, cfg, bg, precision, steps):
+    """ms per step of a direct Orb checkpoint of the C5 architecture (same random draw plus the
+    force and stress heads) on the C5 batch: forward, ForceHead and StressHead, replayed graph."""
+    from tt_atom import orb, synthetic
+    w = synthetic.random_orb_weights(cfg, synthetic.SEEDS["C5"] + synthetic.WEIGHT_SEED_OFFSET,
+                                     direct=True)
+    mdl = orb.OrbModel(w, cfg, precision=precision)
+    graph = orb.OrbGraph(mdl.device, senders=bg.senders, receivers=bg.receivers,
+                         num_nodes=bg.pos.shape[0], atomic_numbers=bg.Z,
+                         cell_shift=bg.cell_shift, natoms=bg.natoms)
+    eng = orb.OrbEngine(mdl, graph)
+    p = bg.pos.to(mdl.device)
+    for _ in range(4):
+        eng.step(p, compute_stress=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.step(p, compute_stress=True)
+    torch.cuda.synchronize()
+    return round((time.perf_counter() - t0) * 1e3 / steps, 3)
+
+
 def device_nl_ms(torch, fn, ref):
     """Median wall time of the device neighbour list (after one warm-up call), and whether it
     reproduced the host graph ``ref`` = (edge_index, shift) exactly."""
@@ -402,7 +424,9 @@ def main():
     # secondary (C3 / C4): the step with the neighbour search in it -- device radius graph and a
     # topology comparison every step, then the replay (the topology does not change here) -- and
     # the cost of a step whose topology did change (new engine, first call launched eagerly)
-    nl_step_ms = topo_step_ms = None
+    nl_step_ms = topo_step_ms = direct_ms = None
+    if wl == "c5":
+        direct_ms = direct_c5_ms(torch, cfg, bg, args.precision, min(args.steps, 10))
     if wl in ("c3", "c4"):
         ei_dev = ei.to(dev)
 
@@ -490,6 +514,7 @@ def main():
                    "neighbor_list_device_equals_host": None if nl_dev is None else nl_dev[1],
                    "ms_per_step_with_neighbor_search": nl_step_ms,
                    "ms_per_step_after_topology_change": topo_step_ms,
+                   "direct_checkpoint_ms_per_step": direct_ms,
                    "energy": energy},
         "roofline": {"bound": "mfma", "kernel": KERNELS[dom],
                      "achieved": round(achieved, 3), "peak": round(PEAKS[dom], 2),

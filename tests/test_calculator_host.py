@@ -196,3 +196,69 @@ def test_orb_graph_topology_matches_numpy():
     with pytest.raises(ValueError, match="out of range"):
         OrbGraph("cpu", senders=torch.tensor([0]), receivers=torch.tensor([N]), num_nodes=N,
                  atomic_numbers=torch.ones(N, dtype=torch.long), natoms=natoms)
+
+
+class _Atoms:
+    """The three members of ase.Atoms the cache and the front door read."""
+
+    def __init__(self, numbers, pbc=False, info=None):
+        self.numbers, self.pbc, self.info = np.asarray(numbers), pbc, dict(info or {})
+
+    def get_atomic_numbers(self):
+        return self.numbers
+
+    def get_pbc(self):
+        return np.broadcast_to(np.asarray(self.pbc, dtype=bool), (3,))
+
+
+def test_bundle_cache_key_and_hits(tmp_path):
+    """The reference's cache naming: reduced composition (H2O == H4O2, any atom order) hashed as
+    sha1("Z:count;...")[:12]; charge, spin, task and an explicit checkpoint each change the name;
+    a hit returns the file, a miss raises with the path."""
+    import hashlib
+    import pytest
+    from tt_atom import bundle_cache as BC
+    assert BC.reduced_composition([8, 1, 1]) == ((1, 2), (8, 1))
+    assert BC.reduced_composition([1, 8, 1, 1, 8, 1]) == ((1, 2), (8, 1))
+    assert BC.composition_hash([1, 1, 8]) == hashlib.sha1(b"1:2;8:1").hexdigest()[:12]
+    p = BC.bundle_path("uma-s-1", "omol", [8, 1, 1], 0, 1, cache_dir=tmp_path)
+    assert p == tmp_path / f"uma-s-1_omol_{hashlib.sha1(b'1:2;8:1').hexdigest()[:12]}_c0_s1.npz"
+    assert p == BC.bundle_path("uma-s-1", "omol", [1, 8, 1, 1, 8, 1], 0, 1, cache_dir=tmp_path)
+    others = {BC.bundle_path("uma-s-1", "omol", [8, 1, 1], 1, 1, cache_dir=tmp_path),
+              BC.bundle_path("uma-s-1", "omol", [8, 1, 1], 0, 2, cache_dir=tmp_path),
+              BC.bundle_path("uma-s-1", "omat", [8, 1, 1], 0, 1, cache_dir=tmp_path),
+              BC.bundle_path("uma-s-1", "omol", [8, 1, 1], 0, 1, cache_dir=tmp_path,
+                             checkpoint=tmp_path / "ckpt.pt")}
+    assert p not in others and len(others) == 4
+    assert BC.infer_task(_Atoms([1], pbc=True)) == "omat"
+    assert BC.infer_task(_Atoms([1], pbc=[True, True, False])) == "omol"
+    with pytest.raises(BC.BundleNotCached, match="export_weights"):
+        BC.get_or_build(_Atoms([8, 1, 1]), cache_dir=tmp_path)
+    p.write_bytes(b"")
+    assert BC.get_or_build(_Atoms([1, 8, 1]), cache_dir=tmp_path) == p
+
+
+def test_orb_weight_cache_and_front_door(tmp_path):
+    import pytest
+    from tt_atom import auto, calculator, orb_weight_cache as OWC
+    assert OWC.weights_path("orb-v3-direct-20-omat", tmp_path) == tmp_path / "direct-20-omat.npz"
+    with pytest.raises(ValueError, match="unknown Orb checkpoint"):
+        OWC.weights_path("orb-v4", tmp_path)
+    with pytest.raises(OWC.WeightsNotCached):
+        OWC.get_or_build("orb-v3-conservative-omol", cache_dir=tmp_path)
+    assert auto._family("UMA-s-1") == "uma" and auto._family("orb-v3-direct-omol") == "orb"
+    with pytest.raises(ValueError, match="unknown model"):
+        auto.Calculator(_Atoms([1]), "mace")
+    with pytest.raises(ValueError, match="needs `atoms`"):
+        auto.Calculator(None, "uma-s-1")
+    with pytest.raises(ValueError, match="only to UMA"):
+        auto.Calculator(None, "orb-v3-direct-omol", task="omol")
+    # a cache hit reaches the calculator class (which needs ase where it is absent); charge and
+    # spin from atoms.info win and the resolved values are stamped back
+    from tt_atom import bundle_cache as BC
+    atoms = _Atoms([8, 1, 1], info={"spin": 3})
+    BC.bundle_path("uma-s-1", "omol", [8, 1, 1], 0, 3, cache_dir=tmp_path).write_bytes(b"")
+    if not calculator.HAVE_ASE:
+        with pytest.raises(ImportError, match="needs ase"):
+            auto.Calculator(atoms, "uma-s-1", cache_dir=tmp_path)
+        assert atoms.info == {"spin": 3, "charge": 0}

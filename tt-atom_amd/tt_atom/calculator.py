@@ -160,6 +160,27 @@ class TTAtomCalculator(_AseCalculator):
                                max_neighbors=max_neighbors)
         self.task = self.task_name = self.session.task
 
+    @classmethod
+    def from_uma(cls, model="uma-s-1", task_name="omol", atoms=None, charge=0, spin=1,
+                 refenv=None, checkpoint=None, cache_dir=None, device=None, device_id=0,
+                 fast=False, trace=False, **kwargs):
+        """Calculator for ``atoms`` from the composition-keyed bundle cache (calculator.py:68-110):
+        charge / spin in ``atoms.info`` win over the arguments and are stamped back onto the
+        atoms, so the bundle's merged routing and the runtime system embedding agree."""
+        from . import bundle_cache
+        if atoms is None:
+            raise ValueError("from_uma needs `atoms`: the merged bundle is chosen by the reduced "
+                             "composition, charge, spin and task")
+        charge = atoms.info.get("charge", charge)
+        spin = atoms.info.get("spin", spin)
+        atoms.info.setdefault("charge", charge)
+        atoms.info.setdefault("spin", spin)
+        path = bundle_cache.get_or_build(atoms, model=model, task=task_name, charge=charge,
+                                         spin=spin, refenv=refenv, checkpoint=checkpoint,
+                                         cache_dir=cache_dir)
+        return cls(str(path), task_name=task_name, device=device, device_id=device_id,
+                   fast=fast, trace=trace, **kwargs)
+
     def calculate(self, atoms=None, properties=("energy", "forces"),
                   system_changes=_all_changes):
         super().calculate(atoms, properties, system_changes)

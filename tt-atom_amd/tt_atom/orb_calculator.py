@@ -236,6 +236,14 @@ class OrbCalculator(_AseCalculator):
                                   precision=precision)
         self.task = self.task_name = self.session.task
 
+    @classmethod
+    def from_checkpoint(cls, checkpoint="orb-v3-conservative-inf-omat", refenv=None,
+                        cache_dir=None, device=None, device_id=0, fast=False, **kwargs):
+        """Calculator from the per-checkpoint weight cache (orb_calculator.py:75-86)."""
+        from . import orb_weight_cache
+        path = orb_weight_cache.get_or_build(checkpoint, refenv=refenv, cache_dir=cache_dir)
+        return cls(str(path), device=device, device_id=device_id, fast=fast, **kwargs)
+
     def calculate(self, atoms=None, properties=("energy", "forces"),
                   system_changes=_all_changes):
         super().calculate(atoms, properties, system_changes)

@@ -389,9 +389,9 @@ def test_gate_fwd_bwd(nat, natural):
     assert torch.equal(gcomb[:, 2 * H:].reshape(R, 9, H), gxo) and torch.equal(gcomb[:, :2 * H], ggo)
 
 
-@pytest.mark.parametrize("n", [16, 128, 200, 512])
+@pytest.mark.parametrize("n", [16, 64, 100, 128, 200, 512])
 def test_ln_silu_fwd_bwd(nat, n):
-    R = 300
+    R = 301                     # odd: the last two-row wavefront of short rows has one row
     g = torch.Generator().manual_seed(n)
     a = torch.randn(R, n, generator=g, dtype=torch.float64) * 2 + 0.5
     gam = 1 + 0.1 * torch.randn(n, generator=g, dtype=torch.float64)
@@ -421,9 +421,16 @@ def test_ln_silu_fwd_bwd(nat, n):
     torch.cuda.synchronize()
     assert torch.equal(so2, so) and torch.equal(gw[:, n:2 * n], gao)
     assert gw[:, :n].abs().max() == 0 and gw[:, 2 * n:].abs().max() == 0
+    # nothing is written past row R - 1
+    nb, sb, gb = (torch.full((R + 1, n), float("nan"), device=DEV) for _ in range(3))
+    nat.ln_silu_fwd(f(a), f(gam), f(bet), nb[:R], sb[:R], R=R, n=n)
+    nat.ln_silu_bwd(f(gs), f(a), no, f(gam), gb[:R], R=R, n=n)
+    torch.cuda.synchronize()
+    assert torch.equal(nb[:R], no) and torch.equal(sb[:R], so) and torch.equal(gb[:R], gao)
+    assert all(bool(t[R].isnan().all()) for t in (nb, sb, gb))
 
 
-@pytest.mark.parametrize("C", [16, 128, 96])
+@pytest.mark.parametrize("C", [16, 128, 96, 256, 300])
 def test_rmsnorm_sh_fwd_bwd(nat, C):
     from oracle.uma import rms_norm_sh
     N = 60

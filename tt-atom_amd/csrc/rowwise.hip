@@ -62,42 +62,48 @@ __global__ __launch_bounds__(256) void k_gate_bwd(const float* __restrict__ g_y,
 }
 
 // ------------------------------------------------------------------ LayerNorm + SiLU (radial MLP)
-// One wave per row; the row stays in registers (element lane + 64 k in slot k, NPL = ceil(n / 64)
-// slots) so that each operand crosses HBM once.  The per-lane partial sums run over k in order, as
-// a strided loop would.  Forward (so2.py:101-115 / geometry.py:161-168):
+// G lanes per row (64, or 32 for rows of at most 128 so that a wavefront holds two rows and twice
+// the bytes are in flight per wave); the row stays in registers (element lane + G k in slot k,
+// NPL slots) so that each operand crosses HBM once.  The per-lane partial sums run over k in
+// order.  A row index past R (the odd tail of a two-row wavefront) reads row R - 1 and stores
+// nothing, so every lane of the wave takes part in the butterflies.  Forward (so2.py:101-115 /
+// geometry.py:161-168):
 //   nrm = (a - mean) * rstd * gamma + beta,  s = silu(nrm)
 // a and nrm rows have stride lda, s rows stride lds.
-template <int NPL>
+template <int G, int NPL>
 __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a,
                                                      const float* __restrict__ gamma,
                                                      const float* __restrict__ beta,
                                                      float* __restrict__ nrm,
                                                      float* __restrict__ s, int64_t R, int n,
                                                      int64_t lda, int64_t lds, float eps) {
-  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int lane = threadIdx.x & 63;
-  if (row >= R) return;
+  const int64_t rw = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / G;
+  const int lane = threadIdx.x & (G - 1);
+  if ((rw / (64 / G)) * (64 / G) >= R) return;  // whole wavefront past the end
+  const bool valid = rw < R;
+  const int64_t row = valid ? rw : R - 1;
   const float* ar = a + row * lda;
   float v[NPL];
   float sum = 0.f;
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
-    const int i = lane + 64 * k;
+    const int i = lane + G * k;
     v[k] = i < n ? ar[i] : 0.f;
     sum += v[k];
   }
-  const float mean = tta_group_sum(sum, 64) / n;
+  const float mean = tta_group_sum(sum, G) / n;
   float sq = 0.f;
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
     const float d = v[k] - mean;
-    if (lane + 64 * k < n) sq += d * d;
+    if (lane + G * k < n) sq += d * d;
   }
-  const float var = tta_group_sum(sq, 64) / n;
+  const float var = tta_group_sum(sq, G) / n;
   const float rstd = 1.0f / sqrtf(var + eps);
+  if (!valid) return;
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
-    const int i = lane + 64 * k;
+    const int i = lane + G * k;
     if (i >= n) continue;
     const float y = (v[k] - mean) * rstd * gamma[i] + beta[i];
     nrm[row * lda + i] = y;
@@ -108,8 +114,8 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
 // Backward of silu(layer_norm(a)) w.r.t. a (so2.py:117-143):
 //   gy = g * silu'(nrm) * gamma;  xhat = (a - mean) * rstd;
 //   g_a = rstd * (gy - mean(gy) - xhat * mean(gy * xhat))
-// g rows stride ldg, a / nrm rows stride lda, g_a rows stride ldo.
-template <int NPL>
+// g rows stride ldg, a / nrm rows stride lda, g_a rows stride ldo.  Same lane layout as above.
+template <int G, int NPL>
 __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g,
                                                      const float* __restrict__ a,
                                                      const float* __restrict__ nrm,
@@ -117,39 +123,42 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
                                                      float* __restrict__ g_a, int64_t R, int n,
                                                      int64_t ldg, int64_t lda, int64_t ldo,
                                                      float eps) {
-  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int lane = threadIdx.x & 63;
-  if (row >= R) return;
+  const int64_t rw = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / G;
+  const int lane = threadIdx.x & (G - 1);
+  if ((rw / (64 / G)) * (64 / G) >= R) return;
+  const bool valid = rw < R;
+  const int64_t row = valid ? rw : R - 1;
   const float* ar = a + row * lda;
   float av[NPL], gy[NPL];
   float sum = 0.f;
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
-    const int i = lane + 64 * k;
+    const int i = lane + G * k;
     const bool in = i < n;
     av[k] = in ? ar[i] : 0.f;
     gy[k] = in ? g[row * ldg + i] * tta_silu_grad(nrm[row * lda + i]) * gamma[i] : 0.f;
     sum += av[k];
   }
-  const float mean = tta_group_sum(sum, 64) / n;
+  const float mean = tta_group_sum(sum, G) / n;
   float sq = 0.f;
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
     const float d = av[k] - mean;
-    if (lane + 64 * k < n) sq += d * d;
+    if (lane + G * k < n) sq += d * d;
   }
-  const float rstd = 1.0f / sqrtf(tta_group_sum(sq, 64) / n + eps);
+  const float rstd = 1.0f / sqrtf(tta_group_sum(sq, G) / n + eps);
   float m1 = 0.f, m2 = 0.f;
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
     m1 += gy[k];
     m2 += gy[k] * ((av[k] - mean) * rstd);
   }
-  m1 = tta_group_sum(m1, 64) / n;
-  m2 = tta_group_sum(m2, 64) / n;
+  m1 = tta_group_sum(m1, G) / n;
+  m2 = tta_group_sum(m2, G) / n;
+  if (!valid) return;
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
-    const int i = lane + 64 * k;
+    const int i = lane + G * k;
     if (i >= n) continue;
     const float xh = (av[k] - mean) * rstd;
     g_a[row * ldo + i] = rstd * (gy[k] - m1 - xh * m2);
@@ -205,6 +214,80 @@ __global__ __launch_bounds__(256) void k_rmsnorm_sh_fwd(const float* __restrict_
         if (add0) o = o + add0[n * C + c];
       }
       yn[j * C + c] = o;
+    }
+  }
+}
+
+// Register-resident form of the RMSNormSH backward for C <= 64 NPL: each lane loads its NPL
+// channels of all 9 coefficient rows of g and x (and of the 3 degree weights) once and every pass
+// works from registers, so a node costs one memory round trip instead of one per pass (C3: 15 vs
+// 26 us per launch).  The sums run in the same order as the loop form (channel blocks k = 0.. in
+// turn, coefficients inside).  The forward keeps its loop form, which measured faster (7.2 vs
+// 8.6 us): its re-reads of the row hit in cache.
+template <int NPL>
+__global__ __launch_bounds__(256) void k_rmsnorm_sh_bwd_r(const float* __restrict__ g,
+                                                          const float* __restrict__ x,
+                                                          const float* __restrict__ aw,
+                                                          const float* __restrict__ inv_in,
+                                                          const float* __restrict__ res,
+                                                          float* __restrict__ out, int64_t N,
+                                                          int C) {
+  const int64_t n = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;
+  const float* xn = x + n * 9 * C;
+  const float* gn = g + n * 9 * C;
+  float xv[9][NPL], gv[9][NPL], wv[3][NPL];
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const int c = lane + 64 * k;
+    const bool in = c < C;
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      xv[j][k] = in ? xn[j * C + c] : 0.f;
+      gv[j][k] = in ? gn[j * C + c] : 0.f;
+    }
+#pragma unroll
+    for (int l = 0; l < 3; ++l) wv[l][k] = in ? aw[l * C + c] : 0.f;
+  }
+  const float inv = inv_in[n];
+  float s0 = 0.f;
+#pragma unroll
+  for (int k = 0; k < NPL; ++k)
+    if (lane + 64 * k < C) s0 += xv[0][k];
+  const float mu = tta_group_sum(s0, 64) / C;
+  float ginv = 0.f;
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    if (lane + 64 * k >= C) continue;
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      const float v = j == 0 ? xv[0][k] - mu : xv[j][k];
+      ginv += gv[j][k] * v * wv[deg_of(j)][k];
+    }
+  }
+  ginv = tta_group_sum(ginv, 64);
+  const float gms = ginv * (inv * inv * inv) * -0.5f;
+  float s1 = 0.f;
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    if (lane + 64 * k >= C) continue;
+    const float v = xv[0][k] - mu;
+    s1 += gv[0][k] * (inv * wv[0][k]) + v * bdw_of(0) * gms * (2.0f / C);
+  }
+  const float m0 = tta_group_sum(s1, 64) / C;
+  float* on = out + n * 9 * C;
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const int c = lane + 64 * k;
+    if (c >= C) continue;
+#pragma unroll
+    for (int j = 0; j < 9; ++j) {
+      const float v = j == 0 ? xv[0][k] - mu : xv[j][k];
+      float gx = gv[j][k] * (inv * wv[deg_of(j)][k]) + v * bdw_of(j) * gms * (2.0f / C);
+      if (j == 0) gx -= m0;
+      if (res) gx += res[n * 9 * C + j * C + c];
+      on[j * C + c] = gx;
     }
   }
 }
@@ -333,19 +416,20 @@ extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* 
                 "tta_ln_silu_fwd: bad sizes (row width 1..512)");
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(a && gamma && beta && nrm && s, "tta_ln_silu_fwd: null pointer");
-  const dim3 grid(tta_blocks(R * 64, 256));
-  if (n <= 64)
-    hipLaunchKernelGGL(k_ln_silu_fwd<1>, grid, dim3(256), 0, stream, a, gamma, beta, nrm, s, R,
-                       (int)n, lda, lds, eps);
+#define TTA_LN_FWD(G, NPL)                                                                  \
+  hipLaunchKernelGGL((k_ln_silu_fwd<G, NPL>), dim3(tta_blocks(R * G, 256)), dim3(256), 0, stream, \
+                     a, gamma, beta, nrm, s, R, (int)n, lda, lds, eps)
+  if (n <= 32)
+    TTA_LN_FWD(32, 1);
+  else if (n <= 64)
+    TTA_LN_FWD(32, 2);
   else if (n <= 128)
-    hipLaunchKernelGGL(k_ln_silu_fwd<2>, grid, dim3(256), 0, stream, a, gamma, beta, nrm, s, R,
-                       (int)n, lda, lds, eps);
+    TTA_LN_FWD(32, 4);
   else if (n <= 256)
-    hipLaunchKernelGGL(k_ln_silu_fwd<4>, grid, dim3(256), 0, stream, a, gamma, beta, nrm, s, R,
-                       (int)n, lda, lds, eps);
+    TTA_LN_FWD(64, 4);
   else
-    hipLaunchKernelGGL(k_ln_silu_fwd<8>, grid, dim3(256), 0, stream, a, gamma, beta, nrm, s, R,
-                       (int)n, lda, lds, eps);
+    TTA_LN_FWD(64, 8);
+#undef TTA_LN_FWD
   TTA_CHECK_LAUNCH("tta_ln_silu_fwd");
   return tta::kOk;
 }
@@ -357,19 +441,20 @@ extern "C" int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm,
                 "tta_ln_silu_bwd: bad sizes (row width 1..512)");
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(g && a && nrm && gamma && g_a, "tta_ln_silu_bwd: null pointer");
-  const dim3 grid(tta_blocks(R * 64, 256));
-  if (n <= 64)
-    hipLaunchKernelGGL(k_ln_silu_bwd<1>, grid, dim3(256), 0, stream, g, a, nrm, gamma, g_a, R,
-                       (int)n, ldg, lda, ldo, eps);
+#define TTA_LN_BWD(G, NPL)                                                                  \
+  hipLaunchKernelGGL((k_ln_silu_bwd<G, NPL>), dim3(tta_blocks(R * G, 256)), dim3(256), 0, stream, \
+                     g, a, nrm, gamma, g_a, R, (int)n, ldg, lda, ldo, eps)
+  if (n <= 32)
+    TTA_LN_BWD(32, 1);
+  else if (n <= 64)
+    TTA_LN_BWD(32, 2);
   else if (n <= 128)
-    hipLaunchKernelGGL(k_ln_silu_bwd<2>, grid, dim3(256), 0, stream, g, a, nrm, gamma, g_a, R,
-                       (int)n, ldg, lda, ldo, eps);
+    TTA_LN_BWD(32, 4);
   else if (n <= 256)
-    hipLaunchKernelGGL(k_ln_silu_bwd<4>, grid, dim3(256), 0, stream, g, a, nrm, gamma, g_a, R,
-                       (int)n, ldg, lda, ldo, eps);
+    TTA_LN_BWD(64, 4);
   else
-    hipLaunchKernelGGL(k_ln_silu_bwd<8>, grid, dim3(256), 0, stream, g, a, nrm, gamma, g_a, R,
-                       (int)n, ldg, lda, ldo, eps);
+    TTA_LN_BWD(64, 8);
+#undef TTA_LN_BWD
   TTA_CHECK_LAUNCH("tta_ln_silu_bwd");
   return tta::kOk;
 }
@@ -392,8 +477,19 @@ extern "C" int tta_rmsnorm_sh_bwd(const float* g, const float* x, const float* a
   TTA_CHECK_ARG(N >= 0 && C > 0, "tta_rmsnorm_sh_bwd: bad sizes");
   if (N == 0) return tta::kOk;
   TTA_CHECK_ARG(g && x && aw && inv && out, "tta_rmsnorm_sh_bwd: null pointer");
-  hipLaunchKernelGGL(k_rmsnorm_sh_bwd, dim3(tta_blocks(N * 64, 256)), dim3(256), 0, stream, g, x,
-                     aw, inv, res, out, N, (int)C);
+  const dim3 grid(tta_blocks(N * 64, 256));
+  if (C <= 64)
+    hipLaunchKernelGGL(k_rmsnorm_sh_bwd_r<1>, grid, dim3(256), 0, stream, g, x, aw, inv, res, out,
+                       N, (int)C);
+  else if (C <= 128)
+    hipLaunchKernelGGL(k_rmsnorm_sh_bwd_r<2>, grid, dim3(256), 0, stream, g, x, aw, inv, res, out,
+                       N, (int)C);
+  else if (C <= 256)
+    hipLaunchKernelGGL(k_rmsnorm_sh_bwd_r<4>, grid, dim3(256), 0, stream, g, x, aw, inv, res, out,
+                       N, (int)C);
+  else
+    hipLaunchKernelGGL(k_rmsnorm_sh_bwd, grid, dim3(256), 0, stream, g, x, aw, inv, res, out, N,
+                       (int)C);
   TTA_CHECK_LAUNCH("tta_rmsnorm_sh_bwd");
   return tta::kOk;
 }

@@ -103,11 +103,13 @@ def test_gemm_batched_strided(nat):
     assert (out.cpu().double() - ref).abs().max() < 1e-4
 
 
-@pytest.mark.parametrize("M,N,K", [(4100, 200, 196), (8192, 640, 768), (5000, 16, 1000)])
+@pytest.mark.parametrize("M,N,K", [(4100, 200, 196), (8192, 640, 768), (5000, 16, 1000),
+                                   (40001, 1100, 128), (9000, 300, 36)])
 @pytest.mark.parametrize("epi", [0, 2, 3, 4])
 def test_split_bf16_gemm_fp32_accuracy(nat, M, N, K, epi):
     """Mode 6 (three bf16 planes, six products) has the accuracy of an fp32 GEMM: its error
-    relative to |A| |B| stays within the fp32 kernel's, on ragged M / N / K tails too."""
+    relative to |A| |B| stays within the fp32 kernel's, on ragged M / N / K tails too, and with
+    thousands of tiles (40001 x 1100: 313 x 9 tiles of 128 x 128)."""
     g = torch.Generator().manual_seed(M + N + K)
     A = torch.randn(M, K, generator=g)
     B = torch.randn(K, N, generator=g) / math.sqrt(K)

@@ -394,3 +394,27 @@ def test_segment_center(nat):
         xi = x.cuda()
         nat.segment_center(xi, ptr.cuda(), xi)                  # in place
         assert torch.equal(xi, out)
+
+
+def test_orb_c5_full_batch_translation(nat):
+    """The full C5 batch: translating every molecule by its own vector leaves every energy and
+    force unchanged (fp32 resolution) and each molecule's forces sum to zero."""
+    cfg = dict(S.CFG_ORB_C5)
+    w = S.random_orb_weights(cfg, S.SEEDS["C5"] + S.WEIGHT_SEED_OFFSET)
+    bg = orb.assemble_orb(S.c5_systems(), cfg["cutoff"], cfg["max_num_neighbors"])
+    model = orb.OrbModel(w, cfg)
+    graph = orb.OrbGraph(model.device, senders=bg.senders, receivers=bg.receivers,
+                         num_nodes=bg.pos.shape[0], atomic_numbers=bg.Z, cell_shift=bg.cell_shift,
+                         natoms=bg.natoms)
+    eng = orb.OrbEngine(model, graph, use_graph=False)
+    raw0, F0, _ = eng.run(bg.pos.to(model.device))
+    F0 = F0.cpu().double()
+    g = torch.Generator().manual_seed(8)
+    shift = (torch.rand(bg.K, 3, generator=g, dtype=torch.float64) - 0.5) * 20.0
+    batch = bg.batch.long()
+    raw1, F1, _ = eng.run((bg.pos.double() + shift[batch]).float().to(model.device))
+    F1 = F1.cpu().double()
+    assert (raw1 - raw0).abs().max() <= 2e-6 * max(1.0, float(raw0.abs().max()))
+    assert (F1 - F0).abs().max() <= 1e-4 * max(1.0, float(F0.abs().max()))
+    sums = torch.zeros(bg.K, 3, dtype=torch.float64).index_add_(0, batch, F0)
+    assert sums.abs().max() <= 1e-4 * max(1.0, float(F0.abs().max()))

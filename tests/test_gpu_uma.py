@@ -184,3 +184,35 @@ def test_c4_full_size_stress():
                              max_neighbors=cfg["max_neighbors"])
     _check(w, cfg, host, pos, Z, ei, _system_embedding(w, cfg, len(Z)), shift, cell=cell,
            label="C4-2048")
+
+
+def test_c3_full_size_rotation_translation():
+    """Size-independent properties at the headline size: on the same topology, a global rotation
+    leaves the energy unchanged and rotates the forces, a translation changes nothing, and the
+    forces sum to zero (to fp32 resolution of 2048 forces)."""
+    from tt_atom import synthetic
+    from tt_atom.geometry import radius_graph
+    cfg = dict(synthetic.CFG_UMA_S)
+    w, host = synthetic.random_uma_bundle(cfg, synthetic.SEEDS["C3"] + 100)
+    pos, Z = synthetic.c3_system()
+    pos, Z = torch.from_numpy(pos), torch.from_numpy(Z)
+    ei, _ = radius_graph(pos, cfg["cutoff"], max_neighbors=cfg["max_neighbors"])
+    eng = _engine(w, cfg, host, Z, ei, _system_embedding(w, cfg, len(Z)))
+    E0, F0 = eng(pos.cuda())
+    F0 = F0.cpu().double()
+    q, _ = torch.linalg.qr(torch.randn(3, 3, dtype=torch.float64,
+                                       generator=torch.Generator().manual_seed(5)))
+    if torch.det(q) < 0:
+        q[:, 0] = -q[:, 0]
+    E1, F1 = eng((pos.double() @ q.T).float().cuda())
+    E2, F2 = eng((pos.double() + torch.tensor([3.1, -7.7, 11.3], dtype=torch.float64))
+                 .float().cuda())
+    F1, F2 = F1.cpu().double(), F2.cpu().double()
+    fmax = float(F0.abs().max())
+    print(f"C3-2048 rotation: dE={abs(E1 - E0):.2e} (E={E0:.5f}) max|dF|="
+          f"{float((F1 - F0 @ q.T).abs().max()):.2e} (|F|max={fmax:.2f}); translation: "
+          f"dE={abs(E2 - E0):.2e} max|dF|={float((F2 - F0).abs().max()):.2e}; "
+          f"|sum F|={float(F0.sum(0).abs().max()):.2e}", flush=True)
+    assert abs(E1 - E0) <= 2e-6 * abs(E0) and abs(E2 - E0) <= 2e-6 * abs(E0)
+    assert (F1 - F0 @ q.T).abs().max() <= 1e-4 and (F2 - F0).abs().max() <= 1e-4
+    assert F0.sum(0).abs().max() <= 1e-3

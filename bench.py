@@ -307,6 +307,11 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="launch the step kernel by kernel instead of replaying its HIP graph "
                          "(for profilers)")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the secondary measurements (device neighbour list, the step with the "
+                         "neighbour search, the step after a topology change, the direct Orb "
+                         "checkpoint), so that a profiler sees only the warm-up, timed and probed "
+                         "steps")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (y = -x) for the HBM counter scale")
     args = ap.parse_args()
@@ -357,9 +362,10 @@ def main():
         geo = geometry.HostGeometry(w, cfg, host["to_m"], host["gauss_offset"],
                                     host["gauss_coeff"], device=dev)
         eng = trace.TracedEngine(bb, geo, Z, ei, se, edge_cell_shift=shift)
-        nl_dev = device_nl_ms(torch, lambda: geometry.radius_graph_device(
-            pos, cfg["cutoff"], cell, None if cell is None else [True] * 3,
-            max_neighbors=cfg["max_neighbors"]),
+        nl_dev = None if args.no_secondary else device_nl_ms(
+            torch, lambda: geometry.radius_graph_device(
+                pos, cfg["cutoff"], cell, None if cell is None else [True] * 3,
+                max_neighbors=cfg["max_neighbors"]),
             (ei, shift if shift is not None else torch.zeros(ei.shape[1], 3)))
         pos_d = pos.to(dev)
         stress = wl == "c4"
@@ -379,9 +385,9 @@ def main():
         from tt_atom import synthetic as syn
         systems = syn.c5_systems(K=256)
         ref_bg = bg
-        nl_dev = device_nl_ms(torch, lambda: (lambda g: (torch.stack([g.receivers, g.senders]),
-                                                         g.cell_shift))(
-            orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"], "device")),
+        nl_dev = None if args.no_secondary else device_nl_ms(
+            torch, lambda: (lambda g: (torch.stack([g.receivers, g.senders]), g.cell_shift))(
+                orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"], "device")),
             (torch.stack([ref_bg.receivers, ref_bg.senders]), ref_bg.cell_shift))
         pos_d = bg.pos.to(mdl.device)
 
@@ -425,9 +431,9 @@ def main():
     # topology comparison every step, then the replay (the topology does not change here) -- and
     # the cost of a step whose topology did change (new engine, first call launched eagerly)
     nl_step_ms = topo_step_ms = direct_ms = None
-    if wl == "c5":
+    if wl == "c5" and not args.no_secondary:
         direct_ms = direct_c5_ms(torch, cfg, bg, args.precision, min(args.steps, 10))
-    if wl in ("c3", "c4"):
+    if wl in ("c3", "c4") and not args.no_secondary:
         ei_dev = ei.to(dev)
 
         def nl_step():

@@ -189,6 +189,103 @@ def build_c5(torch, K=256):
     return cfg, w, bg, nl_ms
 
 
+# Published small-batch throughputs of the reference (p150a card, bf16; docs/perf_baselines.json,
+# CHANGELOG.md:79-85): evaluate_batch end to end, systems per second.
+PUBLISHED_BATCH = {"uma-s-1 omol K=8 ethanol": 111.06617871436099,
+                   "orb-v3-conservative-omol K=8 ethanol": 463.91522419389514,
+                   "orb-v3-conservative-inf-omat K=8 Si 2x1x1": 374.4622548238998,
+                   "orb-v3-conservative-omol K=128 ethanol": 1338.0,
+                   "orb-v3-direct-omol K=128 ethanol": 2056.0}
+# covalent radii (A) of the elements in these inputs, for the Orb ZBL term (ASE's table has the
+# same values; ase is not installed here)
+_RADII = {1: 0.31, 6: 0.76, 7: 0.71, 8: 0.66, 14: 1.11}
+
+
+def run_batch_workload(args, torch):
+    """Small-system throughput, as the reference's release gate measures it: K systems per
+    evaluate_batch call (host neighbour lists and assembly, the device step, the host readout
+    with normalisers and ZBL), median of 5 calls after 2 warm-up calls."""
+    import tempfile
+    import numpy as np
+    from tt_atom import calculator, orb, orb_calculator, synthetic, weights
+    td = pathlib.Path(tempfile.mkdtemp())
+    radii = np.ones(120)
+    for z, r in _RADII.items():
+        radii[z] = r
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        ts = []
+        for _ in range(5):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2]
+
+    res = {}
+    cfg = dict(synthetic.CFG_UMA_S)
+    w, host = synthetic.random_uma_bundle(cfg, synthetic.SEEDS["C3"] + synthetic.WEIGHT_SEED_OFFSET)
+    weights.save_bundle(td / "uma.npz", cfg, w, host)
+    uma = calculator.Session(str(td / "uma.npz"), precision=args.precision)
+    eth8 = synthetic.ethanol_batch(8)
+    t = timed(lambda: uma.evaluate_batch(eth8))
+    res["uma-s-1 omol K=8 ethanol"] = (8 / t, t * 1e3)
+
+    def orb_session(name, direct, cond, cap):
+        c = dict(synthetic.CFG_ORB_C5, has_charge_spin_cond=cond, max_num_neighbors=cap,
+                 task="omol" if cond else "omat")
+        ow = synthetic.random_orb_weights(c, synthetic.SEEDS["C5"] + synthetic.WEIGHT_SEED_OFFSET,
+                                          direct=direct)
+        orb.save_orb_bundle(td / f"{name}.npz", c, ow)
+        return orb_calculator.OrbSession(str(td / f"{name}.npz"), precision=args.precision,
+                                         covalent_radii=radii)
+
+    cons_omol = orb_session("cons_omol", False, True, 120)
+    t = timed(lambda: cons_omol.evaluate_batch(eth8))
+    res["orb-v3-conservative-omol K=8 ethanol"] = (8 / t, t * 1e3)
+    si8 = synthetic.si_batch(8)
+    cons_omat = orb_session("cons_omat", False, False, 1 << 20)
+    t = timed(lambda: cons_omat.evaluate_batch(si8))
+    res["orb-v3-conservative-inf-omat K=8 Si 2x1x1"] = (8 / t, t * 1e3)
+    eth128 = synthetic.ethanol_batch(128)
+    t = timed(lambda: cons_omol.evaluate_batch(eth128))
+    res["orb-v3-conservative-omol K=128 ethanol"] = (128 / t, t * 1e3)
+    dir_omol = orb_session("dir_omol", True, True, 120)
+    t = timed(lambda: dir_omol.evaluate_batch(eth128))
+    res["orb-v3-direct-omol K=128 ethanol"] = (128 / t, t * 1e3)
+
+    head = "uma-s-1 omol K=8 ethanol"
+    out = {
+        "metric": "systems/s, evaluate_batch end to end (K=8 rattled ethanol, uma-s-1 "
+                  "architecture, energy + forces)",
+        "value": round(res[head][0], 2),
+        "unit": "systems/s",
+        "n_gpus": 1,
+        "steps": 5,
+        "warmup": 2,
+        "ms_per_step": round(res[head][1], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(res[head][0] / PUBLISHED_BATCH[head], 2),
+        "dtype": "bf16" if args.precision == "bf16" else "f32",
+        "data": "synthetic: random-init weights of the named architectures; rattled CH3CH2OH "
+                "(G2) and diamond Si 2x1x1 as the reference's release gate builds them",
+        "config": {"workload": "small-system batches (reference docs/perf_baselines.json)",
+                   "precision": args.precision,
+                   "batches": {k: {"systems_per_s": round(v[0], 1),
+                                   "ms_per_call": round(v[1], 3),
+                                   "published_systems_per_s_p150a": PUBLISHED_BATCH[k],
+                                   "ratio": round(v[0] / PUBLISHED_BATCH[k], 2)}
+                               for k, v in res.items()}},
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def direct_c5_ms(torch, cfg, bg, precision, steps):
     """ms per step of a direct Orb checkpoint of the C5 architecture (same random draw plus the
     force and stress heads) on the C5 batch: forward, ForceHead and StressHead, replayed graph."""
@@ -298,9 +395,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c3",
-                    help="c3 (headline), c2 (isolated edgewise kernel), c4 (periodic + stress) "
-                         "or c5 (Orb-v3 batch)")
+    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "batch"), default="c3",
+                    help="c3 (headline), c2 (isolated edgewise kernel), c4 (periodic + stress), "
+                         "c5 (Orb-v3 batch) or batch (small-system evaluate_batch throughput "
+                         "against the reference's published numbers)")
     ap.add_argument("--precision", choices=("f32", "f32-mfma", "bf16"), default="f32",
                     help="GEMM arithmetic: f32 (split-bf16, fp32-accurate), f32-mfma, or bf16 "
                          "operands (the bf16 variants of C2 / C5)")
@@ -333,6 +431,9 @@ def main():
     from tt_atom import _native
 
     wl = args.workload
+    if wl == "batch":
+        run_batch_workload(args, torch)
+        return
     if wl == "c2":
         from tt_atom.edgewise import EdgewiseStep
         ei, vec, x, g, w, jd = build_c2(torch)

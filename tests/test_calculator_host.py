@@ -262,3 +262,42 @@ def test_orb_weight_cache_and_front_door(tmp_path):
         with pytest.raises(ImportError, match="needs ase"):
             auto.Calculator(atoms, "uma-s-1", cache_dir=tmp_path)
         assert atoms.info == {"spin": 3, "charge": 0}
+
+
+def test_orb_batched_host_terms_equal_per_system():
+    """The vectorised host pieces of OrbSession.evaluate_batch against their one-system forms:
+    the conditioning embedding bit for bit, the union ZBL energies / forces (mean and sum
+    aggregation) and the batched energy normaliser to fp64 rounding."""
+    from oracle import orb as O
+    from tt_atom import orb, orb_calculator as OC
+    cfg = dict(synthetic.CFG_ORB_TINY, has_charge_spin_cond=True)
+    w = synthetic.random_orb_weights(cfg, 3)
+    charges, spins, natoms = [0.0, 1.0, -2.0], [1.0, 0.0, 3.0], [4, 2, 5]
+    emb = orb.charge_spin_embedding_batch(w, cfg["latent_dim"], charges, spins, natoms)
+    ref = torch.cat([O.charge_spin_embedding(w, q, s, n) for q, s, n in zip(charges, spins,
+                                                                             natoms)])
+    assert torch.equal(emb, ref)
+    systems = synthetic.ethanol_batch(3) + synthetic.si_batch(2)
+    bg = orb.assemble_orb(systems, 6.0, 120)
+    radii = np.full(120, 0.9)
+    batch = bg.batch.long()
+    for agg in ("mean", "sum"):
+        e, f = OC.zbl_batch(bg.Z, bg.senders, bg.receivers, bg.pos, bg.cell_shift, batch,
+                            bg.natoms, radii, agg)
+        off = 0
+        for k, n in enumerate(bg.natoms):
+            m = (bg.senders >= off) & (bg.senders < off + n)
+            ek, fk, _ = OC.zbl_energy_forces_stress(bg.Z[off:off + n], bg.senders[m] - off,
+                                                    bg.receivers[m] - off, bg.pos[off:off + n],
+                                                    bg.cell_shift[m], radii, aggregation=agg)
+            assert abs(e[k] - ek) <= 1e-12 * max(1.0, abs(ek))
+            assert np.abs(f[off:off + n] - fk).max() <= 1e-10
+            off += n
+        assert np.abs(e).max() > 0
+    raw = torch.tensor([0.3, -1.2, 0.7, 2.0, -0.4], dtype=torch.float64)
+    eb = orb.denormalize_energy_batch(raw, bg.Z, batch, bg.natoms, w)
+    off = 0
+    for k, n in enumerate(bg.natoms):
+        e1 = orb.denormalize_energy(raw[k], bg.Z[off:off + n], n, w)
+        assert abs(float(eb[k]) - float(e1)) <= 1e-12 * max(1.0, abs(float(e1)))
+        off += n

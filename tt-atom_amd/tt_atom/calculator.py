@@ -38,7 +38,7 @@ class Session:
     """One bundle on one GPU; evaluates systems given as arrays."""
 
     def __init__(self, bundle, task_name=None, device=None, gamma=0.0, max_neighbors=None,
-                 neighbor_list="device"):
+                 neighbor_list="device", precision="f32"):
         if neighbor_list not in ("host", "device"):
             raise ValueError("neighbor_list must be 'host' or 'device'")
         self.neighbor_list = neighbor_list
@@ -55,7 +55,7 @@ class Session:
         self._w = w
         self.C = self.cfg["sphere_channels"]
         self.backbone = model.Backbone(w, self.device, self.cfg, bundle.to_grid_mat,
-                                       bundle.from_grid_mat)
+                                       bundle.from_grid_mat, precision=precision)
         self.geo = geometry.HostGeometry(w, self.cfg, bundle.to_m, bundle.gauss_offset,
                                          bundle.gauss_coeff, gamma=gamma,
                                          coefficient_index=bundle.coefficient_index,

@@ -295,6 +295,10 @@ class OrbModel:
                                                                    "stress_head.offdiag_normalizer",
                                                                    "conditioner."))}
 
+    def charge_spin_embedding_batch(self, charges, spins, natoms):
+        """charge_spin_embedding of K systems at once, one row per node [sum natoms, C]."""
+        return charge_spin_embedding_batch(self.host_w, self.C, charges, spins, natoms)
+
     def charge_spin_embedding(self, charge, spin, n):
         """sin/cos charge/spin conditioning broadcast to n nodes (orb_model.py:32-56)."""
         def emb(value, W, is_spin):
@@ -306,6 +310,23 @@ class OrbModel:
         if c.shape[0] != self.C:
             raise RuntimeError("conditioning width does not match latent_dim")
         return c[None].expand(n, -1)
+
+
+def charge_spin_embedding_batch(w, C, charges, spins, natoms):
+    """sin/cos charge / spin conditioning (orb_model.py:32-56) of K systems at once: the same
+    fp32 operations as the one-system form on [K, C/4] blocks, repeated over each system's
+    nodes -> [sum natoms, C]; a zero spin gives a zero spin block."""
+    Wc = torch.as_tensor(w["conditioner.charge_embedding.W"], dtype=torch.float32)
+    Ws = torch.as_tensor(w["conditioner.spin_embedding.W"], dtype=torch.float32)
+    q = torch.as_tensor(charges, dtype=torch.float32).reshape(-1, 1)
+    sp = torch.as_tensor(spins, dtype=torch.float32).reshape(-1, 1)
+    pc = q * Wc[None] * (2.0 * math.pi)
+    ps = sp * Ws[None] * (2.0 * math.pi)
+    es = torch.cat([torch.sin(ps), torch.cos(ps)], 1) * (sp != 0).to(torch.float32)
+    c = torch.cat([torch.sin(pc), torch.cos(pc), es], 1)
+    if c.shape[1] != C:
+        raise RuntimeError("conditioning width does not match latent_dim")
+    return c.repeat_interleave(torch.as_tensor(natoms, dtype=torch.long), dim=0)
 
 
 # ----------------------------------------------------------------------------- engine
@@ -536,6 +557,17 @@ def denormalize_energy(raw, Z, n, w):
     mu = w["energy_head.normalizer.bn.running_mean"].double()
     ref = w["energy_head.reference.linear.weight"].double().reshape(-1)
     return (torch.as_tensor(raw).double() * sigma + mu) * n + ref[torch.as_tensor(Z).long()].sum()
+
+
+def denormalize_energy_batch(raw, Z, batch, natoms, w):
+    """denormalize_energy of K systems at once: raw [K] -> [K] (fp64)."""
+    sigma = w["energy_head.normalizer.bn.running_var"].double().sqrt()
+    mu = w["energy_head.normalizer.bn.running_mean"].double()
+    ref = w["energy_head.reference.linear.weight"].double().reshape(-1)
+    refs = torch.zeros(len(natoms), dtype=torch.float64).index_add_(
+        0, torch.as_tensor(batch).long(), ref[torch.as_tensor(Z).long()])
+    return (torch.as_tensor(raw).double() * sigma + mu) * torch.as_tensor(
+        natoms, dtype=torch.float64) + refs
 
 
 def denormalize_forces(raw_f, n, w):

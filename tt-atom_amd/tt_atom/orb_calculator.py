@@ -41,21 +41,35 @@ _ZBL_D = (3.2, 0.9423, 0.4028, 0.2016)
 _ZBL_A_EXP, _ZBL_A_PRE, _BOHR, _COULOMB = 0.300, 0.4543, 0.529, 14.3996
 
 
-def zbl_energy(Z, senders, receivers, vectors, covalent_radii, p=6, aggregation="mean"):
-    """Pair repulsion of one system (fp64, differentiable in ``vectors``).  Orb's atomic-number
+def _zbl_pairs(Z, senders, receivers, vectors, covalent_radii, p=6):
+    """Per-edge ZBL pair energies (fp64, differentiable in ``vectors``).  Orb's atomic-number
     embedding is indexed by the stored number and its ZBL basis adds one to it
-    (orb_model.py:507-510); that convention is kept."""
+    (orb_model.py:507-510); that convention is kept.  The envelope is zero from the sum of the
+    covalent radii on, so only the pairs inside it are evaluated (the others are exact zeros)."""
     Zu = Z[senders].double() + 1
     Zv = Z[receivers].double() + 1
-    a = _ZBL_A_PRE * _BOHR / (Zu ** _ZBL_A_EXP + Zv ** _ZBL_A_EXP)
-    x = torch.linalg.norm(vectors.double(), dim=1)
-    phi = sum(c * torch.exp(-d * x / a) for c, d in zip(_ZBL_C, _ZBL_D))
     rad = torch.as_tensor(covalent_radii, dtype=torch.float64)
     r_max = rad[Zu.long()] + rad[Zv.long()]
+    vec = vectors.double()
+    with torch.no_grad():
+        near = torch.nonzero(torch.linalg.norm(vec, dim=1) < r_max).reshape(-1)
+    out = torch.zeros(vec.shape[0], dtype=torch.float64)
+    if near.numel() == 0:
+        return out + 0.0 * vec.sum()                   # keeps the graph for autograd callers
+    Zu, Zv, r_max = Zu[near], Zv[near], r_max[near]
+    a = _ZBL_A_PRE * _BOHR / (Zu ** _ZBL_A_EXP + Zv ** _ZBL_A_EXP)
+    x = torch.linalg.norm(vec[near], dim=1)
+    phi = sum(c * torch.exp(-d * x / a) for c, d in zip(_ZBL_C, _ZBL_D))
     q = x / r_max
     env = (1.0 - (p + 1) * (p + 2) / 2.0 * q ** p + p * (p + 2) * q ** (p + 1)
-           - p * (p + 1) / 2.0 * q ** (p + 2)) * (x < r_max).double()
-    v = 0.5 * _COULOMB * Zu * Zv / x * phi * env
+           - p * (p + 1) / 2.0 * q ** (p + 2))
+    return out.index_put((near,), 0.5 * _COULOMB * Zu * Zv / x * phi * env)
+
+
+def zbl_energy(Z, senders, receivers, vectors, covalent_radii, p=6, aggregation="mean"):
+    """Pair repulsion of one system: per-edge energies summed onto senders, then the mean or the
+    sum over nodes (orb_model.py:491-538)."""
+    v = _zbl_pairs(Z, senders, receivers, vectors, covalent_radii, p)
     per_node = torch.zeros(Z.shape[0], dtype=torch.float64).index_add_(0, senders, v)
     if aggregation == "mean":
         return per_node.mean()
@@ -83,6 +97,27 @@ def zbl_energy_forces_stress(Z, senders, receivers, pos, shift, covalent_radii, 
         vol = abs(float(np.linalg.det(np.asarray(cell, dtype=np.float64).reshape(3, 3))))
         stress = full_3x3_to_voigt_6(g[1].numpy() / vol)
     return float(e.detach()), (-g[0]).numpy(), stress
+
+
+def zbl_batch(Z, senders, receivers, pos, shift, batch, natoms, covalent_radii,
+              aggregation="mean"):
+    """Pair repulsion of every system of a disjoint union in one autograd call: (energies [K],
+    forces [N, 3]).  The union's edges never join two systems, so the gradient of the summed
+    system energies gives each atom its own system's force (as orb_calculator.py:296-327
+    computes the union's ZBL once)."""
+    if aggregation not in ("mean", "sum"):
+        raise ValueError(f"aggregation must be 'mean' or 'sum', got {aggregation!r}")
+    pos = torch.as_tensor(pos, dtype=torch.float64).detach().clone().requires_grad_(True)
+    v = pos[receivers] - pos[senders]
+    if shift is not None:
+        v = v + torch.as_tensor(shift, dtype=torch.float64)
+    e = _zbl_pairs(Z, senders, receivers, v, covalent_radii)
+    K = len(natoms)
+    per_sys = torch.zeros(K, dtype=torch.float64).index_add_(0, batch[senders], e)
+    if aggregation == "mean":
+        per_sys = per_sys / torch.as_tensor(natoms, dtype=torch.float64)
+    (g,) = torch.autograd.grad(per_sys.sum(), [pos])
+    return per_sys.detach().numpy(), (-g).numpy()
 
 
 def _default_radii():
@@ -123,11 +158,13 @@ class OrbSession:
 
     def _run(self, bg, compute_stress):
         N = int(bg.pos.shape[0])
-        key = (bg.senders.numel(), tuple(bg.natoms))
+        # the conditioning enters through (charge, spin) per system, so those values (not the
+        # embedding tensors) are part of the engine key
+        cond_key = ((tuple(bg.charges), tuple(bg.spins)) if self.model.has_cond else None)
+        key = (bg.senders.numel(), tuple(bg.natoms), cond_key)
         same = (self._engine is not None and self._key[0] == key
                 and torch.equal(self._key[1], bg.senders) and torch.equal(self._key[2], bg.receivers)
-                and torch.equal(self._key[3], bg.cell_shift) and torch.equal(self._key[4], bg.Z)
-                and torch.equal(self._key[5], self._cond(bg)))
+                and torch.equal(self._key[3], bg.cell_shift) and torch.equal(self._key[4], bg.Z))
         if not same:
             graph = orb.OrbGraph(self.model.device, senders=bg.senders, receivers=bg.receivers,
                                  num_nodes=N, atomic_numbers=bg.Z, cell_shift=bg.cell_shift,
@@ -135,16 +172,13 @@ class OrbSession:
             cond = self._cond(bg) if self.model.has_cond else None
             self._engine = orb.OrbEngine(self.model, graph, cond)
             self._key = (key, bg.senders.clone(), bg.receivers.clone(), bg.cell_shift.clone(),
-                         bg.Z.clone(), self._cond(bg))
+                         bg.Z.clone())
         p = torch.as_tensor(bg.pos, dtype=torch.float32).to(self.model.device)
         raw, F, vir = self._engine.run(p, compute_stress)
         return raw, F.detach().cpu().double(), (None if vir is None else vir.detach().cpu().double())
 
     def _cond(self, bg):
-        if not self.model.has_cond:
-            return torch.zeros(0)
-        return torch.cat([self.model.charge_spin_embedding(q, s, n)
-                          for q, s, n in zip(bg.charges, bg.spins, bg.natoms)])
+        return self.model.charge_spin_embedding_batch(bg.charges, bg.spins, bg.natoms)
 
     def evaluate(self, positions, numbers, cell=None, pbc=None, charge=0.0, spin=0.0,
                  properties=("energy", "forces")):
@@ -196,24 +230,19 @@ class OrbSession:
         want_forces = "forces" in properties
         bg = orb.assemble_orb(systems, self.r_max, self.max_num_neighbors, self.neighbor_list)
         raw, F_raw, _ = self._run(bg, False)
-        energies, forces, off = [], [], 0
-        for k, n in enumerate(bg.natoms):
-            sl = slice(off, off + n)
-            E_k = float(orb.denormalize_energy(raw[k], bg.Z[sl], n, self._w))
-            if self.is_direct:
-                F_k = orb.denormalize_direct_forces(F_raw[sl], self._w).numpy()
-            else:
-                F_k = orb.denormalize_forces(F_raw[sl], n, self._w).numpy()
-            if self.pair_repulsion:
-                m = (bg.senders >= off) & (bg.senders < off + n)
-                e_z, f_z, _ = zbl_energy_forces_stress(
-                    bg.Z[sl], bg.senders[m] - off, bg.receivers[m] - off, bg.pos[sl],
-                    bg.cell_shift[m], self._radii_table(), aggregation=self.zbl_aggregation)
-                E_k, F_k = E_k + e_z, F_k + f_z
-            energies.append(E_k)
-            forces.append(F_k)
-            off += n
-        return dict(energy=np.array(energies), forces=forces if want_forces else None)
+        batch = bg.batch.long()
+        n_of = torch.as_tensor(bg.natoms, dtype=torch.float64)
+        E = orb.denormalize_energy_batch(raw, bg.Z, batch, bg.natoms, self._w).numpy()
+        if self.is_direct:
+            F = orb.denormalize_direct_forces(F_raw, self._w).numpy()
+        else:
+            F = orb.denormalize_forces(F_raw, n_of[batch][:, None], self._w).numpy()
+        if self.pair_repulsion:
+            e_z, f_z = zbl_batch(bg.Z, bg.senders, bg.receivers, bg.pos, bg.cell_shift, batch,
+                                 bg.natoms, self._radii_table(), self.zbl_aggregation)
+            E, F = E + e_z, F + f_z
+        forces = np.split(F, np.cumsum(bg.natoms)[:-1]) if want_forces else None
+        return dict(energy=np.asarray(E, dtype=np.float64), forces=forces)
 
 
 class OrbCalculator(_AseCalculator):

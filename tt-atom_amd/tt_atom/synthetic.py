@@ -334,6 +334,41 @@ def random_orb_weights(cfg, seed, direct=False):
     return w
 
 
+# ------------------------------------------------------------------------------ small batches
+# The reference's small-system throughput legs (scripts/release_gate.py:536-555,
+# docs/perf_baselines.json) time evaluate_batch on K rattled copies of CH3CH2OH (G2 geometry) or
+# of diamond Si 2x1x1; these are the same inputs built without ASE (rattle = N(0, stdev) per
+# coordinate from RandomState(seed), as ase.Atoms.rattle draws it).
+ETHANOL_Z = np.array([6, 6, 8, 1, 1, 1, 1, 1, 1], dtype=np.int64)
+ETHANOL_POS = np.array([[1.168181, -0.400382, 0.0], [0.0, 0.559462, 0.0],
+                        [-1.190083, -0.227669, 0.0], [-1.946623, 0.381525, 0.0],
+                        [0.042557, 1.207508, 0.886933], [0.042557, 1.207508, -0.886933],
+                        [2.115891, 0.1448, 0.0], [1.128599, -1.037234, 0.885881],
+                        [1.128599, -1.037234, -0.885881]])
+
+
+def _rattled(pos, stdev, seed):
+    return (pos + np.random.RandomState(seed).normal(scale=stdev, size=pos.shape)).astype(
+        np.float32)
+
+
+def ethanol_batch(k, stdev=0.08, seed0=10):
+    """K rattled ethanol molecules (charge 0, spin 1) as evaluate_batch system dicts."""
+    return [dict(positions=_rattled(ETHANOL_POS, stdev, seed0 + i), numbers=ETHANOL_Z.copy(),
+                 charge=0.0, spin=1.0) for i in range(k)]
+
+
+def si_batch(k, a=5.43, stdev=0.08, seed0=10):
+    """K rattled diamond-Si 2x1x1 cells (4 atoms, periodic) as evaluate_batch system dicts."""
+    h = a / 2.0
+    prim = np.array([[0.0, h, h], [h, 0.0, h], [h, h, 0.0]])
+    base = np.array([[0.0, 0.0, 0.0], [a / 4, a / 4, a / 4]])
+    pos = np.concatenate([base, base + prim[0]])
+    cell = np.stack([2 * prim[0], prim[1], prim[2]])
+    return [dict(positions=_rattled(pos, stdev, seed0 + i), numbers=np.full(4, 14, np.int64),
+                 cell=cell.astype(np.float32), pbc=[True] * 3) for i in range(k)]
+
+
 # ------------------------------------------------------------------------------ C2
 def c2_weights(seed=SEEDS["C2"] + WEIGHT_SEED_OFFSET, C=128, prefix="c2"):
     """SO(2) convolution weights of the isolated edgewise workload, N(0, 1/sqrt(fan_in)), m = 0

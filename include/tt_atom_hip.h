@@ -20,6 +20,8 @@
 
 #include <stdint.h>
 
+#include "tt_atom_hip_types.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -59,6 +61,15 @@ int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const float* bias, 
                    const float* aux, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldc,
                    int mode, const float* P, int64_t ldp, const int* idx0, const int* idx1,
                    int64_t off1, int64_t n_rows_p, int epilogue, tta_stream_t stream);
+
+/* Up to 4 independent products in one launch (tta_gemm_problem; row-gather terms not
+ * supported): the split-bf16 kernel with packed B operands, or the fp32 kernel with fp32 B.
+ * The three SO(2) m-block contractions of one convolution (so2.py:106-115, 282-294, and the
+ * transposed products of their VJP, forces.py:23-36), which the reference issues one by one,
+ * share the edge rows and run as one launch.  Same checks and results as one call per product;
+ * empty products are skipped. */
+int tta_gemm_bf16x_group(const tta_gemm_problem* probs, int64_t n, int mode, tta_stream_t stream);
+int tta_gemm_f32_group(const tta_gemm_problem* probs, int64_t n, tta_stream_t stream);
 
 /* ---------------------------------------------------------------- edge-frame rotation
  * out[e, m, :] = (sum_j W[e,m,j] [x[src_e, j, :] | x[tgt_e, j, :]]) * rad[e, rb(m), :]

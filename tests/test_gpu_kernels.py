@@ -474,3 +474,48 @@ def test_forces_virial_and_sum(nat):
     assert (Fo.cpu() - ref_F).abs().max() < 1e-5
     assert (Vo.cpu().reshape(3, 3) - ref_V).abs().max() < 1e-3
     assert abs(float(so) - float(x.double().sum())) < 1e-3
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_linear_group_equals_separate_calls(nat, split):
+    """Grouped launches (one launch for up to four products: column blocks of one input and one
+    output, as the SO(2) m-blocks use them, with bias / accumulate / two-output / silu-grad
+    epilogues) give the same bits as one call per product, on both kernels."""
+    g = torch.Generator().manual_seed(11)
+    M = 5000 if split else 700
+    x = torch.randn(M, 9 * 128, generator=g).to(DEV)
+    outs = {}
+    for grouped in (False, True):
+        out = torch.zeros(M, 640 + 512 + 256, device=DEV)
+        out2 = torch.zeros(M, 640 + 512 + 256, device=DEV)  # second output: out's row layout
+        aux = torch.randn(M, 256, generator=torch.Generator().manual_seed(2)).to(DEV)
+        out[:, 640 + 512:] = 0.5
+        ws = [torch.randn(384, 640, generator=torch.Generator().manual_seed(3)) / 20,
+              torch.randn(512, 512, generator=torch.Generator().manual_seed(4)) / 20,
+              torch.randn(256, 256, generator=torch.Generator().manual_seed(5)) / 20]
+        ws = [nat.PackedWeight(w.to(DEV)) for w in ws]
+        bias = torch.randn(640, generator=torch.Generator().manual_seed(6)).to(DEV)
+        items = [(x[:, :384], ws[0], bias, out[:, :640], nat.EPI_STORE),
+                 (x[:, 384:896], ws[1], None, out[:, 640:640 + 512], nat.EPI_PRE_SILU,
+                  out2[:, 640:640 + 512]),
+                 (x[:, 896:1152], ws[2], None, out[:, 640 + 512:], nat.EPI_ACCUM)]
+        if grouped:
+            nat.linear_group(items)
+        else:
+            for it in items:
+                nat.linear(it[0], it[1], it[2], out=it[3], epilogue=it[4],
+                           out2=it[5] if len(it) > 5 else None)
+        # a fourth product type: silu-grad epilogue on its own group of one
+        o4 = torch.empty(M, 256, device=DEV)
+        item4 = (x[:, :256], ws[2], None, o4, nat.EPI_SILU_GRAD, None, aux)
+        if grouped:
+            nat.linear_group([item4])
+        else:
+            nat.linear(x[:, :256], ws[2], out=o4, epilogue=nat.EPI_SILU_GRAD, aux=aux)
+        torch.cuda.synchronize()
+        outs[grouped] = (out.clone(), out2.clone(), o4.clone())
+    for a, b in zip(outs[False], outs[True]):
+        assert torch.equal(a, b)
+    assert outs[True][1][:, :640].abs().max() == 0 and outs[True][1][:, 1152:].abs().max() == 0
+    ref = x[:, :384].double().cpu() @ ws[0].w_t.double().cpu() + bias.double().cpu()
+    assert (outs[True][0][:, :640].cpu().double() - ref).abs().max() < 1e-3

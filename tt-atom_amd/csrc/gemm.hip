@@ -16,6 +16,8 @@
 // the result D[4*(l/16)+r][l%16], r=0..3, lands in accumulator element r of lane l.
 #include "gemm_common.h"
 
+#include <algorithm>
+
 namespace {
 
 using namespace tta_gemm;
@@ -112,8 +114,12 @@ __device__ __forceinline__ void store_b(float (*Bs)[BN + PAD], int t,
 
 // The epilogue is a (wave-uniform) runtime switch so every GEMM of the step is one kernel
 // symbol per tile shape; it runs once per output element and costs nothing next to the K loop.
-template <int BM, int BN, int WGM, int WGN, bool VEC>
-__global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
+// GROUP: blockIdx.z selects the product of g (batch 1 each); otherwise g.p[0] is one strided
+// batch and blockIdx.z its batch index.
+template <int BM, int BN, int WGM, int WGN, bool VEC, bool GROUP>
+__global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmGroup g) {
+  const GemmArgs& p = g.p[GROUP ? blockIdx.z : 0];
+  const int64_t bz = GROUP ? 0 : blockIdx.z;
   typedef Tile<BM, BN, WGM, WGN> TL;
   constexpr int TI = TL::TI, TJ = TL::TJ;
   __shared__ float As[2][BK][BM + PAD];
@@ -125,16 +131,19 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
   const int wm = wave / WGN, wn = wave % WGN;
   const int tn = (p.N + BN - 1) / BN;
   const int ntiles = tn * ((p.M + BM - 1) / BM);
+  // a product of a group uses the first (ntiles rounded up to 8) blocks of the grid, so that
+  // xcd_tile maps them one to one onto its tiles; wider grids belong to other products
+  if ((int)blockIdx.x >= ((ntiles + 7) / 8) * 8) return;
   const int tile = xcd_tile(ntiles);
   if (tile >= ntiles) return;
   const int n0 = (tile % tn) * BN;
   const int m0 = (tile / tn) * BM;
-  const float* A = p.A + (int64_t)blockIdx.z * p.sA;
-  const float* B = static_cast<const float*>(p.B) + (int64_t)blockIdx.z * p.sB;
-  float* C = p.C + (int64_t)blockIdx.z * p.sC;
-  float* C2 = p.C2 ? p.C2 + (int64_t)blockIdx.z * p.sC : nullptr;
-  const float* aux = p.aux ? p.aux + (int64_t)blockIdx.z * p.sC : nullptr;
-  const float* bias = p.bias ? p.bias + (int64_t)blockIdx.z * p.sBias : nullptr;
+  const float* A = p.A + bz * p.sA;
+  const float* B = static_cast<const float*>(p.B) + bz * p.sB;
+  float* C = p.C + bz * p.sC;
+  float* C2 = p.C2 ? p.C2 + bz * p.sC : nullptr;
+  const float* aux = p.aux ? p.aux + bz * p.sC : nullptr;
+  const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
 
   floatx4 acc[TI][TJ];
 #pragma unroll
@@ -183,39 +192,61 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmArgs p) {
   store_tiles<TI, TJ>(p, acc, m0 + rbase, n0 + cbase, li, lk, C, C2, aux, bias);
 }
 
+// n products (group) or one product with `batch` strided copies (n == 1, group false).
 template <int BM, int BN, int WGM, int WGN>
-int launch(const GemmArgs& p, int64_t batch, bool vec, hipStream_t s) {
-  const int64_t ntiles = (int64_t)tta_blocks(p.N, BN) * tta_blocks(p.M, BM);
-  // one workgroup per tile, rounded up to a multiple of 8 so every XCD gets a full share
-  dim3 grid((unsigned)(((ntiles + 7) / 8) * 8), 1, (unsigned)batch);
-  if (ntiles > (1ll << 30)) {
-    tta::set_error("tta_gemm_f32: grid too large");
-    return tta::kBadArgument;
+int launch(const GemmGroup& g, int n, bool group, int64_t batch, bool vec, hipStream_t s) {
+  int64_t gx = 0;
+  for (int i = 0; i < n; ++i) {
+    const int64_t ntiles = (int64_t)tta_blocks(g.p[i].N, BN) * tta_blocks(g.p[i].M, BM);
+    if (ntiles > (1ll << 30)) {
+      tta::set_error("tta_gemm_f32: grid too large");
+      return tta::kBadArgument;
+    }
+    // one workgroup per tile, rounded up to a multiple of 8 so every XCD gets a full share
+    gx = std::max(gx, ((ntiles + 7) / 8) * 8);
   }
-  if (vec)
-    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, true>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, false>), grid, dim3(256), 0, s, p);
+  const dim3 grid((unsigned)gx, 1, (unsigned)(group ? n : batch));
+  if (group) {
+    if (vec)
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, true, true>), grid, dim3(256), 0, s,
+                         g);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, false, true>), grid, dim3(256), 0, s,
+                         g);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, true, false>), grid, dim3(256), 0, s,
+                         g);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, false, false>), grid, dim3(256), 0,
+                         s, g);
+  }
   TTA_CHECK_LAUNCH("tta_gemm_f32");
   return tta::kOk;
 }
 
 // Tile shape per call: 128 x 128 when the grid already fills the chip (>= 960 blocks, about four
-// resident blocks per CU), 64 x 128 for mid-size grids, 32 x 64 for the small node-level GEMMs.
-int dispatch(const GemmArgs& p, int64_t batch, bool vec, hipStream_t s) {
-  const int64_t big = (int64_t)tta_blocks(p.M, 128) * tta_blocks(p.N, 128) * batch;
-  const int64_t mid = (int64_t)tta_blocks(p.M, 64) * tta_blocks(p.N, 128) * batch;
-  if (big >= 960) return launch<128, 128, 2, 2>(p, batch, vec, s);
-  if (mid >= 512) return launch<64, 128, 2, 2>(p, batch, vec, s);
-  return launch<32, 64, 2, 2>(p, batch, vec, s);
+// resident blocks per CU), 64 x 128 for mid-size grids, 32 x 64 for the small node-level GEMMs
+// (counted over every product of a group).
+int dispatch(const GemmGroup& g, int n, bool group, int64_t batch, bool vec, hipStream_t s) {
+  int64_t big = 0, mid = 0;
+  for (int i = 0; i < n; ++i) {
+    big += (int64_t)tta_blocks(g.p[i].M, 128) * tta_blocks(g.p[i].N, 128) * batch;
+    mid += (int64_t)tta_blocks(g.p[i].M, 64) * tta_blocks(g.p[i].N, 128) * batch;
+  }
+  if (big >= 960) return launch<128, 128, 2, 2>(g, n, group, batch, vec, s);
+  if (mid >= 512) return launch<64, 128, 2, 2>(g, n, group, batch, vec, s);
+  return launch<32, 64, 2, 2>(g, n, group, batch, vec, s);
 }
 
 }  // namespace
 
 namespace {
 
-int check_and_run(GemmArgs& p, int64_t M, int64_t N, int64_t K, int64_t batch,
-                  hipStream_t stream, const char* name) {
+// Checks one product and completes p (sizes); *vec: whether its float4 path applies.
+int check(GemmArgs& p, int64_t M, int64_t N, int64_t K, int64_t batch, const char* name,
+          bool* skip, bool* vec) {
+  *skip = false;
   TTA_CHECK_ARG(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "%s: negative size", name);
   TTA_CHECK_ARG(M < (int64_t)1 << 31 && N < (int64_t)1 << 31 && K < (int64_t)1 << 31,
                 "%s: size exceeds int32", name);
@@ -223,16 +254,29 @@ int check_and_run(GemmArgs& p, int64_t M, int64_t N, int64_t K, int64_t batch,
   TTA_CHECK_ARG(p.epi >= 0 && p.epi <= 4, "%s: bad epilogue %d", name, p.epi);
   TTA_CHECK_ARG(p.epi != EPI_PRE_SILU || p.C2, "%s: epilogue 3 needs C2", name);
   TTA_CHECK_ARG(p.epi != EPI_SILU_GRAD || p.aux, "%s: epilogue 4 needs aux", name);
-  if (M == 0 || N == 0 || batch == 0) return tta::kOk;
+  if (M == 0 || N == 0 || batch == 0) {
+    *skip = true;
+    return tta::kOk;
+  }
   TTA_CHECK_ARG(p.A && p.B && p.C, "%s: null pointer", name);
   TTA_CHECK_ARG(p.lda >= K && p.ldb >= N && p.ldc >= N, "%s: leading dimension too small", name);
   p.M = (int)M;
   p.N = (int)N;
   p.K = (int)K;
-  const bool vec = (K % 4 == 0) && (N % 4 == 0) && (p.lda % 4 == 0) && (p.ldb % 4 == 0) &&
-                   (p.sA % 4 == 0) && (p.sB % 4 == 0) && ((uintptr_t)p.A % 16 == 0) &&
-                   ((uintptr_t)p.B % 16 == 0);
-  return dispatch(p, batch, vec, stream);
+  *vec = (K % 4 == 0) && (N % 4 == 0) && (p.lda % 4 == 0) && (p.ldb % 4 == 0) &&
+         (p.sA % 4 == 0) && (p.sB % 4 == 0) && ((uintptr_t)p.A % 16 == 0) &&
+         ((uintptr_t)p.B % 16 == 0);
+  return tta::kOk;
+}
+
+int check_and_run(GemmArgs& p, int64_t M, int64_t N, int64_t K, int64_t batch,
+                  hipStream_t stream, const char* name) {
+  bool skip = false, vec = false;
+  const int rc = check(p, M, N, K, batch, name, &skip, &vec);
+  if (rc != tta::kOk || skip) return rc;
+  GemmGroup g{};
+  g.p[0] = p;
+  return dispatch(g, 1, false, batch, vec, stream);
 }
 
 }  // namespace
@@ -258,4 +302,26 @@ extern "C" int tta_gemm_f32_gather(const float* A, const float* B, float* C, con
   GemmArgs p{A, B, C, bias, C2, aux, 0, 0, 0, lda, ldb, ldc, 0, 0, 0, 0, epilogue,
              P, idx0, idx1, ldp, off1};
   return check_and_run(p, M, N, K, 1, stream, "tta_gemm_f32_gather");
+}
+
+extern "C" int tta_gemm_f32_group(const tta_gemm_problem* probs, int64_t n, hipStream_t stream) {
+  TTA_CHECK_ARG(n >= 0 && n <= kMaxGroup && (probs || n == 0),
+                "tta_gemm_f32_group: 0..%d products", kMaxGroup);
+  GemmGroup g{};
+  int m = 0;
+  bool vec_all = true;
+  for (int64_t i = 0; i < n; ++i) {
+    const tta_gemm_problem& q = probs[i];
+    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= 4, "tta_gemm_f32_group: bad epilogue");
+    GemmArgs p{q.A, q.B, q.C, q.bias, q.C2, q.aux, 0, 0, 0, q.lda, q.ldb, q.ldc, 0, 0, 0, 0,
+               (int)q.epilogue, nullptr, nullptr, nullptr, 0, 0};
+    bool skip = false, vec = false;
+    const int rc = check(p, q.M, q.N, q.K, 1, "tta_gemm_f32_group", &skip, &vec);
+    if (rc != tta::kOk) return rc;
+    if (skip) continue;
+    g.p[m++] = p;
+    vec_all = vec_all && vec;
+  }
+  if (m == 0) return tta::kOk;
+  return dispatch(g, m, true, 1, vec_all, stream);
 }

@@ -32,6 +32,8 @@
 // with one block per CU on every edge- and node-level shape of the two models).
 #include "gemm_common.h"
 
+#include <algorithm>
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 typedef __attribute__((address_space(1))) void* gbl_ptr;
@@ -138,9 +140,10 @@ __device__ __forceinline__ void split8(const floatx4& x0, const floatx4& x1, bf1
 __device__ __forceinline__ int aswz(int row) { return (row >> 1) & 7; }
 
 template <int WM, int MODE>
-__global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(GemmArgs p,
-                                                                               int NT32,
-                                                                               bool vec_ok) {
+__global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(GemmGroup g) {
+  const GemmArgs& p = g.p[blockIdx.z];  // the product of this block (group of one: z = 0)
+  const int NT32 = g.NT32[blockIdx.z];
+  const bool vec_ok = g.vec[blockIdx.z] != 0;
   typedef Split<MODE> S;
   constexpr int NA = S::NA, NB = S::NB;
   constexpr int BM = 64 * WM, NTH = 128 * WM;
@@ -155,6 +158,9 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   const int wm = wave >> 1, wn = wave & 1;
   const int tn = (p.N + BN - 1) / BN;
   const int ntiles = tn * ((p.M + BM - 1) / BM);
+  // a product of a group uses the first (ntiles rounded up to 8) blocks of the grid, so that
+  // xcd_tile maps them one to one onto its tiles; wider grids belong to other products
+  if ((int)blockIdx.x >= ((ntiles + 7) / 8) * 8) return;
   const int tile = xcd_tile(ntiles);
   if (tile >= ntiles) return;
   const int n0 = (tile % tn) * BN;
@@ -319,20 +325,37 @@ __global__ __launch_bounds__(256) void k_pack_b(const float* __restrict__ B, int
   }
 }
 
+// One launch for the n products of g (blockIdx.z = product); each product's blocks beyond its
+// own tile count exit at once.
 template <int WM, int MODE>
-int launch_bf16x(const GemmArgs& p, int NT32, hipStream_t s) {
-  const int64_t ntiles = (int64_t)tta_blocks(p.N, BN) * tta_blocks(p.M, 64 * WM);
-  if (ntiles > (1ll << 30)) {
-    tta::set_error("tta_gemm_bf16x: grid too large");
-    return tta::kBadArgument;
+int launch_bf16x(const GemmGroup& g, int n, hipStream_t s) {
+  int64_t grid = 0;
+  for (int i = 0; i < n; ++i) {
+    const int64_t ntiles = (int64_t)tta_blocks(g.p[i].N, BN) * tta_blocks(g.p[i].M, 64 * WM);
+    if (ntiles > (1ll << 30)) {
+      tta::set_error("tta_gemm_bf16x: grid too large");
+      return tta::kBadArgument;
+    }
+    grid = std::max(grid, ((ntiles + 7) / 8) * 8);
   }
-  auto al = [](const void* q) { return q == nullptr || (uintptr_t)q % 16 == 0; };
-  const bool vec_ok = p.N % 4 == 0 && p.ldc % 4 == 0 && al(p.C) && al(p.C2) && al(p.aux) &&
-                      al(p.bias) && (!p.P || (al(p.P) && p.ldp % 4 == 0 && p.off1 % 4 == 0));
-  hipLaunchKernelGGL((gemm_bf16x_kernel<WM, MODE>), dim3((unsigned)(((ntiles + 7) / 8) * 8)),
-                     dim3(128 * WM), 0, s, p, NT32, vec_ok);
+  hipLaunchKernelGGL((gemm_bf16x_kernel<WM, MODE>), dim3((unsigned)grid, 1, (unsigned)n),
+                     dim3(128 * WM), 0, s, g);
   TTA_CHECK_LAUNCH("tta_gemm_bf16x");
   return tta::kOk;
+}
+
+bool vec_ok_of(const GemmArgs& p) {
+  auto al = [](const void* q) { return q == nullptr || (uintptr_t)q % 16 == 0; };
+  return p.N % 4 == 0 && p.ldc % 4 == 0 && al(p.C) && al(p.C2) && al(p.aux) && al(p.bias) &&
+         (!p.P || (al(p.P) && p.ldp % 4 == 0 && p.off1 % 4 == 0));
+}
+
+int launch_mode(const GemmGroup& g, int n, int mode, hipStream_t s) {
+  switch (mode) {
+    case 1: return launch_bf16x<2, 1>(g, n, s);
+    case 3: return launch_bf16x<2, 3>(g, n, s);
+    default: return launch_bf16x<2, 6>(g, n, s);
+  }
 }
 
 int planes_of(int mode) { return mode == 1 ? 1 : mode == 3 ? 2 : mode == 6 ? 3 : 0; }
@@ -365,12 +388,14 @@ extern "C" int tta_pack_b(const float* B, int64_t K, int64_t N, int64_t ldb, int
   return tta::kOk;
 }
 
-extern "C" int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const float* bias,
-                              float* C2, const float* aux, int64_t M, int64_t N, int64_t K,
-                              int64_t lda, int64_t ldc, int mode, const float* P, int64_t ldp,
-                              const int* idx0, const int* idx1, int64_t off1, int64_t n_rows_p,
-                              int epilogue, hipStream_t stream) {
-  TTA_CHECK_ARG(planes_of(mode) > 0, "tta_gemm_bf16x: mode must be 1, 3 or 6 (got %d)", mode);
+// Argument checks shared by the single and grouped entry points; fills p, NT32 and vec.  Returns
+// kOk with *skip set for an empty product.
+static int prepare_bf16x(const float* A, const void* Bp, float* C, const float* bias, float* C2,
+                         const float* aux, int64_t M, int64_t N, int64_t K, int64_t lda,
+                         int64_t ldc, const float* P, int64_t ldp, const int* idx0,
+                         const int* idx1, int64_t off1, int64_t n_rows_p, int epilogue,
+                         GemmGroup& g, int slot, bool* skip) {
+  *skip = false;
   TTA_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "tta_gemm_bf16x: negative size");
   TTA_CHECK_ARG(M < (int64_t)1 << 31 && N < (int64_t)1 << 30 && K < (int64_t)1 << 30,
                 "tta_gemm_bf16x: size exceeds int32");
@@ -379,7 +404,10 @@ extern "C" int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const fl
   TTA_CHECK_ARG(epilogue != EPI_SILU_GRAD || aux, "tta_gemm_bf16x: epilogue 4 needs aux");
   TTA_CHECK_ARG(!P || (idx0 && idx1 && n_rows_p > 0 && off1 >= 0 && ldp >= off1 + N),
                 "tta_gemm_bf16x: bad row-gather table");
-  if (M == 0 || N == 0) return tta::kOk;
+  if (M == 0 || N == 0) {
+    *skip = true;
+    return tta::kOk;
+  }
   TTA_CHECK_ARG(A && Bp && C, "tta_gemm_bf16x: null pointer");
   TTA_CHECK_ARG(K % 4 == 0 && lda % 4 == 0 && (uintptr_t)A % 16 == 0,
                 "tta_gemm_bf16x: A needs K, lda multiples of 4 and 16-byte alignment");
@@ -387,12 +415,45 @@ extern "C" int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const fl
   TTA_CHECK_ARG(lda < ((int64_t)1 << 21), "tta_gemm_bf16x: lda must be below 2^21 (32-bit "
                 "offsets inside a 256-row tile)");
   TTA_CHECK_ARG((uintptr_t)Bp % 16 == 0, "tta_gemm_bf16x: packed B must be 16-byte aligned");
-  GemmArgs p{A, Bp, C, bias, C2, aux, (int)M, (int)N, (int)K, lda, 0, ldc, 0, 0, 0, 0, epilogue,
-             P, idx0, idx1, ldp, off1};
-  const int NT32 = (int)nt32_padded(N);
-  switch (mode) {
-    case 1: return launch_bf16x<2, 1>(p, NT32, stream);
-    case 3: return launch_bf16x<2, 3>(p, NT32, stream);
-    default: return launch_bf16x<2, 6>(p, NT32, stream);
+  g.p[slot] = GemmArgs{A, Bp, C, bias, C2, aux, (int)M, (int)N, (int)K, lda, 0, ldc, 0, 0, 0,
+                       0, epilogue, P, idx0, idx1, ldp, off1};
+  g.NT32[slot] = (int)nt32_padded(N);
+  g.vec[slot] = vec_ok_of(g.p[slot]) ? 1 : 0;
+  return tta::kOk;
+}
+
+extern "C" int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const float* bias,
+                              float* C2, const float* aux, int64_t M, int64_t N, int64_t K,
+                              int64_t lda, int64_t ldc, int mode, const float* P, int64_t ldp,
+                              const int* idx0, const int* idx1, int64_t off1, int64_t n_rows_p,
+                              int epilogue, hipStream_t stream) {
+  TTA_CHECK_ARG(planes_of(mode) > 0, "tta_gemm_bf16x: mode must be 1, 3 or 6 (got %d)", mode);
+  GemmGroup g{};
+  bool skip = false;
+  const int rc = prepare_bf16x(A, Bp, C, bias, C2, aux, M, N, K, lda, ldc, P, ldp, idx0, idx1,
+                               off1, n_rows_p, epilogue, g, 0, &skip);
+  if (rc != tta::kOk || skip) return rc;
+  return launch_mode(g, 1, mode, stream);
+}
+
+extern "C" int tta_gemm_bf16x_group(const tta_gemm_problem* probs, int64_t n, int mode,
+                                    hipStream_t stream) {
+  TTA_CHECK_ARG(planes_of(mode) > 0, "tta_gemm_bf16x_group: mode must be 1, 3 or 6 (got %d)",
+                mode);
+  TTA_CHECK_ARG(n >= 0 && n <= kMaxGroup && (probs || n == 0),
+                "tta_gemm_bf16x_group: 0..%d products", kMaxGroup);
+  GemmGroup g{};
+  int m = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const tta_gemm_problem& q = probs[i];
+    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= 4, "tta_gemm_bf16x_group: bad epilogue");
+    bool skip = false;
+    const int rc = prepare_bf16x(q.A, q.B, q.C, q.bias, q.C2, q.aux, q.M, q.N, q.K, q.lda, q.ldc,
+                                 nullptr, 0, nullptr, nullptr, 0, 0, (int)q.epilogue, g, m,
+                                 &skip);
+    if (rc != tta::kOk) return rc;
+    if (!skip) ++m;
   }
+  if (m == 0) return tta::kOk;
+  return launch_mode(g, m, mode, stream);
 }

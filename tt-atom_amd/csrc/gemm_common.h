@@ -3,6 +3,7 @@
 #pragma once
 
 #include "common.h"
+#include "../../include/tt_atom_hip_types.h"
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -26,6 +27,17 @@ struct GemmArgs {
   const int* idx0;
   const int* idx1;
   int64_t ldp, off1;
+};
+
+// Up to kMaxGroup independent products in one launch: blockIdx.z selects the product (the
+// kernels of a plain call see a group of one; the fp32 kernel's strided batch uses blockIdx.z
+// itself and is not combined with a group).  vec / NT32 are per product: the fp32 kernel's float4
+// path and the split kernel's packed-B column tiles.
+constexpr int kMaxGroup = 4;
+struct GemmGroup {
+  GemmArgs p[kMaxGroup];
+  int NT32[kMaxGroup];
+  int vec[kMaxGroup];
 };
 
 // Accumulator layout of v_mfma_f32_16x16x{4f32,32bf16}: lane l holds D[4*(l/16)+r][l%16] in

@@ -21,6 +21,14 @@ _I = ctypes.c_int
 _F = ctypes.c_float
 _D = ctypes.c_double
 
+
+class GemmProblem(ctypes.Structure):
+    """tta_gemm_problem (include/tt_atom_hip_types.h): one product of a grouped GEMM launch."""
+    _fields_ = [("A", _P), ("B", _P), ("C", _P), ("bias", _P), ("C2", _P), ("aux", _P),
+                ("M", _I64), ("N", _I64), ("K", _I64), ("lda", _I64), ("ldb", _I64),
+                ("ldc", _I64), ("epilogue", _I64)]
+
+
 # name -> argtypes (all return int status unless listed in _RESTYPE)
 _SIGS = {
     "tta_version": [],
@@ -68,6 +76,8 @@ _SIGS = {
     "tta_pack_b": [_P, _I64, _I64, _I64, _I, _P, _I64, _P],
     "tta_gemm_bf16x": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P, _I64, _P, _P,
                        _I64, _I64, _I, _P],
+    "tta_gemm_bf16x_group": [ctypes.POINTER(GemmProblem), _I64, _I, _P],
+    "tta_gemm_f32_group": [ctypes.POINTER(GemmProblem), _I64, _P],
     "tta_radius_graph_thresholds": [_P, _I64, _P, _P, _P, _I64, _I, _D, _F, _F, _I, _P, _P, _P,
                                     _P, _P],
     "tta_radius_graph_count": [_P, _I64, _P, _P, _P, _I64, _I, _D, _F, _F, _P, _P, _P, _P, _P],
@@ -175,13 +185,33 @@ def set_gemm_probe(probe):
     _gemm_probe = probe
 
 
+def _span(t, name, rows, ld, width, batch=1, stride=0):
+    """Checks that an fp32 device tensor's storage holds rows x width at row stride ld, for
+    `batch` copies `stride` elements apart, starting at the tensor's own offset."""
+    if t is None:
+        return
+    if not t.is_cuda or t.dtype != torch.float32:
+        raise RuntimeError(f"gemm: {name} must be an fp32 device tensor")
+    if rows <= 0 or width <= 0 or batch <= 0:
+        return
+    need = t.storage_offset() + (batch - 1) * stride + (rows - 1) * ld + width
+    if ld < 0 or stride < 0 or need * 4 > t.untyped_storage().nbytes():
+        raise RuntimeError(f"gemm: {name} is too small for {batch} x {rows} x {width} at row "
+                           f"stride {ld} (batch stride {stride})")
+
+
 def gemm(A, B, C, *, M, N, K, lda, ldb, ldc, bias=None, epilogue=EPI_STORE, C2=None, aux=None,
          batch=1, sA=0, sB=0, sC=0, sBias=0):
     """C = epi(A @ B + bias) on raw strided views (A/B/C are base tensors; offsets are applied
     by the caller through ``narrow``/slicing of contiguous storage -> data_ptr)."""
-    for t, nm in ((A, "A"), (B, "B"), (C, "C")):
-        if not t.is_cuda or t.dtype != torch.float32:
-            raise RuntimeError(f"gemm: {nm} must be an fp32 device tensor")
+    # every operand must hold its whole strided extent: the kernel indexes C2 and aux with C's
+    # row stride and batch stride
+    _span(A, "A", M, lda, K, batch, sA)
+    _span(B, "B", K, ldb, N, batch, sB)
+    _span(C, "C", M, ldc, N, batch, sC)
+    _span(C2, "C2", M, ldc, N, batch, sC)
+    _span(aux, "aux", M, ldc, N, batch, sC)
+    _span(bias, "bias", 1, N, N, batch, sBias)
     probe = _gemm_probe
     if probe is not None:
         c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD))
@@ -224,9 +254,21 @@ class PackedWeight:
         return self.w_t.shape
 
 
+def _same_rows(out, out2, aux, where):
+    """out2 and aux are written / read at out's row stride by the GEMM epilogues."""
+    ldc = _ld(out, "out")
+    for t, nm in ((out2, "out2"), (aux, "aux")):
+        if t is not None and (t.shape != out.shape or _ld(t, nm) != ldc):
+            raise RuntimeError(f"{where}: {nm} must have out's shape and row stride")
+
+
 def _gemm_bf16x(x, pw, out, bias, epilogue, out2, aux, P=None, idx0=None, idx1=None, off1=0):
     M, K = x.shape
     N = pw.w_t.shape[1]
+    _same_rows(out, out2, aux, "linear")
+    _span(x, "x", M, _ld(x, "x"), K)
+    for t, nm in ((out, "out"), (out2, "out2"), (aux, "aux")):
+        _span(t, nm, M, _ld(out, "out"), N)
     probe = _gemm_probe
     if probe is not None:
         c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD)) + (2 if P is not None else 0)
@@ -260,6 +302,7 @@ def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None)
         raise RuntimeError(f"linear: inner dims {K} vs {K2}")
     if out is None:
         out = torch.empty(M, N, device=x.device, dtype=torch.float32)
+    _same_rows(out, out2, aux, "linear")
     if isinstance(w_t, PackedWeight):
         if _split_ok(x, w_t):
             _gemm_bf16x(x, w_t, out, bias, epilogue, out2, aux)
@@ -268,6 +311,55 @@ def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None)
     gemm(x, w_t, out, M=M, N=N, K=K, lda=_ld(x, "x"), ldb=_ld(w_t, "w_t"), ldc=_ld(out, "out"),
          bias=bias, epilogue=epilogue, C2=out2, aux=aux)
     return out
+
+
+MAX_GROUP = 4
+
+
+def linear_group(items):
+    """Several independent products y = x @ w_t (+ bias) in one launch: ``items`` = [(x, w_t,
+    bias, out, epilogue, out2, aux)] (the last three optional).  All on the split-bf16 kernel
+    when every product qualifies for it (same plane mode), all on the fp32 kernel when none
+    does; a mix runs one launch per product."""
+    items = [tuple(it) + (EPI_STORE, None, None)[len(it) - 4:] for it in items]
+    for x, w, bias, out, epi, out2, aux in items:
+        if x.shape[1] != w.shape[0] or out.shape != (x.shape[0], w.shape[1]):
+            raise RuntimeError("linear_group: shape mismatch")
+        _same_rows(out, out2, aux, "linear_group")
+    split = [isinstance(w, PackedWeight) and _split_ok(x, w) for x, w, *_ in items]
+    modes = {w.mode for (x, w, *_), sp in zip(items, split) if sp}
+    if len(items) > MAX_GROUP or (any(split) and not all(split)) or len(modes) > 1:
+        for x, w, bias, out, epi, out2, aux in items:
+            linear(x, w, bias, out, epi, out2, aux)
+        return
+    probs = (GemmProblem * len(items))()
+    flops = nbytes = 0.0
+    for i, (x, w, bias, out, epi, out2, aux) in enumerate(items):
+        M, K = x.shape
+        N = w.shape[1]
+        wt = w if split[0] else (w.w_t if isinstance(w, PackedWeight) else w)
+        ldc = _ld(out, "out")
+        probs[i] = GemmProblem(
+            _rows(x, M, _ld(x, "x"), K, "x"),
+            wt.packed.data_ptr() if split[0] else _rows(wt, K, _ld(wt, "w_t"), N, "w_t"),
+            _rows(out, M, ldc, N, "out"),
+            None if bias is None else _ptr(bias, numel=N, name="bias"),
+            None if out2 is None else _rows(out2, M, _ld(out2, "out2"), N, "out2"),
+            None if aux is None else _rows(aux, M, _ld(aux, "aux"), N, "aux"),
+            M, N, K, _ld(x, "x"), 0 if split[0] else _ld(wt, "w_t"), ldc, epi)
+
+        c_passes = 1 + (epi in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD))
+        flops += 2.0 * M * N * K
+        nbytes += 4.0 * (M * K + K * N + c_passes * M * N)
+    probe = _gemm_probe
+    if probe is not None:
+        probe.before(flops, nbytes, f"bf16x{items[0][1].mode}" if split[0] else "f32")
+    if split[0]:
+        _call("tta_gemm_bf16x_group", probs, len(items), items[0][1].mode, _stream())
+    else:
+        _call("tta_gemm_f32_group", probs, len(items), _stream())
+    if probe is not None:
+        probe.after()
 
 
 def _ld(t, name):

@@ -64,9 +64,9 @@ class EdgewiseStep:
                         self.ev, self.dist, self.coef)
         nat.gather_rotate_src(x, self.src, self.coef, self.xe.view(self.E, 9, C))
         s = self.so2
-        nat.linear(self.xe[:, :3 * C], s.wm0_t, s.bm0, out=self.ms[:, :3 * C])
-        nat.linear(self.xe[:, 3 * C:7 * C], s.w1, out=self.ms[:, 3 * C:7 * C])
-        nat.linear(self.xe[:, 7 * C:], s.w2, out=self.ms[:, 7 * C:])
+        nat.linear_group([(self.xe[:, :3 * C], s.wm0_t, s.bm0, self.ms[:, :3 * C]),
+                          (self.xe[:, 3 * C:7 * C], s.w1, None, self.ms[:, 3 * C:7 * C]),
+                          (self.xe[:, 7 * C:], s.w2, None, self.ms[:, 7 * C:])])
         nat.rotate_env_segsum(self.ms.view(self.E, 9, C), self.coef, self.env, self.tgt_ptr, None,
                               self.out, n_in=9, env_first=True, div=1.0)
         return self.out
@@ -79,9 +79,9 @@ class EdgewiseStep:
                                  self.g_m.view(self.E, 9, C), self.g_coef, self.g_env, n_in=9,
                                  env_first=True, div=1.0)
         s = self.so2
-        nat.linear(self.g_m[:, :3 * C], s.wm0, out=self.g_xe[:, :3 * C])
-        nat.linear(self.g_m[:, 3 * C:7 * C], s.w1_t, out=self.g_xe[:, 3 * C:7 * C])
-        nat.linear(self.g_m[:, 7 * C:], s.w2_t, out=self.g_xe[:, 7 * C:])
+        nat.linear_group([(self.g_m[:, :3 * C], s.wm0, None, self.g_xe[:, :3 * C]),
+                          (self.g_m[:, 3 * C:7 * C], s.w1_t, None, self.g_xe[:, 3 * C:7 * C]),
+                          (self.g_m[:, 7 * C:], s.w2_t, None, self.g_xe[:, 7 * C:])])
         nat.gather_rotate_src_bw(self.g_xe.view(self.E, 9, C), x, self.src, self.coef, None,
                                  self.g_coef)
         nat.edge_geometry_bwd(self.ev, self.dist, self.g_coef, None, None, 0, None, 0.0, 1.0, 0,

@@ -218,16 +218,17 @@ class TracedEngine:
             nat.gather_rotate(c.n1, g.src, g.tgt, self.coef, c.rad.out, self.xf)
             xf = self.xf.view(E, NSPH * Cin)
             o1 = c.o1c
-            nat.linear(xf[:, :3 * Cin], s1w.wm0_t, s1w.bm0, out=o1[:, :LH + 3 * H])
-            nat.linear(xf[:, 3 * Cin:7 * Cin], s1w.w1, out=o1[:, LH + 3 * H:LH + 7 * H])
-            nat.linear(xf[:, 7 * Cin:], s1w.w2, out=o1[:, LH + 7 * H:])
+            # the three m-block contractions (m = 0 with the gating columns, 1, 2): one launch
+            nat.linear_group([(xf[:, :3 * Cin], s1w.wm0_t, s1w.bm0, o1[:, :LH + 3 * H]),
+                              (xf[:, 3 * Cin:7 * Cin], s1w.w1, None, o1[:, LH + 3 * H:LH + 7 * H]),
+                              (xf[:, 7 * Cin:], s1w.w2, None, o1[:, LH + 7 * H:])])
             nat.gate_fwd(o1[:, LH:], o1, self.y, bb.gate_idx_mprime, R=E, H=H, L=L, ldx=LHc,
                          ldg=LHc)
             y = self.y.view(E, NSPH * H)
             ms = c.mso2.view(E, NSPH * C)
-            nat.linear(y[:, :3 * H], s2w.wm0_t, s2w.bm0, out=ms[:, :3 * C])
-            nat.linear(y[:, 3 * H:7 * H], s2w.w1, out=ms[:, 3 * C:7 * C])
-            nat.linear(y[:, 7 * H:], s2w.w2, out=ms[:, 7 * C:])
+            nat.linear_group([(y[:, :3 * H], s2w.wm0_t, s2w.bm0, ms[:, :3 * C]),
+                              (y[:, 3 * H:7 * H], s2w.w1, None, ms[:, 3 * C:7 * C]),
+                              (y[:, 7 * H:], s2w.w2, None, ms[:, 7 * C:])])
             nat.rotate_env_segsum(c.mso2, self.coef, self.env, g.tgt_ptr, c.x_in, c.x1, n_in=9,
                                   env_first=True)
             nat.rmsnorm_sh_fwd(c.x1, bw.norm_2.aw, bw.norm_2.ab, None, c.n2, c.inv2)
@@ -276,16 +277,17 @@ class TracedEngine:
                                      self.g_coef, self.g_env, n_in=9, env_first=True)
             gm = self.g_mso2.view(E, NSPH * C)
             gy = self.g_y.view(E, NSPH * H)
-            nat.linear(gm[:, :3 * C], s2w.wm0, out=gy[:, :3 * H])
-            nat.linear(gm[:, 3 * C:7 * C], s2w.w1_t, out=gy[:, 3 * H:7 * H])
-            nat.linear(gm[:, 7 * C:], s2w.w2_t, out=gy[:, 7 * H:])
+            nat.linear_group([(gm[:, :3 * C], s2w.wm0, None, gy[:, :3 * H]),
+                              (gm[:, 3 * C:7 * C], s2w.w1_t, None, gy[:, 3 * H:7 * H]),
+                              (gm[:, 7 * C:], s2w.w2_t, None, gy[:, 7 * H:])])
             o1, g1 = c.o1c, self.g1c
             nat.gate_bwd(self.g_y, o1[:, LH:], o1, g1[:, LH:], g1, bb.gate_idx_mprime, R=E, H=H,
                          L=L, ldx=LHc, ldg=LHc)
             gx = self.g_xf.view(E, NSPH * Cin)
-            nat.linear(g1[:, :LH + 3 * H], s1w.wm0, out=gx[:, :3 * Cin])
-            nat.linear(g1[:, LH + 3 * H:LH + 7 * H], s1w.w1_t, out=gx[:, 3 * Cin:7 * Cin])
-            nat.linear(g1[:, LH + 7 * H:], s1w.w2_t, out=gx[:, 7 * Cin:])
+            nat.linear_group([(g1[:, :LH + 3 * H], s1w.wm0, None, gx[:, :3 * Cin]),
+                              (g1[:, LH + 3 * H:LH + 7 * H], s1w.w1_t, None,
+                               gx[:, 3 * Cin:7 * Cin]),
+                              (g1[:, LH + 7 * H:], s1w.w2_t, None, gx[:, 7 * Cin:])])
             nat.gather_rotate_bw(self.g_xf, c.rad.out, c.n1, g.src, g.tgt, self.coef, self.g_rad,
                                  self.g_mcat, self.g_coef)
             g_n1 = self.gn_a

@@ -62,11 +62,12 @@ int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const float* bias, 
                    int mode, const float* P, int64_t ldp, const int* idx0, const int* idx1,
                    int64_t off1, int64_t n_rows_p, int epilogue, tta_stream_t stream);
 
-/* Up to 4 independent products in one launch (tta_gemm_problem; row-gather terms not
+/* Up to 8 independent products in one launch (tta_gemm_problem; row-gather terms not
  * supported): the split-bf16 kernel with packed B operands, or the fp32 kernel with fp32 B.
  * The three SO(2) m-block contractions of one convolution (so2.py:106-115, 282-294, and the
  * transposed products of their VJP, forces.py:23-36), which the reference issues one by one,
- * share the edge rows and run as one launch.  Same checks and results as one call per product;
+ * share the edge rows and run as one launch, as do the same layer of the radial MLPs of all
+ * blocks.  Same checks and results as one call per product;
  * empty products are skipped. */
 int tta_gemm_bf16x_group(const tta_gemm_problem* probs, int64_t n, int mode, tta_stream_t stream);
 int tta_gemm_f32_group(const tta_gemm_problem* probs, int64_t n, tta_stream_t stream);
@@ -134,12 +135,15 @@ int tta_gate_bwd(const float* g_y, const float* x, const float* gating, float* g
 
 /* Radial MLP LayerNorm + SiLU: nrm = LN(a), s = silu(nrm) (so2.py:101-115) and its backward
  * g_a (so2.py:117-143; ttnn.experimental.fused_ln_bw, fused_ln_bw.hpp:14-21).  Row strides:
- * a / nrm lda, s lds, g ldg, g_a ldo. */
+ * a / nrm lda, s lds, g ldg, g_a ldo.  `groups` LayerNorms of width n side by side in each row
+ * (group k = columns k n .. k n + n - 1, gamma / beta [groups, n]): the radial MLPs of the
+ * edge-degree embedding and of every block, which the reference runs one after another. */
 int tta_ln_silu_fwd(const float* a, const float* gamma, const float* beta, float* nrm, float* s,
-                    int64_t R, int64_t n, int64_t lda, int64_t lds, float eps, tta_stream_t stream);
+                    int64_t R, int64_t n, int64_t groups, int64_t lda, int64_t lds, float eps,
+                    tta_stream_t stream);
 int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm, const float* gamma,
-                    float* g_a, int64_t R, int64_t n, int64_t ldg, int64_t lda, int64_t ldo,
-                    float eps, tta_stream_t stream);
+                    float* g_a, int64_t R, int64_t n, int64_t groups, int64_t ldg, int64_t lda,
+                    int64_t ldo, float eps, tta_stream_t stream);
 
 /* RMSNormSH (norm.py:59-111) with an optional l=0 addend (the system embedding of
  * model.py:164-167); inv [N] kept for the backward (forces.py:49-98; res = residual adjoint). */

@@ -519,3 +519,32 @@ def test_linear_group_equals_separate_calls(nat, split):
     assert outs[True][1][:, :640].abs().max() == 0 and outs[True][1][:, 1152:].abs().max() == 0
     ref = x[:, :384].double().cpu() @ ws[0].w_t.double().cpu() + bias.double().cpu()
     assert (outs[True][0][:, :640].cpu().double() - ref).abs().max() < 1e-3
+
+
+@pytest.mark.parametrize("n", [64, 128, 200])
+def test_ln_silu_groups_equal_per_group(nat, n):
+    """Grouped LayerNorm-SiLU (five radial MLPs side by side, odd row count) gives the same bits
+    as one call per column block."""
+    R, G = 1001, 5
+    g = torch.Generator().manual_seed(n + 1)
+    a = (torch.randn(R, G * n, generator=g) * 2 + 0.3).to(DEV)
+    gam = (1 + 0.1 * torch.randn(G * n, generator=g)).to(DEV)
+    bet = (0.1 * torch.randn(G * n, generator=g)).to(DEV)
+    gy = torch.randn(R, G * n, generator=g).to(DEV)
+    outs = []
+    for grouped in (True, False):
+        nrm, s, ga = (torch.full((R, G * n), float("nan"), device=DEV) for _ in range(3))
+        if grouped:
+            nat.ln_silu_fwd(a, gam, bet, nrm, s, R=R, n=n, groups=G)
+            nat.ln_silu_bwd(gy, a, nrm, gam, ga, R=R, n=n, groups=G)
+        else:
+            for k in range(G):
+                c = slice(k * n, (k + 1) * n)
+                nat.ln_silu_fwd(a[:, c], gam[c], bet[c], nrm[:, c], s[:, c], R=R, n=n,
+                                lda=G * n, lds=G * n)
+                nat.ln_silu_bwd(gy[:, c], a[:, c], nrm[:, c], gam[c], ga[:, c], R=R, n=n,
+                                ldg=G * n, lda=G * n, ldo=G * n)
+        torch.cuda.synchronize()
+        outs.append((nrm.clone(), s.clone(), ga.clone()))
+    for x, y in zip(*outs):
+        assert not bool(x.isnan().any()) and torch.equal(x, y)

@@ -33,7 +33,7 @@ struct GemmArgs {
 // kernels of a plain call see a group of one; the fp32 kernel's strided batch uses blockIdx.z
 // itself and is not combined with a group).  vec / NT32 are per product: the fp32 kernel's float4
 // path and the split kernel's packed-B column tiles.
-constexpr int kMaxGroup = 4;
+constexpr int kMaxGroup = 8;
 struct GemmGroup {
   GemmArgs p[kMaxGroup];
   int NT32[kMaxGroup];

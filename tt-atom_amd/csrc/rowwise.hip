@@ -69,20 +69,28 @@ __global__ __launch_bounds__(256) void k_gate_bwd(const float* __restrict__ g_y,
 // nothing, so every lane of the wave takes part in the butterflies.  Forward (so2.py:101-115 /
 // geometry.py:161-168):
 //   nrm = (a - mean) * rstd * gamma + beta,  s = silu(nrm)
-// a and nrm rows have stride lda, s rows stride lds.
+// a and nrm rows have stride lda, s rows stride lds.  `groups` independent LayerNorms per row
+// (the radial MLPs of several blocks side by side): group k of a row is the n columns from k n,
+// with gamma / beta [groups, n]; a row of a wavefront is one (row, group) pair.
 template <int G, int NPL>
 __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a,
                                                      const float* __restrict__ gamma,
                                                      const float* __restrict__ beta,
                                                      float* __restrict__ nrm,
                                                      float* __restrict__ s, int64_t R, int n,
-                                                     int64_t lda, int64_t lds, float eps) {
+                                                     int groups, int64_t lda, int64_t lds,
+                                                     float eps) {
+  const int64_t RV = R * groups;
   const int64_t rw = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / G;
   const int lane = threadIdx.x & (G - 1);
-  if ((rw / (64 / G)) * (64 / G) >= R) return;  // whole wavefront past the end
-  const bool valid = rw < R;
-  const int64_t row = valid ? rw : R - 1;
-  const float* ar = a + row * lda;
+  if ((rw / (64 / G)) * (64 / G) >= RV) return;  // whole wavefront past the end
+  const bool valid = rw < RV;
+  const int64_t vr = valid ? rw : RV - 1;
+  const int64_t row = vr / groups;
+  const int co = (int)(vr - row * groups) * n;  // column offset of the group
+  gamma += co;
+  beta += co;
+  const float* ar = a + row * lda + co;
   float v[NPL];
   float sum = 0.f;
 #pragma unroll
@@ -106,8 +114,8 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
     const int i = lane + G * k;
     if (i >= n) continue;
     const float y = (v[k] - mean) * rstd * gamma[i] + beta[i];
-    nrm[row * lda + i] = y;
-    s[row * lds + i] = tta_silu(y);
+    nrm[row * lda + co + i] = y;
+    s[row * lds + co + i] = tta_silu(y);
   }
 }
 
@@ -121,14 +129,18 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
                                                      const float* __restrict__ nrm,
                                                      const float* __restrict__ gamma,
                                                      float* __restrict__ g_a, int64_t R, int n,
-                                                     int64_t ldg, int64_t lda, int64_t ldo,
-                                                     float eps) {
+                                                     int groups, int64_t ldg, int64_t lda,
+                                                     int64_t ldo, float eps) {
+  const int64_t RV = R * groups;
   const int64_t rw = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / G;
   const int lane = threadIdx.x & (G - 1);
-  if ((rw / (64 / G)) * (64 / G) >= R) return;
-  const bool valid = rw < R;
-  const int64_t row = valid ? rw : R - 1;
-  const float* ar = a + row * lda;
+  if ((rw / (64 / G)) * (64 / G) >= RV) return;
+  const bool valid = rw < RV;
+  const int64_t vr = valid ? rw : RV - 1;
+  const int64_t row = vr / groups;
+  const int co = (int)(vr - row * groups) * n;
+  gamma += co;
+  const float* ar = a + row * lda + co;
   float av[NPL], gy[NPL];
   float sum = 0.f;
 #pragma unroll
@@ -136,7 +148,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
     const int i = lane + G * k;
     const bool in = i < n;
     av[k] = in ? ar[i] : 0.f;
-    gy[k] = in ? g[row * ldg + i] * tta_silu_grad(nrm[row * lda + i]) * gamma[i] : 0.f;
+    gy[k] = in ? g[row * ldg + co + i] * tta_silu_grad(nrm[row * lda + co + i]) * gamma[i] : 0.f;
     sum += av[k];
   }
   const float mean = tta_group_sum(sum, G) / n;
@@ -161,7 +173,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
     const int i = lane + G * k;
     if (i >= n) continue;
     const float xh = (av[k] - mean) * rstd;
-    g_a[row * ldo + i] = rstd * (gy[k] - m1 - xh * m2);
+    g_a[row * ldo + co + i] = rstd * (gy[k] - m1 - xh * m2);
   }
 }
 
@@ -410,15 +422,17 @@ extern "C" int tta_gate_bwd(const float* g_y, const float* x, const float* gatin
 }
 
 extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* beta, float* nrm,
-                               float* s, int64_t R, int64_t n, int64_t lda, int64_t lds,
-                               float eps, hipStream_t stream) {
-  TTA_CHECK_ARG(R >= 0 && n > 0 && n <= 512 && lda >= n && lds >= n,
-                "tta_ln_silu_fwd: bad sizes (row width 1..512)");
+                               float* s, int64_t R, int64_t n, int64_t groups, int64_t lda,
+                               int64_t lds, float eps, hipStream_t stream) {
+  TTA_CHECK_ARG(R >= 0 && n > 0 && n <= 512 && groups >= 1 && groups <= 64 &&
+                    lda >= groups * n && lds >= groups * n && R * groups < ((int64_t)1 << 40),
+                "tta_ln_silu_fwd: bad sizes (row width 1..512, 1..64 groups)");
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(a && gamma && beta && nrm && s, "tta_ln_silu_fwd: null pointer");
+  const int64_t RV = R * groups;
 #define TTA_LN_FWD(G, NPL)                                                                  \
-  hipLaunchKernelGGL((k_ln_silu_fwd<G, NPL>), dim3(tta_blocks(R * G, 256)), dim3(256), 0, stream, \
-                     a, gamma, beta, nrm, s, R, (int)n, lda, lds, eps)
+  hipLaunchKernelGGL((k_ln_silu_fwd<G, NPL>), dim3(tta_blocks(RV * G, 256)), dim3(256), 0,    \
+                     stream, a, gamma, beta, nrm, s, R, (int)n, (int)groups, lda, lds, eps)
   if (n <= 32)
     TTA_LN_FWD(32, 1);
   else if (n <= 64)
@@ -435,15 +449,19 @@ extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* 
 }
 
 extern "C" int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm,
-                               const float* gamma, float* g_a, int64_t R, int64_t n, int64_t ldg,
-                               int64_t lda, int64_t ldo, float eps, hipStream_t stream) {
-  TTA_CHECK_ARG(R >= 0 && n > 0 && n <= 512 && ldg >= n && lda >= n && ldo >= n,
-                "tta_ln_silu_bwd: bad sizes (row width 1..512)");
+                               const float* gamma, float* g_a, int64_t R, int64_t n,
+                               int64_t groups, int64_t ldg, int64_t lda, int64_t ldo, float eps,
+                               hipStream_t stream) {
+  TTA_CHECK_ARG(R >= 0 && n > 0 && n <= 512 && groups >= 1 && groups <= 64 &&
+                    ldg >= groups * n && lda >= groups * n && ldo >= groups * n &&
+                    R * groups < ((int64_t)1 << 40),
+                "tta_ln_silu_bwd: bad sizes (row width 1..512, 1..64 groups)");
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(g && a && nrm && gamma && g_a, "tta_ln_silu_bwd: null pointer");
+  const int64_t RV = R * groups;
 #define TTA_LN_BWD(G, NPL)                                                                  \
-  hipLaunchKernelGGL((k_ln_silu_bwd<G, NPL>), dim3(tta_blocks(R * G, 256)), dim3(256), 0, stream, \
-                     g, a, nrm, gamma, g_a, R, (int)n, ldg, lda, ldo, eps)
+  hipLaunchKernelGGL((k_ln_silu_bwd<G, NPL>), dim3(tta_blocks(RV * G, 256)), dim3(256), 0,    \
+                     stream, g, a, nrm, gamma, g_a, R, (int)n, (int)groups, ldg, lda, ldo, eps)
   if (n <= 32)
     TTA_LN_BWD(32, 1);
   else if (n <= 64)

@@ -44,8 +44,8 @@ _SIGS = {
     "tta_node_gather_sum": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_gate_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "tta_gate_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
-    "tta_ln_silu_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _P],
-    "tta_ln_silu_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
+    "tta_ln_silu_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
+    "tta_ln_silu_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "tta_rmsnorm_sh_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _P],
     "tta_rmsnorm_sh_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _P],
     "tta_silu_bwd": [_P, _P, _P, _I64, _P],
@@ -313,7 +313,7 @@ def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None)
     return out
 
 
-MAX_GROUP = 4
+MAX_GROUP = 8
 
 
 def linear_group(items):
@@ -498,23 +498,27 @@ def gate_bwd(g_y, x, gating, g_x, g_gating, idx8, *, R, H, L, ldx=None, ldg=None
               _i32(idx8, 8, "idx8"), _stream())
 
 
-def ln_silu_fwd(a, gamma, beta, nrm, s, *, R, n, lda=None, lds=None, eps=1e-5):
-    lda = n if lda is None else lda
-    lds = n if lds is None else lds
-    _hbm_call("k_ln_silu_fwd", 4 * (3 * R * n + 2 * n), "tta_ln_silu_fwd",
-              _rows(a, R, lda, n, "a"), _ptr(gamma, numel=n), _ptr(beta, numel=n),
-              _rows(nrm, R, lda, n, "nrm"), _rows(s, R, lds, n, "s"), R, n, lda, lds, eps,
-              _stream())
+def ln_silu_fwd(a, gamma, beta, nrm, s, *, R, n, groups=1, lda=None, lds=None, eps=1e-5):
+    """``groups`` LayerNorms of width n side by side per row (gamma / beta [groups * n])."""
+    w = groups * n
+    lda = w if lda is None else lda
+    lds = w if lds is None else lds
+    _hbm_call("k_ln_silu_fwd", 4 * (3 * R * w + 2 * w), "tta_ln_silu_fwd",
+              _rows(a, R, lda, w, "a"), _ptr(gamma, numel=w), _ptr(beta, numel=w),
+              _rows(nrm, R, lda, w, "nrm"), _rows(s, R, lds, w, "s"), R, n, groups, lda, lds,
+              eps, _stream())
 
 
-def ln_silu_bwd(g, a, nrm, gamma, g_a, *, R, n, ldg=None, lda=None, ldo=None, eps=1e-5):
-    ldg = n if ldg is None else ldg
-    lda = n if lda is None else lda
-    ldo = n if ldo is None else ldo
-    _hbm_call("k_ln_silu_bwd", 4 * (4 * R * n + n), "tta_ln_silu_bwd",
-              _rows(g, R, ldg, n, "g"), _rows(a, R, lda, n, "a"), _rows(nrm, R, lda, n, "nrm"),
-              _ptr(gamma, numel=n), _rows(g_a, R, ldo, n, "g_a"), R, n, ldg, lda, ldo, eps,
-              _stream())
+def ln_silu_bwd(g, a, nrm, gamma, g_a, *, R, n, groups=1, ldg=None, lda=None, ldo=None,
+                eps=1e-5):
+    w = groups * n
+    ldg = w if ldg is None else ldg
+    lda = w if lda is None else lda
+    ldo = w if ldo is None else ldo
+    _hbm_call("k_ln_silu_bwd", 4 * (4 * R * w + w), "tta_ln_silu_bwd",
+              _rows(g, R, ldg, w, "g"), _rows(a, R, lda, w, "a"), _rows(nrm, R, lda, w, "nrm"),
+              _ptr(gamma, numel=w), _rows(g_a, R, ldo, w, "g_a"), R, n, groups, ldg, lda, ldo,
+              eps, _stream())
 
 
 def rmsnorm_sh_fwd(x, aw, ab, add0, y, inv, eps=1e-5):

@@ -216,6 +216,10 @@ class Backbone:
         self.rad_w0g_all = _gw(torch.cat([r.w0g for r in self.radials], 0).contiguous(), dev, mode)
         if len({r.hidden for r in self.radials}) != 1 or len({r.k_in for r in self.radials}) != 1:
             raise RuntimeError(_UNSUPPORTED.format(what="radial MLPs of different widths"))
+        # the LayerNorm parameters of all radial MLPs side by side (grouped LayerNorm-SiLU)
+        cat = lambda name: torch.cat([getattr(r, name) for r in self.radials]).contiguous()
+        self.rad_ln1w_all, self.rad_ln1b_all = cat("ln1w"), cat("ln1b")
+        self.rad_ln4w_all, self.rad_ln4b_all = cat("ln4w"), cat("ln4b")
         self.gate_idx_mprime = torch.tensor(GATE_IDX_MPRIME, dtype=torch.int32, device=dev)
         self.gate_idx_natural = torch.tensor(GATE_IDX_NATURAL, dtype=torch.int32, device=dev)
 

@@ -81,27 +81,28 @@ class TracedEngine:
         self.g_coef, self.g_env, self.g_gauss = emp(E, 35), emp(E), emp(E, nb)
         self.g_ev, self.forces = emp(E, 3), emp(N, 3)
         self.energy_buf, self.virial_buf, self.virial_work = emp(1), emp(9), emp(256 * 9)
-        # radial MLPs: stacked first layer (pre-LN a0 and LN output of every radial)
+        # radial MLPs side by side (edge-degree, then block 0..L-1): pre-LN, LN and SiLU outputs of
+        # both hidden layers, and the adjoints
         self.a0_all, self.nrm1_all, self.g_a0_all = (emp(E, nrad * hid) for _ in range(3))
+        self.s1_all, self.a3_all, self.nrm4_all, self.s2_all = (emp(E, nrad * hid)
+                                                                for _ in range(4))
+        self.t1_all, self.t2_all = emp(E, nrad * hid), emp(E, nrad * hid)
         # shared edge temporaries
         self.LHc = L * H + NSPH * H                      # combined conv-1 row [gating | out]
         self.xf, self.g_xf, self.g_mcat = emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C)
         self.y, self.g_y = emp(E, NSPH, H), emp(E, NSPH, H)
         self.g1c = emp(E, self.LHc)
         self.g_mso2 = emp(E, NSPH, C)
-        self.g_rad = emp(E, 6 * 2 * C)
-        self.s1, self.s2 = emp(E, hid), emp(E, hid)
-        self.t1, self.t2 = emp(E, hid), emp(E, hid)
-        # per-radial caches (second LN and the output)
-        self.ed = self._radial_cache(E, hid, 3 * C, dev, 0)
-        self.g_edm = emp(E, 3 * C)
+        # per-radial output caches and their adjoints (kept per block: the radial backward of all
+        # blocks runs once, after the blocks)
+        self.ed = self._radial_cache(E, 3 * C, dev, 0)
         # per-block caches
         self.blk = []
         for i, b in enumerate(bb.blocks):
             c = _Buf()
             c.x_in, c.n1, c.x1, c.n2 = (emp(N, NSPH, C) for _ in range(4))
             c.inv1, c.inv2 = emp(N), emp(N)
-            c.rad = self._radial_cache(E, hid, 6 * 2 * C, dev, 1 + i)
+            c.rad = self._radial_cache(E, 6 * 2 * C, dev, 1 + i)
             c.o1c, c.mso2 = emp(E, self.LHc), emp(E, NSPH, C)
             if b.ff_type == "spectral":
                 c.a_s, c.gat, c.h, c.gout = emp(N, L * H), emp(N, L * H), emp(N, NSPH, H), emp(N, NSPH, H)
@@ -122,32 +123,43 @@ class TracedEngine:
         P = max([b.atom_wise.npts for b in bb.blocks if b.ff_type != "spectral"], default=0)
         self.gt1, self.gt2 = emp(N * P, C), emp(N * P, C)
 
-    def _radial_cache(self, E, hid, n_out, dev, r):
+    def _radial_cache(self, E, n_out, dev, r):
         c = _Buf()
         f32 = dict(device=dev, dtype=torch.float32)
         c.r = r
-        c.a3, c.nrm4 = torch.empty(E, hid, **f32), torch.empty(E, hid, **f32)
         c.out = torch.empty(E, n_out, **f32)
+        c.g_out = torch.empty(E, n_out, **f32)
         return c
 
-    # ------------------------------------------------------------------ radial MLP
-    def _radial_fwd(self, rw, c):
-        E, hid, ld = self.E, self.hid, self.nrad * self.hid
-        sl = slice(c.r * hid, (c.r + 1) * hid)
-        nat.ln_silu_fwd(self.a0_all[:, sl], rw.ln1w, rw.ln1b, self.nrm1_all[:, sl], self.s1,
-                        R=E, n=hid, lda=ld, lds=hid)
-        nat.linear(self.s1, rw.w3t, rw.b3, out=c.a3)
-        nat.ln_silu_fwd(c.a3, rw.ln4w, rw.ln4b, c.nrm4, self.s2, R=E, n=hid)
-        nat.linear(self.s2, rw.w6t, rw.b6, out=c.out)
+    # ------------------------------------------------------------------ radial MLPs
+    # The radial MLPs of the edge-degree embedding and of every block (so2.py:54-163) depend only
+    # on the edge features, so they run side by side: one grouped LayerNorm-SiLU per hidden layer
+    # and one grouped GEMM launch per linear, forward before the blocks and backward after them.
+    def _radials_fwd(self):
+        bb, E, hid, R = self.bb, self.E, self.hid, self.nrad
+        col = lambda t, r: t[:, r * hid:(r + 1) * hid]
+        caches = [self.ed] + [c.rad for c in self.blk]
+        nat.ln_silu_fwd(self.a0_all, bb.rad_ln1w_all, bb.rad_ln1b_all, self.nrm1_all, self.s1_all,
+                        R=E, n=hid, groups=R)
+        nat.linear_group([(col(self.s1_all, r), rw.w3t, rw.b3, col(self.a3_all, r))
+                          for r, rw in enumerate(bb.radials)])
+        nat.ln_silu_fwd(self.a3_all, bb.rad_ln4w_all, bb.rad_ln4b_all, self.nrm4_all, self.s2_all,
+                        R=E, n=hid, groups=R)
+        nat.linear_group([(col(self.s2_all, r), rw.w6t, rw.b6, c.out)
+                          for r, (rw, c) in enumerate(zip(bb.radials, caches))])
 
-    def _radial_bwd(self, rw, c, g_out):
-        E, hid, ld = self.E, self.hid, self.nrad * self.hid
-        sl = slice(c.r * hid, (c.r + 1) * hid)
-        nat.linear(g_out, rw.w6, out=self.t1)
-        nat.ln_silu_bwd(self.t1, c.a3, c.nrm4, rw.ln4w, self.t2, R=E, n=hid)
-        nat.linear(self.t2, rw.w3, out=self.t1)
-        nat.ln_silu_bwd(self.t1, self.a0_all[:, sl], self.nrm1_all[:, sl], rw.ln1w,
-                        self.g_a0_all[:, sl], R=E, n=hid, ldg=hid, lda=ld, ldo=ld)
+    def _radials_bwd(self):
+        bb, E, hid, R = self.bb, self.E, self.hid, self.nrad
+        col = lambda t, r: t[:, r * hid:(r + 1) * hid]
+        caches = [self.ed] + [c.rad for c in self.blk]
+        nat.linear_group([(c.g_out, rw.w6, None, col(self.t1_all, r))
+                          for r, (rw, c) in enumerate(zip(bb.radials, caches))])
+        nat.ln_silu_bwd(self.t1_all, self.a3_all, self.nrm4_all, bb.rad_ln4w_all, self.t2_all,
+                        R=E, n=hid, groups=R)
+        nat.linear_group([(col(self.t2_all, r), rw.w3, None, col(self.t1_all, r))
+                          for r, rw in enumerate(bb.radials)])
+        nat.ln_silu_bwd(self.t1_all, self.a0_all, self.nrm1_all, bb.rad_ln1w_all, self.g_a0_all,
+                        R=E, n=hid, groups=R)
 
     # ------------------------------------------------------------------ feed-forward
     def _spectral_fwd(self, aw, c, x, res, out):
@@ -205,8 +217,8 @@ class TracedEngine:
         nat.edge_features(self.dist, g.zsrc, g.ztgt, bb.src_emb, bb.tgt_emb, geo.offset,
                           geo.coeff, geo.cutoff, self.nb, self.ec, self.x_edge, self.env)
         nat.linear(self.x_edge, bb.rad_w0t_all, bb.rad_b0_all, out=self.a0_all)
+        self._radials_fwd()
         # edge-degree node init (geometry.py:268-276)
-        self._radial_fwd(bb.edge_degree, self.ed)
         x = self.blk[0].x_in if self.blk else self.x_final
         nat.rotate_env_segsum(self.ed.out, self.coef, self.env, g.tgt_ptr, self.l0, x, n_in=3,
                               env_first=False, div=geo.rescale)
@@ -214,7 +226,6 @@ class TracedEngine:
         for i, (bw, c) in enumerate(zip(bb.blocks, self.blk)):
             s1w, s2w = bw.so2_1, bw.so2_2
             nat.rmsnorm_sh_fwd(c.x_in, bw.norm_1.aw, bw.norm_1.ab, self.sys_emb, c.n1, c.inv1)
-            self._radial_fwd(s1w.rad, c.rad)
             nat.gather_rotate(c.n1, g.src, g.tgt, self.coef, c.rad.out, self.xf)
             xf = self.xf.view(E, NSPH * Cin)
             o1 = c.o1c
@@ -288,19 +299,18 @@ class TracedEngine:
                               (g1[:, LH + 3 * H:LH + 7 * H], s1w.w1_t, None,
                                gx[:, 3 * Cin:7 * Cin]),
                               (g1[:, LH + 7 * H:], s1w.w2_t, None, gx[:, 7 * Cin:])])
-            nat.gather_rotate_bw(self.g_xf, c.rad.out, c.n1, g.src, g.tgt, self.coef, self.g_rad,
-                                 self.g_mcat, self.g_coef)
+            nat.gather_rotate_bw(self.g_xf, c.rad.out, c.n1, g.src, g.tgt, self.coef,
+                                 c.rad.g_out, self.g_mcat, self.g_coef)
             g_n1 = self.gn_a
             nat.node_gather_sum(self.g_mcat, g.src_ptr, g.src_perm, g.tgt_ptr, None, g_n1)
             g_in = self.gn_b
             nat.rmsnorm_sh_bwd(g_n1, c.x_in, bw.norm_1.aw, c.inv1, g_x1, g_in)
             gcur = g_in
-            self._radial_bwd(s1w.rad, c.rad, self.g_rad)
         # edge-degree init backward (edge_degree.py:69-93)
-        nat.rotate_env_segsum_bw(gcur, g.tgt, self.ed.out, self.coef, self.env, self.g_edm,
+        nat.rotate_env_segsum_bw(gcur, g.tgt, self.ed.out, self.coef, self.env, self.ed.g_out,
                                  self.g_coef, self.g_env, n_in=3, env_first=False,
                                  div=self.geo.rescale)
-        self._radial_bwd(bb.edge_degree, self.ed, self.g_edm)
+        self._radials_bwd()
         # gaussian columns of x_edge: one GEMM over the stacked first-layer adjoints
         nat.linear(self.g_a0_all, bb.rad_w0g_all, out=self.g_gauss)
         # geometry VJP -> forces (forces.py:580-589 in closed form)

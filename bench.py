@@ -638,6 +638,10 @@ def main():
                                   "second pass of the same steps"),
                      "gemm_families": others},
         "hbm_kernels": hbm.summary(),
+        "hbm_kernels_note": ("fractions of the 8 TB/s peak from algorithmic bytes, which count "
+                             "every operand use: node rows gathered per edge are counted per "
+                             "edge although most hit in the L2 / MALL, so a gather kernel can "
+                             "read above 1 (k_gather_rotate)"),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = (cpu_baseline_c5(torch) if wl == "c5" else

@@ -397,14 +397,16 @@ class OrbEngine:
         m, g = self.m, self.g
         nat.orb_edge_features(pos, g.send, g.recv, g.shift, m.r_max, m.nb, self.vec, self.feat,
                               self.cut)
-        # encoder: node path (position independent, not differentiated) and edge path
-        en = m.enc_node
-        nat.linear(self.x_node, en.w_t[0], en.b[0], out=self.enc_h0, epilogue=nat.EPI_SILU)
-        nat.linear(self.enc_h0, en.w_t[1], en.b[1], out=self.enc_h1, epilogue=nat.EPI_SILU)
-        nat.linear(self.enc_h1, en.w_t[2], en.b[2], out=self.hn_out)
+        # encoder: node path (position independent, not differentiated) and edge path; the two
+        # MLPs are independent, so each of their layers is one grouped launch
+        en, ee = m.enc_node, m.enc_edge
+        nat.linear_group([(self.x_node, en.w_t[0], en.b[0], self.enc_h0, nat.EPI_SILU),
+                          (self.feat, ee.w_t[0], ee.b[0], self.ea0, nat.EPI_PRE_SILU, self.h0)])
+        nat.linear_group([(self.enc_h0, en.w_t[1], en.b[1], self.enc_h1, nat.EPI_SILU),
+                          (self.h0, ee.w_t[1], ee.b[1], self.ea1, nat.EPI_PRE_SILU, self.h1)])
+        nat.linear_group([(self.enc_h1, en.w_t[2], en.b[2], self.hn_out),
+                          (self.h1, ee.w_t[2], ee.b[2], self.eh2)])
         nat.rms_residual(self.hn_out, en.norm, None, None, self.nodes[0], None)
-        ee = m.enc_edge
-        self._mlp3(ee, self.feat, self.ea0, self.h0, self.ea1, self.h1, self.eh2)
         L0 = m.layers[0] if m.layers else None
         nat.rms_residual(self.eh2, ee.norm, None, None, self.edges[0], self.einv,
                          None if L0 is None else L0.attn_w, None if L0 is None else L0.attn_b,
@@ -460,10 +462,11 @@ class OrbEngine:
                        aux=self.a1[l])
             nat.linear(self.h1, lay.edge.w[1], out=self.h0, epilogue=nat.EPI_SILU_GRAD,
                        aux=self.a0[l])
-            nat.linear(self.h0, lay.we, out=self.g_e, epilogue=nat.EPI_ACCUM)
             nat.orb_node_segsum2(self.h0, g.send_ptr, g.recv_ptr, g.recv_perm, self.G)
             nat.add_rows(self.g_node_in[:, :C], self.g_n)
-            nat.linear(self.G, lay.wsr, out=self.g_n, epilogue=nat.EPI_ACCUM)
+            # the edge input adjoint and the node adjoint through [W_s | W_r]: one launch
+            nat.linear_group([(self.h0, lay.we, None, self.g_e, nat.EPI_ACCUM),
+                              (self.G, lay.wsr, None, self.g_n, nat.EPI_ACCUM)])
         ee = m.enc_edge
         nat.rms_bwd(self.g_e, self.eh2, ee.norm, self.einv, self.g_h2)
         nat.linear(self.g_h2, ee.w[2], out=self.h1, epilogue=nat.EPI_SILU_GRAD, aux=self.ea1)

@@ -12,13 +12,13 @@ blocks, energy head, the full reverse pass and the geometric VJP, all in HIP ker
 ``value`` = atoms * steps / wall time of the timed steps (atom-steps/s).
 
 Also reported on the same JSON line:
-  roofline      the dominant kernel (the split-bf16 MFMA GEMM that runs the edge-level
+  roofline      the dominant kernel (the split MFMA GEMM that runs the edge-level
                 contractions at fp32 accuracy): algorithmic FLOPs (2MNK) of its launches / their
                 HIP-event durations (recorded on the launch stream during a second pass of the
                 same K steps, so that the timed pass carries no instrumentation), against
-                the ceiling of its arithmetic (bf16 dense MFMA peak 2.5 PFLOP/s / 6 plane
+                the ceiling of its arithmetic (fp16 dense MFMA peak 2.5 PFLOP/s / 3 plane
                 products); ``traffic`` = HBM bytes per launch from rocprofv3 FETCH_SIZE +
-                WRITE_SIZE when profiles/gemm_bf16x6_traffic_c3.txt holds them, else null.  The
+                WRITE_SIZE when profiles/gemm_f16x3_traffic_c3.txt holds them, else null.  The
                 other GEMM kernel family (fp32 MFMA, node-level and short-K products) is listed
                 under ``gemm_families``; ``hbm_kernels`` gives the same for the HBM-bound edge
                 kernels (rotation, segment sums) against the 8 TB/s HBM peak.
@@ -41,18 +41,21 @@ for p in (ROOT, ROOT / "tt-atom_amd"):
         sys.path.insert(0, str(p))
 
 METRIC = "atom-steps/s (energy+forces), uma-s-1 arch 2,048 atoms; % HBM/MFMA roofline"
-# MI355X published dense peaks (TFLOP/s).  The split-bf16 GEMM computes an fp32-accurate product
-# with 6 bf16 plane products (mode 6): its fp32-equivalent ceiling is the bf16 peak / 6.
+# MI355X published dense peaks (TFLOP/s).  The split GEMM computes an fp32-accurate product with
+# 3 fp16 plane products (mode 16, the default) or 6 bf16 plane products (mode 6): its
+# fp32-equivalent ceiling is the fp16 / bf16 dense peak (both 2.5 PFLOP/s) / number of products.
 PEAK_FP32_MFMA = 157.3
 PEAK_HBM_GBPS = 8000.0
 PEAK_BF16_MFMA = 2500.0
-PEAKS = {"f32": PEAK_FP32_MFMA, "bf16x6": PEAK_BF16_MFMA / 6, "bf16x3": PEAK_BF16_MFMA / 3,
-         "bf16x1": PEAK_BF16_MFMA}
+PEAKS = {"f32": PEAK_FP32_MFMA, "f16x3": PEAK_BF16_MFMA / 3, "bf16x6": PEAK_BF16_MFMA / 6,
+         "bf16x3": PEAK_BF16_MFMA / 3, "bf16x1": PEAK_BF16_MFMA}
 KERNELS = {"f32": "gemm_f32_kernel (fp32 MFMA 16x16x4)",
+           "f16x3": "gemm_bf16x_kernel<2,16> (split-fp16, 2x2 power-of-two-scaled planes / 3 "
+                    "products, fp32-accurate)",
            "bf16x6": "gemm_bf16x_kernel<2,6> (split-bf16, 3x3 planes / 6 products, fp32-accurate)",
            "bf16x3": "gemm_bf16x_kernel<2,3> (split-bf16, 2x2 planes / 3 products)",
            "bf16x1": "gemm_bf16x_kernel<2,1> (bf16 operands)"}
-TRAFFIC_FILE = ROOT / "profiles" / "gemm_bf16x6_traffic_c3.txt"
+TRAFFIC_FILE = ROOT / "profiles" / "gemm_f16x3_traffic_c3.txt"
 
 
 class GemmEvents:
@@ -399,9 +402,10 @@ def main():
                     help="c3 (headline), c2 (isolated edgewise kernel), c4 (periodic + stress), "
                          "c5 (Orb-v3 batch) or batch (small-system evaluate_batch throughput "
                          "against the reference's published numbers)")
-    ap.add_argument("--precision", choices=("f32", "f32-mfma", "bf16"), default="f32",
-                    help="GEMM arithmetic: f32 (split-bf16, fp32-accurate), f32-mfma, or bf16 "
-                         "operands (the bf16 variants of C2 / C5)")
+    ap.add_argument("--precision", choices=("f32", "f32-bf16x6", "f32-mfma", "bf16"), default="f32",
+                    help="GEMM arithmetic: f32 (scaled split-fp16, fp32-accurate), f32-bf16x6 "
+                         "(split-bf16, fp32-accurate), f32-mfma, or bf16 operands (the bf16 "
+                         "variants of C2 / C5)")
     ap.add_argument("--eager", action="store_true",
                     help="launch the step kernel by kernel instead of replaying its HIP graph "
                          "(for profilers)")
@@ -569,7 +573,7 @@ def main():
     dom = max(fam, key=lambda k: fam[k]["ms"])
     d = fam[dom]
     achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12 if d["ms"] > 0 else 0.0
-    traffic = read_traffic() if (wl == "c3" and dom == "bf16x6" and args.precision == "f32") \
+    traffic = read_traffic() if (wl == "c3" and dom == "f16x3" and args.precision == "f32") \
         else None
     ms_step = dt / args.steps * 1e3
     others = {k: {"launches": v["n"], "avg_launch_us": round(v["ms"] * 1e3 / max(1, v["n"]), 2),
@@ -631,8 +635,8 @@ def main():
                      "algorithmic_flops_per_launch": round(d["flops"] / max(1, d["n"])),
                      "avg_launch_us": round(d["ms"] * 1e3 / max(1, d["n"]), 2),
                      "peak_note": ("algorithmic fp32 GEMM flops (2MNK) against the ceiling of "
-                                   "the kernel's arithmetic: fp32 MFMA 157.3, or the bf16 dense "
-                                   "MFMA 2500 / number of plane products"),
+                                   "the kernel's arithmetic: fp32 MFMA 157.3, or the fp16 / bf16 "
+                                   "dense MFMA 2500 / number of plane products"),
                      "gemm_share_of_step": round(gemm_ms / (dt * 1e3), 4),
                      "measured": ("HIP events around each launch, on the launch stream, over a "
                                   "second pass of the same steps"),

@@ -45,13 +45,15 @@ int tta_gemm_f32(const float* A, const float* B, float* C, const float* bias, fl
                  int64_t ldc, int64_t batch, int64_t sA, int64_t sB, int64_t sC, int64_t sBias,
                  int epilogue, tta_stream_t stream);
 
-/* Split-bf16 GEMM on the bf16 matrix cores (same contractions as tta_gemm_f32, same epilogues,
- * plus the optional row-gather term of tta_gemm_f32_gather when P is non-NULL).  The fp32 A
- * operand is split on the fly into bf16 planes a = a0 + a1 + a2 (round-to-nearest residuals); the
- * constant B operand is packed once by tta_pack_b.  mode 6: planes 3 x 3, products
- * a0b0 + a0b1 + a1b0 + a0b2 + a2b0 + a1b1 -- fp32 GEMM accuracy; mode 3: 2 x 2 planes, 3 products
- * (~2^-16 relative); mode 1: bf16 operands.  A needs K, lda multiples of 4, lda < 2^21 and
- * 16-byte alignment.
+/* Split GEMM on the fp16 / bf16 matrix cores (same contractions as tta_gemm_f32, same
+ * epilogues, plus the optional row-gather term of tta_gemm_f32_gather when P is non-NULL).  The
+ * fp32 A operand is split on the fly into planes (round-to-nearest residuals); the constant B
+ * operand is packed once by tta_pack_b.  mode 16: two fp16 planes per operand, scaled by powers
+ * of two (B per column at packing, A per row along K), products a0b0 + a0b1 + a1b0 -- fp32 GEMM
+ * accuracy over fp32's whole range, at half the matrix work of mode 6; mode 6: 3 x 3 bf16 planes,
+ * products a0b0 + a0b1 + a1b0 + a0b2 + a2b0 + a1b1 -- fp32 GEMM accuracy; mode 3: 2 x 2 bf16
+ * planes, 3 products (~2^-16 relative); mode 1: bf16 operands.  A needs K, lda multiples of 4,
+ * lda < 2^21 and 16-byte alignment.
  * Replaces the same ttnn.linear / ttnn.matmul call sites as tta_gemm_f32 (the reference runs
  * them in bf16 / bf8 with fp32 accumulation: compute_kernel_config, device.py). */
 int64_t tta_pack_b_elems(int64_t K, int64_t N, int mode);
@@ -63,7 +65,7 @@ int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const float* bias, 
                    int64_t off1, int64_t n_rows_p, int epilogue, tta_stream_t stream);
 
 /* Up to 8 independent products in one launch (tta_gemm_problem; row-gather terms not
- * supported): the split-bf16 kernel with packed B operands, or the fp32 kernel with fp32 B.
+ * supported): the split kernel with packed B operands, or the fp32 kernel with fp32 B.
  * The three SO(2) m-block contractions of one convolution (so2.py:106-115, 282-294, and the
  * transposed products of their VJP, forces.py:23-36), which the reference issues one by one,
  * share the edge rows and run as one launch, as do the same layer of the radial MLPs of all

@@ -106,10 +106,12 @@ def test_gemm_batched_strided(nat):
 @pytest.mark.parametrize("M,N,K", [(4100, 200, 196), (8192, 640, 768), (5000, 16, 1000),
                                    (40001, 1100, 128), (9000, 300, 36)])
 @pytest.mark.parametrize("epi", [0, 2, 3, 4])
-def test_split_bf16_gemm_fp32_accuracy(nat, M, N, K, epi):
-    """Mode 6 (three bf16 planes, six products) has the accuracy of an fp32 GEMM: its error
-    relative to |A| |B| stays within the fp32 kernel's, on ragged M / N / K tails too, and with
-    thousands of tiles (40001 x 1100: 313 x 9 tiles of 128 x 128)."""
+@pytest.mark.parametrize("mode", [6, 16])
+def test_split_bf16_gemm_fp32_accuracy(nat, M, N, K, epi, mode):
+    """Mode 6 (three bf16 planes, six products) and mode 16 (two scaled fp16 planes, three
+    products) have the accuracy of an fp32 GEMM: the error relative to |A| |B| stays within the
+    fp32 kernel's, on ragged M / N / K tails too, and with thousands of tiles (40001 x 1100:
+    313 x 9 tiles of 128 x 128)."""
     g = torch.Generator().manual_seed(M + N + K)
     A = torch.randn(M, K, generator=g)
     B = torch.randn(K, N, generator=g) / math.sqrt(K)
@@ -124,7 +126,7 @@ def test_split_bf16_gemm_fp32_accuracy(nat, M, N, K, epi):
         s = torch.sigmoid(aux.double())
         ref = ref * (s * (1 + aux.double() * (1 - s)))
         scale = scale * 1.2
-    pw = nat.PackedWeight(B.to(DEV), nat.SPLIT_F32)
+    pw = nat.PackedWeight(B.to(DEV), mode)
     outs = {}
     for name, w in (("split", pw), ("f32", B.to(DEV))):
         Cd = C0.clone().to(DEV)
@@ -148,14 +150,59 @@ def test_split_bf16_gemm_modes_and_gather(nat):
     ref = A.double() @ B.double() + P.double()[i0, :N] + P.double()[i1, N:]
     scale = (A.double().abs() @ B.double().abs()).max().item()
     errs = {}
-    for mode in (nat.SPLIT_F32, nat.SPLIT_3, nat.SPLIT_BF16):
+    for mode in (nat.SPLIT_F32, nat.SPLIT_F16X3, nat.SPLIT_3, nat.SPLIT_BF16):
         pw = nat.PackedWeight(B.to(DEV), mode)
         out = torch.empty(M, N, device=DEV)
         nat.linear_gather(A.to(DEV), pw, None, out, P.to(DEV), _i32(i0), _i32(i1), N)
         errs[mode] = (out.cpu().double() - ref).abs().max().item() / scale
     # bf16 operands: ~2^-8 relative; two planes: ~2^-16; three planes: fp32 level
     assert errs[nat.SPLIT_BF16] < 2e-2 and errs[nat.SPLIT_3] < 2e-5 and errs[nat.SPLIT_F32] < 2e-6, errs
-    assert errs[nat.SPLIT_F32] < errs[nat.SPLIT_3] < errs[nat.SPLIT_BF16]
+    assert errs[nat.SPLIT_F16X3] < 2e-6, errs
+    assert max(errs[nat.SPLIT_F32], errs[nat.SPLIT_F16X3]) < errs[nat.SPLIT_3] < errs[nat.SPLIT_BF16]
+
+
+def _scaling_cases():
+    g = torch.Generator().manual_seed(11)
+    M, K, N = 3000, 520, 300
+    rn = lambda *s: torch.randn(*s, generator=g)
+    ru = lambda *s: torch.rand(*s, generator=g)
+    grow = 2.0 ** (torch.arange(K) / 16.0)
+    spikes = rn(M, K)
+    spikes[::7] = 0                      # all-zero rows
+    spikes[1::7, :300] = 0               # rows whose first nonzero values come late
+    spikes[2::7, 17] = 1e6               # one huge value per row
+    colsc = rn(K, N) * 10.0 ** (ru(1, N) * 40 - 20)
+    colsc[:, 5] = 0                      # an all-zero column
+    return {
+        "row scales 1e-30..1e30": (rn(M, K) * 10.0 ** (ru(M, 1) * 60 - 30), rn(K, N)),
+        "element scales 1e-4..1e2": (rn(M, K) * 10.0 ** (ru(M, K) * 6 - 4), rn(K, N)),
+        "growing along K": (rn(M, K) * grow, rn(K, N)),
+        "shrinking along K": (rn(M, K) / grow, rn(K, N)),
+        "zero rows and columns, spikes, column scales": (spikes, colsc),
+        "fp32 subnormal rows": (rn(M, K) * 1e-40, rn(K, N)),
+        "rows near 1e35": (rn(M, K) * 1e35, rn(K, N) / math.sqrt(K)),
+    }
+
+
+@pytest.mark.parametrize("case", list(_scaling_cases()))
+def test_split_f16_scaling(nat, case):
+    """Mode 16's power-of-two scales (per B column at packing, per A row tracked along K with
+    accumulator rescaling) keep fp32 accuracy over fp32's whole range: rows and columns of very
+    different magnitude, values that grow or shrink along K (rescales), all-zero rows and
+    columns, rows whose first nonzero value comes late, isolated huge values, fp32 subnormals."""
+    A, B = _scaling_cases()[case]
+    M, N = A.shape[0], B.shape[1]
+    ref = A.double() @ B.double()
+    scale = A.double().abs() @ B.double().abs()
+    scale = torch.where(scale > 0, scale, torch.ones_like(scale))
+    errs = {}
+    for name, w in (("f16x3", nat.PackedWeight(B.to(DEV), nat.SPLIT_F16X3)), ("f32", B.to(DEV))):
+        out = torch.empty(M, N, device=DEV)
+        nat.linear(A.to(DEV), w, out=out)
+        o = out.cpu().double()
+        assert bool(torch.isfinite(o).all()), (case, name)
+        errs[name] = ((o - ref).abs() / scale).max().item()
+    assert errs["f16x3"] <= max(2.0 * errs["f32"], 1e-6), (case, errs)
 
 
 # ------------------------------------------------------------------------------ geometry

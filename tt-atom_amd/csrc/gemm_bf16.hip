@@ -11,6 +11,19 @@
 //           a0b0 + a0b1 + a1b0 + a0b2 + a2b0 + a1b1      -- the dropped terms are ~2^-24 relative,
 //           so the result has fp32 GEMM accuracy (products of bf16 pairs are exact, the sums are
 //           fp32) at 6/16 of the fp32-MFMA cost per useful flop.
+//   mode 16: two fp16 planes each (v_mfma_f32_32x32x16_f16, same rate), three products
+//           a0b0 + a0b1 + a1b0.  fp16 keeps 11 significant bits, so two planes hold 22 and the
+//           dropped a1b1 and the plane roundings are ~2^-22 relative per product -- random in sign
+//           and, summed over K, well below the fp32 accumulation error itself: fp32 GEMM accuracy
+//           at half the MFMA work of mode 6.  fp16's 5-bit exponent needs scaling by powers of two
+//           (exact): B column n by 2^-F[n] (F from the column's max |b|, packed after the planes),
+//           A row r by 2^-E[r], E tracked online per 16-wide k step.  E stays 0 while the row's
+//           running max is in [2^-1, 2^15) (no scaling at all for ordinary activations); a k step
+//           whose values would reach 2^15 at the current E, or the row's first nonzero k step
+//           outside that window, resets E so the max lands below 2^11 and rescales the row's
+//           accumulators by the (power-of-two) ratio.  Values far below the row max keep an
+//           absolute error under 2^-24 of it (fp16 subnormals).  The epilogue multiplies each
+//           accumulator by 2^(E[r] + F[n]).
 //
 // The 32x32x16 instruction: measured on MI355X it sustains about twice the bf16 rate of
 // 16x16x32 (which issues at half rate).  Operand layout: lane l supplies A[l%32][8*(l/32) + e] and
@@ -18,16 +31,20 @@
 //
 // Packed B layout (tta_pack_b): bf16 [KT][planes][NT32][2][64 lanes][8] with KT = ceil(K/32) and
 // NT32 padded to whole 128-column tiles: one 16(k) x 32(n) fragment is 1 KB, lane l holding
-// B[kt*32 + ks*16 + 8*(l/32) + e][n32*32 + l%32] (zero beyond K, N).
+// B[kt*32 + ks*16 + 8*(l/32) + e][n32*32 + l%32] (zero beyond K, N).  Mode 16 stores fp16
+// planes in the same order, followed by int32 F[NT32 * 32].
 //
-// Block tile (64 WM) x 128 x 32: WM x 2 waves, each 64 x 64 (2 x 2 MFMA tiles of 32 x 32).  Both
+// Block tile (64 WM) x 128 x 32: WM x 2 waves, each 64 x 64 (2 x 2 MFMA tiles of 32 x 32); in
+// mode 16, 2 WM waves of 32 x 128 (1 x 4 tiles), so that each A value split (the VALU work that
+// bounds this mode) feeds four column tiles instead of two (+7 % over 64 x 64).  Both
 // slabs of a k-step reach LDS by direct copies (buffer/global_load ... lds: lane i of a wave
 // writes 16 bytes at the wave's LDS base + 16 i), with no register round trip: A as raw fp32 rows
 // (16-byte chunks XOR-swizzled so that the fragment reads are conflict-free), B as packed.  The
 // copies of slab kt+2 go into the stage slab kt leaves, right after the barrier that retires it,
 // so they have a whole k-step to land.  Each wave reads its A fragment as fp32 and splits it into
 // planes in registers, one 16-wide k half ahead of the MFMAs that consume it.  All modes run
-// WM = 2: 128 x 128 tiles, 256 threads, 80 KB LDS (mode 6), so two blocks share a CU and one's
+// WM = 2: 128 x 128 tiles, 256 threads, 80 KB LDS (mode 6; 68 KB otherwise, the epilogue's
+// staging of the whole tile), so two blocks share a CU and one's
 // epilogue, prologue and barriers overlap the other's MFMAs (measured faster than 256 x 128 tiles
 // with one block per CU on every edge- and node-level shape of the two models).
 #include "gemm_common.h"
@@ -35,6 +52,7 @@
 #include <algorithm>
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
 typedef __attribute__((address_space(1))) void* gbl_ptr;
 
@@ -47,12 +65,14 @@ struct Split;
 template <>
 struct Split<1> {
   static constexpr int NA = 1, NB = 1, NP = 1;
+  static constexpr bool F16 = false;
   static constexpr int pa[1] = {0};
   static constexpr int pb[1] = {0};
 };
 template <>
 struct Split<3> {
   static constexpr int NA = 2, NB = 2, NP = 3;
+  static constexpr bool F16 = false;
   static constexpr int pa[3] = {0, 1, 0};
   static constexpr int pb[3] = {1, 0, 0};
 };
@@ -60,9 +80,38 @@ template <>
 struct Split<6> {
   // smallest terms first
   static constexpr int NA = 3, NB = 3, NP = 6;
+  static constexpr bool F16 = false;
   static constexpr int pa[6] = {1, 0, 2, 0, 1, 0};
   static constexpr int pb[6] = {1, 2, 0, 1, 0, 0};
 };
+template <>
+struct Split<16> {
+  static constexpr int NA = 2, NB = 2, NP = 3;
+  static constexpr bool F16 = true;
+  static constexpr int pa[3] = {1, 0, 0};
+  static constexpr int pb[3] = {0, 1, 0};
+};
+
+// Fragment element type per plane format, and the 32x32x16 MFMA on it.
+template <bool F16>
+struct Frag {
+  typedef bf16x8 T;
+};
+template <>
+struct Frag<true> {
+  typedef f16x8 T;
+};
+__device__ __forceinline__ floatx16 mfma32(bf16x8 a, bf16x8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx16 mfma32(f16x8 a, f16x8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// mode 16 scaling: a B column's values are multiplied by 2^-(e - kTop), e the frexp exponent of
+// its max |value| (max < 2^e), so they land below 2^kTop; an A row's shift follows the rule in the
+// header.  kNoExp marks an A row with no nonzero value yet.
+constexpr int kTop = 11, kNoExp = -100000;
 
 constexpr int BN = 128, BK = 32;
 constexpr int NF = (BN / 32) * 2;  // B fragments per plane per k-step: n32 tiles x k16 halves
@@ -135,6 +184,46 @@ __device__ __forceinline__ void split8(const floatx4& x0, const floatx4& x1, bf1
   }
 }
 
+// x - (fp16 half 0 / half 1 of hpair) in one v_fma_mix_f32, which reads the fp16 operand in
+// place (op_sel_hi marks source 0 as fp16, op_sel picks its half): no conversion back to fp32.
+__device__ __forceinline__ float resid_lo(float x, unsigned hpair) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(hpair), "v"(x));
+  return r;
+}
+__device__ __forceinline__ float resid_hi(float x, unsigned hpair) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=v"(r)
+      : "v"(hpair), "v"(x));
+  return r;
+}
+
+// Split 8 fp32 values, scaled by 2^-sh, into two fp16 planes (round-to-nearest residuals).
+template <int NPL>
+__device__ __forceinline__ void split8_f16(const floatx4& x0, const floatx4& x1, int sh,
+                                           f16x8 (&out)[NPL]) {
+  static_assert(NPL == 2, "two fp16 planes");
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  f2 r[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    r[i] = f2{__builtin_amdgcn_ldexpf(x0[2 * i], -sh), __builtin_amdgcn_ldexpf(x0[2 * i + 1], -sh)};
+    r[i + 2] =
+        f2{__builtin_amdgcn_ldexpf(x1[2 * i], -sh), __builtin_amdgcn_ldexpf(x1[2 * i + 1], -sh)};
+  }
+  h2 h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = __builtin_convertvector(r[i], h2);
+    const unsigned hp = __builtin_bit_cast(unsigned, h[i]);
+    l[i] = __builtin_convertvector(f2{resid_lo(r[i][0], hp), resid_hi(r[i][1], hp)}, h2);
+  }
+  out[0] = f16x8{h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+  out[1] = f16x8{l[0][0], l[0][1], l[1][0], l[1][1], l[2][0], l[2][1], l[3][0], l[3][1]};
+}
+
 // A (fp32) tile row: 8 chunks of 16 B per 32-wide k slab, chunk c of row r stored at c ^ aswz(r):
 // 16 consecutive rows at one logical chunk then cover all 64 banks.
 __device__ __forceinline__ int aswz(int row) { return (row >> 1) & 7; }
@@ -145,17 +234,24 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   const int NT32 = g.NT32[blockIdx.z];
   const bool vec_ok = g.vec[blockIdx.z] != 0;
   typedef Split<MODE> S;
+  // wave tile: TI row blocks x TJ column blocks of 32 x 32 (mode 16: 32 x 128, one A split feeds
+  // four column blocks)
+  constexpr int TI = S::F16 ? 1 : 2, TJ = 4 / TI;
+  typedef typename Frag<S::F16>::T V8;
   constexpr int NA = S::NA, NB = S::NB;
   constexpr int BM = 64 * WM, NTH = 128 * WM;
   constexpr int A_CH = BM * 8, B_CH = NB * NF * 64, STG = A_CH + B_CH;  // 16-byte chunks
   constexpr int APT = A_CH / NTH, BPT = B_CH / NTH;                      // copies per thread
   static_assert(APT * NTH == A_CH && BPT * NTH == B_CH, "slabs must split evenly");
-  __shared__ uint4 smem[2 * STG];
+  // two slab stages, or the whole output tile for the epilogue if that is larger
+  constexpr int LDT = BN + 8;
+  constexpr int SMEM_U4 = 2 * STG > BM * LDT / 4 ? 2 * STG : BM * LDT / 4;
+  __shared__ uint4 smem[SMEM_U4];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = TI == 2 ? wave >> 1 : wave, wn = TI == 2 ? wave & 1 : 0;
   const int tn = (p.N + BN - 1) / BN;
   const int ntiles = tn * ((p.M + BM - 1) / BM);
   // a product of a group uses the first (ntiles rounded up to 8) blocks of the grid, so that
@@ -202,46 +298,105 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
     }
   };
 
-  floatx16 acc[2][2];
+  floatx16 acc[TI][TJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   const int l32 = lane & 31, lh = lane >> 5;
-  const int rbase = wm * 64, cbase = wn * 64;
+  const int rbase = wm * 32 * TI, cbase = wn * 32 * TJ;
   // Fragment reads of one 16-wide k half: raw fp32 A (split later) and the packed B planes.
-  auto rd = [&](int stg, int ks, floatx4 (&x)[2][2], bf16x8 (&b)[2][NB]) {
+  auto rd = [&](int stg, int ks, floatx4 (&x)[TI][2], V8 (&b)[TJ][NB]) {
     const uint4* As = smem + stg * STG;
     const uint4* Bs = As + A_CH;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int q = 0; q < NB; ++q)
-        b[j][q] = __builtin_bit_cast(bf16x8, Bs[(q * NF + (wn * 2 + j) * 2 + ks) * 64 + lane]);
+        b[j][q] = __builtin_bit_cast(V8, Bs[(q * NF + (wn * TJ + j) * 2 + ks) * 64 + lane]);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < TI; ++i) {
       const int row = rbase + i * 32 + l32;
       const int c0 = 4 * ks + 2 * lh;
       x[i][0] = __builtin_bit_cast(floatx4, As[row * 8 + (c0 ^ aswz(row))]);
       x[i][1] = __builtin_bit_cast(floatx4, As[row * 8 + ((c0 + 1) ^ aswz(row))]);
     }
   };
-  auto sp = [&](const floatx4 (&x)[2][2], bf16x8 (&a)[2][NA]) {
+  // mode 16: er[i] = shift E of the lane's A row l32 of row block i, whose values enter the
+  // planes multiplied by 2^-E (lanes l and l + 32 hold the same row and agree); accumulator
+  // element r of a 32 x 32 block belongs to row crow(r) of the block, whose shift lane crow(r)
+  // holds.
+  int er[TI];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) split8<NA>(x[i][0], x[i][1], a[i]);
+  for (int i = 0; i < TI; ++i) er[i] = kNoExp;
+  auto crow = [&](int r) { return 8 * (r >> 2) + 4 * lh + (r & 3); };
+  auto sp = [&](const floatx4 (&x)[TI][2], V8 (&a)[TI][NA]) {
+    if constexpr (S::F16) {
+      int en[TI];
+      bool grow = false;
+#pragma unroll
+      for (int i = 0; i < TI; ++i) {
+        float m = 0.f;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(x[i][c][e]));
+        // the row's other 8 values of this k step are in lane l ^ 32: v_permlane32_swap trades
+        // the upper half of one register with the lower half of another, so with m in both, one
+        // of them ends up holding the partner's m in every lane (a permute through LDS would wait
+        // on the fragment reads in flight).  s_nop 1: the two wait states the swap needs after
+        // the VALU writes of its operands.
+        {
+          float u = m, w = m;
+          asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(u), "+v"(w));
+          m = fmaxf(m, fmaxf(u, w));
+        }
+        const int e = m > 0.f ? __builtin_amdgcn_frexp_expf(m) : kNoExp;
+        // values below 2^e reach 2^(e - E): a new shift once that passes 2^15, and for the row's
+        // first nonzero step (E = kNoExp); the new shift is never below the old one
+        const bool g = e != kNoExp && e - er[i] > 15;
+        en[i] = g ? ((e >= 0 && e <= 15) ? 0 : e - kTop) : er[i];
+        grow |= g;
+      }
+      if (__any(grow)) {  // rare: a row's first nonzero k step, or a much larger value
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+          const int d = er[i] - en[i];  // <= 0; the sentinel's huge d zeroes an all-zero acc
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int dr = __shfl(d, crow(r));
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) acc[i][j][r] = __builtin_amdgcn_ldexpf(acc[i][j][r], dr);
+          }
+          er[i] = en[i];
+        }
+      }
+      // E = 0 on every row of the wave (the common case): no scaling instructions at all
+      bool unscaled = true;
+#pragma unroll
+      for (int i = 0; i < TI; ++i) unscaled &= er[i] == 0 || er[i] == kNoExp;
+      if (__all(unscaled)) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) split8_f16<NA>(x[i][0], x[i][1], 0, a[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) split8_f16<NA>(x[i][0], x[i][1], er[i], a[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TI; ++i) split8<NA>(x[i][0], x[i][1], a[i]);
+    }
   };
-  auto mm = [&](const bf16x8 (&a)[2][NA], const bf16x8 (&b)[2][NB]) {
+  auto mm = [&](const V8 (&a)[TI][NA], const V8 (&b)[TJ][NB]) {
 #pragma unroll
     for (int q = 0; q < S::NP; ++q)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][S::pa[q]], b[j][S::pb[q]],
-                                                              acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TJ; ++j) acc[i][j] = mfma32(a[i][S::pa[q]], b[j][S::pb[q]], acc[i][j]);
   };
 
   // Software pipeline: the fragments of the next k half are read (and A split) while the MFMAs of
@@ -254,8 +409,8 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
     issue(0, 0);
     issue(min(1, nk - 1), 1);
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(APT + BPT) : "memory");
-    floatx4 cx[2][2], nx[2][2];
-    bf16x8 ca[2][NA], cb[2][NB], na[2][NA], nb[2][NB];
+    floatx4 cx[TI][2], nx[TI][2];
+    V8 ca[TI][NA], cb[TJ][NB], na[TI][NA], nb[TJ][NB];
     rd(0, 0, cx, cb);
     sp(cx, ca);
     for (int kt = 0; kt < nk; ++kt) {
@@ -271,21 +426,38 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }
+  if constexpr (S::F16) {
+    // undo the scales: C = acc * 2^(E[row] + F[col]); F follows the planes of the packed B and
+    // has an entry for every column of the padded n32 tiles
+    const int* Fc =
+        reinterpret_cast<const int*>(Bp + (int64_t)((p.K + BK - 1) / BK) * NB * NT32 * 128);
+    int fc[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) fc[j] = Fc[n0 + cbase + j * 32 + l32];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int rs = __shfl(er[i], crow(r));
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          acc[i][j][r] = __builtin_amdgcn_ldexpf(acc[i][j][r], rs + fc[j]);
+      }
+  }
   // Epilogue: stage the accumulators through LDS in row passes, then each thread applies the
   // epilogue to whole float4 column groups and writes coalesced rows.
-  constexpr int LDT = BN + 8;
-  constexpr int SMEM_F = 2 * STG * 4;
+  constexpr int SMEM_F = SMEM_U4 * 4;
   constexpr int RP = (BM * LDT <= SMEM_F) ? BM : (BM / 2 * LDT <= SMEM_F) ? BM / 2
                    : (BM / 4 * LDT <= SMEM_F) ? BM / 4 : 32;
   static_assert(RP % 32 == 0 && RP * LDT <= SMEM_F, "epilogue staging must fit the LDS buffer");
   float* Ct = reinterpret_cast<float*>(smem);
   for (int r0 = 0; r0 < BM; r0 += RP) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < TI; ++i) {
       const int rt = rbase + i * 32 - r0;
       if (rt < 0 || rt >= RP) continue;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < TJ; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           Ct[(rt + 8 * (r >> 2) + 4 * lh + (r & 3)) * LDT + cbase + j * 32 + l32] = acc[i][j][r];
@@ -325,6 +497,48 @@ __global__ __launch_bounds__(256) void k_pack_b(const float* __restrict__ B, int
   }
 }
 
+// mode 16, B side: F[n] = frexp exponent of column n's max |b| minus kTop (0 for an all-zero or
+// padding column), one thread per column of the padded n32 tiles.
+__global__ __launch_bounds__(256) void k_col_exp(const float* __restrict__ B, int K, int N,
+                                                 int64_t ldb, int ncol, int* __restrict__ F) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= ncol) return;
+  float m = 0.f;
+  if (n < N)
+    for (int k = 0; k < K; ++k) m = fmaxf(m, fabsf(B[(int64_t)k * ldb + n]));
+  F[n] = m > 0.f ? __builtin_amdgcn_frexp_expf(m) - kTop : 0;
+}
+
+// mode 16 packing: as k_pack_b with two fp16 planes of b * 2^-F[n].
+__global__ __launch_bounds__(256) void k_pack_b_f16(const float* __restrict__ B, int K, int N,
+                                                    int64_t ldb, int KT, int NT32,
+                                                    const int* __restrict__ F,
+                                                    uint4* __restrict__ out) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)KT * NT32 * 128) return;
+  const int l = (int)(gid % 64);
+  const int ks = (int)((gid / 64) % 2);
+  const int nt = (int)((gid / 128) % NT32);
+  const int kt = (int)(gid / (128 * (int64_t)NT32));
+  const int n = nt * 32 + (l & 31);
+  const int sh = F[n];
+  float r[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int k = kt * 32 + ks * 16 + 8 * (l >> 5) + e;
+    r[e] = (k < K && n < N) ? __builtin_amdgcn_ldexpf(B[(int64_t)k * ldb + n], -sh) : 0.f;
+  }
+  for (int q = 0; q < 2; ++q) {
+    f16x8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      h[e] = (_Float16)r[e];
+      r[e] -= (float)h[e];
+    }
+    out[((((int64_t)kt * 2 + q) * NT32 + nt) * 2 + ks) * 64 + l] = __builtin_bit_cast(uint4, h);
+  }
+}
+
 // One launch for the n products of g (blockIdx.z = product); each product's blocks beyond its
 // own tile count exit at once.
 template <int WM, int MODE>
@@ -354,11 +568,14 @@ int launch_mode(const GemmGroup& g, int n, int mode, hipStream_t s) {
   switch (mode) {
     case 1: return launch_bf16x<2, 1>(g, n, s);
     case 3: return launch_bf16x<2, 3>(g, n, s);
+    case 16: return launch_bf16x<2, 16>(g, n, s);
     default: return launch_bf16x<2, 6>(g, n, s);
   }
 }
 
-int planes_of(int mode) { return mode == 1 ? 1 : mode == 3 ? 2 : mode == 6 ? 3 : 0; }
+int planes_of(int mode) {
+  return mode == 1 ? 1 : mode == 3 ? 2 : mode == 6 ? 3 : mode == 16 ? 2 : 0;
+}
 
 }  // namespace
 
@@ -369,19 +586,31 @@ static int64_t nt32_padded(int64_t N) { return ((N + BN - 1) / BN) * (BN / 32); 
 extern "C" int64_t tta_pack_b_elems(int64_t K, int64_t N, int mode) {
   const int pl = planes_of(mode);
   if (pl == 0 || K <= 0 || N <= 0) return -1;
-  return ((K + 31) / 32) * nt32_padded(N) * 1024 * pl;
+  // mode 16 appends the int32 column exponents F (two 16-bit elements each)
+  return ((K + 31) / 32) * nt32_padded(N) * 1024 * pl + (mode == 16 ? nt32_padded(N) * 64 : 0);
 }
 
 extern "C" int tta_pack_b(const float* B, int64_t K, int64_t N, int64_t ldb, int mode,
                           void* out, int64_t out_elems, hipStream_t stream) {
   const int pl = planes_of(mode);
-  TTA_CHECK_ARG(pl > 0, "tta_pack_b: mode must be 1, 3 or 6 (got %d)", mode);
+  TTA_CHECK_ARG(pl > 0, "tta_pack_b: mode must be 1, 3, 6 or 16 (got %d)", mode);
   TTA_CHECK_ARG(K > 0 && N > 0 && K < (1 << 30) && N < (1 << 30) && ldb >= N,
                 "tta_pack_b: bad sizes");
   TTA_CHECK_ARG(out_elems == tta_pack_b_elems(K, N, mode), "tta_pack_b: output has %lld bf16, "
                 "expected %lld", (long long)out_elems, (long long)tta_pack_b_elems(K, N, mode));
   TTA_CHECK_ARG(B && out && ((uintptr_t)out % 16 == 0), "tta_pack_b: null or misaligned pointer");
   const int KT = (int)((K + 31) / 32), NT32 = (int)nt32_padded(N);
+  if (mode == 16) {
+    uint4* planes = static_cast<uint4*>(out);
+    int* F = reinterpret_cast<int*>(planes + (int64_t)KT * 2 * NT32 * 128);
+    hipLaunchKernelGGL(k_col_exp, dim3(tta_blocks((int64_t)NT32 * 32, 256)), dim3(256), 0, stream,
+                       B, (int)K, (int)N, ldb, NT32 * 32, F);
+    TTA_CHECK_LAUNCH("tta_pack_b");
+    hipLaunchKernelGGL(k_pack_b_f16, dim3(tta_blocks((int64_t)KT * NT32 * 128, 256)), dim3(256), 0,
+                       stream, B, (int)K, (int)N, ldb, KT, NT32, F, planes);
+    TTA_CHECK_LAUNCH("tta_pack_b");
+    return tta::kOk;
+  }
   hipLaunchKernelGGL(k_pack_b, dim3(tta_blocks((int64_t)KT * NT32 * 128, 256)), dim3(256), 0,
                      stream, B, (int)K, (int)N, ldb, pl, KT, NT32, static_cast<uint4*>(out));
   TTA_CHECK_LAUNCH("tta_pack_b");
@@ -427,7 +656,8 @@ extern "C" int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const fl
                               int64_t lda, int64_t ldc, int mode, const float* P, int64_t ldp,
                               const int* idx0, const int* idx1, int64_t off1, int64_t n_rows_p,
                               int epilogue, hipStream_t stream) {
-  TTA_CHECK_ARG(planes_of(mode) > 0, "tta_gemm_bf16x: mode must be 1, 3 or 6 (got %d)", mode);
+  TTA_CHECK_ARG(planes_of(mode) > 0, "tta_gemm_bf16x: mode must be 1, 3, 6 or 16 (got %d)",
+                mode);
   GemmGroup g{};
   bool skip = false;
   const int rc = prepare_bf16x(A, Bp, C, bias, C2, aux, M, N, K, lda, ldc, P, ldp, idx0, idx1,
@@ -438,8 +668,8 @@ extern "C" int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const fl
 
 extern "C" int tta_gemm_bf16x_group(const tta_gemm_problem* probs, int64_t n, int mode,
                                     hipStream_t stream) {
-  TTA_CHECK_ARG(planes_of(mode) > 0, "tta_gemm_bf16x_group: mode must be 1, 3 or 6 (got %d)",
-                mode);
+  TTA_CHECK_ARG(planes_of(mode) > 0,
+                "tta_gemm_bf16x_group: mode must be 1, 3, 6 or 16 (got %d)", mode);
   TTA_CHECK_ARG(n >= 0 && n <= kMaxGroup && (probs || n == 0),
                 "tta_gemm_bf16x_group: 0..%d products", kMaxGroup);
   GemmGroup g{};

@@ -176,7 +176,7 @@ EPI_STORE, EPI_SILU, EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD = 0, 1, 2, 3, 4
 # ``probe.before(flops, nbytes, kind)`` and ``probe.after()`` (the benchmark records HIP events on
 # the launch stream there).  nbytes is the algorithmic traffic: A, B and C once (C twice when
 # accumulated, plus the second output / auxiliary input of epilogues 3 and 4); kind is "f32" for
-# the fp32 MFMA kernel and "bf16x<mode>" for the split-bf16 kernel.
+# the fp32 MFMA kernel and MODE_KIND[mode] for the split kernel.
 _gemm_probe = None
 
 
@@ -226,14 +226,17 @@ def gemm(A, B, C, *, M, N, K, lda, ldb, ldc, bias=None, epilogue=EPI_STORE, C2=N
         probe.after()
 
 
-# Split-bf16 MFMA GEMM modes (tta_gemm_bf16x): 6 = fp32-accurate (three bf16 planes per
-# operand, six products), 3 = two planes / three products, 1 = bf16 operands.
-SPLIT_F32, SPLIT_3, SPLIT_BF16 = 6, 3, 1
+# Split MFMA GEMM modes (tta_gemm_bf16x): 6 = fp32-accurate with three bf16 planes per operand
+# (six products), 16 = fp32-accurate with two power-of-two-scaled fp16 planes per operand (three
+# products), 3 = two bf16 planes / three products, 1 = bf16 operands.
+SPLIT_F32, SPLIT_F16X3, SPLIT_3, SPLIT_BF16 = 6, 16, 3, 1
+# kernel-family name per mode, as the measurement hook reports it
+MODE_KIND = {6: "bf16x6", 16: "f16x3", 3: "bf16x3", 1: "bf16x1"}
 
 
 class PackedWeight:
     """A constant GEMM operand w_t [K, N] (fp32, row-major) plus its bf16-plane packing for the
-    split-bf16 kernel (``mode`` 6, 3 or 1; None keeps only the fp32 matrix for the fp32-MFMA
+    split kernel (``mode`` 6, 16, 3 or 1; None keeps only the fp32 matrix for the fp32-MFMA
     kernel).  ``shape`` / ``T``-free: it stands wherever a [K, N] weight is passed to linear()."""
 
     def __init__(self, w_t, mode=SPLIT_F32):
@@ -273,7 +276,7 @@ def _gemm_bf16x(x, pw, out, bias, epilogue, out2, aux, P=None, idx0=None, idx1=N
     if probe is not None:
         c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD)) + (2 if P is not None else 0)
         probe.before(2.0 * M * N * K, 4.0 * (M * K + K * N + c_passes * M * N),
-                     f"bf16x{pw.mode}")
+                     MODE_KIND[pw.mode])
     _call("tta_gemm_bf16x", x.data_ptr(), pw.packed.data_ptr(), out.data_ptr(),
           None if bias is None else _ptr(bias, numel=N, name="bias"),
           None if out2 is None else out2.data_ptr(), None if aux is None else aux.data_ptr(),
@@ -353,7 +356,7 @@ def linear_group(items):
         nbytes += 4.0 * (M * K + K * N + c_passes * M * N)
     probe = _gemm_probe
     if probe is not None:
-        probe.before(flops, nbytes, f"bf16x{items[0][1].mode}" if split[0] else "f32")
+        probe.before(flops, nbytes, MODE_KIND[items[0][1].mode] if split[0] else "f32")
     if split[0]:
         _call("tta_gemm_bf16x_group", probs, len(items), items[0][1].mode, _stream())
     else:

@@ -37,9 +37,12 @@ def _dev(t, device):
     return out
 
 
-# GEMM arithmetic per precision setting: "f32" = split-bf16 MFMA with six plane products (fp32
-# GEMM accuracy), "f32-mfma" = the fp32 MFMA kernel only, "bf16" = bf16 operands, fp32 accumulate.
-PRECISIONS = {"f32": nat.SPLIT_F32, "f32-mfma": None, "bf16": nat.SPLIT_BF16}
+# GEMM arithmetic per precision setting, all with fp32 accumulation: "f32" = two power-of-two-
+# scaled fp16 planes per operand, three MFMA products (fp32 GEMM accuracy), "f32-bf16x6" = three
+# bf16 planes, six products (fp32 GEMM accuracy), "f32-mfma" = the fp32 MFMA kernel only,
+# "bf16" = bf16 operands.
+PRECISIONS = {"f32": nat.SPLIT_F16X3, "f32-bf16x6": nat.SPLIT_F32, "f32-mfma": None,
+              "bf16": nat.SPLIT_BF16}
 
 
 def _gw(t, device, mode):

@@ -498,15 +498,22 @@ __global__ __launch_bounds__(256) void k_pack_b(const float* __restrict__ B, int
 }
 
 // mode 16, B side: F[n] = frexp exponent of column n's max |b| minus kTop (0 for an all-zero or
-// padding column), one thread per column of the padded n32 tiles.
-__global__ __launch_bounds__(256) void k_col_exp(const float* __restrict__ B, int K, int N,
-                                                 int64_t ldb, int ncol, int* __restrict__ F) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= ncol) return;
+// padding column).  A block of 64 columns x 16 k-strided lanes, reduced through LDS.
+__global__ __launch_bounds__(1024) void k_col_exp(const float* __restrict__ B, int K, int N,
+                                                  int64_t ldb, int ncol, int* __restrict__ F) {
+  __shared__ float part[16][64];
+  const int c = threadIdx.x & 63, kg = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + c;
   float m = 0.f;
   if (n < N)
-    for (int k = 0; k < K; ++k) m = fmaxf(m, fabsf(B[(int64_t)k * ldb + n]));
-  F[n] = m > 0.f ? __builtin_amdgcn_frexp_expf(m) - kTop : 0;
+    for (int k = kg; k < K; k += 16) m = fmaxf(m, fabsf(B[(int64_t)k * ldb + n]));
+  part[kg][c] = m;
+  __syncthreads();
+  if (kg == 0 && n < ncol) {
+#pragma unroll
+    for (int q = 1; q < 16; ++q) m = fmaxf(m, part[q][c]);
+    F[n] = m > 0.f ? __builtin_amdgcn_frexp_expf(m) - kTop : 0;
+  }
 }
 
 // mode 16 packing: as k_pack_b with two fp16 planes of b * 2^-F[n].
@@ -603,7 +610,7 @@ extern "C" int tta_pack_b(const float* B, int64_t K, int64_t N, int64_t ldb, int
   if (mode == 16) {
     uint4* planes = static_cast<uint4*>(out);
     int* F = reinterpret_cast<int*>(planes + (int64_t)KT * 2 * NT32 * 128);
-    hipLaunchKernelGGL(k_col_exp, dim3(tta_blocks((int64_t)NT32 * 32, 256)), dim3(256), 0, stream,
+    hipLaunchKernelGGL(k_col_exp, dim3(tta_blocks((int64_t)NT32 * 32, 64)), dim3(1024), 0, stream,
                        B, (int)K, (int)N, ldb, NT32 * 32, F);
     TTA_CHECK_LAUNCH("tta_pack_b");
     hipLaunchKernelGGL(k_pack_b_f16, dim3(tta_blocks((int64_t)KT * NT32 * 128, 256)), dim3(256), 0,

@@ -17,9 +17,9 @@
 //           and, summed over K, well below the fp32 accumulation error itself: fp32 GEMM accuracy
 //           at half the MFMA work of mode 6.  fp16's 5-bit exponent needs scaling by powers of two
 //           (exact): B column n by 2^-F[n] (F from the column's max |b|, packed after the planes),
-//           A row r by 2^-E[r], E tracked online per 16-wide k step.  E stays 0 while the row's
-//           running max is in [2^-1, 2^15) (no scaling at all for ordinary activations); a k step
-//           whose values would reach 2^15 at the current E, or the row's first nonzero k step
+//           A row r by 2^-E[r], E tracked online per 32-wide k slab.  E stays 0 while the row's
+//           running max is in [2^-1, 2^15) (no scaling at all for ordinary activations); a k slab
+//           whose values would reach 2^15 at the current E, or the row's first nonzero k slab
 //           outside that window, resets E so the max lands below 2^11 and rescales the row's
 //           accumulators by the (power-of-two) ratio.  Values far below the row max keep an
 //           absolute error under 2^-24 of it (fp16 subnormals).  The epilogue multiplies each
@@ -41,9 +41,10 @@
 // writes 16 bytes at the wave's LDS base + 16 i), with no register round trip: A as raw fp32 rows
 // (16-byte chunks XOR-swizzled so that the fragment reads are conflict-free), B as packed.  The
 // copies of slab kt+2 go into the stage slab kt leaves, right after the barrier that retires it,
-// so they have a whole k-step to land.  Each wave reads its A fragment as fp32 and splits it into
-// planes in registers, one 16-wide k half ahead of the MFMAs that consume it.  All modes run
-// WM = 2: 128 x 128 tiles, 256 threads, 80 KB LDS (mode 6; 68 KB otherwise, the epilogue's
+// so they have a whole k-step to land.  Each wave reads its A fragment as fp32 (both 16-wide k
+// halves of a slab at once, for mode 16's per-slab scale check) and splits it into planes in
+// registers, one k half ahead of the MFMAs that consume it.  All modes run
+// WM = 2: 128 x 128 tiles, 256 threads, 80 KB LDS (mode 6; 68 KB for mode 16, the epilogue's
 // staging of the whole tile), so two blocks share a CU and one's
 // epilogue, prologue and barriers overlap the other's MFMAs (measured faster than 256 x 128 tiles
 // with one block per CU on every edge- and node-level shape of the two models).
@@ -243,9 +244,11 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   constexpr int A_CH = BM * 8, B_CH = NB * NF * 64, STG = A_CH + B_CH;  // 16-byte chunks
   constexpr int APT = A_CH / NTH, BPT = B_CH / NTH;                      // copies per thread
   static_assert(APT * NTH == A_CH && BPT * NTH == B_CH, "slabs must split evenly");
-  // two slab stages, or the whole output tile for the epilogue if that is larger
+  // two slab stages; mode 16 (64 KB of stages) rounds up to the whole output tile, 68 KB, for a
+  // one-pass epilogue at the same two blocks per CU (modes 1 and 3 keep 48 / 64 KB: three blocks
+  // per CU for mode 1)
   constexpr int LDT = BN + 8;
-  constexpr int SMEM_U4 = 2 * STG > BM * LDT / 4 ? 2 * STG : BM * LDT / 4;
+  constexpr int SMEM_U4 = (S::F16 && BM * LDT / 4 > 2 * STG) ? BM * LDT / 4 : 2 * STG;
   __shared__ uint4 smem[SMEM_U4];
 
   const int t = threadIdx.x;
@@ -309,14 +312,16 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   const int l32 = lane & 31, lh = lane >> 5;
   const int rbase = wm * 32 * TI, cbase = wn * 32 * TJ;
   // Fragment reads of one 16-wide k half: raw fp32 A (split later) and the packed B planes.
-  auto rd = [&](int stg, int ks, floatx4 (&x)[TI][2], V8 (&b)[TJ][NB]) {
-    const uint4* As = smem + stg * STG;
-    const uint4* Bs = As + A_CH;
+  auto rdB = [&](int stg, int ks, V8 (&b)[TJ][NB]) {
+    const uint4* Bs = smem + stg * STG + A_CH;
 #pragma unroll
     for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int q = 0; q < NB; ++q)
         b[j][q] = __builtin_bit_cast(V8, Bs[(q * NF + (wn * TJ + j) * 2 + ks) * 64 + lane]);
+  };
+  auto rdA = [&](int stg, int ks, floatx4 (&x)[TI][2]) {
+    const uint4* As = smem + stg * STG;
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
       const int row = rbase + i * 32 + l32;
@@ -328,12 +333,12 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   // mode 16: er[i] = shift E of the lane's A row l32 of row block i, whose values enter the
   // planes multiplied by 2^-E (lanes l and l + 32 hold the same row and agree); accumulator
   // element r of a 32 x 32 block belongs to row crow(r) of the block, whose shift lane crow(r)
-  // holds.
+  // holds.  The shift is checked once per 32-wide k slab, over both of its halves.
   int er[TI];
 #pragma unroll
   for (int i = 0; i < TI; ++i) er[i] = kNoExp;
   auto crow = [&](int r) { return 8 * (r >> 2) + 4 * lh + (r & 3); };
-  auto sp = [&](const floatx4 (&x)[TI][2], V8 (&a)[TI][NA]) {
+  auto scale = [&](const floatx4 (&x0)[TI][2], const floatx4 (&x1)[TI][2]) {
     if constexpr (S::F16) {
       int en[TI];
       bool grow = false;
@@ -343,8 +348,8 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) m = fmaxf(m, fabsf(x[i][c][e]));
-        // the row's other 8 values of this k step are in lane l ^ 32: v_permlane32_swap trades
+          for (int e = 0; e < 4; ++e) m = fmaxf(m, fmaxf(fabsf(x0[i][c][e]), fabsf(x1[i][c][e])));
+        // the row's other 16 values of this k slab are in lane l ^ 32: v_permlane32_swap trades
         // the upper half of one register with the lower half of another, so with m in both, one
         // of them ends up holding the partner's m in every lane (a permute through LDS would wait
         // on the fragment reads in flight).  s_nop 1: the two wait states the swap needs after
@@ -356,12 +361,12 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
         }
         const int e = m > 0.f ? __builtin_amdgcn_frexp_expf(m) : kNoExp;
         // values below 2^e reach 2^(e - E): a new shift once that passes 2^15, and for the row's
-        // first nonzero step (E = kNoExp); the new shift is never below the old one
+        // first nonzero slab (E = kNoExp); the new shift is never below the old one
         const bool g = e != kNoExp && e - er[i] > 15;
         en[i] = g ? ((e >= 0 && e <= 15) ? 0 : e - kTop) : er[i];
         grow |= g;
       }
-      if (__any(grow)) {  // rare: a row's first nonzero k step, or a much larger value
+      if (__any(grow)) {  // rare: a row's first nonzero k slab, or a much larger value
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
           const int d = er[i] - en[i];  // <= 0; the sentinel's huge d zeroes an all-zero acc
@@ -374,6 +379,10 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
           er[i] = en[i];
         }
       }
+    }
+  };
+  auto sp = [&](const floatx4 (&x)[TI][2], V8 (&a)[TI][NA]) {
+    if constexpr (S::F16) {
       // E = 0 on every row of the wave (the common case): no scaling instructions at all
       bool unscaled = true;
 #pragma unroll
@@ -409,20 +418,26 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
     issue(0, 0);
     issue(min(1, nk - 1), 1);
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(APT + BPT) : "memory");
-    floatx4 cx[TI][2], nx[TI][2];
+    floatx4 x0[TI][2], x1[TI][2];  // A of both k halves of the slab being split
     V8 ca[TI][NA], cb[TJ][NB], na[TI][NA], nb[TJ][NB];
-    rd(0, 0, cx, cb);
-    sp(cx, ca);
+    rdA(0, 0, x0);
+    rdA(0, 1, x1);
+    rdB(0, 0, cb);
+    scale(x0, x1);
+    sp(x0, ca);
     for (int kt = 0; kt < nk; ++kt) {
       const int stg = kt & 1;
-      rd(stg, 1, nx, nb);
+      rdB(stg, 1, nb);
       mm(ca, cb);
-      sp(nx, na);
+      sp(x1, na);
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
       issue(min(kt + 2, nk - 1), stg);
-      rd(stg ^ 1, 0, cx, cb);
+      rdA(stg ^ 1, 0, x0);
+      rdA(stg ^ 1, 1, x1);
+      rdB(stg ^ 1, 0, cb);
       mm(na, nb);
-      sp(cx, ca);
+      scale(x0, x1);
+      sp(x0, ca);
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
   }

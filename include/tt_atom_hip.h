@@ -266,21 +266,27 @@ int tta_add_rows(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t R, 
  * periodic -> receivers t (columns (j, cell) lexicographic, edge (j, t, cell)).  lo / hi
  * (nullable) bound every row's candidates to its own system of a batch.  Aperiodic keep:
  * 0 < s < mid2 with s the fp32 fma-chain norm^2 and mid2 the square of the midpoint below
- * fp32(cutoff); periodic keep: min2 < d2 <= cut2 over the image shifts [n_cells, 3].
+ * fp32(cutoff); periodic keep: min2 < d2 <= cut2 over the image shifts [n_cells, 3], or, with
+ * clo / chi (nullable, both or neither: per-row [clo, chi) ranges into that table), over the row's
+ * own system's shifts -- a batch of periodic systems concatenates their tables, edge_cell then
+ * indexes the concatenation (every range must lie in [0, n_cells)).
  * thresholds: the k-th smallest cap key (d2, src, cell) of every receiver (err[0] = 1 when a
  * receiver has over 1024 candidates); count: kept entries per row (thresholds null = no cap);
  * write: edges at the caller's exclusive int64 row offsets (edge_cell for periodic graphs). */
 int tta_radius_graph_thresholds(const float* pos, int64_t N, const int* lo, const int* hi,
-                                const float* shifts, int64_t n_cells, int periodic, double mid2,
-                                float cut2, float min2, int k, float* thr_d2, int* thr_src,
-                                int* thr_cell, int* err, tta_stream_t stream);
+                                const float* shifts, int64_t n_cells, const int* clo,
+                                const int* chi, int periodic, double mid2, float cut2,
+                                float min2, int k, float* thr_d2, int* thr_src, int* thr_cell,
+                                int* err, tta_stream_t stream);
 int tta_radius_graph_count(const float* pos, int64_t N, const int* lo, const int* hi,
-                           const float* shifts, int64_t n_cells, int periodic, double mid2,
-                           float cut2, float min2, const float* thr_d2, const int* thr_src,
-                           const int* thr_cell, int* counts, tta_stream_t stream);
+                           const float* shifts, int64_t n_cells, const int* clo, const int* chi,
+                           int periodic, double mid2, float cut2, float min2,
+                           const float* thr_d2, const int* thr_src, const int* thr_cell,
+                           int* counts, tta_stream_t stream);
 int tta_radius_graph_write(const float* pos, int64_t N, const int* lo, const int* hi,
-                           const float* shifts, int64_t n_cells, int periodic, double mid2,
-                           float cut2, float min2, const float* thr_d2, const int* thr_src,
+                           const float* shifts, int64_t n_cells, const int* clo, const int* chi,
+                           int periodic, double mid2, float cut2, float min2,
+                           const float* thr_d2, const int* thr_src,
                            const int* thr_cell, const int64_t* offsets, int64_t* edge_src,
                            int64_t* edge_tgt, int* edge_cell, tta_stream_t stream);
 

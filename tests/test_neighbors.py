@@ -130,3 +130,29 @@ def test_assemble_orb_device_equals_host():
                  (h.pos, d.pos), (h.Z, d.Z), (h.batch, d.batch)):
         assert torch.equal(a, b)
     assert h.natoms == d.natoms
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cap", [None, 12])
+def test_device_graph_batched_periodic(cap):
+    """Periodic systems of one batch share one device pass (per-row node and image-shift ranges):
+    each system's graph equals the host's on it alone, edge for edge with the same shifts, for
+    different cells, sizes, periodicities (3-D, slab, wire) and image counts, with aperiodic
+    systems mixed in."""
+    from tt_atom import synthetic
+    g = np.random.default_rng(5)
+    items = []
+    for reps, pbc, scale in ((2, [True] * 3, 1.0), (3, [True, True, False], 1.03),
+                             (1, [True] * 3, 0.97), (2, [False, True, False], 1.0)):
+        pos, Z, cell = synthetic.c4_system(reps=reps)
+        pos = (pos * scale + g.normal(0, 0.05, pos.shape)).astype(np.float32)
+        items.append((torch.from_numpy(pos), torch.from_numpy((cell * scale).astype(np.float32)),
+                      pbc))
+    items.insert(2, (torch.from_numpy(synthetic.c5_systems(K=1)[0][0].astype(np.float32)), None,
+                     None))
+    host = geometry.system_graphs(items, 6.0, cap, "host")
+    dev = geometry.system_graphs(items, 6.0, cap, "device")
+    for (ei_h, sh_h), (ei_d, sh_d) in zip(host, dev):
+        assert ei_h.shape[1] > 0
+        assert torch.equal(ei_h.cpu().long(), ei_d.cpu().long())
+        assert torch.equal(sh_h.cpu().float(), sh_d.cpu().float())

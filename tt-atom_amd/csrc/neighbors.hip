@@ -31,6 +31,8 @@ struct NL {
   const int* hi;  // per-row end (null: N)
   const float* shifts;
   int n_cells;
+  const int* clo;  // periodic: per-row first image shift (null: 0); a batch of periodic systems
+  const int* chi;  // concatenates their shift tables, each row using its system's (null: n_cells)
   int periodic;
   double mid2;     // aperiodic: keep iff 0 < s < mid2
   float cut2, min2;  // periodic: keep iff min2 < d2 <= cut2
@@ -89,7 +91,8 @@ __device__ __forceinline__ void row_chunk(const NL& p, int r, int j, float3 pr, 
     const float s = norm2_fma(pr, pj);
     if (s > 0.f && (double)s < p.mid2) f(r, j, 0, cap_d2(pr, pj, make_float3(0.f, 0.f, 0.f)));
   } else {
-    for (int c = 0; c < p.n_cells; ++c) {
+    const int c0 = p.clo ? p.clo[r] : 0, c1 = p.chi ? p.chi[r] : p.n_cells;
+    for (int c = c0; c < c1; ++c) {
       const float3 sh = ld3(p.shifts, c);
       const float d2 = disp2(pr, pj, sh);
       if (d2 <= p.cut2 && d2 > p.min2) f(j, r, c, cap_d2(pj, pr, sh));
@@ -137,15 +140,16 @@ __global__ __launch_bounds__(256) void k_nl_thresh(NL p, int k, float* __restric
       cnt += tot;
     } else {
       const float3 pj = j < hi ? ld3(p.pos, j) : make_float3(0.f, 0.f, 0.f);
+      const int c0 = p.clo ? p.clo[t] : 0, c1 = p.chi ? p.chi[t] : p.n_cells;
       if (j < hi)
-        for (int c = 0; c < p.n_cells; ++c) {
+        for (int c = c0; c < c1; ++c) {
           const float d2 = disp2(pt, pj, ld3(p.shifts, c));
           nh += (d2 <= p.cut2 && d2 > p.min2);
         }
       int tot;
       int off = wave_excl_scan(nh, lane, &tot);
       if (nh)
-        for (int c = 0; c < p.n_cells; ++c) {
+        for (int c = c0; c < c1; ++c) {
           const float3 sh = ld3(p.shifts, c);
           const float d2 = disp2(pt, pj, sh);
           if (d2 <= p.cut2 && d2 > p.min2) {
@@ -234,16 +238,18 @@ __global__ __launch_bounds__(256) void k_nl_rows(NL p, int cap, const float* __r
 }  // namespace
 
 static int check_nl(const float* pos, int64_t N, const float* shifts, int64_t n_cells,
-                    int periodic, const char* who) {
+                    const int* clo, const int* chi, int periodic, const char* who) {
   TTA_CHECK_ARG(N >= 0 && N < (1ll << 30), "%s: bad node count", who);
   TTA_CHECK_ARG(N == 0 || pos, "%s: null positions", who);
   TTA_CHECK_ARG(!periodic || (shifts && n_cells > 0 && n_cells < (1 << 20)),
                 "%s: periodic graph needs the image-shift table", who);
+  TTA_CHECK_ARG((clo == nullptr) == (chi == nullptr), "%s: cell ranges both or neither", who);
   return tta::kOk;
 }
 
 static NL make_nl(const float* pos, int64_t N, const int* lo, const int* hi, const float* shifts,
-                  int64_t n_cells, int periodic, double mid2, float cut2, float min2) {
+                  int64_t n_cells, const int* clo, const int* chi, int periodic, double mid2,
+                  float cut2, float min2) {
   NL p;
   p.pos = pos;
   p.N = (int)N;
@@ -251,6 +257,8 @@ static NL make_nl(const float* pos, int64_t N, const int* lo, const int* hi, con
   p.hi = hi;
   p.shifts = shifts;
   p.n_cells = periodic ? (int)n_cells : 1;
+  p.clo = periodic ? clo : nullptr;
+  p.chi = periodic ? chi : nullptr;
   p.periodic = periodic;
   p.mid2 = mid2;
   p.cut2 = cut2;
@@ -260,16 +268,16 @@ static NL make_nl(const float* pos, int64_t N, const int* lo, const int* hi, con
 
 extern "C" int tta_radius_graph_thresholds(const float* pos, int64_t N, const int* lo,
                                            const int* hi, const float* shifts, int64_t n_cells,
-                                           int periodic, double mid2, float cut2, float min2,
+                                           const int* clo, const int* chi, int periodic, double mid2, float cut2, float min2,
                                            int k, float* thr_d2, int* thr_src, int* thr_cell,
                                            int* err, hipStream_t stream) {
-  if (int st = check_nl(pos, N, shifts, n_cells, periodic, "tta_radius_graph_thresholds"))
+  if (int st = check_nl(pos, N, shifts, n_cells, clo, chi, periodic, "tta_radius_graph_thresholds"))
     return st;
   TTA_CHECK_ARG(k > 0, "tta_radius_graph_thresholds: cap k must be positive");
   TTA_CHECK_ARG(N == 0 || (thr_d2 && thr_src && thr_cell && err),
                 "tta_radius_graph_thresholds: null output");
   if (N == 0) return tta::kOk;
-  const NL p = make_nl(pos, N, lo, hi, shifts, n_cells, periodic, mid2, cut2, min2);
+  const NL p = make_nl(pos, N, lo, hi, shifts, n_cells, clo, chi, periodic, mid2, cut2, min2);
   hipLaunchKernelGGL(k_nl_thresh, dim3(tta_blocks(N, WAVES)), dim3(64 * WAVES), 0, stream, p, k,
                      thr_d2, thr_src, thr_cell, err);
   TTA_CHECK_LAUNCH("tta_radius_graph_thresholds");
@@ -277,16 +285,17 @@ extern "C" int tta_radius_graph_thresholds(const float* pos, int64_t N, const in
 }
 
 extern "C" int tta_radius_graph_count(const float* pos, int64_t N, const int* lo, const int* hi,
-                                      const float* shifts, int64_t n_cells, int periodic,
+                                      const float* shifts, int64_t n_cells, const int* clo,
+                                      const int* chi, int periodic,
                                       double mid2, float cut2, float min2, const float* thr_d2,
                                       const int* thr_src, const int* thr_cell, int* counts,
                                       hipStream_t stream) {
-  if (int st = check_nl(pos, N, shifts, n_cells, periodic, "tta_radius_graph_count")) return st;
+  if (int st = check_nl(pos, N, shifts, n_cells, clo, chi, periodic, "tta_radius_graph_count")) return st;
   TTA_CHECK_ARG(N == 0 || counts, "tta_radius_graph_count: null counts");
   TTA_CHECK_ARG((thr_d2 && thr_src && thr_cell) || (!thr_d2 && !thr_src && !thr_cell),
                 "tta_radius_graph_count: thresholds all or none");
   if (N == 0) return tta::kOk;
-  const NL p = make_nl(pos, N, lo, hi, shifts, n_cells, periodic, mid2, cut2, min2);
+  const NL p = make_nl(pos, N, lo, hi, shifts, n_cells, clo, chi, periodic, mid2, cut2, min2);
   hipLaunchKernelGGL(k_nl_rows<false>, dim3(tta_blocks(N, WAVES)), dim3(64 * WAVES), 0, stream,
                      p, thr_d2 != nullptr, thr_d2, thr_src, thr_cell, counts, nullptr, nullptr,
                      nullptr, nullptr);
@@ -295,18 +304,19 @@ extern "C" int tta_radius_graph_count(const float* pos, int64_t N, const int* lo
 }
 
 extern "C" int tta_radius_graph_write(const float* pos, int64_t N, const int* lo, const int* hi,
-                                      const float* shifts, int64_t n_cells, int periodic,
+                                      const float* shifts, int64_t n_cells, const int* clo,
+                                      const int* chi, int periodic,
                                       double mid2, float cut2, float min2, const float* thr_d2,
                                       const int* thr_src, const int* thr_cell,
                                       const int64_t* offsets, int64_t* edge_src,
                                       int64_t* edge_tgt, int* edge_cell, hipStream_t stream) {
-  if (int st = check_nl(pos, N, shifts, n_cells, periodic, "tta_radius_graph_write")) return st;
+  if (int st = check_nl(pos, N, shifts, n_cells, clo, chi, periodic, "tta_radius_graph_write")) return st;
   TTA_CHECK_ARG(N == 0 || (offsets && edge_src && edge_tgt && (!periodic || edge_cell)),
                 "tta_radius_graph_write: null output");
   TTA_CHECK_ARG((thr_d2 && thr_src && thr_cell) || (!thr_d2 && !thr_src && !thr_cell),
                 "tta_radius_graph_write: thresholds all or none");
   if (N == 0) return tta::kOk;
-  const NL p = make_nl(pos, N, lo, hi, shifts, n_cells, periodic, mid2, cut2, min2);
+  const NL p = make_nl(pos, N, lo, hi, shifts, n_cells, clo, chi, periodic, mid2, cut2, min2);
   hipLaunchKernelGGL(k_nl_rows<true>, dim3(tta_blocks(N, WAVES)), dim3(64 * WAVES), 0, stream, p,
                      thr_d2 != nullptr, thr_d2, thr_src, thr_cell, nullptr, offsets, edge_src,
                      edge_tgt, periodic ? edge_cell : nullptr);

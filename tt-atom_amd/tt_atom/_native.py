@@ -78,11 +78,12 @@ _SIGS = {
                        _I64, _I64, _I, _P],
     "tta_gemm_bf16x_group": [ctypes.POINTER(GemmProblem), _I64, _I, _P],
     "tta_gemm_f32_group": [ctypes.POINTER(GemmProblem), _I64, _P],
-    "tta_radius_graph_thresholds": [_P, _I64, _P, _P, _P, _I64, _I, _D, _F, _F, _I, _P, _P, _P,
-                                    _P, _P],
-    "tta_radius_graph_count": [_P, _I64, _P, _P, _P, _I64, _I, _D, _F, _F, _P, _P, _P, _P, _P],
-    "tta_radius_graph_write": [_P, _I64, _P, _P, _P, _I64, _I, _D, _F, _F, _P, _P, _P, _P, _P,
-                               _P, _P, _P],
+    "tta_radius_graph_thresholds": [_P, _I64, _P, _P, _P, _I64, _P, _P, _I, _D, _F, _F, _I, _P,
+                                    _P, _P, _P, _P],
+    "tta_radius_graph_count": [_P, _I64, _P, _P, _P, _I64, _P, _P, _I, _D, _F, _F, _P, _P, _P,
+                               _P, _P],
+    "tta_radius_graph_write": [_P, _I64, _P, _P, _P, _I64, _P, _P, _I, _D, _F, _F, _P, _P, _P,
+                               _P, _P, _P, _P, _P],
 }
 _RESTYPE = {"tta_last_error": ctypes.c_char_p, "tta_pack_b_elems": ctypes.c_int64}
 
@@ -592,17 +593,23 @@ def virial(ev, g_ev, work, out):
 
 
 # ----------------------------------------------------------------------------- neighbour list
-def radius_graph_passes(pos, lo, hi, shifts, periodic, mid2, cut2, min2, k):
+def radius_graph_passes(pos, lo, hi, shifts, periodic, mid2, cut2, min2, k, clo=None, chi=None):
     """The three device passes of the radius graph (thresholds with a cap, per-row counts,
-    ordered write); returns (src int64 [E], tgt int64 [E], cell int32 [E] or None)."""
+    ordered write); returns (src int64 [E], tgt int64 [E], cell int32 [E] or None).  clo / chi:
+    per-row image-shift ranges of a periodic batch (int32 device tensors, checked here on their
+    host copies by the caller, geometry.system_graphs)."""
     N = pos.shape[0]
     dev = pos.device
     n_cells = shifts.shape[0] if periodic else 0
     lo_p = None if lo is None else _i32(lo, N, "lo")
     hi_p = None if hi is None else _i32(hi, N, "hi")
+    if (clo is None) != (chi is None) or (clo is not None and not periodic):
+        raise ValueError("radius graph: cell ranges go with a periodic graph, both or neither")
+    clo_p = None if clo is None else _i32(clo, N, "clo")
+    chi_p = None if chi is None else _i32(chi, N, "chi")
     sh_p = _ptr(shifts, numel=3 * n_cells, name="shifts") if periodic else None
-    common = (_ptr(pos, numel=N * 3, name="pos"), N, lo_p, hi_p, sh_p, n_cells, int(periodic),
-              float(mid2), float(cut2), float(min2))
+    common = (_ptr(pos, numel=N * 3, name="pos"), N, lo_p, hi_p, sh_p, n_cells, clo_p, chi_p,
+              int(periodic), float(mid2), float(cut2), float(min2))
     thr = (None, None, None)
     if k:
         td = torch.empty(N, device=dev, dtype=torch.float32)

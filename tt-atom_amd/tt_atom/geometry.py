@@ -130,11 +130,54 @@ def radius_graph_device(pos, cutoff, cell=None, pbc=None, max_neighbors=None, *,
     return ei, shift
 
 
+def _periodic_batch_device(items, cutoff, max_neighbors):
+    """One batched device pass for periodic systems [(pos, cell, pbc)]: node ranges keep every
+    receiver's candidates in its system and per-row ranges into the concatenated image-shift
+    tables give it its own system's images, so each system's edges, order, cells and cap are those
+    of ``radius_graph_device`` on it alone.  Returns [(edge_index, cell_shift)] on the host, each
+    in its system's own node numbering."""
+    from . import _native as nat
+    pos_l, sh_l = [], []
+    for pos, cell, pbc in items:
+        p = torch.as_tensor(pos, dtype=torch.float32).detach().cpu()
+        pos_l.append(p)
+        sh_l.append(_image_shifts(p, cutoff, cell, pbc))
+    sizes = np.asarray([p.shape[0] for p in pos_l], np.int64)
+    nsh = np.asarray([s.shape[0] for s in sh_l], np.int64)
+    starts = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
+    cst = np.concatenate([[0], np.cumsum(nsh)[:-1]]).astype(np.int64)
+    lo, hi = np.repeat(starts, sizes), np.repeat(starts + sizes, sizes)
+    clo, chi = np.repeat(cst, sizes), np.repeat(cst + nsh, sizes)
+    N, n_cells = int(sizes.sum()), int(nsh.sum())
+    # the kernels index pos[lo..hi) and shifts[clo..chi) unchecked: bound them here
+    if N == 0 or not (lo.min() >= 0 and hi.max() <= N and clo.min() >= 0 and chi.max() <= n_cells
+                      and n_cells < (1 << 20)):
+        raise ValueError("periodic batch: empty or out-of-range node / image ranges")
+    dev = torch.device("cuda")
+    i32 = lambda a: torch.from_numpy(a.astype(np.int32)).to(dev)
+    shifts = torch.cat(sh_l).to(torch.float32)
+    sh_d = shifts.to(dev).contiguous()
+    k = int(max_neighbors) if max_neighbors is not None else 0
+    src, tgt, c = nat.radius_graph_passes(
+        torch.cat(pos_l).to(dev).contiguous(), i32(lo), i32(hi), sh_d, True, 0.0,
+        float(np.float32(cutoff * cutoff)), float(np.float32(1e-8)), k, i32(clo), i32(chi))
+    src, tgt, c = src.cpu(), tgt.cpu(), c.cpu().long()
+    # periodic rows are receivers: edges come grouped by system in order
+    bounds = np.searchsorted(tgt.numpy(), np.concatenate([starts, [N]]))
+    out = []
+    for q in range(len(items)):
+        a, b = int(bounds[q]), int(bounds[q + 1])
+        ei = torch.stack([src[a:b], tgt[a:b]], 0) - int(starts[q])
+        out.append((ei, shifts[c[a:b]]))
+    return out
+
+
 def system_graphs(systems, cutoff, max_neighbors=None, neighbor_list="host"):
     """Per-system neighbour lists of a disjoint batch: ``systems`` = [(pos [n,3], cell or None,
     pbc or None)], result [(edge_index [2,E_k] int64, cell_shift [E_k,3])] on the host, each in
     its system's own node numbering.  ``neighbor_list="device"`` builds all aperiodic systems in
-    one batched GPU pass and periodic ones one by one; the graphs are identical to the host's."""
+    one batched GPU pass and all periodic ones in another; the graphs are identical to the
+    host's."""
     if neighbor_list not in ("host", "device"):
         raise ValueError("neighbor_list must be 'host' or 'device'")
     out = [None] * len(systems)
@@ -156,10 +199,11 @@ def system_graphs(systems, cutoff, max_neighbors=None, neighbor_list="host"):
             for q, k in enumerate(ap):
                 part = ei[:, bounds[q]:bounds[q + 1]] - int(starts[q])
                 out[k] = (part, torch.zeros(part.shape[1], 3))
-        for k, (pos, cell, pbc) in enumerate(systems):
-            if periodic[k]:
-                ei, sh = radius_graph_device(pos, cutoff, cell, pbc, max_neighbors)
-                out[k] = (ei.cpu(), sh.cpu())
+        per = [k for k in range(len(systems)) if periodic[k]]
+        if per:
+            for k, g in zip(per, _periodic_batch_device([systems[k] for k in per], cutoff,
+                                                        max_neighbors)):
+                out[k] = g
     for k, (pos, cell, pbc) in enumerate(systems):
         if out[k] is None:
             out[k] = radius_graph(pos, cutoff, cell, pbc if periodic[k] else None, max_neighbors)

@@ -107,7 +107,7 @@ def assemble_orb(systems, r_max, max_num_neighbors, neighbor_list="host"):
     (disjoint.py:188-197): each sender keeps its ``max_num_neighbors`` nearest neighbours
     (ordered by (d^2, neighbour, image)), the rule the eSCN-MD path uses.
     ``neighbor_list="device"`` builds the same graph on the GPU (all aperiodic systems in one
-    batched pass, periodic ones one by one); the result is identical edge for edge."""
+    batched pass, all periodic ones in another); the result is identical edge for edge."""
     if len(systems) == 0:
         raise ValueError("empty batch")
     fields = []

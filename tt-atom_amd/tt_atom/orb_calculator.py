@@ -100,24 +100,55 @@ def zbl_energy_forces_stress(Z, senders, receivers, pos, shift, covalent_radii, 
 
 
 def zbl_batch(Z, senders, receivers, pos, shift, batch, natoms, covalent_radii,
-              aggregation="mean"):
-    """Pair repulsion of every system of a disjoint union in one autograd call: (energies [K],
-    forces [N, 3]).  The union's edges never join two systems, so the gradient of the summed
-    system energies gives each atom its own system's force (as orb_calculator.py:296-327
-    computes the union's ZBL once)."""
+              aggregation="mean", p=6):
+    """Pair repulsion of every system of a disjoint union: (energies [K], forces [N, 3]), fp64.
+    The union's edges never join two systems, so each atom's force comes from its own system (as
+    orb_calculator.py:296-327 computes the union's ZBL once).  The force is the closed-form
+    derivative of the pair energy of ``_zbl_pairs``, E(x) = k Zu Zv / (2x) * phi(x) * env(x / r)
+    with phi = sum_i c_i exp(-d_i x / a) and env the degree-p polynomial envelope, taken only
+    over the pairs inside the envelope -- the host autograd of zbl_energy_forces_stress, without
+    building a graph per call (same values to fp64 rounding)."""
     if aggregation not in ("mean", "sum"):
         raise ValueError(f"aggregation must be 'mean' or 'sum', got {aggregation!r}")
-    pos = torch.as_tensor(pos, dtype=torch.float64).detach().clone().requires_grad_(True)
-    v = pos[receivers] - pos[senders]
+    Zn = np.asarray(Z, dtype=np.int64)
+    s_i, r_i = np.asarray(senders, dtype=np.int64), np.asarray(receivers, dtype=np.int64)
+    P = np.asarray(pos, dtype=np.float64)
+    v = P[r_i] - P[s_i]
     if shift is not None:
-        v = v + torch.as_tensor(shift, dtype=torch.float64)
-    e = _zbl_pairs(Z, senders, receivers, v, covalent_radii)
+        v = v + np.asarray(shift, dtype=np.float64)
+    rad = np.asarray(covalent_radii, dtype=np.float64)
+    Zu, Zv = Zn[s_i] + 1, Zn[r_i] + 1
+    r_max = rad[Zu] + rad[Zv]
+    x_all = np.sqrt((v * v).sum(1))
+    near = np.nonzero(x_all < r_max)[0]
     K = len(natoms)
-    per_sys = torch.zeros(K, dtype=torch.float64).index_add_(0, batch[senders], e)
-    if aggregation == "mean":
-        per_sys = per_sys / torch.as_tensor(natoms, dtype=torch.float64)
-    (g,) = torch.autograd.grad(per_sys.sum(), [pos])
-    return per_sys.detach().numpy(), (-g).numpy()
+    b = np.asarray(batch, dtype=np.int64)
+    w_sys = 1.0 / np.asarray(natoms, dtype=np.float64) if aggregation == "mean" else np.ones(K)
+    e_sys = np.zeros(K)
+    F = np.zeros_like(P)
+    if near.size:
+        zu, zv, rm, x = Zu[near].astype(np.float64), Zv[near].astype(np.float64), r_max[near], \
+            x_all[near]
+        a = _ZBL_A_PRE * _BOHR / (zu ** _ZBL_A_EXP + zv ** _ZBL_A_EXP)
+        ex = [np.exp(-d * x / a) for d in _ZBL_D]
+        phi = sum(c * e for c, e in zip(_ZBL_C, ex))
+        dphi = sum(-c * d / a * e for c, d, e in zip(_ZBL_C, _ZBL_D, ex))
+        q = x / rm
+        env = (1.0 - (p + 1) * (p + 2) / 2.0 * q ** p + p * (p + 2) * q ** (p + 1)
+               - p * (p + 1) / 2.0 * q ** (p + 2))
+        denv = (-(p + 1) * (p + 2) / 2.0 * p * q ** (p - 1) + p * (p + 2) * (p + 1) * q ** p
+                - p * (p + 1) / 2.0 * (p + 2) * q ** (p + 1)) / rm
+        pre = 0.5 * _COULOMB * zu * zv
+        e = pre / x * phi * env
+        de = pre * (-phi * env / (x * x) + (dphi * env + phi * denv) / x)
+        sys_e = b[s_i[near]]
+        e_sys = np.bincount(sys_e, weights=e, minlength=K) * w_sys
+        g = (w_sys[sys_e] * de / x)[:, None] * v[near]        # dE_sys / dv per pair
+        n = P.shape[0]
+        for c in range(3):
+            F[:, c] = (np.bincount(s_i[near], weights=g[:, c], minlength=n)
+                       - np.bincount(r_i[near], weights=g[:, c], minlength=n))
+    return e_sys, F
 
 
 def _default_radii():

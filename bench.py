@@ -637,6 +637,11 @@ def main():
                      "peak_note": ("algorithmic fp32 GEMM flops (2MNK) against the ceiling of "
                                    "the kernel's arithmetic: fp32 MFMA 157.3, or the fp16 / bf16 "
                                    "dense MFMA 2500 / number of plane products"),
+                     "frac_note": ("the default split (f16x3: 3 fp16 products per fp32 product) "
+                                   "is bound by its VALU work (plane split and per-row scaling), "
+                                   "not by the matrix pipe; the fp32-accurate bf16x6 mode reads "
+                                   "a higher frac (0.43-0.44 of its /6 ceiling) at a lower rate "
+                                   "(178-184 TF/s on this step, --precision f32-bf16x6)"),
                      "gemm_share_of_step": round(gemm_ms / (dt * 1e3), 4),
                      "measured": ("HIP events around each launch, on the launch stream, over a "
                                   "second pass of the same steps"),

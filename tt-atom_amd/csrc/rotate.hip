@@ -42,9 +42,13 @@ template <int V>
 __device__ __forceinline__ typename VecT<V>::T ldv(const float* p) {
   return *reinterpret_cast<const typename VecT<V>::T*>(p);
 }
+// Streaming (nontemporal) stores: every edge-level output here is far larger than the L2 and is
+// consumed by a later kernel, so allocating it in the cache only evicts the gathered node rows
+// (measured on the C3 step: k_node_gather_sum -20 %, k_rotate_env_segsum -14 %,
+// k_gather_rotate_bw -4 %).
 template <int V>
 __device__ __forceinline__ void stv(float* p, typename VecT<V>::T v) {
-  *reinterpret_cast<typename VecT<V>::T*>(p) = v;
+  __builtin_nontemporal_store(v, reinterpret_cast<typename VecT<V>::T*>(p));
 }
 template <int V>
 __device__ __forceinline__ typename VecT<V>::T zv() {

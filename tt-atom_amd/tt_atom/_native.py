@@ -290,7 +290,7 @@ def _gemm_bf16x(x, pw, out, bias, epilogue, out2, aux, P=None, idx0=None, idx1=N
 
 
 def _split_ok(x, pw):
-    """The split-bf16 kernel (128 x 128 x 32 tiles) runs edge-level GEMMs; short-K or small-M
+    """The split kernel (128 x 128 x 32 tiles) runs edge-level GEMMs; short-K or small-M
     products stay on the fp32 MFMA kernel, whose smaller tiles fill the chip better there."""
     M, K = x.shape
     return (isinstance(pw, PackedWeight) and pw.packed is not None and M >= 4096 and K >= 128
@@ -299,7 +299,7 @@ def _split_ok(x, pw):
 
 def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None):
     """y = x @ w_t (+ bias) for 2-D row-major x [M, K] (any row stride) and w_t [K, N] (a tensor
-    or a PackedWeight; a packed weight runs on the split-bf16 kernel when the shapes allow)."""
+    or a PackedWeight; a packed weight runs on the split kernel when the shapes allow)."""
     M, K = x.shape
     K2, N = w_t.shape
     if K != K2:
@@ -322,7 +322,7 @@ MAX_GROUP = 8
 
 def linear_group(items):
     """Several independent products y = x @ w_t (+ bias) in one launch: ``items`` = [(x, w_t,
-    bias, out, epilogue, out2, aux)] (the last three optional).  All on the split-bf16 kernel
+    bias, out, epilogue, out2, aux)] (the last three optional).  All on the split kernel
     when every product qualifies for it (same plane mode), all on the fp32 kernel when none
     does; a mix runs one launch per product."""
     items = [tuple(it) + (EPI_STORE, None, None)[len(it) - 4:] for it in items]

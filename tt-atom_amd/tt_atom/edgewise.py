@@ -6,7 +6,7 @@ This is the message-passing core of the reference's ``Edgewise`` block (edgewise
 gather, ``rotation.rotate`` / fused_rotate, ``SO2Convolution``, inverse rotate, segment sum)
 without the radial MLP, gate and envelope, with the backward of forces.py:352-418 restricted to
 the rotation (Wigner) adjoint and closed by the Wigner VJP of geometry.py:87-155.  Kernels:
-``tta_edge_wigner``, ``tta_gather_rotate_src``, split-bf16 / fp32 GEMMs on the fused
+``tta_edge_wigner``, ``tta_gather_rotate_src``, split / fp32 GEMMs on the fused
 ``[[Wa, Wb], [-Wb, Wa]]`` blocks, ``tta_rotate_env_segsum``; backward
 ``tta_rotate_env_segsum_bw``, transposed GEMMs, ``tta_gather_rotate_src_bw``,
 ``tta_edge_geometry_bwd``.

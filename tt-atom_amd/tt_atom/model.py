@@ -46,7 +46,7 @@ PRECISIONS = {"f32": nat.SPLIT_F16X3, "f32-bf16x6": nat.SPLIT_F32, "f32-mfma": N
 
 
 def _gw(t, device, mode):
-    """A GEMM weight operand [K, N]: packed for the split-bf16 kernel unless mode is None."""
+    """A GEMM weight operand [K, N]: packed for the split kernel unless mode is None."""
     d = t if (isinstance(t, torch.Tensor) and t.is_cuda) else _dev(t, device)
     return nat.PackedWeight(d, mode) if mode is not None else d
 

@@ -523,13 +523,13 @@ def test_forces_virial_and_sum(nat):
     assert abs(float(so) - float(x.double().sum())) < 1e-3
 
 
-@pytest.mark.parametrize("split", [True, False])
-def test_linear_group_equals_separate_calls(nat, split):
+@pytest.mark.parametrize("mode,M", [(16, 5000), (6, 5000), (16, 700)])
+def test_linear_group_equals_separate_calls(nat, mode, M):
     """Grouped launches (one launch for up to four products: column blocks of one input and one
     output, as the SO(2) m-blocks use them, with bias / accumulate / two-output / silu-grad
-    epilogues) give the same bits as one call per product, on both kernels."""
+    epilogues) give the same bits as one call per product, on the split kernel in modes 16 and 6
+    (M = 5000) and on the fp32 kernel (M = 700 < 4096 routes there)."""
     g = torch.Generator().manual_seed(11)
-    M = 5000 if split else 700
     x = torch.randn(M, 9 * 128, generator=g).to(DEV)
     outs = {}
     for grouped in (False, True):
@@ -540,7 +540,7 @@ def test_linear_group_equals_separate_calls(nat, split):
         ws = [torch.randn(384, 640, generator=torch.Generator().manual_seed(3)) / 20,
               torch.randn(512, 512, generator=torch.Generator().manual_seed(4)) / 20,
               torch.randn(256, 256, generator=torch.Generator().manual_seed(5)) / 20]
-        ws = [nat.PackedWeight(w.to(DEV)) for w in ws]
+        ws = [nat.PackedWeight(w.to(DEV), mode) for w in ws]
         bias = torch.randn(640, generator=torch.Generator().manual_seed(6)).to(DEV)
         items = [(x[:, :384], ws[0], bias, out[:, :640], nat.EPI_STORE),
                  (x[:, 384:896], ws[1], None, out[:, 640:640 + 512], nat.EPI_PRE_SILU,

@@ -14,7 +14,7 @@ enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ACCUM = 2, EPI_PRE_SILU = 3, EPI_SILU_GR
 
 struct GemmArgs {
   const float* A;
-  const void* B;  // fp32 [K, N] (fp32 kernel) or packed bf16 planes (split-bf16 kernel)
+  const void* B;  // fp32 [K, N] (fp32 kernel) or packed fp16 / bf16 planes (split kernel)
   float* C;
   const float* bias;
   float* C2;

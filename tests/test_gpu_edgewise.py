@@ -28,6 +28,7 @@ def _ref(ei, vec, x, g, w, N):
 # fp32 CPU oracle itself is 7.3e-5 (relative to max |g_ev|) off the fp64 one on this input, at an
 # edge along -y, so the fp32 bound is 2e-4.
 @pytest.mark.parametrize("precision,tol_out,tol_gev", [("f32", 2e-6, 2e-4),
+                                                       ("f32-bf16x6", 2e-6, 2e-4),
                                                        ("f32-mfma", 2e-6, 2e-4),
                                                        ("bf16", 2e-2, 5e-2)])
 def test_edgewise_step_matches_oracle(nat, precision, tol_out, tol_gev):

@@ -42,6 +42,12 @@ template <int V>
 __device__ __forceinline__ typename VecT<V>::T ldv(const float* p) {
   return *reinterpret_cast<const typename VecT<V>::T*>(p);
 }
+// Nontemporal load for rows read exactly once (the radial rows and the edge adjoint of the
+// gather kernels), so they do not displace the gathered node rows in L2 (-3 % on both kernels).
+template <int V>
+__device__ __forceinline__ typename VecT<V>::T ldv_nt(const float* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const typename VecT<V>::T*>(p));
+}
 // Streaming (nontemporal) stores: every edge-level output here is far larger than the L2 and is
 // consumed by a later kernel, so allocating it in the cache only evicts the gathered node rows
 // (measured on the C3 step: k_node_gather_sum -20 %, k_rotate_env_segsum -14 %,
@@ -202,7 +208,7 @@ __global__ __launch_bounds__(256) void k_gather_rotate(const float* __restrict__
 #pragma unroll
     for (int m = 0; m < NSPH; ++m) {
       T v = o[m];
-      if (RAD) v = v * ldv<V>(rad + (int64_t)e * 6 * W + rad_block(m) * W + V * q);
+      if (RAD) v = v * ldv_nt<V>(rad + (int64_t)e * 6 * W + rad_block(m) * W + V * q);
       stv<V>(orow + m * W, v);
     }
   }
@@ -242,7 +248,7 @@ __global__ __launch_bounds__(256) void k_gather_rotate_bw(
 #pragma unroll
     for (int j = 0; j < NSPH; ++j) in[j] = ldv<V>(row + j * C);
 #pragma unroll
-    for (int m = 0; m < NSPH; ++m) gm[m] = ldv<V>(g_xf + eo + m * W + V * q);
+    for (int m = 0; m < NSPH; ++m) gm[m] = ldv_nt<V>(g_xf + eo + m * W + V * q);
     if (RAD) {
       const float* rr = rad + (int64_t)e * 6 * W + V * q;
       float* gr = g_rad + (int64_t)e * 6 * W + V * q;
@@ -256,7 +262,7 @@ __global__ __launch_bounds__(256) void k_gather_rotate_bw(
       stv<V>(gr + 4 * W, gm[4] * mr[4] + gm[6] * mr[6]);
       stv<V>(gr + 5 * W, gm[7] * mr[7] + gm[8] * mr[8]);
 #pragma unroll
-      for (int m = 0; m < NSPH; ++m) gm[m] = gm[m] * ldv<V>(rr + rad_block(m) * W);
+      for (int m = 0; m < NSPH; ++m) gm[m] = gm[m] * ldv_nt<V>(rr + rad_block(m) * W);
     }
     if (g_mcat) {
       T gi[NSPH];

@@ -187,7 +187,7 @@ def build_c5(torch, K=256):
     w = synthetic.random_orb_weights(cfg, synthetic.SEEDS["C5"] + synthetic.WEIGHT_SEED_OFFSET)
     systems = synthetic.c5_systems(K=K)
     t0 = time.perf_counter()
-    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"], truncate=True)
     nl_ms = (time.perf_counter() - t0) * 1e3
     return cfg, w, bg, nl_ms
 
@@ -492,7 +492,8 @@ def main():
         ref_bg = bg
         nl_dev = None if args.no_secondary else device_nl_ms(
             torch, lambda: (lambda g: (torch.stack([g.receivers, g.senders]), g.cell_shift))(
-                orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"], "device")),
+                orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"], "device",
+                                 truncate=True)),
             (torch.stack([ref_bg.receivers, ref_bg.senders]), ref_bg.cell_shift))
         pos_d = bg.pos.to(mdl.device)
 

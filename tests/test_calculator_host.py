@@ -1,6 +1,7 @@
 """Host-side logic of the calculator front end (no GPU): Voigt conversion, bundle round trip,
 coverage check, neighbour-list cap and configuration generators."""
 import numpy as np
+import pytest
 import torch
 
 from tt_atom import calculator, geometry, synthetic, weights
@@ -301,3 +302,76 @@ def test_orb_batched_host_terms_equal_per_system():
         e1 = orb.denormalize_energy(raw[k], bg.Z[off:off + n], n, w)
         assert abs(float(eb[k]) - float(e1)) <= 1e-12 * max(1.0, abs(float(e1)))
         off += n
+
+
+def test_batch_refused_when_it_does_not_match_the_merged_bundle(tmp_path):
+    """A bundle carrying merge inputs (ref@*) refuses a batch whose reduced composition or
+    (charge, spin) differs from them (calculator.py:191-218); one without them accepts any."""
+    cfg = dict(synthetic.CFG_UMA_S, sphere_channels=8, hidden_channels=8, edge_channels=8,
+               num_distance_basis=8, num_layers=1)
+    w, host = synthetic.random_uma_bundle(cfg, 5)
+    eth = synthetic.ethanol_batch(2)
+    pos0, Z0 = eth[0]["positions"], eth[0]["numbers"]
+    ref = dict(energy=-1.5, forces=np.zeros((len(Z0), 3)), pos=pos0, atomic_numbers=Z0,
+               charge=0.0, spin=1.0)
+    p = tmp_path / "merged.npz"
+    weights.save_bundle(p, cfg, w, host, reference=ref)
+    b = weights.WeightBundle.load(p)
+    r = b.reference
+    assert r["charge"] == 0.0 and r["spin"] == 1.0 and r["energy"] == -1.5
+    assert np.array_equal(r["atomic_numbers"], Z0) and r["cell"] is None
+    ok = list(eth)
+    calculator.check_batch_matches_bundle(b, ok)
+    # water: a different reduced composition
+    Zw = np.array([8, 1, 1])
+    wrong = ok + [dict(positions=np.zeros((3, 3)), numbers=Zw, charge=0.0, spin=1.0)]
+    with pytest.raises(ValueError, match="reduced composition"):
+        calculator.check_batch_matches_bundle(b, wrong)
+    # twice the molecule has the same reduced composition: accepted
+    dbl = dict(positions=np.concatenate([pos0, pos0 + 10.0]), numbers=np.concatenate([Z0, Z0]),
+               charge=0.0, spin=1.0)
+    calculator.check_batch_matches_bundle(b, ok + [dbl])
+    with pytest.raises(ValueError, match="charge, spin"):
+        calculator.check_batch_matches_bundle(
+            b, ok + [dict(positions=pos0, numbers=Z0, charge=1.0, spin=1.0)])
+    with pytest.raises(ValueError, match="charge, spin"):
+        calculator.check_batch_matches_bundle(
+            b, [dict(positions=pos0, numbers=Z0, charge=0.0, spin=2.0)])
+    p2 = tmp_path / "plain.npz"
+    weights.save_bundle(p2, cfg, w, host)
+    b2 = weights.WeightBundle.load(p2)
+    assert b2.reference is None
+    calculator.check_batch_matches_bundle(b2, wrong)
+
+
+def test_assemble_orb_refuses_over_cap_by_default():
+    """As the reference (disjoint.py:188-197): a system whose sender or receiver degree exceeds
+    max_num_neighbors is refused; truncate=True keeps each sender's nearest ones instead."""
+    from tt_atom import orb
+    systems = synthetic.c5_systems(K=2)
+    with pytest.raises(ValueError, match="max_num_neighbors=20"):
+        orb.assemble_orb(systems, 6.0, 20)
+    bg = orb.assemble_orb(systems, 6.0, 20, truncate=True)
+    assert int(torch.bincount(bg.senders).max()) <= 20
+    big = orb.assemble_orb(systems, 6.0, 1000)
+    n = big.pos.shape[0]
+    deg = max(int(torch.bincount(big.senders, minlength=n).max()),
+              int(torch.bincount(big.receivers, minlength=n).max()))
+    assert deg > 20
+    orb.assemble_orb(systems, 6.0, deg)           # exactly at the cap: accepted
+    with pytest.raises(ValueError):
+        orb.assemble_orb(systems, 6.0, deg - 1)
+    # an uncapped graph within the cap is the same with or without truncation
+    same = orb.assemble_orb(systems, 6.0, deg, truncate=True)
+    assert torch.equal(same.senders, big.senders) and torch.equal(same.receivers, big.receivers)
+
+
+def test_radius_graph_device_checks_node_ranges_on_the_host():
+    """Bad node ranges raise before anything reaches the device."""
+    pos = torch.zeros(4, 3)
+    lo = torch.tensor([0, 0, 2, 2])
+    hi = torch.tensor([2, 2, 4, 4])
+    for bad in ((lo[:3], hi), (lo, hi[:2]), (torch.tensor([0, 0, 2, -1]), hi),
+                (lo, torch.tensor([2, 2, 4, 5])), (torch.tensor([0, 3, 2, 2]), hi)):
+        with pytest.raises(ValueError, match="node_ranges"):
+            geometry.radius_graph_device(pos, 5.0, node_ranges=bad, device="cpu")

@@ -89,7 +89,8 @@ def _tiny_batch(K=3, seed=11, cfg=None, n_min=6, n_max=14, side=5.0):
     cfg = dict(S.CFG_ORB_TINY if cfg is None else cfg)
     w = S.random_orb_weights(cfg, seed + S.WEIGHT_SEED_OFFSET)
     systems = S.c5_systems(seed, K=K, n_min=n_min, n_max=n_max, side=side)
-    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"],
+                              truncate=True)
     return cfg, w, systems, bg
 
 
@@ -141,7 +142,8 @@ def test_orb_conditioning_and_batch_consistency(nat):
     # each system alone gives the same result as inside the batch
     off = 0
     for k, sysk in enumerate(systems):
-        one = orb.assemble_orb([sysk], cfg["cutoff"], cfg["max_num_neighbors"])
+        one = orb.assemble_orb([sysk], cfg["cutoff"], cfg["max_num_neighbors"],
+                              truncate=True)
         n = bg.natoms[k]
         r1, F1 = orb.energy_and_forces_batch(model, pos=one.pos, senders=one.senders,
                                              receivers=one.receivers, atomic_numbers=one.Z,
@@ -156,7 +158,8 @@ def test_orb_periodic_stress_matches_oracle(nat):
     cfg = dict(S.CFG_ORB_TINY)
     w = S.random_orb_weights(cfg, 99)
     pos, Z, cell = S.c4_system(seed=4, reps=2, a=3.61, noise=0.05, Z=29)
-    bg = orb.assemble_orb([(pos, Z, cell, [True] * 3)], cfg["cutoff"], cfg["max_num_neighbors"])
+    bg = orb.assemble_orb([(pos, Z, cell, [True] * 3)], cfg["cutoff"],
+                          cfg["max_num_neighbors"], truncate=True)
     model = orb.OrbModel(w, cfg)
     raw, F, vir = orb.energy_and_forces(model, pos=bg.pos, senders=bg.senders,
                                         receivers=bg.receivers, atomic_numbers=bg.Z,
@@ -177,7 +180,8 @@ def test_orb_c5_architecture_reduced_batch(nat):
     cfg = dict(S.CFG_ORB_C5)
     w = S.random_orb_weights(cfg, S.SEEDS["C5"] + S.WEIGHT_SEED_OFFSET)
     systems = S.c5_systems()[:8]
-    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"],
+                              truncate=True)
     model = orb.OrbModel(w, cfg)
     raw, F = orb.energy_and_forces_batch(model, pos=bg.pos, senders=bg.senders,
                                          receivers=bg.receivers, atomic_numbers=bg.Z,
@@ -194,7 +198,8 @@ def test_orb_c5_full_batch(nat):
     """The full C5 workload (256 molecules, 10,150 atoms, E = 196,555) against the fp32 oracle."""
     cfg = dict(S.CFG_ORB_C5)
     w = S.random_orb_weights(cfg, S.SEEDS["C5"] + S.WEIGHT_SEED_OFFSET)
-    bg = orb.assemble_orb(S.c5_systems(), cfg["cutoff"], cfg["max_num_neighbors"])
+    bg = orb.assemble_orb(S.c5_systems(), cfg["cutoff"], cfg["max_num_neighbors"],
+                              truncate=True)
     model = orb.OrbModel(w, cfg)
     raw, F = orb.energy_and_forces_batch(model, pos=bg.pos, senders=bg.senders,
                                          receivers=bg.receivers, atomic_numbers=bg.Z,
@@ -218,7 +223,8 @@ def test_orb_session_single_and_batch(nat, tmp_path):
     res = [sess.evaluate(p, z) for p, z in systems]
     # oracle: raw GNN energy / forces + the same host ZBL
     for (p, z), r in zip(systems, res):
-        bg = orb.assemble_orb([(p, z)], cfg["cutoff"], cfg["max_num_neighbors"])
+        bg = orb.assemble_orb([(p, z)], cfg["cutoff"], cfg["max_num_neighbors"],
+                              truncate=True)
         raw, F = _oracle(cfg, w, bg)
         n = bg.natoms[0]
         e_z, f_z, _ = OC.zbl_energy_forces_stress(bg.Z, bg.senders, bg.receivers, bg.pos,
@@ -243,7 +249,8 @@ def test_orb_step_graph_replays_match_eager():
     cfg = dict(synthetic.CFG_ORB_TINY)
     w = synthetic.random_orb_weights(cfg, 7)
     systems = synthetic.c5_systems(K=4)
-    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"],
+                              truncate=True)
     model = orb.OrbModel(w, cfg)
     graph = orb.OrbGraph(model.device, senders=bg.senders, receivers=bg.receivers,
                          num_nodes=bg.pos.shape[0], atomic_numbers=bg.Z, cell_shift=bg.cell_shift,
@@ -315,7 +322,8 @@ def test_orb_direct_heads_match_oracle(nat, arch):
         cfg = dict(S.CFG_ORB_C5)
         systems = S.c5_systems()[:8]
     w = S.random_orb_weights(cfg, 41, direct=True)
-    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"])
+    bg = orb.assemble_orb(systems, cfg["cutoff"], cfg["max_num_neighbors"],
+                              truncate=True)
     model, eng = _direct_engine(cfg, w, bg)
     assert model.is_direct and model.has_stress_head
     p = bg.pos.to(model.device)
@@ -340,11 +348,13 @@ def test_orb_direct_session(nat, tmp_path):
     path = tmp_path / "orb_direct.npz"
     orb.save_orb_bundle(path, cfg, w)
     radii = np.full(120, 0.6)
-    sess = OC.OrbSession(str(path), pair_repulsion=True, covalent_radii=radii)
+    sess = OC.OrbSession(str(path), pair_repulsion=True, covalent_radii=radii,
+                         truncate_neighbors=True)
     assert sess.is_direct and sess.zbl_aggregation == "sum"
     pos, Z, cell = S.c4_system(seed=4, reps=2, a=3.61, noise=0.05, Z=29)
     r = sess.evaluate(pos, Z, cell=cell, pbc=[True] * 3, properties=("energy", "forces", "stress"))
-    bg = orb.assemble_orb([(pos, Z, cell, [True] * 3)], cfg["cutoff"], cfg["max_num_neighbors"])
+    bg = orb.assemble_orb([(pos, Z, cell, [True] * 3)], cfg["cutoff"],
+                          cfg["max_num_neighbors"], truncate=True)
     e_raw, f_raw, s_raw = O.direct_forward(w, cfg, bg.pos.double(), bg.Z, bg.senders,
                                            bg.receivers, bg.cell_shift.double(), bg.batch,
                                            bg.natoms, compute_stress=True)
@@ -371,7 +381,7 @@ def test_orb_direct_session(nat, tmp_path):
     w_ns = {k: v for k, v in w.items() if not k.startswith("stress_head.")}
     path2 = tmp_path / "orb_direct_nostress.npz"
     orb.save_orb_bundle(path2, cfg, w_ns)
-    sess2 = OC.OrbSession(str(path2), pair_repulsion=False)
+    sess2 = OC.OrbSession(str(path2), pair_repulsion=False, truncate_neighbors=True)
     with pytest.raises(ValueError, match="stress_head"):
         sess2.evaluate(pos, Z, cell=cell, pbc=[True] * 3, properties=("energy", "stress"))
     r2 = sess2.evaluate(pos, Z, cell=cell, pbc=[True] * 3)     # implicit stress: left out
@@ -401,7 +411,8 @@ def test_orb_c5_full_batch_translation(nat):
     force unchanged (fp32 resolution) and each molecule's forces sum to zero."""
     cfg = dict(S.CFG_ORB_C5)
     w = S.random_orb_weights(cfg, S.SEEDS["C5"] + S.WEIGHT_SEED_OFFSET)
-    bg = orb.assemble_orb(S.c5_systems(), cfg["cutoff"], cfg["max_num_neighbors"])
+    bg = orb.assemble_orb(S.c5_systems(), cfg["cutoff"], cfg["max_num_neighbors"],
+                              truncate=True)
     model = orb.OrbModel(w, cfg)
     graph = orb.OrbGraph(model.device, senders=bg.senders, receivers=bg.receivers,
                          num_nodes=bg.pos.shape[0], atomic_numbers=bg.Z, cell_shift=bg.cell_shift,

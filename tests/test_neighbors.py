@@ -124,8 +124,8 @@ def test_assemble_orb_device_equals_host():
     systems = synthetic.c5_systems(K=12)
     pos, Z, cell = synthetic.c4_system(reps=2)
     systems = systems[:5] + [dict(positions=pos, numbers=Z, cell=cell, pbc=[True] * 3)] + systems[5:]
-    h = orb.assemble_orb(systems, 6.0, 20)
-    d = orb.assemble_orb(systems, 6.0, 20, neighbor_list="device")
+    h = orb.assemble_orb(systems, 6.0, 20, truncate=True)
+    d = orb.assemble_orb(systems, 6.0, 20, neighbor_list="device", truncate=True)
     for a, b in ((h.senders, d.senders), (h.receivers, d.receivers), (h.cell_shift, d.cell_shift),
                  (h.pos, d.pos), (h.Z, d.Z), (h.batch, d.batch)):
         assert torch.equal(a, b)

@@ -294,7 +294,8 @@ def _split_ok(x, pw):
     products stay on the fp32 MFMA kernel, whose smaller tiles fill the chip better there."""
     M, K = x.shape
     return (isinstance(pw, PackedWeight) and pw.packed is not None and M >= 4096 and K >= 128
-            and x.data_ptr() % 16 == 0 and _ld(x, "x") % 4 == 0 and _ld(x, "x") < (1 << 21))
+            and K % 4 == 0 and x.data_ptr() % 16 == 0 and _ld(x, "x") % 4 == 0
+            and _ld(x, "x") < (1 << 21))
 
 
 def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None):

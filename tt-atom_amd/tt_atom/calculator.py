@@ -27,6 +27,32 @@ except ImportError:  # pragma: no cover - exercised where ase is absent
     HAVE_ASE = False
 
 
+def check_batch_matches_bundle(bundle, systems):
+    """Refuse a batch that a merged bundle was not built for (calculator.py:191-218): a merged
+    uma-s-1 bundle bakes the MoLE expert routing for one reduced composition and one
+    (charge, spin), so every system must share those of the bundle's merge inputs (``ref@*``).
+    Bundles without merge inputs (random-init weights) accept any batch."""
+    ref = bundle.reference if hasattr(bundle, "reference") else None
+    if ref is None:
+        return
+    from .bundle_cache import reduced_composition
+    from .orb import _fields
+    want_comp = reduced_composition(ref["atomic_numbers"])
+    want_cs = (float(ref["charge"]), float(ref["spin"]))
+    for k, system in enumerate(systems):
+        _, Z, _, _, charge, spin = _fields(system)
+        if reduced_composition(np.asarray(Z)) != want_comp:
+            raise ValueError(
+                f"batched system {k} has a different reduced composition than this bundle: a "
+                "merged bundle bakes the MoLE routing for one reduced composition, so every "
+                "system of a batch must share it; evaluate other compositions with their own "
+                "bundle")
+        if (float(charge), float(spin)) != want_cs:
+            raise ValueError(
+                f"batched system {k} has (charge, spin)=({float(charge)}, {float(spin)}) but "
+                f"this bundle was merged for {want_cs}; every system of a batch must share it")
+
+
 def full_3x3_to_voigt_6(s):
     """ASE's Voigt order (xx, yy, zz, yz, xz, xy) with symmetrised off-diagonals."""
     s = np.asarray(s, dtype=np.float64).reshape(3, 3)
@@ -121,6 +147,7 @@ class Session:
         forces=list[ndarray[N_k, 3]] or None)`` with the per-system energy normaliser applied.
         The step engine (and its HIP graph) is kept while the batch topology is unchanged."""
         from . import disjoint
+        check_batch_matches_bundle(self.bundle, systems)
         bg = disjoint.assemble(systems, self.cfg["cutoff"], self._w, self.C, task=self.task,
                                max_neighbors=self.max_neighbors, neighbor_list=self.neighbor_list)
         periodic = bool(bg.cell_shift.abs().sum() > 0)

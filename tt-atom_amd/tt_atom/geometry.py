@@ -105,6 +105,15 @@ def radius_graph_device(pos, cutoff, cell=None, pbc=None, max_neighbors=None, *,
     periodic = cell is not None and pbc is not None and bool(torch.as_tensor(pbc).any())
     if periodic and node_ranges is not None:
         raise ValueError("node_ranges applies to aperiodic batches only")
+    if node_ranges is not None:
+        # the kernels read pos[lo .. hi) of every row unchecked: bound the ranges on the host
+        lo_h = torch.as_tensor(node_ranges[0]).detach().cpu().reshape(-1).long()
+        hi_h = torch.as_tensor(node_ranges[1]).detach().cpu().reshape(-1).long()
+        if lo_h.numel() != N or hi_h.numel() != N:
+            raise ValueError(f"node_ranges need {N} lo and {N} hi entries, got "
+                             f"{lo_h.numel()} and {hi_h.numel()}")
+        if N and not bool(((lo_h >= 0) & (lo_h <= hi_h) & (hi_h <= N)).all()):
+            raise ValueError("node_ranges must satisfy 0 <= lo <= hi <= N for every node")
     mid2, cut2, min2 = 0.0, 0.0, 0.0
     if periodic:
         shifts = _image_shifts(pos_h, cutoff, cell, pbc)

@@ -100,12 +100,15 @@ def _fields(system):
     return pos, Z, cell, pbc, 0.0, 0.0
 
 
-def assemble_orb(systems, r_max, max_num_neighbors, neighbor_list="host"):
+def assemble_orb(systems, r_max, max_num_neighbors, neighbor_list="host", truncate=False):
     """Block-diagonal graph of ``systems`` (ASE Atoms, dicts or (pos, Z[, cell, pbc]) tuples):
     per-system neighbour list, senders = tgt and receivers = src (Orb's convention), node
-    offsets.  Departure from the reference, which refuses a system whose degree exceeds the cap
-    (disjoint.py:188-197): each sender keeps its ``max_num_neighbors`` nearest neighbours
-    (ordered by (d^2, neighbour, image)), the rule the eSCN-MD path uses.
+    offsets (disjoint.py:162-218).  As the reference does, a system with an atom whose sender or
+    receiver degree exceeds ``max_num_neighbors`` is refused with a ValueError
+    (disjoint.py:188-197).  ``truncate=True`` instead keeps, per sender, its
+    ``max_num_neighbors`` nearest neighbours (ordered by (d^2, neighbour, image)), the cap rule
+    of the eSCN-MD path: an explicit opt-in whose graph is not pinned against orb-models' own
+    truncation (parity unpinned for capped graphs).
     ``neighbor_list="device"`` builds the same graph on the GPU (all aperiodic systems in one
     batched pass, all periodic ones in another); the result is identical edge for edge."""
     if len(systems) == 0:
@@ -115,8 +118,21 @@ def assemble_orb(systems, r_max, max_num_neighbors, neighbor_list="host"):
         pos, Z, cell, pbc, charge, spin = _fields(system)
         fields.append((torch.as_tensor(np.asarray(pos), dtype=torch.float32),
                        torch.as_tensor(np.asarray(Z), dtype=torch.int64), cell, pbc, charge, spin))
-    graphs = system_graphs([(f[0], f[2], f[3]) for f in fields], r_max, max_num_neighbors,
-                           neighbor_list)
+    graphs = system_graphs([(f[0], f[2], f[3]) for f in fields], r_max,
+                           max_num_neighbors if truncate else None, neighbor_list)
+    if not truncate:
+        for k, (ei, _) in enumerate(graphs):
+            n = int(fields[k][1].shape[0])
+            if ei.shape[1] == 0:
+                continue
+            max_deg = max(int(torch.bincount(ei[1], minlength=n).max()),
+                          int(torch.bincount(ei[0], minlength=n).max()))
+            if max_deg > max_num_neighbors:
+                raise ValueError(
+                    f"system {k} has an atom with {max_deg} neighbours within the {r_max} A "
+                    f"cutoff, exceeding max_num_neighbors={max_num_neighbors}; pass "
+                    "truncate=True to keep each atom's nearest max_num_neighbors instead (a "
+                    "graph not pinned against orb-models' own truncation)")
     pos_all, Z_all, s_all, r_all, sh_all, b_all, natoms, q_all, s_spin = ([] for _ in range(9))
     off = 0
     for k, (pos, Z, cell, pbc, charge, spin) in enumerate(fields):

@@ -165,7 +165,10 @@ class OrbSession:
     """One Orb-v3 checkpoint, conservative or direct, on one GPU (orb_calculator.py:26-73)."""
 
     def __init__(self, weights, device=None, device_id=0, precision="f32", pair_repulsion=True,
-                 covalent_radii=None, neighbor_list="device"):
+                 covalent_radii=None, neighbor_list="device", truncate_neighbors=False):
+        """``truncate_neighbors=False`` refuses a system with an atom over the checkpoint's
+        ``max_num_neighbors`` as the reference does (orb_calculator.py:110-125); True keeps each
+        atom's nearest ones instead (``orb.assemble_orb(truncate=True)``)."""
         if isinstance(weights, str):
             weights = orb.OrbWeights.load(weights)
         self.cfg = dict(weights.config)
@@ -178,6 +181,7 @@ class OrbSession:
         self.pair_repulsion = pair_repulsion
         self._radii = covalent_radii
         self.neighbor_list = neighbor_list
+        self.truncate_neighbors = bool(truncate_neighbors)
         self.is_direct = self.model.is_direct
         self.zbl_aggregation = "sum" if self.is_direct else "mean"
         self._engine, self._key = None, None
@@ -221,7 +225,8 @@ class OrbSession:
             if (cell is not None and pbc_a.any()) else None
         system = dict(positions=positions, numbers=numbers, cell=cell_a,
                       pbc=pbc_a if cell_a is not None else None, charge=charge, spin=spin)
-        bg = orb.assemble_orb([system], self.r_max, self.max_num_neighbors, self.neighbor_list)
+        bg = orb.assemble_orb([system], self.r_max, self.max_num_neighbors, self.neighbor_list,
+                              truncate=self.truncate_neighbors)
         explicit_stress = "stress" in properties
         want_stress = cell_a is not None and (explicit_stress or bool(pbc_a.all()))
         if self.is_direct and not self.model.has_stress_head:
@@ -259,7 +264,8 @@ class OrbSession:
         """Disjoint-union batch in one device step (orb_calculator.py:217-327):
         ``dict(energy=ndarray[K], forces=list[ndarray[N_k, 3]] or None)``."""
         want_forces = "forces" in properties
-        bg = orb.assemble_orb(systems, self.r_max, self.max_num_neighbors, self.neighbor_list)
+        bg = orb.assemble_orb(systems, self.r_max, self.max_num_neighbors, self.neighbor_list,
+                              truncate=self.truncate_neighbors)
         raw, F_raw, _ = self._run(bg, False)
         batch = bg.batch.long()
         n_of = torch.as_tensor(bg.natoms, dtype=torch.float64)

@@ -57,6 +57,22 @@ class WeightBundle(NpzBundle):
         return self._t("scale@elem_refs").double() if self.has("scale@elem_refs") else None
 
     @property
+    def reference(self):
+        """The merge inputs a merged bundle carries (``ref@*`` keys, weights.py:45-60): the
+        system the MoLE routing was baked for (positions, numbers, charge, spin, optional cell /
+        pbc) and its fairchem energy / forces, or None for bundles without them (random-init
+        bundles)."""
+        if not self.has("ref@energy"):
+            return None
+        d = self._d
+        return dict(
+            energy=float(d["ref@energy"][0]), forces=np.array(d["ref@forces"]),
+            pos=np.array(d["ref@pos"]), atomic_numbers=np.array(d["ref@atomic_numbers"]),
+            charge=float(d["ref@charge"][0]), spin=float(d["ref@spin"][0]),
+            cell=np.array(d["ref@cell"]) if self.has("ref@cell") else None,
+            pbc=np.array(d["ref@pbc"]) if self.has("ref@pbc") else None)
+
+    @property
     def to_m(self):
         return self.buffer("to_m")
 
@@ -121,8 +137,9 @@ class WeightBundle(NpzBundle):
         return (len(missing) == 0, missing, len(w))
 
 
-def save_bundle(path, cfg, weights, host, scale=None):
-    """Write a bundle in the same layout the loader reads."""
+def save_bundle(path, cfg, weights, host, scale=None, reference=None):
+    """Write a bundle in the same layout the loader reads; ``reference`` (a dict with the keys
+    of ``WeightBundle.reference``) is stored as the ``ref@*`` merge inputs."""
     d = {"config": np.frombuffer(json.dumps(cfg).encode(), dtype=np.uint8)}
     for k, v in weights.items():
         d[f"w@{k}"] = np.asarray(torch.as_tensor(v).detach().cpu().float().numpy())
@@ -131,4 +148,10 @@ def save_bundle(path, cfg, weights, host, scale=None):
             d[f"host@{k}"] = np.asarray(torch.as_tensor(v).detach().cpu().numpy())
     for k, v in (scale or {}).items():
         d[f"scale@{k}"] = np.asarray(v, dtype=np.float64).reshape(-1)
+    for k, v in (reference or {}).items():
+        if v is None:
+            continue
+        if k in ("energy", "charge", "spin"):
+            v = np.asarray([v], dtype=np.float64)
+        d[f"ref@{k}"] = np.asarray(v)
     np.savez(pathlib.Path(path), **d)

@@ -75,20 +75,51 @@ def _ref32(ei, vec, x, g, w, N):
     return out.detach(), g_ev
 
 
-def test_edgewise_full_size_matches_oracle(nat):
-    """The full C2 workload (N = 8192, E = 204,800, C = 128) against the fp64 oracle: output and
-    edge-vector VJP errors (relative to the largest magnitude) within twice those of the fp32
-    CPU oracle on the same inputs, or within the reduced test's bounds (2e-6 / 2e-4)."""
+_FULL_REF = {}
+
+
+def _full_refs():
+    """C2 full-size inputs and the fp64 / fp32 oracle results, computed once per module."""
+    if not _FULL_REF:
+        ei, vec, x, g = S.c2_tensors()
+        w = S.c2_weights()
+        _FULL_REF.update(inputs=(ei, vec, x, g), w=w, ref64=_ref(ei, vec, x, g, w, 8192),
+                         ref32=_ref32(ei, vec, x, g, w, 8192))
+    return _FULL_REF
+
+
+# f32: errors relative to the largest magnitude within twice the fp32 CPU oracle's on the same
+# inputs, or within the reduced test's bounds (2e-6 / 2e-4).
+# bf16 operands (~2^-9 relative rounding per operand): output within 2e-2 of its largest
+# magnitude.  The edge-vector VJP of an edge at polar angle beta from the frame's pole (the +-y
+# axis) carries the Euler-angle derivative d(alpha)/d(ev) ~ 1 / (|ev| sin(beta)), which
+# amplifies any rounding of that edge's coefficient adjoint by 1 / sin(beta): among 204,800
+# random directions the nearest edge sits at sin(beta) ~ 3e-3, and even the fp32 oracle is
+# 1.4e-4 off there.  The bf16 bounds are therefore stated on the conditioning-weighted error
+# max_e |dg_e| sin(beta_e) / max |g| < 5e-2 and on the normwise error ||dg|| / ||g|| < 2e-2.
+@pytest.mark.parametrize("precision", ["f32", "bf16"])
+def test_edgewise_full_size_matches_oracle(nat, precision):
+    """The full C2 workload (N = 8192, E = 204,800, C = 128) against the fp64 oracle."""
     from tt_atom.edgewise import EdgewiseStep
-    ei, vec, x, g = S.c2_tensors()
-    w = S.c2_weights()
-    step = EdgewiseStep(w, "c2", S.jd_matrices(), ei[0], ei[1], 8192)
+    ref = _full_refs()
+    ei, vec, x, g = ref["inputs"]
+    step = EdgewiseStep(ref["w"], "c2", S.jd_matrices(), ei[0], ei[1], 8192, precision=precision)
     out, g_ev = step(x, vec, g)
-    r_out, r_gev = _ref(ei, vec, x, g, w, 8192)
-    f_out, f_gev = _ref32(ei, vec, x, g, w, 8192)
+    r_out, r_gev = ref["ref64"]
+    f_out, f_gev = ref["ref32"]
     rel = lambda a, b: (a.cpu().double() - b).abs().max().item() / b.abs().max().item()
     e_out, e_gev = rel(out, r_out), rel(g_ev, r_gev)
     b_out, b_gev = rel(f_out, r_out), rel(f_gev, r_gev)
-    print(f"C2 full: GPU out {e_out:.2e}, g_ev {e_gev:.2e}; fp32 oracle out {b_out:.2e}, "
-          f"g_ev {b_gev:.2e}", flush=True)
-    assert e_out < max(2e-6, 2 * b_out) and e_gev < max(2e-4, 2 * b_gev), (e_out, e_gev)
+    print(f"C2 full ({precision}): GPU out {e_out:.2e}, g_ev {e_gev:.2e}; fp32 oracle out "
+          f"{b_out:.2e}, g_ev {b_gev:.2e}", flush=True)
+    if precision == "bf16":
+        v = torch.from_numpy(vec).double()
+        sinb = torch.sqrt(v[:, 0] ** 2 + v[:, 2] ** 2) / torch.linalg.norm(v, dim=1)
+        dg = (g_ev.cpu().double() - r_gev).abs().max(dim=1).values
+        w_gev = (dg * sinb).max().item() / r_gev.abs().max().item()
+        n_gev = (torch.linalg.norm(g_ev.cpu().double() - r_gev) / torch.linalg.norm(r_gev)).item()
+        print(f"C2 full (bf16): conditioning-weighted g_ev {w_gev:.2e}, normwise {n_gev:.2e}, "
+              f"min sin(beta) {sinb.min().item():.1e}", flush=True)
+        assert e_out < 2e-2 and w_gev < 5e-2 and n_gev < 2e-2, (e_out, w_gev, n_gev)
+    else:
+        assert e_out < max(2e-6, 2 * b_out) and e_gev < max(2e-4, 2 * b_gev), (e_out, e_gev)

@@ -208,6 +208,86 @@ def test_orb_c5_full_batch(nat):
     _check(cfg, w, bg, raw, F, oracle_dtype=torch.float32)
 
 
+# bf16 operands (8 significant bits, relative rounding 2^-9 per operand) in every edge- and
+# node-level product of the 5-layer, 1024-wide C5 network, with fp32 accumulation: the error of
+# the raw energy and of the forces is a few 1e-3 of their magnitude, against ~1e-7 for the fp32
+# arithmetic.  Stated bounds: raw energy within 2e-2 of max(1, |raw|) per system, forces within
+# 4e-2 of the largest |F| of the batch (both relative, vs the fp64 oracle).
+BF16_TOL_RAW, BF16_TOL_F = 2e-2, 4e-2
+
+
+def _bf16_errors(cfg, w, bg, raw, F, oracle_dtype=torch.float64):
+    ref_raw, ref_F = _oracle(cfg, w, bg, dtype=oracle_dtype)
+    ref_raw, ref_F = ref_raw.double(), ref_F.double()
+    e_raw = ((raw.double() - ref_raw).abs() / ref_raw.abs().clamp_min(1.0)).max().item()
+    e_f = (F.double() - ref_F).abs().max().item() / ref_F.abs().max().item()
+    return e_raw, e_f
+
+
+def test_orb_c5_bf16_matches_oracle(nat):
+    """C5 architecture with bf16 GEMM operands (BASELINE configs[4] 'fp32/bf16') on 8 of its
+    molecules against the fp64 oracle, within the stated bf16 bounds; the fp32 default on the
+    same batch is checked at its own tolerance alongside, and bf16 must actually differ from it
+    (the bf16 kernels ran)."""
+    cfg = dict(S.CFG_ORB_C5)
+    w = S.random_orb_weights(cfg, S.SEEDS["C5"] + S.WEIGHT_SEED_OFFSET)
+    bg = orb.assemble_orb(S.c5_systems()[:8], cfg["cutoff"], cfg["max_num_neighbors"],
+                          truncate=True)
+    kw = dict(pos=bg.pos, senders=bg.senders, receivers=bg.receivers, atomic_numbers=bg.Z,
+              natoms=bg.natoms, cell_shift=bg.cell_shift)
+    raw16, F16 = orb.energy_and_forces_batch(orb.OrbModel(w, cfg, precision="bf16"), **kw)
+    raw32, F32 = orb.energy_and_forces_batch(orb.OrbModel(w, cfg), **kw)
+    e_raw, e_f = _bf16_errors(cfg, w, bg, raw16, F16)
+    print(f"C5 bf16 (8 molecules, E = {bg.senders.numel()}): raw energy rel {e_raw:.2e}, "
+          f"forces rel {e_f:.2e}", flush=True)
+    assert e_raw < BF16_TOL_RAW and e_f < BF16_TOL_F, (e_raw, e_f)
+    assert not torch.equal(F16, F32)
+    _check(cfg, w, bg, raw32, F32)
+
+
+def test_orb_c5_bf16_full_batch_properties(nat):
+    """The full C5 batch (256 molecules) in bf16: (i) the first 128 molecules as a batch of their
+    own give the same per-system results as inside the full batch (every kernel is row-local and
+    every reduction runs in a fixed order, so the slices agree to fp32 rounding; the sub-batch
+    has at least 4096 nodes so that its node-level products take the same bf16 kernel as the full
+    batch's -- smaller products run on the fp32 kernel); (ii) a rigid translation of every
+    molecule leaves the energies unchanged and the forces unchanged within the bf16 bounds;
+    (iii) the forces of every molecule sum to zero within bf16 rounding."""
+    cfg = dict(S.CFG_ORB_C5)
+    w = S.random_orb_weights(cfg, S.SEEDS["C5"] + S.WEIGHT_SEED_OFFSET)
+    systems = S.c5_systems()
+    model = orb.OrbModel(w, cfg, precision="bf16")
+
+    def run(sys_list):
+        bg = orb.assemble_orb(sys_list, cfg["cutoff"], cfg["max_num_neighbors"], truncate=True)
+        raw, F = orb.energy_and_forces_batch(model, pos=bg.pos, senders=bg.senders,
+                                             receivers=bg.receivers, atomic_numbers=bg.Z,
+                                             natoms=bg.natoms, cell_shift=bg.cell_shift)
+        return bg, raw.double(), F.double()
+
+    K = 128
+    bg, raw, F = run(systems)
+    bgK, rawK, FK = run(systems[:K])
+    nK = sum(bgK.natoms)
+    assert nK >= 4096, nK
+    d_raw = ((raw[:K] - rawK).abs() / rawK.abs().clamp_min(1.0)).max().item()
+    d_f = (F[:nK] - FK).abs().max().item() / FK.abs().max().item()
+    print(f"C5 bf16 full batch vs first {K} ({nK} atoms): raw rel {d_raw:.2e}, forces rel "
+          f"{d_f:.2e} (exact: {torch.equal(raw[:K], rawK) and torch.equal(F[:nK], FK)})",
+          flush=True)
+    assert d_raw < 1e-5 and d_f < 1e-4, (d_raw, d_f)
+    shift = np.array([3.7, -1.2, 0.55], np.float32)
+    _, raw_t, F_t = run([(p + shift, z) for p, z in systems])
+    t_raw = ((raw_t - raw).abs() / raw.abs().clamp_min(1.0)).max().item()
+    t_f = (F_t - F).abs().max().item() / F.abs().max().item()
+    print(f"C5 bf16 translation: raw rel {t_raw:.2e}, forces rel {t_f:.2e}", flush=True)
+    assert t_raw < BF16_TOL_RAW and t_f < BF16_TOL_F, (t_raw, t_f)
+    net = torch.zeros(len(bg.natoms), 3, dtype=torch.float64).index_add_(0, bg.batch.long(), F)
+    net_rel = net.abs().max().item() / F.abs().max().item()
+    print(f"C5 bf16 net force per molecule: {net_rel:.2e} of max |F|", flush=True)
+    assert net_rel < BF16_TOL_F
+
+
 def test_orb_session_single_and_batch(nat, tmp_path):
     """OrbSession (the array-level core of OrbCalculator): a saved bundle round trip, one system
     against the oracle, and evaluate_batch == per-system evaluate (ZBL on, with a synthetic

@@ -249,3 +249,304 @@ def test_direct_denormalisers_known_values():
                                     torch.tensor(-1.0), torch.tensor(9.0))
     torch.testing.assert_close(s, torch.tensor([2.1, 4.1, 6.1, 2.0, 5.0, 8.0],
                                                dtype=torch.float64))
+
+
+# ----------------------------------------------------------------------------- known answers
+# Weights that reduce each module to a closed form, with the expected values computed by explicit
+# loops over the edge list from the reference's statement of the layer (orb_model.py:225-266,
+# 127-173, 92-112, 329-355, 381-435).  Every Linear is a scaled permutation-selection matrix in
+# torch [out, in] layout (F.linear(x, W)[i] = sum_j W[i, j] x[j] = scale[i] * x[off + perm[i]]),
+# non-symmetric so a transposed weight changes the answer; RMSNorm weights are non-uniform so a
+# weight applied before the normalisation changes it.
+_SILU = lambda v: v / (1.0 + math.exp(-v))
+_SIG = lambda v: 1.0 / (1.0 + math.exp(-v))
+
+
+def _sel(n_out, n_in, off, perm, scale):
+    W = torch.zeros(n_out, n_in, dtype=torch.float64)
+    for i in range(n_out):
+        W[i, off + perm[i]] = scale[i]
+    return W
+
+
+_P0, _P1, _P2 = [1, 2, 3, 0], [3, 0, 1, 2], [2, 3, 0, 1]
+_S0, _S1, _S2 = [1.0, -0.5, 2.0, 0.7], [1.3, 2.0, 0.5, -1.0], [0.8, -1.2, 1.5, 0.4]
+_B0, _B1, _B2 = [0.1, -0.2, 0.3, 0.0], [0.05, 0.0, -0.15, 0.2], [0.3, -0.1, 0.0, 0.25]
+_LN = [1.0, 2.0, 0.5, 3.0]
+
+
+def _mlpnorm_weights(w, prefix, n_in, off, ln):
+    w[f"{prefix}.mlp.NN-0.weight"] = _sel(4, n_in, off, _P0, _S0)
+    w[f"{prefix}.mlp.NN-0.bias"] = torch.tensor(_B0, dtype=torch.float64)
+    w[f"{prefix}.mlp.NN-1.weight"] = _sel(4, 4, 0, _P1, _S1)
+    w[f"{prefix}.mlp.NN-1.bias"] = torch.tensor(_B1, dtype=torch.float64)
+    w[f"{prefix}.mlp.NN-2.weight"] = _sel(4, 4, 0, _P2, _S2)
+    w[f"{prefix}.mlp.NN-2.bias"] = torch.tensor(_B2, dtype=torch.float64)
+    w[f"{prefix}.layer_norm.weight"] = torch.tensor(ln, dtype=torch.float64)
+
+
+def _mlpnorm_expected(v, ln):
+    """Linear-SiLU-Linear-SiLU-Linear then x * rsqrt(mean(x^2) + 1e-6) * w, for the selection
+    weights of _mlpnorm_weights, on one input block v (4 values)."""
+    h0 = [_SILU(_S0[i] * v[_P0[i]] + _B0[i]) for i in range(4)]
+    h1 = [_SILU(_S1[i] * h0[_P1[i]] + _B1[i]) for i in range(4)]
+    h2 = [_S2[i] * h1[_P2[i]] + _B2[i] for i in range(4)]
+    inv = 1.0 / math.sqrt(sum(t * t for t in h2) / 4 + 1e-6)
+    return [h2[i] * inv * ln[i] for i in range(4)]
+
+
+_SEND, _RECV = [0, 0, 0, 1, 2], [1, 2, 3, 3, 3]       # sender degrees 3,1,1,0; receiver 0,1,1,3
+_CUT = [1.0, 0.5, 0.25, 0.8, 0.6]
+_GR, _BR, _GS, _BS = 0.9, 0.3, -1.4, -1.1              # attention weight on channel 0 / 1, bias
+_LN_NODE = [0.5, 1.5, 2.5, -1.0]
+
+
+def _layer_case(edge_block, node_block, cond):
+    """One attention layer (C = hidden = 4) whose edge MLP reads only input block `edge_block`
+    of [e | n[send] | n[recv]] and whose node MLP reads only block `node_block` of
+    [n | recv_agg | sent_agg]; returns (oracle (nodes, edges), expected (nodes, edges))."""
+    N, E, C = 4, 5, 4
+    nodes = torch.tensor([[0.3 * i - 0.2 * j + 0.05 * i * j for j in range(C)] for i in range(N)],
+                         dtype=torch.float64)
+    edges = torch.tensor([[0.1 * (e + 1) * (-1) ** j + 0.07 * j for j in range(C)]
+                          for e in range(E)], dtype=torch.float64)
+    p = "gnn_stacks.0"
+    w = {}
+    _mlpnorm_weights(w, f"{p}._edge_mlp", 3 * C, edge_block * C, _LN)
+    _mlpnorm_weights(w, f"{p}._node_mlp", 3 * C, node_block * C, _LN_NODE)
+    w[f"{p}._receive_attn.weight"] = torch.tensor([[_GR, 0.0, 0.0, 0.0]], dtype=torch.float64)
+    w[f"{p}._receive_attn.bias"] = torch.tensor([_BR], dtype=torch.float64)
+    w[f"{p}._send_attn.weight"] = torch.tensor([[0.0, _GS, 0.0, 0.0]], dtype=torch.float64)
+    w[f"{p}._send_attn.bias"] = torch.tensor([_BS], dtype=torch.float64)
+    cond_nodes = None
+    n_eff = [list(map(float, r)) for r in nodes]
+    if cond:
+        cond_nodes = torch.tensor([[0.2 * i + 0.1 * j for j in range(6)] for i in range(N)],
+                                  dtype=torch.float64)
+        w[f"{p}._cond_node_proj.weight"] = _sel(C, 6, 2, [3, 0, 2, 1], [1.0, -2.0, 0.5, 1.5])
+        w[f"{p}._cond_node_proj.bias"] = torch.tensor([0.01, 0.02, -0.03, 0.04],
+                                                      dtype=torch.float64)
+        cp = [3, 0, 2, 1]
+        cs = [1.0, -2.0, 0.5, 1.5]
+        cb = [0.01, 0.02, -0.03, 0.04]
+        n_eff = [[n_eff[i][j] + cs[j] * float(cond_nodes[i, 2 + cp[j]]) + cb[j] for j in range(C)]
+                 for i in range(N)]
+    got = O.attention_layer(nodes, edges, torch.tensor(_SEND), torch.tensor(_RECV),
+                            torch.tensor(_CUT, dtype=torch.float64)[:, None], w, p, cond_nodes)
+    # expected, edge by edge
+    ue = []
+    for e in range(E):
+        block = [list(map(float, edges[e])), n_eff[_SEND[e]], n_eff[_RECV[e]]][edge_block]
+        ue.append(_mlpnorm_expected(block, _LN))
+    sent = [[0.0] * C for _ in range(N)]
+    recv = [[0.0] * C for _ in range(N)]
+    for e in range(E):
+        sa = _SIG(_GS * float(edges[e, 1]) + _BS) * _CUT[e]
+        ra = _SIG(_GR * float(edges[e, 0]) + _BR) * _CUT[e]
+        for j in range(C):
+            sent[_SEND[e]][j] += ue[e][j] * sa
+            recv[_RECV[e]][j] += ue[e][j] * ra
+    new_nodes = []
+    for i in range(N):
+        block = [n_eff[i], recv[i], sent[i]][node_block]
+        un = _mlpnorm_expected(block, _LN_NODE)
+        new_nodes.append([n_eff[i][j] + un[j] for j in range(C)])
+    new_edges = [[float(edges[e, j]) + ue[e][j] for j in range(C)] for e in range(E)]
+    return got, (torch.tensor(new_nodes, dtype=torch.float64),
+                 torch.tensor(new_edges, dtype=torch.float64))
+
+
+@pytest.mark.parametrize("cond", [False, True])
+@pytest.mark.parametrize("edge_block,node_block", [(j, k) for j in range(3) for k in range(3)])
+def test_attention_layer_known_answers(edge_block, node_block, cond):
+    """Edge MLP input [e | n[send] | n[recv]], attention gates sigmoid(e W + b) * cutoff from the
+    pre-update edges, sent_agg summed over each node's outgoing (sender) edges and recv_agg over
+    its incoming (receiver) edges, node MLP input [n | recv_agg | sent_agg], the conditioning
+    projection added to the nodes before everything else, residuals on both: against the closed
+    form for every choice of the block each MLP reads.  A swap of the two sums, of the blocks of
+    either concatenation, of the gate channels or a misplaced RMSNorm weight fails here (the
+    sender and receiver degrees of the graph all differ)."""
+    (nodes, edges), (ref_nodes, ref_edges) = _layer_case(edge_block, node_block, cond)
+    torch.testing.assert_close(edges, ref_edges, rtol=0, atol=1e-12)
+    torch.testing.assert_close(nodes, ref_nodes, rtol=0, atol=1e-12)
+
+
+def test_mlpnorm_rmsnorm_known_answer():
+    """MLPNorm on one row against hand-evaluated numbers (not only the closed-form helper): the
+    RMSNorm eps is 1e-6 inside the square root and the weight multiplies after normalising."""
+    w = {}
+    _mlpnorm_weights(w, "m", 4, 0, _LN)
+    x = torch.tensor([[0.4, -0.3, 1.2, 0.05]], dtype=torch.float64)
+    got = O.mlp_norm(x, w, "m")[0]
+    h0 = [_SILU(1.0 * -0.3 + 0.1), _SILU(-0.5 * 1.2 - 0.2), _SILU(2.0 * 0.05 + 0.3),
+          _SILU(0.7 * 0.4 + 0.0)]
+    h1 = [_SILU(1.3 * h0[3] + 0.05), _SILU(2.0 * h0[0]), _SILU(0.5 * h0[1] - 0.15),
+          _SILU(-1.0 * h0[2] + 0.2)]
+    h2 = [0.8 * h1[2] + 0.3, -1.2 * h1[3] - 0.1, 1.5 * h1[0], 0.4 * h1[1] + 0.25]
+    rms = math.sqrt((h2[0] ** 2 + h2[1] ** 2 + h2[2] ** 2 + h2[3] ** 2) / 4 + 1e-6)
+    ref = torch.tensor([h2[0] / rms * 1.0, h2[1] / rms * 2.0, h2[2] / rms * 0.5,
+                        h2[3] / rms * 3.0], dtype=torch.float64)
+    torch.testing.assert_close(got, ref, rtol=0, atol=1e-14)
+
+
+def _head_weights(name, n_out, scale_out, bias_out):
+    w = {f"{name}.mlp.NN-0.weight": _sel(3, 4, 0, [2, 0, 3], [1.5, -0.8, 0.6]),
+         f"{name}.mlp.NN-0.bias": torch.tensor([0.1, -0.2, 0.05], dtype=torch.float64),
+         f"{name}.mlp.NN-1.weight": torch.tensor(scale_out, dtype=torch.float64).reshape(n_out, 3),
+         f"{name}.mlp.NN-1.bias": torch.tensor(bias_out, dtype=torch.float64)}
+    return w
+
+
+_HEAD_NODES = torch.tensor([[0.5, -1.0, 0.25, 2.0], [1.5, 0.0, -0.75, 1.0],
+                            [-0.2, 0.4, 1.1, -0.6], [0.9, 0.3, -1.3, 0.2],
+                            [0.0, 1.2, 0.8, -0.4]], dtype=torch.float64)
+_HEAD_BATCH, _HEAD_NATOMS = torch.tensor([0, 0, 1, 1, 1]), [2, 3]
+
+
+def _head_hidden(row):
+    return [_SILU(1.5 * row[2] + 0.1), _SILU(-0.8 * row[0] - 0.2), _SILU(0.6 * row[3] + 0.05)]
+
+
+def _sys_means():
+    out = []
+    off = 0
+    for n in _HEAD_NATOMS:
+        out.append([sum(float(_HEAD_NODES[off + a, j]) for a in range(n)) / n for j in range(4)])
+        off += n
+    return out
+
+
+def test_energy_head_known_answer_per_system():
+    """EnergyHead(.batch): mean of each system's own node features, then Linear-SiLU-Linear
+    (orb_model.py:329-355); a batch-wide mean would give both systems one value."""
+    wo = [0.7, -1.3, 0.4]
+    w = _head_weights("energy_head", 1, wo, [0.2])
+    got = O.energy_head(_HEAD_NODES, _HEAD_BATCH, _HEAD_NATOMS, w)
+    ref = [sum(wo[i] * h for i, h in enumerate(_head_hidden(m))) + 0.2 for m in _sys_means()]
+    torch.testing.assert_close(got, torch.tensor(ref, dtype=torch.float64), rtol=0, atol=1e-14)
+    assert abs(ref[0] - ref[1]) > 0.1
+
+
+def test_force_and_stress_heads_known_answers_per_system():
+    """ForceHead.batch: per-node Linear-SiLU-Linear, minus the mean prediction of the node's own
+    system (orb_model.py:381-404); StressHead: per-system node mean, then Linear-SiLU-Linear to
+    six Voigt components (orb_model.py:429-435)."""
+    wf = [1.0, 0.5, -0.3, -0.7, 0.2, 1.1, 0.4, -1.5, 0.9]
+    w = _head_weights("forces_head", 3, wf, [0.3, -0.1, 0.2])
+    got = O.force_head(_HEAD_NODES, _HEAD_BATCH, _HEAD_NATOMS, w)
+    pred = []
+    for a in range(5):
+        h = _head_hidden([float(v) for v in _HEAD_NODES[a]])
+        pred.append([sum(wf[3 * c + i] * h[i] for i in range(3)) + [0.3, -0.1, 0.2][c]
+                     for c in range(3)])
+    ref, off = [], 0
+    for n in _HEAD_NATOMS:
+        mean = [sum(pred[off + a][c] for a in range(n)) / n for c in range(3)]
+        ref += [[pred[off + a][c] - mean[c] for c in range(3)] for a in range(n)]
+        off += n
+    torch.testing.assert_close(got, torch.tensor(ref, dtype=torch.float64), rtol=0, atol=1e-14)
+    ws = [0.1 * (k + 1) * (-1) ** k for k in range(18)]
+    bs = [0.01 * k for k in range(6)]
+    w = _head_weights("stress_head", 6, ws, bs)
+    got = O.stress_head(_HEAD_NODES, _HEAD_BATCH, _HEAD_NATOMS, w)
+    ref = []
+    for m in _sys_means():
+        h = _head_hidden(m)
+        ref.append([sum(ws[3 * c + i] * h[i] for i in range(3)) + bs[c] for c in range(6)])
+    torch.testing.assert_close(got, torch.tensor(ref, dtype=torch.float64), rtol=0, atol=1e-14)
+
+
+def test_backbone_composition_known_answer():
+    """Encoder then layers then the energy head (orb_model.py:176-186, gns stacks in order): a
+    two-layer stack whose first layer's MLPs read blocks (n[send], recv_agg) and second (e,
+    sent_agg), composed by hand from the layer closed form, with the encoder MLPs on the atom
+    embedding and the edge features."""
+    C = 4
+    Z = torch.tensor([1, 6, 8, 6])
+    emb = torch.tensor([[0.1 * z - 0.05 * j for j in range(C)] for z in range(10)],
+                       dtype=torch.float64)
+    feat = torch.tensor([[0.2 * e - 0.1 * j + 0.03 * e * j for j in range(C)] for e in range(5)],
+                        dtype=torch.float64)
+    w = {"atom_emb.embeddings.weight": emb}
+    _mlpnorm_weights(w, "_encoder._node_fn", C, 0, [1.0, 0.5, 2.0, 1.5])
+    _mlpnorm_weights(w, "_encoder._edge_fn", C, 0, [0.7, 1.0, 1.3, 0.9])
+    for li, (eb, nb) in enumerate(((1, 1), (0, 2))):
+        p = f"gnn_stacks.{li}"
+        _mlpnorm_weights(w, f"{p}._edge_mlp", 3 * C, eb * C, _LN)
+        _mlpnorm_weights(w, f"{p}._node_mlp", 3 * C, nb * C, _LN_NODE)
+        w[f"{p}._receive_attn.weight"] = torch.tensor([[_GR, 0, 0, 0]], dtype=torch.float64)
+        w[f"{p}._receive_attn.bias"] = torch.tensor([_BR], dtype=torch.float64)
+        w[f"{p}._send_attn.weight"] = torch.tensor([[0, _GS, 0, 0]], dtype=torch.float64)
+        w[f"{p}._send_attn.bias"] = torch.tensor([_BS], dtype=torch.float64)
+    w.update(_head_weights("energy_head", 1, [0.7, -1.3, 0.4], [0.2]))
+    cfg = {"num_message_passing_steps": 2}
+    cut = torch.tensor(_CUT, dtype=torch.float64)[:, None]
+    s, r = torch.tensor(_SEND), torch.tensor(_RECV)
+    got = O.backbone(w, cfg, Z, feat, cut, s, r, torch.zeros(4, dtype=torch.long), [4])
+    # by hand: encoder rows, then the two layers through the layer closed form of the test above
+    nodes = [_mlpnorm_expected([float(v) for v in emb[z]], [1.0, 0.5, 2.0, 1.5]) for z in Z]
+    edges = [_mlpnorm_expected([float(v) for v in feat[e]], [0.7, 1.0, 1.3, 0.9])
+             for e in range(5)]
+    for eb, nb in ((1, 1), (0, 2)):
+        ue = [_mlpnorm_expected([edges[e], nodes[_SEND[e]], nodes[_RECV[e]]][eb], _LN)
+              for e in range(5)]
+        sent = [[0.0] * C for _ in range(4)]
+        recv = [[0.0] * C for _ in range(4)]
+        for e in range(5):
+            sa = _SIG(_GS * edges[e][1] + _BS) * _CUT[e]
+            ra = _SIG(_GR * edges[e][0] + _BR) * _CUT[e]
+            for j in range(C):
+                sent[_SEND[e]][j] += ue[e][j] * sa
+                recv[_RECV[e]][j] += ue[e][j] * ra
+        un = [_mlpnorm_expected([nodes[i], recv[i], sent[i]][nb], _LN_NODE) for i in range(4)]
+        nodes = [[nodes[i][j] + un[i][j] for j in range(C)] for i in range(4)]
+        edges = [[edges[e][j] + ue[e][j] for j in range(C)] for e in range(5)]
+    mean = [sum(nodes[i][j] for i in range(4)) / 4 for j in range(C)]
+    ref = sum(c * h for c, h in zip([0.7, -1.3, 0.4], _head_hidden(mean))) + 0.2
+    assert abs(float(got[0]) - ref) < 1e-12, (float(got[0]), ref)
+
+
+def test_known_answer_tests_catch_planted_wiring_mistakes(monkeypatch):
+    """The layer closed form above is sensitive to each plausible wiring mistake: planted into a
+    copy of the oracle's layer, each one fails the known-answer comparison."""
+    import torch.nn.functional as F
+
+    def layer(mistake):
+        def f(nodes, edges, senders, receivers, cut, w, prefix, cond_nodes=None):
+            N = nodes.shape[0]
+            if cond_nodes is not None and f"{prefix}._cond_node_proj.weight" in w:
+                nodes = nodes + O._lin(cond_nodes, w, f"{prefix}._cond_node_proj")
+            ra = torch.sigmoid(O._lin(edges, w, f"{prefix}._receive_attn")) * cut
+            sa = torch.sigmoid(O._lin(edges, w, f"{prefix}._send_attn")) * cut
+            if mistake == "gates":
+                ra, sa = sa, ra
+            cat = [edges, nodes[senders], nodes[receivers]]
+            if mistake == "edge_order":
+                cat = [edges, nodes[receivers], nodes[senders]]
+            ue = O.mlp_norm(torch.cat(cat, dim=1), w, f"{prefix}._edge_mlp")
+            if mistake == "norm_weight":
+                h = torch.cat(cat, dim=1)
+                for i in range(2):
+                    h = F.silu(O._lin(h, w, f"{prefix}._edge_mlp.mlp.NN-{i}"))
+                h = O._lin(h, w, f"{prefix}._edge_mlp.mlp.NN-2")
+                ue = O.rmsnorm(h * w[f"{prefix}._edge_mlp.layer_norm.weight"],
+                               torch.ones_like(w[f"{prefix}._edge_mlp.layer_norm.weight"]))
+            C = ue.shape[1]
+            si, ri = (receivers, senders) if mistake == "sums" else (senders, receivers)
+            sent = torch.zeros(N, C, dtype=ue.dtype).index_add_(0, si, ue * sa)
+            recv = torch.zeros(N, C, dtype=ue.dtype).index_add_(0, ri, ue * ra)
+            node_cat = [nodes, sent, recv] if mistake == "node_order" else [nodes, recv, sent]
+            un = O.mlp_norm(torch.cat(node_cat, dim=1), w, f"{prefix}._node_mlp")
+            return nodes + un, edges + ue
+        return f
+
+    for mistake in ("gates", "edge_order", "norm_weight", "sums", "node_order"):
+        monkeypatch.setattr(O, "attention_layer", layer(mistake))
+        caught = False
+        for j in range(3):
+            for k in range(3):
+                (nodes, edges), (rn, re_) = _layer_case(j, k, False)
+                if not (torch.allclose(nodes, rn, rtol=0, atol=1e-12)
+                        and torch.allclose(edges, re_, rtol=0, atol=1e-12)):
+                    caught = True
+        assert caught, mistake

@@ -23,8 +23,9 @@ Also reported on the same JSON line:
                 under ``gemm_families``; ``hbm_kernels`` gives the same for the HBM-bound edge
                 kernels (rotation, segment sums) against the 8 TB/s HBM peak.
   cpu_baseline  the CPU oracle (PyTorch-CPU restatement of the reference path) on a bounded sample
-                of the same workload: the C3 model on a 512-atom cluster of the same density
-                (one step after a small warm-up), in atom-steps/s.
+                of the same workload: the full 2048-atom C3 step (a 512-atom cluster of the same
+                density on a slow host), one warm-up step then the median of 3, in atom-steps/s,
+                with the CPU model, core counts and threads in ``sample``.
 """
 from __future__ import annotations
 
@@ -128,11 +129,59 @@ def build_c2(torch, N=8192):
     return ei, vec, x, g, synthetic.c2_weights(), synthetic.jd_matrices()
 
 
+def _cpu_info():
+    """CPU model, physical cores and logical CPUs of this host (from /proc/cpuinfo)."""
+    model, phys, logical = "unknown", set(), 0
+    try:
+        cur = {}
+        for line in open("/proc/cpuinfo"):
+            if ":" not in line:
+                if cur:
+                    phys.add((cur.get("physical id"), cur.get("core id")))
+                cur = {}
+                continue
+            k, v = (t.strip() for t in line.split(":", 1))
+            cur[k] = v
+            if k == "processor":
+                logical += 1
+            elif k == "model name" and model == "unknown":
+                model = v
+        if cur:
+            phys.add((cur.get("physical id"), cur.get("core id")))
+    except OSError:
+        pass
+    return model, len(phys) if phys and None not in next(iter(phys)) else None, logical
+
+
+def _median_of_3(run):
+    """One untimed warm-up call at the measured size, then the median of three timed calls (the
+    CPU-baseline procedure of the reference's CPU-vs-device comparison)."""
+    run()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[1], ts
+
+
+def _cpu_threads(torch):
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    return threads
+
+
+def _cpu_sample_note(what, dt, ts, threads):
+    model, phys, logical = _cpu_info()
+    return (f"{what}; one warm-up step, then the median of 3 steps ({', '.join(f'{t:.2f}' for t in ts)}"
+            f" s -> {dt:.2f} s); {threads} threads on {model} ({phys} physical cores, {logical} "
+            f"logical CPUs visible)")
+
+
 def cpu_baseline_c2(torch):
     """Oracle on a bounded sample of C2: the same pipeline on N = 2048 nodes (E = 51,200)."""
     from oracle import uma as U
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    torch.set_num_threads(threads)
+    threads = _cpu_threads(torch)
     ei, vec, x, g, w, jd = build_c2(torch, N=2048)
 
     def run():
@@ -140,14 +189,11 @@ def cpu_baseline_c2(torch):
         out = U.isolated_edgewise(torch.from_numpy(x), ev, torch.from_numpy(ei[0]),
                                   torch.from_numpy(ei[1]), w, "c2", jd, 2048)
         torch.autograd.grad((out * torch.from_numpy(g)).sum(), ev)
-    run()
-    t0 = time.perf_counter()
-    run()
-    dt = time.perf_counter() - t0
+    dt, ts = _median_of_3(run)
     E = int(ei.shape[1])
     return {"value": round(E / dt, 1), "unit": "edge-steps/s", "cores": threads, "kind": "port",
-            "sample": (f"CPU oracle (torch-CPU fp32) of the C2 pipeline on N=2048 nodes "
-                       f"(E={E}), 1 step after a warm-up step, {dt:.2f} s; {threads} threads")}
+            "sample": _cpu_sample_note(f"CPU oracle (torch-CPU fp32) of the C2 pipeline on "
+                                       f"N=2048 nodes (E={E})", dt, ts, threads)}
 
 
 def build_c3(torch, n_atoms=2048, seed=None):
@@ -330,52 +376,42 @@ def device_nl_ms(torch, fn, ref):
 def cpu_baseline_c5(torch):
     """Orb CPU oracle on a bounded sample of C5: the first 32 molecules of the batch."""
     from oracle import orb as O
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    torch.set_num_threads(threads)
+    threads = _cpu_threads(torch)
     cfg, w, bg, _ = build_c5(torch, K=32)
     args = (w, cfg, bg.pos, bg.Z, bg.senders, bg.receivers, bg.cell_shift, bg.batch, bg.natoms)
-    O.energy_and_forces(*args)                                   # warm-up
-    t0 = time.perf_counter()
-    O.energy_and_forces(*args)
-    dt = time.perf_counter() - t0
+    dt, ts = _median_of_3(lambda: O.energy_and_forces(*args))
     n = int(bg.pos.shape[0])
     return {"value": round(n / dt, 3), "unit": "atom-steps/s", "cores": threads, "kind": "port",
-            "sample": (f"Orb CPU oracle (torch-CPU fp32), first 32 C5 molecules ({n} atoms, "
-                       f"E={int(bg.senders.numel())}), 1 step after a warm-up step, {dt:.1f} s; "
-                       f"{threads} threads")}
+            "sample": _cpu_sample_note(f"Orb CPU oracle (torch-CPU fp32), first 32 C5 molecules "
+                                       f"({n} atoms, E={int(bg.senders.numel())})", dt, ts,
+                                       threads)}
 
 
 def cpu_baseline(torch):
-    """CPU oracle on a bounded sample of the C3 workload."""
+    """CPU oracle on a bounded sample of the C3 workload: the full 2048-atom step when the host
+    runs it in under 12 s (the warm-up step measures that), else a 512-atom cluster of the same
+    density, so that the four steps stay within about half a minute."""
     from oracle import forces as OF
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    torch.set_num_threads(threads)
-    cfg, w, host, pos, Z, ei, se, _ = build_c3(torch, n_atoms=64, seed=301)
-    m = OF.Model(w, cfg, host)
-    OF.energy_and_forces(m, pos, Z, ei, se)                       # warm-up (threads, allocator)
-    # one step of a 512-atom same-density cluster; on a host fast enough for that to take under
-    # 3 s, one step of the full 2048-atom workload instead (the bounded sample stays ~10-30 s)
-    for n_atoms in (512, 2048):
+    threads = _cpu_threads(torch)
+    for n_atoms in (2048, 512):
         cfg, w, host, pos, Z, ei, se, _ = build_c3(torch, n_atoms=n_atoms)
         m = OF.Model(w, cfg, host)
+        run = lambda: OF.energy_and_forces(m, pos, Z, ei, se)
         t0 = time.perf_counter()
-        OF.energy_and_forces(m, pos, Z, ei, se)
-        dt = time.perf_counter() - t0
-        if dt > 3.0:
+        run()                                                # warm-up at the measured size
+        if time.perf_counter() - t0 < 12.0 or n_atoms == 512:
             break
-    model = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    dt = sorted(ts)[1]
     return {"value": round(len(Z) / dt, 3), "unit": "atom-steps/s", "cores": threads,
             "kind": "port",
-            "sample": (f"CPU oracle (torch-CPU restatement of the reference path), C3 model on a "
-                       f"{len(Z)}-atom same-density cluster (E={ei.shape[1]}), 1 step after a "
-                       f"64-atom warm-up, {dt:.1f} s; {threads} threads on {model}")}
+            "sample": _cpu_sample_note(f"CPU oracle (torch-CPU restatement of the reference "
+                                       f"path), C3 model on a {len(Z)}-atom same-density cluster "
+                                       f"(E={ei.shape[1]})", dt, ts, threads)}
 
 
 def read_traffic():

@@ -14,6 +14,9 @@ follows.  Parity pins (see tests/test_oracle_*.py):
 * Wigner blocks: orthogonality, the fixture's ``Jd`` / ``to_m``, closed-form l=1 rotation;
 * neighbour list: brute-force triple loop on tiny inputs with the same fp32 comparisons;
 * forces / stress: fp64 finite differences and rotation/translation invariance;
-* Orb: closed-form-vs-autograd geometry VJP, finite differences ("parity unpinned" against
-  orb-models itself -- no committed Orb vector exists in the reference).
+* system embedding: the goldens' ``host@sys_node_embedding`` and known rand_emb / pos_emb rows;
+* spectral feed-forward: constant-gate closed form and loop known answers (planted mistakes fail);
+* Orb: reference-written geometry vectors, closed-form-vs-autograd geometry VJP, finite
+  differences, and known answers of every layer and head from selection-matrix weights (no
+  committed Orb vector of a full model exists in the reference).
 """

@@ -16,10 +16,16 @@ Pins (tests/test_oracle_orb.py):
     dense one-hot products.
   * direct heads: per-system net force exactly zero, atom-permutation equivariance of the forces
     and invariance of the stress head, batch == per-system, the normaliser split of the six
-    stress components on known values.
-The MLP/attention/head arithmetic has no upstream vector (every Orb golden of the reference is
-gated and uncommitted): against orb-models itself this part is "parity unpinned"; it is pinned by
-the invariants above only.
+    stress components on known values;
+  * known answers (tests/test_oracle_orb.py, "known answers" section): selection-matrix weights
+    reduce MLPNorm, the attention layer (for every choice of the concatenation block each MLP
+    reads, with and without conditioning), the energy / force / stress heads and a two-layer
+    encoder + layers + head composition to closed forms evaluated by explicit loops over the
+    edge list; planted wiring mistakes (swapped sender / receiver sums, concatenation orders,
+    gate channels, a misplaced RMSNorm weight, batch-wide head means) fail them;
+  * denormalisers and the charge / spin conditioning against hand-evaluated values.
+No Orb golden vector of the reference is committed (they are gated), so the composition is pinned
+by the reference's statement of each layer through those known answers and by the invariants.
 """
 from __future__ import annotations
 

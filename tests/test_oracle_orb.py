@@ -550,3 +550,46 @@ def test_known_answer_tests_catch_planted_wiring_mistakes(monkeypatch):
                         and torch.allclose(edges, re_, rtol=0, atol=1e-12)):
                     caught = True
         assert caught, mistake
+
+
+def test_conservative_denormalisers_and_conditioning_known_values():
+    """EnergyHead.denormalize: (raw sigma + mu) n + sum ref[Z] (orb_model.py:588-600); the
+    conservative force and stress scales sigma n (and / |det cell|) with the Voigt order
+    [xx, yy, zz, yz, xz, xy] (orb_model.py:459-488); the sin/cos charge / spin conditioning with
+    the spin part zeroed at spin 0 (orb_model.py:32-56).  Oracle and package host functions
+    against hand-evaluated numbers."""
+    from tt_atom import orb as P
+    ref_w = torch.zeros(119, dtype=torch.float64)
+    ref_w[1], ref_w[6], ref_w[8] = -0.5, -3.0, -4.25
+    Z = torch.tensor([6, 1, 1, 8])
+    e = O.denormalize_energy(torch.tensor(0.5), Z, 4, torch.tensor(1.0), torch.tensor(4.0), ref_w)
+    assert abs(float(e) - ((0.5 * 2 + 1) * 4 - 3.0 - 0.5 - 0.5 - 4.25)) < 1e-12
+    w = {"energy_head.normalizer.bn.running_var": torch.tensor(4.0),
+         "energy_head.normalizer.bn.running_mean": torch.tensor(1.0),
+         "energy_head.reference.linear.weight": ref_w[None]}
+    assert abs(float(P.denormalize_energy(0.5, Z, 4, w)) - float(e)) < 1e-12
+    eb = P.denormalize_energy_batch(torch.tensor([0.5, -1.0]), torch.tensor([6, 1, 1, 8, 8]),
+                                    torch.tensor([0, 0, 0, 0, 1]), [4, 1], w)
+    torch.testing.assert_close(eb, torch.tensor([float(e), (-1.0 * 2 + 1) * 1 - 4.25],
+                                                dtype=torch.float64), rtol=0, atol=1e-12)
+    f = O.denormalize_forces(torch.tensor([[1.0, -2.0, 0.25]]), 4, torch.tensor(4.0))
+    torch.testing.assert_close(f, torch.tensor([[8.0, -16.0, 2.0]], dtype=torch.float64))
+    torch.testing.assert_close(P.denormalize_forces(torch.tensor([[1.0, -2.0, 0.25]]), 4, w), f)
+    vir = torch.tensor([[1.0, 2.0, 3.0], [4.0, 5.0, 6.0], [7.0, 8.0, 9.0]])
+    cell = torch.diag(torch.tensor([2.0, 2.0, 4.0]))                  # volume 16
+    s = P.denormalize_stress(vir, 4, cell, w)                         # scale sigma n / V = 0.5
+    torch.testing.assert_close(s, torch.tensor([0.5, 2.5, 4.5, 3.5, 2.5, 1.5],
+                                               dtype=torch.float64))
+    wc = {"conditioner.charge_embedding.W": torch.tensor([0.25, -0.1], dtype=torch.float64),
+          "conditioner.spin_embedding.W": torch.tensor([0.5, 0.125], dtype=torch.float64)}
+    c = O.charge_spin_embedding(wc, 1.0, 0.0, 2)
+    tp = 2 * math.pi
+    ref = [math.sin(tp * 0.25), math.sin(-tp * 0.1), math.cos(tp * 0.25), math.cos(-tp * 0.1),
+           0.0, 0.0, 0.0, 0.0]
+    torch.testing.assert_close(c, torch.tensor([ref, ref], dtype=torch.float64), rtol=0,
+                               atol=1e-15)
+    c = O.charge_spin_embedding(wc, -2.0, 3.0, 1)
+    ref = [math.sin(-2 * tp * 0.25), math.sin(2 * tp * 0.1), math.cos(-2 * tp * 0.25),
+           math.cos(2 * tp * 0.1), math.sin(3 * tp * 0.5), math.sin(3 * tp * 0.125),
+           math.cos(3 * tp * 0.5), math.cos(3 * tp * 0.125)]
+    torch.testing.assert_close(c, torch.tensor([ref], dtype=torch.float64), rtol=0, atol=1e-14)

@@ -266,3 +266,236 @@ def test_rotation_invariance(golden):
     # equivariant only to fp32 resolution even when evaluated in fp64
     assert abs(E1 - E0) < 1e-6 * max(1.0, abs(E0))
     assert (F1 - F0 @ q.T).abs().max() < 1e-5
+
+
+# ------------------------------------------------------------------ system embedding known answers
+# (geometry.py:23-45)
+@pytest.mark.parametrize("fixture", ["golden", "golden_bulk"])
+def test_csd_embedding_vs_golden(fixture, request):
+    """The system embedding of the committed fairchem goldens (pos_emb encoding, charge 0, spin
+    0, dataset omat): the oracle and the package's host function both reproduce
+    host@sys_node_embedding (one row per node, all equal)."""
+    from tt_atom import geometry as TG
+    g = request.getfixturevalue(fixture)
+    w, ref = g.w(), g.host("sys_node_embedding")
+    chg, spin = g.inp("charge").float(), g.inp("spin").float()
+    for fn in (G.csd_embedding, lambda *a, **k: TG.csd_embedding(*a, **k)):
+        got = fn(w, chg, spin, dataset="omat")
+        assert got.shape == (1, ref.shape[1])
+        assert (got.expand_as(ref) - ref).abs().max() < 1e-6
+
+
+def _csd_select_weights(C):
+    """mix_csd = a scaled selection [4, 12] (C = 4) reading input columns 1, 6, 11 and 2 of
+    [charge | spin | dataset]: the second charge component, the third spin component, the last
+    dataset component and the third charge component, scaled by 1 + i/8."""
+    assert C == 4
+    cols = [1, 6, 11, 2]
+    W = torch.zeros(C, 3 * C, dtype=torch.float64)
+    for i, c in enumerate(cols):
+        W[i, c] = 1.0 + i / 8
+    return W, cols
+
+
+def _silu(v):
+    return v / (1.0 + math.exp(-v))
+
+
+@pytest.mark.parametrize("impl", ["oracle", "package"])
+def test_csd_embedding_rand_emb_known_rows(impl):
+    """rand_emb (uma-s-1): charge c reads row c + 100 of the charge table and spin s row s of the
+    spin table, concatenated with the dataset token before mix_csd and SiLU.  Tables whose rows
+    encode their own index make a wrong offset or a swapped table visible."""
+    from tt_atom import geometry as TG
+    fn = G.csd_embedding if impl == "oracle" else TG.csd_embedding
+    C = 4
+    rows = (torch.arange(201, dtype=torch.float64)[:, None] * 0.01
+            + torch.arange(C, dtype=torch.float64) * 0.001)
+    w = {"charge_embedding.rand_emb.weight": rows,
+         "spin_embedding.rand_emb.weight": -rows[:101] - 0.5,
+         "dataset_embedding.dataset_emb_dict.omol.weight":
+             torch.tensor([[0.3, -0.2, 0.1, 0.05]], dtype=torch.float64),
+         "mix_csd.bias": torch.tensor([0.01, -0.02, 0.03, 0.0], dtype=torch.float64)}
+    w["mix_csd.weight"], cols = _csd_select_weights(C)
+    charge, spin = torch.tensor([-2.0, 0.0, 3.0]), torch.tensor([1.0, 0.0, 5.0])
+    got = fn(w, charge, spin, dataset="omol")
+    for s in range(3):
+        inp = ([0.01 * (charge[s].item() + 100) + 0.001 * j for j in range(C)]
+               + [-(0.01 * spin[s].item() + 0.001 * j) - 0.5 for j in range(C)]
+               + [0.3, -0.2, 0.1, 0.05])
+        ref = [_silu((1.0 + i / 8) * inp[cols[i]] + [0.01, -0.02, 0.03, 0.0][i]) for i in range(C)]
+        assert max(abs(float(got[s, i]) - ref[i]) for i in range(C)) < 1e-12, (s, got[s], ref)
+
+
+@pytest.mark.parametrize("impl", ["oracle", "package"])
+def test_csd_embedding_pos_emb_known_values(impl):
+    """pos_emb: x -> [sin(2 pi x W) | cos(2 pi x W)] per charge and spin, the spin part zeroed
+    where spin == 0 (the charge part never), against hand-evaluated sines and cosines."""
+    from tt_atom import geometry as TG
+    fn = G.csd_embedding if impl == "oracle" else TG.csd_embedding
+    C = 4
+    Wc, Ws = [0.13, -0.4], [0.7, 0.25]
+    w = {"charge_embedding.W": torch.tensor(Wc, dtype=torch.float64),
+         "spin_embedding.W": torch.tensor(Ws, dtype=torch.float64),
+         "dataset_embedding.dataset_emb_dict.omat.weight":
+             torch.tensor([[0.5, 0.25, -0.75, 1.0]], dtype=torch.float64),
+         "mix_csd.bias": torch.zeros(C, dtype=torch.float64)}
+    w["mix_csd.weight"], cols = _csd_select_weights(C)
+    charge, spin = torch.tensor([1.0, 0.0, -1.0]), torch.tensor([0.0, 2.0, 1.0])
+    got = fn(w, charge.double(), spin.double(), dataset="omat")
+    tp = 2 * math.pi
+    for s in range(3):
+        q, sp = charge[s].item(), spin[s].item()
+        enc_q = [math.sin(tp * q * Wc[0]), math.sin(tp * q * Wc[1]),
+                 math.cos(tp * q * Wc[0]), math.cos(tp * q * Wc[1])]
+        enc_s = [math.sin(tp * sp * Ws[0]), math.sin(tp * sp * Ws[1]),
+                 math.cos(tp * sp * Ws[0]), math.cos(tp * sp * Ws[1])] if sp != 0 else [0.0] * 4
+        inp = enc_q + enc_s + [0.5, 0.25, -0.75, 1.0]
+        ref = [_silu((1.0 + i / 8) * inp[cols[i]]) for i in range(C)]
+        assert max(abs(float(got[s, i]) - ref[i]) for i in range(C)) < 1e-12, (s, got[s], ref)
+    # the selection reaches both halves of both encodings and the dataset token
+    assert {c // C for c in cols} == {0, 1, 2}
+
+
+# ------------------------------------------------------------------ spectral FF known answers
+# (spectral.py:146-188: gating = SiLU(scalar_mlp(x0)); h = SO3_Linear_1(x) with one [out, in]
+# weight per degree and the bias on l = 0; SiLU on h0, sigmoid(gating[(l-1)H:lH]) on degree l;
+# SO3_Linear_2)
+def _spectral_weights(C, H, lmax, scalar_w, scalar_b):
+    p = "ff"
+    w = {f"{p}.scalar_mlp.0.weight": scalar_w, f"{p}.scalar_mlp.0.bias": scalar_b}
+    # SO3 linears: degree l uses a non-symmetric selection [out, in] scaled by (l + 1)
+    for name, (o, i) in (("so3_linear_1", (H, C)), ("so3_linear_2", (C, H))):
+        Wt = torch.zeros(lmax + 1, o, i, dtype=torch.float64)
+        for l in range(lmax + 1):
+            for r in range(o):
+                Wt[l, r, (r + l + 1) % i] = (l + 1) * (1.0 if name.endswith("1") else 0.5)
+        w[f"{p}.{name}.weight"] = Wt
+        w[f"{p}.{name}.bias"] = torch.tensor([0.1 * (r + 1) * (-1) ** r for r in range(o)],
+                                             dtype=torch.float64)
+    return w
+
+
+def _spectral_expected(x, w, C, H, lmax):
+    """Explicit loops over nodes, coefficients and channels from the reference's statement."""
+    p = "ff"
+    deg = [l for l in range(lmax + 1) for _ in range(2 * l + 1)]
+    Ws, bs = w[f"{p}.scalar_mlp.0.weight"], w[f"{p}.scalar_mlp.0.bias"]
+    out = torch.zeros_like(x)
+    for n in range(x.shape[0]):
+        a = [sum(float(Ws[r, i]) * float(x[n, 0, i]) for i in range(C)) + float(bs[r])
+             for r in range(lmax * H)]
+        gating = [_silu(v) for v in a]
+        for c, l in enumerate(deg):
+            W1, b1 = w[f"{p}.so3_linear_1.weight"][l], w[f"{p}.so3_linear_1.bias"]
+            h = [sum(float(W1[r, i]) * float(x[n, c, i]) for i in range(C))
+                 + (float(b1[r]) if c == 0 else 0.0) for r in range(H)]
+            if c == 0:
+                g = [_silu(v) for v in h]
+            else:
+                g = [h[r] / (1.0 + math.exp(-gating[(l - 1) * H + r])) for r in range(H)]
+            W2, b2 = w[f"{p}.so3_linear_2.weight"][l], w[f"{p}.so3_linear_2.bias"]
+            for r in range(C):
+                out[n, c, r] = (sum(float(W2[r, i]) * g[i] for i in range(H))
+                                + (float(b2[r]) if c == 0 else 0.0))
+    return out
+
+
+def test_spectral_ff_gate_known_constants():
+    """Zero scalar-MLP weight with a known bias makes every gate a constant: degree 1 is scaled
+    by sigmoid(SiLU(0)) = 1/2 and degree 2 by sigmoid(SiLU(2)) = 0.85341..., l = 0 goes through
+    SiLU; with the identity-like SO3 linears below the output is known in closed form."""
+    C = H = 3
+    lmax = 2
+    w = {"ff.scalar_mlp.0.weight": torch.zeros(lmax * H, C, dtype=torch.float64),
+         "ff.scalar_mlp.0.bias": torch.tensor([0.0] * H + [2.0] * H, dtype=torch.float64)}
+    for name in ("so3_linear_1", "so3_linear_2"):
+        w[f"ff.{name}.weight"] = torch.eye(C, dtype=torch.float64).expand(lmax + 1, C, C).clone()
+        w[f"ff.{name}.bias"] = torch.zeros(C, dtype=torch.float64)
+    x = torch.linspace(-1.5, 2.0, 2 * 9 * C, dtype=torch.float64).reshape(2, 9, C)
+    got = uma.spectral_atomwise(x, w, "ff", lmax, H)
+    g2 = 1.0 / (1.0 + math.exp(-_silu(2.0)))
+    assert abs(g2 - 0.8534092045709026) < 1e-12
+    ref = x.clone()
+    ref[:, 0, :] = x[:, 0, :] * torch.sigmoid(x[:, 0, :])
+    ref[:, 1:4, :] = 0.5 * x[:, 1:4, :]
+    ref[:, 4:9, :] = g2 * x[:, 4:9, :]
+    assert (got - ref).abs().max() < 1e-14
+
+
+def _spectral_case():
+    C, H, lmax = 3, 4, 2
+    gen = torch.Generator().manual_seed(5)
+    Ws = torch.randn(lmax * H, C, generator=gen, dtype=torch.float64)
+    bs = torch.randn(lmax * H, generator=gen, dtype=torch.float64)
+    w = _spectral_weights(C, H, lmax, Ws, bs)
+    x = torch.randn(3, 9, C, generator=gen, dtype=torch.float64)
+    return x, w, C, H, lmax
+
+
+def test_spectral_ff_known_answer_loops():
+    """Random scalar MLP, per-degree selection SO3 linears with distinct scales and biases: the
+    oracle equals the loop evaluation of the reference's statement."""
+    x, w, C, H, lmax = _spectral_case()
+    got = uma.spectral_atomwise(x, w, "ff", lmax, H)
+    assert (got - _spectral_expected(x, w, C, H, lmax)).abs().max() < 1e-12
+
+
+def test_spectral_ff_known_answer_catches_planted_mistakes(monkeypatch):
+    """Each plausible wiring mistake, planted into a copy of the oracle's spectral FF, fails the
+    loop known answer: a missing SiLU on the gating, swapped degree-1 / degree-2 gate rows, the
+    bias on every coefficient, transposed per-degree weights, or one shared weight for all
+    degrees."""
+    import torch.nn.functional as F
+    x, w, C, H, lmax = _spectral_case()
+    ref = _spectral_expected(x, w, C, H, lmax)
+
+    def variant(mistake):
+        def so3(v, Wt, b):
+            outs, s = [], 0
+            for l in range(lmax + 1):
+                n = 2 * l + 1
+                Wl = Wt[0] if mistake == "shared" else Wt[l]
+                ob = v[:, s:s + n, :] @ (Wl if mistake == "transposed" and Wl.shape[0] == Wl.shape[1]
+                                         else Wl.T)
+                if l == 0 or mistake == "bias_all":
+                    ob = ob + b.view(1, 1, -1)
+                outs.append(ob)
+                s += n
+            return torch.cat(outs, 1)
+        a = F.linear(x[:, 0, :], w["ff.scalar_mlp.0.weight"], w["ff.scalar_mlp.0.bias"])
+        gating = a if mistake == "no_silu" else F.silu(a)
+        h = so3(x, w["ff.so3_linear_1.weight"], w["ff.so3_linear_1.bias"])
+        sg = torch.sigmoid(gating)
+        rows = [1, 0] if mistake == "swap_rows" else [0, 1]
+        parts, s = [F.silu(h[:, 0:1, :])], 1
+        for l in range(1, lmax + 1):
+            n = 2 * l + 1
+            r = rows[l - 1]
+            parts.append(h[:, s:s + n, :] * sg[:, r * H:(r + 1) * H].unsqueeze(1))
+            s += n
+        return so3(torch.cat(parts, 1), w["ff.so3_linear_2.weight"], w["ff.so3_linear_2.bias"])
+
+    assert (variant(None) - ref).abs().max() < 1e-12
+    for mistake in ("no_silu", "swap_rows", "bias_all", "shared"):
+        assert (variant(mistake) - ref).abs().max() > 1e-3, mistake
+
+
+def test_safe_acos_atan2_regularised_gradients_known_values():
+    """The regularised derivatives of the Euler angles (geometry.py:87-109): acos' = -1/sqrt(1-x^2)
+    with x clamped to [-1 + 1e-7, 1 - 1e-7] and the root clamped at 1e-7; atan2' = (x, -y) / r^2
+    with r^2 clamped at 1e-7.  Generic points give the textbook derivatives; the poles give the
+    clamped values."""
+    x = torch.tensor([0.6, 1.0, -1.0, 0.0], dtype=torch.float64, requires_grad=True)
+    (g,) = torch.autograd.grad(G.SafeAcos.apply(x).sum(), x)
+    xc = 1 - 1e-7
+    pole = -1.0 / math.sqrt(1 - xc * xc)
+    ref = torch.tensor([-1.25, pole, pole, -1.0], dtype=torch.float64)
+    assert (g - ref).abs().max() < 1e-9 * abs(pole)
+    y = torch.tensor([3.0, 0.0, 1e-5, -2.0], dtype=torch.float64, requires_grad=True)
+    xx = torch.tensor([4.0, 0.0, 0.0, 0.0], dtype=torch.float64, requires_grad=True)
+    gy, gx = torch.autograd.grad(G.SafeAtan2.apply(y, xx).sum(), (y, xx))
+    torch.testing.assert_close(gy, torch.tensor([4 / 25, 0.0, 0.0, 0.0], dtype=torch.float64),
+                               rtol=0, atol=1e-15)
+    torch.testing.assert_close(gx, torch.tensor([-3 / 25, 0.0, -1e-5 / 1e-7, 2.0 / 4.0],
+                                                dtype=torch.float64), rtol=1e-12, atol=1e-15)

@@ -185,6 +185,14 @@ int tta_node_forces(const float* g_ev, const int* src_ptr, const int* src_perm,
 /* virial[3x3] = sum_e sym(ev (x) g_ev) = dE/dstrain (forces.py:516-524); work >= 256*9 floats. */
 int tta_virial(const float* ev, const float* g_ev, int64_t E, float* work, float* out,
                tta_stream_t stream);
+/* tta_virial without the `work` argument: no counterpart in the reference.  For callers that
+ * cannot allocate (code under HIP graph capture, tight MD loops, harnesses that forbid
+ * hipMalloc): it allocates nothing and takes its 256 * 9 partial sums (9 KB) from a device array
+ * of the library, one per GPU, held until the process ends.  Limit: E <= 2^31 - 1 (the same as
+ * tta_virial; the scratch size does not depend on E).  Calls that overlap on one GPU share that
+ * array and race; calls in stream order do not (every call rewrites all of it). */
+int tta_virial_noalloc(const float* ev, const float* g_ev, int64_t E, float* out,
+                       tta_stream_t stream);
 
 /* ---------------------------------------------------------------- Orb-v3 edge MLP + scatter
  * Internal edge order is sender-sorted (stable): sender segments are [send_ptr[n], send_ptr[n+1]),

@@ -16,6 +16,9 @@ void set_error(const char* fmt, ...) {
 
 }  // namespace tta
 
+// geometry.hip: resolves the allocation-free entry points' device scratch on the current device.
+int tta_init_scratch_current_device();
+
 extern "C" const char* tta_last_error(void) { return tta::g_err; }
 
 extern "C" int tta_version(void) { return 1; }
@@ -41,5 +44,5 @@ extern "C" int tta_check_device(char* name_out, int64_t name_len) {
     tta::set_error("tta_check_device: device %s is not gfx950", prop.gcnArchName);
     return tta::kUnsupported;
   }
-  return tta::kOk;
+  return tta_init_scratch_current_device();
 }

@@ -4,6 +4,8 @@
 //
 // Reference: tt_atom/geometry.py:226-280 (forward terms) and the host autograd finish of
 // forces.py:545-589 (here in closed form, geometry_math.h).
+#include <mutex>
+
 #include "common.h"
 #include "geometry_math.h"
 
@@ -148,6 +150,50 @@ __global__ __launch_bounds__(64) void k_virial_final(const float* __restrict__ p
 
 }  // namespace
 
+// ---------------------------------------------------------------------------------------------
+// Allocation-free virial: the partial sums of the two-stage reduction live in this file-scope
+// device array instead of a caller workspace.  Every GPU that runs tta_virial_noalloc holds its
+// own copy until the process ends.  Host code never passes `scratch` itself (its host-side name
+// is not a device address); it passes the per-device address hipGetSymbolAddress returns.
+static __device__ __align__(256) float scratch[kVirBlocks * 9];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, resolved once per device (with that
+// device current) and kept.
+int scratch_for_current_device(const char* who, float** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    tta::set_error("%s: no usable current HIP device (%d)", who, dev);
+    return tta::kUnsupported;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      tta::set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
+                     hipGetErrorString(e));
+      return tta::kLaunchFailed;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return tta::kOk;
+}
+
+}  // namespace
+
+// Called by tta_check_device (the library's set-up call) for the device it checks.
+int tta_init_scratch_current_device() {
+  float* p = nullptr;
+  return scratch_for_current_device("tta_check_device", &p);
+}
+
 extern "C" int tta_edge_wigner(const float* pos, const int* src, const int* tgt,
                                const float* shift, const float* jd, float gamma, float* ev,
                                float* dist, float* coef, int64_t N, int64_t E,
@@ -207,7 +253,7 @@ extern "C" int tta_node_forces(const float* g_ev, const int* src_ptr, const int*
   return tta::kOk;
 }
 
-// `work` must hold 256 * 9 floats.
+// `work` must hold kVirBlocks * 9 = 256 * 9 floats.
 extern "C" int tta_virial(const float* ev, const float* g_ev, int64_t E, float* work, float* out,
                           hipStream_t stream) {
   TTA_CHECK_ARG(E >= 0 && E < (1ll << 31), "tta_virial: bad sizes");
@@ -216,5 +262,23 @@ extern "C" int tta_virial(const float* ev, const float* g_ev, int64_t E, float* 
                      work);
   hipLaunchKernelGGL(k_virial_final, dim3(1), dim3(64), 0, stream, work, kVirBlocks, out);
   TTA_CHECK_LAUNCH("tta_virial");
+  return tta::kOk;
+}
+
+// tta_virial without the workspace argument: the kVirBlocks x 9 partial sums go to this
+// device's `scratch`.  Each block writes its whole row, so nothing needs clearing between calls;
+// calls that overlap on one GPU (concurrent streams) share the array and race.
+extern "C" int tta_virial_noalloc(const float* ev, const float* g_ev, int64_t E, float* out,
+                                  hipStream_t stream) {
+  TTA_CHECK_ARG(E >= 0 && E < (1ll << 31),
+                "tta_virial_noalloc: E = %lld edges is outside [0, 2^31 - 1]", (long long)E);
+  TTA_CHECK_ARG(out && ((ev && g_ev) || E == 0), "tta_virial_noalloc: null pointer");
+  float* part = nullptr;
+  const int st = scratch_for_current_device("tta_virial_noalloc", &part);
+  if (st != tta::kOk) return st;
+  hipLaunchKernelGGL(k_virial_partial, dim3(kVirBlocks), dim3(256), 0, stream, ev, g_ev, (int)E,
+                     part);
+  hipLaunchKernelGGL(k_virial_final, dim3(1), dim3(64), 0, stream, part, kVirBlocks, out);
+  TTA_CHECK_LAUNCH("tta_virial_noalloc");
   return tta::kOk;
 }

@@ -56,6 +56,7 @@ _SIGS = {
     "tta_edge_geometry_bwd": [_P, _P, _P, _P, _P, _I64, _P, _F, _F, _I64, _P, _F, _P, _I64, _P],
     "tta_node_forces": [_P, _P, _P, _P, _P, _I64, _I64, _P],
     "tta_virial": [_P, _P, _I64, _P, _P, _P],
+    "tta_virial_noalloc": [_P, _P, _I64, _P, _P],
     "tta_gemm_f32_gather": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64,
                             _P, _P, _I64, _I64, _I, _P],
     "tta_orb_edge_features": [_P, _P, _P, _P, _F, _I64, _P, _P, _P, _I64, _I64, _P],
@@ -591,6 +592,14 @@ def virial(ev, g_ev, work, out):
     E = ev.shape[0]
     _call("tta_virial", _ptr(ev, numel=E * 3), _ptr(g_ev, numel=E * 3), E,
           _ptr(work, numel=256 * 9, name="work"), _ptr(out, numel=9), _stream())
+
+
+def virial_noalloc(ev, g_ev, out):
+    """``virial`` without a workspace: the library's per-GPU device scratch holds the partial
+    sums (nothing is allocated; overlapping calls on one GPU race)."""
+    E = ev.shape[0]
+    _call("tta_virial_noalloc", _ptr(ev, numel=E * 3), _ptr(g_ev, numel=E * 3), E,
+          _ptr(out, numel=9), _stream())
 
 
 # ----------------------------------------------------------------------------- neighbour list

@@ -18,7 +18,7 @@ Also reported on the same JSON line:
                 same K steps, so that the timed pass carries no instrumentation), against
                 the ceiling of its arithmetic (fp16 dense MFMA peak 2.5 PFLOP/s / 3 plane
                 products); ``traffic`` = HBM bytes per launch from rocprofv3 FETCH_SIZE +
-                WRITE_SIZE when profiles/gemm_f16x3_traffic_c3.txt holds them, else null.  The
+                WRITE_SIZE when profiles/uma_c3_step_counters.txt holds them, else null.  The
                 other GEMM kernel family (fp32 MFMA, node-level and short-K products) is listed
                 under ``gemm_families``; ``hbm_kernels`` gives the same for the HBM-bound edge
                 kernels (rotation, segment sums) against the 8 TB/s HBM peak.
@@ -56,7 +56,10 @@ KERNELS = {"f32": "gemm_f32_kernel (fp32 MFMA 16x16x4)",
            "bf16x6": "gemm_bf16x_kernel<2,6> (split-bf16, 3x3 planes / 6 products, fp32-accurate)",
            "bf16x3": "gemm_bf16x_kernel<2,3> (split-bf16, 2x2 planes / 3 products)",
            "bf16x1": "gemm_bf16x_kernel<2,1> (bf16 operands)"}
-TRAFFIC_FILE = ROOT / "profiles" / "gemm_f16x3_traffic_c3.txt"
+# rocprofv3 counter summary of the C3 step (per-kernel HBM bytes and MFMA counters), written by
+# ``bench.py --summarize-counters`` from the profiler's CSV output; read to report counter-measured
+# HBM bytes next to the algorithmic ones.
+TRAFFIC_FILE = ROOT / "profiles" / "uma_c3_step_counters.txt"
 
 
 class GemmEvents:
@@ -97,12 +100,13 @@ class HbmEvents:
         self.k = {}
         self._cur = None
 
-    def before(self, kernel, nbytes):
+    def before(self, kernel, nbytes, compulsory=None):
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
         self._cur = (e, kernel)
-        d = self.k.setdefault(kernel, {"pairs": [], "nbytes": 0.0})
+        d = self.k.setdefault(kernel, {"pairs": [], "nbytes": 0.0, "compulsory": 0.0})
         d["nbytes"] += nbytes
+        d["compulsory"] += nbytes if compulsory is None else compulsory
 
     def after(self):
         e = self.torch.cuda.Event(enable_timing=True)
@@ -110,16 +114,30 @@ class HbmEvents:
         start, kernel = self._cur
         self.k[kernel]["pairs"].append((start, e))
 
-    def summary(self):
+    def summary(self, traffic=None):
+        """Per kernel: launches, average HIP-event duration, and GB/s from (i) the compulsory
+        bytes (every distinct operand byte once: the least HBM traffic the launch can have;
+        ``frac`` is this one), (ii) the algorithmic per-use bytes (gathered node rows once per
+        edge) and, when ``traffic`` holds the kernel, (iii) the rocprofv3 FETCH_SIZE +
+        WRITE_SIZE bytes per launch of the same workload."""
         out = {}
         for name, d in self.k.items():
             ms = sum(a.elapsed_time(b) for a, b in d["pairs"])
-            n = len(d["pairs"])
-            gbs = d["nbytes"] / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
-            out[name] = {"launches": n, "avg_launch_us": round(ms * 1e3 / max(1, n), 2),
-                         "algorithmic_bytes_per_launch": round(d["nbytes"] / max(1, n)),
-                         "achieved_GBps": round(gbs, 1), "peak_GBps": PEAK_HBM_GBPS,
-                         "frac": round(gbs / PEAK_HBM_GBPS, 4)}
+            n = max(1, len(d["pairs"]))
+            sec = ms * 1e-3 / n
+            rate = (lambda b: b / sec / 1e9 if sec > 0 else 0.0)
+            comp, per_use = d["compulsory"] / n, d["nbytes"] / n
+            e = {"launches": len(d["pairs"]), "avg_launch_us": round(sec * 1e6, 2),
+                 "compulsory_bytes_per_launch": round(comp),
+                 "achieved_GBps": round(rate(comp), 1), "peak_GBps": PEAK_HBM_GBPS,
+                 "frac": round(rate(comp) / PEAK_HBM_GBPS, 4),
+                 "algorithmic_bytes_per_launch": round(per_use),
+                 "algorithmic_GBps": round(rate(per_use), 1)}
+            if traffic and name in traffic:
+                e["counter_bytes_per_launch"] = round(traffic[name])
+                e["counter_GBps"] = round(rate(traffic[name]), 1)
+                e["counter_frac"] = round(rate(traffic[name]) / PEAK_HBM_GBPS, 4)
+            out[name] = e
         return out
 
 
@@ -414,18 +432,133 @@ def cpu_baseline(torch):
                                        f"(E={ei.shape[1]})", dt, ts, threads)}
 
 
-def read_traffic():
-    if not TRAFFIC_FILE.exists():
-        return None
-    vals = {}
-    for line in TRAFFIC_FILE.read_text().splitlines():
-        if ":" in line and not line.startswith("#"):
-            k, v = line.split(":", 1)
-            vals[k.strip()] = v.strip()
-    try:
-        return float(vals["hbm_bytes_per_launch"])
-    except (KeyError, ValueError):
-        return None
+def read_traffic(path=TRAFFIC_FILE):
+    """{kernel: HBM bytes per launch} and {kernel: MFMA counter figures} from the ``traffic`` and
+    ``mfma`` lines of a counter summary written by ``--summarize-counters``."""
+    traffic, mfma = {}, {}
+    if not path.exists():
+        return traffic, mfma
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == "traffic":
+            traffic[parts[1]] = float(parts[2])
+        elif len(parts) >= 3 and parts[0] == "mfma":
+            mfma[parts[1]] = {k: float(v) for k, v in (t.split("=") for t in parts[2:])}
+    return traffic, mfma
+
+
+def _kernel_names(full):
+    """(variant, base) of a profiler kernel name: 'void (anonymous namespace)::k<2, 9>(float..)'
+    -> ('k<2,9>', 'k')."""
+    n = full.replace("(anonymous namespace)::", "")
+    if n.startswith("void "):
+        n = n[5:]
+    depth, end = 0, len(n)
+    for i, ch in enumerate(n):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            end = i
+            break
+    variant = n[:end].replace(" ", "")
+    return variant, variant.split("<", 1)[0]
+
+
+def _read_pmc(d):
+    """rocprofv3 --pmc CSV rows under directory d -> {dispatch: {kernel, counters{}, ns}}."""
+    import csv
+    rows = {}
+    for f in sorted(pathlib.Path(d).rglob("*counter_collection.csv")):
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                key = (str(f), r["Dispatch_Id"])
+                e = rows.setdefault(key, {"kernel": r["Kernel_Name"], "c": {},
+                                          "ns": int(r["End_Timestamp"]) - int(r["Start_Timestamp"])})
+                e["c"][r["Counter_Name"]] = e["c"].get(r["Counter_Name"], 0.0) + float(
+                    r["Counter_Value"])
+    return rows
+
+
+def summarize_counters(root, out_path):
+    """Per-kernel HBM bytes and MFMA counters of a profiled C3 step.
+
+    ``root`` holds the rocprofv3 --pmc output of five runs: step_FETCH_SIZE, step_WRITE_SIZE and
+    step_MFMA (the step under ``--pmc FETCH_SIZE``, ``WRITE_SIZE`` and ``MfmaUtil MfmaFlopsF16
+    MfmaFlopsF32``)
+    and copy_FETCH_SIZE, copy_WRITE_SIZE (``--calibrate-copy``: a 256 MiB read + 256 MiB write
+    copy kernel).  Bytes = counter KiB x 1024 x (the copy's known bytes / what the same counter
+    reads for it)."""
+    root = pathlib.Path(root)
+    copy_bytes = 256 * 1024 * 1024
+    scale = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        vals = [e["c"].get(c, 0.0) for e in _read_pmc(root / f"copy_{c}").values()]
+        scale[c] = copy_bytes / (max(vals) * 1024.0)
+    per = {}
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        for e in _read_pmc(root / f"step_{c}").values():
+            v, b = _kernel_names(e["kernel"])
+            for k in {v, b}:
+                d = per.setdefault(k, {"FETCH_SIZE": [], "WRITE_SIZE": [], "variant": k == v})
+                d[c].append(e["c"].get(c, 0.0))
+    mf = {}
+    mdir = root / "step_MFMA"
+    if mdir.exists():
+        for e in _read_pmc(mdir).values():
+            v, _ = _kernel_names(e["kernel"])
+            d = mf.setdefault(v, {"util": [], "flops": [], "ns": []})
+            d["util"].append(e["c"].get("MfmaUtil", 0.0))
+            d["flops"].append(sum(e["c"].get(c, 0.0) for c in
+                                  ("MfmaFlopsF16", "MfmaFlopsBF16", "MfmaFlopsF32")))
+            d["ns"].append(e["ns"])
+    lines = ["# rocprofv3 counters of the C3 step (uma-s-1 architecture, 2048 atoms, E = 61440), "
+             "MI355X", "# Commands (repository root $REPO on the GPU box; one pass per counter "
+             "group):", "#   cd /tmp && export TMPDIR=/tmp"]
+    step = ("python3 $REPO/bench.py --steps 1 --warmup 1 --no-cpu-baseline --no-secondary --eager")
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        lines.append(f"#   rocprofv3 --pmc {c} --output-format csv -d $REPO/gpurun_out/pmc/step_{c}"
+                     f" -o s -- {step}")
+    lines.append("#   rocprofv3 --pmc MfmaUtil MfmaFlopsF16 MfmaFlopsF32 --output-format csv -d "
+                 f"$REPO/gpurun_out/pmc/step_MFMA -o s -- {step}")
+    for c in ("FETCH_SIZE", "WRITE_SIZE"):
+        lines.append(f"#   rocprofv3 --pmc {c} --output-format csv -d $REPO/gpurun_out/pmc/copy_{c}"
+                     f" -o c -- python3 $REPO/bench.py --calibrate-copy")
+    lines.append("#   python3 $REPO/bench.py --summarize-counters $REPO/gpurun_out/pmc "
+                 "profiles/uma_c3_step_counters.txt")
+    lines.append(f"# Calibration (256 MiB copy): FETCH_SIZE x {scale['FETCH_SIZE']:.4f}, "
+                 f"WRITE_SIZE x {scale['WRITE_SIZE']:.4f}")
+    lines.append("# Three steps are profiled (warm-up, timed, probed); figures are means per launch.")
+    lines.append("#")
+    lines.append("# kernel | launches | FETCH KiB raw | WRITE KiB raw | HBM MB per launch "
+                 "(scaled read + write)")
+    traffic = []
+    for k, d in sorted(per.items(), key=lambda kv: -sum(kv[1]["FETCH_SIZE"])):
+        n = len(d["FETCH_SIZE"])
+        if n == 0 or len(d["WRITE_SIZE"]) != n or "::" in k or k.startswith("__"):
+            continue                       # library kernels only (torch / rocprim / runtime copies)
+        fk, wk = sum(d["FETCH_SIZE"]) / n, sum(d["WRITE_SIZE"]) / n
+        nbytes = 1024.0 * (fk * scale["FETCH_SIZE"] + wk * scale["WRITE_SIZE"])
+        if d["variant"]:
+            lines.append(f"#   {k} | {n} | {fk:.1f} | {wk:.1f} | {nbytes / 1e6:.1f}")
+        traffic.append(f"traffic {k} {nbytes:.0f}")
+    if mf:
+        lines.append("#")
+        lines.append("# MFMA counters (MfmaUtil = matrix-core busy cycles / (GUI-active cycles x "
+                     "SIMDs); MfmaFlopsF16 / F32 = 512 x MOPS, the matrix work actually issued)")
+        for k, d in sorted(mf.items(), key=lambda kv: -sum(kv[1]["ns"])):
+            if max(d["flops"]) <= 0 or "::" in k:
+                continue
+            n = len(d["util"])
+            util = sum(d["util"]) / n
+            fl = sum(d["flops"]) / n
+            us = sum(d["ns"]) / n / 1e3
+            lines.append(f"#   {k} | {n} launches | MfmaUtil {util:.1f} % | {fl / 1e9:.1f} GFLOP "
+                         f"issued per launch | {us:.1f} us under counters | "
+                         f"{fl / (us * 1e-6) / 1e12:.0f} TFLOP/s issued")
+            traffic.append(f"mfma {k} util_pct={util:.2f} issued_flops={fl:.0f} us={us:.2f}")
+    pathlib.Path(out_path).write_text("\n".join(lines + traffic) + "\n")
 
 
 def main():
@@ -452,7 +585,12 @@ def main():
                          "steps")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 256 MiB device copy (y = -x) for the HBM counter scale")
+    ap.add_argument("--summarize-counters", nargs=2, metavar=("PMC_ROOT", "OUT"),
+                    help="write the per-kernel counter summary of rocprofv3 --pmc runs (no GPU)")
     args = ap.parse_args()
+    if args.summarize_counters:
+        summarize_counters(*args.summarize_counters)
+        return
     if args.calibrate_copy:
         import torch
         x = torch.randn(64 * 1024 * 1024, device="cuda")
@@ -610,8 +748,11 @@ def main():
     dom = max(fam, key=lambda k: fam[k]["ms"])
     d = fam[dom]
     achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12 if d["ms"] > 0 else 0.0
-    traffic = read_traffic() if (wl == "c3" and dom == "f16x3" and args.precision == "f32") \
-        else None
+    counted = wl == "c3" and args.precision == "f32"
+    kernel_traffic, kernel_mfma = read_traffic() if counted else ({}, {})
+    dom_kernel = {"f16x3": "gemm_bf16x_kernel<2,16>"}.get(dom)
+    traffic = kernel_traffic.get(dom_kernel) if dom_kernel else None
+    mfma_counters = kernel_mfma.get(dom_kernel) if dom_kernel else None
     ms_step = dt / args.steps * 1e3
     others = {k: {"launches": v["n"], "avg_launch_us": round(v["ms"] * 1e3 / max(1, v["n"]), 2),
                   "achieved_tflops": round(v["flops"] / max(1e-12, v["ms"] * 1e-3) / 1e12, 2),
@@ -668,6 +809,7 @@ def main():
                      "achieved": round(achieved, 3), "peak": round(PEAKS[dom], 2),
                      "unit": "TFLOP/s", "frac": round(achieved / PEAKS[dom], 4),
                      "traffic": traffic, "launches": d["n"],
+                     "mfma_counters": mfma_counters,
                      "algorithmic_bytes_per_launch": round(d["nbytes"] / max(1, d["n"])),
                      "algorithmic_flops_per_launch": round(d["flops"] / max(1, d["n"])),
                      "avg_launch_us": round(d["ms"] * 1e3 / max(1, d["n"]), 2),
@@ -683,11 +825,11 @@ def main():
                      "measured": ("HIP events around each launch, on the launch stream, over a "
                                   "second pass of the same steps"),
                      "gemm_families": others},
-        "hbm_kernels": hbm.summary(),
-        "hbm_kernels_note": ("fractions of the 8 TB/s peak from algorithmic bytes, which count "
-                             "every operand use: node rows gathered per edge are counted per "
-                             "edge although most hit in the L2 / MALL, so a gather kernel can "
-                             "read above 1 (k_gather_rotate)"),
+        "hbm_kernels": hbm.summary(kernel_traffic),
+        "hbm_kernels_note": ("frac = compulsory bytes (every distinct operand byte once) / HIP-event "
+                             "time / 8 TB/s; algorithmic_GBps counts gathered node rows once per "
+                             "edge; counter_GBps uses rocprofv3 FETCH_SIZE + WRITE_SIZE bytes per "
+                             "launch of the same workload (profiles/uma_c3_step_counters.txt)"),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = (cpu_baseline_c5(torch) if wl == "c5" else

@@ -378,9 +378,12 @@ def _ld(t, name):
 
 
 # ----------------------------------------------------------------------------- rotation
-# Optional measurement hook for the HBM-bound edge kernels: ``probe.before(kernel, nbytes)`` /
-# ``probe.after()`` around each launch, nbytes = algorithmic bytes (every operand read or written
-# once per use; gathered node rows count once per edge).
+# Optional measurement hook for the HBM-bound edge kernels: ``probe.before(kernel, nbytes,
+# compulsory)`` / ``probe.after()`` around each launch.  nbytes = algorithmic bytes (every operand
+# read or written once per use: gathered node rows count once per edge); compulsory = every
+# distinct operand byte once (a gathered node tensor counts once), the least HBM traffic the
+# launch can have.  They differ only for the kernels that gather node rows per edge or read an
+# edge row twice.
 _hbm_probe = None
 
 
@@ -389,10 +392,10 @@ def set_hbm_probe(probe):
     _hbm_probe = probe
 
 
-def _hbm_call(kernel, nbytes, name, *args):
+def _hbm_call(kernel, nbytes, name, *args, compulsory=None):
     probe = _hbm_probe
     if probe is not None:
-        probe.before(kernel, float(nbytes))
+        probe.before(kernel, float(nbytes), float(nbytes if compulsory is None else compulsory))
     _call(name, *args)
     if probe is not None:
         probe.after()
@@ -401,11 +404,13 @@ def _hbm_call(kernel, nbytes, name, *args):
 def gather_rotate(x, src, tgt, coef, rad, out):
     N, nsph, C = x.shape
     E = src.numel()
-    nbytes = E * (4 * (9 * C + 9 * C + 35 + (12 * C if rad is not None else 0) + 18 * C) + 8)
+    edge = 4 * (35 + (12 * C if rad is not None else 0) + 18 * C) + 8
+    nbytes = E * (edge + 4 * 18 * C)
     _hbm_call("k_gather_rotate", nbytes, "tta_gather_rotate", _ptr(x, numel=N * 9 * C, name="x"),
               _i32(src, E), _i32(tgt, E),
               _ptr(coef, numel=E * 35, name="coef"), _ptr(rad, numel=E * 12 * C, name="rad"),
-              _ptr(out, numel=E * 18 * C, name="out"), N, E, C, _stream())
+              _ptr(out, numel=E * 18 * C, name="out"), N, E, C, _stream(),
+              compulsory=E * edge + 4 * N * 9 * C)
     return out
 
 
@@ -415,32 +420,34 @@ def gather_rotate_src(x, src, coef, out):
     _hbm_call("k_gather_rotate_src", E * (4 * (9 * C + 35 + 9 * C) + 4), "tta_gather_rotate_src",
               _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E),
               _ptr(coef, numel=E * 35, name="coef"), _ptr(out, numel=E * 9 * C, name="out"), N, E, C,
-              _stream())
+              _stream(), compulsory=E * (4 * (35 + 9 * C) + 4) + 4 * N * 9 * C)
     return out
 
 
 def gather_rotate_src_bw(g_out, x, src, coef, g_in, g_coef):
     N, _, C = x.shape
     E = src.numel()
-    nbytes = E * (4 * (9 * C + 9 * C + 35 + 70 + (9 * C if g_in is not None else 0)) + 4)
-    _hbm_call("k_gather_rotate_src_bw", nbytes, "tta_gather_rotate_src_bw",
+    edge = 4 * (9 * C + 35 + 70 + (9 * C if g_in is not None else 0)) + 4
+    _hbm_call("k_gather_rotate_src_bw", E * (edge + 4 * 9 * C), "tta_gather_rotate_src_bw",
               _ptr(g_out, numel=E * 9 * C, name="g_out"),
               _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E), _ptr(coef, numel=E * 35, name="coef"),
               None if g_in is None else _ptr(g_in, numel=E * 9 * C, name="g_in"),
-              _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream())
+              _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream(),
+              compulsory=E * edge + 4 * N * 9 * C)
 
 
 def gather_rotate_bw(g_xf, rad, x, src, tgt, coef, g_rad, g_mcat, g_coef):
     N, _, C = x.shape
     E = src.numel()
-    nbytes = E * (4 * (18 * C + (24 * C if rad is not None else 0) + 18 * C + 35 + 70 + 18 * C)
-                  + 8)
+    edge = 4 * (18 * C + (24 * C if rad is not None else 0) + 35 + 70 + 18 * C) + 8
+    nbytes = E * (edge + 4 * 18 * C)
     _hbm_call("k_gather_rotate_bw", nbytes, "tta_gather_rotate_bw",
               _ptr(g_xf, numel=E * 18 * C, name="g_xf"),
               _ptr(rad, numel=E * 12 * C, name="rad"), _ptr(x, numel=N * 9 * C, name="x"),
               _i32(src, E), _i32(tgt, E), _ptr(coef, numel=E * 35, name="coef"),
               _ptr(g_rad, numel=E * 12 * C, name="g_rad"), _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
-              _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream())
+              _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream(),
+              compulsory=E * edge + 4 * N * 9 * C)
 
 
 def rotate_env_segsum(m, coef, env, tgt_ptr, res, out, *, n_in, env_first, div=1.0):
@@ -466,7 +473,8 @@ def rotate_env_segsum_bw(g_node, tgt, m, coef, env, g_m, g_coef, g_env, *, n_in,
               _ptr(m, numel=E * n_in * C, name="m"), _ptr(coef, numel=E * 35, name="coef"),
               _ptr(env, numel=E, name="env"), _ptr(g_m, numel=E * n_in * C, name="g_m"),
               _ptr(g_coef, numel=E * 35, name="g_coef"), _ptr(g_env, numel=E, name="g_env"), N, E, C,
-              n_in, int(env_first), float(div), _stream())
+              n_in, int(env_first), float(div), _stream(),
+              compulsory=nbytes - 4 * E * 9 * C + 4 * N * 9 * C)
 
 
 def node_gather_sum(g_mcat, src_ptr, src_perm, tgt_ptr, res, out):
@@ -722,7 +730,8 @@ def orb_segsum(ue, sig, cut, send_ptr, recv_ptr, recv_perm, nodes, node_in):
               _ptr(sig, numel=2 * E, name="sig"), _ptr(cut, numel=E, name="cut"),
               _i32(send_ptr, N + 1), _i32(recv_ptr, N + 1), _i32(recv_perm, E),
               _ptr(nodes, numel=N * C, name="nodes"),
-              _ptr(node_in, numel=N * 3 * C, name="node_in"), N, E, C, _stream())
+              _ptr(node_in, numel=N * 3 * C, name="node_in"), N, E, C, _stream(),
+              compulsory=nbytes - 4 * E * C)
 
 
 def orb_edge_bwd(g_e, g_node_in, ue, sig, cut, h2, inv, wn, attn_w, send, recv, g_h2, g_cut):
@@ -736,7 +745,8 @@ def orb_edge_bwd(g_e, g_node_in, ue, sig, cut, h2, inv, wn, attn_w, send, recv, 
               _ptr(sig, numel=2 * E), _ptr(cut, numel=E), _ptr(h2, numel=n),
               _ptr(inv, numel=E), _ptr(wn, numel=C), _ptr(attn_w, numel=2 * C), _i32(send, E),
               _i32(recv, E), _ptr(g_h2, numel=n, name="g_h2"),
-              _ptr(g_cut, numel=E, name="g_cut"), N, E, C, _stream())
+              _ptr(g_cut, numel=E, name="g_cut"), N, E, C, _stream(),
+              compulsory=nbytes - 4 * 2 * n + 4 * 2 * N * C)
 
 
 def orb_node_segsum2(x, send_ptr, recv_ptr, recv_perm, out):
@@ -745,7 +755,8 @@ def orb_node_segsum2(x, send_ptr, recv_ptr, recv_perm, out):
     nbytes = 4 * (2 * E * H + E + 2 * (N + 1) + 2 * N * H)
     _hbm_call("k_node_segsum2", nbytes, "tta_orb_node_segsum2", _ptr(x, numel=E * H, name="x"),
               _i32(send_ptr, N + 1), _i32(recv_ptr, N + 1), _i32(recv_perm, E),
-              _ptr(out, numel=N * 2 * H, name="out"), N, E, H, _stream())
+              _ptr(out, numel=N * 2 * H, name="out"), N, E, H, _stream(),
+              compulsory=nbytes - 4 * E * H)
 
 
 def segment_mean(x, ptr, out):

@@ -31,29 +31,12 @@ from . import _native as nat
 from .graphs import StepGraphs
 from .geometry import system_graphs
 from .model import PRECISIONS, _gw
-from .weights import NpzBundle
+from .orb_weights import OrbWeights  # noqa: F401  (re-exported: orb.OrbWeights)
 
 HIDDEN_DIM = 1024  # the reference's fixed MLP width (orb_calculator.py:57)
 
 
 # ----------------------------------------------------------------------------- weights
-class OrbWeights(NpzBundle):
-    """``.npz`` bundle of MoleculeGNS parameters: ``config`` JSON + ``w@<state_dict key>``
-    (orb_weights.py:15-26; tools/export_orb_weights.py:51-82)."""
-
-    def activation(self, key):
-        return self._t(f"a@{key}").float()
-
-    def host(self, key):
-        return self._t(f"host@{key}").float()
-
-    def inp(self, key):
-        return self._t(f"in@{key}")
-
-    def out(self, key):
-        return self._t(f"out@{key}")
-
-
 def save_orb_bundle(path, cfg, weights):
     out = {"config": np.frombuffer(json.dumps(cfg).encode(), dtype=np.uint8)}
     for k, v in weights.items():
@@ -253,6 +236,19 @@ class _Layer:
             self.cond_b = _dev(w[f"{prefix}._cond_node_proj.bias"], device)
 
 
+class _Head:
+    """Linear-SiLU-Linear readout weights of an energy / force / stress head
+    (orb_model.py:307-435): forward w_t [in, out], backward w [out, in], biases."""
+
+    def __init__(self, w, prefix, device, n_out):
+        self.w_t = [_dev(w[f"{prefix}.mlp.NN-{i}.weight"].T.contiguous(), device) for i in (0, 1)]
+        self.w = [_dev(w[f"{prefix}.mlp.NN-{i}.weight"], device) for i in (0, 1)]
+        self.b = [_dev(w[f"{prefix}.mlp.NN-{i}.bias"], device) for i in (0, 1)]
+        if self.w_t[1].shape[1] != n_out:
+            raise RuntimeError(f"{prefix} must have {n_out} outputs")
+        self.hidden = int(self.w_t[0].shape[1])
+
+
 class OrbModel:
     """Device-resident Orb-v3 weights, built once per checkpoint (orb_calculator.py:54-73)."""
 
@@ -275,41 +271,62 @@ class OrbModel:
             raise RuntimeError("latent_dim must be a multiple of 4 and at most 1024")
         dev = self.device
         self.node_emb = w["atom_emb.embeddings.weight"]          # host table, gathered per graph
-        self.enc_node = _MLPNorm(w, "_encoder._node_fn", dev, mode)
-        self.enc_edge = _MLPNorm(w, "_encoder._edge_fn", dev, mode)
-        self.layers = [_Layer(w, f"gnn_stacks.{i}", dev, self.C, mode)
-                       for i in range(int(cfg["num_message_passing_steps"]))]
+        enc = (_MLPNorm(w, "_encoder._node_fn", dev, mode),
+               _MLPNorm(w, "_encoder._edge_fn", dev, mode))
+        layers = [_Layer(w, f"gnn_stacks.{i}", dev, self.C, mode)
+                  for i in range(int(cfg["num_message_passing_steps"]))]
+        # direct checkpoints carry a force head (and usually a stress head) and are evaluated by
+        # the forward alone (orb_calculator.py:66-72, 141-185)
+        heads = [_Head(w, "energy_head", dev, 1)]
+        heads.append(_Head(w, "forces_head", dev, 3) if "forces_head.mlp.NN-0.weight" in w
+                     else None)
+        heads.append(_Head(w, "stress_head", dev, 6) if "stress_head.mlp.NN-0.weight" in w
+                     else None)
+        host_w = {k: v for k, v in w.items() if k.startswith(("energy_head.normalizer",
+                                                              "energy_head.reference",
+                                                              "forces_head.normalizer",
+                                                              "stress_head.diag_normalizer",
+                                                              "stress_head.offdiag_normalizer",
+                                                              "conditioner."))}
+        self._finish(enc, layers, heads, host_w)
+
+    def _finish(self, enc, layers, heads, host_w):
+        self.enc_node, self.enc_edge = enc
+        self.layers = list(layers)
         self.H = self.layers[0].edge.hidden if self.layers else self.enc_edge.hidden
         for L in self.layers:
             if L.edge.hidden != self.H or L.node.hidden != self.H:
                 raise RuntimeError("all edge / node MLPs must share one hidden width")
-        self.eh_w_t = [_dev(w[f"energy_head.mlp.NN-{i}.weight"].T.contiguous(), dev) for i in (0, 1)]
-        self.eh_w = [_dev(w[f"energy_head.mlp.NN-{i}.weight"], dev) for i in (0, 1)]
-        self.eh_b = [_dev(w[f"energy_head.mlp.NN-{i}.bias"], dev) for i in (0, 1)]
-        # direct checkpoints carry a force head (and usually a stress head) and are evaluated by
-        # the forward alone (orb_calculator.py:66-72, 141-185)
-        self.is_direct = "forces_head.mlp.NN-0.weight" in w
-        self.has_stress_head = "stress_head.mlp.NN-0.weight" in w
+        eh, fh, sh = heads
+        self.eh_w_t, self.eh_w, self.eh_b = eh.w_t, eh.w, eh.b
+        self.is_direct = fh is not None
+        self.has_stress_head = sh is not None
         self.fh_w_t = self.fh_b = self.sh_w_t = self.sh_b = None
-        if self.is_direct:
-            self.fh_w_t = [_dev(w[f"forces_head.mlp.NN-{i}.weight"].T.contiguous(), dev)
-                           for i in (0, 1)]
-            self.fh_b = [_dev(w[f"forces_head.mlp.NN-{i}.bias"], dev) for i in (0, 1)]
-            if self.fh_w_t[1].shape[1] != 3:
-                raise RuntimeError("the force head must have 3 outputs")
-        if self.has_stress_head:
-            self.sh_w_t = [_dev(w[f"stress_head.mlp.NN-{i}.weight"].T.contiguous(), dev)
-                           for i in (0, 1)]
-            self.sh_b = [_dev(w[f"stress_head.mlp.NN-{i}.bias"], dev) for i in (0, 1)]
-            if self.sh_w_t[1].shape[1] != 6:
-                raise RuntimeError("the stress head must have 6 outputs")
-        self.has_cond = "conditioner.charge_embedding.W" in w
-        self.host_w = {k: v for k, v in w.items() if k.startswith(("energy_head.normalizer",
-                                                                   "energy_head.reference",
-                                                                   "forces_head.normalizer",
-                                                                   "stress_head.diag_normalizer",
-                                                                   "stress_head.offdiag_normalizer",
-                                                                   "conditioner."))}
+        if fh is not None:
+            self.fh_w_t, self.fh_b = fh.w_t, fh.b
+        if sh is not None:
+            self.sh_w_t, self.sh_b = sh.w_t, sh.b
+        self.host_w = dict(host_w)
+        self.has_cond = "conditioner.charge_embedding.W" in self.host_w
+
+    @classmethod
+    def from_parts(cls, enc, layers, heads, *, cfg, device, precision, host_w=None,
+                   node_emb=None):
+        """A model over already-built device weights (the module objects of tt_atom.orb_model):
+        ``enc`` = (node MLPNorm, edge MLPNorm), ``layers`` = interaction-layer weights,
+        ``heads`` = (energy head, force head or None, stress head or None)."""
+        self = cls.__new__(cls)
+        self.precision = precision
+        self.cfg = dict(cfg)
+        self.device = torch.device(device)
+        self.C = int(cfg["latent_dim"])
+        self.nb = int(cfg["num_bases"])
+        self.r_max = float(cfg["cutoff"])
+        if self.nb < 1 or self.nb > 64 or self.nb & (self.nb - 1):
+            raise RuntimeError("num_bases must be a power of two <= 64")
+        self.node_emb = node_emb
+        self._finish(enc, layers, heads, host_w or {})
+        return self
 
     def charge_spin_embedding_batch(self, charges, spins, natoms):
         """charge_spin_embedding of K systems at once, one row per node [sum natoms, C]."""
@@ -353,7 +370,7 @@ class OrbEngine:
     checkpoint the step is the forward and the force / stress heads; otherwise the forward and
     the analytic backward."""
 
-    def __init__(self, model, graph, cond_nodes=None, use_graph=True):
+    def __init__(self, model, graph, cond_nodes=None, use_graph=True, node_feat=None):
         self.m, self.g = model, graph
         dev = model.device
         N, E, K, C, H = graph.N, graph.E, graph.K, model.C, model.H
@@ -362,7 +379,15 @@ class OrbEngine:
         self.use_graph = use_graph
         self._graphs = StepGraphs(self._step)
         self.pos = f(N, 3)
-        self.x_node = _dev(model.node_emb[graph.Z.cpu()], dev)
+        if node_feat is None:
+            if model.node_emb is None:
+                raise ValueError("node_feat is required for a model built without the atom "
+                                 "embedding table")
+            node_feat = model.node_emb[graph.Z.cpu()]
+        if tuple(node_feat.shape) != (N, model.enc_node.w_t[0].shape[0]):
+            raise ValueError(f"node_feat must be [{N}, {model.enc_node.w_t[0].shape[0]}], got "
+                             f"{tuple(node_feat.shape)}")
+        self.x_node = _dev(node_feat, dev)
         self.cond = None if cond_nodes is None else _dev(cond_nodes, dev)
         He = model.eh_w_t[0].shape[1]
         L = len(model.layers)

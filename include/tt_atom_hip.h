@@ -160,6 +160,40 @@ int tta_silu_bwd(const float* g, const float* x, float* out, int64_t n, tta_stre
 int tta_sum(const float* x, int64_t n, int64_t stride, float* out, tta_stream_t stream);
 int tta_fill(float* out, int64_t n, float value, tta_stream_t stream);
 
+/* ---------------------------------------------------------------- fused node-level stages
+ * (csrc/node.hip; C and H multiples of 16 in [16, 128], lmax = 2).
+ * One block's node-level tail: x2 = x1 + SpectralAtomwise(RMSNormSH_2(x1)) (model.py:158-172 with
+ * norm.py:93-111 and spectral.py:146-188), saving inv2 [N], a_s [N, 2H] (pre-SiLU scalar MLP) and
+ * h [N, 9, H] (pre-gate) for the backward; with awn != NULL also the next RMSNormSH of x2 (the
+ * next block's norm_1 plus add0 [N, C] on coefficient 0, or the final norm with add0 = NULL)
+ * into yn / invn.  ws_t [C, 2H]; w1t [3, C, H], w2t [3, H, C] per degree ([in, out]); b1 [H],
+ * b2 [C] the l = 0 biases.  Replaces RMSNormSH + the spectral FF's ttnn chain + the residual add
+ * + the next RMSNormSH (6 launches). */
+int tta_spectral_block_fwd(const float* x1, const float* aw2, const float* ab2, const float* ws_t,
+                           const float* bs, const float* w1t, const float* b1, const float* w2t,
+                           const float* b2, float* inv2, float* a_s, float* h, float* x2,
+                           const float* awn, const float* abn, const float* add0, float* yn,
+                           float* invn, int64_t N, int64_t C, int64_t H, float eps,
+                           tta_stream_t stream);
+/* Its reverse (forces.py:49-98 rmsnorm_bw, 258-346 spectral_bw): g_x2 = RMSNormSH_bw(g_n; x2,
+ * awn, invn) + res (res may be NULL), then g_x1 = RMSNormSH_2_bw(SpectralAtomwise_bw(g_x2)) +
+ * g_x2.  w1 [3, H, C], w2 [3, C, H] per degree ([out, in]); ws [2H, C]. */
+int tta_spectral_block_bwd(const float* g_n, const float* x2, const float* awn,
+                           const float* invn, const float* res, const float* x1,
+                           const float* aw2, const float* inv2, const float* a_s, const float* h,
+                           const float* w1, const float* w2, const float* ws, float* g_x1,
+                           int64_t N, int64_t C, int64_t H, tta_stream_t stream);
+/* Per-node energy MLP on coefficient 0 of ne [N, 9, C] (model.py:223-231): a1 = ne0 w0t + b0,
+ * a2 = silu(a1) w1t + b1, node_e = silu(a2) . w2 + b2 (w2 [H]); a1 / a2 [N, H] saved. */
+int tta_energy_head_fwd(const float* ne, const float* w0t, const float* b0, const float* w1t,
+                        const float* b1, const float* w2, const float* b2, float* a1, float* a2,
+                        float* node_e, int64_t N, int64_t C, int64_t H, tta_stream_t stream);
+/* Its adjoint for dE/dnode_e = 1 (forces.py:438-461): g_ne [N, 9, C] (coefficients 1..8 zero);
+ * w0 [H, C], w1 [H, H] ([out, in]). */
+int tta_energy_head_bwd(const float* a1, const float* a2, const float* w0, const float* w1,
+                        const float* w2, float* g_ne, int64_t N, int64_t C, int64_t H,
+                        tta_stream_t stream);
+
 /* ---------------------------------------------------------------- geometry
  * ev = pos[src] - pos[tgt] (+ shift), dist = |ev|, coef = packed Wigner-D (geometry.py:209-224
  * + 234-240, gauge gamma; jd = [Jd_0 | Jd_1 | Jd_2] 35 floats). */

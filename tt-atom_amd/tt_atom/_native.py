@@ -57,6 +57,10 @@ _SIGS = {
     "tta_node_forces": [_P, _P, _P, _P, _P, _I64, _I64, _P],
     "tta_virial": [_P, _P, _I64, _P, _P, _P],
     "tta_virial_noalloc": [_P, _P, _I64, _P, _P],
+    "tta_spectral_block_fwd": [_P] * 18 + [_I64, _I64, _I64, _F, _P],
+    "tta_spectral_block_bwd": [_P] * 14 + [_I64, _I64, _I64, _P],
+    "tta_energy_head_fwd": [_P] * 10 + [_I64, _I64, _I64, _P],
+    "tta_energy_head_bwd": [_P] * 6 + [_I64, _I64, _I64, _P],
     "tta_gemm_f32_gather": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64,
                             _P, _P, _I64, _I64, _I, _P],
     "tta_orb_edge_features": [_P, _P, _P, _P, _F, _I64, _P, _P, _P, _I64, _I64, _P],
@@ -608,6 +612,66 @@ def virial_noalloc(ev, g_ev, out):
     E = ev.shape[0]
     _call("tta_virial_noalloc", _ptr(ev, numel=E * 3), _ptr(g_ev, numel=E * 3), E,
           _ptr(out, numel=9), _stream())
+
+
+# ----------------------------------------------------------------------------- fused node stages
+def node_fusable(C, H):
+    """The fused node-level kernels take C and H multiples of 16 up to 128."""
+    return C % 16 == 0 and H % 16 == 0 and 16 <= C <= 128 and 16 <= H <= 128
+
+
+def spectral_block_fwd(x1, norm2, ff, inv2, a_s, h, x2, next_norm=None, add0=None, yn=None,
+                       invn=None, eps=1e-5):
+    """x2 = x1 + spectral FF of RMSNormSH_2(x1); with ``next_norm`` also yn = RMSNormSH_next(x2)
+    (+ add0 on coefficient 0).  ``norm2`` / ``next_norm``: (aw [3, C], ab [C]); ``ff``: the
+    per-degree weights (ws_t, bs, w1t, b1, w2t, b2)."""
+    N, _, C = x1.shape
+    H = ff[2].shape[2]
+    nx = N * 9 * C
+    awn, abn = next_norm if next_norm is not None else (None, None)
+    _call("tta_spectral_block_fwd", _ptr(x1, numel=nx, name="x1"), _ptr(norm2[0], numel=3 * C),
+          _ptr(norm2[1], numel=C), _ptr(ff[0], numel=C * 2 * H), _ptr(ff[1], numel=2 * H),
+          _ptr(ff[2], numel=3 * C * H), _ptr(ff[3], numel=H), _ptr(ff[4], numel=3 * H * C),
+          _ptr(ff[5], numel=C), _ptr(inv2, numel=N), _ptr(a_s, numel=N * 2 * H),
+          _ptr(h, numel=N * 9 * H), _ptr(x2, numel=nx, name="x2"),
+          None if awn is None else _ptr(awn, numel=3 * C),
+          None if abn is None else _ptr(abn, numel=C),
+          None if add0 is None else _ptr(add0, numel=N * C, name="add0"),
+          None if yn is None else _ptr(yn, numel=nx, name="yn"),
+          None if invn is None else _ptr(invn, numel=N), N, C, H, float(eps), _stream())
+
+
+def spectral_block_bwd(g_n, x2, next_norm_w, invn, res, x1, aw2, inv2, a_s, h, ffb, g_x1):
+    """g_x1 of one block's node-level tail from the adjoint g_n of the next norm's output;
+    ``ffb``: the per-degree backward weights (w1 [3, H, C], w2 [3, C, H], ws [2H, C])."""
+    N, _, C = x1.shape
+    H = ffb[0].shape[1]
+    nx = N * 9 * C
+    _call("tta_spectral_block_bwd", _ptr(g_n, numel=nx, name="g_n"), _ptr(x2, numel=nx, name="x2"),
+          _ptr(next_norm_w, numel=3 * C), _ptr(invn, numel=N),
+          None if res is None else _ptr(res, numel=nx, name="res"), _ptr(x1, numel=nx, name="x1"),
+          _ptr(aw2, numel=3 * C), _ptr(inv2, numel=N), _ptr(a_s, numel=N * 2 * H),
+          _ptr(h, numel=N * 9 * H), _ptr(ffb[0], numel=3 * H * C), _ptr(ffb[1], numel=3 * C * H),
+          _ptr(ffb[2], numel=2 * H * C), _ptr(g_x1, numel=nx, name="g_x1"), N, C, H, _stream())
+
+
+def energy_head_fwd(ne, w_t, b, a1, a2, node_e):
+    """Per-node energy MLP on coefficient 0 of ne [N, 9, C]: w_t = (w0t [C, H], w1t [H, H],
+    w2 [H]), b = (b0, b1, b2)."""
+    N, _, C = ne.shape
+    H = w_t[0].shape[1]
+    _call("tta_energy_head_fwd", _ptr(ne, numel=N * 9 * C, name="ne"), _ptr(w_t[0], numel=C * H),
+          _ptr(b[0], numel=H), _ptr(w_t[1], numel=H * H), _ptr(b[1], numel=H),
+          _ptr(w_t[2], numel=H), _ptr(b[2], numel=1), _ptr(a1, numel=N * H),
+          _ptr(a2, numel=N * H), _ptr(node_e, numel=N), N, C, H, _stream())
+
+
+def energy_head_bwd(a1, a2, w0, w1, w2, g_ne):
+    N, H = a1.shape
+    C = w0.shape[1]
+    _call("tta_energy_head_bwd", _ptr(a1, numel=N * H), _ptr(a2, numel=N * H),
+          _ptr(w0, numel=H * C), _ptr(w1, numel=H * H), _ptr(w2, numel=H),
+          _ptr(g_ne, numel=N * 9 * C, name="g_ne"), N, C, H, _stream())
 
 
 # ----------------------------------------------------------------------------- neighbour list

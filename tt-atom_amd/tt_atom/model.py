@@ -138,6 +138,22 @@ class SpectralWeights:
         b2 = torch.zeros(NSPH, C)
         b2[0] = w[f"{prefix}.so3_linear_2.bias"]
         self.b1, self.b2 = _dev(b1, device), _dev(b2, device)
+        # per-degree forms for the fused node kernels: [in, out] forward, [out, in] backward
+        W1, W2 = w[f"{prefix}.so3_linear_1.weight"], w[f"{prefix}.so3_linear_2.weight"]
+        self.w1t_deg = _dev(W1.transpose(1, 2).contiguous(), device)     # [3, C, H]
+        self.w2t_deg = _dev(W2.transpose(1, 2).contiguous(), device)     # [3, H, C]
+        self.w1_deg = _dev(W1.contiguous(), device)                      # [3, H, C]
+        self.w2_deg = _dev(W2.contiguous(), device)                      # [3, C, H]
+        self.b1_l0 = _dev(w[f"{prefix}.so3_linear_1.bias"], device)
+        self.b2_l0 = _dev(w[f"{prefix}.so3_linear_2.bias"], device)
+
+    @property
+    def fused_fwd(self):
+        return (self.ws_t, self.bs, self.w1t_deg, self.b1_l0, self.w2t_deg, self.b2_l0)
+
+    @property
+    def fused_bwd(self):
+        return (self.w1_deg, self.w2_deg, self.ws)
 
 
 class GridWeights:

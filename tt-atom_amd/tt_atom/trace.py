@@ -122,6 +122,11 @@ class TracedEngine:
         self.gs_a = emp(N, L * H)
         P = max([b.atom_wise.npts for b in bb.blocks if b.ff_type != "spectral"], default=0)
         self.gt1, self.gt2 = emp(N * P, C), emp(N * P, C)
+        # uma-s-1 form (spectral FF in every block): each block's node-level tail -- RMSNormSH_2,
+        # the spectral FF, the residual add and the next RMSNormSH -- and the energy head run as
+        # single fused kernels, forward and backward
+        self.fused = (len(bb.blocks) > 0 and all(b.ff_type == "spectral" for b in bb.blocks)
+                      and nat.node_fusable(C, H))
 
     def _radial_cache(self, E, n_out, dev, r):
         c = _Buf()
@@ -225,7 +230,8 @@ class TracedEngine:
         Cin = 2 * C
         for i, (bw, c) in enumerate(zip(bb.blocks, self.blk)):
             s1w, s2w = bw.so2_1, bw.so2_2
-            nat.rmsnorm_sh_fwd(c.x_in, bw.norm_1.aw, bw.norm_1.ab, self.sys_emb, c.n1, c.inv1)
+            if not self.fused or i == 0:       # fused: produced by the previous block's tail
+                nat.rmsnorm_sh_fwd(c.x_in, bw.norm_1.aw, bw.norm_1.ab, self.sys_emb, c.n1, c.inv1)
             nat.gather_rotate(c.n1, g.src, g.tgt, self.coef, c.rad.out, self.xf)
             xf = self.xf.view(E, NSPH * Cin)
             o1 = c.o1c
@@ -242,12 +248,28 @@ class TracedEngine:
                               (y[:, 7 * H:], s2w.w2, None, ms[:, 7 * C:])])
             nat.rotate_env_segsum(c.mso2, self.coef, self.env, g.tgt_ptr, c.x_in, c.x1, n_in=9,
                                   env_first=True)
-            nat.rmsnorm_sh_fwd(c.x1, bw.norm_2.aw, bw.norm_2.ab, None, c.n2, c.inv2)
             x_out = self.blk[i + 1].x_in if i + 1 < len(self.blk) else self.x_final
+            if self.fused:
+                if i + 1 < len(self.blk):
+                    nb, nc = bb.blocks[i + 1], self.blk[i + 1]
+                    nxt = dict(next_norm=(nb.norm_1.aw, nb.norm_1.ab), add0=self.sys_emb,
+                               yn=nc.n1, invn=nc.inv1)
+                else:
+                    nxt = dict(next_norm=(bb.final_norm.aw, bb.final_norm.ab), yn=self.ne,
+                               invn=self.inv_f)
+                nat.spectral_block_fwd(c.x1, (bw.norm_2.aw, bw.norm_2.ab),
+                                       bw.atom_wise.fused_fwd, c.inv2, c.a_s, c.h, x_out, **nxt)
+                continue
+            nat.rmsnorm_sh_fwd(c.x1, bw.norm_2.aw, bw.norm_2.ab, None, c.n2, c.inv2)
             if bw.ff_type == "spectral":
                 self._spectral_fwd(bw.atom_wise, c, c.n2, c.x1, x_out)
             else:
                 self._grid_fwd(bw.atom_wise, c, c.n2, c.x1, x_out)
+        if self.fused:
+            nat.energy_head_fwd(self.ne, (bb.eh_w_t[0], bb.eh_w_t[1], bb.eh_w[2]), bb.eh_b,
+                                self.eh_a1, self.eh_a2, self.node_e.view(N))
+            nat.reduce_sum(self.node_e, N, 1, self.energy_buf)
+            return
         nat.rmsnorm_sh_fwd(self.x_final, bb.final_norm.aw, bb.final_norm.ab, None, self.ne,
                            self.inv_f)
         ne2 = self.ne.view(N, NSPH * C)
@@ -260,12 +282,12 @@ class TracedEngine:
 
     # ------------------------------------------------------------------ reverse
     def _backward(self):
-        bb, g = self.bb, self.g
-        E, N, C, H, L = self.E, self.N, self.C, self.H, self.L
-        LH, LHc = L * H, self.LHc
-        Cin = 2 * C
+        bb, N, C = self.bb, self.N, self.C
         nat.fill(self.g_coef, 0.0)
         nat.fill(self.g_env, 0.0)
+        if self.fused:
+            self._backward_fused()
+            return
         # energy head (forces.py:438-461): dE/dnode_e = 1
         nat.linear(self.ones, bb.eh_w[2], out=self.g_eh2, epilogue=nat.EPI_SILU_GRAD, aux=self.eh_a2)
         nat.linear(self.g_eh2, bb.eh_w[1], out=self.g_eh1, epilogue=nat.EPI_SILU_GRAD, aux=self.eh_a1)
@@ -274,7 +296,6 @@ class TracedEngine:
         gcur = self.gn_b
         nat.rmsnorm_sh_bwd(self.gn_a, self.x_final, bb.final_norm.aw, self.inv_f, None, gcur)
         for bw, c in zip(reversed(bb.blocks), reversed(self.blk)):
-            s1w, s2w = bw.so2_1, bw.so2_2
             # x2 = ff(norm2(x1)) + x1
             g_n2 = self.gn_a
             if bw.ff_type == "spectral":
@@ -284,28 +305,68 @@ class TracedEngine:
             g_x1 = self.gn_c
             nat.rmsnorm_sh_bwd(g_n2, c.x1, bw.norm_2.aw, c.inv2, gcur, g_x1)
             # x1 = edgewise(norm1(x_in)) + x_in
-            nat.rotate_env_segsum_bw(g_x1, g.tgt, c.mso2, self.coef, self.env, self.g_mso2,
-                                     self.g_coef, self.g_env, n_in=9, env_first=True)
-            gm = self.g_mso2.view(E, NSPH * C)
-            gy = self.g_y.view(E, NSPH * H)
-            nat.linear_group([(gm[:, :3 * C], s2w.wm0, None, gy[:, :3 * H]),
-                              (gm[:, 3 * C:7 * C], s2w.w1_t, None, gy[:, 3 * H:7 * H]),
-                              (gm[:, 7 * C:], s2w.w2_t, None, gy[:, 7 * H:])])
-            o1, g1 = c.o1c, self.g1c
-            nat.gate_bwd(self.g_y, o1[:, LH:], o1, g1[:, LH:], g1, bb.gate_idx_mprime, R=E, H=H,
-                         L=L, ldx=LHc, ldg=LHc)
-            gx = self.g_xf.view(E, NSPH * Cin)
-            nat.linear_group([(g1[:, :LH + 3 * H], s1w.wm0, None, gx[:, :3 * Cin]),
-                              (g1[:, LH + 3 * H:LH + 7 * H], s1w.w1_t, None,
-                               gx[:, 3 * Cin:7 * Cin]),
-                              (g1[:, LH + 7 * H:], s1w.w2_t, None, gx[:, 7 * Cin:])])
-            nat.gather_rotate_bw(self.g_xf, c.rad.out, c.n1, g.src, g.tgt, self.coef,
-                                 c.rad.g_out, self.g_mcat, self.g_coef)
             g_n1 = self.gn_a
-            nat.node_gather_sum(self.g_mcat, g.src_ptr, g.src_perm, g.tgt_ptr, None, g_n1)
+            self._edgewise_bwd(bw, c, g_x1, g_n1)
             g_in = self.gn_b
             nat.rmsnorm_sh_bwd(g_n1, c.x_in, bw.norm_1.aw, c.inv1, g_x1, g_in)
             gcur = g_in
+        self._backward_tail(gcur)
+
+    def _edgewise_bwd(self, bw, c, g_x1, g_n1):
+        """The edgewise block's reverse from the adjoint g_x1 of its output (the residual's
+        share excluded) to the adjoint g_n1 of its normalised input (forces.py:352-418)."""
+        g = self.g
+        E, C, H, L = self.E, self.C, self.H, self.L
+        LH, LHc, Cin = L * H, self.LHc, 2 * C
+        s1w, s2w = bw.so2_1, bw.so2_2
+        nat.rotate_env_segsum_bw(g_x1, g.tgt, c.mso2, self.coef, self.env, self.g_mso2,
+                                 self.g_coef, self.g_env, n_in=9, env_first=True)
+        gm = self.g_mso2.view(E, NSPH * C)
+        gy = self.g_y.view(E, NSPH * H)
+        nat.linear_group([(gm[:, :3 * C], s2w.wm0, None, gy[:, :3 * H]),
+                          (gm[:, 3 * C:7 * C], s2w.w1_t, None, gy[:, 3 * H:7 * H]),
+                          (gm[:, 7 * C:], s2w.w2_t, None, gy[:, 7 * H:])])
+        o1, g1 = c.o1c, self.g1c
+        nat.gate_bwd(self.g_y, o1[:, LH:], o1, g1[:, LH:], g1, self.bb.gate_idx_mprime, R=E, H=H,
+                     L=L, ldx=LHc, ldg=LHc)
+        gx = self.g_xf.view(E, NSPH * Cin)
+        nat.linear_group([(g1[:, :LH + 3 * H], s1w.wm0, None, gx[:, :3 * Cin]),
+                          (g1[:, LH + 3 * H:LH + 7 * H], s1w.w1_t, None, gx[:, 3 * Cin:7 * Cin]),
+                          (g1[:, LH + 7 * H:], s1w.w2_t, None, gx[:, 7 * Cin:])])
+        nat.gather_rotate_bw(self.g_xf, c.rad.out, c.n1, g.src, g.tgt, self.coef, c.rad.g_out,
+                             self.g_mcat, self.g_coef)
+        nat.node_gather_sum(self.g_mcat, g.src_ptr, g.src_perm, g.tgt_ptr, None, g_n1)
+
+    def _backward_fused(self):
+        """Reverse of the fused forward: the energy head's adjoint, then per block (last first) the
+        fused node-level tail (the next norm's backward + the residual adjoint, the spectral FF
+        and norm_2 backward) and the edgewise reverse; block 0's norm_1 last."""
+        bb, N = self.bb, self.N
+        g_n = self.gn_a
+        nat.energy_head_bwd(self.eh_a1, self.eh_a2, bb.eh_w[0], bb.eh_w[1], bb.eh_w[2], g_n)
+        res = None
+        spare = [self.gn_b, self.gn_c]
+        nblk = len(bb.blocks)
+        for i in reversed(range(nblk)):
+            bw, c = bb.blocks[i], self.blk[i]
+            if i + 1 < nblk:
+                x2, awn, invn = self.blk[i + 1].x_in, bb.blocks[i + 1].norm_1.aw, self.blk[i + 1].inv1
+            else:
+                x2, awn, invn = self.x_final, bb.final_norm.aw, self.inv_f
+            g_x1 = spare[0] if res is not spare[0] else spare[1]
+            nat.spectral_block_bwd(g_n, x2, awn, invn, res, c.x1, bw.norm_2.aw, c.inv2, c.a_s,
+                                   c.h, bw.atom_wise.fused_bwd, g_x1)
+            self._edgewise_bwd(bw, c, g_x1, g_n)          # g_n <- adjoint of this block's n1
+            res = g_x1
+        c0, bw0 = self.blk[0], bb.blocks[0]
+        gcur = spare[0] if res is not spare[0] else spare[1]
+        nat.rmsnorm_sh_bwd(g_n, c0.x_in, bw0.norm_1.aw, c0.inv1, res, gcur)
+        self._backward_tail(gcur)
+
+    def _backward_tail(self, gcur):
+        """Edge-degree init backward, the radial MLPs' backward and the geometry VJP to forces,
+        from the adjoint gcur of block 0's input."""
+        bb, g = self.bb, self.g
         # edge-degree init backward (edge_degree.py:69-93)
         nat.rotate_env_segsum_bw(gcur, g.tgt, self.ed.out, self.coef, self.env, self.ed.g_out,
                                  self.g_coef, self.g_env, n_in=3, env_first=False,

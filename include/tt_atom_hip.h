@@ -158,6 +158,9 @@ int tta_rmsnorm_sh_bwd(const float* g, const float* x, const float* aw, const fl
 int tta_silu_bwd(const float* g, const float* x, float* out, int64_t n, tta_stream_t stream);
 /* Deterministic single-block sum of x[0], x[stride], ... (model.py:233-235 energy sum). */
 int tta_sum(const float* x, int64_t n, int64_t stride, float* out, tta_stream_t stream);
+/* out[k] = sum of x[ptr[k] .. ptr[k+1]) for k < K, each in tta_sum's order: the per-system energies
+ * of a disjoint batch (model.py:241-247 energy_batch's segment sum) in one launch. */
+int tta_segment_sum(const float* x, const int* ptr, int64_t K, float* out, tta_stream_t stream);
 int tta_fill(float* out, int64_t n, float value, tta_stream_t stream);
 
 /* ---------------------------------------------------------------- fused node-level stages

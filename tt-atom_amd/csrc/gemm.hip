@@ -22,14 +22,15 @@ namespace {
 
 using namespace tta_gemm;
 
-constexpr int BK = 16, PAD = 4;
+constexpr int PAD = 4;
 
 // Block tile BM x BN x BK with 4 waves in a WGM x WGN grid; each wave owns (BM/WGM) x (BN/WGN)
 // = TI x TJ MFMA tiles of 16 x 16.  Loads stage A k-major (the 16 lanes sharing a k read 16
 // consecutive rows) and B row-major in LDS; per-thread register prefetch of the next k-slab and
 // two LDS buffers give one barrier per k-step.
-template <int BM, int BN, int WGM, int WGN>
+template <int BM, int BN, int WGM, int WGN, int BK_>
 struct Tile {
+  static constexpr int BK = BK_;
   static constexpr int TI = BM / WGM / 16;
   static constexpr int TJ = BN / WGN / 16;
   static constexpr int A_VEC = BM * BK / 4;   // float4 loads of the A slab
@@ -46,8 +47,8 @@ __device__ __forceinline__ void load_a(const GemmArgs& p, const float* A, int m0
 #pragma unroll
   for (int h = 0; h < TL::A_PER_T; ++h) {
     const int i = t + 256 * h;
-    const int row = m0 + i / (BK / 4);
-    const int k = k0 + (i % (BK / 4)) * 4;
+    const int row = m0 + i / (TL::BK / 4);
+    const int k = k0 + (i % (TL::BK / 4)) * 4;
     const bool in = i < TL::A_VEC && row < p.M;
     if (VEC) {
       floatx4 v = {0.f, 0.f, 0.f, 0.f};
@@ -91,8 +92,8 @@ __device__ __forceinline__ void store_a(float (*As)[BM + PAD], int t,
   for (int h = 0; h < TL::A_PER_T; ++h) {
     const int i = t + 256 * h;
     if (i >= TL::A_VEC) continue;
-    const int r = i / (BK / 4);
-    const int kq = (i % (BK / 4)) * 4;
+    const int r = i / (TL::BK / 4);
+    const int kq = (i % (TL::BK / 4)) * 4;
 #pragma unroll
     for (int c = 0; c < 4; ++c) As[kq + c][r] = ra[4 * h + c];
   }
@@ -116,11 +117,11 @@ __device__ __forceinline__ void store_b(float (*Bs)[BN + PAD], int t,
 // symbol per tile shape; it runs once per output element and costs nothing next to the K loop.
 // GROUP: blockIdx.z selects the product of g (batch 1 each); otherwise g.p[0] is one strided
 // batch and blockIdx.z its batch index.
-template <int BM, int BN, int WGM, int WGN, bool VEC, bool GROUP>
+template <int BM, int BN, int WGM, int WGN, int BK, bool VEC, bool GROUP>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmGroup g) {
   const GemmArgs& p = g.p[GROUP ? blockIdx.z : 0];
   const int64_t bz = GROUP ? 0 : blockIdx.z;
-  typedef Tile<BM, BN, WGM, WGN> TL;
+  typedef Tile<BM, BN, WGM, WGN, BK> TL;
   constexpr int TI = TL::TI, TJ = TL::TJ;
   __shared__ float As[2][BK][BM + PAD];
   __shared__ float Bs[2][BK][BN + PAD];
@@ -193,7 +194,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmGroup g) {
 }
 
 // n products (group) or one product with `batch` strided copies (n == 1, group false).
-template <int BM, int BN, int WGM, int WGN>
+template <int BM, int BN, int WGM, int WGN, int BK>
 int launch(const GemmGroup& g, int n, bool group, int64_t batch, bool vec, hipStream_t s) {
   int64_t gx = 0;
   for (int i = 0; i < n; ++i) {
@@ -208,17 +209,17 @@ int launch(const GemmGroup& g, int n, bool group, int64_t batch, bool vec, hipSt
   const dim3 grid((unsigned)gx, 1, (unsigned)(group ? n : batch));
   if (group) {
     if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, true, true>), grid, dim3(256), 0, s,
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, BK, true, true>), grid, dim3(256), 0, s,
                          g);
     else
-      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, false, true>), grid, dim3(256), 0, s,
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, BK, false, true>), grid, dim3(256), 0, s,
                          g);
   } else {
     if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, true, false>), grid, dim3(256), 0, s,
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, BK, true, false>), grid, dim3(256), 0, s,
                          g);
     else
-      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, false, false>), grid, dim3(256), 0,
+      hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, WGM, WGN, BK, false, false>), grid, dim3(256), 0,
                          s, g);
   }
   TTA_CHECK_LAUNCH("tta_gemm_f32");
@@ -227,16 +228,18 @@ int launch(const GemmGroup& g, int n, bool group, int64_t batch, bool vec, hipSt
 
 // Tile shape per call: 128 x 128 when the grid already fills the chip (>= 960 blocks, about four
 // resident blocks per CU), 64 x 128 for mid-size grids, 32 x 64 for the small node-level GEMMs
-// (counted over every product of a group).
+// (counted over every product of a group).  The small tiles take 64-deep k steps: a grid that
+// small is bound by the latency of its sequence of k steps (each waits out one round of loads),
+// so a quarter of the steps, each with four times the matrix work, finishes sooner.
 int dispatch(const GemmGroup& g, int n, bool group, int64_t batch, bool vec, hipStream_t s) {
   int64_t big = 0, mid = 0;
   for (int i = 0; i < n; ++i) {
     big += (int64_t)tta_blocks(g.p[i].M, 128) * tta_blocks(g.p[i].N, 128) * batch;
     mid += (int64_t)tta_blocks(g.p[i].M, 64) * tta_blocks(g.p[i].N, 128) * batch;
   }
-  if (big >= 960) return launch<128, 128, 2, 2>(g, n, group, batch, vec, s);
-  if (mid >= 512) return launch<64, 128, 2, 2>(g, n, group, batch, vec, s);
-  return launch<32, 64, 2, 2>(g, n, group, batch, vec, s);
+  if (big >= 960) return launch<128, 128, 2, 2, 16>(g, n, group, batch, vec, s);
+  if (mid >= 512) return launch<64, 128, 2, 2, 16>(g, n, group, batch, vec, s);
+  return launch<32, 64, 2, 2, 64>(g, n, group, batch, vec, s);
 }
 
 }  // namespace

@@ -62,26 +62,38 @@ __global__ __launch_bounds__(256) void k_edge_features(
   if (k == 0) env[e] = tta_geo::envelope(d, cutoff);
 }
 
-// g_ev[e] = VJP of (coef, gaussians, envelope, |ev|) at the given adjoints.
+// g_ev[e] = VJP of (coef, gaussians, envelope, |ev|) at the given adjoints.  Four lanes per
+// edge: the gaussian sum (nb terms, the edge's adjoint row read by consecutive lanes) is split
+// over the four and reduced across them in a fixed order; each of the four then evaluates the
+// Wigner part of the VJP in full (identical work, so no divergence) and the first lane stores.
+// Compared with one thread per edge this spreads the nb-long sum of small graphs over four
+// times the threads and makes its row reads contiguous.
+constexpr int kGeoLanes = 4;
+
 __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
     const float* __restrict__ ev, const float* __restrict__ dist,
     const float* __restrict__ g_coef, const float* __restrict__ g_env,
     const float* __restrict__ g_gauss, int64_t ldg, const float* __restrict__ off, float coeff,
     float cutoff, int nb, const float* __restrict__ jd, float gamma, float* __restrict__ g_ev,
     int E) {
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= E) return;
-  float v[3] = {ev[(int64_t)e * 3], ev[(int64_t)e * 3 + 1], ev[(int64_t)e * 3 + 2]};
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int sub = threadIdx.x & (kGeoLanes - 1);
+  const int64_t e0 = gid / kGeoLanes;
+  const bool valid = e0 < E;
+  const int64_t e = valid ? e0 : E - 1;  // lanes past the end mirror the last edge (no store)
+  float v[3] = {ev[e * 3], ev[e * 3 + 1], ev[e * 3 + 2]};
   const float d = dist[e];
   float gd = 0.f;
   if (g_gauss) {
-    const float* gg = g_gauss + (int64_t)e * ldg;
-    for (int k = 0; k < nb; ++k) {
+    const float* gg = g_gauss + e * ldg;
+    for (int k = sub; k < nb; k += kGeoLanes) {
       const float t = d - off[k];
       const float gk = expf(coeff * (t * t));
       gd += gg[k] * (gk * (coeff * (2.f * t)));
     }
   }
+  gd += __shfl_xor(gd, 2, 64);
+  gd += __shfl_xor(gd, 1, 64);
   if (g_env) gd += g_env[e] * tta_geo::envelope_grad(d, cutoff);
   float out[3] = {0.f, 0.f, 0.f};
   if (d > 0.f)
@@ -89,10 +101,11 @@ __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
   if (g_coef) {
     float jl[35], gc[35];
     for (int k = 0; k < 35; ++k) jl[k] = jd[k];
-    for (int k = 0; k < 35; ++k) gc[k] = g_coef[(int64_t)e * 35 + k];
+    for (int k = 0; k < 35; ++k) gc[k] = g_coef[e * 35 + k];
     tta_geo::wigner_vjp(v, gamma, jl, gc, out);
   }
-  for (int k = 0; k < 3; ++k) g_ev[(int64_t)e * 3 + k] = out[k];
+  if (valid && sub == 0)
+    for (int k = 0; k < 3; ++k) g_ev[e * 3 + k] = out[k];
 }
 
 // F[n] = -(sum_{src(e) = n} g_ev[e] - sum_{tgt(e) = n} g_ev[e])   (ev = pos[src] - pos[tgt])
@@ -233,7 +246,8 @@ extern "C" int tta_edge_geometry_bwd(const float* ev, const float* dist, const f
   if (E == 0) return tta::kOk;
   TTA_CHECK_ARG(ev && dist && jd && g_ev, "tta_edge_geometry_bwd: null pointer");
   TTA_CHECK_ARG(!g_gauss || (offsets && ldg >= nb), "tta_edge_geometry_bwd: bad gaussian adjoint");
-  hipLaunchKernelGGL(k_edge_geometry_bwd, dim3(tta_blocks(E, 256)), dim3(256), 0, stream, ev, dist,
+  hipLaunchKernelGGL(k_edge_geometry_bwd, dim3(tta_blocks(E * kGeoLanes, 256)), dim3(256), 0,
+                     stream, ev, dist,
                      g_coef, g_env, g_gauss, ldg, offsets, coeff, cutoff, (int)nb, jd, gamma, g_ev,
                      (int)E);
   TTA_CHECK_LAUNCH("tta_edge_geometry_bwd");

@@ -377,6 +377,27 @@ __global__ __launch_bounds__(1024) void k_sum(const float* __restrict__ x, int64
   }
 }
 
+// Per-segment sums of x over the contiguous ranges [ptr[k], ptr[k+1]), one block per segment,
+// each with exactly k_sum's order (so a system's sum inside a batch equals its sum alone).
+__global__ __launch_bounds__(1024) void k_segment_sum(const float* __restrict__ x,
+                                                      const int* __restrict__ ptr,
+                                                      float* __restrict__ out) {
+  __shared__ float part[16];
+  const int k = blockIdx.x;
+  const float* xs = x + ptr[k];
+  const int64_t n = ptr[k + 1] - ptr[k];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) s += xs[i];
+  s = tta_group_sum(s, 64);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    float v = threadIdx.x < 16 ? part[threadIdx.x] : 0.f;
+    v = tta_group_sum(v, 64);
+    if (threadIdx.x == 0) out[k] = v;
+  }
+}
+
 // out[r, c] = value for all c in [0, n): used to seed the energy adjoint with ones.
 __global__ __launch_bounds__(256) void k_fill(float* __restrict__ out, int64_t n, float value) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -530,6 +551,16 @@ extern "C" int tta_sum(const float* x, int64_t n, int64_t stride, float* out,
   TTA_CHECK_ARG(out && (x || n == 0), "tta_sum: null pointer");
   hipLaunchKernelGGL(k_sum, dim3(1), dim3(1024), 0, stream, x, n, stride, out);
   TTA_CHECK_LAUNCH("tta_sum");
+  return tta::kOk;
+}
+
+extern "C" int tta_segment_sum(const float* x, const int* ptr, int64_t K, float* out,
+                               hipStream_t stream) {
+  TTA_CHECK_ARG(K >= 0 && K <= 0x7fffffff, "tta_segment_sum: bad segment count");
+  if (K == 0) return tta::kOk;
+  TTA_CHECK_ARG(x && ptr && out, "tta_segment_sum: null pointer");
+  hipLaunchKernelGGL(k_segment_sum, dim3((unsigned)K), dim3(1024), 0, stream, x, ptr, out);
+  TTA_CHECK_LAUNCH("tta_segment_sum");
   return tta::kOk;
 }
 

@@ -61,6 +61,7 @@ _SIGS = {
     "tta_spectral_block_bwd": [_P] * 14 + [_I64, _I64, _I64, _P],
     "tta_energy_head_fwd": [_P] * 10 + [_I64, _I64, _I64, _P],
     "tta_energy_head_bwd": [_P] * 6 + [_I64, _I64, _I64, _P],
+    "tta_segment_sum": [_P, _P, _I64, _P, _P],
     "tta_gemm_f32_gather": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64,
                             _P, _P, _I64, _I64, _I, _P],
     "tta_orb_edge_features": [_P, _P, _P, _P, _F, _I64, _P, _P, _P, _I64, _I64, _P],
@@ -560,6 +561,14 @@ def silu_bwd(g, x, out):
 
 def reduce_sum(x, n, stride, out):
     _call("tta_sum", x.data_ptr(), n, stride, _ptr(out, numel=1), _stream())
+
+
+def segment_sum(x, ptr, out):
+    """out[k] = sum of x over [ptr[k], ptr[k+1]) (x contiguous fp32, ptr int32 [K + 1])."""
+    K = out.numel()
+    n = x.numel()
+    _call("tta_segment_sum", _ptr(x, numel=n, name="x"), _i32(ptr, K + 1, "ptr"), K,
+          _ptr(out, numel=K), _stream())
 
 
 def fill(out, value):

@@ -402,13 +402,18 @@ class TracedEngine:
         """Raw energies of the systems of a disjoint batch (contiguous node ranges of sizes
         ``natoms``), each the same device sum over its nodes as a single system's energy
         (Backbone.energy_batch, model.py:241-247); call after ``run``."""
-        if sum(natoms) != self.N:
+        natoms = tuple(int(n) for n in natoms)
+        if sum(natoms) != self.N or min(natoms, default=1) < 0:
             raise ValueError("natoms do not add up to the node count")
+        ptr = getattr(self, "_seg_ptr", None)
+        if ptr is None or ptr[0] != natoms:
+            offs = [0]
+            for n in natoms:
+                offs.append(offs[-1] + n)
+            self._seg_ptr = ptr = (natoms, torch.tensor(offs, dtype=torch.int32,
+                                                        device=self.device))
         out = torch.empty(len(natoms), device=self.device, dtype=torch.float32)
-        off = 0
-        for k, n in enumerate(natoms):
-            nat.reduce_sum(self.node_e[off:off + n], n, 1, out[k:k + 1])
-            off += n
+        nat.segment_sum(self.node_e.view(-1), ptr[1], out)
         return out
 
     def __call__(self, pos, compute_stress=False):

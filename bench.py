@@ -391,6 +391,44 @@ def device_nl_ms(torch, fn, ref):
     return round(sorted(ts)[2], 3), same
 
 
+def run_neighbor_workload(args, torch):
+    """Device neighbour list, row scan against cell list (same graph, checked edge for edge): one
+    JSON line per system and cap with the median wall time of a whole radius_graph_device call
+    (host grid set-up, passes, edge-count read-back) over --steps calls after one warm-up."""
+    from tt_atom import geometry, synthetic
+    cases = [("cluster", synthetic.lattice_cluster(n, 2.2, 2), None, None)
+             for n in (2048, 8192, 16384, 52000, 200000)]
+    cases += [(name, *synthetic.shuffled_fcc(reps, 7), pbc)
+              for name, pbc in (("crystal", [True] * 3), ("slab", [True, True, False]))
+              for reps in (8, 24)]
+    for name, pos, cell, pbc in cases:
+        pos = torch.from_numpy(pos)
+        cell = None if cell is None else torch.from_numpy(cell)
+        for cap in (None, 30):
+            row = {"metric": "neighbor_list_ms", "system": name, "atoms": int(pos.shape[0]),
+                   "pbc": pbc, "cutoff": 6.0, "cap": cap, "data": "synthetic"}
+            out = {}
+            for method in ("rows", "cells"):
+                if method == "rows" and pos.shape[0] > 60000:
+                    continue                      # O(N^2): skipped at 200k atoms
+                fn = lambda: geometry.radius_graph_device(pos, 6.0, cell, pbc,
+                                                          max_neighbors=cap, method=method)
+                out[method] = fn()
+                ts = []
+                for _ in range(max(1, args.steps)):
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    fn()
+                    torch.cuda.synchronize()
+                    ts.append((time.perf_counter() - t0) * 1e3)
+                row[f"{method}_ms"] = round(sorted(ts)[len(ts) // 2], 3)
+            row["edges"] = int(out["cells"][0].shape[1])
+            if "rows" in out:
+                row["same"] = bool(torch.equal(out["rows"][0], out["cells"][0])
+                                   and torch.equal(out["rows"][1], out["cells"][1]))
+            print(json.dumps(row), flush=True)
+
+
 def cpu_baseline_c5(torch):
     """Orb CPU oracle on a bounded sample of C5: the first 32 molecules of the batch."""
     from oracle import orb as O
@@ -561,16 +599,40 @@ def summarize_counters(root, out_path):
     pathlib.Path(out_path).write_text("\n".join(lines + traffic) + "\n")
 
 
+def summarize_trace(trace_csv, out_path, pattern):
+    """Per-kernel, per-grid median durations of a rocprofv3 --kernel-trace CSV for the kernels
+    whose name matches ``pattern`` (rows: kernel, workgroups, dispatches, median us)."""
+    import csv
+    import re
+    groups = {}
+    with open(trace_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("void ", "")
+            name = re.sub(r"\(.*", "", name)
+            if not re.search(pattern, name):
+                continue
+            wgs = int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            groups.setdefault((name, wgs), []).append(us)
+    lines = [f"{'kernel':28s} {'workgroups':>10s} {'dispatches':>10s} {'median_us':>10s}"]
+    for (name, wgs), v in groups.items():
+        v.sort()
+        lines.append(f"{name:28s} {wgs:10d} {len(v):10d} {v[len(v) // 2]:10.2f}")
+    pathlib.Path(out_path).write_text("\n".join(lines) + "\n")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "batch"), default="c3",
+    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "batch", "neighbors"),
+                    default="c3",
                     help="c3 (headline), c2 (isolated edgewise kernel), c4 (periodic + stress), "
-                         "c5 (Orb-v3 batch) or batch (small-system evaluate_batch throughput "
-                         "against the reference's published numbers)")
+                         "c5 (Orb-v3 batch), batch (small-system evaluate_batch throughput "
+                         "against the reference's published numbers) or neighbors (device "
+                         "neighbour list: row scan against cell list, up to 200k atoms)")
     ap.add_argument("--precision", choices=("f32", "f32-bf16x6", "f32-mfma", "bf16"), default="f32",
                     help="GEMM arithmetic: f32 (scaled split-fp16, fp32-accurate), f32-bf16x6 "
                          "(split-bf16, fp32-accurate), f32-mfma, or bf16 operands (the bf16 "
@@ -587,7 +649,13 @@ def main():
                     help="only run a 256 MiB device copy (y = -x) for the HBM counter scale")
     ap.add_argument("--summarize-counters", nargs=2, metavar=("PMC_ROOT", "OUT"),
                     help="write the per-kernel counter summary of rocprofv3 --pmc runs (no GPU)")
+    ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "OUT", "REGEX"),
+                    help="write per-kernel, per-grid median durations of a rocprofv3 kernel "
+                         "trace for kernels matching REGEX (no GPU)")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(*args.summarize_trace)
+        return
     if args.summarize_counters:
         summarize_counters(*args.summarize_counters)
         return
@@ -611,6 +679,9 @@ def main():
     wl = args.workload
     if wl == "batch":
         run_batch_workload(args, torch)
+        return
+    if wl == "neighbors":
+        run_neighbor_workload(args, torch)
         return
     if wl == "c2":
         from tt_atom.edgewise import EdgewiseStep

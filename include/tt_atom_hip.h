@@ -335,6 +335,39 @@ int tta_radius_graph_write(const float* pos, int64_t N, const int* lo, const int
                            const int* thr_cell, const int64_t* offsets, int64_t* edge_src,
                            int64_t* edge_tgt, int* edge_cell, tta_stream_t stream);
 
+/* Cell-list neighbour list: the same edges, order, image cells and cap as the three passes above
+ * (and so as geometry.py:48-81 plus the cap) for one system, at O(N) cost.  Image points
+ * q = pos_j (+ shift_c) are binned on grid (bins of side 1 / inv_h >= cutoff plus a rounding
+ * margin, spanning the atoms' bounding box plus one bin on every side); every row scans the 27
+ * bins around its atom.  build: bin_start [nbins + 1] and the binned points [n_points, 4]
+ * (xyz = q, w = the int32 bits of id = j or j * n_cells + c), n_points = N (aperiodic) or
+ * N * n_cells (< 2^30), with tta_cell_list_workspace(nbins, n_points) ints of workspace.
+ * thresholds: as tta_radius_graph_thresholds (k in [1, 1024], any number of candidates per
+ * receiver); count / write: as tta_radius_graph_count / _write; write sets err[0] = 1 (caller
+ * zeroes it) and skips rows with more than 2048 kept entries, which the caller then writes with
+ * tta_radius_graph_write. */
+int64_t tta_cell_list_workspace(int64_t n_bins, int64_t n_points);
+int tta_cell_list_build(const float* pos, int64_t N, const float* shifts, int64_t n_cells,
+                        int periodic, const tta_cell_grid* grid, int* bin_start, float* points,
+                        int* work, tta_stream_t stream);
+int tta_radius_graph_cells_thresholds(const float* pos, int64_t N, const float* shifts,
+                                      int64_t n_cells, int periodic, const tta_cell_grid* grid,
+                                      const int* bin_start, const float* points, double mid2,
+                                      float cut2, float min2, int k, float* thr_d2, int* thr_src,
+                                      int* thr_cell, tta_stream_t stream);
+int tta_radius_graph_cells_count(const float* pos, int64_t N, const float* shifts,
+                                 int64_t n_cells, int periodic, const tta_cell_grid* grid,
+                                 const int* bin_start, const float* points, double mid2,
+                                 float cut2, float min2, const float* thr_d2, const int* thr_src,
+                                 const int* thr_cell, int* counts, tta_stream_t stream);
+int tta_radius_graph_cells_write(const float* pos, int64_t N, const float* shifts,
+                                 int64_t n_cells, int periodic, const tta_cell_grid* grid,
+                                 const int* bin_start, const float* points, double mid2,
+                                 float cut2, float min2, const float* thr_d2, const int* thr_src,
+                                 const int* thr_cell, const int64_t* offsets, int64_t* edge_src,
+                                 int64_t* edge_tgt, int* edge_cell, int* err,
+                                 tta_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

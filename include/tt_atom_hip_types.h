@@ -21,4 +21,12 @@ typedef struct tta_gemm_problem {
   int64_t epilogue;
 } tta_gemm_problem;
 
+/* Bins of a cell-list neighbour search: bin coordinate u = (x - origin) * inv_h rounded in fp32
+ * per axis, dims bins per axis (x fastest in the linear bin index). */
+typedef struct tta_cell_grid {
+  float origin[3];
+  float inv_h;
+  int dims[3];
+} tta_cell_grid;
+
 #endif

@@ -17,9 +17,11 @@
 // Three passes of one wavefront per row: thresholds (the k-th smallest key of every receiver,
 // only with a cap), per-row counts, and the ordered write at the caller's exclusive row offsets.
 // Rows of a batch of disjoint systems scan only their own node range [lo, hi).
-#include "common.h"
+#include "nl_math.h"
 
 namespace {
+
+using namespace tta_nl;
 
 constexpr int WAVES = 4;
 constexpr int MAXC = 1024;  // candidates per receiver held in LDS by the threshold pass
@@ -37,50 +39,6 @@ struct NL {
   double mid2;     // aperiodic: keep iff 0 < s < mid2
   float cut2, min2;  // periodic: keep iff min2 < d2 <= cut2
 };
-
-__device__ __forceinline__ float3 ld3(const float* p, int i) {
-  return make_float3(p[3 * i], p[3 * i + 1], p[3 * i + 2]);
-}
-
-// torch fp32 norm^2 of a - b (the value whose rounded sqrt the host compares)
-__device__ __forceinline__ float norm2_fma(float3 a, float3 b) {
-  const float x = __fsub_rn(a.x, b.x), y = __fsub_rn(a.y, b.y), z = __fsub_rn(a.z, b.z);
-  return __builtin_fmaf(z, z, __builtin_fmaf(y, y, __fmul_rn(x, x)));
-}
-
-__device__ __forceinline__ float sum_sq(float x, float y, float z) {
-  return __fadd_rn(__fadd_rn(__fmul_rn(x, x), __fmul_rn(y, y)), __fmul_rn(z, z));
-}
-
-// periodic mask quantity: pos_t - (pos_j + sh)
-__device__ __forceinline__ float disp2(float3 pt, float3 pj, float3 sh) {
-  return sum_sq(__fsub_rn(pt.x, __fadd_rn(pj.x, sh.x)), __fsub_rn(pt.y, __fadd_rn(pj.y, sh.y)),
-                __fsub_rn(pt.z, __fadd_rn(pj.z, sh.z)));
-}
-
-// cap key distance: ev = (pos_src - pos_tgt) + sh
-__device__ __forceinline__ float cap_d2(float3 ps, float3 pt, float3 sh) {
-  return sum_sq(__fadd_rn(__fsub_rn(ps.x, pt.x), sh.x), __fadd_rn(__fsub_rn(ps.y, pt.y), sh.y),
-                __fadd_rn(__fsub_rn(ps.z, pt.z), sh.z));
-}
-
-__device__ __forceinline__ bool key_le(float d, int a, int c, float D, int A, int C) {
-  return d < D || (d == D && (a < A || (a == A && c <= C)));
-}
-__device__ __forceinline__ bool key_lt(float d, int a, int c, float D, int A, int C) {
-  return d < D || (d == D && (a < A || (a == A && c < C)));
-}
-
-__device__ __forceinline__ int wave_excl_scan(int v, int lane, int* total) {
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
-  *total = __shfl(x, 63, 64);
-  return x - v;
-}
 
 // One candidate (column) of a row: periodic rows loop over cells inside the lane.
 // Visits, in order, every kept (src, tgt, cell, cap-d2) of row r within column chunk [j0, j0+64).

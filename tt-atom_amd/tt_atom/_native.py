@@ -29,6 +29,11 @@ class GemmProblem(ctypes.Structure):
                 ("ldc", _I64), ("epilogue", _I64)]
 
 
+class CellGrid(ctypes.Structure):
+    """tta_cell_grid (include/tt_atom_hip_types.h): bins of the cell-list neighbour search."""
+    _fields_ = [("origin", _F * 3), ("inv_h", _F), ("dims", _I * 3)]
+
+
 # name -> argtypes (all return int status unless listed in _RESTYPE)
 _SIGS = {
     "tta_version": [],
@@ -90,8 +95,17 @@ _SIGS = {
                                _P, _P],
     "tta_radius_graph_write": [_P, _I64, _P, _P, _P, _I64, _P, _P, _I, _D, _F, _F, _P, _P, _P,
                                _P, _P, _P, _P, _P],
+    "tta_cell_list_workspace": [_I64, _I64],
+    "tta_cell_list_build": [_P, _I64, _P, _I64, _I, ctypes.POINTER(CellGrid), _P, _P, _P, _P],
+    "tta_radius_graph_cells_thresholds": [_P, _I64, _P, _I64, _I, ctypes.POINTER(CellGrid), _P,
+                                          _P, _D, _F, _F, _I, _P, _P, _P, _P],
+    "tta_radius_graph_cells_count": [_P, _I64, _P, _I64, _I, ctypes.POINTER(CellGrid), _P, _P,
+                                     _D, _F, _F, _P, _P, _P, _P, _P],
+    "tta_radius_graph_cells_write": [_P, _I64, _P, _I64, _I, ctypes.POINTER(CellGrid), _P, _P,
+                                     _D, _F, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P],
 }
-_RESTYPE = {"tta_last_error": ctypes.c_char_p, "tta_pack_b_elems": ctypes.c_int64}
+_RESTYPE = {"tta_last_error": ctypes.c_char_p, "tta_pack_b_elems": ctypes.c_int64,
+            "tta_cell_list_workspace": ctypes.c_int64}
 
 EXPORTS = tuple(_SIGS)
 
@@ -725,6 +739,76 @@ def radius_graph_passes(pos, lo, hi, shifts, periodic, mid2, cut2, min2, k, clo=
     if E:
         _call("tta_radius_graph_write", *common, *thr, offsets.data_ptr(), src.data_ptr(),
               tgt.data_ptr(), None if cell is None else cell.data_ptr(), _stream())
+    return src, tgt, cell
+
+
+CELL_ROW_MAX = 2048   # kept entries per row that the cell-list write pass sorts in LDS
+CELL_MAX_K = 1024     # largest cap of the cell-list threshold selection
+
+
+def radius_graph_cells(pos, shifts, periodic, grid, mid2, cut2, min2, k):
+    """The cell-list radius graph of one system: the edges of ``radius_graph_passes`` (same
+    order, image cells and cap) from the 27 bins around every row atom.  ``grid`` = (origin [3],
+    inv_h, dims [3]) from ``geometry.cell_grid``.  A graph with a row of more than CELL_ROW_MAX
+    kept entries is written by the row-scan write pass (same edges)."""
+    N = pos.shape[0]
+    dev = pos.device
+    n_cells = shifts.shape[0] if periodic else 0
+    origin, inv_h, dims = grid
+    g = CellGrid((_F * 3)(*[float(v) for v in origin]), float(inv_h),
+                 (_I * 3)(*[int(v) for v in dims]))
+    nb = int(dims[0]) * int(dims[1]) * int(dims[2])
+    P = N * n_cells if periodic else N
+    if periodic and P >= (1 << 30):
+        raise ValueError("cell list: N * n_cells must stay below 2^30")
+    lib = load()
+    work = torch.empty(int(lib.tta_cell_list_workspace(nb, P)), device=dev, dtype=torch.int32)
+    bin_start = torch.empty(nb + 1, device=dev, dtype=torch.int32)
+    pts = torch.empty(max(P, 1), 4, device=dev, dtype=torch.float32)
+    pos_p = _ptr(pos, numel=N * 3, name="pos")
+    sh_p = _ptr(shifts, numel=3 * n_cells, name="shifts") if periodic else None
+    common = (pos_p, N, sh_p, n_cells, int(periodic), ctypes.byref(g))
+    _call("tta_cell_list_build", *common, bin_start.data_ptr(), pts.data_ptr(), work.data_ptr(),
+          _stream())
+    cl = (bin_start.data_ptr(), pts.data_ptr(), float(mid2), float(cut2), float(min2))
+    thr = (None, None, None)
+    counts = torch.empty(N, device=dev, dtype=torch.int32)
+    if k > CELL_MAX_K and N:
+        # above the selection's limit the cap must be a no-op: every receiver (a row, by the
+        # symmetry of the aperiodic mask) has at most k candidates
+        _call("tta_radius_graph_cells_count", *common, *cl, *thr, counts.data_ptr(), _stream())
+        if int(counts.max()) > k:
+            raise ValueError(f"cell list: a cap of {k} > {CELL_MAX_K} neighbours is supported only "
+                             "when no receiver has more than that many candidates")
+        k = 0
+    if k:
+        td = torch.empty(N, device=dev, dtype=torch.float32)
+        ta = torch.empty(N, device=dev, dtype=torch.int32)
+        tc = torch.empty(N, device=dev, dtype=torch.int32)
+        _call("tta_radius_graph_cells_thresholds", *common, *cl, int(k), td.data_ptr(),
+              ta.data_ptr(), tc.data_ptr(), _stream())
+        thr = (td.data_ptr(), ta.data_ptr(), tc.data_ptr())
+    _call("tta_radius_graph_cells_count", *common, *cl, *thr, counts.data_ptr(), _stream())
+    c64 = counts.to(torch.int64)
+    ends = torch.cumsum(c64, 0)
+    offsets = ends - c64
+    E, cmax = (int(v) for v in torch.stack([ends[-1], c64.max()]).cpu()) if N else (0, 0)
+    src = torch.empty(E, device=dev, dtype=torch.int64)
+    tgt = torch.empty(E, device=dev, dtype=torch.int64)
+    cell = torch.empty(E, device=dev, dtype=torch.int32) if periodic else None
+    if not E:
+        return src, tgt, cell
+    out = (offsets.data_ptr(), src.data_ptr(), tgt.data_ptr(),
+           None if cell is None else cell.data_ptr())
+    if cmax <= CELL_ROW_MAX:
+        err = torch.zeros(1, device=dev, dtype=torch.int32)
+        _call("tta_radius_graph_cells_write", *common, *cl, *thr, *out, err.data_ptr(), _stream())
+        if int(err.item()):
+            raise RuntimeError("cell list: a row overflowed the write pass after the count pass "
+                               "allowed it")
+    else:
+        _call("tta_radius_graph_write", pos_p, N, None, None, sh_p, n_cells, None, None,
+              int(periodic), float(mid2), float(cut2), float(min2), *thr, *out, _stream())
     return src, tgt, cell
 
 

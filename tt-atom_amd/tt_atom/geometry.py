@@ -92,12 +92,67 @@ def _image_shifts(pos, cutoff, cell, pbc):
     return cells.reshape(-1, 3) @ cell
 
 
+# Systems of at least this many atoms take the cell list when the method is "auto"; below it the
+# row scan (every row reads all N candidates; fewer launches and no binning) is as fast or faster
+# on MI355X.  Measured whole calls at a 6 A cutoff: an aperiodic 2k-atom cluster 0.18 ms (rows)
+# against 0.30 ms (cells), 8k atoms 0.46 against 0.37 ms; a 2k-atom periodic crystal 0.65 against
+# 0.45 ms (the row scan visits every image of every atom).
+CELL_LIST_MIN_ATOMS_APERIODIC = 4096
+CELL_LIST_MIN_ATOMS_PERIODIC = 2048
+
+
+def use_cell_list(n_atoms, periodic):
+    """Does method "auto" take the cell list for one system of ``n_atoms``?"""
+    return n_atoms >= (CELL_LIST_MIN_ATOMS_PERIODIC if periodic else CELL_LIST_MIN_ATOMS_APERIODIC)
+
+
+def cell_grid(pos, cutoff, max_bins=None):
+    """Bins of the cell-list neighbour search over the atoms ``pos`` [N, 3]: ``(origin [3] fp32,
+    inv_h fp32, dims [3])`` with bin coordinate ``u = fl(fl(x - origin) * inv_h)`` per axis.
+
+    The bin side ``h = 1 / inv_h`` exceeds the cutoff by a margin above every rounding error of
+    the fp32 distance test and of u itself (2^-10 of the cutoff plus 2^-12 of the box extent;
+    both errors are below 2^-20 relative), so any pair that passes the distance test lies in
+    neighbouring bins on every axis.  The origin sits 1.5 bins below the atoms' bounding box and
+    ``dims`` spans it plus 2.5 bins above, so every atom's bin and its neighbours are on the
+    grid.  At most ``max_bins`` (default max(4096, 2 N)) bins: a sparse system gets wider
+    bins."""
+    p = np.asarray(pos, np.float32).reshape(-1, 3)
+    n = p.shape[0]
+    q = np.ascontiguousarray(p.T)                  # per-axis rows: fast reductions
+    mn = np.fmin.reduce(q, axis=1).astype(np.float64) if n else np.zeros(3)
+    mx = np.fmax.reduce(q, axis=1).astype(np.float64) if n else np.zeros(3)
+    if not (np.isfinite(mn).all() and np.isfinite(mx).all()):
+        # infinite or all-NaN coordinates: the box of the finite atoms (the others have no edge)
+        fin = p[np.isfinite(p).all(1)].astype(np.float64)
+        mn = fin.min(0) if fin.shape[0] else np.zeros(3)
+        mx = fin.max(0) if fin.shape[0] else np.zeros(3)
+    ext = mx - mn
+    cap = int(max_bins) if max_bins is not None else max(4096, 2 * n)
+    h = float(cutoff) * (1.0 + 2.0 ** -10) + float(ext.max()) * 2.0 ** -12
+    while True:
+        dims = np.floor(ext / h).astype(np.int64) + 4
+        if int(np.prod(dims)) <= cap:
+            break
+        h *= 1.25
+    inv_h = np.float32(1.0 / (h * (1.0 + 2.0 ** -20)))     # fp32 rounding keeps 1 / inv_h >= h
+    origin = (mn - 1.5 * h).astype(np.float32)
+    return tuple(float(v) for v in origin), float(inv_h), tuple(int(v) for v in dims)
+
+
 def radius_graph_device(pos, cutoff, cell=None, pbc=None, max_neighbors=None, *,
-                        node_ranges=None, device=None):
+                        node_ranges=None, device=None, method="auto"):
     """``radius_graph`` computed on the GPU: the same edges in the same order with the same
     ``cell_shift`` values (device tensors).  ``node_ranges`` ([N] lo, [N] hi) restricts every
     node's candidates to its own system in a batch of disjoint aperiodic systems (the
-    concatenation of the per-system graphs, node indices global)."""
+    concatenation of the per-system graphs, node indices global).  ``method``: "rows" scans
+    every candidate of a row (O(N^2)), "cells" bins the atoms (and periodic images) and scans the
+    27 bins around each one (O(N), one system: no ``node_ranges``), "auto" takes the cell list
+    for one system as large as ``use_cell_list`` asks.  Both give the same graph."""
+    if method not in ("auto", "rows", "cells"):
+        raise ValueError("method must be 'auto', 'rows' or 'cells'")
+    if method == "cells" and node_ranges is not None:
+        raise ValueError("the cell list builds one system; batches with node_ranges use 'rows'")
     dev = torch.device(device) if device is not None else (
         pos.device if torch.is_tensor(pos) and pos.is_cuda else torch.device("cuda"))
     pos_h = torch.as_tensor(pos, dtype=torch.float32).detach().cpu()
@@ -132,8 +187,16 @@ def radius_graph_device(pos, cutoff, cell=None, pbc=None, max_neighbors=None, *,
     from . import _native as nat
     k = int(max_neighbors) if max_neighbors is not None else 0
     sh_d = shifts.to(dev).contiguous()
-    src, tgt, c = nat.radius_graph_passes(pos_h.to(dev).contiguous(), lo, hi, sh_d, periodic,
-                                          mid2, cut2, min2, k)
+    cells = method == "cells" or (method == "auto" and node_ranges is None
+                                  and use_cell_list(N, periodic)
+                                  and (not periodic or N * shifts.shape[0] < (1 << 30)))
+    if cells:
+        src, tgt, c = nat.radius_graph_cells(pos_h.to(dev).contiguous(), sh_d, periodic,
+                                             cell_grid(pos_h.numpy(), cutoff), mid2, cut2, min2,
+                                             k)
+    else:
+        src, tgt, c = nat.radius_graph_passes(pos_h.to(dev).contiguous(), lo, hi, sh_d,
+                                              periodic, mid2, cut2, min2, k)
     ei = torch.stack([src, tgt], 0)
     shift = sh_d[c.long()] if periodic else torch.zeros(src.shape[0], 3, device=dev)
     return ei, shift
@@ -193,7 +256,15 @@ def system_graphs(systems, cutoff, max_neighbors=None, neighbor_list="host"):
     periodic = [c is not None and p is not None and bool(np.asarray(p).any())
                 for (_, c, p) in systems]
     if neighbor_list == "device":
-        ap = [k for k in range(len(systems)) if not periodic[k]]
+        # large systems one at a time through the cell list, the rest in batched row scans
+        for k, (pos, cell, pbc) in enumerate(systems):
+            if use_cell_list(int(np.asarray(pos).reshape(-1, 3).shape[0]), periodic[k]):
+                ei, sh = radius_graph_device(torch.as_tensor(np.asarray(pos), dtype=torch.float32),
+                                             cutoff, cell if periodic[k] else None,
+                                             pbc if periodic[k] else None, max_neighbors,
+                                             method="cells")
+                out[k] = (ei.cpu(), sh.cpu())
+        ap = [k for k in range(len(systems)) if not periodic[k] and out[k] is None]
         if ap:
             sizes = [int(systems[k][0].shape[0]) for k in ap]
             starts = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.int64)
@@ -208,7 +279,7 @@ def system_graphs(systems, cutoff, max_neighbors=None, neighbor_list="host"):
             for q, k in enumerate(ap):
                 part = ei[:, bounds[q]:bounds[q + 1]] - int(starts[q])
                 out[k] = (part, torch.zeros(part.shape[1], 3))
-        per = [k for k in range(len(systems)) if periodic[k]]
+        per = [k for k in range(len(systems)) if periodic[k] and out[k] is None]
         if per:
             for k, g in zip(per, _periodic_batch_device([systems[k] for k in per], cutoff,
                                                         max_neighbors)):

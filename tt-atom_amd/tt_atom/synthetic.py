@@ -113,6 +113,27 @@ def c4_system(seed=SEEDS["C4"], reps=8, a=3.61, noise=0.05, Z=29):
     return pos.astype(np.float32), np.full(len(pos), Z, np.int64), cell.astype(np.float32)
 
 
+def lattice_cluster(n, spacing=2.2, seed=0):
+    """About ``n`` atoms on a jittered cubic lattice (spacing 2.2 A, N(0, 0.55 A) jitter) inside a
+    ball, in random index order: a large aperiodic neighbour-list workload (about 75 neighbours
+    within 6 A) whose index order carries no spatial locality."""
+    rng = np.random.default_rng(seed)
+    r = (3.0 * n / (4.0 * np.pi)) ** (1.0 / 3.0) * spacing
+    m = int(np.ceil(r / spacing))
+    g = np.stack(np.meshgrid(*[np.arange(-m, m + 1)] * 3, indexing="ij"), -1).reshape(-1, 3)
+    p = g * spacing + rng.normal(0.0, 0.25 * spacing, g.shape)
+    p = p[(p * p).sum(1) <= r * r]
+    return p[rng.permutation(p.shape[0])].astype(np.float32)
+
+
+def shuffled_fcc(reps, seed=0):
+    """The C4 FCC supercell (reps^3 conventional cells) with its atoms in random index order:
+    (pos, cell)."""
+    pos, Z, cell = c4_system(reps=reps)
+    perm = np.random.default_rng(seed).permutation(pos.shape[0])
+    return pos[perm], cell
+
+
 def c2_graph(seed=SEEDS["C2"], N=8192, deg=25):
     """Isolated edgewise workload: dst-sorted edges (in-degree ``deg``), uniform random src != dst,
     unit directions with lengths uniform in [0.8, 6] A."""

@@ -203,6 +203,19 @@ __device__ __forceinline__ float resid_hi(float x, unsigned hpair) {
   return r;
 }
 
+// max(|a|, |b|, c) and max(a, b, c) in one v_max3_f32 (abs as source modifiers; fmaxf would
+// add a canonicalising max per operand).  Only the exponent of the result is used.
+__device__ __forceinline__ float max3_abs(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, |%1|, |%2|, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 // Split 8 fp32 values, scaled by 2^-sh, into two fp16 planes (round-to-nearest residuals).
 template <int NPL>
 __device__ __forceinline__ void split8_f16(const floatx4& x0, const floatx4& x1, int sh,
@@ -235,6 +248,7 @@ __device__ __forceinline__ int aswz(int row) { return (row >> 1) & 7; }
 template <int WM, int MODE>
 __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(GemmGroup g) {
   const GemmArgs& p = g.p[blockIdx.z];  // the product of this block (group of one: z = 0)
+  const int K = p.K;                     // kept in a scalar register across the k loop
   const int NT32 = g.NT32[blockIdx.z];
   const bool vec_ok = g.vec[blockIdx.z] != 0;
   typedef Split<MODE> S;
@@ -273,34 +287,58 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   // k >= K) gets an offset past num_records and is copied as zeros.
   const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float*>(p.A + (int64_t)m0 * p.lda), (short)0, 0x7ffffffe, 0x00020000);
-  int arow[APT], acol[APT];
+  // Copy offsets: the per-lane byte offsets are fixed for the tile and the k step enters as the
+  // (scalar) soffset, so a k step's copies cost no vector address arithmetic.  An A row past M
+  // gets a voffset past num_records (copied as zeros); a slab that runs past K (K % 32 != 0, the
+  // last slab only) checks its columns per lane instead.  LDS destinations are wave-uniform.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int rows_left = p.M - m0;
+  int avo[APT], acol[APT];
 #pragma unroll
   for (int h = 0; h < APT; ++h) {
     const int L = t + NTH * h;  // LDS chunk this lane fills
     const int row = L >> 3;
-    arow[h] = row;
     acol[h] = 4 * ((L & 7) ^ aswz(row));
+    avo[h] = row < rows_left ? (row * (int)p.lda + acol[h]) * 4 : (int)0x7fffffff;
   }
-  const int rows_left = p.M - m0;
+  // packed B: every offset of the buffer fits in 31 bits (checked on the host)
+  const __amdgpu_buffer_rsrc_t brsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.B), (short)0, 0x7ffffffe, 0x00020000);
+  int bvo[BPT];
+#pragma unroll
+  for (int h = 0; h < BPT; ++h) {
+    const int c = t + NTH * h;
+    const int pl = c / (NF * 64), f = (c / 64) % NF, l = c % 64;
+    bvo[h] = (((pl * NT32 + nt0 + (f >> 1)) * 2 + (f & 1)) * 64 + l) * 16;
+  }
+  const int bstep = NB * NT32 * 128 * 16;  // bytes of one packed k slab
 
   auto issue = [&](int kt, int stg) {
-    uint4* base = smem + stg * STG;
+    uint4* base = smem + stg * STG + 64 * wave_s;  // + NTH * h: this wave's 64 chunks of copy h
     const int k0 = kt * BK;
+    // (the offsets go through locals: hipcc's host pass drops the kernel's launch stub when a
+    // builtin argument reads a lambda-captured array element directly)
+    if (k0 + BK <= K) {
 #pragma unroll
-    for (int h = 0; h < APT; ++h) {
-      const int k = k0 + acol[h];
-      const int o = (arow[h] * (int)p.lda + k) * 4;
-      const int off = ((arow[h] < rows_left) & (k < p.K)) ? o : (int)0x7fffffff;
-      const int L = t + NTH * h;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_ptr)(base + (L - lane)), 16, off, 0, 0,
-                                               0);
+      for (int h = 0; h < APT; ++h) {
+        const int vo = avo[h];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_ptr)(base + NTH * h), 16, vo,
+                                                 k0 * 4, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < APT; ++h) {
+        const int vo = avo[h], k = k0 + acol[h];
+        const int off = (vo != (int)0x7fffffff && k < K) ? vo + k0 * 4 : (int)0x7fffffff;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_ptr)(base + NTH * h), 16, off, 0, 0,
+                                                 0);
+      }
     }
 #pragma unroll
     for (int h = 0; h < BPT; ++h) {
-      const int c = t + NTH * h;
-      const int pl = c / (NF * 64), f = (c / 64) % NF, l = c % 64;
-      const uint4* g = Bp + ((((int64_t)kt * NB + pl) * NT32 + nt0 + (f >> 1)) * 2 + (f & 1)) * 64 + l;
-      __builtin_amdgcn_global_load_lds((gbl_ptr)g, (lds_ptr)(base + A_CH + (c - l)), 16, 0, 0);
+      const int vo = bvo[h];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(brsrc, (lds_ptr)(base + A_CH + NTH * h), 16, vo,
+                                               kt * bstep, 0, 0);
     }
   };
 
@@ -340,6 +378,7 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   int er[TI];
 #pragma unroll
   for (int i = 0; i < TI; ++i) er[i] = kNoExp;
+  bool unscaled = true;  // wave-uniform: E is 0 or unset on every row (the common case)
   auto crow = [&](int r) { return 8 * (r >> 2) + 4 * lh + (r & 3); };
   auto scale = [&](const floatx4 (&x0)[TI][2], const floatx4 (&x1)[TI][2]) {
     if constexpr (S::F16) {
@@ -351,7 +390,7 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) m = fmaxf(m, fmaxf(fabsf(x0[i][c][e]), fabsf(x1[i][c][e])));
+          for (int e = 0; e < 4; ++e) m = max3_abs(x0[i][c][e], x1[i][c][e], m);
         // the row's other 16 values of this k slab are in lane l ^ 32: v_permlane32_swap trades
         // the upper half of one register with the lower half of another, so with m in both, one
         // of them ends up holding the partner's m in every lane (a permute through LDS would wait
@@ -360,7 +399,7 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
         {
           float u = m, w = m;
           asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(u), "+v"(w));
-          m = fmaxf(m, fmaxf(u, w));
+          m = max3(m, u, w);
         }
         const int e = m > 0.f ? __builtin_amdgcn_frexp_expf(m) : kNoExp;
         // values below 2^e reach 2^(e - E): a new shift once that passes 2^15, and for the row's
@@ -381,16 +420,17 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
           }
           er[i] = en[i];
         }
+        bool u = true;
+#pragma unroll
+        for (int i = 0; i < TI; ++i) u &= er[i] == 0 || er[i] == kNoExp;
+        unscaled = __all(u);
       }
     }
   };
   auto sp = [&](const floatx4 (&x)[TI][2], V8 (&a)[TI][NA]) {
     if constexpr (S::F16) {
       // E = 0 on every row of the wave (the common case): no scaling instructions at all
-      bool unscaled = true;
-#pragma unroll
-      for (int i = 0; i < TI; ++i) unscaled &= er[i] == 0 || er[i] == kNoExp;
-      if (__all(unscaled)) {
+      if (unscaled) {
 #pragma unroll
         for (int i = 0; i < TI; ++i) split8_f16<NA>(x[i][0], x[i][1], 0, a[i]);
       } else {
@@ -416,7 +456,7 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   // landed and its reads of slab kt returned, so after it slab kt+1 is visible to all and slab kt's
   // stage takes the copies of slab kt+2.  Slab indices past the end are clamped (harmless
   // re-copies, never read) so every step issues the same copies.
-  const int nk = (p.K + BK - 1) / BK;
+  const int nk = (K + BK - 1) / BK;
   if (nk > 0) {
     issue(0, 0);
     issue(min(1, nk - 1), 1);
@@ -669,6 +709,8 @@ static int prepare_bf16x(const float* A, const void* Bp, float* C, const float* 
   TTA_CHECK_ARG(lda < ((int64_t)1 << 21), "tta_gemm_bf16x: lda must be below 2^21 (32-bit "
                 "offsets inside a 256-row tile)");
   TTA_CHECK_ARG((uintptr_t)Bp % 16 == 0, "tta_gemm_bf16x: packed B must be 16-byte aligned");
+  TTA_CHECK_ARG(tta_pack_b_elems(K, N, 6) * 2 < ((int64_t)1 << 31),
+                "tta_gemm_bf16x: packed B above 2 GB (the copies use 32-bit buffer offsets)");
   g.p[slot] = GemmArgs{A, Bp, C, bias, C2, aux, (int)M, (int)N, (int)K, lda, 0, ldc, 0, 0, 0,
                        0, epilogue, P, idx0, idx1, ldp, off1};
   g.NT32[slot] = (int)nt32_padded(N);

@@ -139,6 +139,35 @@ def test_split_bf16_gemm_fp32_accuracy(nat, M, N, K, epi, mode):
             scale.max())
 
 
+@pytest.mark.parametrize("mode,tol", [(1, 2e-2), (3, 2e-4), (6, 1e-6), (16, 1e-6)])
+def test_split_gemm_persistent_tiles(nat, mode, tol):
+    """More tiles than resident blocks: every block of the split kernel walks several tiles
+    (70001 x 700 -> 547 x 6 tiles of 128 x 128 over at most two blocks per compute unit), with a
+    ragged last row tile and column tile and a K (100) that ends inside a 32-wide slab; plus a
+    grouped launch whose two products have different tile counts.  Error relative to |A| |B| as
+    the mode's planes allow (bf16: 2^-8; two bf16 planes: 2^-16; fp32-accurate modes 6 / 16)."""
+    g = torch.Generator().manual_seed(70 + mode)
+    M, N, K = 70001, 700, 100
+    A = torch.randn(M, K, generator=g)
+    B = torch.randn(K, N, generator=g) / math.sqrt(K)
+    bias = torch.randn(N, generator=g)
+    ref = A.double() @ B.double() + bias.double()
+    scale = A.double().abs() @ B.double().abs() + 1.0
+    pw = nat.PackedWeight(B.to(DEV), mode)
+    out = torch.full((M, N), float("nan"), device=DEV)
+    nat.linear(A.to(DEV), pw, bias.to(DEV), out=out)
+    err = ((out.cpu().double() - ref).abs() / scale).max().item()
+    assert err < tol, err
+    # grouped: the same product next to a small one (5000 rows: 40 x 6 tiles)
+    out_g = torch.full((M, N), float("nan"), device=DEV)
+    small = torch.full((5000, N), float("nan"), device=DEV)
+    nat.linear_group([(A.to(DEV), pw, bias.to(DEV), out_g),
+                      (A[:5000].to(DEV), pw, None, small)])
+    assert torch.equal(out_g, out)
+    assert torch.equal(small.cpu(), (out - bias.to(DEV))[:5000].cpu()) or \
+        ((small.cpu().double() - (ref - bias.double())[:5000]).abs() / scale[:5000]).max() < tol
+
+
 def test_split_bf16_gemm_modes_and_gather(nat):
     g = torch.Generator().manual_seed(3)
     M, N, K, Nn = 6000, 256, 512, 300

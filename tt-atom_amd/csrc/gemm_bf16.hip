@@ -129,33 +129,43 @@ __device__ __forceinline__ float epi_one(const GemmArgs& p, float v, int row, in
   return v;
 }
 
-// Rows [row0, row0 + rows) of a 128-column output tile staged in LDS (row stride ldt floats):
-// thread t takes float4 column groups t, t + nth, ...; vec_ok (host-checked 16-byte alignment of
-// every operand row) selects the float4 path.
-__device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct, int ldt, int rows,
-                                           int row0, int n0, int t, int nth, bool vec_ok) {
-#pragma unroll 1
-  for (int idx = t; idx < rows * (BN / 4); idx += nth) {
-    const int rr = idx / (BN / 4), c4 = idx % (BN / 4);
-    const int row = row0 + rr, col = n0 + 4 * c4;
-    if (row >= p.M || col >= p.N) continue;
-    const floatx4 a = *reinterpret_cast<const floatx4*>(Ct + rr * ldt + 4 * c4);
-    const int64_t off = (int64_t)row * p.ldc + col;
-    if (vec_ok && col + 3 < p.N) {
-      floatx4 v = a;
-      if (p.bias) v += *reinterpret_cast<const floatx4*>(p.bias + col);
-      if (p.P)
+// Rows [row0, row0 + rows) of a 128-column output tile staged in LDS (row stride ldt floats).
+// Thread t owns float4 column group t % 32 and rows t / 32, t / 32 + nth / 32, ...: the bias,
+// the column checks and the lane's column offset are set once, and the epilogue type is a
+// template parameter, so a row costs one LDS read, one address add and one 16-byte store.
+// vec_ok (host-checked 16-byte alignment of every operand row) selects the float4 path; full
+// (the tile lies inside M x N) drops the bounds checks.
+template <int EPI>
+__device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct, int ldt,
+                                              int rows, int row0, int n0, int t, int nth,
+                                              bool vec_ok, bool full) {
+  const int c4 = t & 31, rstep = nth >> 5;
+  const int col = n0 + 4 * c4;
+  if (vec_ok && (full || col + 3 < p.N)) {
+    const floatx4 bv = p.bias ? *reinterpret_cast<const floatx4*>(p.bias + col)
+                              : floatx4{0.f, 0.f, 0.f, 0.f};
+    const bool gather = p.P != nullptr;
+#pragma unroll 4
+    for (int rr = t >> 5; rr < rows; rr += rstep) {
+      const int row = row0 + rr;
+      if (!full && row >= p.M) break;
+      floatx4 v = *reinterpret_cast<const floatx4*>(Ct + rr * ldt + 4 * c4) + bv;
+      const int64_t off = (int64_t)row * p.ldc + col;
+      if (gather)
         v += *reinterpret_cast<const floatx4*>(p.P + (int64_t)p.idx0[row] * p.ldp + col) +
              *reinterpret_cast<const floatx4*>(p.P + (int64_t)p.idx1[row] * p.ldp + p.off1 + col);
-      if (p.epi == EPI_ACCUM) v += *reinterpret_cast<const floatx4*>(p.C + off);
-      if (p.epi == EPI_SILU || p.epi == EPI_PRE_SILU || p.epi == EPI_SILU_GRAD) {
-        floatx4 w = v;
-        const floatx4 x = p.epi == EPI_SILU_GRAD ? *reinterpret_cast<const floatx4*>(p.aux + off)
-                                                 : v;
+      if constexpr (EPI == EPI_ACCUM) v += *reinterpret_cast<const floatx4*>(p.C + off);
+      if constexpr (EPI == EPI_SILU || EPI == EPI_PRE_SILU || EPI == EPI_SILU_GRAD) {
+        floatx4 w;
+        if constexpr (EPI == EPI_SILU_GRAD) {
+          const floatx4 x = *reinterpret_cast<const floatx4*>(p.aux + off);
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          w[e] = p.epi == EPI_SILU_GRAD ? v[e] * tta_silu_grad(x[e]) : tta_silu(v[e]);
-        if (p.epi == EPI_PRE_SILU)
+          for (int e = 0; e < 4; ++e) w[e] = v[e] * tta_silu_grad(x[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = tta_silu(v[e]);
+        }
+        if constexpr (EPI == EPI_PRE_SILU)
           __builtin_nontemporal_store(w, reinterpret_cast<floatx4*>(p.C2 + off));
         else
           v = w;
@@ -164,8 +174,14 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
       // evict the A row panels that the other column tiles are still re-reading from L2
       // (+15-17 % on the write-heavy short-K shapes)
       __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(p.C + off));
-    } else {
-      for (int e = 0; e < 4 && col + e < p.N; ++e) p.C[off + e] = epi_one(p, a[e], row, col + e);
+    }
+  } else {
+    for (int rr = t >> 5; rr < rows; rr += rstep) {
+      const int row = row0 + rr;
+      if (row >= p.M) break;
+      const floatx4 a = *reinterpret_cast<const floatx4*>(Ct + rr * ldt + 4 * c4);
+      for (int e = 0; e < 4 && col + e < p.N; ++e)
+        p.C[(int64_t)row * p.ldc + col + e] = epi_one(p, a[e], row, col + e);
     }
   }
 }
@@ -274,44 +290,58 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   const int wm = TI == 2 ? wave >> 1 : wave, wn = TI == 2 ? wave & 1 : 0;
   const int tn = (p.N + BN - 1) / BN;
   const int ntiles = tn * ((p.M + BM - 1) / BM);
-  // a product of a group uses the first (ntiles rounded up to 8) blocks of the grid, so that
-  // xcd_tile maps them one to one onto its tiles; wider grids belong to other products
-  if ((int)blockIdx.x >= ((ntiles + 7) / 8) * 8) return;
-  const int tile = xcd_tile(ntiles);
-  if (tile >= ntiles) return;
-  const int n0 = (tile % tn) * BN;
-  const int m0 = (tile / tn) * BM;
-  const int nt0 = n0 / 32;
+  // Persistent tiles: a product of a group runs on the first gb = min(ntiles rounded up to 8,
+  // g.cap) blocks of the grid (wider grids belong to other products).  Block b sits on XCD b % 8
+  // (the dispatcher's round robin) and walks that XCD's contiguous range of tiles -- row-major
+  // (m, n) order, so neighbours share A row panels in that XCD's L2 -- with stride gb / 8.
+  const int gb = min(((ntiles + 7) / 8) * 8, g.cap);
+  if ((int)blockIdx.x >= gb) return;
+  const int per_xcd = (ntiles + 7) / 8, stride = gb / 8;
+  const int t_end = min(((int)blockIdx.x % 8 + 1) * per_xcd, ntiles);
+  int tile = ((int)blockIdx.x % 8) * per_xcd + (int)blockIdx.x / 8;
+  if (tile >= t_end) return;
   const uint4* Bp = static_cast<const uint4*>(p.B);
-  // A through a buffer resource based at the tile's first row: an out-of-range chunk (row >= M or
-  // k >= K) gets an offset past num_records and is copied as zeros.
-  const __amdgpu_buffer_rsrc_t arsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(p.A + (int64_t)m0 * p.lda), (short)0, 0x7ffffffe, 0x00020000);
-  // Copy offsets: the per-lane byte offsets are fixed for the tile and the k step enters as the
-  // (scalar) soffset, so a k step's copies cost no vector address arithmetic.  An A row past M
-  // gets a voffset past num_records (copied as zeros); a slab that runs past K (K % 32 != 0, the
-  // last slab only) checks its columns per lane instead.  LDS destinations are wave-uniform.
+  // Copy offsets: the per-lane byte offsets are fixed for a tile and the k step enters as the
+  // (scalar) soffset, so a k step's copies cost no vector address arithmetic.  A goes through a
+  // buffer resource based at the tile's first row; a row past M gets a voffset past num_records
+  // (copied as zeros); a slab that runs past K (K % 32 != 0, the last slab only) checks its
+  // columns per lane instead.  LDS destinations are wave-uniform.
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  const int rows_left = p.M - m0;
-  int avo[APT], acol[APT];
+  int arow[APT], aoff[APT], acol[APT];
 #pragma unroll
   for (int h = 0; h < APT; ++h) {
     const int L = t + NTH * h;  // LDS chunk this lane fills
-    const int row = L >> 3;
-    acol[h] = 4 * ((L & 7) ^ aswz(row));
-    avo[h] = row < rows_left ? (row * (int)p.lda + acol[h]) * 4 : (int)0x7fffffff;
+    arow[h] = L >> 3;
+    acol[h] = 4 * ((L & 7) ^ aswz(arow[h]));
+    aoff[h] = (arow[h] * (int)p.lda + acol[h]) * 4;
   }
   // packed B: every offset of the buffer fits in 31 bits (checked on the host)
   const __amdgpu_buffer_rsrc_t brsrc =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.B), (short)0, 0x7ffffffe, 0x00020000);
-  int bvo[BPT];
+  int boff[BPT];
 #pragma unroll
   for (int h = 0; h < BPT; ++h) {
     const int c = t + NTH * h;
     const int pl = c / (NF * 64), f = (c / 64) % NF, l = c % 64;
-    bvo[h] = (((pl * NT32 + nt0 + (f >> 1)) * 2 + (f & 1)) * 64 + l) * 16;
+    boff[h] = (((pl * NT32 + (f >> 1)) * 2 + (f & 1)) * 64 + l) * 16;
   }
   const int bstep = NB * NT32 * 128 * 16;  // bytes of one packed k slab
+
+  // copy parameters of the tile being loaded (they move on to the next tile before the epilogue)
+  int m0 = 0, n0 = 0;
+  __amdgpu_buffer_rsrc_t arsrc;
+  int avo[APT], bvo[BPT];
+  auto set_tile = [&](int tl) {
+    n0 = (tl % tn) * BN;
+    m0 = (tl / tn) * BM;
+    arsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.A + (int64_t)m0 * p.lda),
+                                              (short)0, 0x7ffffffe, 0x00020000);
+    const int rows_left = p.M - m0;
+#pragma unroll
+    for (int h = 0; h < APT; ++h) avo[h] = arow[h] < rows_left ? aoff[h] : (int)0x7fffffff;
+#pragma unroll
+    for (int h = 0; h < BPT; ++h) bvo[h] = boff[h] + (n0 / 32) * 2048;
+  };
 
   auto issue = [&](int kt, int stg) {
     uint4* base = smem + stg * STG + 64 * wave_s;  // + NTH * h: this wave's 64 chunks of copy h
@@ -455,74 +485,116 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   // the current one run.  One barrier per slab: each wave arrives with its copies of slab kt+1
   // landed and its reads of slab kt returned, so after it slab kt+1 is visible to all and slab kt's
   // stage takes the copies of slab kt+2.  Slab indices past the end are clamped (harmless
-  // re-copies, never read) so every step issues the same copies.
+  // re-copies, never read) so every step issues the same copies.  A tile's slab 0 always sits in
+  // stage 0, slab 1 in stage 1.
   const int nk = (K + BK - 1) / BK;
-  if (nk > 0) {
-    issue(0, 0);
-    issue(min(1, nk - 1), 1);
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(APT + BPT) : "memory");
-    floatx4 x0[TI][2], x1[TI][2];  // A of both k halves of the slab being split
-    V8 ca[TI][NA], cb[TJ][NB], na[TI][NA], nb[TJ][NB];
-    rdA(0, 0, x0);
-    rdA(0, 1, x1);
-    rdB(0, 0, cb);
-    scale(x0, x1);
-    sp(x0, ca);
-    for (int kt = 0; kt < nk; ++kt) {
-      const int stg = kt & 1;
-      rdB(stg, 1, nb);
-      mm(ca, cb);
-      sp(x1, na);
-      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      issue(min(kt + 2, nk - 1), stg);
-      rdA(stg ^ 1, 0, x0);
-      rdA(stg ^ 1, 1, x1);
-      rdB(stg ^ 1, 0, cb);
-      mm(na, nb);
-      scale(x0, x1);
-      sp(x0, ca);
-    }
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  }
-  if constexpr (S::F16) {
-    // undo the scales: C = acc * 2^(E[row] + F[col]); F follows the planes of the packed B and
-    // has an entry for every column of the padded n32 tiles
-    const int* Fc =
-        reinterpret_cast<const int*>(Bp + (int64_t)((p.K + BK - 1) / BK) * NB * NT32 * 128);
-    int fc[TJ];
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) fc[j] = Fc[n0 + cbase + j * 32 + l32];
-#pragma unroll
-    for (int i = 0; i < TI; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rs = __shfl(er[i], crow(r));
-#pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          acc[i][j][r] = __builtin_amdgcn_ldexpf(acc[i][j][r], rs + fc[j]);
-      }
-  }
-  // Epilogue: stage the accumulators through LDS in row passes, then each thread applies the
-  // epilogue to whole float4 column groups and writes coalesced rows.
+  const int* Fc =
+      S::F16 ? reinterpret_cast<const int*>(Bp + (int64_t)nk * NB * NT32 * 128) : nullptr;
   constexpr int SMEM_F = SMEM_U4 * 4;
   constexpr int RP = (BM * LDT <= SMEM_F) ? BM : (BM / 2 * LDT <= SMEM_F) ? BM / 2
                    : (BM / 4 * LDT <= SMEM_F) ? BM / 4 : 32;
   static_assert(RP % 32 == 0 && RP * LDT <= SMEM_F, "epilogue staging must fit the LDS buffer");
-  float* Ct = reinterpret_cast<float*>(smem);
-  for (int r0 = 0; r0 < BM; r0 += RP) {
+
+  set_tile(tile);
+  if (nk > 0) issue(0, 0);
+  for (;;) {
+    const int cm0 = m0, cn0 = n0;  // the tile computed in this pass
 #pragma unroll
-    for (int i = 0; i < TI; ++i) {
-      const int rt = rbase + i * 32 - r0;
-      if (rt < 0 || rt >= RP) continue;
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
       for (int j = 0; j < TJ; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          Ct[(rt + 8 * (r >> 2) + 4 * lh + (r & 3)) * LDT + cbase + j * 32 + l32] = acc[i][j][r];
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) er[i] = kNoExp;
+    unscaled = true;
+    if (nk > 0) {
+      issue(min(1, nk - 1), 1);
+      // slab 0 landed (with everything issued before it: vector memory operations complete in
+      // order); slab 1 may still be in flight
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(APT + BPT) : "memory");
+      floatx4 x0[TI][2], x1[TI][2];  // A of both k halves of the slab being split
+      V8 ca[TI][NA], cb[TJ][NB], na[TI][NA], nb[TJ][NB];
+      rdA(0, 0, x0);
+      rdA(0, 1, x1);
+      rdB(0, 0, cb);
+      scale(x0, x1);
+      sp(x0, ca);
+      for (int kt = 0; kt < nk; ++kt) {
+        const int stg = kt & 1;
+        rdB(stg, 1, nb);
+        mm(ca, cb);
+        sp(x1, na);
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        issue(min(kt + 2, nk - 1), stg);
+        rdA(stg ^ 1, 0, x0);
+        rdA(stg ^ 1, 1, x1);
+        rdB(stg ^ 1, 0, cb);
+        mm(na, nb);
+        scale(x0, x1);
+        sp(x0, ca);
+      }
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     }
-    __syncthreads();
-    epilogue_rows(p, Ct, LDT, RP, m0 + r0, n0, t, NTH, vec_ok);
-    __syncthreads();
+    const int next = tile + stride;
+    const bool more = next < t_end;
+    if constexpr (S::F16) {
+      // undo the scales: C = acc * 2^(E[row] + F[col]); F follows the planes of the packed B and
+      // has an entry for every column of the padded n32 tiles
+      int fc[TJ];
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) fc[j] = Fc[cn0 + cbase + j * 32 + l32];
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rs = __shfl(er[i], crow(r));
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+            acc[i][j][r] = __builtin_amdgcn_ldexpf(acc[i][j][r], rs + fc[j]);
+        }
+    }
+    // Epilogue: stage the accumulators through LDS in row passes (one pass in mode 16), then each
+    // thread applies the epilogue to float4 column groups and writes coalesced rows.  The
+    // barriers wait for LDS only; the output stores stay in flight.
+    {
+      const bool full = cm0 + BM <= p.M && cn0 + BN <= p.N;
+      float* Ct = reinterpret_cast<float*>(smem);
+      for (int r0 = 0; r0 < BM; r0 += RP) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+          const int rt = rbase + i * 32 - r0;
+          if (rt < 0 || rt >= RP) continue;
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              Ct[(rt + crow(r)) * LDT + cbase + j * 32 + l32] = acc[i][j][r];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        switch (p.epi) {
+          case EPI_SILU:
+            epilogue_rows<EPI_SILU>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            break;
+          case EPI_ACCUM:
+            epilogue_rows<EPI_ACCUM>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            break;
+          case EPI_PRE_SILU:
+            epilogue_rows<EPI_PRE_SILU>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            break;
+          case EPI_SILU_GRAD:
+            epilogue_rows<EPI_SILU_GRAD>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            break;
+          default:
+            epilogue_rows<EPI_STORE>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      }
+    }
+    if (!more) break;
+    tile = next;
+    set_tile(tile);
+    if (nk > 0) issue(0, 0);
   }
 }
 
@@ -606,16 +678,33 @@ __global__ __launch_bounds__(256) void k_pack_b_f16(const float* __restrict__ B,
 
 // One launch for the n products of g (blockIdx.z = product); each product's blocks beyond its
 // own tile count exit at once.
+// Blocks per product of the persistent tile loop: two per compute unit (the kernel's occupancy),
+// rounded up to whole XCD rounds of 8.
+int persistent_cap() {
+  static int cap[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cap[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cap[dev] = ((2 * cus + 7) / 8) * 8;
+  }
+  return cap[dev];
+}
+
 template <int WM, int MODE>
-int launch_bf16x(const GemmGroup& g, int n, hipStream_t s) {
+int launch_bf16x(GemmGroup& g, int n, hipStream_t s) {
   int64_t grid = 0;
+  g.cap = persistent_cap();
   for (int i = 0; i < n; ++i) {
     const int64_t ntiles = (int64_t)tta_blocks(g.p[i].N, BN) * tta_blocks(g.p[i].M, 64 * WM);
     if (ntiles > (1ll << 30)) {
       tta::set_error("tta_gemm_bf16x: grid too large");
       return tta::kBadArgument;
     }
-    grid = std::max(grid, ((ntiles + 7) / 8) * 8);
+    grid = std::max(grid, std::min<int64_t>(((ntiles + 7) / 8) * 8, g.cap));
   }
   hipLaunchKernelGGL((gemm_bf16x_kernel<WM, MODE>), dim3((unsigned)grid, 1, (unsigned)n),
                      dim3(128 * WM), 0, s, g);
@@ -629,7 +718,7 @@ bool vec_ok_of(const GemmArgs& p) {
          (!p.P || (al(p.P) && p.ldp % 4 == 0 && p.off1 % 4 == 0));
 }
 
-int launch_mode(const GemmGroup& g, int n, int mode, hipStream_t s) {
+int launch_mode(GemmGroup& g, int n, int mode, hipStream_t s) {
   switch (mode) {
     case 1: return launch_bf16x<2, 1>(g, n, s);
     case 3: return launch_bf16x<2, 3>(g, n, s);

@@ -38,6 +38,7 @@ struct GemmGroup {
   GemmArgs p[kMaxGroup];
   int NT32[kMaxGroup];
   int vec[kMaxGroup];
+  int cap;  // split kernel: most blocks per product (persistent tile loop), a multiple of 8
 };
 
 // Accumulator layout of v_mfma_f32_16x16x{4f32,32bf16}: lane l holds D[4*(l/16)+r][l%16] in

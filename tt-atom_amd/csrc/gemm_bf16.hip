@@ -371,6 +371,22 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
                                                kt * bstep, 0, 0);
     }
   };
+  // the copies of a slab that ends inside K (every slab when K % 32 == 0): no column checks
+  auto issue_full = [&](int kt, int stg) {
+    uint4* base = smem + stg * STG + 64 * wave_s;
+#pragma unroll
+    for (int h = 0; h < APT; ++h) {
+      const int vo = avo[h];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(arsrc, (lds_ptr)(base + NTH * h), 16, vo,
+                                               kt * BK * 4, 0, 0);
+    }
+#pragma unroll
+    for (int h = 0; h < BPT; ++h) {
+      const int vo = bvo[h];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(brsrc, (lds_ptr)(base + A_CH + NTH * h), 16, vo,
+                                               kt * bstep, 0, 0);
+    }
+  };
 
   floatx16 acc[TI][TJ];
 #pragma unroll
@@ -410,7 +426,8 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   for (int i = 0; i < TI; ++i) er[i] = kNoExp;
   bool unscaled = true;  // wave-uniform: E is 0 or unset on every row (the common case)
   auto crow = [&](int r) { return 8 * (r >> 2) + 4 * lh + (r & 3); };
-  auto scale = [&](const floatx4 (&x0)[TI][2], const floatx4 (&x1)[TI][2]) {
+  // returns whether a shift changed (the accumulators were rescaled)
+  auto scale = [&](const floatx4 (&x0)[TI][2], const floatx4 (&x1)[TI][2]) -> bool {
     if constexpr (S::F16) {
       int en[TI];
       bool grow = false;
@@ -454,7 +471,20 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
 #pragma unroll
         for (int i = 0; i < TI; ++i) u &= er[i] == 0 || er[i] == kNoExp;
         unscaled = __all(u);
+        return true;
       }
+    }
+    return false;
+  };
+  // the split of an unscaled wave (every mode but a scaled mode-16 wave): no branch, so that the
+  // scheduler can interleave it with the MFMAs of the other k half
+  auto sp_fast = [&](const floatx4 (&x)[TI][2], V8 (&a)[TI][NA]) {
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+      if constexpr (S::F16)
+        split8_f16<NA>(x[i][0], x[i][1], 0, a[i]);
+      else
+        split8<NA>(x[i][0], x[i][1], a[i]);
     }
   };
   auto sp = [&](const floatx4 (&x)[TI][2], V8 (&a)[TI][NA]) {
@@ -520,7 +550,34 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
       rdB(0, 0, cb);
       scale(x0, x1);
       sp(x0, ca);
-      for (int kt = 0; kt < nk; ++kt) {
+      int kt = 0;
+      // Fast loop (K a multiple of 32 and no row of the wave scaled: every product here): no
+      // branch between a k half's MFMAs and the split of the next half, which the scheduler
+      // interleaves.  x0 is split before its slab's shift check and split again in the rare case
+      // that the check rescales; a wave that acquires a nonzero shift finishes in the general loop.
+      if (K % BK == 0 && (!S::F16 || unscaled)) {
+        for (; kt < nk; ++kt) {
+          const int stg = kt & 1;
+          rdB(stg, 1, nb);
+          mm(ca, cb);
+          sp_fast(x1, na);
+          asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+          issue_full(min(kt + 2, nk - 1), stg);
+          rdA(stg ^ 1, 0, x0);
+          rdA(stg ^ 1, 1, x1);
+          rdB(stg ^ 1, 0, cb);
+          mm(na, nb);
+          sp_fast(x0, ca);
+          if (scale(x0, x1)) {
+            sp(x0, ca);
+            if (S::F16 && !unscaled) {
+              ++kt;
+              break;
+            }
+          }
+        }
+      }
+      for (; kt < nk; ++kt) {
         const int stg = kt & 1;
         rdB(stg, 1, nb);
         mm(ca, cb);

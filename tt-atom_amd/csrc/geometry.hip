@@ -68,32 +68,65 @@ __global__ __launch_bounds__(256) void k_edge_features(
 // Wigner part of the VJP in full (identical work, so no divergence) and the first lane stores.
 // Compared with one thread per edge this spreads the nb-long sum of small graphs over four
 // times the threads and makes its row reads contiguous.
-constexpr int kGeoLanes = 4;
+// Edge-geometry VJP, EPB edges per 256-thread block in two phases.  Phase 1, the Gaussian-basis
+// adjoint sum_k g[e, k] d/dd exp(coeff (d - off_k)^2): 16 lanes per edge, each lane a float4 of
+// k per pass (V4: nb and the row stride multiples of 4, 16-byte aligned rows; else scalar), so a
+// load instruction covers four edges with 256 contiguous bytes each; the 16 partial sums reduce
+// by shuffles in a fixed order into LDS.  Phase 2: one thread per edge adds the envelope term and
+// the Wigner-D VJP (geometry_math.h) and writes g_ev.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
+template <int EPB, bool V4>
 __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
     const float* __restrict__ ev, const float* __restrict__ dist,
     const float* __restrict__ g_coef, const float* __restrict__ g_env,
     const float* __restrict__ g_gauss, int64_t ldg, const float* __restrict__ off, float coeff,
     float cutoff, int nb, const float* __restrict__ jd, float gamma, float* __restrict__ g_ev,
     int E) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int sub = threadIdx.x & (kGeoLanes - 1);
-  const int64_t e0 = gid / kGeoLanes;
-  const bool valid = e0 < E;
-  const int64_t e = valid ? e0 : E - 1;  // lanes past the end mirror the last edge (no store)
-  float v[3] = {ev[e * 3], ev[e * 3 + 1], ev[e * 3 + 2]};
-  const float d = dist[e];
-  float gd = 0.f;
+  __shared__ float sgd[EPB];
+  const int64_t eb = (int64_t)blockIdx.x * EPB;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (g_gauss) {
-    const float* gg = g_gauss + e * ldg;
-    for (int k = sub; k < nb; k += kGeoLanes) {
-      const float t = d - off[k];
-      const float gk = expf(coeff * (t * t));
-      gd += gg[k] * (gk * (coeff * (2.f * t)));
+    const int sub = lane & 15, grp = lane >> 4;
+#pragma unroll 1
+    for (int s = 0; s < EPB / 16; ++s) {
+      const int loc = w * (EPB / 4) + s * 4 + grp;  // this 16-lane group's edge in the block
+      const int64_t e = eb + loc;
+      float acc = 0.f;
+      if (e < E) {
+        const float d = dist[e];
+        const float* gg = g_gauss + e * ldg;
+        if (V4) {
+          for (int k = 4 * sub; k < nb; k += 64) {
+            const floatx4 gv = *reinterpret_cast<const floatx4*>(gg + k);
+            const floatx4 ov = *reinterpret_cast<const floatx4*>(off + k);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float t = d - ov[q];
+              acc += gv[q] * (expf(coeff * (t * t)) * (coeff * (2.f * t)));
+            }
+          }
+        } else {
+          for (int k = sub; k < nb; k += 16) {
+            const float t = d - off[k];
+            acc += gg[k] * (expf(coeff * (t * t)) * (coeff * (2.f * t)));
+          }
+        }
+      }
+      acc += __shfl_xor(acc, 8, 64);
+      acc += __shfl_xor(acc, 4, 64);
+      acc += __shfl_xor(acc, 2, 64);
+      acc += __shfl_xor(acc, 1, 64);
+      if (sub == 0) sgd[loc] = acc;
     }
   }
-  gd += __shfl_xor(gd, 2, 64);
-  gd += __shfl_xor(gd, 1, 64);
+  __syncthreads();
+  if ((int)threadIdx.x >= EPB) return;
+  const int64_t e = eb + threadIdx.x;
+  if (e >= E) return;
+  float v[3] = {ev[e * 3], ev[e * 3 + 1], ev[e * 3 + 2]};
+  const float d = dist[e];
+  float gd = g_gauss ? sgd[threadIdx.x] : 0.f;
   if (g_env) gd += g_env[e] * tta_geo::envelope_grad(d, cutoff);
   float out[3] = {0.f, 0.f, 0.f};
   if (d > 0.f)
@@ -104,8 +137,7 @@ __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
     for (int k = 0; k < 35; ++k) gc[k] = g_coef[e * 35 + k];
     tta_geo::wigner_vjp(v, gamma, jl, gc, out);
   }
-  if (valid && sub == 0)
-    for (int k = 0; k < 3; ++k) g_ev[e * 3 + k] = out[k];
+  for (int k = 0; k < 3; ++k) g_ev[e * 3 + k] = out[k];
 }
 
 // F[n] = -(sum_{src(e) = n} g_ev[e] - sum_{tgt(e) = n} g_ev[e])   (ev = pos[src] - pos[tgt])
@@ -246,10 +278,20 @@ extern "C" int tta_edge_geometry_bwd(const float* ev, const float* dist, const f
   if (E == 0) return tta::kOk;
   TTA_CHECK_ARG(ev && dist && jd && g_ev, "tta_edge_geometry_bwd: null pointer");
   TTA_CHECK_ARG(!g_gauss || (offsets && ldg >= nb), "tta_edge_geometry_bwd: bad gaussian adjoint");
-  hipLaunchKernelGGL(k_edge_geometry_bwd, dim3(tta_blocks(E * kGeoLanes, 256)), dim3(256), 0,
-                     stream, ev, dist,
-                     g_coef, g_env, g_gauss, ldg, offsets, coeff, cutoff, (int)nb, jd, gamma, g_ev,
-                     (int)E);
+  // 256 edges per block (a full thread per edge in phase 2) once there are enough blocks to fill
+  // the GPU; small graphs take 64 per block for four times the blocks
+  const bool v4 = g_gauss && nb % 4 == 0 && ldg % 4 == 0 && (uintptr_t)g_gauss % 16 == 0 &&
+                  (uintptr_t)offsets % 16 == 0;
+  const bool wide = E >= 256 * 512;
+  auto launch = [&](auto kern, int epb) {
+    hipLaunchKernelGGL(kern, dim3(tta_blocks(E, epb)), dim3(256), 0, stream, ev, dist, g_coef,
+                       g_env, g_gauss, ldg, offsets, coeff, cutoff, (int)nb, jd, gamma, g_ev,
+                       (int)E);
+  };
+  if (wide)
+    v4 ? launch(k_edge_geometry_bwd<256, true>, 256) : launch(k_edge_geometry_bwd<256, false>, 256);
+  else
+    v4 ? launch(k_edge_geometry_bwd<64, true>, 64) : launch(k_edge_geometry_bwd<64, false>, 64);
   TTA_CHECK_LAUNCH("tta_edge_geometry_bwd");
   return tta::kOk;
 }

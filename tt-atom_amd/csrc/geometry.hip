@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (g_gauss) {
     const int sub = lane & 15, grp = lane >> 4;
-#pragma unroll 1
+#pragma unroll 2
     for (int s = 0; s < EPB / 16; ++s) {
       const int loc = w * (EPB / 4) + s * 4 + grp;  // this 16-lane group's edge in the block
       const int64_t e = eb + loc;
@@ -97,6 +97,8 @@ __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
         const float d = dist[e];
         const float* gg = g_gauss + e * ldg;
         if (V4) {
+          // unrolled so that several rows' loads are in flight before the exponentials
+#pragma unroll 8
           for (int k = 4 * sub; k < nb; k += 64) {
             const floatx4 gv = *reinterpret_cast<const floatx4*>(gg + k);
             const floatx4 ov = *reinterpret_cast<const floatx4*>(off + k);

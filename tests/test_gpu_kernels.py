@@ -105,7 +105,7 @@ def test_gemm_batched_strided(nat):
 
 @pytest.mark.parametrize("M,N,K", [(4100, 200, 196), (8192, 640, 768), (5000, 16, 1000),
                                    (40001, 1100, 128), (9000, 300, 36)])
-@pytest.mark.parametrize("epi", [0, 2, 3, 4])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
 @pytest.mark.parametrize("mode", [6, 16])
 def test_split_bf16_gemm_fp32_accuracy(nat, M, N, K, epi, mode):
     """Mode 6 (three bf16 planes, six products) and mode 16 (two scaled fp16 planes, three
@@ -120,7 +120,9 @@ def test_split_bf16_gemm_fp32_accuracy(nat, M, N, K, epi, mode):
     aux = torch.randn(M, N, generator=g)
     ref = (A.double() @ B.double()) + bias.double()
     scale = A.double().abs() @ B.double().abs() + 1.0
-    if epi == 2:
+    if epi == 1:
+        ref = torch.nn.functional.silu(ref)
+    elif epi == 2:
         ref = ref + C0.double()
     elif epi == 4:
         s = torch.sigmoid(aux.double())

@@ -135,7 +135,7 @@ __device__ __forceinline__ float epi_one(const GemmArgs& p, float v, int row, in
 // template parameter, so a row costs one LDS read, one address add and one 16-byte store.
 // vec_ok (host-checked 16-byte alignment of every operand row) selects the float4 path; full
 // (the tile lies inside M x N) drops the bounds checks.
-template <int EPI>
+template <int EPI, bool BATCH>
 __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct, int ldt,
                                               int rows, int row0, int n0, int t, int nth,
                                               bool vec_ok, bool full) {
@@ -145,6 +145,57 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
     const floatx4 bv = p.bias ? *reinterpret_cast<const floatx4*>(p.bias + col)
                               : floatx4{0.f, 0.f, 0.f, 0.f};
     const bool gather = p.P != nullptr;
+    constexpr bool LOADS = EPI == EPI_ACCUM || EPI == EPI_SILU_GRAD;
+    constexpr int RB = 8;
+    if (BATCH && full && (LOADS || gather) && rows % (RB * rstep) == 0) {
+      // An epilogue that reads memory (the accumulated C, the SiLU argument, the gathered rows;
+      // BATCH: mode 16, whose register budget has room for it)
+      // issues a batch of RB rows' loads -- the gather indices first, then the rows they name --
+      // before it uses any, so their latencies overlap instead of adding up row by row.
+#pragma unroll 1
+      for (int rb = t >> 5; rb < rows; rb += RB * rstep) {
+        int i0[RB], i1[RB];
+        floatx4 ex[RB], pv[RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+          const int row = row0 + rb + i * rstep;
+          if (gather) {
+            i0[i] = p.idx0[row];
+            i1[i] = p.idx1[row];
+          }
+          if constexpr (EPI == EPI_ACCUM)
+            ex[i] = *reinterpret_cast<const floatx4*>(p.C + (int64_t)row * p.ldc + col);
+          if constexpr (EPI == EPI_SILU_GRAD)
+            ex[i] = *reinterpret_cast<const floatx4*>(p.aux + (int64_t)row * p.ldc + col);
+        }
+        if (gather) {
+#pragma unroll
+          for (int i = 0; i < RB; ++i)
+            pv[i] = *reinterpret_cast<const floatx4*>(p.P + (int64_t)i0[i] * p.ldp + col) +
+                    *reinterpret_cast<const floatx4*>(p.P + (int64_t)i1[i] * p.ldp + p.off1 + col);
+        }
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+          const int rr = rb + i * rstep, row = row0 + rr;
+          floatx4 v = *reinterpret_cast<const floatx4*>(Ct + rr * ldt + 4 * c4) + bv;
+          const int64_t off = (int64_t)row * p.ldc + col;
+          if (gather) v += pv[i];
+          if constexpr (EPI == EPI_ACCUM) v += ex[i];
+          if constexpr (EPI == EPI_SILU || EPI == EPI_PRE_SILU || EPI == EPI_SILU_GRAD) {
+            floatx4 w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              w[e] = EPI == EPI_SILU_GRAD ? v[e] * tta_silu_grad(ex[i][e]) : tta_silu(v[e]);
+            if constexpr (EPI == EPI_PRE_SILU)
+              __builtin_nontemporal_store(w, reinterpret_cast<floatx4*>(p.C2 + off));
+            else
+              v = w;
+          }
+          __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(p.C + off));
+        }
+      }
+      return;
+    }
 #pragma unroll 4
     for (int rr = t >> 5; rr < rows; rr += rstep) {
       const int row = row0 + rr;
@@ -631,19 +682,19 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         switch (p.epi) {
           case EPI_SILU:
-            epilogue_rows<EPI_SILU>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            epilogue_rows<EPI_SILU, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
             break;
           case EPI_ACCUM:
-            epilogue_rows<EPI_ACCUM>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            epilogue_rows<EPI_ACCUM, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
             break;
           case EPI_PRE_SILU:
-            epilogue_rows<EPI_PRE_SILU>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            epilogue_rows<EPI_PRE_SILU, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
             break;
           case EPI_SILU_GRAD:
-            epilogue_rows<EPI_SILU_GRAD>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            epilogue_rows<EPI_SILU_GRAD, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
             break;
           default:
-            epilogue_rows<EPI_STORE>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            epilogue_rows<EPI_STORE, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
         }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       }

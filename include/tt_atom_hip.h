@@ -91,6 +91,18 @@ int tta_gather_rotate_bw(const float* g_xf, const float* rad, const float* x, co
                          const int* tgt, const float* coef, float* g_rad, float* g_mcat,
                          float* g_coef, int64_t N, int64_t E, int64_t C, tta_stream_t stream);
 
+/* tta_gather_rotate_bw (rad required) walked by destination node over the destination-sorted
+ * edges (tgt_ptr [N+1]): g_rad and g_coef as there; g_mcat gets its source half [.., 0:C] only,
+ * and tsum [N,9,C] = the destination half summed over each node's edges in edge order (zeros for
+ * a node without edges), bit-identical to tta_node_gather_sum's destination sum; g_coef's channel
+ * sum runs per half (equal to tta_gather_rotate_bw's to fp32 rounding).  C <= 256.  Same
+ * reference functions as tta_gather_rotate_bw plus the destination scatter of
+ * forces.py:384-412, whose [E,9,C] half it never writes. */
+int tta_gather_rotate_bw_dst(const float* g_xf, const float* rad, const float* x, const int* src,
+                             const int* tgt_ptr, const float* coef, float* g_rad, float* g_mcat,
+                             float* g_coef, float* tsum, int64_t N, int64_t E, int64_t C,
+                             tta_stream_t stream);
+
 /* Source-only variant: out[e, m, :] = sum_j W[e,m,j] x[src_e, j, :], out [E, 9, C] m-primed --
  * rotation.rotate (rotation.py:211-222) applied to source features gathered by edge (the C2
  * isolated-edgewise pipeline).  Its backward writes g_in[e] = W[e]^T g_out[e] (skipped when g_in
@@ -122,6 +134,12 @@ int tta_rotate_env_segsum_bw(const float* g_node, const int* tgt, const float* m
 int tta_node_gather_sum(const float* g_mcat, const int* src_ptr, const int* src_perm,
                         const int* tgt_ptr, const float* res, float* out, int64_t N, int64_t E,
                         int64_t C, tta_stream_t stream);
+
+/* tta_node_gather_sum with the destination sums given (tsum [N,9,C] from
+ * tta_gather_rotate_bw_dst): out[n] = (sum_{src(e)=n} g_mcat[e,:,0:C] + tsum[n]) + res[n]. */
+int tta_node_gather_sum_dst(const float* g_mcat, const int* src_ptr, const int* src_perm,
+                            const float* tsum, const float* res, float* out, int64_t N, int64_t E,
+                            int64_t C, tta_stream_t stream);
 
 /* ---------------------------------------------------------------- element / row-wise
  * Gate: y[r,0] = silu(x[r,0]); y[r,c] = x[r,c] sigmoid(gating[r, idx8[c-1]]).  x [R,9,H] rows of

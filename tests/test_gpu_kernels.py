@@ -361,6 +361,49 @@ def test_gather_rotate_fwd_bwd(nat, C):
     assert (gn.cpu().double() - gx).abs().max() < 1e-3
 
 
+@pytest.mark.parametrize("C", [16, 32, 64, 128])
+def test_gather_rotate_bw_dst_bit_equal(nat, C):
+    """The destination-walked backward (a block per node, the destination half of the adjoint
+    summed in registers) gives the same bits as the edge-walked kernel followed by the CSR node
+    sum for g_rad, the source half of g_mcat and the node adjoint, and the accumulated g_coef to
+    fp32 rounding (its channel sum runs per half, then adds the halves), on a graph with a
+    destination hub, nodes without incoming edges and isolated nodes."""
+    N, E = 60, 700
+    g = torch.Generator().manual_seed(C + 7)
+    tgt = torch.randint(0, N - 6, (E,), generator=g)
+    tgt[:200] = 5                                           # destination hub
+    tgt = torch.sort(tgt).values                            # edges sorted by destination
+    src = torch.randint(0, N - 3, (E,), generator=g)        # nodes N-3.. isolated
+    x = torch.randn(N, 9, C, generator=g)
+    coef = torch.randn(E, 35, generator=g)
+    rad = torch.randn(E, 6, 2 * C, generator=g)
+    gout = torch.randn(E, 9, 2 * C, generator=g)
+    gc0 = torch.randn(E, 35, generator=g)                   # g_coef is accumulated into
+    f = lambda t: t.to(DEV).contiguous()
+    sptr, perm, tptr = _csr(src, N), torch.argsort(src, stable=True), _csr(tgt, N)
+    outs = {}
+    for walk in ("edge", "dst"):
+        g_rad = torch.full((E, 6, 2 * C), float("nan"), device=DEV)
+        g_mcat = torch.zeros(E, 9, 2 * C, device=DEV)
+        g_coef = f(gc0.clone())
+        gn = torch.full((N, 9, C), float("nan"), device=DEV)
+        if walk == "edge":
+            nat.gather_rotate_bw(f(gout), f(rad), f(x), _i32(src), _i32(tgt), f(coef), g_rad,
+                                 g_mcat, g_coef)
+            nat.node_gather_sum(g_mcat, _i32(sptr), _i32(perm), _i32(tptr), None, gn)
+        else:
+            tsum = torch.full((N, 9, C), float("nan"), device=DEV)
+            nat.gather_rotate_bw_dst(f(gout), f(rad), f(x), _i32(src), _i32(tptr), f(coef), g_rad,
+                                     g_mcat, g_coef, tsum)
+            nat.node_gather_sum_dst(g_mcat, _i32(sptr), _i32(perm), tsum, None, gn)
+        torch.cuda.synchronize()
+        outs[walk] = (g_rad.cpu(), g_mcat.cpu()[:, :, :C], gn.cpu(), g_coef.cpu())
+    for a, b in zip(outs["edge"][:3], outs["dst"][:3]):
+        assert torch.equal(a, b)
+    ga, gb = outs["edge"][3].double(), outs["dst"][3].double()
+    assert ((ga - gb).abs() / (ga.abs() + 1.0)).max() < 1e-5
+
+
 @pytest.mark.parametrize("C", [16, 128, 256, 1024])
 def test_node_gather_sum_order_and_hubs(nat, C):
     """Every node's sum is bit-equal to a plain fp32 loop in edge order (src edges in the

@@ -276,6 +276,85 @@ __global__ __launch_bounds__(256) void k_gather_rotate_bw(
   if (lane < NNZ) g_coef[(int64_t)e * NNZ + lane] += tot;
 }
 
+// k_gather_rotate_bw walked by destination: a 128-thread block per node n goes over its edges
+// [tgt_ptr[n], tgt_ptr[n+1]) (edges sorted by destination); wave 0 takes the source half of the
+// channels (x[src_e] rows), wave 1 the destination half (x[n] rows).  Per edge as
+// k_gather_rotate_bw (RAD, two halves), except that the destination half of the adjoint g_mcat
+// is not stored: wave 1 sums it over the node's edges in ascending order from zero -- the order
+// of k_node_gather_sum's destination loop, so the sum is bit-identical -- and writes it to
+// tsum[n] [9, C] (zeros for a node without edges).  The coefficient adjoint of an edge is each
+// wave's channel sum, the two added in wave order (source half first).  Every channel of a half
+// sits in one lane vector (C / V <= 64).
+template <int V>
+__global__ __launch_bounds__(128) void k_gather_rotate_bw_dst(
+    const float* __restrict__ g_xf, const float* __restrict__ rad, const float* __restrict__ x,
+    const int* __restrict__ src, const int* __restrict__ tgt_ptr, const float* __restrict__ coef,
+    float* __restrict__ g_rad, float* __restrict__ g_mcat, float* __restrict__ g_coef,
+    float* __restrict__ tsum, int N, int C) {
+  typedef typename VecT<V>::T T;
+  __shared__ float red[2][NNZ * 4];
+  __shared__ float half1[NNZ];
+  const int lane = threadIdx.x & 63;
+  const int h = threadIdx.x >> 6;  // channel half: 0 source, 1 destination
+  const int n = blockIdx.x;
+  if (n >= N) return;
+  const int W = 2 * C, cq = C / V, q = lane;
+  const bool active = q < cq;
+  const int e0 = tgt_ptr[n], e1 = tgt_ptr[n + 1];
+  const int co = h * C + V * q;  // this lane's first channel within a 2C row
+  T b[NSPH];
+#pragma unroll
+  for (int j = 0; j < NSPH; ++j) b[j] = zv<V>();
+  for (int e = e0; e < e1; ++e) {
+    float c[NNZ];
+    load_coef(coef, e, c);
+    float gc[NNZ];
+#pragma unroll
+    for (int k = 0; k < NNZ; ++k) gc[k] = 0.f;
+    const float gco = (h == 0 && lane < NNZ) ? g_coef[(int64_t)e * NNZ + lane] : 0.f;
+    if (active) {
+      const int64_t s = wave_uniform(src[e]);
+      const int64_t eo = (int64_t)e * NSPH * W;
+      const float* row = h == 0 ? x + s * NSPH * C + V * q : x + (int64_t)n * NSPH * C + V * q;
+      T in[NSPH], gm[NSPH], mr[NSPH];
+#pragma unroll
+      for (int j = 0; j < NSPH; ++j) in[j] = ldv<V>(row + j * C);
+#pragma unroll
+      for (int m = 0; m < NSPH; ++m) gm[m] = ldv_nt<V>(g_xf + eo + m * W + co);
+      rot_fwd(c, in, mr);
+      float* grp = g_rad + (int64_t)e * 6 * W + co;
+      stv<V>(grp + 0 * W, gm[0] * mr[0]);
+      stv<V>(grp + 1 * W, gm[1] * mr[1]);
+      stv<V>(grp + 2 * W, gm[2] * mr[2]);
+      stv<V>(grp + 3 * W, gm[3] * mr[3] + gm[5] * mr[5]);
+      stv<V>(grp + 4 * W, gm[4] * mr[4] + gm[6] * mr[6]);
+      stv<V>(grp + 5 * W, gm[7] * mr[7] + gm[8] * mr[8]);
+      const float* rp = rad + (int64_t)e * 6 * W + co;
+#pragma unroll
+      for (int m = 0; m < NSPH; ++m) gm[m] = gm[m] * ldv_nt<V>(rp + rad_block(m) * W);
+      T gi[NSPH];
+      rot_inv<9>(c, gm, gi);
+      if (h == 1) {
+#pragma unroll
+        for (int j = 0; j < NSPH; ++j) b[j] = b[j] + gi[j];
+      } else {
+#pragma unroll
+        for (int j = 0; j < NSPH; ++j) stv<V>(g_mcat + eo + j * W + co, gi[j]);
+      }
+      coef_partials<9, V>(gm, in, gc);
+    }
+    const float tot = wave_sums<NNZ>(gc, red[h], lane);
+    if (h == 1 && lane < NNZ) half1[lane] = tot;
+    __syncthreads();
+    if (h == 0 && lane < NNZ) g_coef[(int64_t)e * NNZ + lane] = gco + (tot + half1[lane]);
+    __syncthreads();
+  }
+  if (h == 1 && active) {
+#pragma unroll
+    for (int j = 0; j < NSPH; ++j) stv<V>(tsum + (int64_t)n * NSPH * C + j * C + V * q, b[j]);
+  }
+}
+
 // -------------------------------------------------------------------------------------------
 // Inverse rotation + envelope + destination-sorted segmented sum (+ residual):
 //   out[n, j, :] = res[n, j, :] + sum_{e in [ptr[n], ptr[n+1])} contrib_e[j, :]
@@ -414,14 +493,16 @@ template <int V>
 __global__ __launch_bounds__(256) void k_node_gather_sum(
     const float* __restrict__ g_mcat, const int* __restrict__ src_ptr,
     const int* __restrict__ src_perm, const int* __restrict__ tgt_ptr,
-    const float* __restrict__ res, float* __restrict__ out, int N, int C) {
+    const float* __restrict__ res, float* __restrict__ out, int N, int C,
+    const float* __restrict__ tsum = nullptr) {
   typedef typename VecT<V>::T T;
   const int lane = threadIdx.x & 63;
   const int n = wave_uniform(blockIdx.x * WAVES + (threadIdx.x >> 6));
   if (n >= N) return;
   const int W = 2 * C, nq = C / V;
   const int s0 = wave_uniform(src_ptr[n]), s1 = wave_uniform(src_ptr[n + 1]);
-  const int t0 = wave_uniform(tgt_ptr[n]), t1 = wave_uniform(tgt_ptr[n + 1]);
+  const int t0 = tgt_ptr ? wave_uniform(tgt_ptr[n]) : 0;
+  const int t1 = tgt_ptr ? wave_uniform(tgt_ptr[n + 1]) : 0;
   for (int q = lane; q < nq; q += 64) {
     T a[NSPH], b[NSPH];
 #pragma unroll
@@ -431,9 +512,15 @@ __global__ __launch_bounds__(256) void k_node_gather_sum(
 #pragma unroll
       for (int j = 0; j < NSPH; ++j) a[j] = a[j] + ldv<V>(g_mcat + e * NSPH * W + j * W + V * q);
     }
-    for (int64_t e = t0; e < t1; ++e) {
+    if (tsum) {  // the destination sums, already formed by k_gather_rotate_bw_dst
 #pragma unroll
-      for (int j = 0; j < NSPH; ++j) b[j] = b[j] + ldv<V>(g_mcat + e * NSPH * W + j * W + C + V * q);
+      for (int j = 0; j < NSPH; ++j) b[j] = ldv<V>(tsum + (int64_t)n * NSPH * C + j * C + V * q);
+    } else {
+      for (int64_t e = t0; e < t1; ++e) {
+#pragma unroll
+        for (int j = 0; j < NSPH; ++j)
+          b[j] = b[j] + ldv<V>(g_mcat + e * NSPH * W + j * W + C + V * q);
+      }
     }
 #pragma unroll
     for (int j = 0; j < NSPH; ++j) {
@@ -515,6 +602,29 @@ extern "C" int tta_gather_rotate_bw(const float* g_xf, const float* rad, const f
                          (int)C);
   });
   TTA_CHECK_LAUNCH("tta_gather_rotate_bw");
+  return tta::kOk;
+}
+
+extern "C" int tta_gather_rotate_bw_dst(const float* g_xf, const float* rad, const float* x,
+                                        const int* src, const int* tgt_ptr, const float* coef,
+                                        float* g_rad, float* g_mcat, float* g_coef, float* tsum,
+                                        int64_t N, int64_t E, int64_t C, hipStream_t stream) {
+  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C / pick_v(C) <= 64,
+                "tta_gather_rotate_bw_dst: channel count C=%lld needs C / V <= 64 (C <= 256)",
+                (long long)C);
+  TTA_CHECK_ARG(E >= 0 && N >= 0 && E < (1ll << 31) && N < (1ll << 31),
+                "tta_gather_rotate_bw_dst: bad sizes");
+  if (N == 0) return tta::kOk;
+  TTA_CHECK_ARG(tgt_ptr && tsum && (E == 0 || (g_xf && rad && x && src && coef && g_rad &&
+                                                g_mcat && g_coef)),
+                "tta_gather_rotate_bw_dst: null pointer");
+  const int V = pick_v(C);
+  TTA_V_DISPATCH(V, {
+    hipLaunchKernelGGL((k_gather_rotate_bw_dst<VV>), dim3((unsigned)N), dim3(128), 0, stream,
+                       g_xf, rad, x, src, tgt_ptr, coef, g_rad, g_mcat, g_coef, tsum, (int)N,
+                       (int)C);
+  });
+  TTA_CHECK_LAUNCH("tta_gather_rotate_bw_dst");
   return tta::kOk;
 }
 
@@ -617,6 +727,25 @@ extern "C" int tta_rotate_env_segsum_bw(const float* g_node, const int* tgt, con
                          div);
   });
   TTA_CHECK_LAUNCH("tta_rotate_env_segsum_bw");
+  return tta::kOk;
+}
+
+extern "C" int tta_node_gather_sum_dst(const float* g_mcat, const int* src_ptr,
+                                       const int* src_perm, const float* tsum, const float* res,
+                                       float* out, int64_t N, int64_t E, int64_t C,
+                                       hipStream_t stream) {
+  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C <= 4096,
+                "tta_node_gather_sum_dst: unsupported channel count C=%lld", (long long)C);
+  TTA_CHECK_ARG(N >= 0 && E >= 0 && N < (1ll << 31), "tta_node_gather_sum_dst: bad sizes");
+  if (N == 0) return tta::kOk;
+  TTA_CHECK_ARG(src_ptr && src_perm && tsum && out && (g_mcat || E == 0),
+                "tta_node_gather_sum_dst: null pointer");
+  const int V = pick_v(C);
+  TTA_V_DISPATCH(V, {
+    hipLaunchKernelGGL((k_node_gather_sum<VV>), dim3(wave_blocks(N)), dim3(256), 0, stream,
+                       g_mcat, src_ptr, src_perm, nullptr, res, out, (int)N, (int)C, tsum);
+  });
+  TTA_CHECK_LAUNCH("tta_node_gather_sum_dst");
   return tta::kOk;
 }
 

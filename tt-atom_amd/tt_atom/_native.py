@@ -42,6 +42,8 @@ _SIGS = {
     "tta_gemm_f32": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                      _I64, _I64, _I64, _I, _P],
     "tta_gather_rotate": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "tta_gather_rotate_bw_dst": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "tta_node_gather_sum_dst": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_gather_rotate_bw": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_rotate_env_segsum": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _F, _P],
     "tta_rotate_env_segsum_bw": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _F,
@@ -467,6 +469,36 @@ def gather_rotate_bw(g_xf, rad, x, src, tgt, coef, g_rad, g_mcat, g_coef):
               _ptr(g_rad, numel=E * 12 * C, name="g_rad"), _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
               _ptr(g_coef, numel=E * 35, name="g_coef"), N, E, C, _stream(),
               compulsory=E * edge + 4 * N * 9 * C)
+
+
+def gather_rotate_bw_dst(g_xf, rad, x, src, tgt_ptr, coef, g_rad, g_mcat, g_coef, tsum):
+    """gather_rotate_bw walked by destination node (edges sorted by destination, tgt_ptr their
+    CSR offsets): g_mcat gets its source half only, and tsum [N, 9, C] receives the destination
+    half already summed per node (the sum node_gather_sum would form, bit for bit).  C <= 256."""
+    N, _, C = x.shape
+    E = src.numel()
+    edge = 4 * (18 * C + 24 * C + 35 + 70 + 9 * C) + 4
+    _hbm_call("k_gather_rotate_bw_dst", E * (edge + 4 * 9 * C) + 4 * N * 9 * C,
+              "tta_gather_rotate_bw_dst",
+              _ptr(g_xf, numel=E * 18 * C, name="g_xf"), _ptr(rad, numel=E * 12 * C, name="rad"),
+              _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E), _i32(tgt_ptr, N + 1, "tgt_ptr"),
+              _ptr(coef, numel=E * 35, name="coef"), _ptr(g_rad, numel=E * 12 * C, name="g_rad"),
+              _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"), _ptr(g_coef, numel=E * 35, name="g_coef"),
+              _ptr(tsum, numel=N * 9 * C, name="tsum"), N, E, C, _stream(),
+              compulsory=E * edge + 4 * N * 9 * C * 2)
+
+
+def node_gather_sum_dst(g_mcat, src_ptr, src_perm, tsum, res, out):
+    """node_gather_sum with the destination sums precomputed (tsum from gather_rotate_bw_dst)."""
+    N, _, C = out.shape
+    E = src_perm.numel()
+    nbytes = 4 * (E * 9 * C + (N + 1) + E + N * 9 * C * (2 + (res is not None)))
+    _hbm_call("k_node_gather_sum", nbytes, "tta_node_gather_sum_dst",
+              _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
+              _i32(src_ptr, N + 1, "src_ptr"), _i32(src_perm, E, "src_perm"),
+              _ptr(tsum, numel=N * 9 * C, name="tsum"), _ptr(res, numel=N * 9 * C, name="res"),
+              _ptr(out, numel=N * 9 * C, name="out"), N, E, C, _stream())
+    return out
 
 
 def rotate_env_segsum(m, coef, env, tgt_ptr, res, out, *, n_in, env_first, div=1.0):

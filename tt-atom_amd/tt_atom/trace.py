@@ -91,6 +91,7 @@ class TracedEngine:
         self.LHc = L * H + NSPH * H                      # combined conv-1 row [gating | out]
         self.xf, self.g_xf, self.g_mcat = emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C)
         self.y, self.g_y = emp(E, NSPH, H), emp(E, NSPH, H)
+        self.g_tsum = emp(N, NSPH, C)                    # per-node destination adjoint sums
         self.g1c = emp(E, self.LHc)
         self.g_mso2 = emp(E, NSPH, C)
         # per-radial output caches and their adjoints (kept per block: the radial backward of all
@@ -333,9 +334,16 @@ class TracedEngine:
         nat.linear_group([(g1[:, :LH + 3 * H], s1w.wm0, None, gx[:, :3 * Cin]),
                           (g1[:, LH + 3 * H:LH + 7 * H], s1w.w1_t, None, gx[:, 3 * Cin:7 * Cin]),
                           (g1[:, LH + 7 * H:], s1w.w2_t, None, gx[:, 7 * Cin:])])
-        nat.gather_rotate_bw(self.g_xf, c.rad.out, c.n1, g.src, g.tgt, self.coef, c.rad.g_out,
-                             self.g_mcat, self.g_coef)
-        nat.node_gather_sum(self.g_mcat, g.src_ptr, g.src_perm, g.tgt_ptr, None, g_n1)
+        if self.C <= 256:
+            # walked by destination: the destination half of the adjoint is summed per node in
+            # the rotation backward instead of crossing HBM twice as [E, 9, C]
+            nat.gather_rotate_bw_dst(self.g_xf, c.rad.out, c.n1, g.src, g.tgt_ptr, self.coef,
+                                     c.rad.g_out, self.g_mcat, self.g_coef, self.g_tsum)
+            nat.node_gather_sum_dst(self.g_mcat, g.src_ptr, g.src_perm, self.g_tsum, None, g_n1)
+        else:
+            nat.gather_rotate_bw(self.g_xf, c.rad.out, c.n1, g.src, g.tgt, self.coef,
+                                 c.rad.g_out, self.g_mcat, self.g_coef)
+            nat.node_gather_sum(self.g_mcat, g.src_ptr, g.src_perm, g.tgt_ptr, None, g_n1)
 
     def _backward_fused(self):
         """Reverse of the fused forward: the energy head's adjoint, then per block (last first) the

@@ -145,11 +145,11 @@ def test_split_bf16_gemm_fp32_accuracy(nat, M, N, K, epi, mode):
 def test_split_gemm_persistent_tiles(nat, mode, tol):
     """More tiles than resident blocks: every block of the split kernel walks several tiles
     (70001 x 700 -> 547 x 6 tiles of 128 x 128 over at most two blocks per compute unit), with a
-    ragged last row tile and column tile and a K (100) that ends inside a 32-wide slab; plus a
+    ragged last row tile and column tile and a K (164) that ends inside a 32-wide slab; plus a
     grouped launch whose two products have different tile counts.  Error relative to |A| |B| as
     the mode's planes allow (bf16: 2^-8; two bf16 planes: 2^-16; fp32-accurate modes 6 / 16)."""
     g = torch.Generator().manual_seed(70 + mode)
-    M, N, K = 70001, 700, 100
+    M, N, K = 70001, 700, 164
     A = torch.randn(M, K, generator=g)
     B = torch.randn(K, N, generator=g) / math.sqrt(K)
     bias = torch.randn(N, generator=g)
@@ -168,6 +168,53 @@ def test_split_gemm_persistent_tiles(nat, mode, tol):
     assert torch.equal(out_g, out)
     assert torch.equal(small.cpu(), (out - bias.to(DEV))[:5000].cpu()) or \
         ((small.cpu().double() - (ref - bias.double())[:5000]).abs() / scale[:5000]).max() < tol
+
+
+@pytest.mark.parametrize("K", [128, 100, 36])
+@pytest.mark.parametrize("epi", [0, 1])
+def test_split_gemm_short_k_panel(nat, K, epi):
+    """Short-K mode-16 products (K <= 128, at least three 128-column tiles, plain or SiLU
+    epilogue) run on the panel kernel: a workgroup splits a 256-row panel of A once and sweeps a
+    run of column tiles.  K = 128 goes through linear_group as the radial output layer does (two
+    products of different widths: 1536 = two runs of six tiles, 1100 = nine tiles with a ragged
+    last one); the K that end inside a 32-wide slab through the C entry point.  Ragged rows
+    (20001 = 78 panels + 33 rows), and rows whose scale leaves the unscaled window (max 2^20,
+    2^-12 and 2^-30 times the rest, an all-zero row).  Error at fp32 level, each row's against
+    its own |A| |B|."""
+    g = torch.Generator().manual_seed(K + 7 * epi)
+    M1, M2 = 20001, 6000
+    A1 = torch.randn(M1, K, generator=g)
+    B1 = torch.randn(K, 1536, generator=g) / math.sqrt(K)
+    bias1 = torch.randn(1536, generator=g)
+    A2 = torch.randn(M2, K, generator=g)
+    A2[5] *= 2.0 ** 20
+    A2[300] *= 2.0 ** -12
+    A2[301] *= 2.0 ** -30
+    A2[302] = 0.0
+    A2[M2 - 1, : K // 2] *= 1e3
+    B2 = torch.randn(K, 1100, generator=g) / math.sqrt(K)
+    pw1, pw2 = nat.PackedWeight(B1.to(DEV), 16), nat.PackedWeight(B2.to(DEV), 16)
+    o1 = torch.full((M1, 1536), float("nan"), device=DEV)
+    o2 = torch.full((M2, 1100), float("nan"), device=DEV)
+    if K == 128:
+        nat.linear_group([(A1.to(DEV), pw1, bias1.to(DEV), o1, epi),
+                          (A2.to(DEV), pw2, None, o2, epi)])
+    else:
+        nat._gemm_bf16x(A1.to(DEV), pw1, o1, bias1.to(DEV), epi, None, None)
+        nat._gemm_bf16x(A2.to(DEV), pw2, o2, None, epi, None, None)
+    for A, B, bias, o in ((A1, B1, bias1, o1), (A2, B2, None, o2)):
+        ref = A.double() @ B.double()
+        mag = A.double().abs() @ B.double().abs()
+        if bias is not None:
+            ref = ref + bias.double()
+            mag = mag + bias.double().abs()
+        if epi == 1:
+            ref = torch.nn.functional.silu(ref)
+        out = o.cpu().double()
+        assert torch.isfinite(out).all()
+        err = (out - ref).abs() / mag.clamp_min(1e-300)
+        err[mag == 0] = (out - ref).abs()[mag == 0]
+        assert err.max().item() < 2e-6, (err.max(dim=1).values.argmax().item(), err.max().item())
 
 
 def test_split_bf16_gemm_modes_and_gather(nat):

@@ -735,6 +735,242 @@ __global__ __launch_bounds__(256) void k_pack_b(const float* __restrict__ B, int
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Short-K mode-16 products (K <= 128; plain or SiLU epilogue): the panel kernel.
+//
+// The tiled kernel splits a tile's A fragments once per 128-column tile, so on short-K, wide-N
+// products (the radial output layer, 61440 x 1536 x 128) every tile pays the A split, a prologue
+// and an LDS-staged epilogue for a k loop of four steps.  Here a workgroup of PW waves owns a
+// panel of 32 PW rows and a run of 128-column tiles.  Each wave loads its 32 rows once, takes each
+// row's scale over the whole of K (E = 0 while the row max is in [2^-1, 2^15), else the max lands
+// below 2^kTop, as in the tiled kernel) and keeps the two fp16 planes in registers for the whole
+// run, while the packed B tiles, with their column exponents and bias, stream through a
+// double-buffered LDS stage.  Each output tile is computed transposed, D^T = B^T A^T: the packed B
+// fragment is the MFMA's first operand and the A planes its second, so accumulator elements
+// 4g .. 4g + 3 of lane l are four consecutive columns of row l % 32 and the epilogue stores float4
+// straight from registers.
+constexpr int PW = 8;            // waves per panel workgroup
+constexpr int PROWS = 32 * PW;   // rows per panel
+constexpr int PSTR = 36;         // row stride (floats) of a wave's 32 x 32 output staging block
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+template <int KT>
+__global__ __launch_bounds__(64 * PW, 1) void gemm_f16x3_panel(GemmGroup g, int run) {
+  typedef f16x8 V8;
+  const GemmArgs& p = g.p[blockIdx.z];
+  const int NT32 = g.NT32[blockIdx.z];
+  const int ntile = NT32 / 4;  // 128-column tiles of the padded packed B
+  const int nrun = (ntile + run - 1) / run;
+  const int npanel = (p.M + PROWS - 1) / PROWS;
+  if ((int)blockIdx.x >= npanel * nrun) return;
+  const int panel = (int)blockIdx.x / nrun;
+  const int t0 = ((int)blockIdx.x % nrun) * run, t1 = min(ntile, t0 + run);
+  constexpr int S = 2 * KT;        // 16-wide k steps
+  constexpr int TCH = KT * 1024;   // 16-byte chunks of one B tile: [kt][plane][n32 (4)][ks][lane]
+  // the output staging blocks (PW x 32 x PSTR floats) reuse the B tile the MFMAs have finished
+  constexpr int BCH = TCH > PW * 8 * PSTR ? TCH : PW * 8 * PSTR;
+  __shared__ u32x4 bs[2][BCH];
+  __shared__ u32x4 fb[2][64];      // per tile: the column exponents F, then the bias
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const u32x4* Bp = static_cast<const u32x4*>(p.B);
+  const int* Fc = reinterpret_cast<const int*>(Bp + (int64_t)KT * 2 * NT32 * 128);
+  const bool silu = p.epi == EPI_SILU;
+
+  // B tile nt: chunk c = 2 kt + plane holds the four n32 column blocks of the tile contiguously
+  // (8 KB), thread tid copying 16 bytes of each.  Wave 0 also takes F (lanes 0..31) and the bias
+  // (lanes 32..63) in one load whose address is chosen per lane (a lane without a bias value
+  // reads F and zeroes it when it stashes): a single destination register set, so that no
+  // masked half overwrites registers the other half's load is still filling.
+  u32x4 pre[2 * KT];
+  u32x4 pfb = u32x4{0u, 0u, 0u, 0u};
+  bool pz = false;
+  auto fetch = [&](int nt) {
+#pragma unroll
+    for (int c = 0; c < 2 * KT; ++c) pre[c] = Bp[((int64_t)c * NT32 + 4 * nt) * 128 + tid];
+    if (wave == 0) {
+      const int n = nt * 128 + 4 * (lane - 32);
+      const bool bok = lane >= 32 && p.bias != nullptr && n < p.N;
+      const void* src = bok ? static_cast<const void*>(p.bias + n)
+                            : static_cast<const void*>(Fc + nt * 128 + 4 * (lane & 31));
+      pfb = *static_cast<const u32x4*>(src);
+      pz = lane >= 32 && !bok;
+    }
+  };
+  auto stash = [&](int b) {
+#pragma unroll
+    for (int c = 0; c < 2 * KT; ++c) bs[b][c * 512 + tid] = pre[c];
+    if (wave == 0) fb[b][lane] = pz ? u32x4{0u, 0u, 0u, 0u} : pfb;
+  };
+
+  // this lane's row: A[row][16 s + 8 (lane / 32) + e], e = 0..7, is the MFMA's second operand
+  const int row = panel * PROWS + wave * 32 + (lane & 31);
+  const bool rok = row < p.M;
+  floatx4 xa[S][2];
+  {
+    const float* ar = p.A + (int64_t)(rok ? row : 0) * p.lda;
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k = 16 * st + 8 * (lane >> 5) + 4 * h;
+        xa[st][h] = (rok && k < p.K) ? *reinterpret_cast<const floatx4*>(ar + k)
+                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+  }
+  fetch(t0);
+  float mx = 0.f;
+#pragma unroll
+  for (int st = 0; st < S; ++st)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      mx = max3_abs(xa[st][h][0], xa[st][h][1], mx);
+      mx = max3_abs(xa[st][h][2], xa[st][h][3], mx);
+    }
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const int sh =
+      (mx > 0.f && !(mx >= 0.5f && mx < 32768.f)) ? __builtin_amdgcn_frexp_expf(mx) - kTop : 0;
+  V8 ap[S][2];
+#pragma unroll
+  for (int st = 0; st < S; ++st) split8_f16<2>(xa[st][0], xa[st][1], sh, ap[st]);
+  stash(0);
+  if (t0 + 1 < t1) fetch(t0 + 1);
+  __syncthreads();
+
+  const bool full_rows = (panel + 1) * PROWS <= p.M;
+  const int c4 = lane & 7, r8 = lane >> 3, cl = 4 * (lane >> 5);
+  float* const cw = p.C + (int64_t)(panel * PROWS + wave * 32) * p.ldc;  // the wave's first row
+  for (int nt = t0; nt < t1; ++nt) {
+    const int b = (nt - t0) & 1;
+    const bool more = nt + 1 < t1;
+    floatx16 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+    const u32x4* bt = bs[b];
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+      const int kt = st >> 1, ks = st & 1;
+      // the three products of mode 16, smallest first: a1 b0, a0 b1, a0 b0 (one column block's
+      // B fragments live at a time: the register budget of two waves per SIMD)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const V8 b0 = __builtin_bit_cast(V8, bt[(2 * kt) * 512 + j * 128 + ks * 64 + lane]);
+        const V8 b1 = __builtin_bit_cast(V8, bt[(2 * kt + 1) * 512 + j * 128 + ks * 64 + lane]);
+        acc[j] = mfma32(b0, ap[st][1], acc[j]);
+        acc[j] = mfma32(b1, ap[st][0], acc[j]);
+        acc[j] = mfma32(b0, ap[st][0], acc[j]);
+      }
+    }
+    __syncthreads();  // every wave is done reading B tile b: it becomes the staging area
+    // Tile nt + 1 (fetched before the stores of tile nt - 1) goes to LDS, and tile nt + 2 is
+    // fetched before this tile's stores are issued.  Memory operations complete in issue order,
+    // so waiting for a fetch waits for the stores issued before it: those of the tile before
+    // last, which have had a whole tile to drain.
+    if (more) stash(b ^ 1);
+    // vmcnt(0): after a stash nothing of this thread's is in flight (its LDS writes waited for
+    // every load).  Said explicitly, the compiler's wait insertion stops carrying the F / bias
+    // load past the `more` branches (it cannot tell that they agree) and no longer waits out the
+    // stores of the tile before reusing its registers at the next fetch.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    if (nt + 2 < t1) fetch(nt + 2);
+    // C = acc * 2^(E + F[col]) + bias (element 4 q + i of acc[j] is column 32 j + 8 q + cl + i),
+    // through LDS one 32 x 32 block at a time: the scaled accumulators go in by rows of the MFMA
+    // layout and come back as 128-byte row segments, so that a store instruction writes eight
+    // whole rows' lines instead of 32-byte pieces of 32 rows.
+    const int4* fbi = reinterpret_cast<const int4*>(fb[b]);
+    const floatx4* fbb = reinterpret_cast<const floatx4*>(fb[b] + 32);
+    float* stg = reinterpret_cast<float*>(bs[b]) + wave * 32 * PSTR;
+    const bool full = full_rows && (nt + 1) * 128 <= p.N;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = 8 * q + cl;
+        const int4 f = fbi[(32 * j + c) >> 2];
+        floatx4 v;
+        v[0] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 0], sh + f.x);
+        v[1] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 1], sh + f.y);
+        v[2] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 2], sh + f.z);
+        v[3] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 3], sh + f.w);
+        *reinterpret_cast<floatx4*>(stg + (lane & 31) * PSTR + c) = v;
+      }
+      const int n = nt * 128 + 32 * j + 4 * c4;
+      const floatx4 bv = fbb[(32 * j + 4 * c4) >> 2];
+      floatx4 v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v[i] = *reinterpret_cast<const floatx4*>(stg + (r8 + 8 * i) * PSTR + 4 * c4) + bv;
+        if (silu) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[i][e] = tta_silu(v[i][e]);
+        }
+      }
+      if (full) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          __builtin_nontemporal_store(
+              v[i], reinterpret_cast<floatx4*>(cw + (int64_t)(r8 + 8 * i) * p.ldc + n));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rr = r8 + 8 * i;
+          if (panel * PROWS + wave * 32 + rr < p.M && n < p.N)
+            __builtin_nontemporal_store(
+                v[i], reinterpret_cast<floatx4*>(cw + (int64_t)rr * p.ldc + n));
+        }
+      }
+    }
+    __syncthreads();  // tile b ^ 1 is in LDS; every wave is done with its staging block
+  }
+}
+
+// The panel kernel takes a mode-16 group whose products all have one KT = ceil(K / 32) <= 4, the
+// plain or SiLU epilogue, no row gathers, float4-aligned outputs and at least three 128-column
+// tiles; runs of at most kPanelRun column tiles keep several workgroups per compute unit.
+constexpr int kPanelRun = 12;
+
+bool panel_ok(const GemmGroup& g, int n) {
+  const int kt = (g.p[0].K + 31) / 32;
+  if (kt < 1 || kt > 4) return false;
+  for (int i = 0; i < n; ++i) {
+    const GemmArgs& p = g.p[i];
+    if ((p.K + 31) / 32 != kt || p.P || !g.vec[i] || (p.epi != EPI_STORE && p.epi != EPI_SILU) ||
+        p.N < 3 * BN)
+      return false;
+  }
+  return true;
+}
+
+int launch_panel(GemmGroup& g, int n, hipStream_t s) {
+  int64_t grid = 0;
+  int run = 1;
+  for (int i = 0; i < n; ++i) {
+    const int ntile = g.NT32[i] / 4;
+    const int nr = (ntile + kPanelRun - 1) / kPanelRun;
+    run = std::max(run, (ntile + nr - 1) / nr);
+  }
+  for (int i = 0; i < n; ++i) {
+    const int64_t nrun = (g.NT32[i] / 4 + run - 1) / run;
+    grid = std::max(grid, (int64_t)tta_blocks(g.p[i].M, PROWS) * nrun);
+  }
+  if (grid > (1ll << 30)) {
+    tta::set_error("tta_gemm_bf16x: grid too large");
+    return tta::kBadArgument;
+  }
+  const dim3 gd((unsigned)grid, 1, (unsigned)n), bd(64 * PW);
+  switch ((g.p[0].K + 31) / 32) {
+    case 1: hipLaunchKernelGGL(gemm_f16x3_panel<1>, gd, bd, 0, s, g, run); break;
+    case 2: hipLaunchKernelGGL(gemm_f16x3_panel<2>, gd, bd, 0, s, g, run); break;
+    case 3: hipLaunchKernelGGL(gemm_f16x3_panel<3>, gd, bd, 0, s, g, run); break;
+    default: hipLaunchKernelGGL(gemm_f16x3_panel<4>, gd, bd, 0, s, g, run); break;
+  }
+  TTA_CHECK_LAUNCH("tta_gemm_bf16x");
+  return tta::kOk;
+}
+
 // mode 16, B side: F[n] = frexp exponent of column n's max |b| minus kTop (0 for an all-zero or
 // padding column).  A block of 64 columns x 16 k-strided lanes, reduced through LDS.
 __global__ __launch_bounds__(1024) void k_col_exp(const float* __restrict__ B, int K, int N,
@@ -830,7 +1066,7 @@ int launch_mode(GemmGroup& g, int n, int mode, hipStream_t s) {
   switch (mode) {
     case 1: return launch_bf16x<2, 1>(g, n, s);
     case 3: return launch_bf16x<2, 3>(g, n, s);
-    case 16: return launch_bf16x<2, 16>(g, n, s);
+    case 16: return panel_ok(g, n) ? launch_panel(g, n, s) : launch_bf16x<2, 16>(g, n, s);
     default: return launch_bf16x<2, 6>(g, n, s);
   }
 }

@@ -744,19 +744,27 @@ __global__ __launch_bounds__(256) void k_pack_b(const float* __restrict__ B, int
 // panel of 32 PW rows and a run of 128-column tiles.  Each wave loads its 32 rows once, takes each
 // row's scale over the whole of K (E = 0 while the row max is in [2^-1, 2^15), else the max lands
 // below 2^kTop, as in the tiled kernel) and keeps the two fp16 planes in registers for the whole
-// run, while the packed B tiles, with their column exponents and bias, stream through a
-// double-buffered LDS stage.  Each output tile is computed transposed, D^T = B^T A^T: the packed B
-// fragment is the MFMA's first operand and the A planes its second, so accumulator elements
-// 4g .. 4g + 3 of lane l are four consecutive columns of row l % 32 and the epilogue stores float4
-// straight from registers.
-constexpr int PW = 8;            // waves per panel workgroup
+// run.  The packed B tiles, their column exponents and the bias reach LDS by direct copies
+// (buffer_load ... lds, no register round trip; F and the bias through registers).  Each output tile is computed transposed,
+// D^T = B^T A^T: the packed B fragment is the MFMA's first operand and the A planes its second, so
+// accumulator elements 4g .. 4g + 3 of lane l are four consecutive columns of row l % 32; the
+// epilogue stages them through LDS (16 rows at a time) and stores 128-byte row segments.
+// Requires ldc < 2^22 (32-bit store offsets within a wave's 32 rows).
+//
+// Two workgroups share a compute unit (76 KB of LDS each, one B tile buffer), so that one's
+// MFMAs run while the other waits for its stores and its next tile: loads (the copies among
+// them) and stores share one counter and may complete out of issue order, so the only wait that
+// guarantees the copies have landed is vmcnt(0), which also waits out the tile's stores.  The
+// next tile's copies are issued as soon as every wave is done reading the current one, ahead of
+// the stores, so that their latency and the stores' overlap.
+constexpr int PW = 4;            // waves per panel workgroup
 constexpr int PROWS = 32 * PW;   // rows per panel
-constexpr int PSTR = 36;         // row stride (floats) of a wave's 32 x 32 output staging block
+constexpr int PSTR = 36;         // row stride (floats) of a wave's 16 x 32 output staging block
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 template <int KT>
-__global__ __launch_bounds__(64 * PW, 1) void gemm_f16x3_panel(GemmGroup g, int run) {
+__global__ __launch_bounds__(64 * PW, 2) void gemm_f16x3_panel(GemmGroup g, int run) {
   typedef f16x8 V8;
   const GemmArgs& p = g.p[blockIdx.z];
   const int NT32 = g.NT32[blockIdx.z];
@@ -766,29 +774,37 @@ __global__ __launch_bounds__(64 * PW, 1) void gemm_f16x3_panel(GemmGroup g, int 
   if ((int)blockIdx.x >= npanel * nrun) return;
   const int panel = (int)blockIdx.x / nrun;
   const int t0 = ((int)blockIdx.x % nrun) * run, t1 = min(ntile, t0 + run);
-  constexpr int S = 2 * KT;        // 16-wide k steps
-  constexpr int TCH = KT * 1024;   // 16-byte chunks of one B tile: [kt][plane][n32 (4)][ks][lane]
-  // the output staging blocks (PW x 32 x PSTR floats) reuse the B tile the MFMAs have finished
-  constexpr int BCH = TCH > PW * 8 * PSTR ? TCH : PW * 8 * PSTR;
-  __shared__ u32x4 bs[2][BCH];
-  __shared__ u32x4 fb[2][64];      // per tile: the column exponents F, then the bias
+  constexpr int S = 2 * KT;           // 16-wide k steps
+  constexpr int TCH = KT * 1024;      // 16-byte chunks of one B tile: [kt][plane][n32 (4)][ks][lane]
+  constexpr int PPW = 16 * KT / PW;   // 1 KB copies per wave per tile
+  __shared__ u32x4 bs[TCH];
+  __shared__ u32x4 fb[2][64];         // per tile: the column exponents F, then the bias
+  __shared__ float stage[PW * 16 * PSTR];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const u32x4* Bp = static_cast<const u32x4*>(p.B);
-  const int* Fc = reinterpret_cast<const int*>(Bp + (int64_t)KT * 2 * NT32 * 128);
+  const int planes_bytes = KT * 2 * NT32 * 2048;
+  // packed B and its F: every offset fits in 31 bits (checked on the host)
+  const __amdgpu_buffer_rsrc_t brs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.B), (short)0, 0x7ffffffe, 0x00020000);
   const bool silu = p.epi == EPI_SILU;
 
-  // B tile nt: chunk c = 2 kt + plane holds the four n32 column blocks of the tile contiguously
-  // (8 KB), thread tid copying 16 bytes of each.  Wave 0 also takes F (lanes 0..31) and the bias
-  // (lanes 32..63) in one load whose address is chosen per lane (a lane without a bias value
-  // reads F and zeroes it when it stashes): a single destination register set, so that no
-  // masked half overwrites registers the other half's load is still filling.
-  u32x4 pre[2 * KT];
+  // B tile nt -> LDS: 1 KB copy q = 8 c + sub (chunk c = 2 kt + plane holds the tile's four n32
+  // column blocks contiguously) lands at bs + 64 q; wave w issues copies PPW w .. PPW (w + 1) - 1.
+  // (A direct copy addresses LDS below 64 KB, which the B tile fills at K = 128: F and the bias
+  // go through registers.)  Wave 0 loads F (lanes 0..31) and the bias (lanes 32..63) in one
+  // load whose address is chosen per lane (a lane without a bias value reads F and zeroes it when
+  // it writes fb): a single destination register set, so that no masked half overwrites
+  // registers the other half's load is still filling.
   u32x4 pfb = u32x4{0u, 0u, 0u, 0u};
   bool pz = false;
-  auto fetch = [&](int nt) {
+  const int* Fc = reinterpret_cast<const int*>(static_cast<const char*>(p.B) + planes_bytes);
+  auto copy_tile = [&](int nt) {
 #pragma unroll
-    for (int c = 0; c < 2 * KT; ++c) pre[c] = Bp[((int64_t)c * NT32 + 4 * nt) * 128 + tid];
+    for (int i = 0; i < PPW; ++i) {
+      const int q = wave * PPW + i, c = q >> 3, sub = q & 7;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (lds_ptr)(bs + 64 * q), 16, lane * 16,
+                                               c * NT32 * 2048 + nt * 8192 + sub * 1024, 0, 0);
+    }
     if (wave == 0) {
       const int n = nt * 128 + 4 * (lane - 32);
       const bool bok = lane >= 32 && p.bias != nullptr && n < p.N;
@@ -798,10 +814,8 @@ __global__ __launch_bounds__(64 * PW, 1) void gemm_f16x3_panel(GemmGroup g, int 
       pz = lane >= 32 && !bok;
     }
   };
-  auto stash = [&](int b) {
-#pragma unroll
-    for (int c = 0; c < 2 * KT; ++c) bs[b][c * 512 + tid] = pre[c];
-    if (wave == 0) fb[b][lane] = pz ? u32x4{0u, 0u, 0u, 0u} : pfb;
+  auto put_fb = [&](int fbuf) {
+    if (wave == 0) fb[fbuf][lane] = pz ? u32x4{0u, 0u, 0u, 0u} : pfb;
   };
 
   // this lane's row: A[row][16 s + 8 (lane / 32) + e], e = 0..7, is the MFMA's second operand
@@ -819,7 +833,7 @@ __global__ __launch_bounds__(64 * PW, 1) void gemm_f16x3_panel(GemmGroup g, int 
                                      : floatx4{0.f, 0.f, 0.f, 0.f};
       }
   }
-  fetch(t0);
+  copy_tile(t0);
   float mx = 0.f;
 #pragma unroll
   for (int st = 0; st < S; ++st)
@@ -834,96 +848,112 @@ __global__ __launch_bounds__(64 * PW, 1) void gemm_f16x3_panel(GemmGroup g, int 
   V8 ap[S][2];
 #pragma unroll
   for (int st = 0; st < S; ++st) split8_f16<2>(xa[st][0], xa[st][1], sh, ap[st]);
-  stash(0);
-  if (t0 + 1 < t1) fetch(t0 + 1);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the first tile's copies have landed
+  put_fb(0);
   __syncthreads();
 
   const bool full_rows = (panel + 1) * PROWS <= p.M;
-  const int c4 = lane & 7, r8 = lane >> 3, cl = 4 * (lane >> 5);
-  float* const cw = p.C + (int64_t)(panel * PROWS + wave * 32) * p.ldc;  // the wave's first row
+  const int c4 = lane & 7, r8 = lane >> 3, cl = 4 * (lane >> 5), rl = lane & 31;
+  // output rows through a buffer based at the wave's first row (byte offsets below 2^31: ldc is
+  // checked on the host)
+  const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(
+      p.C + (int64_t)(panel * PROWS + wave * 32) * p.ldc, (short)0, 0x7ffffffe, 0x00020000);
+  const int ldc4 = (int)p.ldc * 4;
+  float* const stg = stage + wave * 16 * PSTR;
   for (int nt = t0; nt < t1; ++nt) {
-    const int b = (nt - t0) & 1;
-    const bool more = nt + 1 < t1;
+    const int fbuf = (nt - t0) & 1;
     floatx16 acc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
-    const u32x4* bt = bs[b];
 #pragma unroll
     for (int st = 0; st < S; ++st) {
       const int kt = st >> 1, ks = st & 1;
-      // the three products of mode 16, smallest first: a1 b0, a0 b1, a0 b0 (one column block's
-      // B fragments live at a time: the register budget of two waves per SIMD)
+      // the three products of mode 16, smallest first: a1 b0, a0 b1, a0 b0
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const V8 b0 = __builtin_bit_cast(V8, bt[(2 * kt) * 512 + j * 128 + ks * 64 + lane]);
-        const V8 b1 = __builtin_bit_cast(V8, bt[(2 * kt + 1) * 512 + j * 128 + ks * 64 + lane]);
+        const V8 b0 = __builtin_bit_cast(V8, bs[(2 * kt) * 512 + j * 128 + ks * 64 + lane]);
+        const V8 b1 = __builtin_bit_cast(V8, bs[(2 * kt + 1) * 512 + j * 128 + ks * 64 + lane]);
         acc[j] = mfma32(b0, ap[st][1], acc[j]);
         acc[j] = mfma32(b1, ap[st][0], acc[j]);
         acc[j] = mfma32(b0, ap[st][0], acc[j]);
       }
     }
-    __syncthreads();  // every wave is done reading B tile b: it becomes the staging area
-    // Tile nt + 1 (fetched before the stores of tile nt - 1) goes to LDS, and tile nt + 2 is
-    // fetched before this tile's stores are issued.  Memory operations complete in issue order,
-    // so waiting for a fetch waits for the stores issued before it: those of the tile before
-    // last, which have had a whole tile to drain.
-    if (more) stash(b ^ 1);
-    // vmcnt(0): after a stash nothing of this thread's is in flight (its LDS writes waited for
-    // every load).  Said explicitly, the compiler's wait insertion stops carrying the F / bias
-    // load past the `more` branches (it cannot tell that they agree) and no longer waits out the
-    // stores of the tile before reusing its registers at the next fetch.
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    if (nt + 2 < t1) fetch(nt + 2);
+    const bool more = nt + 1 < t1;
+    __syncthreads();  // every wave is done reading B tile nt
     // C = acc * 2^(E + F[col]) + bias (element 4 q + i of acc[j] is column 32 j + 8 q + cl + i),
-    // through LDS one 32 x 32 block at a time: the scaled accumulators go in by rows of the MFMA
-    // layout and come back as 128-byte row segments, so that a store instruction writes eight
-    // whole rows' lines instead of 32-byte pieces of 32 rows.
-    const int4* fbi = reinterpret_cast<const int4*>(fb[b]);
-    const floatx4* fbb = reinterpret_cast<const floatx4*>(fb[b] + 32);
-    float* stg = reinterpret_cast<float*>(bs[b]) + wave * 32 * PSTR;
-    const bool full = full_rows && (nt + 1) * 128 <= p.N;
+    // through LDS one 16 x 32 block at a time: rows 16 h .. 16 h + 15 of column block j go in by
+    // rows of the MFMA layout and come back as 128-byte row segments o[j][h][i] (row
+    // 16 h + r8 + 8 i, columns 32 j + 4 c4 ..), so that a store instruction writes eight whole
+    // rows' lines instead of 32-byte pieces of 32 rows.  All of the tile's LDS work comes before
+    // the next tile's copies are issued (the compiler would otherwise wait for those copies, and
+    // every store before them, at each LDS access), and the stores after them.
+    const int4* fbi = reinterpret_cast<const int4*>(fb[fbuf]);
+    const floatx4* fbb = reinterpret_cast<const floatx4*>(fb[fbuf] + 32);
+    floatx4 o[4][2][2];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c = 8 * q + cl;
-        const int4 f = fbi[(32 * j + c) >> 2];
-        floatx4 v;
-        v[0] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 0], sh + f.x);
-        v[1] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 1], sh + f.y);
-        v[2] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 2], sh + f.z);
-        v[3] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 3], sh + f.w);
-        *reinterpret_cast<floatx4*>(stg + (lane & 31) * PSTR + c) = v;
-      }
-      const int n = nt * 128 + 32 * j + 4 * c4;
-      const floatx4 bv = fbb[(32 * j + 4 * c4) >> 2];
       floatx4 v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[i] = *reinterpret_cast<const floatx4*>(stg + (r8 + 8 * i) * PSTR + 4 * c4) + bv;
-        if (silu) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[i][e] = tta_silu(v[i][e]);
-        }
+      for (int q = 0; q < 4; ++q) {
+        const int4 f = fbi[(32 * j + 8 * q + cl) >> 2];
+        v[q][0] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 0], sh + f.x);
+        v[q][1] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 1], sh + f.y);
+        v[q][2] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 2], sh + f.z);
+        v[q][3] = __builtin_amdgcn_ldexpf(acc[j][4 * q + 3], sh + f.w);
       }
-      if (full) {
+      const floatx4 bv = fbb[(32 * j + 4 * c4) >> 2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          __builtin_nontemporal_store(
-              v[i], reinterpret_cast<floatx4*>(cw + (int64_t)(r8 + 8 * i) * p.ldc + n));
-      } else {
+      for (int h = 0; h < 2; ++h) {
+        // The staging block passes values between lanes of the wave: its LDS writes and reads
+        // run in program order, but a lane that skips the (masked) write has nothing ordering
+        // its read after the other lanes' writes, so code motion across the block boundaries is
+        // fenced off (wave_barrier: no instruction, a scheduling barrier for the wave).
+        __builtin_amdgcn_wave_barrier();
+        if ((rl >> 4) == h) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int rr = r8 + 8 * i;
-          if (panel * PROWS + wave * 32 + rr < p.M && n < p.N)
-            __builtin_nontemporal_store(
-                v[i], reinterpret_cast<floatx4*>(cw + (int64_t)rr * p.ldc + n));
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<floatx4*>(stg + (rl & 15) * PSTR + 8 * q + cl) = v[q];
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          o[j][h][i] = *reinterpret_cast<const floatx4*>(stg + (r8 + 8 * i) * PSTR + 4 * c4) + bv;
+          if (silu) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[j][h][i][e] = tta_silu(o[j][h][i][e]);
+          }
         }
       }
     }
-    __syncthreads();  // tile b ^ 1 is in LDS; every wave is done with its staging block
+    if (more) copy_tile(nt + 1);
+    // Sixteen buffer stores, every tile: a lane whose row is past M or whose column is past N
+    // stores at an offset past the buffer's end, which the hardware drops (no branches).
+    {
+      int coff[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = nt * 128 + 32 * j + 4 * c4;
+        coff[j] = n < p.N ? 4 * n : -1;
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int rr = 16 * h + r8 + 8 * i;
+          const bool rv = full_rows || panel * PROWS + wave * 32 + rr < p.M;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int off = (rv && coff[j] >= 0) ? rr * ldc4 + coff[j] : 0x7fffffff;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[j][h][i]), crs,
+                                                   off, 0, 2);
+          }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the copies (and the stores) are done
+    if (more) put_fb(fbuf ^ 1);
+    __syncthreads();
   }
 }
 
@@ -938,7 +968,7 @@ bool panel_ok(const GemmGroup& g, int n) {
   for (int i = 0; i < n; ++i) {
     const GemmArgs& p = g.p[i];
     if ((p.K + 31) / 32 != kt || p.P || !g.vec[i] || (p.epi != EPI_STORE && p.epi != EPI_SILU) ||
-        p.N < 3 * BN)
+        p.N < 3 * BN || p.ldc >= (int64_t)1 << 22)
       return false;
   }
   return true;

@@ -763,22 +763,25 @@ constexpr int PSTR = 36;         // row stride (floats) of a wave's 16 x 32 outp
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-template <int KT>
-__global__ __launch_bounds__(64 * PW, 2) void gemm_f16x3_panel(GemmGroup g, int run) {
+template <int KT, int NJ>
+__global__ __launch_bounds__(64 * PW, NJ == 2 ? 3 : 2) void gemm_f16x3_panel(GemmGroup g,
+                                                                             int run) {
   typedef f16x8 V8;
+  constexpr int TN = 32 * NJ;  // columns per tile
   const GemmArgs& p = g.p[blockIdx.z];
   const int NT32 = g.NT32[blockIdx.z];
-  const int ntile = NT32 / 4;  // 128-column tiles of the padded packed B
+  const int ntile = NT32 / NJ;  // TN-column tiles of the padded packed B
   const int nrun = (ntile + run - 1) / run;
   const int npanel = (p.M + PROWS - 1) / PROWS;
   if ((int)blockIdx.x >= npanel * nrun) return;
   const int panel = (int)blockIdx.x / nrun;
   const int t0 = ((int)blockIdx.x % nrun) * run, t1 = min(ntile, t0 + run);
   constexpr int S = 2 * KT;           // 16-wide k steps
-  constexpr int TCH = KT * 1024;      // 16-byte chunks of one B tile: [kt][plane][n32 (4)][ks][lane]
-  constexpr int PPW = 16 * KT / PW;   // 1 KB copies per wave per tile
+  constexpr int CCH = NJ * 128;       // 16-byte chunks of one (kt, plane) chunk: [n32 (NJ)][ks][lane]
+  constexpr int TCH = 2 * KT * CCH;   // 16-byte chunks of one B tile
+  constexpr int PPW = TCH / 64 / PW;  // 1 KB copies per wave per tile
   __shared__ u32x4 bs[TCH];
-  __shared__ u32x4 fb[2][64];         // per tile: the column exponents F, then the bias
+  __shared__ u32x4 fb[2][16 * NJ];    // per tile: the column exponents F, then the bias
   __shared__ float stage[PW * 16 * PSTR];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -788,34 +791,36 @@ __global__ __launch_bounds__(64 * PW, 2) void gemm_f16x3_panel(GemmGroup g, int 
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.B), (short)0, 0x7ffffffe, 0x00020000);
   const bool silu = p.epi == EPI_SILU;
 
-  // B tile nt -> LDS: 1 KB copy q = 8 c + sub (chunk c = 2 kt + plane holds the tile's four n32
+  // B tile nt -> LDS: 1 KB copy q = 2 NJ c + sub (chunk c = 2 kt + plane holds the tile's NJ n32
   // column blocks contiguously) lands at bs + 64 q; wave w issues copies PPW w .. PPW (w + 1) - 1.
-  // (A direct copy addresses LDS below 64 KB, which the B tile fills at K = 128: F and the bias
-  // go through registers.)  Wave 0 loads F (lanes 0..31) and the bias (lanes 32..63) in one
-  // load whose address is chosen per lane (a lane without a bias value reads F and zeroes it when
-  // it writes fb): a single destination register set, so that no masked half overwrites
-  // registers the other half's load is still filling.
+  // (A direct copy addresses LDS below 64 KB, which the B tile can fill: F and the bias go
+  // through registers.)  Wave 0 loads F (lanes 0 .. 8 NJ - 1) and the bias (the next 8 NJ lanes)
+  // in one load whose address is chosen per lane (a lane without a bias value reads F and zeroes
+  // it when it writes fb): a single destination register set, so that no masked part overwrites
+  // registers another part's load is still filling.
   u32x4 pfb = u32x4{0u, 0u, 0u, 0u};
   bool pz = false;
   const int* Fc = reinterpret_cast<const int*>(static_cast<const char*>(p.B) + planes_bytes);
   auto copy_tile = [&](int nt) {
 #pragma unroll
     for (int i = 0; i < PPW; ++i) {
-      const int q = wave * PPW + i, c = q >> 3, sub = q & 7;
+      const int q = wave * PPW + i, c = q / (2 * NJ), sub = q % (2 * NJ);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (lds_ptr)(bs + 64 * q), 16, lane * 16,
-                                               c * NT32 * 2048 + nt * 8192 + sub * 1024, 0, 0);
+                                               c * NT32 * 2048 + nt * (NJ * 2048) + sub * 1024,
+                                               0, 0);
     }
     if (wave == 0) {
-      const int n = nt * 128 + 4 * (lane - 32);
-      const bool bok = lane >= 32 && p.bias != nullptr && n < p.N;
+      const bool isb = (lane & (8 * NJ)) != 0;
+      const int n = nt * TN + 4 * (lane & (8 * NJ - 1));
+      const bool bok = isb && p.bias != nullptr && n < p.N;
       const void* src = bok ? static_cast<const void*>(p.bias + n)
-                            : static_cast<const void*>(Fc + nt * 128 + 4 * (lane & 31));
+                            : static_cast<const void*>(Fc + n);
       pfb = *static_cast<const u32x4*>(src);
-      pz = lane >= 32 && !bok;
+      pz = isb && !bok;
     }
   };
   auto put_fb = [&](int fbuf) {
-    if (wave == 0) fb[fbuf][lane] = pz ? u32x4{0u, 0u, 0u, 0u} : pfb;
+    if (wave == 0 && lane < 16 * NJ) fb[fbuf][lane] = pz ? u32x4{0u, 0u, 0u, 0u} : pfb;
   };
 
   // this lane's row: A[row][16 s + 8 (lane / 32) + e], e = 0..7, is the MFMA's second operand
@@ -862,9 +867,9 @@ __global__ __launch_bounds__(64 * PW, 2) void gemm_f16x3_panel(GemmGroup g, int 
   float* const stg = stage + wave * 16 * PSTR;
   for (int nt = t0; nt < t1; ++nt) {
     const int fbuf = (nt - t0) & 1;
-    floatx16 acc[4];
+    floatx16 acc[NJ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
 #pragma unroll
@@ -872,9 +877,9 @@ __global__ __launch_bounds__(64 * PW, 2) void gemm_f16x3_panel(GemmGroup g, int 
       const int kt = st >> 1, ks = st & 1;
       // the three products of mode 16, smallest first: a1 b0, a0 b1, a0 b0
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const V8 b0 = __builtin_bit_cast(V8, bs[(2 * kt) * 512 + j * 128 + ks * 64 + lane]);
-        const V8 b1 = __builtin_bit_cast(V8, bs[(2 * kt + 1) * 512 + j * 128 + ks * 64 + lane]);
+      for (int j = 0; j < NJ; ++j) {
+        const V8 b0 = __builtin_bit_cast(V8, bs[(2 * kt) * CCH + j * 128 + ks * 64 + lane]);
+        const V8 b1 = __builtin_bit_cast(V8, bs[(2 * kt + 1) * CCH + j * 128 + ks * 64 + lane]);
         acc[j] = mfma32(b0, ap[st][1], acc[j]);
         acc[j] = mfma32(b1, ap[st][0], acc[j]);
         acc[j] = mfma32(b0, ap[st][0], acc[j]);
@@ -890,10 +895,10 @@ __global__ __launch_bounds__(64 * PW, 2) void gemm_f16x3_panel(GemmGroup g, int 
     // the next tile's copies are issued (the compiler would otherwise wait for those copies, and
     // every store before them, at each LDS access), and the stores after them.
     const int4* fbi = reinterpret_cast<const int4*>(fb[fbuf]);
-    const floatx4* fbb = reinterpret_cast<const floatx4*>(fb[fbuf] + 32);
-    floatx4 o[4][2][2];
+    const floatx4* fbb = reinterpret_cast<const floatx4*>(fb[fbuf] + 8 * NJ);
+    floatx4 o[NJ][2][2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       floatx4 v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -928,13 +933,13 @@ __global__ __launch_bounds__(64 * PW, 2) void gemm_f16x3_panel(GemmGroup g, int 
       }
     }
     if (more) copy_tile(nt + 1);
-    // Sixteen buffer stores, every tile: a lane whose row is past M or whose column is past N
+    // 4 NJ buffer stores, every tile: a lane whose row is past M or whose column is past N
     // stores at an offset past the buffer's end, which the hardware drops (no branches).
     {
-      int coff[4];
+      int coff[NJ];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = nt * 128 + 32 * j + 4 * c4;
+      for (int j = 0; j < NJ; ++j) {
+        const int n = nt * TN + 32 * j + 4 * c4;
         coff[j] = n < p.N ? 4 * n : -1;
       }
 #pragma unroll
@@ -944,7 +949,7 @@ __global__ __launch_bounds__(64 * PW, 2) void gemm_f16x3_panel(GemmGroup g, int 
           const int rr = 16 * h + r8 + 8 * i;
           const bool rv = full_rows || panel * PROWS + wave * 32 + rr < p.M;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
+          for (int j = 0; j < NJ; ++j) {
             const int off = (rv && coff[j] >= 0) ? rr * ldc4 + coff[j] : 0x7fffffff;
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[j][h][i]), crs,
                                                    off, 0, 2);
@@ -959,8 +964,9 @@ __global__ __launch_bounds__(64 * PW, 2) void gemm_f16x3_panel(GemmGroup g, int 
 
 // The panel kernel takes a mode-16 group whose products all have one KT = ceil(K / 32) <= 4, the
 // plain or SiLU epilogue, no row gathers, float4-aligned outputs and at least three 128-column
-// tiles; runs of at most kPanelRun column tiles keep several workgroups per compute unit.
-constexpr int kPanelRun = 12;
+// tiles.  Tiles are kPanelNJ x 32 columns wide (2: three workgroups per compute unit, 4: two);
+// runs of at most kPanelRun x 128 columns keep several workgroups per compute unit.
+constexpr int kPanelRun = 6, kPanelNJ = 2;
 
 bool panel_ok(const GemmGroup& g, int n) {
   const int kt = (g.p[0].K + 31) / 32;
@@ -975,15 +981,16 @@ bool panel_ok(const GemmGroup& g, int n) {
 }
 
 int launch_panel(GemmGroup& g, int n, hipStream_t s) {
+  constexpr int NJ = kPanelNJ, RUN = kPanelRun * 4 / NJ;
   int64_t grid = 0;
   int run = 1;
   for (int i = 0; i < n; ++i) {
-    const int ntile = g.NT32[i] / 4;
-    const int nr = (ntile + kPanelRun - 1) / kPanelRun;
+    const int ntile = g.NT32[i] / NJ;
+    const int nr = (ntile + RUN - 1) / RUN;
     run = std::max(run, (ntile + nr - 1) / nr);
   }
   for (int i = 0; i < n; ++i) {
-    const int64_t nrun = (g.NT32[i] / 4 + run - 1) / run;
+    const int64_t nrun = (g.NT32[i] / NJ + run - 1) / run;
     grid = std::max(grid, (int64_t)tta_blocks(g.p[i].M, PROWS) * nrun);
   }
   if (grid > (1ll << 30)) {
@@ -992,10 +999,10 @@ int launch_panel(GemmGroup& g, int n, hipStream_t s) {
   }
   const dim3 gd((unsigned)grid, 1, (unsigned)n), bd(64 * PW);
   switch ((g.p[0].K + 31) / 32) {
-    case 1: hipLaunchKernelGGL(gemm_f16x3_panel<1>, gd, bd, 0, s, g, run); break;
-    case 2: hipLaunchKernelGGL(gemm_f16x3_panel<2>, gd, bd, 0, s, g, run); break;
-    case 3: hipLaunchKernelGGL(gemm_f16x3_panel<3>, gd, bd, 0, s, g, run); break;
-    default: hipLaunchKernelGGL(gemm_f16x3_panel<4>, gd, bd, 0, s, g, run); break;
+    case 1: hipLaunchKernelGGL((gemm_f16x3_panel<1, NJ>), gd, bd, 0, s, g, run); break;
+    case 2: hipLaunchKernelGGL((gemm_f16x3_panel<2, NJ>), gd, bd, 0, s, g, run); break;
+    case 3: hipLaunchKernelGGL((gemm_f16x3_panel<3, NJ>), gd, bd, 0, s, g, run); break;
+    default: hipLaunchKernelGGL((gemm_f16x3_panel<4, NJ>), gd, bd, 0, s, g, run); break;
   }
   TTA_CHECK_LAUNCH("tta_gemm_bf16x");
   return tta::kOk;

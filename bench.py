@@ -48,11 +48,13 @@ METRIC = "atom-steps/s (energy+forces), uma-s-1 arch 2,048 atoms; % HBM/MFMA roo
 PEAK_FP32_MFMA = 157.3
 PEAK_HBM_GBPS = 8000.0
 PEAK_BF16_MFMA = 2500.0
-PEAKS = {"f32": PEAK_FP32_MFMA, "f16x3": PEAK_BF16_MFMA / 3, "bf16x6": PEAK_BF16_MFMA / 6,
-         "bf16x3": PEAK_BF16_MFMA / 3, "bf16x1": PEAK_BF16_MFMA}
+PEAKS = {"f32": PEAK_FP32_MFMA, "f16x3": PEAK_BF16_MFMA / 3, "f16x3-panel": PEAK_BF16_MFMA / 3,
+         "bf16x6": PEAK_BF16_MFMA / 6, "bf16x3": PEAK_BF16_MFMA / 3, "bf16x1": PEAK_BF16_MFMA}
 KERNELS = {"f32": "gemm_f32_kernel (fp32 MFMA 16x16x4)",
            "f16x3": "gemm_bf16x_kernel<2,16> (split-fp16, 2x2 power-of-two-scaled planes / 3 "
                     "products, fp32-accurate)",
+           "f16x3-panel": "gemm_f16x3_panel<KT,2> (the same split-fp16 arithmetic for K <= 128: "
+                          "the radial output layer)",
            "bf16x6": "gemm_bf16x_kernel<2,6> (split-bf16, 3x3 planes / 6 products, fp32-accurate)",
            "bf16x3": "gemm_bf16x_kernel<2,3> (split-bf16, 2x2 planes / 3 products)",
            "bf16x1": "gemm_bf16x_kernel<2,1> (bf16 operands)"}

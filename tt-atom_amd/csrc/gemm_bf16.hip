@@ -751,12 +751,12 @@ __global__ __launch_bounds__(256) void k_pack_b(const float* __restrict__ B, int
 // epilogue stages them through LDS (16 rows at a time) and stores 128-byte row segments.
 // Requires ldc < 2^22 (32-bit store offsets within a wave's 32 rows).
 //
-// Two workgroups share a compute unit (76 KB of LDS each, one B tile buffer), so that one's
-// MFMAs run while the other waits for its stores and its next tile: loads (the copies among
-// them) and stores share one counter and may complete out of issue order, so the only wait that
-// guarantees the copies have landed is vmcnt(0), which also waits out the tile's stores.  The
-// next tile's copies are issued as soon as every wave is done reading the current one, ahead of
-// the stores, so that their latency and the stores' overlap.
+// Several workgroups share a compute unit (64-column tiles: three, 43 KB of LDS each, one B tile
+// buffer), so that one's MFMAs run while another waits for its stores and its next tile: loads
+// (the copies among them) and stores share one counter and are not ordered with each other, so
+// the only wait that guarantees the copies have landed is vmcnt(0), which also waits out the
+// tile's stores.  The next tile's copies are issued as soon as every wave is done reading the
+// current one, ahead of the stores, so that their latency and the stores' overlap.
 constexpr int PW = 4;            // waves per panel workgroup
 constexpr int PROWS = 32 * PW;   // rows per panel
 constexpr int PSTR = 36;         // row stride (floats) of a wave's 16 x 32 output staging block
@@ -793,8 +793,8 @@ __global__ __launch_bounds__(64 * PW, NJ == 2 ? 3 : 2) void gemm_f16x3_panel(Gem
 
   // B tile nt -> LDS: 1 KB copy q = 2 NJ c + sub (chunk c = 2 kt + plane holds the tile's NJ n32
   // column blocks contiguously) lands at bs + 64 q; wave w issues copies PPW w .. PPW (w + 1) - 1.
-  // (A direct copy addresses LDS below 64 KB, which the B tile can fill: F and the bias go
-  // through registers.)  Wave 0 loads F (lanes 0 .. 8 NJ - 1) and the bias (the next 8 NJ lanes)
+  // F and the bias go through registers: wave 0 loads F (lanes 0 .. 8 NJ - 1) and the bias (the
+  // next 8 NJ lanes)
   // in one load whose address is chosen per lane (a lane without a bias value reads F and zeroes
   // it when it writes fb): a single destination register set, so that no masked part overwrites
   // registers another part's load is still filling.

@@ -255,6 +255,16 @@ def gemm(A, B, C, *, M, N, K, lda, ldb, ldc, bias=None, epilogue=EPI_STORE, C2=N
 SPLIT_F32, SPLIT_F16X3, SPLIT_3, SPLIT_BF16 = 6, 16, 3, 1
 # kernel-family name per mode, as the measurement hook reports it
 MODE_KIND = {6: "bf16x6", 16: "f16x3", 3: "bf16x3", 1: "bf16x1"}
+# mode-16 products that tta_gemm_bf16x(_group) runs on its short-K panel kernel (K <= 128, one
+# 32-wide k-slab count for the whole group, plain or SiLU epilogue, no row gathers, at least 384
+# columns, 16-byte aligned rows and operands, ldc < 2^22) are reported as their own family
+PANEL_KIND = "f16x3-panel"
+
+
+def _panel_item(M, N, K, ldc, epilogue, ptrs, gather=False):
+    al = all(q is None or q % 16 == 0 for q in ptrs)
+    return (K <= 128 and epilogue in (EPI_STORE, EPI_SILU) and not gather and N >= 384
+            and N % 4 == 0 and ldc % 4 == 0 and ldc < (1 << 22) and al)
 
 
 class PackedWeight:
@@ -298,8 +308,11 @@ def _gemm_bf16x(x, pw, out, bias, epilogue, out2, aux, P=None, idx0=None, idx1=N
     probe = _gemm_probe
     if probe is not None:
         c_passes = 1 + (epilogue in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD)) + (2 if P is not None else 0)
+        panel = pw.mode == 16 and _panel_item(
+            M, N, K, _ld(out, "out"), epilogue,
+            [out.data_ptr(), None if bias is None else bias.data_ptr()], gather=P is not None)
         probe.before(2.0 * M * N * K, 4.0 * (M * K + K * N + c_passes * M * N),
-                     MODE_KIND[pw.mode])
+                     PANEL_KIND if panel else MODE_KIND[pw.mode])
     _call("tta_gemm_bf16x", x.data_ptr(), pw.packed.data_ptr(), out.data_ptr(),
           None if bias is None else _ptr(bias, numel=N, name="bias"),
           None if out2 is None else out2.data_ptr(), None if aux is None else aux.data_ptr(),
@@ -361,6 +374,10 @@ def linear_group(items):
         return
     probs = (GemmProblem * len(items))()
     flops = nbytes = 0.0
+    panel = split[0] and items[0][1].mode == 16 and len({(x.shape[1] + 31) // 32 for x, *_ in items}) == 1
+    for x, w, bias, out, epi, out2, aux in items:
+        panel = panel and _panel_item(x.shape[0], w.shape[1], x.shape[1], _ld(out, "out"), epi,
+                                      [out.data_ptr(), None if bias is None else bias.data_ptr()])
     for i, (x, w, bias, out, epi, out2, aux) in enumerate(items):
         M, K = x.shape
         N = w.shape[1]
@@ -380,7 +397,8 @@ def linear_group(items):
         nbytes += 4.0 * (M * K + K * N + c_passes * M * N)
     probe = _gemm_probe
     if probe is not None:
-        probe.before(flops, nbytes, MODE_KIND[items[0][1].mode] if split[0] else "f32")
+        probe.before(flops, nbytes, (PANEL_KIND if panel else MODE_KIND[items[0][1].mode])
+                     if split[0] else "f32")
     if split[0]:
         _call("tta_gemm_bf16x_group", probs, len(items), items[0][1].mode, _stream())
     else:

@@ -263,6 +263,7 @@ struct SpecFwdArgs {
   int64_t N;
   int C, H;
   float eps;
+  int npb;                                // nodes per workgroup, NT or NT / 2 (rows past it zero)
 };
 
 __global__ __launch_bounds__(NTH, 1) void k_spectral_block_fwd(SpecFwdArgs p) {
@@ -270,8 +271,8 @@ __global__ __launch_bounds__(NTH, 1) void k_spectral_block_fwd(SpecFwdArgs p) {
   __shared__ float gat[NT * (2 * CMAX + 4)];
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int C = p.C, H = p.H, LH = 2 * H, ldg = 2 * CMAX + 4;
-  const int64_t n0 = (int64_t)blockIdx.x * NT;
-  const int nv = (int)min((int64_t)NT, p.N - n0);
+  const int64_t n0 = (int64_t)blockIdx.x * p.npb;
+  const int nv = (int)min((int64_t)p.npb, p.N - n0);
   // 1. x1 rows -> LDS (rows of absent nodes zero)
   load_tile(buf, p.x1, n0, nv, C, wave, lane);
   __syncthreads();
@@ -388,6 +389,7 @@ struct SpecBwdArgs {
   float* g_x1;                            // [N, 9, C]
   int64_t N;
   int C, H;
+  int npb;                                // nodes per workgroup, NT or NT / 2 (rows past it zero)
 };
 
 __global__ __launch_bounds__(NTH, 1) void k_spectral_block_bwd(SpecBwdArgs p) {
@@ -395,8 +397,8 @@ __global__ __launch_bounds__(NTH, 1) void k_spectral_block_bwd(SpecBwdArgs p) {
   __shared__ float gas[NT * (2 * CMAX + 4)];
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int C = p.C, H = p.H, LH = 2 * H, ldg = 2 * CMAX + 4;
-  const int64_t n0 = (int64_t)blockIdx.x * NT;
-  const int nv = (int)min((int64_t)NT, p.N - n0);
+  const int64_t n0 = (int64_t)blockIdx.x * p.npb;
+  const int nv = (int)min((int64_t)p.npb, p.N - n0);
   // 1. g_x2 = next-norm backward (+ res), one wave per node; kept in registers for step 5 and
   //    written to LDS as the FF's output adjoint (absent nodes: zero rows).  The x2 tile comes
   //    into LDS by coalesced rows; each wave's g_n values (its nodes wave + NW s, channels
@@ -676,6 +678,24 @@ bool node_dims_ok(int64_t N, int C, int H) {
 
 }  // namespace
 
+// Nodes per workgroup of the spectral kernels: NT, or NT / 2 when NT-node workgroups would not
+// cover the compute units (their MFMA tiles keep NT rows, the rows past the workgroup's nodes
+// zero, so a half-full workgroup costs about what a full one does but the per-node phases --
+// loads, norms, stores -- halve and twice as many units work).
+static int spectral_npb(int64_t N) {
+  static int cus_of[64] = {0};  // compute units per device, queried once
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus_of[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cus_of[dev] = cus;
+  }
+  return (N + NT - 1) / NT < cus_of[dev] ? NT / 2 : NT;
+}
+
 extern "C" int tta_spectral_block_fwd(const float* x1, const float* aw2, const float* ab2,
                                       const float* ws_t, const float* bs, const float* w1t,
                                       const float* b1, const float* w2t, const float* b2,
@@ -692,8 +712,8 @@ extern "C" int tta_spectral_block_fwd(const float* x1, const float* aw2, const f
   TTA_CHECK_ARG(!awn || (abn && yn && invn), "tta_spectral_block_fwd: incomplete next norm");
   if (N == 0) return tta::kOk;
   SpecFwdArgs p{x1, aw2, ab2, ws_t, bs, w1t, b1, w2t, b2, inv2, a_s, h, x2,
-                awn, abn, add0, yn, invn, N, (int)C, (int)H, eps};
-  hipLaunchKernelGGL(k_spectral_block_fwd, dim3(tta_blocks(N, NT)), dim3(NTH), 0, stream, p);
+                awn, abn, add0, yn, invn, N, (int)C, (int)H, eps, spectral_npb(N)};
+  hipLaunchKernelGGL(k_spectral_block_fwd, dim3(tta_blocks(N, p.npb)), dim3(NTH), 0, stream, p);
   TTA_CHECK_LAUNCH("tta_spectral_block_fwd");
   return tta::kOk;
 }
@@ -712,8 +732,8 @@ extern "C" int tta_spectral_block_bwd(const float* g_n, const float* x2, const f
                 "tta_spectral_block_bwd: null pointer");
   if (N == 0) return tta::kOk;
   SpecBwdArgs p{g_n, x2, awn, invn, res, x1, aw2, inv2, a_s, h, w1, w2, ws, g_x1, N, (int)C,
-                (int)H};
-  hipLaunchKernelGGL(k_spectral_block_bwd, dim3(tta_blocks(N, NT)), dim3(NTH), 0, stream, p);
+                (int)H, spectral_npb(N)};
+  hipLaunchKernelGGL(k_spectral_block_bwd, dim3(tta_blocks(N, p.npb)), dim3(NTH), 0, stream, p);
   TTA_CHECK_LAUNCH("tta_spectral_block_bwd");
   return tta::kOk;
 }

@@ -173,7 +173,7 @@ def test_split_gemm_persistent_tiles(nat, mode, tol):
 @pytest.mark.parametrize("K", [128, 100, 36])
 @pytest.mark.parametrize("epi", [0, 1])
 def test_split_gemm_short_k_panel(nat, K, epi):
-    """Short-K mode-16 products (K <= 128, at least three 128-column tiles, plain or SiLU
+    """Short-K mode-16 products (K <= 128, at least 128 columns, plain or SiLU
     epilogue) run on the panel kernel: a workgroup splits a 256-row panel of A once and sweeps a
     run of column tiles.  K = 128 goes through linear_group as the radial output layer does (two
     products of different widths: 1536 = two runs of six tiles, 1100 = nine tiles with a ragged

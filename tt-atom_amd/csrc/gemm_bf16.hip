@@ -963,8 +963,8 @@ __global__ __launch_bounds__(64 * PW, NJ == 2 ? 3 : 2) void gemm_f16x3_panel(Gem
 }
 
 // The panel kernel takes a mode-16 group whose products all have one KT = ceil(K / 32) <= 4, the
-// plain or SiLU epilogue, no row gathers, float4-aligned outputs and at least three 128-column
-// tiles.  Tiles are kPanelNJ x 32 columns wide (2: three workgroups per compute unit, 4: two);
+// plain or SiLU epilogue, no row gathers, float4-aligned outputs and at least 128 columns.
+// Tiles are kPanelNJ x 32 columns wide (2: three workgroups per compute unit, 4: two);
 // runs of at most kPanelRun x 128 columns keep several workgroups per compute unit.
 constexpr int kPanelRun = 6, kPanelNJ = 2;
 
@@ -974,7 +974,7 @@ bool panel_ok(const GemmGroup& g, int n) {
   for (int i = 0; i < n; ++i) {
     const GemmArgs& p = g.p[i];
     if ((p.K + 31) / 32 != kt || p.P || !g.vec[i] || (p.epi != EPI_STORE && p.epi != EPI_SILU) ||
-        p.N < 3 * BN || p.ldc >= (int64_t)1 << 22)
+        p.N < BN || p.ldc >= (int64_t)1 << 22)
       return false;
   }
   return true;

@@ -256,14 +256,14 @@ SPLIT_F32, SPLIT_F16X3, SPLIT_3, SPLIT_BF16 = 6, 16, 3, 1
 # kernel-family name per mode, as the measurement hook reports it
 MODE_KIND = {6: "bf16x6", 16: "f16x3", 3: "bf16x3", 1: "bf16x1"}
 # mode-16 products that tta_gemm_bf16x(_group) runs on its short-K panel kernel (K <= 128, one
-# 32-wide k-slab count for the whole group, plain or SiLU epilogue, no row gathers, at least 384
+# 32-wide k-slab count for the whole group, plain or SiLU epilogue, no row gathers, at least 128
 # columns, 16-byte aligned rows and operands, ldc < 2^22) are reported as their own family
 PANEL_KIND = "f16x3-panel"
 
 
 def _panel_item(M, N, K, ldc, epilogue, ptrs, gather=False):
     al = all(q is None or q % 16 == 0 for q in ptrs)
-    return (K <= 128 and epilogue in (EPI_STORE, EPI_SILU) and not gather and N >= 384
+    return (K <= 128 and epilogue in (EPI_STORE, EPI_SILU) and not gather and N >= 128
             and N % 4 == 0 and ldc % 4 == 0 and ldc < (1 << 22) and al)
 
 

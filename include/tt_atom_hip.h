@@ -157,13 +157,15 @@ int tta_gate_bwd(const float* g_y, const float* x, const float* gating, float* g
  * g_a (so2.py:117-143; ttnn.experimental.fused_ln_bw, fused_ln_bw.hpp:14-21).  Row strides:
  * a / nrm lda, s lds, g ldg, g_a ldo.  `groups` LayerNorms of width n side by side in each row
  * (group k = columns k n .. k n + n - 1, gamma / beta [groups, n]): the radial MLPs of the
- * edge-degree embedding and of every block, which the reference runs one after another. */
+ * edge-degree embedding and of every block, which the reference runs one after another.
+ * nrm may be NULL in both: the forward then does not write it and the backward recomputes it
+ * from a, gamma and beta (same values as the forward's), which it then requires. */
 int tta_ln_silu_fwd(const float* a, const float* gamma, const float* beta, float* nrm, float* s,
                     int64_t R, int64_t n, int64_t groups, int64_t lda, int64_t lds, float eps,
                     tta_stream_t stream);
 int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm, const float* gamma,
-                    float* g_a, int64_t R, int64_t n, int64_t groups, int64_t ldg, int64_t lda,
-                    int64_t ldo, float eps, tta_stream_t stream);
+                    const float* beta, float* g_a, int64_t R, int64_t n, int64_t groups,
+                    int64_t ldg, int64_t lda, int64_t ldo, float eps, tta_stream_t stream);
 
 /* RMSNormSH (norm.py:59-111) with an optional l=0 addend (the system embedding of
  * model.py:164-167); inv [N] kept for the backward (forces.py:49-98; res = residual adjoint). */

@@ -598,6 +598,15 @@ def test_ln_silu_fwd_bwd(nat, n):
     torch.cuda.synchronize()
     assert torch.equal(nb[:R], no) and torch.equal(sb[:R], so) and torch.equal(gb[:R], gao)
     assert all(bool(t[R].isnan().all()) for t in (nb, sb, gb))
+    # without the saved LayerNorm output: the forward does not write it, the backward recomputes
+    # it from a, gamma and beta -- the same values, so the same adjoint bit for bit
+    s3, g3 = torch.empty(R, n, device=DEV), torch.full((R + 1, n), float("nan"), device=DEV)
+    nat.ln_silu_fwd(f(a), f(gam), f(bet), None, s3, R=R, n=n)
+    nat.ln_silu_bwd(f(gs), f(a), None, f(gam), g3[:R], R=R, n=n, beta=f(bet))
+    torch.cuda.synchronize()
+    assert torch.equal(s3, so) and torch.equal(g3[:R], gao) and bool(g3[R].isnan().all())
+    with pytest.raises(RuntimeError):
+        nat.ln_silu_bwd(f(gs), f(a), None, f(gam), g3[:R], R=R, n=n)
 
 
 @pytest.mark.parametrize("C", [16, 128, 96, 256, 300])

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
     const int i = lane + G * k;
     if (i >= n) continue;
     const float y = (v[k] - mean) * rstd * gamma[i] + beta[i];
-    nrm[row * lda + co + i] = y;
+    if (nrm) nrm[row * lda + co + i] = y;
     s[row * lds + co + i] = tta_silu(y);
   }
 }
@@ -125,11 +125,14 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
 //   gy = g * silu'(nrm) * gamma;  xhat = (a - mean) * rstd;
 //   g_a = rstd * (gy - mean(gy) - xhat * mean(gy * xhat))
 // g rows stride ldg, a / nrm rows stride lda, g_a rows stride ldo.  Same lane layout as above.
-template <int G, int NPL>
+// RECOMP: nrm is not read but recomputed from a, gamma and beta with the forward's operations
+// (the same row statistics and the same expression, so the same values).
+template <int G, int NPL, bool RECOMP>
 __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g,
                                                      const float* __restrict__ a,
                                                      const float* __restrict__ nrm,
                                                      const float* __restrict__ gamma,
+                                                     const float* __restrict__ beta,
                                                      float* __restrict__ g_a, int64_t R, int n,
                                                      int groups, int64_t ldg, int64_t lda,
                                                      int64_t ldo, float eps) {
@@ -142,6 +145,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   const int64_t row = vr / groups;
   const int co = (int)(vr - row * groups) * n;
   gamma += co;
+  if (RECOMP) beta += co;
   const float* ar = a + row * lda + co;
   float av[NPL], gy[NPL];
   float sum = 0.f;
@@ -150,7 +154,10 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
     const int i = lane + G * k;
     const bool in = i < n;
     av[k] = in ? ar[i] : 0.f;
-    gy[k] = in ? g[row * ldg + co + i] * tta_silu_grad(nrm[row * lda + co + i]) * gamma[i] : 0.f;
+    if (RECOMP)
+      gy[k] = in ? g[row * ldg + co + i] : 0.f;
+    else
+      gy[k] = in ? g[row * ldg + co + i] * tta_silu_grad(nrm[row * lda + co + i]) * gamma[i] : 0.f;
     sum += av[k];
   }
   const float mean = tta_group_sum(sum, G) / n;
@@ -160,7 +167,17 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
     const float d = av[k] - mean;
     if (lane + G * k < n) sq += d * d;
   }
-  const float rstd = 1.0f / sqrtf(tta_group_sum(sq, G) / n + eps);
+  const float var = tta_group_sum(sq, G) / n;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  if (RECOMP) {
+#pragma unroll
+    for (int k = 0; k < NPL; ++k) {
+      const int i = lane + G * k;
+      if (i >= n) continue;
+      const float y = (av[k] - mean) * rstd * gamma[i] + beta[i];
+      gy[k] = gy[k] * tta_silu_grad(y) * gamma[i];
+    }
+  }
   float m1 = 0.f, m2 = 0.f;
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
@@ -451,7 +468,7 @@ extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* 
                     lda >= groups * n && lds >= groups * n && R * groups < ((int64_t)1 << 40),
                 "tta_ln_silu_fwd: bad sizes (row width 1..512, 1..64 groups)");
   if (R == 0) return tta::kOk;
-  TTA_CHECK_ARG(a && gamma && beta && nrm && s, "tta_ln_silu_fwd: null pointer");
+  TTA_CHECK_ARG(a && gamma && beta && s, "tta_ln_silu_fwd: null pointer");
   const int64_t RV = R * groups;
 #define TTA_LN_FWD(G, NPL)                                                                  \
   hipLaunchKernelGGL((k_ln_silu_fwd<G, NPL>), dim3(tta_blocks(RV * G, 256)), dim3(256), 0,    \
@@ -472,19 +489,28 @@ extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* 
 }
 
 extern "C" int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm,
-                               const float* gamma, float* g_a, int64_t R, int64_t n,
-                               int64_t groups, int64_t ldg, int64_t lda, int64_t ldo, float eps,
-                               hipStream_t stream) {
+                               const float* gamma, const float* beta, float* g_a, int64_t R,
+                               int64_t n, int64_t groups, int64_t ldg, int64_t lda, int64_t ldo,
+                               float eps, hipStream_t stream) {
   TTA_CHECK_ARG(R >= 0 && n > 0 && n <= 512 && groups >= 1 && groups <= 64 &&
                     ldg >= groups * n && lda >= groups * n && ldo >= groups * n &&
                     R * groups < ((int64_t)1 << 40),
                 "tta_ln_silu_bwd: bad sizes (row width 1..512, 1..64 groups)");
   if (R == 0) return tta::kOk;
-  TTA_CHECK_ARG(g && a && nrm && gamma && g_a, "tta_ln_silu_bwd: null pointer");
+  TTA_CHECK_ARG(g && a && gamma && g_a && (nrm || beta),
+                "tta_ln_silu_bwd: null pointer (nrm, or beta to recompute it, is required)");
   const int64_t RV = R * groups;
 #define TTA_LN_BWD(G, NPL)                                                                  \
-  hipLaunchKernelGGL((k_ln_silu_bwd<G, NPL>), dim3(tta_blocks(RV * G, 256)), dim3(256), 0,    \
-                     stream, g, a, nrm, gamma, g_a, R, (int)n, (int)groups, ldg, lda, ldo, eps)
+  do {                                                                                      \
+    if (nrm)                                                                                \
+      hipLaunchKernelGGL((k_ln_silu_bwd<G, NPL, false>), dim3(tta_blocks(RV * G, 256)),     \
+                         dim3(256), 0, stream, g, a, nrm, gamma, beta, g_a, R, (int)n,      \
+                         (int)groups, ldg, lda, ldo, eps);                                  \
+    else                                                                                    \
+      hipLaunchKernelGGL((k_ln_silu_bwd<G, NPL, true>), dim3(tta_blocks(RV * G, 256)),      \
+                         dim3(256), 0, stream, g, a, nrm, gamma, beta, g_a, R, (int)n,      \
+                         (int)groups, ldg, lda, ldo, eps);                                  \
+  } while (0)
   if (n <= 32)
     TTA_LN_BWD(32, 1);
   else if (n <= 64)

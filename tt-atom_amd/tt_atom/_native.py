@@ -52,7 +52,7 @@ _SIGS = {
     "tta_gate_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "tta_gate_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "tta_ln_silu_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
-    "tta_ln_silu_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P],
+    "tta_ln_silu_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "tta_rmsnorm_sh_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _P],
     "tta_rmsnorm_sh_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _P],
     "tta_silu_bwd": [_P, _P, _P, _I64, _P],
@@ -582,26 +582,34 @@ def gate_bwd(g_y, x, gating, g_x, g_gating, idx8, *, R, H, L, ldx=None, ldg=None
 
 
 def ln_silu_fwd(a, gamma, beta, nrm, s, *, R, n, groups=1, lda=None, lds=None, eps=1e-5):
-    """``groups`` LayerNorms of width n side by side per row (gamma / beta [groups * n])."""
+    """``groups`` LayerNorms of width n side by side per row (gamma / beta [groups * n]).
+    ``nrm`` (the LayerNorm output) may be None: then it is not written, and ln_silu_bwd
+    recomputes it."""
     w = groups * n
     lda = w if lda is None else lda
     lds = w if lds is None else lds
-    _hbm_call("k_ln_silu_fwd", 4 * (3 * R * w + 2 * w), "tta_ln_silu_fwd",
+    _hbm_call("k_ln_silu_fwd", 4 * ((2 + (nrm is not None)) * R * w + 2 * w), "tta_ln_silu_fwd",
               _rows(a, R, lda, w, "a"), _ptr(gamma, numel=w), _ptr(beta, numel=w),
-              _rows(nrm, R, lda, w, "nrm"), _rows(s, R, lds, w, "s"), R, n, groups, lda, lds,
-              eps, _stream())
+              None if nrm is None else _rows(nrm, R, lda, w, "nrm"), _rows(s, R, lds, w, "s"),
+              R, n, groups, lda, lds, eps, _stream())
 
 
 def ln_silu_bwd(g, a, nrm, gamma, g_a, *, R, n, groups=1, ldg=None, lda=None, ldo=None,
-                eps=1e-5):
+                eps=1e-5, beta=None):
+    """Backward of silu(layer_norm(a)); with ``nrm`` None the LayerNorm output is recomputed
+    from a, gamma and ``beta`` (the same values the forward produced)."""
     w = groups * n
     ldg = w if ldg is None else ldg
     lda = w if lda is None else lda
     ldo = w if ldo is None else ldo
-    _hbm_call("k_ln_silu_bwd", 4 * (4 * R * w + w), "tta_ln_silu_bwd",
-              _rows(g, R, ldg, w, "g"), _rows(a, R, lda, w, "a"), _rows(nrm, R, lda, w, "nrm"),
-              _ptr(gamma, numel=w), _rows(g_a, R, ldo, w, "g_a"), R, n, groups, ldg, lda, ldo,
-              eps, _stream())
+    if nrm is None and beta is None:
+        raise RuntimeError("ln_silu_bwd: nrm, or beta to recompute it, is required")
+    nbytes = 4 * (4 * R * w + w) if nrm is not None else 4 * (3 * R * w + 2 * w)
+    _hbm_call("k_ln_silu_bwd", nbytes, "tta_ln_silu_bwd",
+              _rows(g, R, ldg, w, "g"), _rows(a, R, lda, w, "a"),
+              None if nrm is None else _rows(nrm, R, lda, w, "nrm"), _ptr(gamma, numel=w),
+              None if beta is None else _ptr(beta, numel=w), _rows(g_a, R, ldo, w, "g_a"), R, n,
+              groups, ldg, lda, ldo, eps, _stream())
 
 
 def rmsnorm_sh_fwd(x, aw, ab, add0, y, inv, eps=1e-5):

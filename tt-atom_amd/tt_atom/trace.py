@@ -81,11 +81,11 @@ class TracedEngine:
         self.g_coef, self.g_env, self.g_gauss = emp(E, 35), emp(E), emp(E, nb)
         self.g_ev, self.forces = emp(E, 3), emp(N, 3)
         self.energy_buf, self.virial_buf, self.virial_work = emp(1), emp(9), emp(256 * 9)
-        # radial MLPs side by side (edge-degree, then block 0..L-1): pre-LN, LN and SiLU outputs of
-        # both hidden layers, and the adjoints
-        self.a0_all, self.nrm1_all, self.g_a0_all = (emp(E, nrad * hid) for _ in range(3))
-        self.s1_all, self.a3_all, self.nrm4_all, self.s2_all = (emp(E, nrad * hid)
-                                                                for _ in range(4))
+        # radial MLPs side by side (edge-degree, then block 0..L-1): pre-LN and SiLU outputs of
+        # both hidden layers (the LayerNorm outputs are recomputed in the backward), and the
+        # adjoints
+        self.a0_all, self.g_a0_all = (emp(E, nrad * hid) for _ in range(2))
+        self.s1_all, self.a3_all, self.s2_all = (emp(E, nrad * hid) for _ in range(3))
         self.t1_all, self.t2_all = emp(E, nrad * hid), emp(E, nrad * hid)
         # shared edge temporaries
         self.LHc = L * H + NSPH * H                      # combined conv-1 row [gating | out]
@@ -145,11 +145,11 @@ class TracedEngine:
         bb, E, hid, R = self.bb, self.E, self.hid, self.nrad
         col = lambda t, r: t[:, r * hid:(r + 1) * hid]
         caches = [self.ed] + [c.rad for c in self.blk]
-        nat.ln_silu_fwd(self.a0_all, bb.rad_ln1w_all, bb.rad_ln1b_all, self.nrm1_all, self.s1_all,
+        nat.ln_silu_fwd(self.a0_all, bb.rad_ln1w_all, bb.rad_ln1b_all, None, self.s1_all,
                         R=E, n=hid, groups=R)
         nat.linear_group([(col(self.s1_all, r), rw.w3t, rw.b3, col(self.a3_all, r))
                           for r, rw in enumerate(bb.radials)])
-        nat.ln_silu_fwd(self.a3_all, bb.rad_ln4w_all, bb.rad_ln4b_all, self.nrm4_all, self.s2_all,
+        nat.ln_silu_fwd(self.a3_all, bb.rad_ln4w_all, bb.rad_ln4b_all, None, self.s2_all,
                         R=E, n=hid, groups=R)
         nat.linear_group([(col(self.s2_all, r), rw.w6t, rw.b6, c.out)
                           for r, (rw, c) in enumerate(zip(bb.radials, caches))])
@@ -160,12 +160,12 @@ class TracedEngine:
         caches = [self.ed] + [c.rad for c in self.blk]
         nat.linear_group([(c.g_out, rw.w6, None, col(self.t1_all, r))
                           for r, (rw, c) in enumerate(zip(bb.radials, caches))])
-        nat.ln_silu_bwd(self.t1_all, self.a3_all, self.nrm4_all, bb.rad_ln4w_all, self.t2_all,
-                        R=E, n=hid, groups=R)
+        nat.ln_silu_bwd(self.t1_all, self.a3_all, None, bb.rad_ln4w_all, self.t2_all,
+                        R=E, n=hid, groups=R, beta=bb.rad_ln4b_all)
         nat.linear_group([(col(self.t2_all, r), rw.w3, None, col(self.t1_all, r))
                           for r, rw in enumerate(bb.radials)])
-        nat.ln_silu_bwd(self.t1_all, self.a0_all, self.nrm1_all, bb.rad_ln1w_all, self.g_a0_all,
-                        R=E, n=hid, groups=R)
+        nat.ln_silu_bwd(self.t1_all, self.a0_all, None, bb.rad_ln1w_all, self.g_a0_all,
+                        R=E, n=hid, groups=R, beta=bb.rad_ln1b_all)
 
     # ------------------------------------------------------------------ feed-forward
     def _spectral_fwd(self, aw, c, x, res, out):

@@ -4,6 +4,8 @@
 // deterministic reductions.
 #include "common.h"
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
 namespace {
 
 struct GateIdx {
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(256) void k_gate_bwd(const float* __restrict__ g_y,
 // a and nrm rows have stride lda, s rows stride lds.  `groups` independent LayerNorms per row
 // (the radial MLPs of several blocks side by side): group k of a row is the n columns from k n,
 // with gamma / beta [groups, n]; a row of a wavefront is one (row, group) pair.
-template <int G, int NPL>
+template <int G, int NPL, bool VEC>
 __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a,
                                                      const float* __restrict__ gamma,
                                                      const float* __restrict__ beta,
@@ -93,12 +95,22 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
   gamma += co;
   beta += co;
   const float* ar = a + row * lda + co;
+  // element k of lane l: column l + G k, or with VEC (n = 4 G, 16-byte aligned rows) column
+  // 4 l + k, all four in one float4
   float v[NPL];
+  if constexpr (VEC) {
+    static_assert(NPL == 4, "float4 rows");
+    const floatx4 x = *reinterpret_cast<const floatx4*>(ar + 4 * lane);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = x[k];
+  }
   float sum = 0.f;
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
-    const int i = lane + G * k;
-    v[k] = i < n ? ar[i] : 0.f;
+    if constexpr (!VEC) {
+      const int i = lane + G * k;
+      v[k] = i < n ? ar[i] : 0.f;
+    }
     sum += v[k];
   }
   const float mean = tta_group_sum(sum, G) / n;
@@ -106,11 +118,24 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
     const float d = v[k] - mean;
-    if (lane + G * k < n) sq += d * d;
+    if (VEC || lane + G * k < n) sq += d * d;
   }
   const float var = tta_group_sum(sq, G) / n;
   const float rstd = 1.0f / sqrtf(var + eps);
   if (!valid) return;
+  if constexpr (VEC) {
+    const floatx4 gm = *reinterpret_cast<const floatx4*>(gamma + 4 * lane);
+    const floatx4 bt = *reinterpret_cast<const floatx4*>(beta + 4 * lane);
+    floatx4 y, sv;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      y[k] = (v[k] - mean) * rstd * gm[k] + bt[k];
+      sv[k] = tta_silu(y[k]);
+    }
+    if (nrm) *reinterpret_cast<floatx4*>(nrm + row * lda + co + 4 * lane) = y;
+    *reinterpret_cast<floatx4*>(s + row * lds + co + 4 * lane) = sv;
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
     const int i = lane + G * k;
@@ -127,7 +152,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
 // g rows stride ldg, a / nrm rows stride lda, g_a rows stride ldo.  Same lane layout as above.
 // RECOMP: nrm is not read but recomputed from a, gamma and beta with the forward's operations
 // (the same row statistics and the same expression, so the same values).
-template <int G, int NPL, bool RECOMP>
+template <int G, int NPL, bool RECOMP, bool VEC>
 __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g,
                                                      const float* __restrict__ a,
                                                      const float* __restrict__ nrm,
@@ -149,33 +174,62 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   const float* ar = a + row * lda + co;
   float av[NPL], gy[NPL];
   float sum = 0.f;
+  // element layout as in k_ln_silu_fwd
+  if constexpr (VEC) {
+    static_assert(NPL == 4, "float4 rows");
+    const floatx4 x = *reinterpret_cast<const floatx4*>(ar + 4 * lane);
+    const floatx4 gv = *reinterpret_cast<const floatx4*>(g + row * ldg + co + 4 * lane);
+    floatx4 nv = {0.f, 0.f, 0.f, 0.f}, gm = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (!RECOMP) {
+      nv = *reinterpret_cast<const floatx4*>(nrm + row * lda + co + 4 * lane);
+      gm = *reinterpret_cast<const floatx4*>(gamma + 4 * lane);
+    }
 #pragma unroll
-  for (int k = 0; k < NPL; ++k) {
-    const int i = lane + G * k;
-    const bool in = i < n;
-    av[k] = in ? ar[i] : 0.f;
-    if (RECOMP)
-      gy[k] = in ? g[row * ldg + co + i] : 0.f;
-    else
-      gy[k] = in ? g[row * ldg + co + i] * tta_silu_grad(nrm[row * lda + co + i]) * gamma[i] : 0.f;
-    sum += av[k];
+    for (int k = 0; k < 4; ++k) {
+      av[k] = x[k];
+      gy[k] = RECOMP ? gv[k] : gv[k] * tta_silu_grad(nv[k]) * gm[k];
+      sum += av[k];
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < NPL; ++k) {
+      const int i = lane + G * k;
+      const bool in = i < n;
+      av[k] = in ? ar[i] : 0.f;
+      if (RECOMP)
+        gy[k] = in ? g[row * ldg + co + i] : 0.f;
+      else
+        gy[k] =
+            in ? g[row * ldg + co + i] * tta_silu_grad(nrm[row * lda + co + i]) * gamma[i] : 0.f;
+      sum += av[k];
+    }
   }
   const float mean = tta_group_sum(sum, G) / n;
   float sq = 0.f;
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
     const float d = av[k] - mean;
-    if (lane + G * k < n) sq += d * d;
+    if (VEC || lane + G * k < n) sq += d * d;
   }
   const float var = tta_group_sum(sq, G) / n;
   const float rstd = 1.0f / sqrtf(var + eps);
   if (RECOMP) {
+    if constexpr (VEC) {
+      const floatx4 gm = *reinterpret_cast<const floatx4*>(gamma + 4 * lane);
+      const floatx4 bt = *reinterpret_cast<const floatx4*>(beta + 4 * lane);
 #pragma unroll
-    for (int k = 0; k < NPL; ++k) {
-      const int i = lane + G * k;
-      if (i >= n) continue;
-      const float y = (av[k] - mean) * rstd * gamma[i] + beta[i];
-      gy[k] = gy[k] * tta_silu_grad(y) * gamma[i];
+      for (int k = 0; k < 4; ++k) {
+        const float y = (av[k] - mean) * rstd * gm[k] + bt[k];
+        gy[k] = gy[k] * tta_silu_grad(y) * gm[k];
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < NPL; ++k) {
+        const int i = lane + G * k;
+        if (i >= n) continue;
+        const float y = (av[k] - mean) * rstd * gamma[i] + beta[i];
+        gy[k] = gy[k] * tta_silu_grad(y) * gamma[i];
+      }
     }
   }
   float m1 = 0.f, m2 = 0.f;
@@ -187,6 +241,16 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   m1 = tta_group_sum(m1, G) / n;
   m2 = tta_group_sum(m2, G) / n;
   if (!valid) return;
+  if constexpr (VEC) {
+    floatx4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float xh = (av[k] - mean) * rstd;
+      o[k] = rstd * (gy[k] - m1 - xh * m2);
+    }
+    *reinterpret_cast<floatx4*>(g_a + row * ldo + co + 4 * lane) = o;
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
     const int i = lane + G * k;
@@ -461,6 +525,9 @@ extern "C" int tta_gate_bwd(const float* g_y, const float* x, const float* gatin
   return tta::kOk;
 }
 
+// a null pointer counts as aligned (an operand the call does not use)
+static bool al16(const void* q) { return ((uintptr_t)q & 15) == 0; }
+
 extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* beta, float* nrm,
                                float* s, int64_t R, int64_t n, int64_t groups, int64_t lda,
                                int64_t lds, float eps, hipStream_t stream) {
@@ -470,19 +537,27 @@ extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* 
   if (R == 0) return tta::kOk;
   TTA_CHECK_ARG(a && gamma && beta && s, "tta_ln_silu_fwd: null pointer");
   const int64_t RV = R * groups;
-#define TTA_LN_FWD(G, NPL)                                                                  \
-  hipLaunchKernelGGL((k_ln_silu_fwd<G, NPL>), dim3(tta_blocks(RV * G, 256)), dim3(256), 0,    \
-                     stream, a, gamma, beta, nrm, s, R, (int)n, (int)groups, lda, lds, eps)
+  // float4 rows (four contiguous columns per lane) when a row group is exactly four per lane and
+  // every row starts 16-byte aligned
+  const bool vec = (n == 128 || n == 256) && lda % 4 == 0 && lds % 4 == 0 && al16(a) &&
+                   al16(gamma) && al16(beta) && al16(nrm) && al16(s);
+#define TTA_LN_FWD(G, NPL, VEC)                                                             \
+  hipLaunchKernelGGL((k_ln_silu_fwd<G, NPL, VEC>), dim3(tta_blocks(RV * G, 256)), dim3(256),  \
+                     0, stream, a, gamma, beta, nrm, s, R, (int)n, (int)groups, lda, lds, eps)
   if (n <= 32)
-    TTA_LN_FWD(32, 1);
+    TTA_LN_FWD(32, 1, false);
   else if (n <= 64)
-    TTA_LN_FWD(32, 2);
+    TTA_LN_FWD(32, 2, false);
+  else if (n <= 128 && vec)
+    TTA_LN_FWD(32, 4, true);
   else if (n <= 128)
-    TTA_LN_FWD(32, 4);
+    TTA_LN_FWD(32, 4, false);
+  else if (n <= 256 && vec)
+    TTA_LN_FWD(64, 4, true);
   else if (n <= 256)
-    TTA_LN_FWD(64, 4);
+    TTA_LN_FWD(64, 4, false);
   else
-    TTA_LN_FWD(64, 8);
+    TTA_LN_FWD(64, 8, false);
 #undef TTA_LN_FWD
   TTA_CHECK_LAUNCH("tta_ln_silu_fwd");
   return tta::kOk;
@@ -500,27 +575,33 @@ extern "C" int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm,
   TTA_CHECK_ARG(g && a && gamma && g_a && (nrm || beta),
                 "tta_ln_silu_bwd: null pointer (nrm, or beta to recompute it, is required)");
   const int64_t RV = R * groups;
-#define TTA_LN_BWD(G, NPL)                                                                  \
+  const bool vec = (n == 128 || n == 256) && ldg % 4 == 0 && lda % 4 == 0 && ldo % 4 == 0 &&
+                   al16(g) && al16(a) && al16(nrm) && al16(gamma) && al16(beta) && al16(g_a);
+#define TTA_LN_BWD(G, NPL, VEC)                                                             \
   do {                                                                                      \
     if (nrm)                                                                                \
-      hipLaunchKernelGGL((k_ln_silu_bwd<G, NPL, false>), dim3(tta_blocks(RV * G, 256)),     \
+      hipLaunchKernelGGL((k_ln_silu_bwd<G, NPL, false, VEC>), dim3(tta_blocks(RV * G, 256)), \
                          dim3(256), 0, stream, g, a, nrm, gamma, beta, g_a, R, (int)n,      \
                          (int)groups, ldg, lda, ldo, eps);                                  \
     else                                                                                    \
-      hipLaunchKernelGGL((k_ln_silu_bwd<G, NPL, true>), dim3(tta_blocks(RV * G, 256)),      \
+      hipLaunchKernelGGL((k_ln_silu_bwd<G, NPL, true, VEC>), dim3(tta_blocks(RV * G, 256)), \
                          dim3(256), 0, stream, g, a, nrm, gamma, beta, g_a, R, (int)n,      \
                          (int)groups, ldg, lda, ldo, eps);                                  \
   } while (0)
   if (n <= 32)
-    TTA_LN_BWD(32, 1);
+    TTA_LN_BWD(32, 1, false);
   else if (n <= 64)
-    TTA_LN_BWD(32, 2);
+    TTA_LN_BWD(32, 2, false);
+  else if (n <= 128 && vec)
+    TTA_LN_BWD(32, 4, true);
   else if (n <= 128)
-    TTA_LN_BWD(32, 4);
+    TTA_LN_BWD(32, 4, false);
+  else if (n <= 256 && vec)
+    TTA_LN_BWD(64, 4, true);
   else if (n <= 256)
-    TTA_LN_BWD(64, 4);
+    TTA_LN_BWD(64, 4, false);
   else
-    TTA_LN_BWD(64, 8);
+    TTA_LN_BWD(64, 8, false);
 #undef TTA_LN_BWD
   TTA_CHECK_LAUNCH("tta_ln_silu_bwd");
   return tta::kOk;

@@ -322,9 +322,12 @@ def test_edge_wigner_matches_oracle(nat):
     assert (coef.cpu() - torch.stack([g32[:, i, j] for i, j in IJ], 1)).abs().max() < 2e-6
 
 
-def test_edge_features_matches_oracle(nat):
+@pytest.mark.parametrize("nb,ec", [(32, 8), (30, 6)])
+def test_edge_features_matches_oracle(nat, nb, ec):
+    """Gaussian basis, species embeddings and envelope; (32, 8) runs the float4 wavefront-per-edge
+    kernel, (30, 6) the element-per-thread one."""
     g = torch.Generator().manual_seed(3)
-    E, nb, ec = 400, 32, 8
+    E = 400
     dist = torch.rand(E, generator=g) * 6.5 + 0.2
     zs, zt = torch.randint(0, 10, (E,), generator=g), torch.randint(0, 10, (E,), generator=g)
     semb, temb = torch.randn(10, ec, generator=g), torch.randn(10, ec, generator=g)

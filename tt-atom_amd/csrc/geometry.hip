@@ -62,6 +62,41 @@ __global__ __launch_bounds__(256) void k_edge_features(
   if (k == 0) env[e] = tta_geo::envelope(d, cutoff);
 }
 
+// The same row, one wavefront per edge and four consecutive columns per lane and store
+// (nb, ec multiples of 4; 16-byte aligned x_edge and embedding rows): no per-element index
+// division and whole 16-byte stores.  The same per-element arithmetic as k_edge_features.
+typedef float floatx4e __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void k_edge_features_v4(
+    const float* __restrict__ dist, const int* __restrict__ zs, const int* __restrict__ zt,
+    const float* __restrict__ semb, const float* __restrict__ temb, const float* __restrict__ off,
+    float coeff, float cutoff, int nb, int ec, float* __restrict__ x_edge,
+    float* __restrict__ env, int E) {
+  const int lane = threadIdx.x & 63;
+  const int64_t e = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (e >= E) return;
+  const int w4 = (nb + 2 * ec) / 4, nb4 = nb / 4, ec4 = ec / 4;
+  const float d = dist[e];
+  floatx4e* row = reinterpret_cast<floatx4e*>(x_edge + e * (int64_t)(nb + 2 * ec));
+  const int s = ec ? zs[e] : 0, t = ec ? zt[e] : 0;
+  for (int q = lane; q < w4; q += 64) {
+    floatx4e v;
+    if (q < nb4) {
+      const floatx4e o = reinterpret_cast<const floatx4e*>(off)[q];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float u = d - o[i];
+        v[i] = expf(coeff * (u * u));
+      }
+    } else if (q < nb4 + ec4) {
+      v = reinterpret_cast<const floatx4e*>(semb + (int64_t)s * ec)[q - nb4];
+    } else {
+      v = reinterpret_cast<const floatx4e*>(temb + (int64_t)t * ec)[q - nb4 - ec4];
+    }
+    row[q] = v;
+  }
+  if (lane == 0) env[e] = tta_geo::envelope(d, cutoff);
+}
+
 // g_ev[e] = VJP of (coef, gaussians, envelope, |ev|) at the given adjoints.  Four lanes per
 // edge: the gaussian sum (nb terms, the edge's adjoint row read by consecutive lanes) is split
 // over the four and reduced across them in a fixed order; each of the four then evaluates the
@@ -264,9 +299,15 @@ extern "C" int tta_edge_features(const float* dist, const int* zsrc, const int* 
   TTA_CHECK_ARG(dist && offsets && x_edge && env && (ec == 0 || (zsrc && ztgt && src_emb && tgt_emb)),
                 "tta_edge_features: null pointer");
   const int64_t total = E * (nb + 2 * ec);
-  hipLaunchKernelGGL(k_edge_features, dim3(tta_blocks(total, 256)), dim3(256), 0, stream, dist,
-                     zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, (int)nb, (int)ec,
-                     x_edge, env, (int)E);
+  auto al = [](const void* q) { return q == nullptr || ((uintptr_t)q & 15) == 0; };
+  if (nb % 4 == 0 && ec % 4 == 0 && al(x_edge) && al(offsets) && al(src_emb) && al(tgt_emb))
+    hipLaunchKernelGGL(k_edge_features_v4, dim3(tta_blocks(E, 4)), dim3(256), 0, stream, dist,
+                       zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, (int)nb, (int)ec,
+                       x_edge, env, (int)E);
+  else
+    hipLaunchKernelGGL(k_edge_features, dim3(tta_blocks(total, 256)), dim3(256), 0, stream,
+                       dist, zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, (int)nb,
+                       (int)ec, x_edge, env, (int)E);
   TTA_CHECK_LAUNCH("tta_edge_features");
   return tta::kOk;
 }

@@ -654,6 +654,23 @@ def test_forces_virial_and_sum(nat):
     assert (Fo.cpu() - ref_F).abs().max() < 1e-5
     assert (Vo.cpu().reshape(3, 3) - ref_V).abs().max() < 1e-3
     assert abs(float(so) - float(x.double().sum())) < 1e-3
+    # a hub node (300 source and 200 destination edges: many passes of the 16 lanes of a node),
+    # isolated nodes, and the same bits on a second call
+    N2, E2 = 40, 900
+    src2 = torch.randint(0, 30, (E2,), generator=g)
+    tgt2 = torch.randint(0, 30, (E2,), generator=g)
+    src2[:300], tgt2[300:500] = 7, 7
+    o = torch.argsort(tgt2, stable=True)
+    src2, tgt2 = src2[o], tgt2[o]
+    g2 = torch.randn(E2, 3, generator=g)
+    ref2 = -(torch.zeros(N2, 3).index_add(0, src2, g2) - torch.zeros(N2, 3).index_add(0, tgt2, g2))
+    F2 = [torch.empty(N2, 3, device=DEV) for _ in range(2)]
+    for Fi in F2:
+        nat.node_forces(g2.to(DEV), _i32(_csr(src2, N2)), _i32(torch.argsort(src2, stable=True)),
+                        _i32(_csr(tgt2, N2)), Fi)
+    torch.cuda.synchronize()
+    assert (F2[0].cpu() - ref2).abs().max() < 1e-4 and torch.equal(F2[0], F2[1])
+    assert F2[0][30:].abs().max() == 0
 
 
 @pytest.mark.parametrize("mode,M", [(16, 5000), (6, 5000), (16, 700)])

@@ -178,21 +178,37 @@ __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
 }
 
 // F[n] = -(sum_{src(e) = n} g_ev[e] - sum_{tgt(e) = n} g_ev[e])   (ev = pos[src] - pos[tgt])
+// 16 lanes per node: lane j takes the node's source edges j, j + 16, ... and destination edges
+// likewise, and the 16 partial sums meet in a fixed xor-tree order (deterministic).
 __global__ __launch_bounds__(256) void k_node_forces(const float* __restrict__ g_ev,
                                                      const int* __restrict__ src_ptr,
                                                      const int* __restrict__ src_perm,
                                                      const int* __restrict__ tgt_ptr,
                                                      float* __restrict__ forces, int N) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= N) return;
+  const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+  const int n = gid >> 4, j = gid & 15;
+  const bool on = n < N;
   float a[3] = {0.f, 0.f, 0.f}, b[3] = {0.f, 0.f, 0.f};
-  for (int k = src_ptr[n]; k < src_ptr[n + 1]; ++k) {
-    const int64_t e = src_perm[k];
-    for (int c = 0; c < 3; ++c) a[c] += g_ev[e * 3 + c];
+  if (on) {
+    for (int k = src_ptr[n] + j; k < src_ptr[n + 1]; k += 16) {
+      const int64_t e = src_perm[k];
+#pragma unroll
+      for (int c = 0; c < 3; ++c) a[c] += g_ev[e * 3 + c];
+    }
+    for (int64_t e = tgt_ptr[n] + j; e < tgt_ptr[n + 1]; e += 16)
+#pragma unroll
+      for (int c = 0; c < 3; ++c) b[c] += g_ev[e * 3 + c];
   }
-  for (int64_t e = tgt_ptr[n]; e < tgt_ptr[n + 1]; ++e)
-    for (int c = 0; c < 3; ++c) b[c] += g_ev[e * 3 + c];
-  for (int c = 0; c < 3; ++c) forces[(int64_t)n * 3 + c] = -(a[c] - b[c]);
+  // every lane of the wavefront takes part in the shuffles (nodes past N contribute zeros)
+#pragma unroll
+  for (int m = 8; m >= 1; m >>= 1)
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      a[c] += __shfl_xor(a[c], m, 16);
+      b[c] += __shfl_xor(b[c], m, 16);
+    }
+  if (on && j == 0)
+    for (int c = 0; c < 3; ++c) forces[(int64_t)n * 3 + c] = -(a[c] - b[c]);
 }
 
 // Virial dE/dstrain = sum_e 0.5 (ev_a g_b + ev_b g_a): fixed-order two-stage reduction.
@@ -342,11 +358,11 @@ extern "C" int tta_edge_geometry_bwd(const float* ev, const float* dist, const f
 extern "C" int tta_node_forces(const float* g_ev, const int* src_ptr, const int* src_perm,
                                const int* tgt_ptr, float* forces, int64_t N, int64_t E,
                                hipStream_t stream) {
-  TTA_CHECK_ARG(N >= 0 && N < (1ll << 31) && E >= 0, "tta_node_forces: bad sizes");
+  TTA_CHECK_ARG(N >= 0 && N < (1ll << 27) && E >= 0, "tta_node_forces: bad sizes (N < 2^27)");
   if (N == 0) return tta::kOk;
   TTA_CHECK_ARG(src_ptr && src_perm && tgt_ptr && forces && (g_ev || E == 0),
                 "tta_node_forces: null pointer");
-  hipLaunchKernelGGL(k_node_forces, dim3(tta_blocks(N, 256)), dim3(256), 0, stream, g_ev, src_ptr,
+  hipLaunchKernelGGL(k_node_forces, dim3(tta_blocks(N * 16, 256)), dim3(256), 0, stream, g_ev, src_ptr,
                      src_perm, tgt_ptr, forces, (int)N);
   TTA_CHECK_LAUNCH("tta_node_forces");
   return tta::kOk;

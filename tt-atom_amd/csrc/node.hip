@@ -563,6 +563,7 @@ struct HeadArgs {
   float* g_ne;                            // backward output [N, 9, C]
   int64_t N;
   int C, H;
+  int npb;                                // nodes per workgroup, NT or NT / 2 (rows past it zero)
 };
 
 // Per-node energy MLP on coefficient 0: a1 = ne0 @ w0t + b0, s1 = silu(a1), a2 = s1 @ w1t + b1,
@@ -571,8 +572,8 @@ __global__ __launch_bounds__(NTH, 1) void k_energy_head_fwd(HeadArgs p) {
   __shared__ float buf[NT * LDP];
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int C = p.C, H = p.H;
-  const int64_t n0 = (int64_t)blockIdx.x * NT;
-  const int nv = (int)min((int64_t)NT, p.N - n0);
+  const int64_t n0 = (int64_t)blockIdx.x * p.npb;
+  const int nv = (int)min((int64_t)p.npb, p.N - n0);
   for (int rr = wave; rr < NT; rr += NW)
     for (int ch = lane; ch < C; ch += 64)
       buf[rr * LDP + ch] = rr < nv ? p.ne[(n0 + rr) * 9 * C + ch] : 0.f;
@@ -630,8 +631,8 @@ __global__ __launch_bounds__(NTH, 1) void k_energy_head_bwd(HeadArgs p) {
   __shared__ float buf[NT * LDP];
   const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int C = p.C, H = p.H;
-  const int64_t n0 = (int64_t)blockIdx.x * NT;
-  const int nv = (int)min((int64_t)NT, p.N - n0);
+  const int64_t n0 = (int64_t)blockIdx.x * p.npb;
+  const int nv = (int)min((int64_t)p.npb, p.N - n0);
   for (int rr = wave; rr < NT; rr += NW)
     for (int ch = lane; ch < H; ch += 64)
       buf[rr * LDP + ch] = rr < nv ? p.w2[ch] * tta_silu_grad(p.a2[(n0 + rr) * H + ch]) : 0.f;
@@ -678,7 +679,7 @@ bool node_dims_ok(int64_t N, int C, int H) {
 
 }  // namespace
 
-// Nodes per workgroup of the spectral kernels: NT, or NT / 2 when NT-node workgroups would not
+// Nodes per workgroup of the node kernels: NT, or NT / 2 when NT-node workgroups would not
 // cover the compute units (their MFMA tiles keep NT rows, the rows past the workgroup's nodes
 // zero, so a half-full workgroup costs about what a full one does but the per-node phases --
 // loads, norms, stores -- halve and twice as many units work).
@@ -748,8 +749,8 @@ extern "C" int tta_energy_head_fwd(const float* ne, const float* w0t, const floa
                 "tta_energy_head_fwd: null pointer");
   if (N == 0) return tta::kOk;
   HeadArgs p{ne, w0t, b0, w1t, b1, w2, b2, nullptr, nullptr, a1, a2, node_e, nullptr, N, (int)C,
-             (int)H};
-  hipLaunchKernelGGL(k_energy_head_fwd, dim3(tta_blocks(N, NT)), dim3(NTH), 0, stream, p);
+             (int)H, spectral_npb(N)};
+  hipLaunchKernelGGL(k_energy_head_fwd, dim3(tta_blocks(N, p.npb)), dim3(NTH), 0, stream, p);
   TTA_CHECK_LAUNCH("tta_energy_head_fwd");
   return tta::kOk;
 }
@@ -762,8 +763,9 @@ extern "C" int tta_energy_head_bwd(const float* a1, const float* a2, const float
   TTA_CHECK_ARG(a1 && a2 && w0 && w1 && w2 && g_ne, "tta_energy_head_bwd: null pointer");
   if (N == 0) return tta::kOk;
   HeadArgs p{nullptr, nullptr, nullptr, nullptr, nullptr, w2, nullptr, w0, w1,
-             const_cast<float*>(a1), const_cast<float*>(a2), nullptr, g_ne, N, (int)C, (int)H};
-  hipLaunchKernelGGL(k_energy_head_bwd, dim3(tta_blocks(N, NT)), dim3(NTH), 0, stream, p);
+             const_cast<float*>(a1), const_cast<float*>(a2), nullptr, g_ne, N, (int)C, (int)H,
+             spectral_npb(N)};
+  hipLaunchKernelGGL(k_energy_head_bwd, dim3(tta_blocks(N, p.npb)), dim3(NTH), 0, stream, p);
   TTA_CHECK_LAUNCH("tta_energy_head_bwd");
   return tta::kOk;
 }

@@ -4,7 +4,9 @@
  * Conventions (every entry point):
  *   - device pointers to caller-allocated buffers (the PyTorch caching allocator owns memory;
  *     nothing here allocates), int64_t sizes, fp32 data, int32 indices, row-major layouts;
- *   - work is enqueued on `stream` (hipStream_t, passed as void*), stream-ordered, reentrant;
+ *   - work is enqueued on `stream` (hipStream_t, passed as void*), stream-ordered, reentrant
+ *     (one exception: tta_virial_noalloc shares a per-GPU device array between calls, so calls
+ *     of it that overlap on one GPU race; see its declaration);
  *   - return 0 on success, non-zero on bad arguments / launch failure, with the message in
  *     tta_last_error() (thread-local).  The Python layer raises RuntimeError on non-zero,
  *     matching the reference's fail-loud validation (fused_rotate_device_operation.cpp:16-44

@@ -174,12 +174,13 @@ def test_split_gemm_persistent_tiles(nat, mode, tol):
 @pytest.mark.parametrize("epi", [0, 1])
 def test_split_gemm_short_k_panel(nat, K, epi):
     """Short-K mode-16 products (K <= 128, at least 128 columns, plain or SiLU
-    epilogue) run on the panel kernel: a workgroup splits a 256-row panel of A once and sweeps a
+    epilogue) run on the panel kernel: a workgroup splits a 128-row panel of A once and sweeps a
     run of column tiles.  K = 128 goes through linear_group as the radial output layer does (two
-    products of different widths: 1536 = two runs of six tiles, 1100 = nine tiles with a ragged
-    last one); the K that end inside a 32-wide slab through the C entry point.  Ragged rows
-    (20001 = 78 panels + 33 rows), and rows whose scale leaves the unscaled window (max 2^20,
-    2^-12 and 2^-30 times the rest, an all-zero row).  Error at fp32 level, each row's against
+    products of different widths: 1536 = two runs of twelve 64-column tiles, 1100 = eighteen
+    tiles, in runs of twelve and six, with a ragged last one); the K that end inside a 32-wide
+    slab through the C entry point.  Ragged rows (20001 = 156 panels of 128 rows + 33 rows), and
+    rows whose scale leaves the unscaled window (max 2^20, 2^-12 and 2^-30 times the rest, an
+    all-zero row).  Error at fp32 level, each row's against
     its own |A| |B|."""
     g = torch.Generator().manual_seed(K + 7 * epi)
     M1, M2 = 20001, 6000
@@ -562,7 +563,7 @@ def test_gate_fwd_bwd(nat, natural):
     assert torch.equal(gcomb[:, 2 * H:].reshape(R, 9, H), gxo) and torch.equal(gcomb[:, :2 * H], ggo)
 
 
-@pytest.mark.parametrize("n", [16, 64, 100, 128, 200, 512])
+@pytest.mark.parametrize("n", [16, 64, 100, 128, 200, 256, 512])
 def test_ln_silu_fwd_bwd(nat, n):
     R = 301                     # odd: the last two-row wavefront of short rows has one row
     g = torch.Generator().manual_seed(n)
@@ -610,6 +611,24 @@ def test_ln_silu_fwd_bwd(nat, n):
     assert torch.equal(s3, so) and torch.equal(g3[:R], gao) and bool(g3[R].isnan().all())
     with pytest.raises(RuntimeError):
         nat.ln_silu_bwd(f(gs), f(a), None, f(gam), g3[:R], R=R, n=n)
+    # g 4 bytes off a 16-byte boundary sends the backward down the element-wise path while the
+    # forward (aligned rows) took the float4 one: the row statistics are summed in the same order
+    # on both paths, so the recomputed LayerNorm output and the adjoint equal the float4 ones
+    gbuf = torch.empty(R * n + 1, device=DEV)
+    gmis = gbuf[1:].view(R, n)
+    gmis.copy_(f(gs))
+    g4, g5 = torch.empty(R, n, device=DEV), torch.empty(R, n, device=DEV)
+    nat.ln_silu_bwd(gmis, f(a), None, f(gam), g4, R=R, n=n, beta=f(bet))
+    nat.ln_silu_bwd(gmis, f(a), no, f(gam), g5, R=R, n=n)
+    # and the forward on the element-wise path (misaligned LayerNorm output)
+    nbuf = torch.empty(R * n + 1, device=DEV)
+    nmis = nbuf[1:].view(R, n)
+    s6 = torch.empty(R, n, device=DEV)
+    nat.ln_silu_fwd(f(a), f(gam), f(bet), nmis, s6, R=R, n=n)
+    torch.cuda.synchronize()
+    for t, what in ((g4, "recomputed, element-wise"), (g5, "saved, element-wise")):
+        assert torch.equal(t, gao), f"{what} adjoint differs in {int((t != gao).sum())} elements"
+    assert torch.equal(nmis, no) and torch.equal(s6, so), "element-wise forward differs"
 
 
 @pytest.mark.parametrize("C", [16, 128, 96, 256, 300])

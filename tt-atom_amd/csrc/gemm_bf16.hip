@@ -51,6 +51,7 @@
 #include "gemm_common.h"
 
 #include <algorithm>
+#include <atomic>
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -378,7 +379,9 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   }
   const int bstep = NB * NT32 * 128 * 16;  // bytes of one packed k slab
 
-  // copy parameters of the tile being loaded (they move on to the next tile before the epilogue)
+  // copy parameters of the tile being loaded: they move on to the next tile after the epilogue's
+  // last lgkmcnt(0) + s_barrier, and only then are that tile's slab-0 copies issued, because the
+  // epilogue's staging area aliases stage 0
   int m0 = 0, n0 = 0;
   __amdgpu_buffer_rsrc_t arsrc;
   int avo[APT], bvo[BPT];
@@ -1061,18 +1064,22 @@ __global__ __launch_bounds__(256) void k_pack_b_f16(const float* __restrict__ B,
 // own tile count exit at once.
 // Blocks per product of the persistent tile loop: two per compute unit (the kernel's occupancy),
 // rounded up to whole XCD rounds of 8.
+// The per-device entries are atomics: host threads calling the library at the same time may both
+// fill an entry, with the same value.
 int persistent_cap() {
-  static int cap[64] = {0};
+  static std::atomic<int> cap[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cap[dev] == 0) {
+  int c = cap[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       cus = 256;
-    cap[dev] = ((2 * cus + 7) / 8) * 8;
+    c = ((2 * cus + 7) / 8) * 8;
+    cap[dev].store(c, std::memory_order_relaxed);
   }
-  return cap[dev];
+  return c;
 }
 
 template <int WM, int MODE>

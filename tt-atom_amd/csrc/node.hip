@@ -24,6 +24,8 @@
 // Requirements (checked on the host): C and H multiples of 16, at most 128; lmax = 2.
 #include "common.h"
 
+#include <atomic>
+
 namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -684,17 +686,19 @@ bool node_dims_ok(int64_t N, int C, int H) {
 // zero, so a half-full workgroup costs about what a full one does but the per-node phases --
 // loads, norms, stores -- halve and twice as many units work).
 static int spectral_npb(int64_t N) {
-  static int cus_of[64] = {0};  // compute units per device, queried once
+  // compute units per device, queried once; atomics, since host threads calling the library at
+  // the same time may both fill an entry (with the same value)
+  static std::atomic<int> cus_of[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cus_of[dev] == 0) {
-    int cus = 0;
+  int cus = cus_of[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       cus = 256;
-    cus_of[dev] = cus;
+    cus_of[dev].store(cus, std::memory_order_relaxed);
   }
-  return (N + NT - 1) / NT < cus_of[dev] ? NT / 2 : NT;
+  return (N + NT - 1) / NT < cus ? NT / 2 : NT;
 }
 
 extern "C" int tta_spectral_block_fwd(const float* x1, const float* aw2, const float* ab2,

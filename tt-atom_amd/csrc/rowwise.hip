@@ -67,9 +67,12 @@ __global__ __launch_bounds__(256) void k_gate_bwd(const float* __restrict__ g_y,
 
 // ------------------------------------------------------------------ LayerNorm + SiLU (radial MLP)
 // G lanes per row (64, or 32 for rows of at most 128 so that a wavefront holds two rows and twice
-// the bytes are in flight per wave); the row stays in registers (element lane + G k in slot k,
+// the bytes are in flight per wave); the row stays in registers (element NPL lane + k in slot k,
 // NPL slots) so that each operand crosses HBM once.  The per-lane partial sums run over k in
-// order.  A row index past R (the odd tail of a two-row wavefront) reads row R - 1 and stores
+// order.  The float4 path (VEC) and the element-wise path hold the same columns in the same
+// slots and are compiled without fused multiply-adds, so both round every operation alike
+// whichever path the forward and the backward take (the backward's recomputed LayerNorm output
+// equals the forward's bit for bit).  A row index past R (the odd tail of a two-row wavefront) reads row R - 1 and stores
 // nothing, so every lane of the wave takes part in the butterflies.  Forward (so2.py:101-115 /
 // geometry.py:161-168):
 //   nrm = (a - mean) * rstd * gamma + beta,  s = silu(nrm)
@@ -84,6 +87,9 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
                                                      float* __restrict__ s, int64_t R, int n,
                                                      int groups, int64_t lda, int64_t lds,
                                                      float eps) {
+  // no fused multiply-adds: the float4 and the element-wise paths (and the forward and the
+  // backward's recomputation) then round every operation alike
+#pragma clang fp contract(off)
   const int64_t RV = R * groups;
   const int64_t rw = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / G;
   const int lane = threadIdx.x & (G - 1);
@@ -95,8 +101,8 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
   gamma += co;
   beta += co;
   const float* ar = a + row * lda + co;
-  // element k of lane l: column l + G k, or with VEC (n = 4 G, 16-byte aligned rows) column
-  // 4 l + k, all four in one float4
+  // element k of lane l: column NPL l + k; with VEC (n = 4 G, 16-byte aligned rows) all four
+  // in one float4
   float v[NPL];
   if constexpr (VEC) {
     static_assert(NPL == 4, "float4 rows");
@@ -108,7 +114,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
     if constexpr (!VEC) {
-      const int i = lane + G * k;
+      const int i = NPL * lane + k;
       v[k] = i < n ? ar[i] : 0.f;
     }
     sum += v[k];
@@ -118,7 +124,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
     const float d = v[k] - mean;
-    if (VEC || lane + G * k < n) sq += d * d;
+    if (VEC || NPL * lane + k < n) sq += d * d;
   }
   const float var = tta_group_sum(sq, G) / n;
   const float rstd = 1.0f / sqrtf(var + eps);
@@ -138,7 +144,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
   }
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
-    const int i = lane + G * k;
+    const int i = NPL * lane + k;
     if (i >= n) continue;
     const float y = (v[k] - mean) * rstd * gamma[i] + beta[i];
     if (nrm) nrm[row * lda + co + i] = y;
@@ -161,6 +167,9 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
                                                      float* __restrict__ g_a, int64_t R, int n,
                                                      int groups, int64_t ldg, int64_t lda,
                                                      int64_t ldo, float eps) {
+  // no fused multiply-adds: the float4 and the element-wise paths (and the forward and the
+  // backward's recomputation) then round every operation alike
+#pragma clang fp contract(off)
   const int64_t RV = R * groups;
   const int64_t rw = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / G;
   const int lane = threadIdx.x & (G - 1);
@@ -193,7 +202,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   } else {
 #pragma unroll
     for (int k = 0; k < NPL; ++k) {
-      const int i = lane + G * k;
+      const int i = NPL * lane + k;
       const bool in = i < n;
       av[k] = in ? ar[i] : 0.f;
       if (RECOMP)
@@ -209,7 +218,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
     const float d = av[k] - mean;
-    if (VEC || lane + G * k < n) sq += d * d;
+    if (VEC || NPL * lane + k < n) sq += d * d;
   }
   const float var = tta_group_sum(sq, G) / n;
   const float rstd = 1.0f / sqrtf(var + eps);
@@ -225,7 +234,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
     } else {
 #pragma unroll
       for (int k = 0; k < NPL; ++k) {
-        const int i = lane + G * k;
+        const int i = NPL * lane + k;
         if (i >= n) continue;
         const float y = (av[k] - mean) * rstd * gamma[i] + beta[i];
         gy[k] = gy[k] * tta_silu_grad(y) * gamma[i];
@@ -253,7 +262,7 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   }
 #pragma unroll
   for (int k = 0; k < NPL; ++k) {
-    const int i = lane + G * k;
+    const int i = NPL * lane + k;
     if (i >= n) continue;
     const float xh = (av[k] - mean) * rstd;
     g_a[row * ldo + co + i] = rstd * (gy[k] - m1 - xh * m2);

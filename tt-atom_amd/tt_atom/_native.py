@@ -632,7 +632,10 @@ def silu_bwd(g, x, out):
 
 
 def reduce_sum(x, n, stride, out):
-    _call("tta_sum", x.data_ptr(), n, stride, _ptr(out, numel=1), _stream())
+    """out[0] = sum of x[0], x[stride], ..., x[(n - 1) * stride] (x fp32 on the device)."""
+    if stride < 1:
+        raise RuntimeError("reduce_sum: stride must be >= 1")
+    _call("tta_sum", _rows(x, n, stride, 1, "x"), n, stride, _ptr(out, numel=1), _stream())
 
 
 def segment_sum(x, ptr, out):
@@ -667,9 +670,12 @@ def edge_features(dist, zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, nb
 def edge_geometry_bwd(ev, dist, g_coef, g_env, g_gauss, ldg, offsets, coeff, cutoff, nb, jd,
                       gamma, g_ev):
     E = dist.numel()
+    if g_gauss is not None and (ldg < nb or offsets is None or offsets.numel() < nb):
+        raise RuntimeError("edge_geometry_bwd: g_gauss needs ldg >= nb and nb offsets")
     _call("tta_edge_geometry_bwd", _ptr(ev, numel=E * 3), _ptr(dist, numel=E),
           _ptr(g_coef, numel=E * 35, name="g_coef"), _ptr(g_env, numel=E, name="g_env"),
-          None if g_gauss is None else g_gauss.data_ptr(), ldg, _ptr(offsets, name="offsets"),
+          None if g_gauss is None else _rows(g_gauss, E, ldg, nb, "g_gauss"), ldg,
+          _ptr(offsets, name="offsets"),
           float(coeff), float(cutoff), nb, _ptr(jd, numel=35), float(gamma),
           _ptr(g_ev, numel=E * 3), E, _stream())
 

@@ -64,7 +64,7 @@ class Session:
     """One bundle on one GPU; evaluates systems given as arrays."""
 
     def __init__(self, bundle, task_name=None, device=None, gamma=0.0, max_neighbors=None,
-                 neighbor_list="device", precision="f32"):
+                 neighbor_list="device", precision="f32", fast=False):
         if neighbor_list not in ("host", "device"):
             raise ValueError("neighbor_list must be 'host' or 'device'")
         self.neighbor_list = neighbor_list
@@ -81,7 +81,7 @@ class Session:
         self._w = w
         self.C = self.cfg["sphere_channels"]
         self.backbone = model.Backbone(w, self.device, self.cfg, bundle.to_grid_mat,
-                                       bundle.from_grid_mat, precision=precision)
+                                       bundle.from_grid_mat, precision=precision, fast=fast)
         self.geo = geometry.HostGeometry(w, self.cfg, bundle.to_m, bundle.gauss_offset,
                                          bundle.gauss_coeff, gamma=gamma,
                                          coefficient_index=bundle.coefficient_index,
@@ -179,12 +179,11 @@ class TTAtomCalculator(_AseCalculator):
         if not HAVE_ASE:
             raise ImportError("TTAtomCalculator needs ase; tt_atom.calculator.Session evaluates "
                               "arrays without it")
-        if fast:
-            raise RuntimeError("fast (reduced-precision) mode is not part of this fp32 build")
         super().__init__(**kwargs)
         dev = device if device is not None else torch.device(f"cuda:{device_id}")
+        # fast=True: bf16 GEMM operands (model.Backbone), as OrbCalculator does
         self.session = Session(bundle, task_name=task_name, device=dev, gamma=gamma,
-                               max_neighbors=max_neighbors)
+                               max_neighbors=max_neighbors, fast=fast)
         self.task = self.task_name = self.session.task
 
     @classmethod

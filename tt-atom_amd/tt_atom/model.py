@@ -197,8 +197,11 @@ class Backbone:
 
     def __init__(self, weights, device, cfg, to_grid_mat=None, from_grid_mat=None, *, fast=False,
                  n_gauss=None, precision="f32"):
+        # fast=True is the reference's reduced-precision device path (bf16 / bf8 weights and
+        # edge tensors, device.py:146-155, calculator.py:22-66): here bf16 GEMM operands with
+        # fp32 accumulation, the same rule as the Orb modules (orb_model._precision)
         if fast:
-            raise RuntimeError("fast (reduced-precision) mode is not part of this fp32 build")
+            precision = "bf16"
         if precision not in PRECISIONS:
             raise RuntimeError(f"precision must be one of {sorted(PRECISIONS)}")
         self.precision = precision

@@ -28,6 +28,7 @@ import numpy as np
 import torch
 
 from . import _native as nat
+from .engine_cache import cached_engine
 from .graphs import StepGraphs
 from .geometry import system_graphs
 from .model import PRECISIONS, _gw
@@ -565,13 +566,22 @@ class OrbEngine:
 
 
 # ----------------------------------------------------------------------------- functional API
-def _prepare(model, pos, senders, receivers, atomic_numbers, cell_shift, natoms, cond_nodes):
+def _prepare(model, pos, senders, receivers, atomic_numbers, cell_shift, natoms, cond_nodes,
+             slot):
+    """The step engine of this topology: the one kept on ``model`` from the last call with the
+    same senders, receivers, species, cell shifts, system sizes and conditioning
+    (``engine_cache``, so a fixed-topology loop replays the captured step), else a new one."""
     dev = model.device
     N = int(torch.as_tensor(atomic_numbers).shape[0])
-    graph = OrbGraph(dev, senders=senders, receivers=receivers, num_nodes=N,
-                     atomic_numbers=atomic_numbers, cell_shift=cell_shift, natoms=natoms)
-    # one step per engine: launched eagerly (a graph pays off from the second step on)
-    eng = OrbEngine(model, graph, cond_nodes, use_graph=False)
+
+    def build():
+        graph = OrbGraph(dev, senders=senders, receivers=receivers, num_nodes=N,
+                         atomic_numbers=atomic_numbers, cell_shift=cell_shift, natoms=natoms)
+        return OrbEngine(model, graph, cond_nodes)
+
+    key = (senders, receivers, atomic_numbers, cell_shift,
+           None if natoms is None else tuple(int(n) for n in natoms), cond_nodes)
+    eng = cached_engine(model, slot, key, build)
     p = torch.as_tensor(pos, dtype=torch.float32).to(dev).contiguous()
     return eng, p
 
@@ -580,7 +590,8 @@ def energy_and_forces(model, *, pos, senders, receivers, atomic_numbers, cell_sh
                       compute_stress=False, cond_nodes=None):
     """Single system (orb_forces.py:307-378): raw energy (float), raw forces [N, 3] (host fp32)
     and, with ``compute_stress``, the raw virial dE/dstrain [3, 3]."""
-    eng, p = _prepare(model, pos, senders, receivers, atomic_numbers, cell_shift, None, cond_nodes)
+    eng, p = _prepare(model, pos, senders, receivers, atomic_numbers, cell_shift, None, cond_nodes,
+                      "energy_and_forces")
     raw, F, vir = eng.run(p, compute_stress)
     out = (float(raw[0]), F.detach().cpu().clone())
     return out if not compute_stress else out + (vir.detach().cpu().clone(),)
@@ -590,7 +601,7 @@ def energy_and_forces_batch(model, *, pos, senders, receivers, atomic_numbers, n
                             cell_shift=None, cond_nodes=None):
     """Disjoint-union batch (orb_forces.py:257-304): raw energies [K] (fp64) and raw forces."""
     eng, p = _prepare(model, pos, senders, receivers, atomic_numbers, cell_shift, natoms,
-                      cond_nodes)
+                      cond_nodes, "energy_and_forces_batch")
     raw, F, _ = eng.run(p, False)
     return raw, F.detach().cpu().clone()
 

@@ -292,9 +292,10 @@ class OrbCalculator(_AseCalculator):
         if not HAVE_ASE:
             raise ImportError("OrbCalculator needs ase; tt_atom.orb_calculator.OrbSession "
                               "evaluates arrays without it")
+        # fast=True (the reference's bf8 weights, orb_calculator.py:26-73) selects bf16 GEMM
+        # operands, as the Orb modules and the UMA calculator do
         if fast:
-            raise RuntimeError("fast (bf8) weights are not part of this build; use "
-                               "precision='bf16' for bf16 GEMM operands")
+            precision = "bf16"
         super().__init__(**kwargs)
         # bucketing pads edge counts so ttnn reuses compiled shapes; the HIP kernels are shape-
         # generic, so it changes nothing here

@@ -18,6 +18,7 @@ from __future__ import annotations
 import torch
 
 from . import orb as _orb
+from .engine_cache import cached_engine
 
 __all__ = ["energy_and_forces", "energy_and_forces_batch"]
 
@@ -46,15 +47,24 @@ def _model(encoder, layers, ehead, device, r_max, num_bases):
 
 
 def _engine(m, pos, senders, receivers, atomic_numbers, node_feat, cell_shift, natoms,
-            cond_nodes):
+            cond_nodes, slot):
+    """The step engine of this topology, kept on the OrbModel between calls with the same
+    senders, receivers, species, node features, cell shifts, system sizes and conditioning
+    (``engine_cache``: a fixed-topology MD loop replays the captured step)."""
     N = int(torch.as_tensor(atomic_numbers).shape[0])
-    graph = _orb.OrbGraph(m.device, senders=senders, receivers=receivers, num_nodes=N,
-                          atomic_numbers=atomic_numbers, cell_shift=cell_shift, natoms=natoms)
     cond = cond_nodes if (cond_nodes is not None and any(
         l.cond_w_t is not None for l in m.layers)) else None
-    # one step per call, launched eagerly (a graph pays off from the second step of a topology)
-    eng = _orb.OrbEngine(m, graph, cond, use_graph=False,
-                         node_feat=torch.as_tensor(node_feat, dtype=torch.float32))
+
+    def build():
+        graph = _orb.OrbGraph(m.device, senders=senders, receivers=receivers, num_nodes=N,
+                              atomic_numbers=atomic_numbers, cell_shift=cell_shift,
+                              natoms=natoms)
+        return _orb.OrbEngine(m, graph, cond,
+                              node_feat=torch.as_tensor(node_feat, dtype=torch.float32))
+
+    key = (senders, receivers, atomic_numbers, torch.as_tensor(node_feat), cell_shift,
+           None if natoms is None else tuple(int(n) for n in natoms), cond)
+    eng = cached_engine(m, slot, key, build)
     p = torch.as_tensor(pos).to(m.device, torch.float32).contiguous()
     return eng, p
 
@@ -68,7 +78,7 @@ def energy_and_forces(encoder, layers, ehead, device, *, pos, senders, receivers
     ``pos``'s floating dtype."""
     m = _model(encoder, layers, ehead, device, r_max, num_bases)
     eng, p = _engine(m, pos, senders, receivers, atomic_numbers, node_feat, cell_shift, None,
-                     cond_nodes)
+                     cond_nodes, "energy_and_forces")
     raw, F, vir = eng.run(p, compute_stress)
     dt = pos.dtype if torch.is_tensor(pos) and pos.is_floating_point() else torch.float32
     out = (float(raw[0]), F.detach().to("cpu", dt))
@@ -105,7 +115,7 @@ def energy_and_forces_batch(encoder, layers, ehead, device, *, pos, senders, rec
         raise ValueError("seg_mean_T must be the transpose of seg_mean")
     m = _model(encoder, layers, ehead, device, r_max, num_bases)
     eng, p = _engine(m, pos, senders, receivers, atomic_numbers, node_feat, cell_shift, natoms,
-                     cond_nodes)
+                     cond_nodes, "energy_and_forces_batch")
     raw, F, _ = eng.run(p, False)
     dt = pos.dtype if torch.is_tensor(pos) and pos.is_floating_point() else torch.float32
     return raw, F.detach().to("cpu", dt)

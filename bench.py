@@ -62,6 +62,11 @@ KERNELS = {"f32": "gemm_f32_kernel (fp32 MFMA 16x16x4)",
 # ``bench.py --summarize-counters`` from the profiler's CSV output; read to report counter-measured
 # HBM bytes next to the algorithmic ones.
 TRAFFIC_FILE = ROOT / "profiles" / "uma_c3_step_counters.txt"
+# per workload: the counter summary and the profiled step's title and command
+COUNTER_FILES = {"c3": TRAFFIC_FILE, "c5": ROOT / "profiles" / "orb_c5_step_counters.txt"}
+COUNTER_TITLES = {
+    "c3": "C3 step (uma-s-1 architecture, 2048 atoms, E = 61440)",
+    "c5": "C5 step (Orb-v3 conservative architecture, 256 molecules, 10,150 atoms, E = 196,555)"}
 
 
 class GemmEvents:
@@ -521,8 +526,8 @@ def _read_pmc(d):
     return rows
 
 
-def summarize_counters(root, out_path):
-    """Per-kernel HBM bytes and MFMA counters of a profiled C3 step.
+def summarize_counters(root, out_path, workload="c3"):
+    """Per-kernel HBM bytes and MFMA counters of a profiled step (C3 or C5).
 
     ``root`` holds the rocprofv3 --pmc output of five runs: step_FETCH_SIZE, step_WRITE_SIZE and
     step_MFMA (the step under ``--pmc FETCH_SIZE``, ``WRITE_SIZE`` and ``MfmaUtil MfmaFlopsF16
@@ -553,20 +558,22 @@ def summarize_counters(root, out_path):
             d["flops"].append(sum(e["c"].get(c, 0.0) for c in
                                   ("MfmaFlopsF16", "MfmaFlopsBF16", "MfmaFlopsF32")))
             d["ns"].append(e["ns"])
-    lines = ["# rocprofv3 counters of the C3 step (uma-s-1 architecture, 2048 atoms, E = 61440), "
-             "MI355X", "# Commands (repository root $REPO on the GPU box; one pass per counter "
-             "group):", "#   cd /tmp && export TMPDIR=/tmp"]
-    step = ("python3 $REPO/bench.py --steps 1 --warmup 1 --no-cpu-baseline --no-secondary --eager")
+    lines = [f"# rocprofv3 counters of the {COUNTER_TITLES[workload]}, MI355X",
+             "# Commands (repository root $REPO on the GPU box; one pass per counter group):",
+             "#   cd /tmp && export TMPDIR=/tmp"]
+    wl_arg = "" if workload == "c3" else f" --workload {workload}"
+    step = (f"python3 $REPO/bench.py{wl_arg} --steps 1 --warmup 1 --no-cpu-baseline --no-secondary "
+            "--eager")
     for c in ("FETCH_SIZE", "WRITE_SIZE"):
-        lines.append(f"#   rocprofv3 --pmc {c} --output-format csv -d $REPO/gpurun_out/pmc/step_{c}"
-                     f" -o s -- {step}")
+        lines.append(f"#   rocprofv3 --pmc {c} --output-format csv -d $REPO/gpurun_out/{root.name}/"
+                     f"step_{c} -o s -- {step}")
     lines.append("#   rocprofv3 --pmc MfmaUtil MfmaFlopsF16 MfmaFlopsF32 --output-format csv -d "
-                 f"$REPO/gpurun_out/pmc/step_MFMA -o s -- {step}")
+                 f"$REPO/gpurun_out/{root.name}/step_MFMA -o s -- {step}")
     for c in ("FETCH_SIZE", "WRITE_SIZE"):
-        lines.append(f"#   rocprofv3 --pmc {c} --output-format csv -d $REPO/gpurun_out/pmc/copy_{c}"
-                     f" -o c -- python3 $REPO/bench.py --calibrate-copy")
-    lines.append("#   python3 $REPO/bench.py --summarize-counters $REPO/gpurun_out/pmc "
-                 "profiles/uma_c3_step_counters.txt")
+        lines.append(f"#   rocprofv3 --pmc {c} --output-format csv -d $REPO/gpurun_out/{root.name}/"
+                     f"copy_{c} -o c -- python3 $REPO/bench.py --calibrate-copy")
+    lines.append(f"#   python3 $REPO/bench.py{wl_arg} --summarize-counters $REPO/gpurun_out/"
+                 f"{root.name} {pathlib.Path(out_path).as_posix()}")
     lines.append(f"# Calibration (256 MiB copy): FETCH_SIZE x {scale['FETCH_SIZE']:.4f}, "
                  f"WRITE_SIZE x {scale['WRITE_SIZE']:.4f}")
     lines.append("# Three steps are profiled (warm-up, timed, probed); figures are means per launch.")
@@ -599,6 +606,34 @@ def summarize_counters(root, out_path):
                          f"{fl / (us * 1e-6) / 1e12:.0f} TFLOP/s issued")
             traffic.append(f"mfma {k} util_pct={util:.2f} issued_flops={fl:.0f} us={us:.2f}")
     pathlib.Path(out_path).write_text("\n".join(lines + traffic) + "\n")
+
+
+def summarize_stats(stats_csv, out_path, workload="c3", steps=5, warmup=2):
+    """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv of the eager step:
+    the top 30 kernels by total time, with the command that produced the CSV."""
+    import csv
+    rows = list(csv.DictReader(open(stats_csv, newline="")))
+    tot = sum(float(r["TotalDurationNs"]) for r in rows)
+    nsteps = warmup + 2 * steps          # warm-up, timed pass, probed pass
+    wl_arg = "" if workload == "c3" else f" --workload {workload}"
+    cmd = (f"rocprofv3 --kernel-trace --stats --output-format csv -d $REPO/gpurun_out/kt_{workload} "
+           f"-o {workload} -- python3 $REPO/bench.py{wl_arg} --steps {steps} --warmup {warmup} "
+           "--no-cpu-baseline --no-secondary --eager")
+    lines = [f"# {COUNTER_TITLES[workload]}: rocprofv3 kernel statistics, MI355X", "",
+             "Command (repository root $REPO on the GPU box):", "", "```",
+             "cd /tmp && export TMPDIR=/tmp", cmd,
+             f"python3 $REPO/bench.py{wl_arg} --summarize-stats $REPO/gpurun_out/kt_{workload}/"
+             f"{workload}_kernel_stats.csv {pathlib.Path(out_path).as_posix()}", "```", "",
+             f"{nsteps} steps profiled (warm-up, timed and the probed pass, all launched kernel by "
+             f"kernel); total kernel time {tot / 1e6:.2f} ms = {tot / 1e6 / nsteps:.2f} ms per step.",
+             "", "| share | calls | avg us | kernel |", "|---:|---:|---:|---|"]
+    for r in rows[:30]:
+        name = r["Name"].replace("(anonymous namespace)::", "")
+        if len(name) > 70:
+            name = name[:70] + "..."
+        lines.append(f"| {float(r['Percentage']):.2f}% | {r['Calls']} | "
+                     f"{float(r['AverageNs']) / 1000:.1f} | `{name}` |")
+    pathlib.Path(out_path).write_text("\n".join(lines) + "\n")
 
 
 def summarize_trace(trace_csv, out_path, pattern):
@@ -651,6 +686,9 @@ def main():
                     help="only run a 256 MiB device copy (y = -x) for the HBM counter scale")
     ap.add_argument("--summarize-counters", nargs=2, metavar=("PMC_ROOT", "OUT"),
                     help="write the per-kernel counter summary of rocprofv3 --pmc runs (no GPU)")
+    ap.add_argument("--summarize-stats", nargs=2, metavar=("STATS_CSV", "OUT"),
+                    help="write the markdown kernel table of a rocprofv3 --stats run of the eager "
+                         "step (--steps 5 --warmup 2) (no GPU)")
     ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_CSV", "OUT", "REGEX"),
                     help="write per-kernel, per-grid median durations of a rocprofv3 kernel "
                          "trace for kernels matching REGEX (no GPU)")
@@ -658,8 +696,11 @@ def main():
     if args.summarize_trace:
         summarize_trace(*args.summarize_trace)
         return
+    if args.summarize_stats:
+        summarize_stats(*args.summarize_stats, workload=args.workload or "c3")
+        return
     if args.summarize_counters:
-        summarize_counters(*args.summarize_counters)
+        summarize_counters(*args.summarize_counters, workload=args.workload or "c3")
         return
     if args.calibrate_copy:
         import torch
@@ -821,8 +862,8 @@ def main():
     dom = max(fam, key=lambda k: fam[k]["ms"])
     d = fam[dom]
     achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12 if d["ms"] > 0 else 0.0
-    counted = wl == "c3" and args.precision == "f32"
-    kernel_traffic, kernel_mfma = read_traffic() if counted else ({}, {})
+    counted = wl in COUNTER_FILES and args.precision == "f32"
+    kernel_traffic, kernel_mfma = read_traffic(COUNTER_FILES[wl]) if counted else ({}, {})
     dom_kernel = {"f16x3": "gemm_bf16x_kernel<2,16>"}.get(dom)
     traffic = kernel_traffic.get(dom_kernel) if dom_kernel else None
     mfma_counters = kernel_mfma.get(dom_kernel) if dom_kernel else None
@@ -889,10 +930,12 @@ def main():
                      "peak_note": ("algorithmic fp32 GEMM flops (2MNK) against the ceiling of "
                                    "the kernel's arithmetic: fp32 MFMA 157.3, or the fp16 / bf16 "
                                    "dense MFMA 2500 / number of plane products"),
-                     "frac_note": ("the default split (f16x3: 3 fp16 products per fp32 product) "
-                                   "is bound by its VALU work (plane split and per-row scaling), "
-                                   "not by the matrix pipe; the fp32-accurate bf16x6 mode reads "
-                                   "a higher frac (0.43-0.44 of its /6 ceiling) at a lower rate "
+                     "frac_note": ("the default split (f16x3: 3 fp16 products per fp32 "
+                                   "product); the peak assumes the 2.4 GHz clock, which the part "
+                                   "does not hold under this load, and each 128 x 128 tile ends "
+                                   "in an epilogue that writes 64 KB (13-35 % of a tile's time "
+                                   "on these shapes); the fp32-accurate bf16x6 mode reads a "
+                                   "higher frac (0.43-0.44 of its /6 ceiling) at a lower rate "
                                    "(178-184 TF/s on this step, --precision f32-bf16x6)"),
                      "gemm_share_of_step": round(gemm_ms / (dt * 1e3), 4),
                      "measured": ("HIP events around each launch, on the launch stream, over a "
@@ -902,7 +945,9 @@ def main():
         "hbm_kernels_note": ("frac = compulsory bytes (every distinct operand byte once) / HIP-event "
                              "time / 8 TB/s; algorithmic_GBps counts gathered node rows once per "
                              "edge; counter_GBps uses rocprofv3 FETCH_SIZE + WRITE_SIZE bytes per "
-                             "launch of the same workload (profiles/uma_c3_step_counters.txt)"),
+                             "launch of the same workload ("
+                             + (COUNTER_FILES[wl].relative_to(ROOT).as_posix() if counted
+                                else "no counter summary for this workload") + ")"),
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = (cpu_baseline_c5(torch) if wl == "c5" else

@@ -119,8 +119,22 @@ __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
     float cutoff, int nb, const float* __restrict__ jd, float gamma, float* __restrict__ g_ev,
     int E) {
   __shared__ float sgd[EPB];
+  // the block's g_coef rows (EPB x 35 floats, contiguous), read coalesced before phase 1 so that
+  // the loads overlap it; phase 2 takes each edge's row from LDS (an odd stride: no bank
+  // conflicts) instead of 35 loads per thread that each touch 64 cache lines
+  __shared__ float sgc[EPB * 35];
   const int64_t eb = (int64_t)blockIdx.x * EPB;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  constexpr int GCL = (EPB * 35 + 255) / 256;  // coalesced g_coef loads per thread
+  float gcr[GCL];
+  const int gclim = (int)min((int64_t)EPB, (int64_t)E - eb) * 35;
+  if (g_coef) {
+#pragma unroll
+    for (int j = 0; j < GCL; ++j) {
+      const int i = min((int)threadIdx.x + 256 * j, gclim - 1);  // every load issued (exact waits)
+      gcr[j] = g_coef[eb * 35 + i];
+    }
+  }
   if (g_gauss) {
     const int sub = lane & 15, grp = lane >> 4;
 #pragma unroll 2
@@ -157,6 +171,13 @@ __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
       if (sub == 0) sgd[loc] = acc;
     }
   }
+  if (g_coef) {
+#pragma unroll
+    for (int j = 0; j < GCL; ++j) {
+      const int i = (int)threadIdx.x + 256 * j;
+      if (i < gclim) sgc[i] = gcr[j];
+    }
+  }
   __syncthreads();
   if ((int)threadIdx.x >= EPB) return;
   const int64_t e = eb + threadIdx.x;
@@ -171,7 +192,7 @@ __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
   if (g_coef) {
     float jl[35], gc[35];
     for (int k = 0; k < 35; ++k) jl[k] = jd[k];
-    for (int k = 0; k < 35; ++k) gc[k] = g_coef[e * 35 + k];
+    for (int k = 0; k < 35; ++k) gc[k] = sgc[threadIdx.x * 35 + k];
     tta_geo::wigner_vjp(v, gamma, jl, gc, out);
   }
   for (int k = 0; k < 3; ++k) g_ev[e * 3 + k] = out[k];

@@ -296,7 +296,9 @@ __global__ __launch_bounds__(256) void k_rms_bwd(const float* __restrict__ g,
 }
 
 // node_in[n] = [nodes[n] | sum_{recv(e)=n} ue[e] a_r[e] | sum_{send(e)=n} ue[e] a_s[e]] with
-// a = sigmoid gate * cutoff (orb_model.py:245-259).  One wavefront per node.
+// a = sigmoid gate * cutoff (orb_model.py:245-259).  One wavefront per node; KQ float4 groups of
+// a row per lane (rows of up to 256 KQ floats) and U = 16 / KQ edge rows in flight per lane.
+template <int KQ>
 __global__ __launch_bounds__(256) void k_segsum(const float* __restrict__ ue,
                                                 const float* __restrict__ sig,
                                                 const float* __restrict__ cut,
@@ -305,40 +307,41 @@ __global__ __launch_bounds__(256) void k_segsum(const float* __restrict__ ue,
                                                 const int* __restrict__ recv_perm,
                                                 const float* __restrict__ nodes,
                                                 float* __restrict__ node_in, int64_t N, int C) {
+  constexpr int U = 16 / KQ;
   const int lane = threadIdx.x & 63;
   const int64_t n = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
   const int nq = C / 4;
-  floatx4 sr[kMaxQ], ssn[kMaxQ];
+  floatx4 sr[KQ], ssn[KQ];
 #pragma unroll
-  for (int k = 0; k < kMaxQ; ++k) sr[k] = ssn[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < KQ; ++k) sr[k] = ssn[k] = floatx4{0.f, 0.f, 0.f, 0.f};
   // Up to 64 edges of a segment at a time: lane i fetches edge i's index and weight (one load
-  // each for the wave), then the rows of kU edges at a time are all in flight before any is added;
+  // each for the wave), then the rows of U edges at a time are all in flight before any is added;
   // the additions keep the plain loop's edge order.
   const int r0 = recv_ptr[n], r1 = recv_ptr[n + 1];
   for (int j0 = r0; j0 < r1; j0 += 64) {
     const int cnt = min(64, r1 - j0);
     const int my_e = lane < cnt ? recv_perm[j0 + lane] : 0;
     const float my_w = lane < cnt ? sig[2 * my_e + 0] * cut[my_e] : 0.f;
-    for (int u0 = 0; u0 < cnt; u0 += kU) {
-      floatx4 v[kU][kMaxQ];
+    for (int u0 = 0; u0 < cnt; u0 += U) {
+      // every row load is issued (past the chunk: its last edge again; past the row: its last
+      // float4), so the compiler's wait counts stay exact; the extra values are not added
+      floatx4 v[U][KQ];
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int e = __shfl(my_e, u0 + u, 64);
+      for (int u = 0; u < U; ++u) {
+        const int e = __shfl(my_e, min(u0 + u, cnt - 1), 64);
 #pragma unroll
-        for (int k = 0; k < kMaxQ; ++k) {
-          const int q = lane + 64 * k;
-          v[u][k] = (u0 + u < cnt && q < nq)
-                        ? reinterpret_cast<const floatx4*>(ue + (int64_t)e * C)[q]
-                        : floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < KQ; ++k) {
+          const int q = min(lane + 64 * k, nq - 1);
+          v[u][k] = reinterpret_cast<const floatx4*>(ue + (int64_t)e * C)[q];
         }
       }
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
+      for (int u = 0; u < U; ++u) {
         const float w = __shfl(my_w, u0 + u, 64);
         if (u0 + u < cnt)
 #pragma unroll
-          for (int k = 0; k < kMaxQ; ++k) sr[k] += v[u][k] * w;
+          for (int k = 0; k < KQ; ++k) sr[k] += v[u][k] * w;
       }
     }
   }
@@ -346,29 +349,28 @@ __global__ __launch_bounds__(256) void k_segsum(const float* __restrict__ ue,
   for (int j0 = s0; j0 < s1; j0 += 64) {
     const int cnt = min(64, s1 - j0);
     const float my_w = lane < cnt ? sig[2 * (j0 + lane) + 1] * cut[j0 + lane] : 0.f;
-    for (int u0 = 0; u0 < cnt; u0 += kU) {
-      floatx4 v[kU][kMaxQ];
+    for (int u0 = 0; u0 < cnt; u0 += U) {
+      floatx4 v[U][KQ];
 #pragma unroll
-      for (int u = 0; u < kU; ++u)
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int k = 0; k < kMaxQ; ++k) {
-          const int q = lane + 64 * k;
-          v[u][k] = (u0 + u < cnt && q < nq)
-                        ? reinterpret_cast<const floatx4*>(ue + (int64_t)(j0 + u0 + u) * C)[q]
-                        : floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < KQ; ++k) {
+          const int q = min(lane + 64 * k, nq - 1);
+          v[u][k] = reinterpret_cast<const floatx4*>(
+              ue + (int64_t)(j0 + min(u0 + u, cnt - 1)) * C)[q];
         }
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
+      for (int u = 0; u < U; ++u) {
         const float w = __shfl(my_w, u0 + u, 64);
         if (u0 + u < cnt)
 #pragma unroll
-          for (int k = 0; k < kMaxQ; ++k) ssn[k] += v[u][k] * w;
+          for (int k = 0; k < KQ; ++k) ssn[k] += v[u][k] * w;
       }
     }
   }
   floatx4* out = reinterpret_cast<floatx4*>(node_in + n * 3 * C);
 #pragma unroll
-  for (int k = 0; k < kMaxQ; ++k) {
+  for (int k = 0; k < KQ; ++k) {
     const int q = lane + 64 * k;
     if (q >= nq) continue;
     out[q] = reinterpret_cast<const floatx4*>(nodes + n * C)[q];
@@ -641,8 +643,18 @@ extern "C" int tta_orb_segsum(const float* ue, const float* sig, const float* cu
   if (N == 0) return tta::kOk;
   TTA_CHECK_ARG(send_ptr && recv_ptr && nodes && node_in && (E == 0 || (ue && sig && cut && recv_perm)),
                 "tta_orb_segsum: null pointer");
-  hipLaunchKernelGGL(k_segsum, dim3(tta_blocks(N, 4)), dim3(256), 0, stream, ue, sig, cut,
-                     send_ptr, recv_ptr, recv_perm, nodes, node_in, N, (int)C);
+  // float4 groups per lane: rows of up to 256, 512, 768 or 1024 floats
+  const int kq = (int)((C / 4 + 63) / 64);
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(tta_blocks(N, 4)), dim3(256), 0, stream, ue, sig, cut,
+                       send_ptr, recv_ptr, recv_perm, nodes, node_in, N, (int)C);
+  };
+  if (kq <= 1)
+    launch(k_segsum<1>);
+  else if (kq == 2)
+    launch(k_segsum<2>);
+  else
+    launch(k_segsum<4>);
   TTA_CHECK_LAUNCH("tta_orb_segsum");
   return tta::kOk;
 }

@@ -359,10 +359,20 @@ __global__ __launch_bounds__(128) void k_gather_rotate_bw_dst(
 // Inverse rotation + envelope + destination-sorted segmented sum (+ residual):
 //   out[n, j, :] = res[n, j, :] + sum_{e in [ptr[n], ptr[n+1])} contrib_e[j, :]
 // ENV_FIRST (edgewise.py:72-86):  contrib = W^T (m[e] * env[e])
-// otherwise (geometry.py:269-276, edge-degree init): contrib = ((W^T pad(m[e])) * env[e]) / div
+// otherwise (geometry.py:269-276, edge-degree init): contrib = (W^T pad(m[e])) * (env[e] / div)
 // Edges of a segment are summed in ascending order starting from zero, then the residual is
-// added: the order index_add_ followed by "+ x_res" uses.  One wave per node; the next edge's
-// rows are loaded before the current edge is accumulated.
+// added: the order index_add_ followed by "+ x_res" uses.  One wave per node walks its edges in
+// order; the loads of edge e + PF are issued before edge e is accumulated, so PF edges' worth of
+// loads are in flight: each edge's message rows, and its 35 coefficients and envelope in one
+// coalesced load (lane k < 35 holds coefficient k, lane 35 the envelope) whose values reach the
+// arithmetic through v_readlane with constant lane indices (scalar loads per edge would put a
+// scalar-memory round trip on every edge of the chain).
+// PF: 4 edges in flight, 2 for wide rows (V NIN > 18 floats per lane per edge) to stay within
+// 256 registers.  Every slot refill issues the same loads unconditionally (the edge index clamped
+// to the segment's last edge, the clamped edge's values then unused), so the compiler's wait
+// counts stay exact: a conditional load would make it wait for all loads at the join.
+constexpr int kSegPF = 4;
+
 template <int V, int NIN, bool ENV_FIRST>
 __global__ __launch_bounds__(256) void k_rotate_env_segsum(
     const float* __restrict__ m, const float* __restrict__ coef, const float* __restrict__ env,
@@ -374,47 +384,78 @@ __global__ __launch_bounds__(256) void k_rotate_env_segsum(
   if (n >= N) return;
   const int e0 = wave_uniform(ptr[n]), e1 = wave_uniform(ptr[n + 1]);
   const int nq = C / V;
-  for (int q = lane; q < nq; q += 64) {
+  const float rdiv = 1.f / div;
+  constexpr int PF = V * NIN > 18 ? 2 : kSegPF;
+  // lane k < 35 loads coefficient k of the edge, the other lanes its envelope (lane 35's copy is
+  // the one read): one load instruction, no branch
+  const int ce_off = lane < NNZ ? lane : 0;
+  auto load_ce = [&](int e) -> float {
+    const float* p = lane < NNZ ? coef + (int64_t)e * NNZ + ce_off : env + e;
+    return *p;
+  };
+  for (int q0 = 0; q0 < nq; q0 += 64) {
+    // every lane runs the loop, also past the channel rows (its row loads then read channel 0
+    // and it stores nothing), so that lanes 0..35 all take part in the coefficient loads
+    const int q = q0 + lane;
+    const bool qv = q < nq;
+    const int qq = qv ? q : 0;
     T acc[NSPH];
 #pragma unroll
     for (int j = 0; j < NSPH; ++j) acc[j] = zv<V>();
-    T nxt[NIN];
     if (e0 < e1) {
+      T rows[PF][NIN];
+      float ce[PF];
+      auto load_slot = [&](int s, int e) {
+        e = min(e, e1 - 1);
+        ce[s] = load_ce(e);
 #pragma unroll
-      for (int mm = 0; mm < NIN; ++mm) nxt[mm] = ldv<V>(m + (int64_t)e0 * NIN * C + mm * C + V * q);
+        for (int mm = 0; mm < NIN; ++mm) rows[s][mm] = ldv<V>(m + (int64_t)e * NIN * C + mm * C + V * qq);
+      };
+#pragma unroll
+      for (int s = 0; s < PF; ++s) load_slot(s, e0 + s);
+      for (int eb = e0; eb < e1; eb += PF) {
+#pragma unroll
+        for (int s = 0; s < PF; ++s) {
+          const int e = eb + s;
+          T in[NSPH];
+#pragma unroll
+          for (int mm = 0; mm < NSPH; ++mm) in[mm] = zv<V>();
+#pragma unroll
+          for (int mm = 0; mm < NIN; ++mm) in[mm] = rows[s][mm];
+          float c[NNZ];
+          const int cev = __float_as_int(ce[s]);
+#pragma unroll
+          for (int k = 0; k < NNZ; ++k) c[k] = __int_as_float(__builtin_amdgcn_readlane(cev, k));
+          const float ev = __int_as_float(__builtin_amdgcn_readlane(cev, NNZ));
+          // refill this slot with edge e + PF before the arithmetic of edge e
+          load_slot(s, e + PF);
+          if (e < e1) {  // wave-uniform
+            if (ENV_FIRST) {
+#pragma unroll
+              for (int mm = 0; mm < NIN; ++mm) in[mm] = in[mm] * ev;
+            }
+            T o[NSPH];
+            rot_inv<NIN>(c, in, o);
+            // edge-degree scaling: one per-edge factor env / div (a division per element made
+            // this variant VALU-bound; the factor rounds once, so values move by an ulp at most)
+            const float sc = ENV_FIRST ? 1.f : ev * rdiv;
+#pragma unroll
+            for (int j = 0; j < NSPH; ++j) {
+              T v = o[j];
+              if (!ENV_FIRST) v = v * sc;
+              acc[j] = acc[j] + v;
+            }
+          }
+        }
+      }
     }
-    for (int e = e0; e < e1; ++e) {
-      T in[NSPH];
-#pragma unroll
-      for (int mm = 0; mm < NSPH; ++mm) in[mm] = zv<V>();
-#pragma unroll
-      for (int mm = 0; mm < NIN; ++mm) in[mm] = nxt[mm];
-      if (e + 1 < e1) {
-#pragma unroll
-        for (int mm = 0; mm < NIN; ++mm)
-          nxt[mm] = ldv<V>(m + (int64_t)(e + 1) * NIN * C + mm * C + V * q);
-      }
-      float c[NNZ];
-      load_coef(coef, e, c);
-      const float ev = env[e];
-      if (ENV_FIRST) {
-#pragma unroll
-        for (int mm = 0; mm < NIN; ++mm) in[mm] = in[mm] * ev;
-      }
-      T o[NSPH];
-      rot_inv<NIN>(c, in, o);
+    if (qv) {
 #pragma unroll
       for (int j = 0; j < NSPH; ++j) {
-        T v = o[j];
-        if (!ENV_FIRST) v = (v * ev) / div;
-        acc[j] = acc[j] + v;
+        T v = acc[j];
+        if (res) v = v + ldv<V>(res + (int64_t)n * NSPH * C + j * C + V * q);
+        stv<V>(out + (int64_t)n * NSPH * C + j * C + V * q, v);
       }
-    }
-#pragma unroll
-    for (int j = 0; j < NSPH; ++j) {
-      T v = acc[j];
-      if (res) v = v + ldv<V>(res + (int64_t)n * NSPH * C + j * C + V * q);
-      stv<V>(out + (int64_t)n * NSPH * C + j * C + V * q, v);
     }
   }
 }
@@ -424,8 +465,8 @@ __global__ __launch_bounds__(256) void k_rotate_env_segsum(
 // ENV_FIRST (forces.py:366-376):
 //   g_back = g_node[tgt]; g_env_in = W g_back; g_m = g_env_in * env;
 //   g_env += <g_env_in, m>;  g_coef(m,j) += <g_back[j], m[m] * env>
-// otherwise (edge-degree, forward v = ((W^T pad(m)) * env) / div):
-//   g_v2 = g_node[tgt] / div; g_v1 = g_v2 * env; g_env += <g_v2, W^T pad(m)>;
+// otherwise (edge-degree, forward v = (W^T pad(m)) * (env / div)):
+//   g_v2 = g_node[tgt] (1 / div); g_v1 = g_v2 * env; g_env += <g_v2, W^T pad(m)>;
 //   g_m = (W g_v1)[:NIN];  g_coef(m,j) += <g_v1[j], pad(m)[m]>
 template <int V, int NIN, bool ENV_FIRST>
 __global__ __launch_bounds__(256) void k_rotate_env_segsum_bw(
@@ -443,6 +484,7 @@ __global__ __launch_bounds__(256) void k_rotate_env_segsum_bw(
   load_coef(coef, e, c);
   const float ev = env[e];
   const int64_t t = wave_uniform(tgt[e]);
+  const float rdiv = 1.f / div;
   float gc[NNZ + 1];  // 35 coefficient partials + the envelope partial
 #pragma unroll
   for (int k = 0; k <= NNZ; ++k) gc[k] = 0.f;
@@ -469,7 +511,7 @@ __global__ __launch_bounds__(256) void k_rotate_env_segsum_bw(
       rot_inv<NIN>(c, mi, v1);
 #pragma unroll
       for (int j = 0; j < NSPH; ++j) {
-        const T g2 = gb[j] / div;
+        const T g2 = gb[j] * rdiv;  // (a division per element made this variant VALU-bound)
         gc[NNZ] += hsum<V>(g2 * v1[j]);
         g1[j] = g2 * ev;
       }

@@ -431,6 +431,32 @@ def set_hbm_probe(probe):
     _hbm_probe = probe
 
 
+def _pick_v(W):
+    """Vector width of the rotation kernels for rows of W channels (pick_v in csrc/rotate.hip)."""
+    return 4 if W >= 256 else 2 if W >= 128 else 1
+
+
+def _tf(b):
+    return "true" if b else "false"
+
+
+def _al16(*ts):
+    return all(t is None or t.data_ptr() % 16 == 0 for t in ts)
+
+
+def _ln_variant(n, vec):
+    """(G, NPL, VEC) of the LayerNorm-SiLU launch for rows of n (tta_ln_silu_fwd/_bwd)."""
+    if n <= 32:
+        return 32, 1, False
+    if n <= 64:
+        return 32, 2, False
+    if n <= 128:
+        return 32, 4, vec
+    if n <= 256:
+        return 64, 4, vec
+    return 64, 8, False
+
+
 def _hbm_call(kernel, nbytes, name, *args, compulsory=None):
     probe = _hbm_probe
     if probe is not None:
@@ -445,7 +471,7 @@ def gather_rotate(x, src, tgt, coef, rad, out):
     E = src.numel()
     edge = 4 * (35 + (12 * C if rad is not None else 0) + 18 * C) + 8
     nbytes = E * (edge + 4 * 18 * C)
-    _hbm_call("k_gather_rotate", nbytes, "tta_gather_rotate", _ptr(x, numel=N * 9 * C, name="x"),
+    _hbm_call(f"k_gather_rotate<{_pick_v(2 * C)},{_tf(rad is not None)},2>", nbytes, "tta_gather_rotate", _ptr(x, numel=N * 9 * C, name="x"),
               _i32(src, E), _i32(tgt, E),
               _ptr(coef, numel=E * 35, name="coef"), _ptr(rad, numel=E * 12 * C, name="rad"),
               _ptr(out, numel=E * 18 * C, name="out"), N, E, C, _stream(),
@@ -456,7 +482,7 @@ def gather_rotate(x, src, tgt, coef, rad, out):
 def gather_rotate_src(x, src, coef, out):
     N, _, C = x.shape
     E = src.numel()
-    _hbm_call("k_gather_rotate_src", E * (4 * (9 * C + 35 + 9 * C) + 4), "tta_gather_rotate_src",
+    _hbm_call(f"k_gather_rotate<{_pick_v(C)},false,1>", E * (4 * (9 * C + 35 + 9 * C) + 4), "tta_gather_rotate_src",
               _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E),
               _ptr(coef, numel=E * 35, name="coef"), _ptr(out, numel=E * 9 * C, name="out"), N, E, C,
               _stream(), compulsory=E * (4 * (35 + 9 * C) + 4) + 4 * N * 9 * C)
@@ -467,7 +493,7 @@ def gather_rotate_src_bw(g_out, x, src, coef, g_in, g_coef):
     N, _, C = x.shape
     E = src.numel()
     edge = 4 * (9 * C + 35 + 70 + (9 * C if g_in is not None else 0)) + 4
-    _hbm_call("k_gather_rotate_src_bw", E * (edge + 4 * 9 * C), "tta_gather_rotate_src_bw",
+    _hbm_call(f"k_gather_rotate_bw<{_pick_v(C)},false,1>", E * (edge + 4 * 9 * C), "tta_gather_rotate_src_bw",
               _ptr(g_out, numel=E * 9 * C, name="g_out"),
               _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E), _ptr(coef, numel=E * 35, name="coef"),
               None if g_in is None else _ptr(g_in, numel=E * 9 * C, name="g_in"),
@@ -480,7 +506,7 @@ def gather_rotate_bw(g_xf, rad, x, src, tgt, coef, g_rad, g_mcat, g_coef):
     E = src.numel()
     edge = 4 * (18 * C + (24 * C if rad is not None else 0) + 35 + 70 + 18 * C) + 8
     nbytes = E * (edge + 4 * 18 * C)
-    _hbm_call("k_gather_rotate_bw", nbytes, "tta_gather_rotate_bw",
+    _hbm_call(f"k_gather_rotate_bw<{_pick_v(2 * C)},{_tf(rad is not None)},2>", nbytes, "tta_gather_rotate_bw",
               _ptr(g_xf, numel=E * 18 * C, name="g_xf"),
               _ptr(rad, numel=E * 12 * C, name="rad"), _ptr(x, numel=N * 9 * C, name="x"),
               _i32(src, E), _i32(tgt, E), _ptr(coef, numel=E * 35, name="coef"),
@@ -496,7 +522,7 @@ def gather_rotate_bw_dst(g_xf, rad, x, src, tgt_ptr, coef, g_rad, g_mcat, g_coef
     N, _, C = x.shape
     E = src.numel()
     edge = 4 * (18 * C + 24 * C + 35 + 70 + 9 * C) + 4
-    _hbm_call("k_gather_rotate_bw_dst", E * (edge + 4 * 9 * C) + 4 * N * 9 * C,
+    _hbm_call(f"k_gather_rotate_bw_dst<{_pick_v(C)}>", E * (edge + 4 * 9 * C) + 4 * N * 9 * C,
               "tta_gather_rotate_bw_dst",
               _ptr(g_xf, numel=E * 18 * C, name="g_xf"), _ptr(rad, numel=E * 12 * C, name="rad"),
               _ptr(x, numel=N * 9 * C, name="x"), _i32(src, E), _i32(tgt_ptr, N + 1, "tgt_ptr"),
@@ -511,7 +537,7 @@ def node_gather_sum_dst(g_mcat, src_ptr, src_perm, tsum, res, out):
     N, _, C = out.shape
     E = src_perm.numel()
     nbytes = 4 * (E * 9 * C + (N + 1) + E + N * 9 * C * (2 + (res is not None)))
-    _hbm_call("k_node_gather_sum", nbytes, "tta_node_gather_sum_dst",
+    _hbm_call(f"k_node_gather_sum<{_pick_v(C)}>", nbytes, "tta_node_gather_sum_dst",
               _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
               _i32(src_ptr, N + 1, "src_ptr"), _i32(src_perm, E, "src_perm"),
               _ptr(tsum, numel=N * 9 * C, name="tsum"), _ptr(res, numel=N * 9 * C, name="res"),
@@ -523,7 +549,7 @@ def rotate_env_segsum(m, coef, env, tgt_ptr, res, out, *, n_in, env_first, div=1
     N, _, C = out.shape
     E = coef.shape[0]
     nbytes = 4 * (E * (n_in * C + 36) + (N + 1) + N * 9 * C * (1 + (res is not None)))
-    _hbm_call("k_rotate_env_segsum", nbytes, "tta_rotate_env_segsum",
+    _hbm_call(f"k_rotate_env_segsum<{_pick_v(C)},{n_in},{_tf(env_first)}>", nbytes, "tta_rotate_env_segsum",
               _ptr(m, numel=E * n_in * C, name="m"),
               _ptr(coef, numel=E * 35, name="coef"), _ptr(env, numel=E, name="env"),
               _i32(tgt_ptr, N + 1, "tgt_ptr"), _ptr(res, numel=N * 9 * C, name="res"),
@@ -537,7 +563,7 @@ def rotate_env_segsum_bw(g_node, tgt, m, coef, env, g_m, g_coef, g_env, *, n_in,
     N, _, C = g_node.shape
     E = tgt.numel()
     nbytes = 4 * E * (9 * C + 1 + 2 * n_in * C + 35 + 1 + 70 + 2)
-    _hbm_call("k_rotate_env_segsum_bw", nbytes, "tta_rotate_env_segsum_bw",
+    _hbm_call(f"k_rotate_env_segsum_bw<{_pick_v(C)},{n_in},{_tf(env_first)}>", nbytes, "tta_rotate_env_segsum_bw",
               _ptr(g_node, numel=N * 9 * C, name="g_node"), _i32(tgt, E),
               _ptr(m, numel=E * n_in * C, name="m"), _ptr(coef, numel=E * 35, name="coef"),
               _ptr(env, numel=E, name="env"), _ptr(g_m, numel=E * n_in * C, name="g_m"),
@@ -550,7 +576,7 @@ def node_gather_sum(g_mcat, src_ptr, src_perm, tgt_ptr, res, out):
     N, _, C = out.shape
     E = src_perm.numel()
     nbytes = 4 * (E * 18 * C + 2 * (N + 1) + E + N * 9 * C * (1 + (res is not None)))
-    _hbm_call("k_node_gather_sum", nbytes, "tta_node_gather_sum",
+    _hbm_call(f"k_node_gather_sum<{_pick_v(C)}>", nbytes, "tta_node_gather_sum",
               _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
               _i32(src_ptr, N + 1, "src_ptr"), _i32(src_perm, E, "src_perm"),
               _i32(tgt_ptr, N + 1, "tgt_ptr"), _ptr(res, numel=N * 9 * C, name="res"),
@@ -588,7 +614,10 @@ def ln_silu_fwd(a, gamma, beta, nrm, s, *, R, n, groups=1, lda=None, lds=None, e
     w = groups * n
     lda = w if lda is None else lda
     lds = w if lds is None else lds
-    _hbm_call("k_ln_silu_fwd", 4 * ((2 + (nrm is not None)) * R * w + 2 * w), "tta_ln_silu_fwd",
+    G, NPL, VEC = _ln_variant(n, n in (128, 256) and lda % 4 == 0 and lds % 4 == 0
+                              and _al16(a, gamma, beta, nrm, s))
+    _hbm_call(f"k_ln_silu_fwd<{G},{NPL},{_tf(VEC)}>", 4 * ((2 + (nrm is not None)) * R * w + 2 * w),
+              "tta_ln_silu_fwd",
               _rows(a, R, lda, w, "a"), _ptr(gamma, numel=w), _ptr(beta, numel=w),
               None if nrm is None else _rows(nrm, R, lda, w, "nrm"), _rows(s, R, lds, w, "s"),
               R, n, groups, lda, lds, eps, _stream())
@@ -605,7 +634,9 @@ def ln_silu_bwd(g, a, nrm, gamma, g_a, *, R, n, groups=1, ldg=None, lda=None, ld
     if nrm is None and beta is None:
         raise RuntimeError("ln_silu_bwd: nrm, or beta to recompute it, is required")
     nbytes = 4 * (4 * R * w + w) if nrm is not None else 4 * (3 * R * w + 2 * w)
-    _hbm_call("k_ln_silu_bwd", nbytes, "tta_ln_silu_bwd",
+    G, NPL, VEC = _ln_variant(n, n in (128, 256) and ldg % 4 == 0 and lda % 4 == 0
+                              and ldo % 4 == 0 and _al16(g, a, nrm, gamma, beta, g_a))
+    _hbm_call(f"k_ln_silu_bwd<{G},{NPL},{_tf(nrm is None)},{_tf(VEC)}>", nbytes, "tta_ln_silu_bwd",
               _rows(g, R, ldg, w, "g"), _rows(a, R, lda, w, "a"),
               None if nrm is None else _rows(nrm, R, lda, w, "nrm"), _ptr(gamma, numel=w),
               None if beta is None else _ptr(beta, numel=w), _rows(g_a, R, ldo, w, "g_a"), R, n,
@@ -654,17 +685,27 @@ def fill(out, value):
 def edge_wigner(pos, src, tgt, shift, jd, gamma, ev, dist, coef):
     N = pos.shape[0]
     E = src.numel()
-    _call("tta_edge_wigner", _ptr(pos, numel=N * 3, name="pos"), _i32(src, E), _i32(tgt, E),
-          _ptr(shift, numel=E * 3, name="shift"), _ptr(jd, numel=35, name="jd"), float(gamma),
-          _ptr(ev, numel=E * 3), _ptr(dist, numel=E), _ptr(coef, numel=E * 35), N, E, _stream())
+    sh = 12 if shift is not None else 0
+    # per edge: src / tgt, two gathered positions, the shift; out ev, dist, 35 coefficients
+    _hbm_call("k_edge_wigner", E * (8 + 24 + sh + 12 + 4 + 140) + 140, "tta_edge_wigner",
+              _ptr(pos, numel=N * 3, name="pos"), _i32(src, E), _i32(tgt, E),
+              _ptr(shift, numel=E * 3, name="shift"), _ptr(jd, numel=35, name="jd"), float(gamma),
+              _ptr(ev, numel=E * 3), _ptr(dist, numel=E), _ptr(coef, numel=E * 35), N, E,
+              _stream(), compulsory=E * (8 + sh + 12 + 4 + 140) + 12 * N + 140)
 
 
 def edge_features(dist, zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, nb, ec, x_edge, env):
     E = dist.numel()
-    _call("tta_edge_features", _ptr(dist, numel=E), _i32(zsrc, E), _i32(ztgt, E),
-          _ptr(src_emb, name="src_emb"), _ptr(tgt_emb, name="tgt_emb"),
-          _ptr(offsets, numel=nb, name="offsets"), float(coeff), float(cutoff), nb, ec,
-          _ptr(x_edge, numel=E * (nb + 2 * ec), name="x_edge"), _ptr(env, numel=E), E, _stream())
+    v4 = nb % 4 == 0 and ec % 4 == 0 and _al16(x_edge, offsets, src_emb, tgt_emb)
+    # per edge: dist, two species, two gathered embedding rows; out x_edge row and envelope
+    _hbm_call("k_edge_features_v4" if v4 else "k_edge_features",
+              E * (4 + 8 + 8 * ec + 4 * (nb + 2 * ec) + 4) + 4 * nb, "tta_edge_features",
+              _ptr(dist, numel=E), _i32(zsrc, E), _i32(ztgt, E),
+              _ptr(src_emb, name="src_emb"), _ptr(tgt_emb, name="tgt_emb"),
+              _ptr(offsets, numel=nb, name="offsets"), float(coeff), float(cutoff), nb, ec,
+              _ptr(x_edge, numel=E * (nb + 2 * ec), name="x_edge"), _ptr(env, numel=E), E,
+              _stream(), compulsory=E * (4 + 8 + 4 * (nb + 2 * ec) + 4) + 4 * nb
+              + 4 * sum(t.numel() for t in (src_emb, tgt_emb) if t is not None))
 
 
 def edge_geometry_bwd(ev, dist, g_coef, g_env, g_gauss, ldg, offsets, coeff, cutoff, nb, jd,
@@ -672,12 +713,17 @@ def edge_geometry_bwd(ev, dist, g_coef, g_env, g_gauss, ldg, offsets, coeff, cut
     E = dist.numel()
     if g_gauss is not None and (ldg < nb or offsets is None or offsets.numel() < nb):
         raise RuntimeError("edge_geometry_bwd: g_gauss needs ldg >= nb and nb offsets")
-    _call("tta_edge_geometry_bwd", _ptr(ev, numel=E * 3), _ptr(dist, numel=E),
-          _ptr(g_coef, numel=E * 35, name="g_coef"), _ptr(g_env, numel=E, name="g_env"),
-          None if g_gauss is None else _rows(g_gauss, E, ldg, nb, "g_gauss"), ldg,
-          _ptr(offsets, name="offsets"),
-          float(coeff), float(cutoff), nb, _ptr(jd, numel=35), float(gamma),
-          _ptr(g_ev, numel=E * 3), E, _stream())
+    v4 = (g_gauss is not None and nb % 4 == 0 and ldg % 4 == 0 and _al16(g_gauss, offsets))
+    kern = f"k_edge_geometry_bwd<{256 if E >= 256 * 512 else 64},{_tf(v4)}>"
+    # per edge: ev, dist, g_coef, g_env, the Gaussian-adjoint row; out g_ev
+    per = 12 + 4 + (140 if g_coef is not None else 0) + (4 if g_env is not None else 0) + \
+        (4 * nb if g_gauss is not None else 0) + 12
+    _hbm_call(kern, E * per + 4 * nb + 140, "tta_edge_geometry_bwd", _ptr(ev, numel=E * 3),
+              _ptr(dist, numel=E), _ptr(g_coef, numel=E * 35, name="g_coef"),
+              _ptr(g_env, numel=E, name="g_env"),
+              None if g_gauss is None else _rows(g_gauss, E, ldg, nb, "g_gauss"), ldg,
+              _ptr(offsets, name="offsets"), float(coeff), float(cutoff), nb,
+              _ptr(jd, numel=35), float(gamma), _ptr(g_ev, numel=E * 3), E, _stream())
 
 
 def node_forces(g_ev, src_ptr, src_perm, tgt_ptr, forces):

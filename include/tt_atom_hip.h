@@ -231,6 +231,16 @@ int tta_edge_features(const float* dist, const int* zsrc, const int* ztgt, const
                       const float* tgt_emb, const float* offsets, float coeff, float cutoff,
                       int64_t nb, int64_t ec, float* x_edge, float* env, int64_t E,
                       tta_stream_t stream);
+/* tta_edge_wigner and tta_edge_features in one launch (the forward geometry of
+ * geometry.py:226-251 as the step uses it: ev, dist, coef, x_edge, env from pos); same arguments
+ * and results.  Rows that are not four-column aligned (nb or ec not multiples of 4, x_edge,
+ * offsets or embedding tables not 16-byte aligned) run the two kernels instead. */
+int tta_edge_geometry_fwd(const float* pos, const int* src, const int* tgt, const float* shift,
+                          const float* jd, float gamma, const int* zsrc, const int* ztgt,
+                          const float* src_emb, const float* tgt_emb, const float* offsets,
+                          float coeff, float cutoff, int64_t nb, int64_t ec, float* ev,
+                          float* dist, float* coef, float* x_edge, float* env, int64_t N,
+                          int64_t E, tta_stream_t stream);
 /* g_ev from the coefficient, envelope and gaussian adjoints: the closed form of the host
  * torch.autograd.grad finish of forces.py:580-586 (regularised acos/atan2 of geometry.py:87-109). */
 int tta_edge_geometry_bwd(const float* ev, const float* dist, const float* g_coef,

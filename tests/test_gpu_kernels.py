@@ -347,6 +347,41 @@ def test_edge_features_matches_oracle(nat, nb, ec):
     assert (env.cpu() - ref_env).abs().max() < 1e-5
 
 
+@pytest.mark.parametrize("E,nb,ec,periodic", [(1000, 32, 8, False), (130, 512, 128, True),
+                                              (64, 16, 0, False), (77, 30, 6, True)])
+def test_edge_geometry_fwd_equals_two_passes(nat, E, nb, ec, periodic):
+    """The one-launch forward geometry equals tta_edge_wigner + tta_edge_features bit for bit:
+    blocks of 64 edges with a partial last block (1000, 130, 77), the C3 row width (512 + 2 x 128),
+    no species embedding (ec = 0), and rows that take the two-kernel route (30, 6)."""
+    g = torch.Generator().manual_seed(11)
+    N = 50
+    pos = (torch.rand(N, 3, generator=g) * 8.0).to(DEV)
+    src, tgt = torch.randint(0, N, (E,), generator=g), torch.randint(0, N, (E,), generator=g)
+    tgt = torch.where(tgt == src, (tgt + 1) % N, tgt)
+    shift = (torch.randint(-1, 2, (E, 3), generator=g).float() * 8.0).to(DEV) if periodic else None
+    zs, zt = torch.randint(0, 10, (E,), generator=g), torch.randint(0, 10, (E,), generator=g)
+    semb = torch.randn(10, ec, generator=g).to(DEV) if ec else None
+    temb = torch.randn(10, ec, generator=g).to(DEV) if ec else None
+    off = torch.linspace(0, 6.0, nb).to(DEV)
+    coeff = -0.5 / float(2 * (off[1] - off[0])) ** 2
+    jdf = torch.cat([j.reshape(-1) for j in _jd()]).to(DEV)
+
+    def outs():
+        return (torch.full((E, 3), 7.0, device=DEV), torch.full((E,), 7.0, device=DEV),
+                torch.full((E, 35), 7.0, device=DEV), torch.full((E, nb + 2 * ec), 7.0, device=DEV),
+                torch.full((E,), 7.0, device=DEV))
+
+    a, b = outs(), outs()
+    args = (_i32(src), _i32(tgt), shift, jdf, 0.3)
+    nat.edge_wigner(pos, *args, a[0], a[1], a[2])
+    nat.edge_features(a[1], _i32(zs), _i32(zt), semb, temb, off, coeff, 6.0, nb, ec, a[3], a[4])
+    nat.edge_geometry_fwd(pos, *args, _i32(zs), _i32(zt), semb, temb, off, coeff, 6.0, nb, ec,
+                          *b)
+    torch.cuda.synchronize()
+    for name, x, y in zip(("ev", "dist", "coef", "x_edge", "env"), a, b):
+        assert torch.equal(x, y), name
+
+
 def test_geometry_vjp_matches_autograd(nat):
     jd = _jd()
     ev = _test_vectors(400, 1)

@@ -12,6 +12,9 @@
 namespace {
 
 // One thread per edge: ev = pos[src] - pos[tgt] (+ shift), dist = |ev|, coef = packed W(ev).
+// The block's 256 coefficient rows (35 floats each) and edge vectors are staged in LDS and then
+// stored with consecutive lanes on consecutive floats: a thread storing its own row would make
+// each store instruction touch 64 cache lines.
 __global__ __launch_bounds__(256) void k_edge_wigner(const float* __restrict__ pos,
                                                      const int* __restrict__ src,
                                                      const int* __restrict__ tgt,
@@ -20,21 +23,30 @@ __global__ __launch_bounds__(256) void k_edge_wigner(const float* __restrict__ p
                                                      float* __restrict__ ev_out,
                                                      float* __restrict__ dist_out,
                                                      float* __restrict__ coef_out, int E) {
-  const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= E) return;
-  const int s = src[e], t = tgt[e];
-  float ev[3];
-  for (int k = 0; k < 3; ++k) {
-    ev[k] = pos[s * 3 + k] - pos[t * 3 + k];
-    if (shift) ev[k] = ev[k] + shift[(int64_t)e * 3 + k];
-    ev_out[(int64_t)e * 3 + k] = ev[k];
+  __shared__ float sc[256 * 35];  // odd row stride: conflict-free per-thread rows
+  __shared__ float sv[256 * 3];
+  const int64_t eb = (int64_t)blockIdx.x * 256;
+  const int nv = (int)min((int64_t)256, (int64_t)E - eb);
+  const int t = threadIdx.x;
+  if (t < nv) {
+    const int64_t e = eb + t;
+    const int s = src[e], g = tgt[e];
+    float ev[3];
+    for (int k = 0; k < 3; ++k) {
+      ev[k] = pos[s * 3 + k] - pos[g * 3 + k];
+      if (shift) ev[k] = ev[k] + shift[e * 3 + k];
+      sv[t * 3 + k] = ev[k];
+    }
+    dist_out[e] = sqrtf(ev[0] * ev[0] + ev[1] * ev[1] + ev[2] * ev[2]);
+    float jl[35];
+    for (int k = 0; k < 35; ++k) jl[k] = jd[k];
+    float c[35];
+    tta_geo::wigner_coef(ev, gamma, jl, c);
+    for (int k = 0; k < 35; ++k) sc[t * 35 + k] = c[k];
   }
-  dist_out[e] = sqrtf(ev[0] * ev[0] + ev[1] * ev[1] + ev[2] * ev[2]);
-  float jl[35];
-  for (int k = 0; k < 35; ++k) jl[k] = jd[k];
-  float c[35];
-  tta_geo::wigner_coef(ev, gamma, jl, c);
-  for (int k = 0; k < 35; ++k) coef_out[(int64_t)e * 35 + k] = c[k];
+  __syncthreads();
+  for (int i = t; i < nv * 35; i += 256) coef_out[eb * 35 + i] = sc[i];
+  for (int i = t; i < nv * 3; i += 256) ev_out[eb * 3 + i] = sv[i];
 }
 
 // x_edge[e] = [exp(coeff (d - off_k)^2) (nb) | src_emb[z_src] (ec) | tgt_emb[z_tgt] (ec)], env[e].
@@ -97,19 +109,137 @@ __global__ __launch_bounds__(256) void k_edge_features_v4(
   if (lane == 0) env[e] = tta_geo::envelope(d, cutoff);
 }
 
-// g_ev[e] = VJP of (coef, gaussians, envelope, |ev|) at the given adjoints.  Four lanes per
-// edge: the gaussian sum (nb terms, the edge's adjoint row read by consecutive lanes) is split
-// over the four and reduced across them in a fixed order; each of the four then evaluates the
-// Wigner part of the VJP in full (identical work, so no divergence) and the first lane stores.
-// Compared with one thread per edge this spreads the nb-long sum of small graphs over four
-// times the threads and makes its row reads contiguous.
-// Edge-geometry VJP, EPB edges per 256-thread block in two phases.  Phase 1, the Gaussian-basis
-// adjoint sum_k g[e, k] d/dd exp(coeff (d - off_k)^2): 16 lanes per edge, each lane a float4 of
-// k per pass (V4: nb and the row stride multiples of 4, 16-byte aligned rows; else scalar), so a
-// load instruction covers four edges with 256 contiguous bytes each; the 16 partial sums reduce
-// by shuffles in a fixed order into LDS.  Phase 2: one thread per edge adds the envelope term and
-// the Wigner-D VJP (geometry_math.h) and writes g_ev.
+// The two forward kernels above in one pass, 64 edges per 256-thread block.  Wave 0 forms the
+// block's edge vectors and distances (one lane per edge, into LDS with the edges' species), then
+// the Wigner coefficients, while waves 1-3 write the block's feature rows with the arithmetic of
+// k_edge_features_v4.  The rows of 64 consecutive edges are one contiguous range, taken as a flat
+// sequence of float4 columns over the 192 threads, so the stores are contiguous across the waves
+// and every thread has independent columns in flight.  The serial Wigner evaluation overlaps the
+// row stores instead of running as a launch of its own with one wavefront per SIMD.  Coefficient
+// rows and edge vectors leave through LDS with consecutive lanes on consecutive floats.
+// Requires the v4 conditions of k_edge_features_v4 and (nb + 2 ec) / 4 < 2^12.
+__global__ __launch_bounds__(256) void k_edge_geometry_fwd(
+    const float* __restrict__ pos, const int* __restrict__ src, const int* __restrict__ tgt,
+    const float* __restrict__ shift, const float* __restrict__ jd, float gamma,
+    const int* __restrict__ zs, const int* __restrict__ zt, const float* __restrict__ semb,
+    const float* __restrict__ temb, const float* __restrict__ off, float coeff, float cutoff,
+    int nb, int ec, float* __restrict__ ev_out, float* __restrict__ dist_out,
+    float* __restrict__ coef_out, float* __restrict__ x_edge, float* __restrict__ env, int E) {
+  __shared__ float sc[64 * 35];
+  __shared__ float sv[64 * 3];
+  __shared__ float sd[64];
+  __shared__ int sz[2][64];
+  const int64_t eb = (int64_t)blockIdx.x * 64;
+  const int nv = (int)min((int64_t)64, (int64_t)E - eb);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  float ev[3] = {0.f, 0.f, 0.f};
+  if (w == 0 && lane < nv) {
+    const int64_t e = eb + lane;
+    const int s = src[e], g = tgt[e];
+    for (int k = 0; k < 3; ++k) {
+      ev[k] = pos[s * 3 + k] - pos[g * 3 + k];
+      if (shift) ev[k] = ev[k] + shift[e * 3 + k];
+      sv[lane * 3 + k] = ev[k];
+    }
+    const float d = sqrtf(ev[0] * ev[0] + ev[1] * ev[1] + ev[2] * ev[2]);
+    sd[lane] = d;
+    sz[0][lane] = ec ? zs[e] : 0;
+    sz[1][lane] = ec ? zt[e] : 0;
+    dist_out[e] = d;
+    env[e] = tta_geo::envelope(d, cutoff);
+  }
+  __syncthreads();
+  if (w == 0) {
+    if (lane < nv) {
+      float jl[35];
+      for (int k = 0; k < 35; ++k) jl[k] = jd[k];
+      float c[35];
+      tta_geo::wigner_coef(ev, gamma, jl, c);
+      for (int k = 0; k < 35; ++k) sc[lane * 35 + k] = c[k];
+    }
+  } else {
+    const int w4 = (nb + 2 * ec) / 4, nb4 = nb / 4, ec4 = ec / 4;
+    const float rw4 = 1.f / (float)w4;
+    floatx4e* rows = reinterpret_cast<floatx4e*>(x_edge + eb * (int64_t)(nb + 2 * ec));
+    const int total = nv * w4;
+#pragma unroll 4
+    for (int idx = (int)threadIdx.x - 64; idx < total; idx += 192) {
+      // idx / w4 from the float reciprocal (idx < 2^18), corrected to the exact quotient
+      int i = (int)((float)idx * rw4);
+      i += (i + 1) * w4 <= idx ? 1 : 0;
+      i -= i * w4 > idx ? 1 : 0;
+      const int q = idx - i * w4;
+      floatx4e v;
+      if (q < nb4) {
+        const float d = sd[i];
+        const floatx4e o = reinterpret_cast<const floatx4e*>(off)[q];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float u = d - o[j];
+          v[j] = expf(coeff * (u * u));
+        }
+      } else if (q < nb4 + ec4) {
+        v = reinterpret_cast<const floatx4e*>(semb + (int64_t)sz[0][i] * ec)[q - nb4];
+      } else {
+        v = reinterpret_cast<const floatx4e*>(temb + (int64_t)sz[1][i] * ec)[q - nb4 - ec4];
+      }
+      rows[idx] = v;
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < nv * 35; i += 256) coef_out[eb * 35 + i] = sc[i];
+  for (int i = threadIdx.x; i < nv * 3; i += 256) ev_out[eb * 3 + i] = sv[i];
+}
+
+// Edge-geometry VJP: g_ev[e] from the adjoints of (coef, gaussians, envelope, |ev|), EPB edges
+// per 256-thread block.  The Gaussian-basis adjoint sum_k g[e, k] d/dd exp(coeff (d - off_k)^2)
+// runs 16 lanes per edge, each lane a float4 of k per pass (V4: nb and the row stride multiples
+// of 4, 16-byte aligned rows; else scalar), so a load instruction covers four edges with 256
+// contiguous bytes each; the 16 partial sums reduce by shuffles in a fixed order into LDS.  The
+// Wigner-D VJP (geometry_math.h) then runs one thread per edge after the block's barrier and
+// reads the edge's coefficient adjoints from LDS, where the block's rows (EPB x 35 contiguous
+// floats) arrive by coalesced loads issued before the sums, instead of 35 loads per thread that
+// each touch 64 cache lines.  EPB = 256 for graphs large enough to fill the GPU at one thread per
+// edge, 64 (the sums over all four waves, the VJP on one) for smaller ones.  Giving the VJP to
+// one wave while the other three form the sums measured slower (46 vs 40 us at E = 61,440): the
+// sums, not the VJP, bound the kernel.
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// This 16-lane group's share of the Gaussian-adjoint sum of edge e, reduced over the group.
+template <bool V4>
+__device__ __forceinline__ float gauss_adjoint(const float* __restrict__ dist,
+                                               const float* __restrict__ g_gauss, int64_t ldg,
+                                               const float* __restrict__ off, float coeff, int nb,
+                                               int64_t e, bool valid, int sub) {
+  float acc = 0.f;
+  if (valid) {
+    const float d = dist[e];
+    const float* gg = g_gauss + e * ldg;
+    if (V4) {
+      // unrolled so that several rows' loads are in flight before the exponentials
+#pragma unroll 8
+      for (int k = 4 * sub; k < nb; k += 64) {
+        const floatx4 gv = *reinterpret_cast<const floatx4*>(gg + k);
+        const floatx4 ov = *reinterpret_cast<const floatx4*>(off + k);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float t = d - ov[q];
+          acc += gv[q] * (expf(coeff * (t * t)) * (coeff * (2.f * t)));
+        }
+      }
+    } else {
+      for (int k = sub; k < nb; k += 16) {
+        const float t = d - off[k];
+        acc += gg[k] * (expf(coeff * (t * t)) * (coeff * (2.f * t)));
+      }
+    }
+  }
+  acc += __shfl_xor(acc, 8, 64);
+  acc += __shfl_xor(acc, 4, 64);
+  acc += __shfl_xor(acc, 2, 64);
+  acc += __shfl_xor(acc, 1, 64);
+  return acc;
+}
 
 template <int EPB, bool V4>
 __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
@@ -118,57 +248,27 @@ __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
     const float* __restrict__ g_gauss, int64_t ldg, const float* __restrict__ off, float coeff,
     float cutoff, int nb, const float* __restrict__ jd, float gamma, float* __restrict__ g_ev,
     int E) {
+  static_assert(EPB == 64 || EPB == 256, "64 or 256 edges per block");
   __shared__ float sgd[EPB];
-  // the block's g_coef rows (EPB x 35 floats, contiguous), read coalesced before phase 1 so that
-  // the loads overlap it; phase 2 takes each edge's row from LDS (an odd stride: no bank
-  // conflicts) instead of 35 loads per thread that each touch 64 cache lines
-  __shared__ float sgc[EPB * 35];
+  __shared__ float sgc[EPB * 35];  // odd row stride: conflict-free per-thread rows
   const int64_t eb = (int64_t)blockIdx.x * EPB;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, sub = lane & 15, grp = lane >> 4;
+  const int nv = (int)min((int64_t)EPB, (int64_t)E - eb);
+  const int gclim = nv * 35;
   constexpr int GCL = (EPB * 35 + 255) / 256;  // coalesced g_coef loads per thread
   float gcr[GCL];
-  const int gclim = (int)min((int64_t)EPB, (int64_t)E - eb) * 35;
   if (g_coef) {
 #pragma unroll
-    for (int j = 0; j < GCL; ++j) {
-      const int i = min((int)threadIdx.x + 256 * j, gclim - 1);  // every load issued (exact waits)
-      gcr[j] = g_coef[eb * 35 + i];
-    }
+    for (int j = 0; j < GCL; ++j)  // every load issued (exact waits), clamped to the block's rows
+      gcr[j] = g_coef[eb * 35 + min((int)threadIdx.x + 256 * j, gclim - 1)];
   }
   if (g_gauss) {
-    const int sub = lane & 15, grp = lane >> 4;
 #pragma unroll 2
     for (int s = 0; s < EPB / 16; ++s) {
       const int loc = w * (EPB / 4) + s * 4 + grp;  // this 16-lane group's edge in the block
-      const int64_t e = eb + loc;
-      float acc = 0.f;
-      if (e < E) {
-        const float d = dist[e];
-        const float* gg = g_gauss + e * ldg;
-        if (V4) {
-          // unrolled so that several rows' loads are in flight before the exponentials
-#pragma unroll 8
-          for (int k = 4 * sub; k < nb; k += 64) {
-            const floatx4 gv = *reinterpret_cast<const floatx4*>(gg + k);
-            const floatx4 ov = *reinterpret_cast<const floatx4*>(off + k);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float t = d - ov[q];
-              acc += gv[q] * (expf(coeff * (t * t)) * (coeff * (2.f * t)));
-            }
-          }
-        } else {
-          for (int k = sub; k < nb; k += 16) {
-            const float t = d - off[k];
-            acc += gg[k] * (expf(coeff * (t * t)) * (coeff * (2.f * t)));
-          }
-        }
-      }
-      acc += __shfl_xor(acc, 8, 64);
-      acc += __shfl_xor(acc, 4, 64);
-      acc += __shfl_xor(acc, 2, 64);
-      acc += __shfl_xor(acc, 1, 64);
-      if (sub == 0) sgd[loc] = acc;
+      const float acc =
+          gauss_adjoint<V4>(dist, g_gauss, ldg, off, coeff, nb, eb + loc, loc < nv, sub);
+      if (sub == 0 && loc < nv) sgd[loc] = acc;
     }
   }
   if (g_coef) {
@@ -179,22 +279,22 @@ __global__ __launch_bounds__(256) void k_edge_geometry_bwd(
     }
   }
   __syncthreads();
-  if ((int)threadIdx.x >= EPB) return;
-  const int64_t e = eb + threadIdx.x;
-  if (e >= E) return;
-  float v[3] = {ev[e * 3], ev[e * 3 + 1], ev[e * 3 + 2]};
-  const float d = dist[e];
-  float gd = g_gauss ? sgd[threadIdx.x] : 0.f;
-  if (g_env) gd += g_env[e] * tta_geo::envelope_grad(d, cutoff);
+  const int t = threadIdx.x;
+  if (t >= nv) return;
+  const int64_t e = eb + t;
+  const float v[3] = {ev[e * 3], ev[e * 3 + 1], ev[e * 3 + 2]};
   float out[3] = {0.f, 0.f, 0.f};
-  if (d > 0.f)
-    for (int k = 0; k < 3; ++k) out[k] = gd * (v[k] / d);
   if (g_coef) {
     float jl[35], gc[35];
     for (int k = 0; k < 35; ++k) jl[k] = jd[k];
-    for (int k = 0; k < 35; ++k) gc[k] = sgc[threadIdx.x * 35 + k];
+    for (int k = 0; k < 35; ++k) gc[k] = sgc[t * 35 + k];
     tta_geo::wigner_vjp(v, gamma, jl, gc, out);
   }
+  const float d = dist[e];
+  float gd = g_gauss ? sgd[t] : 0.f;
+  if (g_env) gd += g_env[e] * tta_geo::envelope_grad(d, cutoff);
+  if (d > 0.f)
+    for (int k = 0; k < 3; ++k) out[k] += gd * (v[k] / d);
   for (int k = 0; k < 3; ++k) g_ev[e * 3 + k] = out[k];
 }
 
@@ -346,6 +446,35 @@ extern "C" int tta_edge_features(const float* dist, const int* zsrc, const int* 
                        dist, zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, (int)nb,
                        (int)ec, x_edge, env, (int)E);
   TTA_CHECK_LAUNCH("tta_edge_features");
+  return tta::kOk;
+}
+
+extern "C" int tta_edge_geometry_fwd(const float* pos, const int* src, const int* tgt,
+                                     const float* shift, const float* jd, float gamma,
+                                     const int* zsrc, const int* ztgt, const float* src_emb,
+                                     const float* tgt_emb, const float* offsets, float coeff,
+                                     float cutoff, int64_t nb, int64_t ec, float* ev, float* dist,
+                                     float* coef, float* x_edge, float* env, int64_t N,
+                                     int64_t E, hipStream_t stream) {
+  TTA_CHECK_ARG(E >= 0 && E < (1ll << 31) && N >= 0 && nb > 0 && ec >= 0,
+                "tta_edge_geometry_fwd: bad sizes");
+  if (E == 0) return tta::kOk;
+  TTA_CHECK_ARG(pos && src && tgt && jd && ev && dist && coef && offsets && x_edge && env &&
+                    (ec == 0 || (zsrc && ztgt && src_emb && tgt_emb)),
+                "tta_edge_geometry_fwd: null pointer");
+  auto al = [](const void* q) { return q == nullptr || ((uintptr_t)q & 15) == 0; };
+  if (!(nb % 4 == 0 && ec % 4 == 0 && nb + 2 * ec < (1 << 14) && al(x_edge) && al(offsets) &&
+        al(src_emb) && al(tgt_emb))) {
+    // rows that the four-column kernel cannot take: the two passes, same arithmetic
+    const int st = tta_edge_wigner(pos, src, tgt, shift, jd, gamma, ev, dist, coef, N, E, stream);
+    if (st != tta::kOk) return st;
+    return tta_edge_features(dist, zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, nb, ec,
+                             x_edge, env, E, stream);
+  }
+  hipLaunchKernelGGL(k_edge_geometry_fwd, dim3(tta_blocks(E, 64)), dim3(256), 0, stream, pos, src,
+                     tgt, shift, jd, gamma, zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff,
+                     (int)nb, (int)ec, ev, dist, coef, x_edge, env, (int)E);
+  TTA_CHECK_LAUNCH("tta_edge_geometry_fwd");
   return tta::kOk;
 }
 

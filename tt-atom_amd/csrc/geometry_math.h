@@ -28,52 +28,77 @@ TTA_HD int row_koff_l2(int r) {
   return r == 0 ? 30 : (r == 1 ? 20 : (r == 2 ? 4 : (r == 3 ? 12 : 25)));
 }
 
-// Dense z-rotation block of degree l (size n = 2l+1): Z[i][i] = cos(f_i t), Z[i][n-1-i] =
-// sin(f_i t), f_i = l - i (geometry.py:124-136; the centre is cos(0) + sin(0) = 1).
+// The z-rotation block of degree L (size n = 2L+1, geometry.py:124-136) is sparse: row i holds
+// cos(f t) at column i and sin(f t) at column n-1-i, f = L - i, and the centre row is exactly 1
+// (cos 0 + sin 0).  Its entries are the cosines and sines of t and 2t only, so one ZTrig per
+// angle serves both degrees, and products with a Z block touch two terms per entry instead of n.
+struct ZTrig {
+  float c[3], s[3];  // cos(k t), sin(k t), k = 0, 1, 2
+};
+
+TTA_HD ZTrig ztrig(float t) {
+  ZTrig z;
+  z.c[0] = 1.f;
+  z.s[0] = 0.f;
+  z.c[1] = cosf(t);
+  z.s[1] = sinf(t);
+  z.c[2] = cosf(2.f * t);
+  z.s[2] = sinf(2.f * t);
+  return z;
+}
+
+TTA_HD float zcos(const ZTrig& z, int f) { return z.c[f < 0 ? -f : f]; }
+TTA_HD float zsin(const ZTrig& z, int f) { return f < 0 ? -z.s[-f] : z.s[f]; }
+
+// out = Z M (n x n, row-major); the two terms of each entry are added in column order of Z.
 template <int L>
-TTA_HD void zrot(float t, float* Z) {
+TTA_HD void zleft(const ZTrig& z, const float* M, float* out) {
   constexpr int n = 2 * L + 1;
-  for (int i = 0; i < n * n; ++i) Z[i] = 0.f;
+#pragma unroll
   for (int i = 0; i < n; ++i) {
-    const float fa = (float)(L - i) * t;
-    Z[i * n + i] += cosf(fa);
-    Z[i * n + (n - 1 - i)] += sinf(fa);
+    const int f = L - i, i2 = n - 1 - i;
+#pragma unroll
+    for (int j = 0; j < n; ++j) {
+      if (f == 0) {
+        out[i * n + j] = M[i * n + j];
+      } else {
+        const float d = zcos(z, f) * M[i * n + j], a = zsin(z, f) * M[i2 * n + j];
+        out[i * n + j] = i < i2 ? d + a : a + d;
+      }
+    }
   }
 }
 
-// d Z / d t
+// out = M Z; column j of Z holds cos(f_j t) at row j and sin(-f_j t) at row n-1-j.
 template <int L>
-TTA_HD void zrot_d(float t, float* Z) {
+TTA_HD void zright(const ZTrig& z, const float* M, float* out) {
   constexpr int n = 2 * L + 1;
-  for (int i = 0; i < n * n; ++i) Z[i] = 0.f;
-  for (int i = 0; i < n; ++i) {
-    const float f = (float)(L - i);
-    const float fa = f * t;
-    Z[i * n + i] += -f * sinf(fa);
-    Z[i * n + (n - 1 - i)] += f * cosf(fa);
+#pragma unroll
+  for (int j = 0; j < n; ++j) {
+    const int f = L - j, j2 = n - 1 - j;
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+      if (f == 0) {
+        out[i * n + j] = M[i * n + j];
+      } else {
+        const float d = M[i * n + j] * zcos(z, f), a = M[i * n + j2] * zsin(z, -f);
+        out[i * n + j] = j < j2 ? d + a : a + d;
+      }
+    }
   }
 }
 
 template <int n>
 TTA_HD void matmul(const float* A, const float* B, float* C) {
+#pragma unroll
   for (int i = 0; i < n; ++i)
+#pragma unroll
     for (int j = 0; j < n; ++j) {
       float s = 0.f;
+#pragma unroll
       for (int k = 0; k < n; ++k) s += A[i * n + k] * B[k * n + j];
       C[i * n + j] = s;
     }
-}
-
-// D = ((((Za J) Zb) J) Zc), the torch evaluation order of geometry.py:142.
-template <int L>
-TTA_HD void wigner_block(const float* J, const float* Za, const float* Zb, const float* Zc,
-                         float* D) {
-  constexpr int n = 2 * L + 1;
-  float T1[n * n], T2[n * n];
-  matmul<n>(Za, J, T1);
-  matmul<n>(T1, Zb, T2);
-  matmul<n>(T2, J, T1);
-  matmul<n>(T1, Zc, D);
 }
 
 struct Frame {
@@ -99,64 +124,107 @@ TTA_HD Frame frame_of(const float ev[3], float gamma) {
   return f;
 }
 
+// D = ((((Za J) Zb) J) Zc), the torch evaluation order of geometry.py:142, with the Z products
+// taken sparse (the dense products add exact zeros).
+template <int L>
+TTA_HD void wigner_block(const float* J, const ZTrig& za, const ZTrig& zb, const ZTrig& zc,
+                         float* D) {
+  constexpr int n = 2 * L + 1;
+  float T1[n * n], T2[n * n];
+  zleft<L>(za, J, T1);
+  zright<L>(zb, T1, T2);
+  matmul<n>(T2, J, T1);
+  zright<L>(zc, T1, D);
+}
+
 // Packed Wigner coefficients [35] of one edge.  jd = [Jd_0 (1) | Jd_1 (9) | Jd_2 (25)].
 TTA_HD void wigner_coef(const float ev[3], float gamma, const float* jd, float* coef) {
   const Frame f = frame_of(ev, gamma);
+  const ZTrig za = ztrig(f.alpha_u), zb = ztrig(f.beta_u), zc = ztrig(f.gamma_u);
   // l = 0: D = Za J Zb J Zc with 1x1 blocks; every Z_0 is exactly 1.
   coef[0] = ((jd[0] * 1.f) * 1.f * jd[0]) * 1.f;
   {
-    float Za[9], Zb[9], Zc[9], D[9];
-    zrot<1>(f.alpha_u, Za);
-    zrot<1>(f.beta_u, Zb);
-    zrot<1>(f.gamma_u, Zc);
-    wigner_block<1>(jd + 1, Za, Zb, Zc, D);
+    float D[9];
+    wigner_block<1>(jd + 1, za, zb, zc, D);
     for (int r = 0; r < 3; ++r)
       for (int q = 0; q < 3; ++q) coef[row_koff_l1(r) + q] = D[r * 3 + q];
   }
   {
-    float Za[25], Zb[25], Zc[25], D[25];
-    zrot<2>(f.alpha_u, Za);
-    zrot<2>(f.beta_u, Zb);
-    zrot<2>(f.gamma_u, Zc);
-    wigner_block<2>(jd + 10, Za, Zb, Zc, D);
+    float D[25];
+    wigner_block<2>(jd + 10, za, zb, zc, D);
     for (int r = 0; r < 5; ++r)
       for (int q = 0; q < 5; ++q) coef[row_koff_l2(r) + q] = D[r * 5 + q];
   }
 }
 
-// sum_ij G_ij d D_ij / d(beta_u), d(gamma_u) for one degree block.
+// sum_ij G_ij d D_ij / d(beta_u) and d D_ij / d(gamma_u) for one degree block, D = A Zb J Zc with
+// A = Za J.  By the cyclic trace,
+//   gb = sum_kl dZb_kl (A^T G B^T)_kl,  B = J Zc,
+//   gc = sum_kl dZc_kl (R^T G)_kl,      R = A Zb J,
+// and dZ (d/dt of Z) is nonzero only at (k, k) = -f sin(f t) and (k, n-1-k) = f cos(f t), so
+// only those 2(n-1) entries of the two n x n products are formed.
 template <int L>
-TTA_HD void block_angle_grads(const float* J, const Frame& f, const float* G, float& gb,
-                              float& gc) {
+TTA_HD void block_angle_grads(const float* J, const ZTrig& za, const ZTrig& zb, const ZTrig& zc,
+                              const float* G, float& gb, float& gc) {
   constexpr int n = 2 * L + 1;
-  float Za[n * n], Zb[n * n], Zc[n * n], dZ[n * n], D[n * n];
-  zrot<L>(f.alpha_u, Za);
-  zrot<L>(f.beta_u, Zb);
-  zrot<L>(f.gamma_u, Zc);
-  zrot_d<L>(f.beta_u, dZ);
-  wigner_block<L>(J, Za, dZ, Zc, D);
-  for (int i = 0; i < n * n; ++i) gb += G[i] * D[i];
-  zrot_d<L>(f.gamma_u, dZ);
-  wigner_block<L>(J, Za, Zb, dZ, D);
-  for (int i = 0; i < n * n; ++i) gc += G[i] * D[i];
+  float A[n * n], T[n * n], R[n * n];
+  zleft<L>(za, J, A);
+  zright<L>(zb, A, T);
+  matmul<n>(T, J, R);
+#pragma unroll
+  for (int k = 0; k < n; ++k) {
+    const int f = L - k, k2 = n - 1 - k;
+    if (f == 0) continue;
+    float dd = 0.f, da = 0.f;  // (R^T G)_{k,k}, (R^T G)_{k,k2}
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+      dd += R[i * n + k] * G[i * n + k];
+      da += R[i * n + k] * G[i * n + k2];
+    }
+    gc += (-(float)f * zsin(zc, f)) * dd + ((float)f * zcos(zc, f)) * da;
+  }
+  zright<L>(zc, J, T);  // B = J Zc
+  // P = G B^T, reusing R
+#pragma unroll
+  for (int i = 0; i < n; ++i)
+#pragma unroll
+    for (int l = 0; l < n; ++l) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < n; ++j) s += G[i * n + j] * T[l * n + j];
+      R[i * n + l] = s;
+    }
+#pragma unroll
+  for (int k = 0; k < n; ++k) {
+    const int f = L - k, k2 = n - 1 - k;
+    if (f == 0) continue;
+    float dd = 0.f, da = 0.f;  // (A^T P)_{k,k}, (A^T P)_{k,k2}
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+      dd += A[i * n + k] * R[i * n + k];
+      da += A[i * n + k] * R[i * n + k2];
+    }
+    gb += (-(float)f * zsin(zb, f)) * dd + ((float)f * zcos(zb, f)) * da;
+  }
 }
 
 // VJP of wigner_coef: given g_coef[35] returns g_ev[3] (adds into g_ev).
 TTA_HD void wigner_vjp(const float ev[3], float gamma, const float* jd, const float* gcoef,
                        float g_ev[3]) {
   const Frame f = frame_of(ev, gamma);
+  const ZTrig za = ztrig(f.alpha_u), zb = ztrig(f.beta_u), zc = ztrig(f.gamma_u);
   float gb = 0.f, gc = 0.f;
   {
     float G[9];
     for (int r = 0; r < 3; ++r)
       for (int q = 0; q < 3; ++q) G[r * 3 + q] = gcoef[row_koff_l1(r) + q];
-    block_angle_grads<1>(jd + 1, f, G, gb, gc);
+    block_angle_grads<1>(jd + 1, za, zb, zc, G, gb, gc);
   }
   {
     float G[25];
     for (int r = 0; r < 5; ++r)
       for (int q = 0; q < 5; ++q) G[r * 5 + q] = gcoef[row_koff_l2(r) + q];
-    block_angle_grads<2>(jd + 10, f, G, gb, gc);
+    block_angle_grads<2>(jd + 10, za, zb, zc, G, gb, gc);
   }
   // beta_u = -beta, gamma_u = -alpha
   const float g_beta = -gb;

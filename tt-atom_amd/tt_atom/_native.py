@@ -59,6 +59,8 @@ _SIGS = {
     "tta_sum": [_P, _I64, _I64, _P, _P],
     "tta_fill": [_P, _I64, _F, _P],
     "tta_edge_wigner": [_P, _P, _P, _P, _P, _F, _P, _P, _P, _I64, _I64, _P],
+    "tta_edge_geometry_fwd": [_P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _F, _F, _I64, _I64,
+                              _P, _P, _P, _P, _P, _I64, _I64, _P],
     "tta_edge_features": [_P, _P, _P, _P, _P, _P, _F, _F, _I64, _I64, _P, _P, _I64, _P],
     "tta_edge_geometry_bwd": [_P, _P, _P, _P, _P, _I64, _P, _F, _F, _I64, _P, _F, _P, _I64, _P],
     "tta_node_forces": [_P, _P, _P, _P, _P, _I64, _I64, _P],
@@ -705,6 +707,36 @@ def edge_features(dist, zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, nb
               _ptr(offsets, numel=nb, name="offsets"), float(coeff), float(cutoff), nb, ec,
               _ptr(x_edge, numel=E * (nb + 2 * ec), name="x_edge"), _ptr(env, numel=E), E,
               _stream(), compulsory=E * (4 + 8 + 4 * (nb + 2 * ec) + 4) + 4 * nb
+              + 4 * sum(t.numel() for t in (src_emb, tgt_emb) if t is not None))
+
+
+def edge_geometry_fwd(pos, src, tgt, shift, jd, gamma, zsrc, ztgt, src_emb, tgt_emb, offsets,
+                      coeff, cutoff, nb, ec, ev, dist, coef, x_edge, env):
+    """edge_wigner + edge_features in one launch (same results)."""
+    N = pos.shape[0]
+    E = src.numel()
+    v4 = (nb % 4 == 0 and ec % 4 == 0 and nb + 2 * ec < (1 << 14)
+          and _al16(x_edge, offsets, src_emb, tgt_emb))
+    if not v4:
+        edge_wigner(pos, src, tgt, shift, jd, gamma, ev, dist, coef)
+        edge_features(dist, zsrc, ztgt, src_emb, tgt_emb, offsets, coeff, cutoff, nb, ec,
+                      x_edge, env)
+        return
+    sh = 12 if shift is not None else 0
+    W = nb + 2 * ec
+    # per edge: src / tgt, two gathered positions, the shift, two species, two gathered
+    # embedding rows; out ev, dist, 35 coefficients, the x_edge row and the envelope
+    _hbm_call("k_edge_geometry_fwd",
+              E * (8 + 24 + sh + 8 + 8 * ec + 12 + 4 + 140 + 4 * W + 4) + 140 + 4 * nb,
+              "tta_edge_geometry_fwd",
+              _ptr(pos, numel=N * 3, name="pos"), _i32(src, E), _i32(tgt, E),
+              _ptr(shift, numel=E * 3, name="shift"), _ptr(jd, numel=35, name="jd"), float(gamma),
+              _i32(zsrc, E), _i32(ztgt, E), _ptr(src_emb, name="src_emb"),
+              _ptr(tgt_emb, name="tgt_emb"), _ptr(offsets, numel=nb, name="offsets"),
+              float(coeff), float(cutoff), nb, ec, _ptr(ev, numel=E * 3),
+              _ptr(dist, numel=E), _ptr(coef, numel=E * 35),
+              _ptr(x_edge, numel=E * W, name="x_edge"), _ptr(env, numel=E), N, E, _stream(),
+              compulsory=E * (8 + sh + 8 + 12 + 4 + 140 + 4 * W + 4) + 12 * N + 140 + 4 * nb
               + 4 * sum(t.numel() for t in (src_emb, tgt_emb) if t is not None))
 
 

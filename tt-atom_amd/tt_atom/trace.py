@@ -218,10 +218,10 @@ class TracedEngine:
         bb, geo, g = self.bb, self.geo, self.g
         E, N, C, H, L = self.E, self.N, self.C, self.H, self.L
         LH, LHc = L * H, self.LHc
-        nat.edge_wigner(self.pos, g.src, g.tgt, g.shift, geo.jd, geo.gamma, self.ev, self.dist,
-                        self.coef)
-        nat.edge_features(self.dist, g.zsrc, g.ztgt, bb.src_emb, bb.tgt_emb, geo.offset,
-                          geo.coeff, geo.cutoff, self.nb, self.ec, self.x_edge, self.env)
+        nat.edge_geometry_fwd(self.pos, g.src, g.tgt, g.shift, geo.jd, geo.gamma, g.zsrc,
+                              g.ztgt, bb.src_emb, bb.tgt_emb, geo.offset, geo.coeff, geo.cutoff,
+                              self.nb, self.ec, self.ev, self.dist, self.coef, self.x_edge,
+                              self.env)
         nat.linear(self.x_edge, bb.rad_w0t_all, bb.rad_b0_all, out=self.a0_all)
         self._radials_fwd()
         # edge-degree node init (geometry.py:268-276)

@@ -75,6 +75,17 @@ int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const float* bias, 
  * empty products are skipped. */
 int tta_gemm_bf16x_group(const tta_gemm_problem* probs, int64_t n, int mode, tta_stream_t stream);
 int tta_gemm_f32_group(const tta_gemm_problem* probs, int64_t n, tta_stream_t stream);
+/* tta_gemm_f32_group for launches too small to fill the GPU (the node- and edge-level linears
+ * of small systems, the same call sites).  When the products have fewer than 160 tiles of
+ * 32 x 64 in all, those with K >= 256 have their K cut into chunks (multiples of 64, at least
+ * 128); each chunk's partial product is written to work and a second launch sums the chunks in
+ * order and applies the epilogue.  A product's k sums may be ordered differently than in a
+ * launch of other products; a product of one chunk gives the bits of tta_gemm_f32.
+ * tta_gemm_f32_splitk_work returns the floats work must hold (0: nothing splits, use
+ * tta_gemm_f32_group; -1: bad list).  Deterministic (no atomics). */
+int64_t tta_gemm_f32_splitk_work(const tta_gemm_problem* probs, int64_t n);
+int tta_gemm_f32_group_splitk(const tta_gemm_problem* probs, int64_t n, float* work,
+                              int64_t work_floats, tta_stream_t stream);
 
 /* ---------------------------------------------------------------- edge-frame rotation
  * out[e, m, :] = (sum_j W[e,m,j] [x[src_e, j, :] | x[tgt_e, j, :]]) * rad[e, rb(m), :]

@@ -90,6 +90,62 @@ def test_gemm_matches_torch(nat, M, N, K, epi):
         assert (C2.cpu().double() - torch.nn.functional.silu(ref)).abs().max() < tol
 
 
+@pytest.mark.parametrize("M,N,K", [(72, 1024, 1024), (72, 1024, 256), (576, 256, 1024),
+                                   (37, 100, 300), (1, 64, 512)])
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
+def test_gemm_splitk_matches_fp64(nat, M, N, K, epi):
+    """Small-grid fp32 products run as k chunks plus an in-order reduction (the linears of small
+    systems): fp64 reference at the fp32 kernel's tolerance, every epilogue, K not a multiple of
+    the chunk, N and K not multiples of 4 (scalar loads), a single row."""
+    g = torch.Generator().manual_seed(M + 3 * N + K)
+    A, B = torch.randn(M, K, generator=g), torch.randn(K, N, generator=g)
+    bias, C0, aux = torch.randn(N, generator=g), torch.randn(M, N, generator=g), \
+        torch.randn(M, N, generator=g)
+    probs = (nat.GemmProblem * 1)(nat.GemmProblem(None, None, None, None, None, None, M, N, K,
+                                                  K, N, N, epi))
+    assert nat.load().tta_gemm_f32_splitk_work(probs, 1) > 0      # this shape takes the split
+    Cd, C2 = C0.clone().to(DEV), torch.zeros(M, N, device=DEV)
+    nat.linear(A.to(DEV), B.to(DEV), bias.to(DEV), out=Cd, epilogue=epi, out2=C2, aux=aux.to(DEV))
+    torch.cuda.synchronize()
+    ref = (A.double() @ B.double()) + bias.double()
+    if epi == 1:
+        ref = torch.nn.functional.silu(ref)
+    elif epi == 2:
+        ref = ref + C0.double()
+    elif epi == 4:
+        s = torch.sigmoid(aux.double())
+        ref = ref * (s * (1 + aux.double() * (1 - s)))
+    tol = 2e-5 * math.sqrt(K) * float(ref.abs().max())
+    assert (Cd.cpu().double() - ref).abs().max() < tol
+    if epi == 3:
+        assert (C2.cpu().double() - torch.nn.functional.silu(ref)).abs().max() < tol
+
+
+def test_gemm_splitk_group_bits(nat):
+    """Split-K launches: a product the rule leaves in one chunk (K = 128) gets the bits of the
+    unsplit fp32 kernel, a split product matches its unsplit value to fp32 rounding, and repeated
+    launches are bit-identical.  (70 + 50 tiles of 32 x 64: below the 160-tile limit.)"""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(300, 1024, generator=g).to(DEV)
+    w1, w2 = torch.randn(1024, 448, generator=g).to(DEV), torch.randn(128, 320, generator=g).to(DEV)
+    b2 = torch.randn(320, generator=g).to(DEV)
+    o1, o2 = torch.empty(300, 448, device=DEV), torch.empty(300, 320, device=DEV)
+    items = [(x, w1, None, o1, nat.EPI_SILU), (x[:, :128], w2, b2, o2, nat.EPI_STORE)]
+    probs = (nat.GemmProblem * 2)(*[nat.GemmProblem(None, None, None, None, None, None, 300, w.shape[1],
+                                                    a.shape[1], 1024, w.shape[1], w.shape[1], 0)
+                                    for a, w, *_ in items])
+    assert nat.load().tta_gemm_f32_splitk_work(probs, 2) > 0
+    nat.linear_group(items)
+    r1, r2 = torch.empty_like(o1), torch.empty_like(o2)
+    nat.gemm(x, w1, r1, M=300, N=448, K=1024, lda=1024, ldb=448, ldc=448, epilogue=nat.EPI_SILU)
+    nat.gemm(x, w2, r2, M=300, N=320, K=128, lda=1024, ldb=320, ldc=320, bias=b2)
+    a1, a2 = torch.empty_like(o1), torch.empty_like(o2)
+    nat.linear_group([(x, w1, None, a1, nat.EPI_SILU), (x[:, :128], w2, b2, a2, nat.EPI_STORE)])
+    torch.cuda.synchronize()
+    assert torch.equal(o2, r2) and torch.equal(o2, a2) and torch.equal(o1, a1)
+    assert (o1 - r1).abs().max() < 1e-4 * float(r1.abs().max())
+
+
 def test_gemm_batched_strided(nat):
     g = torch.Generator().manual_seed(5)
     N_, C, H = 50, 32, 24
@@ -731,8 +787,10 @@ def test_forces_virial_and_sum(nat):
 def test_linear_group_equals_separate_calls(nat, mode, M):
     """Grouped launches (one launch for up to four products: column blocks of one input and one
     output, as the SO(2) m-blocks use them, with bias / accumulate / two-output / silu-grad
-    epilogues) give the same bits as one call per product, on the split kernel in modes 16 and 6
-    (M = 5000) and on the fp32 kernel (M = 700 < 4096 routes there)."""
+    epilogues) give the same bits as one call per product on the split kernel in modes 16 and 6
+    (M = 5000).  On the fp32 kernel (M = 700 < 4096 routes there) a product that alone is too
+    small to fill the GPU (700 x 256, 88 tiles) runs split-K alone but not in the group, so the
+    two agree to fp32 rounding there and bit for bit elsewhere."""
     g = torch.Generator().manual_seed(11)
     x = torch.randn(M, 9 * 128, generator=g).to(DEV)
     outs = {}
@@ -766,7 +824,11 @@ def test_linear_group_equals_separate_calls(nat, mode, M):
         torch.cuda.synchronize()
         outs[grouped] = (out.clone(), out2.clone(), o4.clone())
     for a, b in zip(outs[False], outs[True]):
-        assert torch.equal(a, b)
+        if M >= 4096:
+            assert torch.equal(a, b)
+        else:
+            assert torch.equal(a[:, :640 + 512], b[:, :640 + 512])
+            assert (a - b).abs().max() <= 1e-5 * max(1.0, float(a.abs().max()))
     assert outs[True][1][:, :640].abs().max() == 0 and outs[True][1][:, 1152:].abs().max() == 0
     ref = x[:, :384].double().cpu() @ ws[0].w_t.double().cpu() + bias.double().cpu()
     assert (outs[True][0][:, :640].cpu().double() - ref).abs().max() < 1e-3

@@ -42,8 +42,8 @@ struct Tile {
 };
 
 template <class TL, int BM, bool VEC>
-__device__ __forceinline__ void load_a(const GemmArgs& p, const float* A, int m0, int k0, int t,
-                                       float (&ra)[TL::A_PER_T * 4]) {
+__device__ __forceinline__ void load_a(const GemmArgs& p, const float* A, int m0, int k0, int kmax,
+                                       int t, float (&ra)[TL::A_PER_T * 4]) {
 #pragma unroll
   for (int h = 0; h < TL::A_PER_T; ++h) {
     const int i = t + 256 * h;
@@ -52,26 +52,26 @@ __device__ __forceinline__ void load_a(const GemmArgs& p, const float* A, int m0
     const bool in = i < TL::A_VEC && row < p.M;
     if (VEC) {
       floatx4 v = {0.f, 0.f, 0.f, 0.f};
-      if (in && k < p.K) v = *reinterpret_cast<const floatx4*>(A + (int64_t)row * p.lda + k);
+      if (in && k < kmax) v = *reinterpret_cast<const floatx4*>(A + (int64_t)row * p.lda + k);
 #pragma unroll
       for (int c = 0; c < 4; ++c) ra[4 * h + c] = v[c];
     } else {
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        ra[4 * h + c] = (in && k + c < p.K) ? A[(int64_t)row * p.lda + k + c] : 0.f;
+        ra[4 * h + c] = (in && k + c < kmax) ? A[(int64_t)row * p.lda + k + c] : 0.f;
     }
   }
 }
 
 template <class TL, int BN, bool VEC>
-__device__ __forceinline__ void load_b(const GemmArgs& p, const float* B, int n0, int k0, int t,
-                                       float (&rb)[TL::B_PER_T * 4]) {
+__device__ __forceinline__ void load_b(const GemmArgs& p, const float* B, int n0, int k0, int kmax,
+                                       int t, float (&rb)[TL::B_PER_T * 4]) {
 #pragma unroll
   for (int h = 0; h < TL::B_PER_T; ++h) {
     const int i = t + 256 * h;
     const int k = k0 + i / (BN / 4);
     const int col = n0 + (i % (BN / 4)) * 4;
-    const bool in = i < TL::B_VEC && k < p.K;
+    const bool in = i < TL::B_VEC && k < kmax;
     if (VEC) {
       floatx4 v = {0.f, 0.f, 0.f, 0.f};
       if (in && col < p.N) v = *reinterpret_cast<const floatx4*>(B + (int64_t)k * p.ldb + col);
@@ -116,8 +116,9 @@ __device__ __forceinline__ void store_b(float (*Bs)[BN + PAD], int t,
 // The epilogue is a (wave-uniform) runtime switch so every GEMM of the step is one kernel
 // symbol per tile shape; it runs once per output element and costs nothing next to the K loop.
 // GROUP: blockIdx.z selects the product of g (batch 1 each); otherwise g.p[0] is one strided
-// batch and blockIdx.z its batch index.
-template <int BM, int BN, int WGM, int WGN, int BK, bool VEC, bool GROUP>
+// batch and blockIdx.z its batch index.  SPLIT (with GROUP): blockIdx.y selects a k chunk of
+// g.kch[z]; the block stores its raw partial sums for k_splitk_reduce instead of the epilogue.
+template <int BM, int BN, int WGM, int WGN, int BK, bool VEC, bool GROUP, bool SPLIT = false>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmGroup g) {
   const GemmArgs& p = g.p[GROUP ? blockIdx.z : 0];
   const int64_t bz = GROUP ? 0 : blockIdx.z;
@@ -146,6 +147,12 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmGroup g) {
   const float* aux = p.aux ? p.aux + bz * p.sC : nullptr;
   const float* bias = p.bias ? p.bias + bz * p.sBias : nullptr;
 
+  // k range of this block: the whole of K, or chunk blockIdx.y of the product's chunk length
+  const int kc = SPLIT ? g.kch[blockIdx.z] : 0;
+  const int kbeg = SPLIT ? (int)blockIdx.y * kc : 0;
+  if (SPLIT && kbeg >= p.K) return;  // a product with fewer chunks than the grid's
+  const int kend = SPLIT ? min(p.K, kbeg + kc) : p.K;
+
   floatx4 acc[TI][TJ];
 #pragma unroll
   for (int i = 0; i < TI; ++i)
@@ -153,9 +160,9 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmGroup g) {
     for (int j = 0; j < TJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   float ra[TL::A_PER_T * 4], rb[TL::B_PER_T * 4];
-  const int nk = (p.K + BK - 1) / BK;
-  load_a<TL, BM, VEC>(p, A, m0, 0, t, ra);
-  load_b<TL, BN, VEC>(p, B, n0, 0, t, rb);
+  const int nk = (kend - kbeg + BK - 1) / BK;
+  load_a<TL, BM, VEC>(p, A, m0, kbeg, kend, t, ra);
+  load_b<TL, BN, VEC>(p, B, n0, kbeg, kend, t, rb);
   store_a<TL, BM>(As[0], t, ra);
   store_b<TL, BN>(Bs[0], t, rb);
   __syncthreads();
@@ -166,8 +173,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmGroup g) {
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < nk) {
-      load_a<TL, BM, VEC>(p, A, m0, (kt + 1) * BK, t, ra);
-      load_b<TL, BN, VEC>(p, B, n0, (kt + 1) * BK, t, rb);
+      load_a<TL, BM, VEC>(p, A, m0, kbeg + (kt + 1) * BK, kend, t, ra);
+      load_b<TL, BN, VEC>(p, B, n0, kbeg + (kt + 1) * BK, kend, t, rb);
     }
 #pragma unroll
     for (int kk = 0; kk < BK / 4; ++kk) {
@@ -190,7 +197,47 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmGroup g) {
     __syncthreads();
   }
 
-  store_tiles<TI, TJ>(p, acc, m0 + rbase, n0 + cbase, li, lk, C, C2, aux, bias);
+  if constexpr (SPLIT) {
+    // raw partial of this chunk, [M, N] row-major
+    float* W = g.work + g.woff[blockIdx.z] + (int64_t)blockIdx.y * p.M * p.N;
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+      const int col = n0 + cbase + j * 16 + li;
+      if (col >= p.N) continue;
+#pragma unroll
+      for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = m0 + rbase + i * 16 + lk * 4 + r;
+          if (row < p.M) W[(int64_t)row * p.N + col] = acc[i][j][r];
+        }
+    }
+  } else {
+    store_tiles<TI, TJ>(p, acc, m0 + rbase, n0 + cbase, li, lk, C, C2, aux, bias);
+  }
+}
+
+// C = epi(sum of the product's k-chunk partials, in chunk order, + bias): the epilogue of
+// store_tiles on the split-K partials.  blockIdx.z selects the product, threads stride over its
+// M x N outputs.
+__global__ __launch_bounds__(256) void k_splitk_reduce(GemmGroup g) {
+  const GemmArgs& p = g.p[blockIdx.z];
+  const int64_t MN = (int64_t)p.M * p.N;
+  const int ns = (p.K + g.kch[blockIdx.z] - 1) / g.kch[blockIdx.z];
+  const float* W = g.work + g.woff[blockIdx.z];
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int row = (int)(i / p.N), col = (int)(i - (int64_t)row * p.N);
+    float v = ns > 0 ? W[i] : 0.f;  // K = 0: the epilogue of a zero product
+    for (int s = 1; s < ns; ++s) v += W[s * MN + i];
+    if (p.bias) v += p.bias[col];
+    const int64_t off = (int64_t)row * p.ldc + col;
+    if (p.epi == EPI_SILU) v = tta_silu(v);
+    if (p.epi == EPI_ACCUM) v += p.C[off];
+    if (p.epi == EPI_PRE_SILU) p.C2[off] = tta_silu(v);
+    if (p.epi == EPI_SILU_GRAD) v = v * tta_silu_grad(p.aux[off]);
+    p.C[off] = v;
+  }
 }
 
 // n products (group) or one product with `batch` strided copies (n == 1, group false).
@@ -327,4 +374,103 @@ extern "C" int tta_gemm_f32_group(const tta_gemm_problem* probs, int64_t n, hipS
   }
   if (m == 0) return tta::kOk;
   return dispatch(g, m, true, 1, vec_all, stream);
+}
+
+// Split-K form of tta_gemm_f32_group.  A launch whose products have fewer than 160 tiles of
+// 32 x 64 in all leaves most compute units idle and is bound by the latency of each
+// workgroup's k loop (about 20 us at K = 1024); its products with K >= 256 then have their K cut
+// into chunks (multiples of 64, at least 128) aiming at about 640 workgroups, and the others run
+// as one chunk.  With more tiles the fp32 matrix rate of the launch bounds it and splitting one
+// small product of a group measured slower, so nothing is split.  The decision belongs to the
+// launch: a product's k sums may be ordered differently grouped and alone, while a one-chunk
+// product gives the bits of tta_gemm_f32 (its partial is the whole k loop, in the same k order).
+namespace {
+
+int64_t splitk_tiles(const tta_gemm_problem* probs, int64_t n) {
+  int64_t tiles = 0;
+  for (int64_t i = 0; i < n; ++i)
+    if (probs[i].M > 0 && probs[i].N > 0)
+      tiles += tta_blocks(probs[i].M, 32) * tta_blocks(probs[i].N, 64);
+  return tiles;
+}
+
+// chunk length for a product of the launch (K itself: one chunk)
+int64_t splitk_chunk(int64_t K, int64_t tiles) {
+  const int64_t one = std::max<int64_t>(1, K);
+  if (K < 256 || tiles >= 160) return one;
+  const int64_t chunks = std::min<int64_t>((640 + tiles - 1) / tiles, K / 128);
+  if (chunks < 2) return one;
+  return ((K + chunks - 1) / chunks + 63) / 64 * 64;
+}
+
+}  // namespace
+
+// Workspace of tta_gemm_f32_group_splitk for these products, in floats: the sum over products
+// of ceil(K / chunk) * M * N when some product takes more than one chunk, else 0 (nothing to
+// gain over tta_gemm_f32_group).
+extern "C" int64_t tta_gemm_f32_splitk_work(const tta_gemm_problem* probs, int64_t n) {
+  if (n < 0 || n > kMaxGroup || (!probs && n > 0)) return -1;
+  const int64_t tiles = splitk_tiles(probs, n);
+  int64_t need = 0;
+  bool split = false;
+  for (int64_t i = 0; i < n; ++i) {
+    const tta_gemm_problem& q = probs[i];
+    if (q.M <= 0 || q.N <= 0 || q.K < 0) continue;
+    const int64_t kc = splitk_chunk(q.K, tiles);
+    const int64_t chunks = (q.K + kc - 1) / kc;
+    split = split || chunks > 1;
+    need += chunks * q.M * q.N;
+  }
+  return split ? need : 0;
+}
+
+extern "C" int tta_gemm_f32_group_splitk(const tta_gemm_problem* probs, int64_t n, float* work,
+                                         int64_t work_floats, hipStream_t stream) {
+  TTA_CHECK_ARG(n >= 0 && n <= kMaxGroup && (probs || n == 0),
+                "tta_gemm_f32_group_splitk: 0..%d products", kMaxGroup);
+  GemmGroup g{};
+  int m = 0;
+  bool vec_all = true;
+  int64_t need = 0, max_chunks = 0, max_tiles = 0, max_mn = 0;
+  const int64_t tiles = splitk_tiles(probs, n);
+  for (int64_t i = 0; i < n; ++i) {
+    const tta_gemm_problem& q = probs[i];
+    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= 4, "tta_gemm_f32_group_splitk: bad epilogue");
+    GemmArgs p{q.A, q.B, q.C, q.bias, q.C2, q.aux, 0, 0, 0, q.lda, q.ldb, q.ldc, 0, 0, 0, 0,
+               (int)q.epilogue, nullptr, nullptr, nullptr, 0, 0};
+    bool skip = false, vec = false;
+    const int rc = check(p, q.M, q.N, q.K, 1, "tta_gemm_f32_group_splitk", &skip, &vec);
+    if (rc != tta::kOk) return rc;
+    if (skip) continue;
+    const int64_t kc = splitk_chunk(q.K, tiles);
+    const int64_t chunks = (q.K + kc - 1) / kc;
+    g.kch[m] = (int)kc;
+    g.woff[m] = need;
+    need += chunks * q.M * q.N;
+    max_chunks = std::max(max_chunks, chunks);
+    max_tiles = std::max(max_tiles, (int64_t)tta_blocks(q.N, 64) * tta_blocks(q.M, 32));
+    max_mn = std::max(max_mn, q.M * q.N);
+    g.p[m++] = p;
+    vec_all = vec_all && vec;
+  }
+  if (m == 0) return tta::kOk;
+  TTA_CHECK_ARG(work && work_floats >= need,
+                "tta_gemm_f32_group_splitk: work holds %lld floats, needs %lld",
+                (long long)work_floats, (long long)need);
+  TTA_CHECK_ARG(max_chunks <= 65535 && max_tiles <= (1ll << 30),
+                "tta_gemm_f32_group_splitk: grid too large");
+  g.work = work;
+  if (max_chunks > 0) {
+    const dim3 grid((unsigned)(((max_tiles + 7) / 8) * 8), (unsigned)max_chunks, (unsigned)m);
+    if (vec_all)
+      hipLaunchKernelGGL((gemm_f32_kernel<32, 64, 2, 2, 64, true, true, true>), grid, dim3(256), 0,
+                         stream, g);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<32, 64, 2, 2, 64, false, true, true>), grid, dim3(256),
+                         0, stream, g);
+  }
+  const int64_t rb = std::min<int64_t>((max_mn + 255) / 256, 2048);
+  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)rb, 1, (unsigned)m), dim3(256), 0, stream, g);
+  TTA_CHECK_LAUNCH("tta_gemm_f32_group_splitk");
+  return tta::kOk;
 }

@@ -39,6 +39,11 @@ struct GemmGroup {
   int NT32[kMaxGroup];
   int vec[kMaxGroup];
   int cap;  // split kernel: most blocks per product (persistent tile loop), a multiple of 8
+  // split-K fp32 kernel: blockIdx.y takes k range [y * kch[z], (y + 1) * kch[z]) of product z
+  // and writes its raw partial [M, N] to work + woff[z] + y * M * N
+  float* work;
+  int64_t woff[kMaxGroup];
+  int kch[kMaxGroup];
 };
 
 // Accumulator layout of v_mfma_f32_16x16x{4f32,32bf16}: lane l holds D[4*(l/16)+r][l%16] in

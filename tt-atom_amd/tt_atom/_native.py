@@ -93,6 +93,8 @@ _SIGS = {
                        _I64, _I64, _I, _P],
     "tta_gemm_bf16x_group": [ctypes.POINTER(GemmProblem), _I64, _I, _P],
     "tta_gemm_f32_group": [ctypes.POINTER(GemmProblem), _I64, _P],
+    "tta_gemm_f32_splitk_work": [ctypes.POINTER(GemmProblem), _I64],
+    "tta_gemm_f32_group_splitk": [ctypes.POINTER(GemmProblem), _I64, _P, _I64, _P],
     "tta_radius_graph_thresholds": [_P, _I64, _P, _P, _P, _I64, _P, _P, _I, _D, _F, _F, _I, _P,
                                     _P, _P, _P, _P],
     "tta_radius_graph_count": [_P, _I64, _P, _P, _P, _I64, _P, _P, _I, _D, _F, _F, _P, _P, _P,
@@ -109,7 +111,7 @@ _SIGS = {
                                      _D, _F, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P],
 }
 _RESTYPE = {"tta_last_error": ctypes.c_char_p, "tta_pack_b_elems": ctypes.c_int64,
-            "tta_cell_list_workspace": ctypes.c_int64}
+            "tta_cell_list_workspace": ctypes.c_int64, "tta_gemm_f32_splitk_work": ctypes.c_int64}
 
 EXPORTS = tuple(_SIGS)
 
@@ -335,6 +337,43 @@ def _split_ok(x, pw):
             and _ld(x, "x") < (1 << 21))
 
 
+def _gemm_f32_splitk(items):
+    """items = [(x, w_t, bias, out, epilogue, out2, aux)] of fp32 row-major products: one
+    tta_gemm_f32_group_splitk call (k chunks run as separate workgroups, then a reduction) with
+    a workspace from the caching allocator, when the library's rule splits any of them (grids
+    too small to fill the GPU, K >= 256).  Returns False, having launched nothing, otherwise."""
+    probs = (GemmProblem * len(items))()
+    flops = nbytes = 0.0
+    for i, (x, w, bias, out, epi, out2, aux) in enumerate(items):
+        M, K = x.shape
+        N = w.shape[1]
+        ldc = _ld(out, "out")
+        probs[i] = GemmProblem(
+            _rows(x, M, _ld(x, "x"), K, "x"), _rows(w, K, _ld(w, "w_t"), N, "w_t"),
+            _rows(out, M, ldc, N, "out"),
+            None if bias is None else _ptr(bias, numel=N, name="bias"),
+            None if out2 is None else _rows(out2, M, _ld(out2, "out2"), N, "out2"),
+            None if aux is None else _rows(aux, M, _ld(aux, "aux"), N, "aux"),
+            M, N, K, _ld(x, "x"), _ld(w, "w_t"), ldc, epi)
+        flops += 2.0 * M * N * K
+        nbytes += 4.0 * (M * K + K * N + (1 + (epi in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD)))
+                         * M * N)
+    need = load().tta_gemm_f32_splitk_work(probs, len(items))
+    if need < 0:
+        raise RuntimeError("tta_gemm_f32_splitk_work: bad product list")
+    if need == 0:
+        return False
+    work = torch.empty(need, device=items[0][0].device, dtype=torch.float32)
+    probe = _gemm_probe
+    if probe is not None:
+        probe.before(flops, nbytes, "f32")
+    _call("tta_gemm_f32_group_splitk", probs, len(items), work.data_ptr(), work.numel(),
+          _stream())
+    if probe is not None:
+        probe.after()
+    return True
+
+
 def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None):
     """y = x @ w_t (+ bias) for 2-D row-major x [M, K] (any row stride) and w_t [K, N] (a tensor
     or a PackedWeight; a packed weight runs on the split kernel when the shapes allow)."""
@@ -350,6 +389,8 @@ def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None)
             _gemm_bf16x(x, w_t, out, bias, epilogue, out2, aux)
             return out
         w_t = w_t.w_t
+    if M < 4096 and K >= 256 and _gemm_f32_splitk([(x, w_t, bias, out, epilogue, out2, aux)]):
+        return out
     gemm(x, w_t, out, M=M, N=N, K=K, lda=_ld(x, "x"), ldb=_ld(w_t, "w_t"), ldc=_ld(out, "out"),
          bias=bias, epilogue=epilogue, C2=out2, aux=aux)
     return out
@@ -373,6 +414,9 @@ def linear_group(items):
     if len(items) > MAX_GROUP or (any(split) and not all(split)) or len(modes) > 1:
         for x, w, bias, out, epi, out2, aux in items:
             linear(x, w, bias, out, epi, out2, aux)
+        return
+    if not split[0] and any(x.shape[1] >= 256 for x, *_ in items) and _gemm_f32_splitk(
+            [(x, w.w_t if isinstance(w, PackedWeight) else w, *rest) for x, w, *rest in items]):
         return
     probs = (GemmProblem * len(items))()
     flops = nbytes = 0.0

@@ -340,6 +340,42 @@ def test_split_f16_scaling(nat, case):
     assert errs["f16x3"] <= max(2.0 * errs["f32"], 1e-6), (case, errs)
 
 
+@pytest.mark.parametrize("case", ["grows past 2^15", "late first values", "tiny late values"])
+def test_split_f16_fast_loop_retry(nat, case):
+    """K a multiple of 32: waves whose rows are all unscaled after the first slab run the fast
+    loop, which leaves the per-slab scale events to one check per tile and computes a tile again
+    on the checked path when a row needs a rescale.  A row planted into one tile of a normal
+    matrix -- values that pass 2^15 from k = 256 on, a row that is zero for its first slab, or one
+    whose late values are tiny -- must leave every other row bit-identical to the run without it
+    (a retry computes the first case's whole tile on the checked path; a row still unset after
+    its first slab sends its wave there directly), and be accurate itself."""
+    g = torch.Generator().manual_seed(5)
+    M, K, N = 1000, 512, 384                 # the split kernel through its C entry point
+    A = torch.randn(M, K, generator=g)
+    B = torch.randn(K, N, generator=g) / math.sqrt(K)
+    pw = nat.PackedWeight(B.to(DEV), nat.SPLIT_F16X3)
+    r = 300                                  # a row inside the third 128-row tile
+    A2 = A.clone()
+    if case == "grows past 2^15":
+        A2[r, 256:] *= 2.0 ** 17
+    elif case == "late first values":
+        A2[r, :32] = 0.0
+    else:
+        A2[r, :64] = 0.0
+        A2[r, 64:] *= 2.0 ** -20
+    outs = []
+    for a in (A, A2):
+        out = torch.empty(M, N, device=DEV)
+        nat._gemm_bf16x(a.to(DEV), pw, out, None, nat.EPI_STORE, None, None)
+        outs.append(out.cpu())
+    others = torch.ones(M, dtype=torch.bool)
+    others[r] = False
+    assert torch.equal(outs[0][others], outs[1][others])
+    ref = A2[r].double() @ B.double()
+    mag = A2[r].double().abs() @ B.double().abs()
+    assert ((outs[1][r].double() - ref).abs() / mag).max().item() < 2e-6
+
+
 # ------------------------------------------------------------------------------ geometry
 def _oracle_wig(ev, jd):
     eul = OG.euler_angles(ev)

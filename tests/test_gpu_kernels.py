@@ -342,13 +342,12 @@ def test_split_f16_scaling(nat, case):
 
 @pytest.mark.parametrize("case", ["grows past 2^15", "late first values", "tiny late values"])
 def test_split_f16_fast_loop_retry(nat, case):
-    """K a multiple of 32: waves whose rows are all unscaled after the first slab run the fast
-    loop, which leaves the per-slab scale events to one check per tile and computes a tile again
-    on the checked path when a row needs a rescale.  A row planted into one tile of a normal
-    matrix -- values that pass 2^15 from k = 256 on, a row that is zero for its first slab, or one
-    whose late values are tiny -- must leave every other row bit-identical to the run without it
-    (a retry computes the first case's whole tile on the checked path; a row still unset after
-    its first slab sends its wave there directly), and be accurate itself."""
+    """K a multiple of 32: waves whose rows are all unscaled run the fast loop, whose slab check
+    only branches out for a scale event (a row passing 2^15, or a row's first nonzero slab).  A
+    row planted into one tile of a normal matrix -- values that pass 2^15 from k = 256 on, a row
+    that is zero for its first slab, or one whose late values are tiny -- must leave every other
+    row bit-identical to the run without it (the event rescales only its own row), and be
+    accurate itself."""
     g = torch.Generator().manual_seed(5)
     M, K, N = 1000, 512, 384                 # the split kernel through its C entry point
     A = torch.randn(M, K, generator=g)

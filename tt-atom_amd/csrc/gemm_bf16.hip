@@ -309,16 +309,6 @@ __device__ __forceinline__ void split8_f16(const floatx4& x0, const floatx4& x1,
   out[1] = f16x8{l[0][0], l[0][1], l[1][0], l[1][1], l[2][0], l[2][1], l[3][0], l[3][1]};
 }
 
-// max(m, m of lane l ^ 32): v_permlane32_swap trades the upper half of one register with the
-// lower half of another, so with m in both, one of them ends up holding the partner's m in every
-// lane (a permute through LDS would wait on the fragment reads in flight).  The builtin, unlike
-// inline assembly, leaves the compiler free to schedule it (and to insert its wait states).
-__device__ __forceinline__ float row_max(float m) {
-  const unsigned b = __builtin_bit_cast(unsigned, m);
-  const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
-  return max3(m, __builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
-}
-
 // A (fp32) tile row: 8 chunks of 16 B per 32-wide k slab, chunk c of row r stored at c ^ aswz(r):
 // 16 consecutive rows at one logical chunk then cover all 64 banks.
 __device__ __forceinline__ int aswz(int row) { return (row >> 1) & 7; }
@@ -502,8 +492,16 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
         for (int c = 0; c < 2; ++c)
 #pragma unroll
           for (int e = 0; e < 4; ++e) m = max3_abs(x0[i][c][e], x1[i][c][e], m);
-        // the row's other 16 values of this k slab are in lane l ^ 32
-        m = row_max(m);
+        // the row's other 16 values of this k slab are in lane l ^ 32: v_permlane32_swap trades
+        // the upper half of one register with the lower half of another, so with m in both, one
+        // of them ends up holding the partner's m in every lane (a permute through LDS would wait
+        // on the fragment reads in flight).  s_nop 1: the two wait states the swap needs after
+        // the VALU writes of its operands.
+        {
+          float u = m, w = m;
+          asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(u), "+v"(w));
+          m = max3(m, u, w);
+        }
         const int e = m > 0.f ? __builtin_amdgcn_frexp_expf(m) : kNoExp;
         // values below 2^e reach 2^(e - E): a new shift once that passes 2^15, and for the row's
         // first nonzero slab (E = kNoExp); the new shift is never below the old one
@@ -531,48 +529,6 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
       }
     }
     return false;
-  };
-  // scale() for a tile's first slab: every row is unset and every accumulator still zero, so a
-  // row's first shift needs no rescaling (ldexp of zero is zero) and no branch.  Returns whether
-  // every row of the wave now has E = 0 (the fast loop's condition).
-  auto scale_first = [&](const floatx4 (&x0)[TI][2], const floatx4 (&x1)[TI][2]) -> bool {
-    bool all0 = true;
-    if constexpr (S::F16) {
-      bool u = true;
-#pragma unroll
-      for (int i = 0; i < TI; ++i) {
-        float m = 0.f;
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) m = max3_abs(x0[i][c][e], x1[i][c][e], m);
-        m = row_max(m);
-        const int e = __builtin_amdgcn_frexp_expf(m);
-        er[i] = m > 0.f ? ((e >= 0 && e <= 15) ? 0 : e - kTop) : kNoExp;
-        u &= er[i] == 0 || er[i] == kNoExp;
-        all0 &= er[i] == 0;
-      }
-      unscaled = __all(u);
-      all0 = __all(all0);
-    }
-    return all0;
-  };
-  // The fast loop's form of scale() for a wave whose rows all have E = 0: the only event of
-  // scale() there is a row's slab max reaching 2^15 (e - 0 > 15 for its frexp exponent e), and a
-  // row's max reaches it exactly when one of its two lanes' (l, l ^ 32) does.  Per slab the lane
-  // only folds its values into a running max mx (a branch per slab costs 5-9 % of the kernel's
-  // time, and so does mask logic on scalar registers); after the loop mx >= 2^15 makes the tile
-  // `bad`, and the caller computes it again on the checked path, whose results the fast loop's
-  // equal bit for bit whenever nothing is bad.
-  auto fast_track = [&](const floatx4 (&x0)[TI][2], const floatx4 (&x1)[TI][2], float (&mx)[TI]) {
-    if constexpr (S::F16) {
-#pragma unroll
-      for (int i = 0; i < TI; ++i)
-#pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) mx[i] = max3_abs(x0[i][c][e], x1[i][c][e], mx[i]);
-    }
   };
   // the split of an unscaled wave (every mode but a scaled mode-16 wave): no branch, so that the
   // scheduler can interleave it with the MFMAs of the other k half
@@ -622,16 +578,9 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   constexpr int RP = (BM * LDT <= SMEM_F) ? BM : (BM / 2 * LDT <= SMEM_F) ? BM / 2
                    : (BM / 4 * LDT <= SMEM_F) ? BM / 4 : 32;
   static_assert(RP % 32 == 0 && RP * LDT <= SMEM_F, "epilogue staging must fit the LDS buffer");
-  static_assert(!S::F16 || ((BM - 1) * LDT + BN >= 2 * STG * 4 && BM * LDT <= SMEM_F),
-                "the retry flags need staging padding beyond the copy stages");
 
   set_tile(tile);
   if (nk > 0) issue(0, 0);
-  // retry: this tile again on the checked path (its fast loop met a scale event it does not
-  // handle, in some wave); it goes round the tile loop once more without the epilogue, so that
-  // every copy is issued from the same few code sites (more sites make the compiler's LDS-DMA
-  // tracking give up and wait for every copy before each fragment read)
-  bool retry = false;
   for (;;) {
     const int cm0 = m0, cn0 = n0;  // the tile computed in this pass
 #pragma unroll
@@ -643,7 +592,6 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
 #pragma unroll
     for (int i = 0; i < TI; ++i) er[i] = kNoExp;
     unscaled = true;
-    bool bad = false;
     if (nk > 0) {
       issue(min(1, nk - 1), 1);
       // slab 0 landed (with everything issued before it: vector memory operations complete in
@@ -654,17 +602,14 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
       rdA(0, 0, x0);
       rdA(0, 1, x1);
       rdB(0, 0, cb);
-      const bool all0 = scale_first(x0, x1);
+      scale(x0, x1);
       sp(x0, ca);
       int kt = 0;
-      // Fast loop (K a multiple of 32 and every row of the wave at E = 0 after its first slab:
-      // every product here): no branch between a k half's MFMAs and the split of the next half,
-      // which the scheduler interleaves; the slab checks of fast_track are judged once at the end
-      // of the tile.  A wave with a scaled or still all-zero row runs the checked loop.
-      if (!retry && K % BK == 0 && (!S::F16 || all0)) {
-        float mx[TI];
-#pragma unroll
-        for (int i = 0; i < TI; ++i) mx[i] = 0.f;
+      // Fast loop (K a multiple of 32 and no row of the wave scaled: every product here): no
+      // branch between a k half's MFMAs and the split of the next half, which the scheduler
+      // interleaves.  x0 is split before its slab's shift check and split again in the rare case
+      // that the check rescales; a wave that acquires a nonzero shift finishes in the general loop.
+      if (K % BK == 0 && (!S::F16 || unscaled)) {
         for (; kt < nk; ++kt) {
           const int stg = kt & 1;
           rdB(stg, 1, nb);
@@ -677,10 +622,14 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
           rdB(stg ^ 1, 0, cb);
           mm(na, nb);
           sp_fast(x0, ca);
-          fast_track(x0, x1, mx);
+          if (scale(x0, x1)) {
+            sp(x0, ca);
+            if (S::F16 && !unscaled) {
+              ++kt;
+              break;
+            }
+          }
         }
-#pragma unroll
-        for (int i = 0; i < TI; ++i) bad = bad | (mx[i] >= 32768.f);
       }
       for (; kt < nk; ++kt) {
         const int stg = kt & 1;
@@ -696,23 +645,8 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
         scale(x0, x1);
         sp(x0, ca);
       }
-      // The fast loop's verdict is block-wide (every wave issues its share of the copies): one
-      // flag per wave in the padding columns of the epilogue's last staging row, which no copy
-      // and no staging store touches, written before the tile's last barrier and read after it.
-      // (__syncthreads_or, with its own LDS object, makes the compiler wait for every copy
-      // before each fragment read.)
-      int* flag = reinterpret_cast<int*>(smem) + (BM - 1) * LDT + BN;
-      const bool wave_bad = __any(bad);  // over all lanes, outside the one-lane store below
-      if (S::F16 && lane == 0) flag[wave] = wave_bad ? 1 : 0;
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if constexpr (S::F16) bad = (flag[0] | flag[1] | flag[2] | flag[3]) != 0;
     }
-    if (bad && !retry) {
-      retry = true;
-      issue(0, 0);
-      continue;
-    }
-    retry = false;
     const int next = tile + stride;
     const bool more = next < t_end;
     if constexpr (S::F16) {

@@ -263,6 +263,21 @@ def build_c5(torch, K=256):
     return cfg, w, bg, nl_ms
 
 
+def c5_cap_report(torch, cfg, bg, K=256):
+    """How the C5 graph relates to the reference's rule, which refuses a system with an atom of
+    sender or receiver degree above max_num_neighbors (disjoint.py:188-197): the degrees of the
+    uncapped graph and the edges the per-sender cap (assemble_orb(truncate=True)) dropped."""
+    from tt_atom import orb, synthetic
+    full = orb.assemble_orb(synthetic.c5_systems(K=K), cfg["cutoff"], 1 << 30, truncate=True)
+    n = int(full.pos.shape[0])
+    deg = max(int(torch.bincount(full.senders, minlength=n).max()),
+              int(torch.bincount(full.receivers, minlength=n).max()))
+    kept, total = int(bg.senders.numel()), int(full.senders.numel())
+    return {"max_num_neighbors": int(cfg["max_num_neighbors"]), "max_degree_uncapped": deg,
+            "edges_uncapped": total, "edges_kept": kept, "edges_dropped_by_cap": total - kept,
+            "reference_would_refuse": deg > int(cfg["max_num_neighbors"])}
+
+
 # Published small-batch throughputs of the reference (p150a card, bf16; docs/perf_baselines.json,
 # CHANGELOG.md:79-85): evaluate_batch end to end, systems per second.
 PUBLISHED_BATCH = {"uma-s-1 omol K=8 ethanol": 111.06617871436099,
@@ -824,7 +839,9 @@ def main():
     # secondary (C3 / C4): the step with the neighbour search in it -- device radius graph and a
     # topology comparison every step, then the replay (the topology does not change here) -- and
     # the cost of a step whose topology did change (new engine, first call launched eagerly)
-    nl_step_ms = topo_step_ms = direct_ms = None
+    nl_step_ms = topo_step_ms = direct_ms = cap_report = None
+    if wl == "c5":
+        cap_report = c5_cap_report(torch, cfg, bg)
     if wl == "c5" and not args.no_secondary:
         direct_ms = direct_c5_ms(torch, cfg, bg, args.precision, min(args.steps, 10))
     if wl in ("c3", "c4") and not args.no_secondary:
@@ -918,6 +935,7 @@ def main():
                    "ms_per_step_with_neighbor_search": nl_step_ms,
                    "ms_per_step_after_topology_change": topo_step_ms,
                    "direct_checkpoint_ms_per_step": direct_ms,
+                   "graph_cap": cap_report,
                    "energy": energy},
         "roofline": {"bound": "mfma", "kernel": KERNELS[dom],
                      "achieved": round(achieved, 3), "peak": round(PEAKS[dom], 2),

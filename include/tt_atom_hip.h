@@ -74,6 +74,17 @@ int tta_gemm_bf16x(const float* A, const void* Bp, float* C, const float* bias, 
  * blocks.  Same checks and results as one call per product;
  * empty products are skipped. */
 int tta_gemm_bf16x_group(const tta_gemm_problem* probs, int64_t n, int mode, tta_stream_t stream);
+/* tta_gemm_bf16x_group for launches too small to fill the GPU (the same call sites on small
+ * systems, where the fp32 kernel would otherwise run them at its matrix rate): when the products
+ * have fewer than 128 tiles of 128 x 128 in all, those with K >= 256 have their K cut into
+ * chunks of whole 32-wide slabs (at least 128); each chunk's partial product goes to work and a
+ * second launch sums the chunks in order and applies bias and epilogue.  No row-gather term.
+ * tta_gemm_bf16x_splitk_work returns the floats work (16-byte aligned) must hold (0: nothing
+ * splits; -1: bad list).  Deterministic; a product's k sums may be ordered differently than in
+ * another launch. */
+int64_t tta_gemm_bf16x_splitk_work(const tta_gemm_problem* probs, int64_t n);
+int tta_gemm_bf16x_group_splitk(const tta_gemm_problem* probs, int64_t n, int mode, float* work,
+                                int64_t work_floats, tta_stream_t stream);
 int tta_gemm_f32_group(const tta_gemm_problem* probs, int64_t n, tta_stream_t stream);
 /* tta_gemm_f32_group for launches too small to fill the GPU (the node- and edge-level linears
  * of small systems, the same call sites).  When the products have fewer than 160 tiles of

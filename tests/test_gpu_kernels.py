@@ -146,6 +146,76 @@ def test_gemm_splitk_group_bits(nat):
     assert (o1 - r1).abs().max() < 1e-4 * float(r1.abs().max())
 
 
+@pytest.mark.parametrize("epi", [0, 1, 2, 3, 4])
+def test_split_gemm_small_splitk(nat, epi):
+    """Small-M products of packed (mode 16) weights that would run unsplit on the fp32 kernel at
+    its matrix rate take the split kernel's split-K form: 576 x 1024 x 1024 (8 chunks of 128)
+    against fp64 at the split kernel's fp32-level accuracy, every epilogue, with rows scaled far
+    outside the unscaled window and a row whose values only start in the second chunk, and
+    bit-identical on a second call."""
+    g = torch.Generator().manual_seed(40 + epi)
+    M, N, K = 576, 1024, 1024
+    A = torch.randn(M, K, generator=g)
+    A[3] *= 2.0 ** 20
+    A[4] *= 2.0 ** -30
+    A[5, :200] = 0.0
+    A[6, 700:] *= 2.0 ** 17
+    B = torch.randn(K, N, generator=g) / math.sqrt(K)
+    bias, C0, aux = torch.randn(N, generator=g), torch.randn(M, N, generator=g), \
+        torch.randn(M, N, generator=g)
+    pw = nat.PackedWeight(B.to(DEV), nat.SPLIT_F16X3)
+    probs = (nat.GemmProblem * 1)(nat.GemmProblem(None, None, None, None, None, None, M, N, K,
+                                                  K, 0, N, epi))
+    assert nat.load().tta_gemm_bf16x_splitk_work(probs, 1) > 0
+    outs = []
+    for _ in range(2):
+        Cd, C2 = C0.clone().to(DEV), torch.zeros(M, N, device=DEV)
+        nat.linear(A.to(DEV), pw, bias.to(DEV), out=Cd, epilogue=epi, out2=C2, aux=aux.to(DEV))
+        torch.cuda.synchronize()
+        outs.append((Cd.cpu(), C2.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    ref = (A.double() @ B.double()) + bias.double()
+    mag = A.double().abs() @ B.double().abs() + bias.double().abs()
+    if epi == 1:
+        ref = torch.nn.functional.silu(ref)
+    elif epi == 2:
+        ref = ref + C0.double()
+        mag = mag + C0.double().abs()
+    elif epi == 4:
+        # the fp32 SiLU derivative itself is good to ~1e-7 absolute, which dominates where
+        # silu'(aux) nears its zero
+        s = torch.sigmoid(aux.double())
+        d = s * (1 + aux.double() * (1 - s))
+        ref, mag = ref * d, mag * (d.abs() + 0.05)
+    out = outs[0][0].double()
+    assert torch.isfinite(out).all()
+    assert ((out - ref).abs() / mag).max().item() < 2e-6
+    if epi == 3:
+        pre = (A.double() @ B.double()) + bias.double()
+        assert ((outs[0][1].double() - torch.nn.functional.silu(pre)).abs() / mag).max() < 2e-6
+
+
+def test_split_gemm_small_splitk_group(nat):
+    """An SO(2)-shaped group at 576 edges (the three m-block products, K = 768 / 1024 / 512)
+    through linear_group on the split kernel's split-K form, each product against fp64."""
+    g = torch.Generator().manual_seed(77)
+    M = 576
+    shapes = [(768, 640), (1024, 512), (512, 256)]
+    xs = [torch.randn(M, K, generator=g) for K, _ in shapes]
+    ws = [torch.randn(K, N, generator=g) / math.sqrt(K) for K, N in shapes]
+    pws = [nat.PackedWeight(w.to(DEV), nat.SPLIT_F16X3) for w in ws]
+    outs = [torch.full((M, N), float("nan"), device=DEV) for _, N in shapes]
+    probs = (nat.GemmProblem * 3)(*[nat.GemmProblem(None, None, None, None, None, None, M, N, K,
+                                                    K, 0, N, 0) for K, N in shapes])
+    assert nat.load().tta_gemm_bf16x_splitk_work(probs, 3) > 0
+    nat.linear_group([(x.to(DEV), pw, None, o) for x, pw, o in zip(xs, pws, outs)])
+    torch.cuda.synchronize()
+    for x, w, o in zip(xs, ws, outs):
+        ref = x.double() @ w.double()
+        mag = x.double().abs() @ w.double().abs()
+        assert ((o.cpu().double() - ref).abs() / mag).max().item() < 2e-6
+
+
 def test_gemm_batched_strided(nat):
     g = torch.Generator().manual_seed(5)
     N_, C, H = 50, 32, 24

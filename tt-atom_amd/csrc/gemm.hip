@@ -217,29 +217,6 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmGroup g) {
   }
 }
 
-// C = epi(sum of the product's k-chunk partials, in chunk order, + bias): the epilogue of
-// store_tiles on the split-K partials.  blockIdx.z selects the product, threads stride over its
-// M x N outputs.
-__global__ __launch_bounds__(256) void k_splitk_reduce(GemmGroup g) {
-  const GemmArgs& p = g.p[blockIdx.z];
-  const int64_t MN = (int64_t)p.M * p.N;
-  const int ns = (p.K + g.kch[blockIdx.z] - 1) / g.kch[blockIdx.z];
-  const float* W = g.work + g.woff[blockIdx.z];
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int row = (int)(i / p.N), col = (int)(i - (int64_t)row * p.N);
-    float v = ns > 0 ? W[i] : 0.f;  // K = 0: the epilogue of a zero product
-    for (int s = 1; s < ns; ++s) v += W[s * MN + i];
-    if (p.bias) v += p.bias[col];
-    const int64_t off = (int64_t)row * p.ldc + col;
-    if (p.epi == EPI_SILU) v = tta_silu(v);
-    if (p.epi == EPI_ACCUM) v += p.C[off];
-    if (p.epi == EPI_PRE_SILU) p.C2[off] = tta_silu(v);
-    if (p.epi == EPI_SILU_GRAD) v = v * tta_silu_grad(p.aux[off]);
-    p.C[off] = v;
-  }
-}
-
 // n products (group) or one product with `batch` strided copies (n == 1, group false).
 template <int BM, int BN, int WGM, int WGN, int BK>
 int launch(const GemmGroup& g, int n, bool group, int64_t batch, bool vec, hipStream_t s) {

@@ -136,6 +136,26 @@ __device__ __forceinline__ float epi_one(const GemmArgs& p, float v, int row, in
 // template parameter, so a row costs one LDS read, one address add and one 16-byte store.
 // vec_ok (host-checked 16-byte alignment of every operand row) selects the float4 path; full
 // (the tile lies inside M x N) drops the bounds checks.
+// Split-K: rows [row0, row0 + rows) of a staged tile, as they are, into the chunk's partial W
+// (row-major, row stride N, 16-byte aligned base); the reduction applies bias and epilogue.
+__device__ __forceinline__ void partial_rows(float* W, int M, int N, const float* Ct, int ldt,
+                                             int rows, int row0, int n0, int t, int nth) {
+  const int c4 = t & 31, rstep = nth >> 5;
+  const int col = n0 + 4 * c4;
+  if (col >= N) return;
+  for (int rr = t >> 5; rr < rows; rr += rstep) {
+    const int row = row0 + rr;
+    if (row >= M) break;
+    const floatx4 a = *reinterpret_cast<const floatx4*>(Ct + rr * ldt + 4 * c4);
+    float* w = W + (int64_t)row * N + col;
+    if (N % 4 == 0 && col + 3 < N) {
+      *reinterpret_cast<floatx4*>(w) = a;
+    } else {
+      for (int e = 0; e < 4 && col + e < N; ++e) w[e] = a[e];
+    }
+  }
+}
+
 template <int EPI, bool BATCH>
 __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct, int ldt,
                                               int rows, int row0, int n0, int t, int nth,
@@ -572,6 +592,12 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   // re-copies, never read) so every step issues the same copies.  A tile's slab 0 always sits in
   // stage 0, slab 1 in stage 1.
   const int nk = (K + BK - 1) / BK;
+  // k range of this block: slabs [kt0, kt1), all of K, or with split-K (g.work set) chunk
+  // blockIdx.y of g.kch[z] columns (a multiple of BK), whose partial product goes to g.work
+  const bool split = g.work != nullptr;
+  const int kt0 = split ? (int)blockIdx.y * (g.kch[blockIdx.z] / BK) : 0;
+  const int kt1 = split ? min(nk, kt0 + g.kch[blockIdx.z] / BK) : nk;
+  if (kt0 >= kt1 && split) return;
   const int* Fc =
       S::F16 ? reinterpret_cast<const int*>(Bp + (int64_t)nk * NB * NT32 * 128) : nullptr;
   constexpr int SMEM_F = SMEM_U4 * 4;
@@ -580,7 +606,7 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
   static_assert(RP % 32 == 0 && RP * LDT <= SMEM_F, "epilogue staging must fit the LDS buffer");
 
   set_tile(tile);
-  if (nk > 0) issue(0, 0);
+  if (kt1 > kt0) issue(kt0, 0);
   for (;;) {
     const int cm0 = m0, cn0 = n0;  // the tile computed in this pass
 #pragma unroll
@@ -592,8 +618,8 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
 #pragma unroll
     for (int i = 0; i < TI; ++i) er[i] = kNoExp;
     unscaled = true;
-    if (nk > 0) {
-      issue(min(1, nk - 1), 1);
+    if (kt1 > kt0) {
+      issue(min(kt0 + 1, kt1 - 1), 1);
       // slab 0 landed (with everything issued before it: vector memory operations complete in
       // order); slab 1 may still be in flight
       asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(APT + BPT) : "memory");
@@ -604,19 +630,19 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
       rdB(0, 0, cb);
       scale(x0, x1);
       sp(x0, ca);
-      int kt = 0;
+      int kt = kt0;
       // Fast loop (K a multiple of 32 and no row of the wave scaled: every product here): no
       // branch between a k half's MFMAs and the split of the next half, which the scheduler
       // interleaves.  x0 is split before its slab's shift check and split again in the rare case
       // that the check rescales; a wave that acquires a nonzero shift finishes in the general loop.
       if (K % BK == 0 && (!S::F16 || unscaled)) {
-        for (; kt < nk; ++kt) {
-          const int stg = kt & 1;
+        for (; kt < kt1; ++kt) {
+          const int stg = (kt - kt0) & 1;
           rdB(stg, 1, nb);
           mm(ca, cb);
           sp_fast(x1, na);
           asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-          issue_full(min(kt + 2, nk - 1), stg);
+          issue_full(min(kt + 2, kt1 - 1), stg);
           rdA(stg ^ 1, 0, x0);
           rdA(stg ^ 1, 1, x1);
           rdB(stg ^ 1, 0, cb);
@@ -631,13 +657,13 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
           }
         }
       }
-      for (; kt < nk; ++kt) {
-        const int stg = kt & 1;
+      for (; kt < kt1; ++kt) {
+        const int stg = (kt - kt0) & 1;
         rdB(stg, 1, nb);
         mm(ca, cb);
         sp(x1, na);
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        issue(min(kt + 2, nk - 1), stg);
+        issue(min(kt + 2, kt1 - 1), stg);
         rdA(stg ^ 1, 0, x0);
         rdA(stg ^ 1, 1, x1);
         rdB(stg ^ 1, 0, cb);
@@ -683,7 +709,10 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
               Ct[(rt + crow(r)) * LDT + cbase + j * 32 + l32] = acc[i][j][r];
         }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        switch (p.epi) {
+        if (split) {
+          partial_rows(g.work + g.woff[blockIdx.z] + (int64_t)blockIdx.y * p.M * p.N, p.M, p.N,
+                       Ct, LDT, RP, cm0 + r0, cn0, t, NTH);
+        } else switch (p.epi) {
           case EPI_SILU:
             epilogue_rows<EPI_SILU, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
             break;
@@ -705,7 +734,7 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
     if (!more) break;
     tile = next;
     set_tile(tile);
-    if (nk > 0) issue(0, 0);
+    if (kt1 > kt0) issue(kt0, 0);
   }
 }
 
@@ -1083,7 +1112,7 @@ int persistent_cap() {
 }
 
 template <int WM, int MODE>
-int launch_bf16x(GemmGroup& g, int n, hipStream_t s) {
+int launch_bf16x(GemmGroup& g, int n, hipStream_t s, unsigned chunks = 1) {
   int64_t grid = 0;
   g.cap = persistent_cap();
   for (int i = 0; i < n; ++i) {
@@ -1094,7 +1123,7 @@ int launch_bf16x(GemmGroup& g, int n, hipStream_t s) {
     }
     grid = std::max(grid, std::min<int64_t>(((ntiles + 7) / 8) * 8, g.cap));
   }
-  hipLaunchKernelGGL((gemm_bf16x_kernel<WM, MODE>), dim3((unsigned)grid, 1, (unsigned)n),
+  hipLaunchKernelGGL((gemm_bf16x_kernel<WM, MODE>), dim3((unsigned)grid, chunks, (unsigned)n),
                      dim3(128 * WM), 0, s, g);
   TTA_CHECK_LAUNCH("tta_gemm_bf16x");
   return tta::kOk;
@@ -1106,13 +1135,43 @@ bool vec_ok_of(const GemmArgs& p) {
          (!p.P || (al(p.P) && p.ldp % 4 == 0 && p.off1 % 4 == 0));
 }
 
-int launch_mode(GemmGroup& g, int n, int mode, hipStream_t s) {
+int launch_mode(GemmGroup& g, int n, int mode, hipStream_t s, unsigned chunks = 1) {
+  if (chunks > 1) {  // split-K: the tiled kernel (the panel kernel takes K <= 128 only)
+    switch (mode) {
+      case 1: return launch_bf16x<2, 1>(g, n, s, chunks);
+      case 3: return launch_bf16x<2, 3>(g, n, s, chunks);
+      case 16: return launch_bf16x<2, 16>(g, n, s, chunks);
+      default: return launch_bf16x<2, 6>(g, n, s, chunks);
+    }
+  }
   switch (mode) {
     case 1: return launch_bf16x<2, 1>(g, n, s);
     case 3: return launch_bf16x<2, 3>(g, n, s);
     case 16: return panel_ok(g, n) ? launch_panel(g, n, s) : launch_bf16x<2, 16>(g, n, s);
     default: return launch_bf16x<2, 6>(g, n, s);
   }
+}
+
+// Split-K of the tiled kernel for launches too small to fill the GPU (the linears of small
+// systems): when the products have fewer than 128 tiles of 128 x 128 in all, those with K >= 256
+// have their K cut into chunks of whole 32-wide slabs (at least 128 columns) aiming at about 512
+// workgroups; each chunk's partial product (scales undone) goes to the workspace and
+// k_splitk_reduce sums the chunks in order and applies bias and epilogue.  The decision belongs
+// to the launch (a product's k sums may be ordered differently in another launch).
+int64_t bf16x_splitk_tiles(const tta_gemm_problem* probs, int64_t n) {
+  int64_t tiles = 0;
+  for (int64_t i = 0; i < n; ++i)
+    if (probs[i].M > 0 && probs[i].N > 0)
+      tiles += tta_blocks(probs[i].M, 128) * tta_blocks(probs[i].N, BN);
+  return tiles;
+}
+
+int64_t bf16x_splitk_chunk(int64_t K, int64_t tiles) {
+  const int64_t one = std::max<int64_t>(BK, (K + BK - 1) / BK * BK);  // all slabs in one chunk
+  if (K < 256 || tiles >= 128) return one;
+  const int64_t chunks = std::min<int64_t>((512 + tiles - 1) / tiles, K / 128);
+  if (chunks < 2) return one;
+  return ((K + chunks - 1) / chunks + BK - 1) / BK * BK;
 }
 
 int planes_of(int mode) {
@@ -1230,4 +1289,70 @@ extern "C" int tta_gemm_bf16x_group(const tta_gemm_problem* probs, int64_t n, in
   }
   if (m == 0) return tta::kOk;
   return launch_mode(g, m, mode, stream);
+}
+
+// Workspace of tta_gemm_bf16x_group_splitk in floats: the sum over products of
+// ceil(K / chunk) * M * N when some product takes more than one chunk, else 0 (nothing to gain
+// over tta_gemm_bf16x_group); -1 for a bad list.
+extern "C" int64_t tta_gemm_bf16x_splitk_work(const tta_gemm_problem* probs, int64_t n) {
+  if (n < 0 || n > kMaxGroup || (!probs && n > 0)) return -1;
+  const int64_t tiles = bf16x_splitk_tiles(probs, n);
+  int64_t need = 0;
+  bool split = false;
+  for (int64_t i = 0; i < n; ++i) {
+    const tta_gemm_problem& q = probs[i];
+    if (q.M <= 0 || q.N <= 0 || q.K <= 0) continue;
+    const int64_t kc = bf16x_splitk_chunk(q.K, tiles);
+    const int64_t chunks = (q.K + kc - 1) / kc;
+    split = split || chunks > 1;
+    need += (chunks * q.M * q.N + 3) / 4 * 4;  // each product's partials 16-byte aligned
+  }
+  return split ? need : 0;
+}
+
+// tta_gemm_bf16x_group with the k chunks of tta_gemm_bf16x_splitk_work (no row gathers).
+extern "C" int tta_gemm_bf16x_group_splitk(const tta_gemm_problem* probs, int64_t n, int mode,
+                                           float* work, int64_t work_floats,
+                                           hipStream_t stream) {
+  TTA_CHECK_ARG(planes_of(mode) > 0,
+                "tta_gemm_bf16x_group_splitk: mode must be 1, 3, 6 or 16 (got %d)", mode);
+  TTA_CHECK_ARG(n >= 0 && n <= kMaxGroup && (probs || n == 0),
+                "tta_gemm_bf16x_group_splitk: 0..%d products", kMaxGroup);
+  GemmGroup g{};
+  int m = 0;
+  const int64_t tiles = bf16x_splitk_tiles(probs, n);
+  int64_t need = 0, max_chunks = 1, max_mn = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const tta_gemm_problem& q = probs[i];
+    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= 4,
+                  "tta_gemm_bf16x_group_splitk: bad epilogue");
+    bool skip = false;
+    const int rc = prepare_bf16x(q.A, q.B, q.C, q.bias, q.C2, q.aux, q.M, q.N, q.K, q.lda, q.ldc,
+                                 nullptr, 0, nullptr, nullptr, 0, 0, (int)q.epilogue, g, m,
+                                 &skip);
+    if (rc != tta::kOk) return rc;
+    if (skip) continue;
+    TTA_CHECK_ARG(q.K > 0, "tta_gemm_bf16x_group_splitk: K must be positive");
+    const int64_t kc = bf16x_splitk_chunk(q.K, tiles);
+    const int64_t chunks = (q.K + kc - 1) / kc;
+    g.kch[m] = (int)kc;
+    g.woff[m] = need;
+    need += (chunks * q.M * q.N + 3) / 4 * 4;  // each product's partials 16-byte aligned
+    max_chunks = std::max(max_chunks, chunks);
+    max_mn = std::max(max_mn, q.M * q.N);
+    ++m;
+  }
+  if (m == 0) return tta::kOk;
+  TTA_CHECK_ARG(work && work_floats >= need && (uintptr_t)work % 16 == 0,
+                "tta_gemm_bf16x_group_splitk: work holds %lld floats (16-byte aligned), needs "
+                "%lld", (long long)work_floats, (long long)need);
+  TTA_CHECK_ARG(max_chunks <= 65535, "tta_gemm_bf16x_group_splitk: too many chunks");
+  if (max_chunks == 1) return launch_mode(g, m, mode, stream);  // nothing splits: direct
+  g.work = work;
+  const int rc = launch_mode(g, m, mode, stream, (unsigned)max_chunks);
+  if (rc != tta::kOk) return rc;
+  const int64_t rb = std::min<int64_t>((max_mn + 255) / 256, 2048);
+  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)rb, 1, (unsigned)m), dim3(256), 0, stream, g);
+  TTA_CHECK_LAUNCH("tta_gemm_bf16x_group_splitk");
+  return tta::kOk;
 }

@@ -94,6 +94,8 @@ _SIGS = {
     "tta_gemm_bf16x_group": [ctypes.POINTER(GemmProblem), _I64, _I, _P],
     "tta_gemm_f32_group": [ctypes.POINTER(GemmProblem), _I64, _P],
     "tta_gemm_f32_splitk_work": [ctypes.POINTER(GemmProblem), _I64],
+    "tta_gemm_bf16x_splitk_work": [ctypes.POINTER(GemmProblem), _I64],
+    "tta_gemm_bf16x_group_splitk": [ctypes.POINTER(GemmProblem), _I64, _I, _P, _I64, _P],
     "tta_gemm_f32_group_splitk": [ctypes.POINTER(GemmProblem), _I64, _P, _I64, _P],
     "tta_radius_graph_thresholds": [_P, _I64, _P, _P, _P, _I64, _P, _P, _I, _D, _F, _F, _I, _P,
                                     _P, _P, _P, _P],
@@ -111,7 +113,8 @@ _SIGS = {
                                      _D, _F, _F, _P, _P, _P, _P, _P, _P, _P, _P, _P],
 }
 _RESTYPE = {"tta_last_error": ctypes.c_char_p, "tta_pack_b_elems": ctypes.c_int64,
-            "tta_cell_list_workspace": ctypes.c_int64, "tta_gemm_f32_splitk_work": ctypes.c_int64}
+            "tta_cell_list_workspace": ctypes.c_int64, "tta_gemm_f32_splitk_work": ctypes.c_int64,
+            "tta_gemm_bf16x_splitk_work": ctypes.c_int64}
 
 EXPORTS = tuple(_SIGS)
 
@@ -328,13 +331,62 @@ def _gemm_bf16x(x, pw, out, bias, epilogue, out2, aux, P=None, idx0=None, idx1=N
         probe.after()
 
 
-def _split_ok(x, pw):
+def _split_ok(x, pw, min_rows=4096):
     """The split kernel (128 x 128 x 32 tiles) runs edge-level GEMMs; short-K or small-M
-    products stay on the fp32 MFMA kernel, whose smaller tiles fill the chip better there."""
+    products stay on the fp32 MFMA kernel, whose smaller tiles fill the chip better there
+    (small-M products of packed weights may take the split kernel's split-K form instead:
+    ``_small_split``)."""
     M, K = x.shape
-    return (isinstance(pw, PackedWeight) and pw.packed is not None and M >= 4096 and K >= 128
-            and K % 4 == 0 and x.data_ptr() % 16 == 0 and _ld(x, "x") % 4 == 0
+    return (isinstance(pw, PackedWeight) and pw.packed is not None and M >= min_rows
+            and K >= 128 and K % 4 == 0 and x.data_ptr() % 16 == 0 and _ld(x, "x") % 4 == 0
             and _ld(x, "x") < (1 << 21))
+
+
+def _fp32_tiles(shapes):
+    return sum(-(-M // 32) * -(-N // 64) for M, N in shapes)
+
+
+def _small_split(items):
+    """items = [(x, PackedWeight, bias, out, epilogue, out2, aux)] of products with M < 4096:
+    the split kernel's split-K launch (tta_gemm_bf16x_group_splitk) when the fp32 kernel would run
+    them unsplit at its matrix rate (160 or more of its 32 x 64 tiles in all: its split-K form
+    takes smaller launches) and the split kernel's rule splits them.  Returns False, having
+    launched nothing, otherwise."""
+    if not all(isinstance(w, PackedWeight) and w.packed is not None and w.mode == items[0][1].mode
+               and x.shape[0] < 4096 and x.shape[1] >= 256 and _split_ok(x, w, min_rows=1)
+               for x, w, *_ in items):
+        return False
+    if _fp32_tiles([(x.shape[0], w.shape[1]) for x, w, *_ in items]) < 160:
+        return False
+    probs = (GemmProblem * len(items))()
+    flops = nbytes = 0.0
+    for i, (x, w, bias, out, epi, out2, aux) in enumerate(items):
+        M, K = x.shape
+        N = w.shape[1]
+        ldc = _ld(out, "out")
+        probs[i] = GemmProblem(
+            _rows(x, M, _ld(x, "x"), K, "x"), w.packed.data_ptr(), _rows(out, M, ldc, N, "out"),
+            None if bias is None else _ptr(bias, numel=N, name="bias"),
+            None if out2 is None else _rows(out2, M, _ld(out2, "out2"), N, "out2"),
+            None if aux is None else _rows(aux, M, _ld(aux, "aux"), N, "aux"),
+            M, N, K, _ld(x, "x"), 0, ldc, epi)
+        flops += 2.0 * M * N * K
+        nbytes += 4.0 * (M * K + K * N + (1 + (epi in (EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD)))
+                         * M * N)
+    need = load().tta_gemm_bf16x_splitk_work(probs, len(items))
+    if need < 0:
+        raise RuntimeError("tta_gemm_bf16x_splitk_work: bad product list")
+    if need == 0:
+        return False
+    work = torch.empty(need, device=items[0][0].device, dtype=torch.float32)
+    probe = _gemm_probe
+    if probe is not None:
+        probe.before(flops, nbytes, MODE_KIND[items[0][1].mode])
+    _call("tta_gemm_bf16x_group_splitk", probs, len(items), items[0][1].mode, work.data_ptr(),
+          work.numel(), _stream())
+    if probe is not None:
+        probe.after()
+    return True
 
 
 def _gemm_f32_splitk(items):
@@ -388,6 +440,8 @@ def linear(x, w_t, bias=None, out=None, epilogue=EPI_STORE, out2=None, aux=None)
         if _split_ok(x, w_t):
             _gemm_bf16x(x, w_t, out, bias, epilogue, out2, aux)
             return out
+        if _small_split([(x, w_t, bias, out, epilogue, out2, aux)]):
+            return out
         w_t = w_t.w_t
     if M < 4096 and K >= 256 and _gemm_f32_splitk([(x, w_t, bias, out, epilogue, out2, aux)]):
         return out
@@ -414,6 +468,8 @@ def linear_group(items):
     if len(items) > MAX_GROUP or (any(split) and not all(split)) or len(modes) > 1:
         for x, w, bias, out, epi, out2, aux in items:
             linear(x, w, bias, out, epi, out2, aux)
+        return
+    if not any(split) and _small_split(items):
         return
     if not split[0] and any(x.shape[1] >= 256 for x, *_ in items) and _gemm_f32_splitk(
             [(x, w.w_t if isinstance(w, PackedWeight) else w, *rest) for x, w, *rest in items]):

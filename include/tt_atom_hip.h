@@ -38,7 +38,7 @@ int tta_check_device(char* name_out, int64_t name_len);
 /* ---------------------------------------------------------------- dense contractions (MFMA)
  * C[b] = epi(A[b] @ B[b] + bias[b]); A [M,K] (lda), B [K,N] (ldb), C [M,N] (ldc), batch
  * strides sA/sB/sC/sBias.  epilogue: 0 store, 1 silu, 2 accumulate, 3 store v and silu(v) to
- * C2, 4 store v * silu'(aux).
+ * C2, 4 store v * silu'(aux), 5 sigmoid (6: the gate, tta_gemm_bf16x_group_gate only).
  * Replaces the ttnn.linear / ttnn.matmul calls of so2.py:106-115, 282-294 (SO(2) m-block GEMMs
  * with the [[Wa,Wb],[-Wb,Wa]] fused weight of so2.py:230-253), forces.py:23-36 (_mm transpose
  * GEMMs of the VJP), spectral.py:176-187, grid.py:64-75 and model.py:223-231 (energy head). */
@@ -85,6 +85,19 @@ int tta_gemm_bf16x_group(const tta_gemm_problem* probs, int64_t n, int mode, tta
 int64_t tta_gemm_bf16x_splitk_work(const tta_gemm_problem* probs, int64_t n);
 int tta_gemm_bf16x_group_splitk(const tta_gemm_problem* probs, int64_t n, int mode, float* work,
                                 int64_t work_floats, tta_stream_t stream);
+/* An SO(2) convolution's coefficient products with the gate of its output applied as they are
+ * written (activation.py:53-70 after so2.py:282-294): every product has epilogue 6, and product
+ * i's output column j is channel j % H of SH coefficient c0[i] + j / H (N a multiple of H,
+ * coefficients up to 8).  Coefficient 0: C = silu(v), and v (bias included) is stored to x0
+ * (rows of stride ldx0, H wide); coefficient c > 0: C = v sig[row, idx8[c-1] H + h], sig being
+ * the sigmoid of the convolution's gating columns (rows of stride ldg; an earlier launch with
+ * epilogue 5).  C equals tta_gate_fwd applied to the ungated products bit for bit; C, bias,
+ * sig and x0 16-byte aligned with row strides and H multiples of 4.  work / work_floats as for
+ * tta_gemm_bf16x_group_splitk (size from tta_gemm_bf16x_splitk_work); work NULL: never split. */
+int tta_gemm_bf16x_group_gate(const tta_gemm_problem* probs, int64_t n, int mode,
+                              const int64_t* c0, const float* sig, int64_t ldg, float* x0,
+                              int64_t ldx0, int64_t H, const int* idx8, float* work,
+                              int64_t work_floats, tta_stream_t stream);
 int tta_gemm_f32_group(const tta_gemm_problem* probs, int64_t n, tta_stream_t stream);
 /* tta_gemm_f32_group for launches too small to fill the GPU (the node- and edge-level linears
  * of small systems, the same call sites).  When the products have fewer than 160 tiles of
@@ -168,7 +181,9 @@ int tta_node_gather_sum_dst(const float* g_mcat, const int* src_ptr, const int* 
 /* ---------------------------------------------------------------- element / row-wise
  * Gate: y[r,0] = silu(x[r,0]); y[r,c] = x[r,c] sigmoid(gating[r, idx8[c-1]]).  x [R,9,H] rows of
  * stride ldx, gating [R, L*H] rows of stride ldg (column blocks of one GEMM output allowed),
- * y / g_y contiguous [R,9,H]; g_x / g_gating share the strides of x / gating.
+ * y / g_y contiguous [R,9,H]; g_x / g_gating share the strides of x / gating.  idx8: 8 ints in
+ * host memory (read while the launch is built; likewise for tta_gate_bwd_y and
+ * tta_gemm_bf16x_group_gate).
  * activation.py:29-70 (m-primed idx), spectral.py:129-144 (natural idx); backward
  * forces.py:104-130 (and ttnn.experimental.fused_gate, fused_gate.hpp:14-21). */
 int tta_gate_fwd(const float* x, const float* gating, float* y, int64_t R, int64_t H, int64_t L,
@@ -176,6 +191,15 @@ int tta_gate_fwd(const float* x, const float* gating, float* y, int64_t R, int64
 int tta_gate_bwd(const float* g_y, const float* x, const float* gating, float* g_x,
                  float* g_gating, int64_t R, int64_t H, int64_t L, int64_t ldx, int64_t ldg,
                  const int* idx8, tta_stream_t stream);
+/* The gate backward (forces.py:104-130) from the gated output y of tta_gemm_bf16x_group_gate
+ * instead of its input x: g_x[0] = g_y[0] silu'(x0), g_x[c] = g_y[c] sig[t_c],
+ * g_gating[t] = (1 - sig[t]) sum of g_y[c] y[c] over the coefficients of index t (equal to
+ * tta_gate_bwd's sigmoid'(gating) sum g_y x up to fp32 rounding).  sig = sigmoid(gating).
+ * g_y, y contiguous [R,9,H]; sig, x0, g_x and g_gating rows of strides ldg, ldx0, ldgx, ldgg. */
+int tta_gate_bwd_y(const float* g_y, const float* y, const float* sig, const float* x0,
+                   float* g_x, float* g_gating, int64_t R, int64_t H, int64_t L, int64_t ldg,
+                   int64_t ldx0, int64_t ldgx, int64_t ldgg, const int* idx8,
+                   tta_stream_t stream);
 
 /* Radial MLP LayerNorm + SiLU: nrm = LN(a), s = silu(nrm) (so2.py:101-115) and its backward
  * g_a (so2.py:117-143; ttnn.experimental.fused_ln_bw, fused_ln_bw.hpp:14-21).  Row strides:

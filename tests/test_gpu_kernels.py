@@ -759,6 +759,110 @@ def test_gate_fwd_bwd(nat, natural):
     assert torch.equal(gcomb[:, 2 * H:].reshape(R, 9, H), gxo) and torch.equal(gcomb[:, :2 * H], ggo)
 
 
+def _conv1_case(M, H, cin, seed):
+    """Operands of an SO(2) conv-1 at channel width cin: x rows of the three m-blocks (3, 4 and 2
+    coefficients of 2 cin), the m = 0 weight [3 cin, 2 H + 3 H] with its gating columns first,
+    the m = 1 and m = 2 weights, the m = 0 bias."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, 9 * 2 * cin, generator=g)
+    x[5] *= 2.0 ** 18                      # a row far outside the unscaled window
+    wm0 = torch.randn(3 * 2 * cin, 5 * H, generator=g) / math.sqrt(6 * cin)
+    w1 = torch.randn(4 * 2 * cin, 4 * H, generator=g) / math.sqrt(8 * cin)
+    w2 = torch.randn(2 * 2 * cin, 2 * H, generator=g) / math.sqrt(4 * cin)
+    bm0 = torch.randn(5 * H, generator=g)
+    return x, wm0, w1, w2, bm0
+
+
+@pytest.mark.parametrize("mode,M", [(16, 5000), (1, 5000), (16, 700)])
+def test_gemm_gate_epilogue(nat, mode, M):
+    """The gate applied in the SO(2) conv-1 products' epilogue (tta_gemm_bf16x_group_gate, m-primed
+    gate table, H = 48 so that 128-column tiles straddle coefficients) after the gating columns'
+    sigmoid epilogue: at M = 5000 (direct launches, ragged last row tile) the gated rows and
+    coefficient 0's pre-activation equal the ungated launch followed by tta_gate_fwd bit for bit,
+    the sigmoids match; at M = 700 (split-K, the gate applied in the reduction) all of them match
+    fp64 at fp32-GEMM accuracy."""
+    H, cin, L = 48, 32, 2
+    x, wm0, w1, w2, bm0 = _conv1_case(M, H, cin, 60 + mode + M)
+    idx = (0, 1, 0, 1, 0, 1, 1, 1)
+    P = lambda w: nat.PackedWeight(w.to(DEV).contiguous(), mode)
+    xd = x.to(DEV)
+    k0, k1 = 3 * 2 * cin, 7 * 2 * cin
+    # fused: the gating sigmoids, then the gated coefficient products
+    sig = torch.empty(M, L * H, device=DEV)
+    y = torch.full((M, 9 * H), float("nan"), device=DEV)
+    x0 = torch.full((M, H), float("nan"), device=DEV)
+    nat.linear(xd[:, :k0], P(wm0[:, :L * H]), bm0[:L * H].to(DEV), out=sig,
+               epilogue=nat.EPI_SIGMOID)
+    nat.linear_group_gate([(xd[:, :k0], P(wm0[:, L * H:]), bm0[L * H:].to(DEV), y[:, :3 * H]),
+                           (xd[:, k0:k1], P(w1), None, y[:, 3 * H:7 * H]),
+                           (xd[:, k1:], P(w2), None, y[:, 7 * H:])], (0, 3, 7), sig, x0, idx, H)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all() and torch.isfinite(x0).all()
+    if M >= 4096:
+        o1 = torch.empty(M, L * H + 9 * H, device=DEV)
+        nat.linear_group([(xd[:, :k0], P(wm0), bm0.to(DEV), o1[:, :L * H + 3 * H]),
+                          (xd[:, k0:k1], P(w1), None, o1[:, L * H + 3 * H:L * H + 7 * H]),
+                          (xd[:, k1:], P(w2), None, o1[:, L * H + 7 * H:])])
+        yr = torch.empty(M, 9, H, device=DEV)
+        nat.gate_fwd(o1[:, L * H:], o1, yr, idx, R=M, H=H, L=L, ldx=L * H + 9 * H,
+                     ldg=L * H + 9 * H)
+        torch.cuda.synchronize()
+        assert (sig.cpu().double() - torch.sigmoid(o1[:, :L * H].cpu().double())).abs().max() < 3e-7
+        assert torch.equal(x0, o1[:, L * H:L * H + H])
+        assert torch.equal(y, yr.view(M, 9 * H))
+        return
+    xd64 = x.double()
+    pre = torch.cat([xd64[:, :k0] @ wm0.double() + bm0.double(), xd64[:, k0:k1] @ w1.double(),
+                     xd64[:, k1:] @ w2.double()], 1)
+    mag = torch.cat([xd64[:, :k0].abs() @ wm0.double().abs() + bm0.double().abs(),
+                     xd64[:, k0:k1].abs() @ w1.double().abs(),
+                     xd64[:, k1:].abs() @ w2.double().abs()], 1)
+    gpre, cpre = pre[:, :L * H], pre[:, L * H:].view(M, 9, H)
+    sg = torch.sigmoid(gpre).view(M, L, H)[:, list(idx), :]
+    yref = torch.cat([torch.nn.functional.silu(cpre[:, :1]), cpre[:, 1:] * sg], 1)
+    cmag = mag[:, L * H:].view(M, 9, H)
+    # sigmoid' <= 1/4: the sigmoid's error is at most a quarter of its argument's
+    assert ((sig.cpu().double() - torch.sigmoid(gpre)).abs() / mag[:, :L * H]).max() < 2e-6
+    assert ((x0.cpu().double() - cpre[:, 0]).abs() / cmag[:, 0]).max() < 2e-6
+    assert ((y.cpu().double().view(M, 9, H) - yref).abs() / cmag).max() < 4e-6
+
+
+def test_gate_bwd_from_output(nat):
+    """tta_gate_bwd_y (the gate backward from the gated output, the gating sigmoids and
+    coefficient 0's pre-activation) against tta_gate_bwd (from the gate's input) and fp64
+    autograd, on strided operand views: coefficient 0's adjoint bit for bit, the rest to fp32
+    rounding (the sigmoids come from torch here)."""
+    R, H, L = 300, 48, 2
+    idx = (0, 1, 0, 1, 0, 1, 1, 1)
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(R, 9, H, generator=g, dtype=torch.float64)
+    gat = torch.randn(R, L * H, generator=g, dtype=torch.float64)
+    gy = torch.randn(R, 9, H, generator=g, dtype=torch.float64)
+    xr, gr = x.clone().requires_grad_(True), gat.clone().requires_grad_(True)
+    sg = torch.sigmoid(gr).view(R, L, H)[:, list(idx), :]
+    yy = torch.cat([torch.nn.functional.silu(xr[:, :1]), xr[:, 1:] * sg], 1)
+    gx_ref, gg_ref = torch.autograd.grad((yy * gy).sum(), [xr, gr])
+    f = lambda t: t.float().to(DEV).contiguous()
+    y = torch.empty(R, 9, H, device=DEV)
+    nat.gate_fwd(f(x), f(gat), y, idx, R=R, H=H, L=L)
+    gxo, ggo = torch.empty(R, 9, H, device=DEV), torch.empty(R, L * H, device=DEV)
+    nat.gate_bwd(f(gy), f(x), f(gat), gxo, ggo, idx, R=R, H=H, L=L)
+    # the new kernel's operands as column blocks of wider rows
+    sig_w = torch.zeros(R, L * H + 8, device=DEV)
+    sig_w[:, 4:4 + L * H] = torch.sigmoid(f(gat))
+    x0_w = torch.zeros(R, 2 * H, device=DEV)
+    x0_w[:, H:] = f(x[:, 0])
+    g1 = torch.full((R, L * H + 9 * H), float("nan"), device=DEV)
+    nat.gate_bwd_y(f(gy), y, sig_w[:, 4:4 + L * H], x0_w[:, H:], g1[:, L * H:], g1[:, :L * H],
+                   idx, R=R, H=H, L=L)
+    torch.cuda.synchronize()
+    gxn = g1[:, L * H:].view(R, 9, H)
+    assert torch.equal(gxn[:, 0], gxo[:, 0])
+    assert (gxn - gxo).abs().max() < 1e-6
+    gg = g1[:, :L * H].cpu().double()
+    assert (gg - ggo.cpu().double()).abs().max() < 1e-6
+    assert (gg - gg_ref).abs().max() < 1e-5
+    assert (gxn.cpu().double() - gx_ref).abs().max() < 1e-5
 @pytest.mark.parametrize("n", [16, 64, 100, 128, 200, 256, 512])
 def test_ln_silu_fwd_bwd(nat, n):
     R = 301                     # odd: the last two-row wavefront of short rows has one row

@@ -14,16 +14,17 @@ pytestmark = pytest.mark.gpu
 E_REL, F_ABS, S_ABS = 1e-6, 1e-4, 1e-5
 
 
-def _engine(w, cfg, host, Z, ei, se, shift=None):
+def _engine(w, cfg, host, Z, ei, se, shift=None, precision="f32"):
     from tt_atom import geometry, model, trace
-    bb = model.Backbone(w, "cuda", cfg, host.get("to_grid_mat"), host.get("from_grid_mat"))
+    bb = model.Backbone(w, "cuda", cfg, host.get("to_grid_mat"), host.get("from_grid_mat"),
+                        precision=precision)
     geo = geometry.HostGeometry(w, cfg, host["to_m"], host["gauss_offset"], host["gauss_coeff"],
                                 device="cuda")
     return trace.TracedEngine(bb, geo, Z, ei, se, edge_cell_shift=shift)
 
 
-def _check(w, cfg, host, pos, Z, ei, se, shift=None, cell=None, label=""):
-    eng = _engine(w, cfg, host, Z, ei, se, shift)
+def _check(w, cfg, host, pos, Z, ei, se, shift=None, cell=None, label="", precision="f32"):
+    eng = _engine(w, cfg, host, Z, ei, se, shift, precision)
     stress = cell is not None
     out = eng(pos.cuda(), compute_stress=stress)
     torch.cuda.synchronize()
@@ -74,7 +75,10 @@ def _system_embedding(w, cfg, n, charge=0, spin=1):
     return se.expand(n, -1).contiguous()
 
 
-def test_c1_tiny(golden):
+@pytest.mark.parametrize("precision", ["f32", "f32-mfma"])
+def test_c1_tiny(golden, precision):
+    """C1 with packed weights (the gate applied in the conv-1 products' epilogue) and with the
+    fp32 MFMA kernel only (ungated conv-1 output, then the gate pass)."""
     from tt_atom import synthetic
     from tt_atom.geometry import radius_graph
     cfg = dict(synthetic.CFG_C1)
@@ -84,7 +88,9 @@ def test_c1_tiny(golden):
     pos, Z = synthetic.c1_system()
     pos, Z = torch.from_numpy(pos), torch.from_numpy(Z)
     ei, _ = radius_graph(pos, cfg["cutoff"], max_neighbors=cfg["max_neighbors"])
-    _check(w, cfg, host, pos, Z, ei, _system_embedding(w, cfg, len(Z)), label="C1")
+    eng, _ = _check(w, cfg, host, pos, Z, ei, _system_embedding(w, cfg, len(Z)),
+                    label=f"C1 {precision}", precision=precision)
+    assert all(b.so2_1.gate_split == (precision == "f32") for b in eng.bb.blocks)
 
 
 def test_c3_reduced():

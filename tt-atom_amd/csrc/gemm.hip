@@ -278,7 +278,7 @@ int check(GemmArgs& p, int64_t M, int64_t N, int64_t K, int64_t batch, const cha
   TTA_CHECK_ARG(M < (int64_t)1 << 31 && N < (int64_t)1 << 31 && K < (int64_t)1 << 31,
                 "%s: size exceeds int32", name);
   TTA_CHECK_ARG(tta_blocks(M, 32) <= 65535 && batch <= 65535, "%s: grid too large", name);
-  TTA_CHECK_ARG(p.epi >= 0 && p.epi <= 4, "%s: bad epilogue %d", name, p.epi);
+  TTA_CHECK_ARG(p.epi >= 0 && p.epi <= EPI_SIGMOID, "%s: bad epilogue %d", name, p.epi);
   TTA_CHECK_ARG(p.epi != EPI_PRE_SILU || p.C2, "%s: epilogue 3 needs C2", name);
   TTA_CHECK_ARG(p.epi != EPI_SILU_GRAD || p.aux, "%s: epilogue 4 needs aux", name);
   if (M == 0 || N == 0 || batch == 0) {
@@ -339,7 +339,7 @@ extern "C" int tta_gemm_f32_group(const tta_gemm_problem* probs, int64_t n, hipS
   bool vec_all = true;
   for (int64_t i = 0; i < n; ++i) {
     const tta_gemm_problem& q = probs[i];
-    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= 4, "tta_gemm_f32_group: bad epilogue");
+    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= EPI_SIGMOID, "tta_gemm_f32_group: bad epilogue");
     GemmArgs p{q.A, q.B, q.C, q.bias, q.C2, q.aux, 0, 0, 0, q.lda, q.ldb, q.ldc, 0, 0, 0, 0,
                (int)q.epilogue, nullptr, nullptr, nullptr, 0, 0};
     bool skip = false, vec = false;
@@ -412,7 +412,8 @@ extern "C" int tta_gemm_f32_group_splitk(const tta_gemm_problem* probs, int64_t 
   const int64_t tiles = splitk_tiles(probs, n);
   for (int64_t i = 0; i < n; ++i) {
     const tta_gemm_problem& q = probs[i];
-    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= 4, "tta_gemm_f32_group_splitk: bad epilogue");
+    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= EPI_SIGMOID,
+                  "tta_gemm_f32_group_splitk: bad epilogue");
     GemmArgs p{q.A, q.B, q.C, q.bias, q.C2, q.aux, 0, 0, 0, q.lda, q.ldb, q.ldc, 0, 0, 0, 0,
                (int)q.epilogue, nullptr, nullptr, nullptr, 0, 0};
     bool skip = false, vec = false;

@@ -124,6 +124,7 @@ __device__ __forceinline__ float epi_one(const GemmArgs& p, float v, int row, in
     v += p.P[(int64_t)p.idx0[row] * p.ldp + col] + p.P[(int64_t)p.idx1[row] * p.ldp + p.off1 + col];
   const int64_t off = (int64_t)row * p.ldc + col;
   if (p.epi == EPI_SILU) v = tta_silu(v);
+  if (p.epi == EPI_SIGMOID) v = tta_sigmoid_acc(v);
   if (p.epi == EPI_ACCUM) v += p.C[off];
   if (p.epi == EPI_PRE_SILU) p.C2[off] = tta_silu(v);
   if (p.epi == EPI_SILU_GRAD) v = v * tta_silu_grad(p.aux[off]);
@@ -156,17 +157,39 @@ __device__ __forceinline__ void partial_rows(float* W, int M, int N, const float
   }
 }
 
+// EPI_GATE (ge, gc0: the launch's gate operands and the product's first coefficient) takes the
+// float4 path only (the host requires its alignments); a thread's four columns lie in one
+// coefficient (H % 4 == 0).
 template <int EPI, bool BATCH>
 __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct, int ldt,
                                               int rows, int row0, int n0, int t, int nth,
-                                              bool vec_ok, bool full) {
+                                              bool vec_ok, bool full,
+                                              const GateEpi* ge = nullptr, int gc0 = 0) {
   const int c4 = t & 31, rstep = nth >> 5;
   const int col = n0 + 4 * c4;
   if (vec_ok && (full || col + 3 < p.N)) {
     const floatx4 bv = p.bias ? *reinterpret_cast<const floatx4*>(p.bias + col)
                               : floatx4{0.f, 0.f, 0.f, 0.f};
     const bool gather = p.P != nullptr;
-    constexpr bool LOADS = EPI == EPI_ACCUM || EPI == EPI_SILU_GRAD;
+    // gate: coefficient gc of this thread's columns, their channel gh, gating column gcol
+    int gc = 0, gh = 0, gcol = 0;
+    if constexpr (EPI == EPI_GATE) {
+      gc = gate_coef(*ge, gc0, col);
+      gh = col - (gc - gc0) * ge->H;
+      gcol = gc > 0 ? gate_gcol(*ge, gc, gh) : 0;
+    }
+    // gate epilogue of one float4: coefficient 0 stores its pre-activation and takes SiLU, the
+    // others are scaled by their gating sigmoids gv
+    auto gate4 = [&](floatx4& v, const floatx4& gv, int row) {
+      if (gc == 0) {
+        __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(ge->x0 + (int64_t)row * ge->ldx0 + gh));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = tta_silu(v[e]);
+      } else {
+        v = v * gv;
+      }
+    };
+    constexpr bool LOADS = EPI == EPI_ACCUM || EPI == EPI_SILU_GRAD || EPI == EPI_GATE;
     constexpr int RB = 8;
     if (BATCH && full && (LOADS || gather) && rows % (RB * rstep) == 0) {
       // An epilogue that reads memory (the accumulated C, the SiLU argument, the gathered rows;
@@ -188,6 +211,9 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
             ex[i] = *reinterpret_cast<const floatx4*>(p.C + (int64_t)row * p.ldc + col);
           if constexpr (EPI == EPI_SILU_GRAD)
             ex[i] = *reinterpret_cast<const floatx4*>(p.aux + (int64_t)row * p.ldc + col);
+          if constexpr (EPI == EPI_GATE)
+            if (gc > 0)
+              ex[i] = *reinterpret_cast<const floatx4*>(ge->sig + (int64_t)row * ge->ldg + gcol);
         }
         if (gather) {
 #pragma unroll
@@ -202,6 +228,11 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
           const int64_t off = (int64_t)row * p.ldc + col;
           if (gather) v += pv[i];
           if constexpr (EPI == EPI_ACCUM) v += ex[i];
+          if constexpr (EPI == EPI_GATE) gate4(v, ex[i], row);
+          if constexpr (EPI == EPI_SIGMOID) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = tta_sigmoid_acc(v[e]);
+          }
           if constexpr (EPI == EPI_SILU || EPI == EPI_PRE_SILU || EPI == EPI_SILU_GRAD) {
             floatx4 w;
 #pragma unroll
@@ -227,6 +258,16 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
         v += *reinterpret_cast<const floatx4*>(p.P + (int64_t)p.idx0[row] * p.ldp + col) +
              *reinterpret_cast<const floatx4*>(p.P + (int64_t)p.idx1[row] * p.ldp + p.off1 + col);
       if constexpr (EPI == EPI_ACCUM) v += *reinterpret_cast<const floatx4*>(p.C + off);
+      if constexpr (EPI == EPI_GATE) {
+        const floatx4 gv =
+            gc > 0 ? *reinterpret_cast<const floatx4*>(ge->sig + (int64_t)row * ge->ldg + gcol)
+                   : floatx4{0.f, 0.f, 0.f, 0.f};
+        gate4(v, gv, row);
+      }
+      if constexpr (EPI == EPI_SIGMOID) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = tta_sigmoid_acc(v[e]);
+      }
       if constexpr (EPI == EPI_SILU || EPI == EPI_PRE_SILU || EPI == EPI_SILU_GRAD) {
         floatx4 w;
         if constexpr (EPI == EPI_SILU_GRAD) {
@@ -247,7 +288,7 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
       // (+15-17 % on the write-heavy short-K shapes)
       __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(p.C + off));
     }
-  } else {
+  } else if constexpr (EPI != EPI_GATE) {
     for (int rr = t >> 5; rr < rows; rr += rstep) {
       const int row = row0 + rr;
       if (row >= p.M) break;
@@ -724,6 +765,13 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
             break;
           case EPI_SILU_GRAD:
             epilogue_rows<EPI_SILU_GRAD, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            break;
+          case EPI_SIGMOID:
+            epilogue_rows<EPI_SIGMOID, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
+            break;
+          case EPI_GATE:
+            epilogue_rows<EPI_GATE, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full,
+                                            &g.gate, g.gc0[blockIdx.z]);
             break;
           default:
             epilogue_rows<EPI_STORE, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
@@ -1224,12 +1272,13 @@ static int prepare_bf16x(const float* A, const void* Bp, float* C, const float* 
                          const float* aux, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldc, const float* P, int64_t ldp, const int* idx0,
                          const int* idx1, int64_t off1, int64_t n_rows_p, int epilogue,
-                         GemmGroup& g, int slot, bool* skip) {
+                         GemmGroup& g, int slot, bool* skip, bool gate = false) {
   *skip = false;
   TTA_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "tta_gemm_bf16x: negative size");
   TTA_CHECK_ARG(M < (int64_t)1 << 31 && N < (int64_t)1 << 30 && K < (int64_t)1 << 30,
                 "tta_gemm_bf16x: size exceeds int32");
-  TTA_CHECK_ARG(epilogue >= 0 && epilogue <= 4, "tta_gemm_bf16x: bad epilogue %d", epilogue);
+  TTA_CHECK_ARG(gate ? epilogue == EPI_GATE : (epilogue >= 0 && epilogue <= EPI_SIGMOID),
+                "tta_gemm_bf16x: bad epilogue %d", epilogue);
   TTA_CHECK_ARG(epilogue != EPI_PRE_SILU || C2, "tta_gemm_bf16x: epilogue 3 needs C2");
   TTA_CHECK_ARG(epilogue != EPI_SILU_GRAD || aux, "tta_gemm_bf16x: epilogue 4 needs aux");
   TTA_CHECK_ARG(!P || (idx0 && idx1 && n_rows_p > 0 && off1 >= 0 && ldp >= off1 + N),
@@ -1279,7 +1328,8 @@ extern "C" int tta_gemm_bf16x_group(const tta_gemm_problem* probs, int64_t n, in
   int m = 0;
   for (int64_t i = 0; i < n; ++i) {
     const tta_gemm_problem& q = probs[i];
-    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= 4, "tta_gemm_bf16x_group: bad epilogue");
+    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= EPI_SIGMOID,
+                  "tta_gemm_bf16x_group: bad epilogue");
     bool skip = false;
     const int rc = prepare_bf16x(q.A, q.B, q.C, q.bias, q.C2, q.aux, q.M, q.N, q.K, q.lda, q.ldc,
                                  nullptr, 0, nullptr, nullptr, 0, 0, (int)q.epilogue, g, m,
@@ -1310,30 +1360,41 @@ extern "C" int64_t tta_gemm_bf16x_splitk_work(const tta_gemm_problem* probs, int
   return split ? need : 0;
 }
 
-// tta_gemm_bf16x_group with the k chunks of tta_gemm_bf16x_splitk_work (no row gathers).
-extern "C" int tta_gemm_bf16x_group_splitk(const tta_gemm_problem* probs, int64_t n, int mode,
-                                           float* work, int64_t work_floats,
-                                           hipStream_t stream) {
-  TTA_CHECK_ARG(planes_of(mode) > 0,
-                "tta_gemm_bf16x_group_splitk: mode must be 1, 3, 6 or 16 (got %d)", mode);
-  TTA_CHECK_ARG(n >= 0 && n <= kMaxGroup && (probs || n == 0),
-                "tta_gemm_bf16x_group_splitk: 0..%d products", kMaxGroup);
-  GemmGroup g{};
+// tta_gemm_bf16x_group with the k chunks of tta_gemm_bf16x_splitk_work (no row gathers); work
+// NULL: never split.  gate (g.gate set by the caller): every product has the gate epilogue, with
+// first coefficient c0[i].
+static int group_splitk_impl(const tta_gemm_problem* probs, int64_t n, int mode, float* work,
+                             int64_t work_floats, hipStream_t stream, GemmGroup& g, bool gate,
+                             const int64_t* c0) {
+  const char* who = gate ? "tta_gemm_bf16x_group_gate" : "tta_gemm_bf16x_group_splitk";
+  TTA_CHECK_ARG(planes_of(mode) > 0, "%s: mode must be 1, 3, 6 or 16 (got %d)", who, mode);
+  TTA_CHECK_ARG(n >= 0 && n <= kMaxGroup && (probs || n == 0), "%s: 0..%d products", who,
+                kMaxGroup);
   int m = 0;
   const int64_t tiles = bf16x_splitk_tiles(probs, n);
   int64_t need = 0, max_chunks = 1, max_mn = 0;
   for (int64_t i = 0; i < n; ++i) {
     const tta_gemm_problem& q = probs[i];
-    TTA_CHECK_ARG(q.epilogue >= 0 && q.epilogue <= 4,
-                  "tta_gemm_bf16x_group_splitk: bad epilogue");
+    TTA_CHECK_ARG(gate ? q.epilogue == EPI_GATE : (q.epilogue >= 0 && q.epilogue <= EPI_SIGMOID),
+                  "%s: bad epilogue %lld", who, (long long)q.epilogue);
     bool skip = false;
     const int rc = prepare_bf16x(q.A, q.B, q.C, q.bias, q.C2, q.aux, q.M, q.N, q.K, q.lda, q.ldc,
                                  nullptr, 0, nullptr, nullptr, 0, 0, (int)q.epilogue, g, m,
-                                 &skip);
+                                 &skip, gate);
     if (rc != tta::kOk) return rc;
     if (skip) continue;
-    TTA_CHECK_ARG(q.K > 0, "tta_gemm_bf16x_group_splitk: K must be positive");
-    const int64_t kc = bf16x_splitk_chunk(q.K, tiles);
+    TTA_CHECK_ARG(q.K > 0, "%s: K must be positive", who);
+    if (gate) {
+      TTA_CHECK_ARG(q.N % g.gate.H == 0 && c0[i] >= 0 && c0[i] + q.N / g.gate.H <= 9,
+                    "%s: product %lld: N = %lld columns from coefficient %lld do not fit 9 "
+                    "coefficients of H = %d", who, (long long)i, (long long)q.N,
+                    (long long)c0[i], g.gate.H);
+      TTA_CHECK_ARG(g.vec[m], "%s: product %lld needs 16-byte aligned C, bias and row strides",
+                    who, (long long)i);
+      g.gc0[m] = (int)c0[i];
+    }
+    // the gate entry without a workspace never splits
+    const int64_t kc = (!gate || work) ? bf16x_splitk_chunk(q.K, tiles) : (q.K + BK - 1) / BK * BK;
     const int64_t chunks = (q.K + kc - 1) / kc;
     g.kch[m] = (int)kc;
     g.woff[m] = need;
@@ -1343,16 +1404,46 @@ extern "C" int tta_gemm_bf16x_group_splitk(const tta_gemm_problem* probs, int64_
     ++m;
   }
   if (m == 0) return tta::kOk;
-  TTA_CHECK_ARG(work && work_floats >= need && (uintptr_t)work % 16 == 0,
-                "tta_gemm_bf16x_group_splitk: work holds %lld floats (16-byte aligned), needs "
-                "%lld", (long long)work_floats, (long long)need);
-  TTA_CHECK_ARG(max_chunks <= 65535, "tta_gemm_bf16x_group_splitk: too many chunks");
+  if (!gate || max_chunks > 1)
+    TTA_CHECK_ARG(work && work_floats >= need && (uintptr_t)work % 16 == 0,
+                  "%s: work holds %lld floats (16-byte aligned), needs %lld", who,
+                  (long long)work_floats, (long long)need);
   if (max_chunks == 1) return launch_mode(g, m, mode, stream);  // nothing splits: direct
+  TTA_CHECK_ARG(max_chunks <= 65535, "%s: too many chunks", who);
   g.work = work;
   const int rc = launch_mode(g, m, mode, stream, (unsigned)max_chunks);
   if (rc != tta::kOk) return rc;
   const int64_t rb = std::min<int64_t>((max_mn + 255) / 256, 2048);
   hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)rb, 1, (unsigned)m), dim3(256), 0, stream, g);
-  TTA_CHECK_LAUNCH("tta_gemm_bf16x_group_splitk");
+  TTA_CHECK_LAUNCH(who);
   return tta::kOk;
+}
+
+extern "C" int tta_gemm_bf16x_group_splitk(const tta_gemm_problem* probs, int64_t n, int mode,
+                                           float* work, int64_t work_floats,
+                                           hipStream_t stream) {
+  GemmGroup g{};
+  return group_splitk_impl(probs, n, mode, work, work_floats, stream, g, false, nullptr);
+}
+
+extern "C" int tta_gemm_bf16x_group_gate(const tta_gemm_problem* probs, int64_t n, int mode,
+                                         const int64_t* c0, const float* sig, int64_t ldg,
+                                         float* x0, int64_t ldx0, int64_t H, const int* idx8,
+                                         float* work, int64_t work_floats, hipStream_t stream) {
+  TTA_CHECK_ARG(c0 && idx8 && sig && x0, "tta_gemm_bf16x_group_gate: null pointer");
+  TTA_CHECK_ARG(H > 0 && H % 4 == 0 && H < (1 << 20), "tta_gemm_bf16x_group_gate: H = %lld must "
+                "be a positive multiple of 4", (long long)H);
+  GemmGroup g{};
+  unsigned tab = 0;
+  int tmax = 0;
+  for (int c = 0; c < 8; ++c) {
+    TTA_CHECK_ARG(idx8[c] >= 0 && idx8[c] < 15, "tta_gemm_bf16x_group_gate: bad gate index");
+    tab |= (unsigned)idx8[c] << (4 * c);
+    tmax = std::max(tmax, idx8[c]);
+  }
+  TTA_CHECK_ARG(ldg >= (tmax + 1) * H && ldg % 4 == 0 && ldx0 >= H && ldx0 % 4 == 0 &&
+                    (uintptr_t)sig % 16 == 0 && (uintptr_t)x0 % 16 == 0,
+                "tta_gemm_bf16x_group_gate: sig / x0 rows too short or not 16-byte aligned");
+  g.gate = GateEpi{sig, x0, ldg, ldx0, (int)H, tab};
+  return group_splitk_impl(probs, n, mode, work, work_floats, stream, g, true, c0);
 }

@@ -10,7 +10,31 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 namespace tta_gemm {
 
-enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ACCUM = 2, EPI_PRE_SILU = 3, EPI_SILU_GRAD = 4 };
+enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ACCUM = 2, EPI_PRE_SILU = 3, EPI_SILU_GRAD = 4,
+       EPI_SIGMOID = 5, EPI_GATE = 6 };
+
+// The gate epilogue (EPI_GATE, split kernel only) of one launch: a product's output column col
+// is channel h = col % H of SH coefficient c = c0 + col / H (c0 per product, GemmGroup::gc0).
+// Coefficient 0 gets SiLU and its pre-activation is also stored (x0 rows, stride ldx0, H wide);
+// coefficient c > 0 is multiplied by sig[row * ldg + t * H + h], the sigmoid of the gating
+// columns (an earlier launch with the EPI_SIGMOID epilogue), with degree index
+// t = (tab >> 4 (c - 1)) & 15 -- the GateActivation of an SO(2) convolution's output applied as
+// the convolution writes it (activation.py:53-70).
+struct GateEpi {
+  const float* sig;
+  float* x0;
+  int64_t ldg, ldx0;
+  int H;
+  unsigned tab;
+};
+
+__device__ __forceinline__ int gate_coef(const GateEpi& ge, int c0, int col) {
+  return c0 + col / ge.H;
+}
+// gating column of coefficient c > 0, channel h
+__device__ __forceinline__ int gate_gcol(const GateEpi& ge, int c, int h) {
+  return (int)((ge.tab >> (4 * (c - 1))) & 15u) * ge.H + h;
+}
 
 struct GemmArgs {
   const float* A;
@@ -44,6 +68,9 @@ struct GemmGroup {
   float* work;
   int64_t woff[kMaxGroup];
   int kch[kMaxGroup];
+  // EPI_GATE products: the launch's gate operands and each product's first coefficient
+  GateEpi gate;
+  int gc0[kMaxGroup];
 };
 
 // Accumulator layout of v_mfma_f32_16x16x{4f32,32bf16}: lane l holds D[4*(l/16)+r][l%16] in
@@ -70,6 +97,7 @@ __device__ __forceinline__ void store_tiles(const GemmArgs& p, const floatx4 (&a
                p.P[(int64_t)p.idx1[row] * p.ldp + p.off1 + col];
         const int64_t off = (int64_t)row * p.ldc + col;
         if (EPI == EPI_SILU) v = tta_silu(v);
+        if (EPI == EPI_SIGMOID) v = tta_sigmoid_acc(v);
         if (EPI == EPI_ACCUM) v += C[off];
         if (EPI == EPI_PRE_SILU) C2[off] = tta_silu(v);
         if (EPI == EPI_SILU_GRAD) v = v * tta_silu_grad(aux[off]);
@@ -104,6 +132,7 @@ __device__ __forceinline__ void store_tiles32(const GemmArgs& p,
                p.P[(int64_t)p.idx1[row] * p.ldp + p.off1 + col];
         const int64_t off = (int64_t)row * p.ldc + col;
         if (EPI == EPI_SILU) v = tta_silu(v);
+        if (EPI == EPI_SIGMOID) v = tta_sigmoid_acc(v);
         if (EPI == EPI_ACCUM) v += C[off];
         if (EPI == EPI_PRE_SILU) C2[off] = tta_silu(v);
         if (EPI == EPI_SILU_GRAD) v = v * tta_silu_grad(aux[off]);
@@ -129,7 +158,18 @@ static __global__ __launch_bounds__(256) void k_splitk_reduce(GemmGroup g) {
     for (int s = 1; s < ns; ++s) v += W[s * MN + i];
     if (p.bias) v += p.bias[col];
     const int64_t off = (int64_t)row * p.ldc + col;
+    if (p.epi == EPI_GATE) {
+      const GateEpi& ge = g.gate;
+      const int c = gate_coef(ge, g.gc0[blockIdx.z], col), h = col - (c - g.gc0[blockIdx.z]) * ge.H;
+      if (c == 0) {
+        ge.x0[(int64_t)row * ge.ldx0 + h] = v;
+        v = tta_silu(v);
+      } else {
+        v *= ge.sig[(int64_t)row * ge.ldg + gate_gcol(ge, c, h)];
+      }
+    }
     if (p.epi == EPI_SILU) v = tta_silu(v);
+    if (p.epi == EPI_SIGMOID) v = tta_sigmoid_acc(v);
     if (p.epi == EPI_ACCUM) v += p.C[off];
     if (p.epi == EPI_PRE_SILU) p.C2[off] = tta_silu(v);
     if (p.epi == EPI_SILU_GRAD) v = v * tta_silu_grad(p.aux[off]);

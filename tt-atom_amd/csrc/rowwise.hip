@@ -65,6 +65,40 @@ __global__ __launch_bounds__(256) void k_gate_bwd(const float* __restrict__ g_y,
   for (int t = 0; t < L; ++t) g_gating[r * ldg + t * H + h] = acc[t] * (sg[t] * (1.f - sg[t]));
 }
 
+// Backward from the gated output, for a forward whose gate ran in the producing GEMM's epilogue
+// (which keeps y, the gating sigmoids sig and coefficient 0's pre-activation x0, not x):
+//   g_x[0] = g_y[0] silu'(x0),  g_x[c] = g_y[c] sig[t_c],
+//   g_gating[t] = (1 - sig[t]) sum over c of degree index t of g_y[c] y[c]
+// -- y[c] = x[c] sig[t], so the sum is sigmoid'(gating[t]) sum g_y[c] x[c], the gating adjoint
+// of forces.py:104-130.  g_y and y are contiguous [R, 9, H]; the other operands have their own
+// row strides.
+__global__ __launch_bounds__(256) void k_gate_bwd_y(
+    const float* __restrict__ g_y, const float* __restrict__ y, const float* __restrict__ sig,
+    const float* __restrict__ x0, float* __restrict__ g_x, float* __restrict__ g_gating,
+    int64_t R, int H, int L, int64_t ldg, int64_t ldx0, int64_t ldgx, int64_t ldgg, GateIdx idx) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= R * H) return;
+  const int64_t r = gid / H;
+  const int h = (int)(gid % H);
+  const float* yr = y + r * 9 * H;
+  const float* gr = g_y + r * 9 * H;
+  float* gx = g_x + r * ldgx;
+  float sg[8], acc[8];
+  for (int t = 0; t < L; ++t) {
+    sg[t] = sig[r * ldg + t * H + h];
+    acc[t] = 0.f;
+  }
+  __builtin_nontemporal_store(gr[h] * tta_silu_grad(x0[r * ldx0 + h]), gx + h);
+#pragma unroll
+  for (int c = 1; c < 9; ++c) {
+    const int t = idx.v[c - 1];
+    const float g = gr[c * H + h];
+    __builtin_nontemporal_store(g * sg[t], gx + c * H + h);
+    acc[t] += g * yr[c * H + h];
+  }
+  for (int t = 0; t < L; ++t) g_gating[r * ldgg + t * H + h] = acc[t] * (1.f - sg[t]);
+}
+
 // ------------------------------------------------------------------ LayerNorm + SiLU (radial MLP)
 // G lanes per row (64, or 32 for rows of at most 128 so that a wavefront holds two rows and twice
 // the bytes are in flight per wave); the row stays in registers (element NPL lane + k in slot k,
@@ -531,6 +565,27 @@ extern "C" int tta_gate_bwd(const float* g_y, const float* x, const float* gatin
   hipLaunchKernelGGL(k_gate_bwd, dim3(tta_blocks(R * H, 256)), dim3(256), 0, stream, g_y, x,
                      gating, g_x, g_gating, R, (int)H, (int)L, ldx, ldg, gi);
   TTA_CHECK_LAUNCH("tta_gate_bwd");
+  return tta::kOk;
+}
+
+extern "C" int tta_gate_bwd_y(const float* g_y, const float* y, const float* sig,
+                              const float* x0, float* g_x, float* g_gating, int64_t R, int64_t H,
+                              int64_t L, int64_t ldg, int64_t ldx0, int64_t ldgx, int64_t ldgg,
+                              const int* idx8, hipStream_t stream) {
+  TTA_CHECK_ARG(R >= 0 && H > 0 && L >= 1 && L <= 8, "tta_gate_bwd_y: bad sizes");
+  TTA_CHECK_ARG(ldg >= L * H && ldx0 >= H && ldgx >= 9 * H && ldgg >= L * H,
+                "tta_gate_bwd_y: row stride too small");
+  TTA_CHECK_ARG(idx8, "tta_gate_bwd_y: null index table");
+  GateIdx gi;
+  for (int i = 0; i < 8; ++i) {
+    TTA_CHECK_ARG(idx8[i] >= 0 && idx8[i] < L, "tta_gate_bwd_y: gate index out of range");
+    gi.v[i] = idx8[i];
+  }
+  if (R == 0) return tta::kOk;
+  TTA_CHECK_ARG(g_y && y && sig && x0 && g_x && g_gating, "tta_gate_bwd_y: null pointer");
+  hipLaunchKernelGGL(k_gate_bwd_y, dim3(tta_blocks(R * H, 256)), dim3(256), 0, stream, g_y, y,
+                     sig, x0, g_x, g_gating, R, (int)H, (int)L, ldg, ldx0, ldgx, ldgg, gi);
+  TTA_CHECK_LAUNCH("tta_gate_bwd_y");
   return tta::kOk;
 }
 

@@ -51,6 +51,7 @@ _SIGS = {
     "tta_node_gather_sum": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_gate_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "tta_gate_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
+    "tta_gate_bwd_y": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "tta_ln_silu_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "tta_ln_silu_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "tta_rmsnorm_sh_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _P],
@@ -96,6 +97,8 @@ _SIGS = {
     "tta_gemm_f32_splitk_work": [ctypes.POINTER(GemmProblem), _I64],
     "tta_gemm_bf16x_splitk_work": [ctypes.POINTER(GemmProblem), _I64],
     "tta_gemm_bf16x_group_splitk": [ctypes.POINTER(GemmProblem), _I64, _I, _P, _I64, _P],
+    "tta_gemm_bf16x_group_gate": [ctypes.POINTER(GemmProblem), _I64, _I, _P, _P, _I64, _P, _I64,
+                                  _I64, _P, _P, _I64, _P],
     "tta_gemm_f32_group_splitk": [ctypes.POINTER(GemmProblem), _I64, _P, _I64, _P],
     "tta_radius_graph_thresholds": [_P, _I64, _P, _P, _P, _I64, _P, _P, _I, _D, _F, _F, _I, _P,
                                     _P, _P, _P, _P],
@@ -186,6 +189,16 @@ def _i32(t, numel=None, name="index"):
     return _ptr(t, torch.int32, numel, name)
 
 
+def _host_idx8(idx, name="idx8"):
+    """The 8-entry gate index table as host memory (the entry points read it on the host while
+    they build the launch): a sequence of ints or a tensor (a device tensor is copied back, so
+    pass a sequence inside a graph capture)."""
+    vals = idx.tolist() if isinstance(idx, torch.Tensor) else list(idx)
+    if len(vals) != 8:
+        raise RuntimeError(f"{name} must have 8 entries, got {len(vals)}")
+    return (ctypes.c_int * 8)(*(int(v) for v in vals))
+
+
 def _rows(t, rows, ld, width, name="tensor"):
     """Pointer of a row-strided fp32 view; checks that rows x width at stride ld stay inside the
     tensor's storage (the kernels index ptr[r * ld + c] for r < rows, c < width)."""
@@ -201,6 +214,8 @@ def _rows(t, rows, ld, width, name="tensor"):
 
 # ----------------------------------------------------------------------------- GEMM
 EPI_STORE, EPI_SILU, EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD = 0, 1, 2, 3, 4
+EPI_SIGMOID = 5
+EPI_GATE = 6  # tta_gemm_bf16x_group_gate only
 
 # Optional measurement hook: when set, every GEMM launch is bracketed by
 # ``probe.before(flops, nbytes, kind)`` and ``probe.after()`` (the benchmark records HIP events on
@@ -387,6 +402,58 @@ def _small_split(items):
     if probe is not None:
         probe.after()
     return True
+
+
+def linear_group_gate(items, c0, sig, x0, idx8, H):
+    """The coefficient products of an SO(2) convolution with its gate applied as they are
+    written (tta_gemm_bf16x_group_gate): ``items`` = [(x, PackedWeight, bias, out)], product i's
+    columns being coefficients c0[i], c0[i] + 1, ... of H channels each; ``sig`` [M, L * H]
+    the sigmoid of the convolution's gating columns (any row stride; linear() with
+    EPI_SIGMOID), ``x0`` [M, H] receives coefficient 0's pre-activation.  Launches with fewer than 4096 rows take the split-K form when the library's
+    rule splits them."""
+    if not items or len(items) > MAX_GROUP or len(c0) != len(items):
+        raise RuntimeError("linear_group_gate: 1..8 products, one first coefficient each")
+    mode = items[0][1].mode
+    probs = (GemmProblem * len(items))()
+    flops = nbytes = 0.0
+    L = max(_host_idx8(idx8)) + 1
+    M = items[0][0].shape[0]
+    for i, (x, w, bias, out) in enumerate(items):
+        if not (isinstance(w, PackedWeight) and w.packed is not None and w.mode == mode
+                and x.shape[1] % 4 == 0 and x.data_ptr() % 16 == 0 and _ld(x, "x") % 4 == 0
+                and _ld(x, "x") < (1 << 21)):
+            raise RuntimeError("linear_group_gate: every product needs a packed weight of one "
+                               "mode and a 16-byte aligned x with K, row stride multiples of 4")
+        Mi, K = x.shape
+        N = w.shape[1]
+        if Mi != M or K != w.shape[0] or out.shape != (M, N) or N % H:
+            raise RuntimeError("linear_group_gate: shape mismatch")
+        ldc = _ld(out, "out")
+        probs[i] = GemmProblem(_rows(x, M, _ld(x, "x"), K, "x"), w.packed.data_ptr(),
+                               _rows(out, M, ldc, N, "out"),
+                               None if bias is None else _ptr(bias, numel=N, name="bias"),
+                               None, None, M, N, K, _ld(x, "x"), 0, ldc, EPI_GATE)
+        flops += 2.0 * M * N * K
+        # A, B, the output and a gating sigmoid per gated output (coefficient 0: its x0 copy)
+        nbytes += 4.0 * (M * K + K * N + 2 * M * N)
+    gp = _rows(sig, M, _ld(sig, "sig"), L * H, "sig")
+    xp = _rows(x0, M, _ld(x0, "x0"), H, "x0")
+    work = None
+    if M < 4096:
+        need = load().tta_gemm_bf16x_splitk_work(probs, len(items))
+        if need < 0:
+            raise RuntimeError("tta_gemm_bf16x_splitk_work: bad product list")
+        if need > 0:
+            work = torch.empty(need, device=items[0][0].device, dtype=torch.float32)
+    probe = _gemm_probe
+    if probe is not None:
+        probe.before(flops, nbytes, MODE_KIND[mode])
+    _call("tta_gemm_bf16x_group_gate", probs, len(items), mode,
+          (ctypes.c_int64 * len(items))(*c0), gp, _ld(sig, "sig"), xp, _ld(x0, "x0"), H,
+          _host_idx8(idx8), None if work is None else work.data_ptr(),
+          0 if work is None else work.numel(), _stream())
+    if probe is not None:
+        probe.after()
 
 
 def _gemm_f32_splitk(items):
@@ -693,8 +760,7 @@ def gate_fwd(x, gating, y, idx8, *, R, H, L, ldx=None, ldg=None):
     ldg = L * H if ldg is None else ldg
     _hbm_call("k_gate_fwd", 4 * R * H * (18 + L), "tta_gate_fwd",
               _rows(x, R, ldx, 9 * H, "x"), _rows(gating, R, ldg, L * H, "gating"),
-              _ptr(y, numel=R * 9 * H, name="y"), R, H, L, ldx, ldg, _i32(idx8, 8, "idx8"),
-              _stream())
+              _ptr(y, numel=R * 9 * H, name="y"), R, H, L, ldx, ldg, _host_idx8(idx8), _stream())
     return y
 
 
@@ -705,8 +771,21 @@ def gate_bwd(g_y, x, gating, g_x, g_gating, idx8, *, R, H, L, ldx=None, ldg=None
     _hbm_call("k_gate_bwd", 4 * R * H * (27 + 2 * L), "tta_gate_bwd",
               _ptr(g_y, numel=R * 9 * H, name="g_y"), _rows(x, R, ldx, 9 * H, "x"),
               _rows(gating, R, ldg, L * H, "gating"), _rows(g_x, R, ldx, 9 * H, "g_x"),
-              _rows(g_gating, R, ldg, L * H, "g_gating"), R, H, L, ldx, ldg,
-              _i32(idx8, 8, "idx8"), _stream())
+              _rows(g_gating, R, ldg, L * H, "g_gating"), R, H, L, ldx, ldg, _host_idx8(idx8),
+              _stream())
+
+
+def gate_bwd_y(g_y, y, sig, x0, g_x, g_gating, idx8, *, R, H, L):
+    """The gate backward from the gated output y (contiguous [R, 9, H], as g_y), the gating
+    sigmoids sig and coefficient 0's pre-activation x0 (tta_gate_bwd_y); sig, x0, g_x and
+    g_gating are row-strided 2-D views."""
+    ldg, ldx0, ldgx, ldgg = (_ld(t, nm) for t, nm in ((sig, "sig"), (x0, "x0"),
+                                                      (g_x, "g_x"), (g_gating, "g_gating")))
+    _hbm_call("k_gate_bwd_y", 4 * R * H * (27 + 2 * L), "tta_gate_bwd_y",
+              _ptr(g_y, numel=R * 9 * H, name="g_y"), _ptr(y, numel=R * 9 * H, name="y"),
+              _rows(sig, R, ldg, L * H, "sig"), _rows(x0, R, ldx0, H, "x0"),
+              _rows(g_x, R, ldgx, 9 * H, "g_x"), _rows(g_gating, R, ldgg, L * H, "g_gating"),
+              R, H, L, ldg, ldx0, ldgx, ldgg, _host_idx8(idx8), _stream())
 
 
 def ln_silu_fwd(a, gamma, beta, nrm, s, *, R, n, groups=1, lda=None, lds=None, eps=1e-5):

@@ -100,6 +100,15 @@ class SO2Weights:
         self.wm0_t = _gw(wm0.T, device, mode)                           # [3 cin, extra + 3 hout]
         self.bm0 = _dev(bm0, device)
         self.wm0 = _gw(wm0, device, mode)                               # [extra + 3 hout, 3 cin]
+        # packed weights: the gating columns and the coefficient columns as separate products,
+        # so that the gate can be applied in the coefficient products' epilogue
+        # (the split kernel's float4 epilogue and 16-byte aligned m-block column offsets)
+        self.gate_split = mode is not None and extra > 0 and hout % 4 == 0 and cin % 4 == 0
+        if self.gate_split:
+            self.wm0g_t = _gw(wm0[:extra].T.contiguous(), device, mode)    # [3 cin, extra]
+            self.wm0c_t = _gw(wm0[extra:].T.contiguous(), device, mode)    # [3 cin, 3 hout]
+            self.bm0g = _dev(bm0[:extra].contiguous(), device)
+            self.bm0c = _dev(bm0[extra:].contiguous(), device)
         b1 = _so2_block(w[f"{prefix}.so2_m_conv.0.fc.weight"])          # [4 cin, 4 hout]
         b2 = _so2_block(w[f"{prefix}.so2_m_conv.1.fc.weight"])          # [2 cin, 2 hout]
         if b1.shape != (4 * cin, 4 * hout) or b2.shape != (2 * cin, 2 * hout):
@@ -242,8 +251,9 @@ class Backbone:
         cat = lambda name: torch.cat([getattr(r, name) for r in self.radials]).contiguous()
         self.rad_ln1w_all, self.rad_ln1b_all = cat("ln1w"), cat("ln1b")
         self.rad_ln4w_all, self.rad_ln4b_all = cat("ln4w"), cat("ln4b")
-        self.gate_idx_mprime = torch.tensor(GATE_IDX_MPRIME, dtype=torch.int32, device=dev)
-        self.gate_idx_natural = torch.tensor(GATE_IDX_NATURAL, dtype=torch.int32, device=dev)
+        # host tables: the entry points read them while building a launch
+        self.gate_idx_mprime = GATE_IDX_MPRIME
+        self.gate_idx_natural = GATE_IDX_NATURAL
 
 
 class GraphContext:

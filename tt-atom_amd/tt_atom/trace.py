@@ -90,7 +90,9 @@ class TracedEngine:
         # shared edge temporaries
         self.LHc = L * H + NSPH * H                      # combined conv-1 row [gating | out]
         self.xf, self.g_xf, self.g_mcat = emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C)
-        self.y, self.g_y = emp(E, NSPH, H), emp(E, NSPH, H)
+        self.g_y = emp(E, NSPH, H)
+        if not all(b.so2_1.gate_split for b in bb.blocks):
+            self.y = emp(E, NSPH, H)                     # gated conv-1 rows of the unsplit path
         self.g_tsum = emp(N, NSPH, C)                    # per-node destination adjoint sums
         self.g1c = emp(E, self.LHc)
         self.g_mso2 = emp(E, NSPH, C)
@@ -104,7 +106,13 @@ class TracedEngine:
             c.x_in, c.n1, c.x1, c.n2 = (emp(N, NSPH, C) for _ in range(4))
             c.inv1, c.inv2 = emp(N), emp(N)
             c.rad = self._radial_cache(E, 6 * 2 * C, dev, 1 + i)
-            c.o1c, c.mso2 = emp(E, self.LHc), emp(E, NSPH, C)
+            c.mso2 = emp(E, NSPH, C)
+            if b.so2_1.gate_split:
+                # the gate runs in the conv-1 epilogue: gating sigmoids, the gated rows (conv-2's
+                # input, kept for the backward) and coefficient 0's pre-activation
+                c.sig1, c.y1, c.x01 = emp(E, L * H), emp(E, NSPH, H), emp(E, H)
+            else:
+                c.o1c = emp(E, self.LHc)         # [gating | ungated coefficients]
             if b.ff_type == "spectral":
                 c.a_s, c.gat, c.h, c.gout = emp(N, L * H), emp(N, L * H), emp(N, NSPH, H), emp(N, NSPH, H)
             else:
@@ -235,14 +243,26 @@ class TracedEngine:
                 nat.rmsnorm_sh_fwd(c.x_in, bw.norm_1.aw, bw.norm_1.ab, self.sys_emb, c.n1, c.inv1)
             nat.gather_rotate(c.n1, g.src, g.tgt, self.coef, c.rad.out, self.xf)
             xf = self.xf.view(E, NSPH * Cin)
-            o1 = c.o1c
-            # the three m-block contractions (m = 0 with the gating columns, 1, 2): one launch
-            nat.linear_group([(xf[:, :3 * Cin], s1w.wm0_t, s1w.bm0, o1[:, :LH + 3 * H]),
-                              (xf[:, 3 * Cin:7 * Cin], s1w.w1, None, o1[:, LH + 3 * H:LH + 7 * H]),
-                              (xf[:, 7 * Cin:], s1w.w2, None, o1[:, LH + 7 * H:])])
-            nat.gate_fwd(o1[:, LH:], o1, self.y, bb.gate_idx_mprime, R=E, H=H, L=L, ldx=LHc,
-                         ldg=LHc)
-            y = self.y.view(E, NSPH * H)
+            if s1w.gate_split:
+                # the gating columns' sigmoids first, then the three m-block contractions (m = 0,
+                # 1, 2: one launch) with the gate applied as their rows are written
+                nat.linear(xf[:, :3 * Cin], s1w.wm0g_t, s1w.bm0g, out=c.sig1,
+                           epilogue=nat.EPI_SIGMOID)
+                yv = c.y1.view(E, NSPH * H)
+                nat.linear_group_gate([(xf[:, :3 * Cin], s1w.wm0c_t, s1w.bm0c, yv[:, :3 * H]),
+                                       (xf[:, 3 * Cin:7 * Cin], s1w.w1, None, yv[:, 3 * H:7 * H]),
+                                       (xf[:, 7 * Cin:], s1w.w2, None, yv[:, 7 * H:])],
+                                      (0, 3, 7), c.sig1, c.x01, bb.gate_idx_mprime, H)
+                y = yv
+            else:
+                o1 = c.o1c
+                # the three m-block contractions (m = 0 with the gating columns, 1, 2): one launch
+                nat.linear_group([(xf[:, :3 * Cin], s1w.wm0_t, s1w.bm0, o1[:, :LH + 3 * H]),
+                                  (xf[:, 3 * Cin:7 * Cin], s1w.w1, None, o1[:, LH + 3 * H:LH + 7 * H]),
+                                  (xf[:, 7 * Cin:], s1w.w2, None, o1[:, LH + 7 * H:])])
+                nat.gate_fwd(o1[:, LH:], o1, self.y, bb.gate_idx_mprime, R=E, H=H, L=L, ldx=LHc,
+                             ldg=LHc)
+                y = self.y.view(E, NSPH * H)
             ms = c.mso2.view(E, NSPH * C)
             nat.linear_group([(y[:, :3 * H], s2w.wm0_t, s2w.bm0, ms[:, :3 * C]),
                               (y[:, 3 * H:7 * H], s2w.w1, None, ms[:, 3 * C:7 * C]),
@@ -327,9 +347,14 @@ class TracedEngine:
         nat.linear_group([(gm[:, :3 * C], s2w.wm0, None, gy[:, :3 * H]),
                           (gm[:, 3 * C:7 * C], s2w.w1_t, None, gy[:, 3 * H:7 * H]),
                           (gm[:, 7 * C:], s2w.w2_t, None, gy[:, 7 * H:])])
-        o1, g1 = c.o1c, self.g1c
-        nat.gate_bwd(self.g_y, o1[:, LH:], o1, g1[:, LH:], g1, self.bb.gate_idx_mprime, R=E, H=H,
-                     L=L, ldx=LHc, ldg=LHc)
+        g1 = self.g1c
+        if s1w.gate_split:
+            nat.gate_bwd_y(self.g_y, c.y1, c.sig1, c.x01, g1[:, LH:], g1[:, :LH],
+                           self.bb.gate_idx_mprime, R=E, H=H, L=L)
+        else:
+            o1 = c.o1c
+            nat.gate_bwd(self.g_y, o1[:, LH:], o1, g1[:, LH:], g1, self.bb.gate_idx_mprime, R=E,
+                         H=H, L=L, ldx=LHc, ldg=LHc)
         gx = self.g_xf.view(E, NSPH * Cin)
         nat.linear_group([(g1[:, :LH + 3 * H], s1w.wm0, None, gx[:, :3 * Cin]),
                           (g1[:, LH + 3 * H:LH + 7 * H], s1w.w1_t, None, gx[:, 3 * Cin:7 * Cin]),

@@ -38,7 +38,8 @@ int tta_check_device(char* name_out, int64_t name_len);
 /* ---------------------------------------------------------------- dense contractions (MFMA)
  * C[b] = epi(A[b] @ B[b] + bias[b]); A [M,K] (lda), B [K,N] (ldb), C [M,N] (ldc), batch
  * strides sA/sB/sC/sBias.  epilogue: 0 store, 1 silu, 2 accumulate, 3 store v and silu(v) to
- * C2, 4 store v * silu'(aux), 5 sigmoid (6: the gate, tta_gemm_bf16x_group_gate only).
+ * C2, 4 store v * silu'(aux), 5 sigmoid (6 / 7: the gate and its input adjoint,
+ * tta_gemm_bf16x_group_gate / _gate_bwd only).
  * Replaces the ttnn.linear / ttnn.matmul calls of so2.py:106-115, 282-294 (SO(2) m-block GEMMs
  * with the [[Wa,Wb],[-Wb,Wa]] fused weight of so2.py:230-253), forces.py:23-36 (_mm transpose
  * GEMMs of the VJP), spectral.py:176-187, grid.py:64-75 and model.py:223-231 (energy head). */
@@ -98,6 +99,15 @@ int tta_gemm_bf16x_group_gate(const tta_gemm_problem* probs, int64_t n, int mode
                               const int64_t* c0, const float* sig, int64_t ldg, float* x0,
                               int64_t ldx0, int64_t H, const int* idx8, float* work,
                               int64_t work_floats, tta_stream_t stream);
+/* The adjoint products of that convolution's VJP (forces.py:23-36, the m-block transposes) with
+ * the gate's input adjoint applied as they are written (forces.py:104-130): every product has
+ * epilogue 7; coefficient 0: C = v silu'(x0), coefficient c > 0: C = v sig[row, idx8[c-1] H + h]
+ * (sig, x0 as kept by the forward; read only).  The gating adjoint follows from
+ * tta_gate_gating_bwd.  Same layout rules, checks and work as tta_gemm_bf16x_group_gate. */
+int tta_gemm_bf16x_group_gate_bwd(const tta_gemm_problem* probs, int64_t n, int mode,
+                                  const int64_t* c0, const float* sig, int64_t ldg,
+                                  const float* x0, int64_t ldx0, int64_t H, const int* idx8,
+                                  float* work, int64_t work_floats, tta_stream_t stream);
 int tta_gemm_f32_group(const tta_gemm_problem* probs, int64_t n, tta_stream_t stream);
 /* tta_gemm_f32_group for launches too small to fill the GPU (the node- and edge-level linears
  * of small systems, the same call sites).  When the products have fewer than 160 tiles of
@@ -182,8 +192,8 @@ int tta_node_gather_sum_dst(const float* g_mcat, const int* src_ptr, const int* 
  * Gate: y[r,0] = silu(x[r,0]); y[r,c] = x[r,c] sigmoid(gating[r, idx8[c-1]]).  x [R,9,H] rows of
  * stride ldx, gating [R, L*H] rows of stride ldg (column blocks of one GEMM output allowed),
  * y / g_y contiguous [R,9,H]; g_x / g_gating share the strides of x / gating.  idx8: 8 ints in
- * host memory (read while the launch is built; likewise for tta_gate_bwd_y and
- * tta_gemm_bf16x_group_gate).
+ * host memory (read while the launch is built; likewise for tta_gate_gating_bwd and
+ * tta_gemm_bf16x_group_gate(_bwd)).
  * activation.py:29-70 (m-primed idx), spectral.py:129-144 (natural idx); backward
  * forces.py:104-130 (and ttnn.experimental.fused_gate, fused_gate.hpp:14-21). */
 int tta_gate_fwd(const float* x, const float* gating, float* y, int64_t R, int64_t H, int64_t L,
@@ -191,15 +201,14 @@ int tta_gate_fwd(const float* x, const float* gating, float* y, int64_t R, int64
 int tta_gate_bwd(const float* g_y, const float* x, const float* gating, float* g_x,
                  float* g_gating, int64_t R, int64_t H, int64_t L, int64_t ldx, int64_t ldg,
                  const int* idx8, tta_stream_t stream);
-/* The gate backward (forces.py:104-130) from the gated output y of tta_gemm_bf16x_group_gate
- * instead of its input x: g_x[0] = g_y[0] silu'(x0), g_x[c] = g_y[c] sig[t_c],
- * g_gating[t] = (1 - sig[t]) sum of g_y[c] y[c] over the coefficients of index t (equal to
- * tta_gate_bwd's sigmoid'(gating) sum g_y x up to fp32 rounding).  sig = sigmoid(gating).
- * g_y, y contiguous [R,9,H]; sig, x0, g_x and g_gating rows of strides ldg, ldx0, ldgx, ldgg. */
-int tta_gate_bwd_y(const float* g_y, const float* y, const float* sig, const float* x0,
-                   float* g_x, float* g_gating, int64_t R, int64_t H, int64_t L, int64_t ldg,
-                   int64_t ldx0, int64_t ldgx, int64_t ldgg, const int* idx8,
-                   tta_stream_t stream);
+/* The gating adjoint of the gate above (forces.py:104-130) once the adjoint products have applied
+ * its input adjoint (tta_gemm_bf16x_group_gate_bwd wrote g_x): g_gating[t] =
+ * ((1 - sig[t]) / sig[t]) sum of g_x[c] y[c] over the coefficients c > 0 of index t, which is
+ * sigmoid'(gating[t]) sum g_y[c] x[c] (0 where sig underflowed to 0).  y the gated rows
+ * (contiguous [R,9,H]); g_x, sig and g_gating rows of strides ldgx, ldg, ldgg. */
+int tta_gate_gating_bwd(const float* g_x, const float* y, const float* sig, float* g_gating,
+                        int64_t R, int64_t H, int64_t L, int64_t ldgx, int64_t ldg, int64_t ldgg,
+                        const int* idx8, tta_stream_t stream);
 
 /* Radial MLP LayerNorm + SiLU: nrm = LN(a), s = silu(nrm) (so2.py:101-115) and its backward
  * g_a (so2.py:117-143; ttnn.experimental.fused_ln_bw, fused_ln_bw.hpp:14-21).  Row strides:

@@ -827,108 +827,81 @@ def test_gemm_gate_epilogue(nat, mode, M):
     assert ((y.cpu().double().view(M, 9, H) - yref).abs() / cmag).max() < 4e-6
 
 
-def test_gate_bwd_from_output(nat):
-    """tta_gate_bwd_y (the gate backward from the gated output, the gating sigmoids and
-    coefficient 0's pre-activation) against tta_gate_bwd (from the gate's input) and fp64
-    autograd, on strided operand views: coefficient 0's adjoint bit for bit, the rest to fp32
-    rounding (the sigmoids come from torch here)."""
-    R, H, L = 300, 48, 2
+@pytest.mark.parametrize("M", [5000, 700])
+def test_gemm_gate_bwd_epilogue(nat, M):
+    """The SO(2) conv-2 adjoint products with the gate's input adjoint applied in their epilogue
+    (tta_gemm_bf16x_group_gate_bwd) and the gating adjoint from them (tta_gate_gating_bwd), on
+    strided views of one [gating | coefficients] adjoint row: at M = 5000 the coefficient
+    adjoints equal the plain products followed by tta_gate_bwd bit for bit (the sigmoids come
+    from the GEMM's sigmoid epilogue on the same gating pre-activations) and the gating adjoint
+    matches it to fp32 rounding; at M = 700 (split-K) both match fp64."""
+    H, C, L = 48, 64, 2                                # K = 192, 256, 128: all on the split kernel
     idx = (0, 1, 0, 1, 0, 1, 1, 1)
-    g = torch.Generator().manual_seed(7)
-    x = torch.randn(R, 9, H, generator=g, dtype=torch.float64)
-    gat = torch.randn(R, L * H, generator=g, dtype=torch.float64)
-    gy = torch.randn(R, 9, H, generator=g, dtype=torch.float64)
-    xr, gr = x.clone().requires_grad_(True), gat.clone().requires_grad_(True)
-    sg = torch.sigmoid(gr).view(R, L, H)[:, list(idx), :]
-    yy = torch.cat([torch.nn.functional.silu(xr[:, :1]), xr[:, 1:] * sg], 1)
-    gx_ref, gg_ref = torch.autograd.grad((yy * gy).sum(), [xr, gr])
-    f = lambda t: t.float().to(DEV).contiguous()
-    y = torch.empty(R, 9, H, device=DEV)
-    nat.gate_fwd(f(x), f(gat), y, idx, R=R, H=H, L=L)
-    gxo, ggo = torch.empty(R, 9, H, device=DEV), torch.empty(R, L * H, device=DEV)
-    nat.gate_bwd(f(gy), f(x), f(gat), gxo, ggo, idx, R=R, H=H, L=L)
-    # the new kernel's operands as column blocks of wider rows
-    sig_w = torch.zeros(R, L * H + 8, device=DEV)
-    sig_w[:, 4:4 + L * H] = torch.sigmoid(f(gat))
-    x0_w = torch.zeros(R, 2 * H, device=DEV)
-    x0_w[:, H:] = f(x[:, 0])
-    g1 = torch.full((R, L * H + 9 * H), float("nan"), device=DEV)
-    nat.gate_bwd_y(f(gy), y, sig_w[:, 4:4 + L * H], x0_w[:, H:], g1[:, L * H:], g1[:, :L * H],
-                   idx, R=R, H=H, L=L)
+    g = torch.Generator().manual_seed(90 + M)
+    gm = torch.randn(M, 9 * C, generator=g)
+    gm[7] *= 2.0 ** -20
+    W0 = torch.randn(3 * C, 3 * H, generator=g) / math.sqrt(3 * C)
+    W1 = torch.randn(4 * C, 4 * H, generator=g) / math.sqrt(4 * C)
+    W2 = torch.randn(2 * C, 2 * H, generator=g) / math.sqrt(2 * C)
+    x = torch.randn(M, 9, H, generator=g)
+    gx_in = torch.randn(M, 64, generator=g)            # gating pre-activations = gx_in @ Wg + bg
+    Wg = torch.randn(64, L * H, generator=g) / 4.0
+    bg = torch.randn(L * H, generator=g)
+    P = lambda w: nat.PackedWeight(w.to(DEV).contiguous(), nat.SPLIT_F16X3)
+    Pg = P(Wg)
+    gat = torch.empty(M, L * H, device=DEV)
+    sig = torch.empty(M, L * H, device=DEV)
+    nat.linear(gx_in.to(DEV), Pg, bg.to(DEV), out=gat)
+    nat.linear(gx_in.to(DEV), Pg, bg.to(DEV), out=sig, epilogue=nat.EPI_SIGMOID)
+    xd = x.to(DEV)
+    y = torch.empty(M, 9, H, device=DEV)
+    nat.gate_fwd(xd, gat, y, idx, R=M, H=H, L=L)
+    x0 = xd[:, 0].contiguous()
+    gmd = gm.to(DEV)
+    LHc = L * H + 9 * H
+    g1 = torch.full((M, LHc), float("nan"), device=DEV)
+    nat.linear_group_gate([(gmd[:, :3 * C], P(W0), None, g1[:, L * H:L * H + 3 * H]),
+                           (gmd[:, 3 * C:7 * C], P(W1), None, g1[:, L * H + 3 * H:L * H + 7 * H]),
+                           (gmd[:, 7 * C:], P(W2), None, g1[:, L * H + 7 * H:])],
+                          (0, 3, 7), sig, x0, idx, H, backward=True)
+    nat.gate_gating_bwd(g1[:, L * H:], y, sig, g1[:, :L * H], idx, R=M, H=H, L=L)
     torch.cuda.synchronize()
-    gxn = g1[:, L * H:].view(R, 9, H)
-    assert torch.equal(gxn[:, 0], gxo[:, 0])
-    assert (gxn - gxo).abs().max() < 1e-6
-    gg = g1[:, :L * H].cpu().double()
-    assert (gg - ggo.cpu().double()).abs().max() < 1e-6
-    assert (gg - gg_ref).abs().max() < 1e-5
-    assert (gxn.cpu().double() - gx_ref).abs().max() < 1e-5
-@pytest.mark.parametrize("n", [16, 64, 100, 128, 200, 256, 512])
-def test_ln_silu_fwd_bwd(nat, n):
-    R = 301                     # odd: the last two-row wavefront of short rows has one row
-    g = torch.Generator().manual_seed(n)
-    a = torch.randn(R, n, generator=g, dtype=torch.float64) * 2 + 0.5
-    gam = 1 + 0.1 * torch.randn(n, generator=g, dtype=torch.float64)
-    bet = 0.1 * torch.randn(n, generator=g, dtype=torch.float64)
-    ar = a.clone().requires_grad_(True)
-    nrm = torch.nn.functional.layer_norm(ar, (n,), gam, bet, 1e-5)
-    s = torch.nn.functional.silu(nrm)
-    gs = torch.randn(R, n, generator=g, dtype=torch.float64)
-    (ga,) = torch.autograd.grad((s * gs).sum(), [ar])
-    f = lambda t: t.float().to(DEV).contiguous()
-    no, so, gao = (torch.empty(R, n, device=DEV) for _ in range(3))
-    nat.ln_silu_fwd(f(a), f(gam), f(bet), no, so, R=R, n=n)
-    nat.ln_silu_bwd(f(gs), f(a), no, f(gam), gao, R=R, n=n)
-    torch.cuda.synchronize()
-    assert (no.cpu().double() - nrm.detach()).abs().max() < 1e-5
-    assert (so.cpu().double() - s.detach()).abs().max() < 1e-5
-    assert (gao.cpu().double() - ga).abs().max() < 1e-4
-    # strided rows: a / nrm / g_a as a column block of a wider buffer
-    wide = torch.zeros(R, 3 * n, device=DEV)
-    wide[:, n:2 * n] = f(a)
-    nw, gw = torch.zeros(R, 3 * n, device=DEV), torch.zeros(R, 3 * n, device=DEV)
-    so2 = torch.empty(R, n, device=DEV)
-    nat.ln_silu_fwd(wide[:, n:2 * n], f(gam), f(bet), nw[:, n:2 * n], so2, R=R, n=n, lda=3 * n,
-                    lds=n)
-    nat.ln_silu_bwd(f(gs), wide[:, n:2 * n], nw[:, n:2 * n], f(gam), gw[:, n:2 * n], R=R, n=n,
-                    ldg=n, lda=3 * n, ldo=3 * n)
-    torch.cuda.synchronize()
-    assert torch.equal(so2, so) and torch.equal(gw[:, n:2 * n], gao)
-    assert gw[:, :n].abs().max() == 0 and gw[:, 2 * n:].abs().max() == 0
-    # nothing is written past row R - 1
-    nb, sb, gb = (torch.full((R + 1, n), float("nan"), device=DEV) for _ in range(3))
-    nat.ln_silu_fwd(f(a), f(gam), f(bet), nb[:R], sb[:R], R=R, n=n)
-    nat.ln_silu_bwd(f(gs), f(a), no, f(gam), gb[:R], R=R, n=n)
-    torch.cuda.synchronize()
-    assert torch.equal(nb[:R], no) and torch.equal(sb[:R], so) and torch.equal(gb[:R], gao)
-    assert all(bool(t[R].isnan().all()) for t in (nb, sb, gb))
-    # without the saved LayerNorm output: the forward does not write it, the backward recomputes
-    # it from a, gamma and beta -- the same values, so the same adjoint bit for bit
-    s3, g3 = torch.empty(R, n, device=DEV), torch.full((R + 1, n), float("nan"), device=DEV)
-    nat.ln_silu_fwd(f(a), f(gam), f(bet), None, s3, R=R, n=n)
-    nat.ln_silu_bwd(f(gs), f(a), None, f(gam), g3[:R], R=R, n=n, beta=f(bet))
-    torch.cuda.synchronize()
-    assert torch.equal(s3, so) and torch.equal(g3[:R], gao) and bool(g3[R].isnan().all())
-    with pytest.raises(RuntimeError):
-        nat.ln_silu_bwd(f(gs), f(a), None, f(gam), g3[:R], R=R, n=n)
-    # g 4 bytes off a 16-byte boundary sends the backward down the element-wise path while the
-    # forward (aligned rows) took the float4 one: the row statistics are summed in the same order
-    # on both paths, so the recomputed LayerNorm output and the adjoint equal the float4 ones
-    gbuf = torch.empty(R * n + 1, device=DEV)
-    gmis = gbuf[1:].view(R, n)
-    gmis.copy_(f(gs))
-    g4, g5 = torch.empty(R, n, device=DEV), torch.empty(R, n, device=DEV)
-    nat.ln_silu_bwd(gmis, f(a), None, f(gam), g4, R=R, n=n, beta=f(bet))
-    nat.ln_silu_bwd(gmis, f(a), no, f(gam), g5, R=R, n=n)
-    # and the forward on the element-wise path (misaligned LayerNorm output)
-    nbuf = torch.empty(R * n + 1, device=DEV)
-    nmis = nbuf[1:].view(R, n)
-    s6 = torch.empty(R, n, device=DEV)
-    nat.ln_silu_fwd(f(a), f(gam), f(bet), nmis, s6, R=R, n=n)
-    torch.cuda.synchronize()
-    for t, what in ((g4, "recomputed, element-wise"), (g5, "saved, element-wise")):
-        assert torch.equal(t, gao), f"{what} adjoint differs in {int((t != gao).sum())} elements"
-    assert torch.equal(nmis, no) and torch.equal(s6, so), "element-wise forward differs"
+    assert torch.isfinite(g1).all()
+    if M >= 4096:
+        gy = torch.empty(M, 9 * H, device=DEV)
+        nat.linear_group([(gmd[:, :3 * C], P(W0), None, gy[:, :3 * H]),
+                          (gmd[:, 3 * C:7 * C], P(W1), None, gy[:, 3 * H:7 * H]),
+                          (gmd[:, 7 * C:], P(W2), None, gy[:, 7 * H:])])
+        gxo, ggo = torch.empty(M, 9, H, device=DEV), torch.empty(M, L * H, device=DEV)
+        nat.gate_bwd(gy, xd, gat, gxo, ggo, idx, R=M, H=H, L=L)
+        torch.cuda.synchronize()
+        assert torch.equal(g1[:, L * H:].reshape(M, 9, H), gxo)
+        scale = ggo.abs().max().item()
+        assert (g1[:, :L * H] - ggo).abs().max().item() <= 2e-6 * scale
+        return
+    gy_ref = torch.cat([gm.double()[:, :3 * C] @ W0.double(), gm.double()[:, 3 * C:7 * C] @ W1.double(),
+                        gm.double()[:, 7 * C:] @ W2.double()], 1).view(M, 9, H)
+    gy_mag = torch.cat([gm.double()[:, :3 * C].abs() @ W0.double().abs(),
+                        gm.double()[:, 3 * C:7 * C].abs() @ W1.double().abs(),
+                        gm.double()[:, 7 * C:].abs() @ W2.double().abs()], 1).view(M, 9, H)
+    s64 = sig.cpu().double().view(M, L, H)
+    sc = s64[:, list(idx), :]
+    x64 = x.double()
+    sgrad0 = torch.sigmoid(x64[:, 0]) * (1 + x64[:, 0] * (1 - torch.sigmoid(x64[:, 0])))
+    gx_ref = torch.cat([gy_ref[:, :1] * sgrad0[:, None], gy_ref[:, 1:] * sc], 1)
+    gx_mag = torch.cat([gy_mag[:, :1] * (sgrad0.abs()[:, None] + 0.05), gy_mag[:, 1:] * sc], 1)
+    out = g1[:, L * H:].cpu().double().view(M, 9, H)
+    assert ((out - gx_ref).abs() / gx_mag).max() < 4e-6
+    gg_ref = torch.zeros(M, L, H, dtype=torch.float64)
+    gg_mag = torch.zeros(M, L, H, dtype=torch.float64)
+    for c in range(1, 9):
+        t = idx[c - 1]
+        gg_ref[:, t] += gy_ref[:, c] * x64[:, c]
+        gg_mag[:, t] += gy_mag[:, c] * x64[:, c].abs()
+    d = s64 * (1 - s64)
+    gg_ref, gg_mag = gg_ref * d, gg_mag * d
+    gg = g1[:, :L * H].cpu().double().view(M, L, H)
+    assert ((gg - gg_ref).abs() / (gg_mag + 1e-30)).max() < 1e-5
 
 
 @pytest.mark.parametrize("C", [16, 128, 96, 256, 300])

@@ -157,14 +157,15 @@ __device__ __forceinline__ void partial_rows(float* W, int M, int N, const float
   }
 }
 
-// EPI_GATE (ge, gc0: the launch's gate operands and the product's first coefficient) takes the
-// float4 path only (the host requires its alignments); a thread's four columns lie in one
-// coefficient (H % 4 == 0).
+// EPI_GATE / EPI_GATE_BWD (ge, gc0: the launch's gate operands and the product's first
+// coefficient) take the float4 path only (the host requires their alignments); a thread's four
+// columns lie in one coefficient (H % 4 == 0).
 template <int EPI, bool BATCH>
 __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct, int ldt,
                                               int rows, int row0, int n0, int t, int nth,
                                               bool vec_ok, bool full,
                                               const GateEpi* ge = nullptr, int gc0 = 0) {
+  constexpr bool GATE = EPI == EPI_GATE || EPI == EPI_GATE_BWD;
   const int c4 = t & 31, rstep = nth >> 5;
   const int col = n0 + 4 * c4;
   if (vec_ok && (full || col + 3 < p.N)) {
@@ -173,23 +174,35 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
     const bool gather = p.P != nullptr;
     // gate: coefficient gc of this thread's columns, their channel gh, gating column gcol
     int gc = 0, gh = 0, gcol = 0;
-    if constexpr (EPI == EPI_GATE) {
+    if constexpr (GATE) {
       gc = gate_coef(*ge, gc0, col);
       gh = col - (gc - gc0) * ge->H;
       gcol = gc > 0 ? gate_gcol(*ge, gc, gh) : 0;
     }
-    // gate epilogue of one float4: coefficient 0 stores its pre-activation and takes SiLU, the
-    // others are scaled by their gating sigmoids gv
+    // gate epilogue of one float4: coefficient 0 stores its pre-activation and takes SiLU (the
+    // backward: is multiplied by silu' of the stored x0 values gv), the others are scaled by their
+    // gating sigmoids gv
     auto gate4 = [&](floatx4& v, const floatx4& gv, int row) {
-      if (gc == 0) {
+      if (gc > 0) {
+        v = v * gv;
+      } else if constexpr (EPI == EPI_GATE) {
         __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(ge->x0 + (int64_t)row * ge->ldx0 + gh));
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = tta_silu(v[e]);
       } else {
-        v = v * gv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v[e] * tta_silu_grad(gv[e]);
       }
     };
-    constexpr bool LOADS = EPI == EPI_ACCUM || EPI == EPI_SILU_GRAD || EPI == EPI_GATE;
+    // the gate operand of one float4 of row `row`: its sigmoids, or (backward, coefficient 0) x0
+    auto gload = [&](int row) -> floatx4 {
+      if (gc > 0)
+        return *reinterpret_cast<const floatx4*>(ge->sig + (int64_t)row * ge->ldg + gcol);
+      if constexpr (EPI == EPI_GATE_BWD)
+        return *reinterpret_cast<const floatx4*>(ge->x0 + (int64_t)row * ge->ldx0 + gh);
+      return floatx4{0.f, 0.f, 0.f, 0.f};
+    };
+    constexpr bool LOADS = EPI == EPI_ACCUM || EPI == EPI_SILU_GRAD || GATE;
     constexpr int RB = 8;
     if (BATCH && full && (LOADS || gather) && rows % (RB * rstep) == 0) {
       // An epilogue that reads memory (the accumulated C, the SiLU argument, the gathered rows;
@@ -211,9 +224,7 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
             ex[i] = *reinterpret_cast<const floatx4*>(p.C + (int64_t)row * p.ldc + col);
           if constexpr (EPI == EPI_SILU_GRAD)
             ex[i] = *reinterpret_cast<const floatx4*>(p.aux + (int64_t)row * p.ldc + col);
-          if constexpr (EPI == EPI_GATE)
-            if (gc > 0)
-              ex[i] = *reinterpret_cast<const floatx4*>(ge->sig + (int64_t)row * ge->ldg + gcol);
+          if constexpr (GATE) ex[i] = gload(row);
         }
         if (gather) {
 #pragma unroll
@@ -228,7 +239,7 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
           const int64_t off = (int64_t)row * p.ldc + col;
           if (gather) v += pv[i];
           if constexpr (EPI == EPI_ACCUM) v += ex[i];
-          if constexpr (EPI == EPI_GATE) gate4(v, ex[i], row);
+          if constexpr (GATE) gate4(v, ex[i], row);
           if constexpr (EPI == EPI_SIGMOID) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = tta_sigmoid_acc(v[e]);
@@ -258,12 +269,7 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
         v += *reinterpret_cast<const floatx4*>(p.P + (int64_t)p.idx0[row] * p.ldp + col) +
              *reinterpret_cast<const floatx4*>(p.P + (int64_t)p.idx1[row] * p.ldp + p.off1 + col);
       if constexpr (EPI == EPI_ACCUM) v += *reinterpret_cast<const floatx4*>(p.C + off);
-      if constexpr (EPI == EPI_GATE) {
-        const floatx4 gv =
-            gc > 0 ? *reinterpret_cast<const floatx4*>(ge->sig + (int64_t)row * ge->ldg + gcol)
-                   : floatx4{0.f, 0.f, 0.f, 0.f};
-        gate4(v, gv, row);
-      }
+      if constexpr (GATE) gate4(v, gload(row), row);
       if constexpr (EPI == EPI_SIGMOID) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = tta_sigmoid_acc(v[e]);
@@ -288,7 +294,7 @@ __device__ __forceinline__ void epilogue_rows(const GemmArgs& p, const float* Ct
       // (+15-17 % on the write-heavy short-K shapes)
       __builtin_nontemporal_store(v, reinterpret_cast<floatx4*>(p.C + off));
     }
-  } else if constexpr (EPI != EPI_GATE) {
+  } else if constexpr (!GATE) {
     for (int rr = t >> 5; rr < rows; rr += rstep) {
       const int row = row0 + rr;
       if (row >= p.M) break;
@@ -772,6 +778,10 @@ __global__ __launch_bounds__(128 * WM, WM == 2 ? 2 : 1) void gemm_bf16x_kernel(G
           case EPI_GATE:
             epilogue_rows<EPI_GATE, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full,
                                             &g.gate, g.gc0[blockIdx.z]);
+            break;
+          case EPI_GATE_BWD:
+            epilogue_rows<EPI_GATE_BWD, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok,
+                                                full, &g.gate, g.gc0[blockIdx.z]);
             break;
           default:
             epilogue_rows<EPI_STORE, S::F16>(p, Ct, LDT, RP, cm0 + r0, cn0, t, NTH, vec_ok, full);
@@ -1272,12 +1282,12 @@ static int prepare_bf16x(const float* A, const void* Bp, float* C, const float* 
                          const float* aux, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldc, const float* P, int64_t ldp, const int* idx0,
                          const int* idx1, int64_t off1, int64_t n_rows_p, int epilogue,
-                         GemmGroup& g, int slot, bool* skip, bool gate = false) {
+                         GemmGroup& g, int slot, bool* skip, int gate_epi = 0) {
   *skip = false;
   TTA_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "tta_gemm_bf16x: negative size");
   TTA_CHECK_ARG(M < (int64_t)1 << 31 && N < (int64_t)1 << 30 && K < (int64_t)1 << 30,
                 "tta_gemm_bf16x: size exceeds int32");
-  TTA_CHECK_ARG(gate ? epilogue == EPI_GATE : (epilogue >= 0 && epilogue <= EPI_SIGMOID),
+  TTA_CHECK_ARG(gate_epi ? epilogue == gate_epi : (epilogue >= 0 && epilogue <= EPI_SIGMOID),
                 "tta_gemm_bf16x: bad epilogue %d", epilogue);
   TTA_CHECK_ARG(epilogue != EPI_PRE_SILU || C2, "tta_gemm_bf16x: epilogue 3 needs C2");
   TTA_CHECK_ARG(epilogue != EPI_SILU_GRAD || aux, "tta_gemm_bf16x: epilogue 4 needs aux");
@@ -1361,12 +1371,15 @@ extern "C" int64_t tta_gemm_bf16x_splitk_work(const tta_gemm_problem* probs, int
 }
 
 // tta_gemm_bf16x_group with the k chunks of tta_gemm_bf16x_splitk_work (no row gathers); work
-// NULL: never split.  gate (g.gate set by the caller): every product has the gate epilogue, with
-// first coefficient c0[i].
+// NULL: never split.  gate_epi (EPI_GATE or EPI_GATE_BWD, g.gate set by the caller): every
+// product has that epilogue, with first coefficient c0[i].
 static int group_splitk_impl(const tta_gemm_problem* probs, int64_t n, int mode, float* work,
-                             int64_t work_floats, hipStream_t stream, GemmGroup& g, bool gate,
+                             int64_t work_floats, hipStream_t stream, GemmGroup& g, int gate_epi,
                              const int64_t* c0) {
-  const char* who = gate ? "tta_gemm_bf16x_group_gate" : "tta_gemm_bf16x_group_splitk";
+  const bool gate = gate_epi != 0;
+  const char* who = gate_epi == EPI_GATE       ? "tta_gemm_bf16x_group_gate"
+                    : gate_epi == EPI_GATE_BWD ? "tta_gemm_bf16x_group_gate_bwd"
+                                               : "tta_gemm_bf16x_group_splitk";
   TTA_CHECK_ARG(planes_of(mode) > 0, "%s: mode must be 1, 3, 6 or 16 (got %d)", who, mode);
   TTA_CHECK_ARG(n >= 0 && n <= kMaxGroup && (probs || n == 0), "%s: 0..%d products", who,
                 kMaxGroup);
@@ -1375,12 +1388,12 @@ static int group_splitk_impl(const tta_gemm_problem* probs, int64_t n, int mode,
   int64_t need = 0, max_chunks = 1, max_mn = 0;
   for (int64_t i = 0; i < n; ++i) {
     const tta_gemm_problem& q = probs[i];
-    TTA_CHECK_ARG(gate ? q.epilogue == EPI_GATE : (q.epilogue >= 0 && q.epilogue <= EPI_SIGMOID),
+    TTA_CHECK_ARG(gate ? q.epilogue == gate_epi : (q.epilogue >= 0 && q.epilogue <= EPI_SIGMOID),
                   "%s: bad epilogue %lld", who, (long long)q.epilogue);
     bool skip = false;
     const int rc = prepare_bf16x(q.A, q.B, q.C, q.bias, q.C2, q.aux, q.M, q.N, q.K, q.lda, q.ldc,
                                  nullptr, 0, nullptr, nullptr, 0, 0, (int)q.epilogue, g, m,
-                                 &skip, gate);
+                                 &skip, gate_epi);
     if (rc != tta::kOk) return rc;
     if (skip) continue;
     TTA_CHECK_ARG(q.K > 0, "%s: K must be positive", who);
@@ -1423,27 +1436,47 @@ extern "C" int tta_gemm_bf16x_group_splitk(const tta_gemm_problem* probs, int64_
                                            float* work, int64_t work_floats,
                                            hipStream_t stream) {
   GemmGroup g{};
-  return group_splitk_impl(probs, n, mode, work, work_floats, stream, g, false, nullptr);
+  return group_splitk_impl(probs, n, mode, work, work_floats, stream, g, 0, nullptr);
+}
+
+// the gate operands shared by the forward and backward gate entries
+static int gate_setup(GemmGroup& g, const char* who, const int64_t* c0, const float* sig,
+                      int64_t ldg, const float* x0, int64_t ldx0, int64_t H, const int* idx8) {
+  TTA_CHECK_ARG(c0 && idx8 && sig && x0, "%s: null pointer", who);
+  TTA_CHECK_ARG(H > 0 && H % 4 == 0 && H < (1 << 20), "%s: H = %lld must be a positive multiple "
+                "of 4", who, (long long)H);
+  unsigned tab = 0;
+  int tmax = 0;
+  for (int c = 0; c < 8; ++c) {
+    TTA_CHECK_ARG(idx8[c] >= 0 && idx8[c] < 15, "%s: bad gate index", who);
+    tab |= (unsigned)idx8[c] << (4 * c);
+    tmax = std::max(tmax, idx8[c]);
+  }
+  TTA_CHECK_ARG(ldg >= (tmax + 1) * H && ldg % 4 == 0 && ldx0 >= H && ldx0 % 4 == 0 &&
+                    (uintptr_t)sig % 16 == 0 && (uintptr_t)x0 % 16 == 0,
+                "%s: sig / x0 rows too short or not 16-byte aligned", who);
+  g.gate = GateEpi{sig, const_cast<float*>(x0), ldg, ldx0, (int)H, tab};
+  return tta::kOk;
 }
 
 extern "C" int tta_gemm_bf16x_group_gate(const tta_gemm_problem* probs, int64_t n, int mode,
                                          const int64_t* c0, const float* sig, int64_t ldg,
                                          float* x0, int64_t ldx0, int64_t H, const int* idx8,
                                          float* work, int64_t work_floats, hipStream_t stream) {
-  TTA_CHECK_ARG(c0 && idx8 && sig && x0, "tta_gemm_bf16x_group_gate: null pointer");
-  TTA_CHECK_ARG(H > 0 && H % 4 == 0 && H < (1 << 20), "tta_gemm_bf16x_group_gate: H = %lld must "
-                "be a positive multiple of 4", (long long)H);
   GemmGroup g{};
-  unsigned tab = 0;
-  int tmax = 0;
-  for (int c = 0; c < 8; ++c) {
-    TTA_CHECK_ARG(idx8[c] >= 0 && idx8[c] < 15, "tta_gemm_bf16x_group_gate: bad gate index");
-    tab |= (unsigned)idx8[c] << (4 * c);
-    tmax = std::max(tmax, idx8[c]);
-  }
-  TTA_CHECK_ARG(ldg >= (tmax + 1) * H && ldg % 4 == 0 && ldx0 >= H && ldx0 % 4 == 0 &&
-                    (uintptr_t)sig % 16 == 0 && (uintptr_t)x0 % 16 == 0,
-                "tta_gemm_bf16x_group_gate: sig / x0 rows too short or not 16-byte aligned");
-  g.gate = GateEpi{sig, x0, ldg, ldx0, (int)H, tab};
-  return group_splitk_impl(probs, n, mode, work, work_floats, stream, g, true, c0);
+  const int rc = gate_setup(g, "tta_gemm_bf16x_group_gate", c0, sig, ldg, x0, ldx0, H, idx8);
+  if (rc != tta::kOk) return rc;
+  return group_splitk_impl(probs, n, mode, work, work_floats, stream, g, EPI_GATE, c0);
+}
+
+extern "C" int tta_gemm_bf16x_group_gate_bwd(const tta_gemm_problem* probs, int64_t n, int mode,
+                                             const int64_t* c0, const float* sig, int64_t ldg,
+                                             const float* x0, int64_t ldx0, int64_t H,
+                                             const int* idx8, float* work, int64_t work_floats,
+                                             hipStream_t stream) {
+  GemmGroup g{};
+  const int rc =
+      gate_setup(g, "tta_gemm_bf16x_group_gate_bwd", c0, sig, ldg, x0, ldx0, H, idx8);
+  if (rc != tta::kOk) return rc;
+  return group_splitk_impl(probs, n, mode, work, work_floats, stream, g, EPI_GATE_BWD, c0);
 }

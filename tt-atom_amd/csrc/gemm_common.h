@@ -11,7 +11,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 namespace tta_gemm {
 
 enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ACCUM = 2, EPI_PRE_SILU = 3, EPI_SILU_GRAD = 4,
-       EPI_SIGMOID = 5, EPI_GATE = 6 };
+       EPI_SIGMOID = 5, EPI_GATE = 6, EPI_GATE_BWD = 7 };
 
 // The gate epilogue (EPI_GATE, split kernel only) of one launch: a product's output column col
 // is channel h = col % H of SH coefficient c = c0 + col / H (c0 per product, GemmGroup::gc0).
@@ -19,7 +19,9 @@ enum { EPI_STORE = 0, EPI_SILU = 1, EPI_ACCUM = 2, EPI_PRE_SILU = 3, EPI_SILU_GR
 // coefficient c > 0 is multiplied by sig[row * ldg + t * H + h], the sigmoid of the gating
 // columns (an earlier launch with the EPI_SIGMOID epilogue), with degree index
 // t = (tab >> 4 (c - 1)) & 15 -- the GateActivation of an SO(2) convolution's output applied as
-// the convolution writes it (activation.py:53-70).
+// the convolution writes it (activation.py:53-70).  EPI_GATE_BWD, the adjoint of the gate's
+// input applied as the adjoint products write it (forces.py:104-130): coefficient 0 is multiplied
+// by silu'(x0), coefficient c > 0 by the same sigmoid.
 struct GateEpi {
   const float* sig;
   float* x0;
@@ -158,14 +160,16 @@ static __global__ __launch_bounds__(256) void k_splitk_reduce(GemmGroup g) {
     for (int s = 1; s < ns; ++s) v += W[s * MN + i];
     if (p.bias) v += p.bias[col];
     const int64_t off = (int64_t)row * p.ldc + col;
-    if (p.epi == EPI_GATE) {
+    if (p.epi == EPI_GATE || p.epi == EPI_GATE_BWD) {
       const GateEpi& ge = g.gate;
       const int c = gate_coef(ge, g.gc0[blockIdx.z], col), h = col - (c - g.gc0[blockIdx.z]) * ge.H;
-      if (c == 0) {
+      if (c > 0) {
+        v *= ge.sig[(int64_t)row * ge.ldg + gate_gcol(ge, c, h)];
+      } else if (p.epi == EPI_GATE) {
         ge.x0[(int64_t)row * ge.ldx0 + h] = v;
         v = tta_silu(v);
       } else {
-        v *= ge.sig[(int64_t)row * ge.ldg + gate_gcol(ge, c, h)];
+        v *= tta_silu_grad(ge.x0[(int64_t)row * ge.ldx0 + h]);
       }
     }
     if (p.epi == EPI_SILU) v = tta_silu(v);

@@ -65,38 +65,31 @@ __global__ __launch_bounds__(256) void k_gate_bwd(const float* __restrict__ g_y,
   for (int t = 0; t < L; ++t) g_gating[r * ldg + t * H + h] = acc[t] * (sg[t] * (1.f - sg[t]));
 }
 
-// Backward from the gated output, for a forward whose gate ran in the producing GEMM's epilogue
-// (which keeps y, the gating sigmoids sig and coefficient 0's pre-activation x0, not x):
-//   g_x[0] = g_y[0] silu'(x0),  g_x[c] = g_y[c] sig[t_c],
-//   g_gating[t] = (1 - sig[t]) sum over c of degree index t of g_y[c] y[c]
-// -- y[c] = x[c] sig[t], so the sum is sigmoid'(gating[t]) sum g_y[c] x[c], the gating adjoint
-// of forces.py:104-130.  g_y and y are contiguous [R, 9, H]; the other operands have their own
-// row strides.
-__global__ __launch_bounds__(256) void k_gate_bwd_y(
-    const float* __restrict__ g_y, const float* __restrict__ y, const float* __restrict__ sig,
-    const float* __restrict__ x0, float* __restrict__ g_x, float* __restrict__ g_gating,
-    int64_t R, int H, int L, int64_t ldg, int64_t ldx0, int64_t ldgx, int64_t ldgg, GateIdx idx) {
+// The gating adjoint of a gate whose forward ran in the producing GEMM's epilogue and whose input
+// adjoint g_x (g_x[c] = g_y[c] s[t_c], coefficient 0 aside) the adjoint GEMM's epilogue wrote:
+// with y[c] = x[c] s[t] (the gated rows kept from the forward) and s = sigmoid(gating),
+//   g_gating[t] = sigmoid'(gating[t]) sum_c g_y[c] x[c] = ((1 - s[t]) / s[t]) sum_c g_x[c] y[c]
+// over the coefficients c > 0 of degree index t (forces.py:104-130); an s that underflowed to 0
+// gives 0 (its true value is below 2^-126 times the sum).  y contiguous [R, 9, H]; g_x, sig and
+// g_gating have their own row strides.
+__global__ __launch_bounds__(256) void k_gate_gating_bwd(
+    const float* __restrict__ g_x, const float* __restrict__ y, const float* __restrict__ sig,
+    float* __restrict__ g_gating, int64_t R, int H, int L, int64_t ldgx, int64_t ldg,
+    int64_t ldgg, GateIdx idx) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= R * H) return;
   const int64_t r = gid / H;
   const int h = (int)(gid % H);
   const float* yr = y + r * 9 * H;
-  const float* gr = g_y + r * 9 * H;
-  float* gx = g_x + r * ldgx;
-  float sg[8], acc[8];
-  for (int t = 0; t < L; ++t) {
-    sg[t] = sig[r * ldg + t * H + h];
-    acc[t] = 0.f;
-  }
-  __builtin_nontemporal_store(gr[h] * tta_silu_grad(x0[r * ldx0 + h]), gx + h);
+  const float* gr = g_x + r * ldgx;
+  float acc[8];
+  for (int t = 0; t < L; ++t) acc[t] = 0.f;
 #pragma unroll
-  for (int c = 1; c < 9; ++c) {
-    const int t = idx.v[c - 1];
-    const float g = gr[c * H + h];
-    __builtin_nontemporal_store(g * sg[t], gx + c * H + h);
-    acc[t] += g * yr[c * H + h];
+  for (int c = 1; c < 9; ++c) acc[idx.v[c - 1]] += gr[c * H + h] * yr[c * H + h];
+  for (int t = 0; t < L; ++t) {
+    const float sg = sig[r * ldg + t * H + h];
+    g_gating[r * ldgg + t * H + h] = sg > 0.f ? acc[t] * ((1.f - sg) / sg) : 0.f;
   }
-  for (int t = 0; t < L; ++t) g_gating[r * ldgg + t * H + h] = acc[t] * (1.f - sg[t]);
 }
 
 // ------------------------------------------------------------------ LayerNorm + SiLU (radial MLP)
@@ -568,24 +561,24 @@ extern "C" int tta_gate_bwd(const float* g_y, const float* x, const float* gatin
   return tta::kOk;
 }
 
-extern "C" int tta_gate_bwd_y(const float* g_y, const float* y, const float* sig,
-                              const float* x0, float* g_x, float* g_gating, int64_t R, int64_t H,
-                              int64_t L, int64_t ldg, int64_t ldx0, int64_t ldgx, int64_t ldgg,
-                              const int* idx8, hipStream_t stream) {
-  TTA_CHECK_ARG(R >= 0 && H > 0 && L >= 1 && L <= 8, "tta_gate_bwd_y: bad sizes");
-  TTA_CHECK_ARG(ldg >= L * H && ldx0 >= H && ldgx >= 9 * H && ldgg >= L * H,
-                "tta_gate_bwd_y: row stride too small");
-  TTA_CHECK_ARG(idx8, "tta_gate_bwd_y: null index table");
+extern "C" int tta_gate_gating_bwd(const float* g_x, const float* y, const float* sig,
+                                   float* g_gating, int64_t R, int64_t H, int64_t L,
+                                   int64_t ldgx, int64_t ldg, int64_t ldgg, const int* idx8,
+                                   hipStream_t stream) {
+  TTA_CHECK_ARG(R >= 0 && H > 0 && L >= 1 && L <= 8, "tta_gate_gating_bwd: bad sizes");
+  TTA_CHECK_ARG(ldgx >= 9 * H && ldg >= L * H && ldgg >= L * H,
+                "tta_gate_gating_bwd: row stride too small");
+  TTA_CHECK_ARG(idx8, "tta_gate_gating_bwd: null index table");
   GateIdx gi;
   for (int i = 0; i < 8; ++i) {
-    TTA_CHECK_ARG(idx8[i] >= 0 && idx8[i] < L, "tta_gate_bwd_y: gate index out of range");
+    TTA_CHECK_ARG(idx8[i] >= 0 && idx8[i] < L, "tta_gate_gating_bwd: gate index out of range");
     gi.v[i] = idx8[i];
   }
   if (R == 0) return tta::kOk;
-  TTA_CHECK_ARG(g_y && y && sig && x0 && g_x && g_gating, "tta_gate_bwd_y: null pointer");
-  hipLaunchKernelGGL(k_gate_bwd_y, dim3(tta_blocks(R * H, 256)), dim3(256), 0, stream, g_y, y,
-                     sig, x0, g_x, g_gating, R, (int)H, (int)L, ldg, ldx0, ldgx, ldgg, gi);
-  TTA_CHECK_LAUNCH("tta_gate_bwd_y");
+  TTA_CHECK_ARG(g_x && y && sig && g_gating, "tta_gate_gating_bwd: null pointer");
+  hipLaunchKernelGGL(k_gate_gating_bwd, dim3(tta_blocks(R * H, 256)), dim3(256), 0, stream, g_x,
+                     y, sig, g_gating, R, (int)H, (int)L, ldgx, ldg, ldgg, gi);
+  TTA_CHECK_LAUNCH("tta_gate_gating_bwd");
   return tta::kOk;
 }
 

@@ -51,7 +51,7 @@ _SIGS = {
     "tta_node_gather_sum": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_gate_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "tta_gate_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
-    "tta_gate_bwd_y": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P],
+    "tta_gate_gating_bwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "tta_ln_silu_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "tta_ln_silu_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "tta_rmsnorm_sh_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _P],
@@ -99,6 +99,8 @@ _SIGS = {
     "tta_gemm_bf16x_group_splitk": [ctypes.POINTER(GemmProblem), _I64, _I, _P, _I64, _P],
     "tta_gemm_bf16x_group_gate": [ctypes.POINTER(GemmProblem), _I64, _I, _P, _P, _I64, _P, _I64,
                                   _I64, _P, _P, _I64, _P],
+    "tta_gemm_bf16x_group_gate_bwd": [ctypes.POINTER(GemmProblem), _I64, _I, _P, _P, _I64, _P,
+                                      _I64, _I64, _P, _P, _I64, _P],
     "tta_gemm_f32_group_splitk": [ctypes.POINTER(GemmProblem), _I64, _P, _I64, _P],
     "tta_radius_graph_thresholds": [_P, _I64, _P, _P, _P, _I64, _P, _P, _I, _D, _F, _F, _I, _P,
                                     _P, _P, _P, _P],
@@ -215,7 +217,7 @@ def _rows(t, rows, ld, width, name="tensor"):
 # ----------------------------------------------------------------------------- GEMM
 EPI_STORE, EPI_SILU, EPI_ACCUM, EPI_PRE_SILU, EPI_SILU_GRAD = 0, 1, 2, 3, 4
 EPI_SIGMOID = 5
-EPI_GATE = 6  # tta_gemm_bf16x_group_gate only
+EPI_GATE, EPI_GATE_BWD = 6, 7  # tta_gemm_bf16x_group_gate / _gate_bwd only
 
 # Optional measurement hook: when set, every GEMM launch is bracketed by
 # ``probe.before(flops, nbytes, kind)`` and ``probe.after()`` (the benchmark records HIP events on
@@ -404,13 +406,15 @@ def _small_split(items):
     return True
 
 
-def linear_group_gate(items, c0, sig, x0, idx8, H):
+def linear_group_gate(items, c0, sig, x0, idx8, H, backward=False):
     """The coefficient products of an SO(2) convolution with its gate applied as they are
     written (tta_gemm_bf16x_group_gate): ``items`` = [(x, PackedWeight, bias, out)], product i's
     columns being coefficients c0[i], c0[i] + 1, ... of H channels each; ``sig`` [M, L * H]
     the sigmoid of the convolution's gating columns (any row stride; linear() with
-    EPI_SIGMOID), ``x0`` [M, H] receives coefficient 0's pre-activation.  Launches with fewer than 4096 rows take the split-K form when the library's
-    rule splits them."""
+    EPI_SIGMOID), ``x0`` [M, H] receives coefficient 0's pre-activation.  ``backward``: the
+    adjoint products with the gate's input adjoint applied instead
+    (tta_gemm_bf16x_group_gate_bwd; x0 is read).  Launches with fewer than 4096 rows take the
+    split-K form when the library's rule splits them."""
     if not items or len(items) > MAX_GROUP or len(c0) != len(items):
         raise RuntimeError("linear_group_gate: 1..8 products, one first coefficient each")
     mode = items[0][1].mode
@@ -432,7 +436,8 @@ def linear_group_gate(items, c0, sig, x0, idx8, H):
         probs[i] = GemmProblem(_rows(x, M, _ld(x, "x"), K, "x"), w.packed.data_ptr(),
                                _rows(out, M, ldc, N, "out"),
                                None if bias is None else _ptr(bias, numel=N, name="bias"),
-                               None, None, M, N, K, _ld(x, "x"), 0, ldc, EPI_GATE)
+                               None, None, M, N, K, _ld(x, "x"), 0, ldc,
+                               EPI_GATE_BWD if backward else EPI_GATE)
         flops += 2.0 * M * N * K
         # A, B, the output and a gating sigmoid per gated output (coefficient 0: its x0 copy)
         nbytes += 4.0 * (M * K + K * N + 2 * M * N)
@@ -448,7 +453,8 @@ def linear_group_gate(items, c0, sig, x0, idx8, H):
     probe = _gemm_probe
     if probe is not None:
         probe.before(flops, nbytes, MODE_KIND[mode])
-    _call("tta_gemm_bf16x_group_gate", probs, len(items), mode,
+    _call("tta_gemm_bf16x_group_gate_bwd" if backward else "tta_gemm_bf16x_group_gate", probs,
+          len(items), mode,
           (ctypes.c_int64 * len(items))(*c0), gp, _ld(sig, "sig"), xp, _ld(x0, "x0"), H,
           _host_idx8(idx8), None if work is None else work.data_ptr(),
           0 if work is None else work.numel(), _stream())
@@ -775,17 +781,15 @@ def gate_bwd(g_y, x, gating, g_x, g_gating, idx8, *, R, H, L, ldx=None, ldg=None
               _stream())
 
 
-def gate_bwd_y(g_y, y, sig, x0, g_x, g_gating, idx8, *, R, H, L):
-    """The gate backward from the gated output y (contiguous [R, 9, H], as g_y), the gating
-    sigmoids sig and coefficient 0's pre-activation x0 (tta_gate_bwd_y); sig, x0, g_x and
-    g_gating are row-strided 2-D views."""
-    ldg, ldx0, ldgx, ldgg = (_ld(t, nm) for t, nm in ((sig, "sig"), (x0, "x0"),
-                                                      (g_x, "g_x"), (g_gating, "g_gating")))
-    _hbm_call("k_gate_bwd_y", 4 * R * H * (27 + 2 * L), "tta_gate_bwd_y",
-              _ptr(g_y, numel=R * 9 * H, name="g_y"), _ptr(y, numel=R * 9 * H, name="y"),
-              _rows(sig, R, ldg, L * H, "sig"), _rows(x0, R, ldx0, H, "x0"),
-              _rows(g_x, R, ldgx, 9 * H, "g_x"), _rows(g_gating, R, ldgg, L * H, "g_gating"),
-              R, H, L, ldg, ldx0, ldgx, ldgg, _host_idx8(idx8), _stream())
+def gate_gating_bwd(g_x, y, sig, g_gating, idx8, *, R, H, L):
+    """The gating adjoint from the gate's input adjoint g_x (written by linear_group_gate with
+    backward=True), the gated rows y (contiguous [R, 9, H]) and the gating sigmoids sig
+    (tta_gate_gating_bwd); g_x, sig and g_gating are row-strided 2-D views."""
+    ldgx, ldg, ldgg = (_ld(t, nm) for t, nm in ((g_x, "g_x"), (sig, "sig"), (g_gating, "g_gating")))
+    _hbm_call("k_gate_gating_bwd", 4 * R * H * (16 + 2 * L), "tta_gate_gating_bwd",
+              _rows(g_x, R, ldgx, 9 * H, "g_x"), _ptr(y, numel=R * 9 * H, name="y"),
+              _rows(sig, R, ldg, L * H, "sig"), _rows(g_gating, R, ldgg, L * H, "g_gating"),
+              R, H, L, ldgx, ldg, ldgg, _host_idx8(idx8), _stream())
 
 
 def ln_silu_fwd(a, gamma, beta, nrm, s, *, R, n, groups=1, lda=None, lds=None, eps=1e-5):

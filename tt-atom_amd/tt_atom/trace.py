@@ -90,9 +90,9 @@ class TracedEngine:
         # shared edge temporaries
         self.LHc = L * H + NSPH * H                      # combined conv-1 row [gating | out]
         self.xf, self.g_xf, self.g_mcat = emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C)
-        self.g_y = emp(E, NSPH, H)
         if not all(b.so2_1.gate_split for b in bb.blocks):
-            self.y = emp(E, NSPH, H)                     # gated conv-1 rows of the unsplit path
+            # the gated conv-1 rows and their adjoint on the path with the gate as its own pass
+            self.y, self.g_y = emp(E, NSPH, H), emp(E, NSPH, H)
         self.g_tsum = emp(N, NSPH, C)                    # per-node destination adjoint sums
         self.g1c = emp(E, self.LHc)
         self.g_mso2 = emp(E, NSPH, C)
@@ -343,15 +343,23 @@ class TracedEngine:
         nat.rotate_env_segsum_bw(g_x1, g.tgt, c.mso2, self.coef, self.env, self.g_mso2,
                                  self.g_coef, self.g_env, n_in=9, env_first=True)
         gm = self.g_mso2.view(E, NSPH * C)
-        gy = self.g_y.view(E, NSPH * H)
-        nat.linear_group([(gm[:, :3 * C], s2w.wm0, None, gy[:, :3 * H]),
-                          (gm[:, 3 * C:7 * C], s2w.w1_t, None, gy[:, 3 * H:7 * H]),
-                          (gm[:, 7 * C:], s2w.w2_t, None, gy[:, 7 * H:])])
         g1 = self.g1c
         if s1w.gate_split:
-            nat.gate_bwd_y(self.g_y, c.y1, c.sig1, c.x01, g1[:, LH:], g1[:, :LH],
-                           self.bb.gate_idx_mprime, R=E, H=H, L=L)
+            # conv-2's adjoint products with the gate's input adjoint applied as they are written
+            # (straight into the coefficient part of conv-1's adjoint operand), then the gating
+            # adjoint from them and the kept gated rows
+            nat.linear_group_gate([(gm[:, :3 * C], s2w.wm0, None, g1[:, LH:LH + 3 * H]),
+                                   (gm[:, 3 * C:7 * C], s2w.w1_t, None, g1[:, LH + 3 * H:LH + 7 * H]),
+                                   (gm[:, 7 * C:], s2w.w2_t, None, g1[:, LH + 7 * H:])],
+                                  (0, 3, 7), c.sig1, c.x01, self.bb.gate_idx_mprime, H,
+                                  backward=True)
+            nat.gate_gating_bwd(g1[:, LH:], c.y1, c.sig1, g1[:, :LH], self.bb.gate_idx_mprime,
+                                R=E, H=H, L=L)
         else:
+            gy = self.g_y.view(E, NSPH * H)
+            nat.linear_group([(gm[:, :3 * C], s2w.wm0, None, gy[:, :3 * H]),
+                              (gm[:, 3 * C:7 * C], s2w.w1_t, None, gy[:, 3 * H:7 * H]),
+                              (gm[:, 7 * C:], s2w.w2_t, None, gy[:, 7 * H:])])
             o1 = c.o1c
             nat.gate_bwd(self.g_y, o1[:, LH:], o1, g1[:, LH:], g1, self.bb.gate_idx_mprime, R=E,
                          H=H, L=L, ldx=LHc, ldg=LHc)

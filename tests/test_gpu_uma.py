@@ -77,8 +77,8 @@ def _system_embedding(w, cfg, n, charge=0, spin=1):
 
 @pytest.mark.parametrize("precision", ["f32", "f32-mfma"])
 def test_c1_tiny(golden, precision):
-    """C1 with packed weights (the gate applied in the conv-1 products' epilogue) and with the
-    fp32 MFMA kernel only (ungated conv-1 output, then the gate pass)."""
+    """C1 with packed weights and with the fp32 MFMA kernel only (both below the 4096 edges from
+    which the gate runs in the SO(2) GEMM epilogues: the gate passes)."""
     from tt_atom import synthetic
     from tt_atom.geometry import radius_graph
     cfg = dict(synthetic.CFG_C1)
@@ -91,6 +91,7 @@ def test_c1_tiny(golden, precision):
     eng, _ = _check(w, cfg, host, pos, Z, ei, _system_embedding(w, cfg, len(Z)),
                     label=f"C1 {precision}", precision=precision)
     assert all(b.so2_1.gate_split == (precision == "f32") for b in eng.bb.blocks)
+    assert not eng.gate_fused
 
 
 def test_c3_reduced():
@@ -103,6 +104,7 @@ def test_c3_reduced():
     pos, Z = torch.from_numpy(pos), torch.from_numpy(Z)
     ei, _ = radius_graph(pos, cfg["cutoff"], max_neighbors=cfg["max_neighbors"])
     eng, out = _check(w, cfg, host, pos, Z, ei, _system_embedding(w, cfg, len(Z)), label="C3-256")
+    assert eng.gate_fused                   # 256 atoms at the C3 density: over 4096 edges
     # fixed topology: a second step is bit-identical (deterministic reductions, no atomics)
     out2 = eng(pos.cuda())
     assert out2[0] == out[0] and torch.equal(out2[1], out[1])

@@ -90,7 +90,11 @@ class TracedEngine:
         # shared edge temporaries
         self.LHc = L * H + NSPH * H                      # combined conv-1 row [gating | out]
         self.xf, self.g_xf, self.g_mcat = emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C)
-        if not all(b.so2_1.gate_split for b in bb.blocks):
+        # the gate in the SO(2) GEMM epilogues for edge-level launches on the split kernel; below
+        # 4096 edges (launch-latency bound) the separate gating product would add launches, so
+        # the gate keeps its own passes there
+        self.gate_fused = E >= 4096 and all(b.so2_1.gate_split for b in bb.blocks)
+        if not self.gate_fused:
             # the gated conv-1 rows and their adjoint on the path with the gate as its own pass
             self.y, self.g_y = emp(E, NSPH, H), emp(E, NSPH, H)
         self.g_tsum = emp(N, NSPH, C)                    # per-node destination adjoint sums
@@ -107,7 +111,7 @@ class TracedEngine:
             c.inv1, c.inv2 = emp(N), emp(N)
             c.rad = self._radial_cache(E, 6 * 2 * C, dev, 1 + i)
             c.mso2 = emp(E, NSPH, C)
-            if b.so2_1.gate_split:
+            if self.gate_fused:
                 # the gate runs in the conv-1 epilogue: gating sigmoids, the gated rows (conv-2's
                 # input, kept for the backward) and coefficient 0's pre-activation
                 c.sig1, c.y1, c.x01 = emp(E, L * H), emp(E, NSPH, H), emp(E, H)
@@ -243,7 +247,7 @@ class TracedEngine:
                 nat.rmsnorm_sh_fwd(c.x_in, bw.norm_1.aw, bw.norm_1.ab, self.sys_emb, c.n1, c.inv1)
             nat.gather_rotate(c.n1, g.src, g.tgt, self.coef, c.rad.out, self.xf)
             xf = self.xf.view(E, NSPH * Cin)
-            if s1w.gate_split:
+            if self.gate_fused:
                 # the gating columns' sigmoids first, then the three m-block contractions (m = 0,
                 # 1, 2: one launch) with the gate applied as their rows are written
                 nat.linear(xf[:, :3 * Cin], s1w.wm0g_t, s1w.bm0g, out=c.sig1,
@@ -344,7 +348,7 @@ class TracedEngine:
                                  self.g_coef, self.g_env, n_in=9, env_first=True)
         gm = self.g_mso2.view(E, NSPH * C)
         g1 = self.g1c
-        if s1w.gate_split:
+        if self.gate_fused:
             # conv-2's adjoint products with the gate's input adjoint applied as they are written
             # (straight into the coefficient part of conv-1's adjoint operand), then the gating
             # adjoint from them and the kept gated rows

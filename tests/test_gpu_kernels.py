@@ -904,6 +904,74 @@ def test_gemm_gate_bwd_epilogue(nat, M):
     assert ((gg - gg_ref).abs() / (gg_mag + 1e-30)).max() < 1e-5
 
 
+@pytest.mark.parametrize("n", [16, 64, 100, 128, 200, 256, 512])
+def test_ln_silu_fwd_bwd(nat, n):
+    R = 301                     # odd: the last two-row wavefront of short rows has one row
+    g = torch.Generator().manual_seed(n)
+    a = torch.randn(R, n, generator=g, dtype=torch.float64) * 2 + 0.5
+    gam = 1 + 0.1 * torch.randn(n, generator=g, dtype=torch.float64)
+    bet = 0.1 * torch.randn(n, generator=g, dtype=torch.float64)
+    ar = a.clone().requires_grad_(True)
+    nrm = torch.nn.functional.layer_norm(ar, (n,), gam, bet, 1e-5)
+    s = torch.nn.functional.silu(nrm)
+    gs = torch.randn(R, n, generator=g, dtype=torch.float64)
+    (ga,) = torch.autograd.grad((s * gs).sum(), [ar])
+    f = lambda t: t.float().to(DEV).contiguous()
+    no, so, gao = (torch.empty(R, n, device=DEV) for _ in range(3))
+    nat.ln_silu_fwd(f(a), f(gam), f(bet), no, so, R=R, n=n)
+    nat.ln_silu_bwd(f(gs), f(a), no, f(gam), gao, R=R, n=n)
+    torch.cuda.synchronize()
+    assert (no.cpu().double() - nrm.detach()).abs().max() < 1e-5
+    assert (so.cpu().double() - s.detach()).abs().max() < 1e-5
+    assert (gao.cpu().double() - ga).abs().max() < 1e-4
+    # strided rows: a / nrm / g_a as a column block of a wider buffer
+    wide = torch.zeros(R, 3 * n, device=DEV)
+    wide[:, n:2 * n] = f(a)
+    nw, gw = torch.zeros(R, 3 * n, device=DEV), torch.zeros(R, 3 * n, device=DEV)
+    so2 = torch.empty(R, n, device=DEV)
+    nat.ln_silu_fwd(wide[:, n:2 * n], f(gam), f(bet), nw[:, n:2 * n], so2, R=R, n=n, lda=3 * n,
+                    lds=n)
+    nat.ln_silu_bwd(f(gs), wide[:, n:2 * n], nw[:, n:2 * n], f(gam), gw[:, n:2 * n], R=R, n=n,
+                    ldg=n, lda=3 * n, ldo=3 * n)
+    torch.cuda.synchronize()
+    assert torch.equal(so2, so) and torch.equal(gw[:, n:2 * n], gao)
+    assert gw[:, :n].abs().max() == 0 and gw[:, 2 * n:].abs().max() == 0
+    # nothing is written past row R - 1
+    nb, sb, gb = (torch.full((R + 1, n), float("nan"), device=DEV) for _ in range(3))
+    nat.ln_silu_fwd(f(a), f(gam), f(bet), nb[:R], sb[:R], R=R, n=n)
+    nat.ln_silu_bwd(f(gs), f(a), no, f(gam), gb[:R], R=R, n=n)
+    torch.cuda.synchronize()
+    assert torch.equal(nb[:R], no) and torch.equal(sb[:R], so) and torch.equal(gb[:R], gao)
+    assert all(bool(t[R].isnan().all()) for t in (nb, sb, gb))
+    # without the saved LayerNorm output: the forward does not write it, the backward recomputes
+    # it from a, gamma and beta -- the same values, so the same adjoint bit for bit
+    s3, g3 = torch.empty(R, n, device=DEV), torch.full((R + 1, n), float("nan"), device=DEV)
+    nat.ln_silu_fwd(f(a), f(gam), f(bet), None, s3, R=R, n=n)
+    nat.ln_silu_bwd(f(gs), f(a), None, f(gam), g3[:R], R=R, n=n, beta=f(bet))
+    torch.cuda.synchronize()
+    assert torch.equal(s3, so) and torch.equal(g3[:R], gao) and bool(g3[R].isnan().all())
+    with pytest.raises(RuntimeError):
+        nat.ln_silu_bwd(f(gs), f(a), None, f(gam), g3[:R], R=R, n=n)
+    # g 4 bytes off a 16-byte boundary sends the backward down the element-wise path while the
+    # forward (aligned rows) took the float4 one: the row statistics are summed in the same order
+    # on both paths, so the recomputed LayerNorm output and the adjoint equal the float4 ones
+    gbuf = torch.empty(R * n + 1, device=DEV)
+    gmis = gbuf[1:].view(R, n)
+    gmis.copy_(f(gs))
+    g4, g5 = torch.empty(R, n, device=DEV), torch.empty(R, n, device=DEV)
+    nat.ln_silu_bwd(gmis, f(a), None, f(gam), g4, R=R, n=n, beta=f(bet))
+    nat.ln_silu_bwd(gmis, f(a), no, f(gam), g5, R=R, n=n)
+    # and the forward on the element-wise path (misaligned LayerNorm output)
+    nbuf = torch.empty(R * n + 1, device=DEV)
+    nmis = nbuf[1:].view(R, n)
+    s6 = torch.empty(R, n, device=DEV)
+    nat.ln_silu_fwd(f(a), f(gam), f(bet), nmis, s6, R=R, n=n)
+    torch.cuda.synchronize()
+    for t, what in ((g4, "recomputed, element-wise"), (g5, "saved, element-wise")):
+        assert torch.equal(t, gao), f"{what} adjoint differs in {int((t != gao).sum())} elements"
+    assert torch.equal(nmis, no) and torch.equal(s6, so), "element-wise forward differs"
+
+
 @pytest.mark.parametrize("C", [16, 128, 96, 256, 300])
 def test_rmsnorm_sh_fwd_bwd(nat, C):
     from oracle.uma import rms_norm_sh

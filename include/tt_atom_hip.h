@@ -188,6 +188,28 @@ int tta_node_gather_sum_dst(const float* g_mcat, const int* src_ptr, const int* 
                             const float* tsum, const float* res, float* out, int64_t N, int64_t E,
                             int64_t C, tta_stream_t stream);
 
+/* ---------------------------------------------------------------- per-op rotation and scatter
+ * For callers that drive the blocks op by op (the fused step uses the kernels above).
+ * tta_rotate_pattern: out[e, r, w] = sum over q in [ptr[r], ptr[r+1]) of coef[e, k[q]] *
+ * x[e, blk[q], w] -- x [E, n_in, W], coef [E, nnz], out [E, n_out, W], all contiguous; the
+ * pattern (ptr [n_out + 1], k and blk [nnz]) in host memory, n_in <= 255, n_out <= 64,
+ * nnz <= 512.  With the pattern grouped by output row (k = the pair's index) it is
+ * rotation.rotate (rotation.py:211-222, ttnn.experimental.fused_rotate, fused_rotate.hpp:15-23);
+ * grouped by input column, the input half of rotation.rotate_bw (rotation.py:225-244).
+ * tta_rotate_pattern_gc: gc[e, k] = sum_w g_out[e, ii[k], w] x_in[e, jj[k], w] (ii, jj host
+ * arrays), the coefficient half of rotate_bw (rotation.py:246-260, fused_rotate_gc.hpp:15-23).
+ * tta_segment_sum_table: out[n, w] = sum over d < Dmax of msg[gather[n Dmax + d], w] (gather a
+ * device int32 [N * Dmax]; entries outside [0, n_msg), the sentinel, add nothing): segment_sum
+ * over build_gather's table (scatter.py:35-89).  Fixed summation order, no atomics. */
+int tta_rotate_pattern(const float* x, const float* coef, float* out, int64_t E, int64_t n_in,
+                       int64_t n_out, int64_t W, int64_t nnz, const int* ptr, const int* k,
+                       const int* blk, tta_stream_t stream);
+int tta_rotate_pattern_gc(const float* g_out, const float* x_in, float* gc, int64_t E,
+                          int64_t n_in, int64_t n_out, int64_t W, int64_t nnz, const int* ii,
+                          const int* jj, tta_stream_t stream);
+int tta_segment_sum_table(const float* msg, const int* gather, float* out, int64_t n_msg,
+                          int64_t N, int64_t Dmax, int64_t W, tta_stream_t stream);
+
 /* ---------------------------------------------------------------- element / row-wise
  * Gate: y[r,0] = silu(x[r,0]); y[r,c] = x[r,c] sigmoid(gating[r, idx8[c-1]]).  x [R,9,H] rows of
  * stride ldx, gating [R, L*H] rows of stride ldg (column blocks of one GEMM output allowed),

@@ -5,11 +5,13 @@ Same module and class names as the reference package for the path it covers
 ``model.Backbone``, ``model.GraphContext``, ``forces.energy_and_forces``,
 ``trace.TracedEngine``, ``weights.WeightBundle``, ``calculator.TTAtomCalculator``,
 ``orb.OrbWeights`` / ``orb.energy_and_forces(_batch)``, ``orb_calculator.OrbCalculator``,
-``bundle_cache`` / ``orb_weight_cache`` and the ``Calculator`` front door); the compute runs in
+``bundle_cache`` / ``orb_weight_cache``, the per-op ``rotation`` / ``scatter`` entry points and the
+``Calculator`` front door); the compute runs in
 hand-written HIP kernels behind the C ABI of ``include/tt_atom_hip.h``.
 """
 __all__ = ["geometry", "model", "forces", "trace", "weights", "synthetic", "calculator", "orb",
-           "orb_calculator", "bundle_cache", "orb_weight_cache", "auto", "Calculator"]
+           "orb_calculator", "bundle_cache", "orb_weight_cache", "auto", "rotation", "scatter",
+           "Calculator"]
 __version__ = "0.1.0"
 
 

@@ -52,6 +52,9 @@ _SIGS = {
     "tta_gate_fwd": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "tta_gate_bwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "tta_gate_gating_bwd": [_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P],
+    "tta_rotate_pattern": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P],
+    "tta_rotate_pattern_gc": [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P],
+    "tta_segment_sum_table": [_P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "tta_ln_silu_fwd": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "tta_ln_silu_bwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "tta_rmsnorm_sh_fwd": [_P, _P, _P, _P, _P, _P, _I64, _I64, _F, _P],
@@ -790,6 +793,46 @@ def gate_gating_bwd(g_x, y, sig, g_gating, idx8, *, R, H, L):
               _rows(g_x, R, ldgx, 9 * H, "g_x"), _ptr(y, numel=R * 9 * H, name="y"),
               _rows(sig, R, ldg, L * H, "sig"), _rows(g_gating, R, ldgg, L * H, "g_gating"),
               R, H, L, ldgx, ldg, ldgg, _host_idx8(idx8), _stream())
+
+
+def _host_i32(vals, name):
+    vals = [int(v) for v in vals]
+    return (ctypes.c_int * max(1, len(vals)))(*vals)
+
+
+def rotate_pattern(x, coef, out, ptr, k, blk, *, E, n_in, n_out, W):
+    """out [E, n_out, W] = the sparse-pattern rotation of x [E, n_in, W] by coef [E, nnz]
+    (tta_rotate_pattern): the terms of output block r are q in [ptr[r], ptr[r+1]), coefficient
+    column k[q] times input block blk[q] (host sequences)."""
+    nnz = len(k)
+    if len(ptr) != n_out + 1 or len(blk) != nnz:
+        raise RuntimeError("rotate_pattern: ptr needs n_out + 1 entries and blk one per term")
+    _hbm_call("k_rotate_pattern", 4 * E * ((n_in + n_out) * W + nnz), "tta_rotate_pattern",
+              _ptr(x, numel=E * n_in * W, name="x"), _ptr(coef, numel=E * nnz, name="coef"),
+              _ptr(out, numel=E * n_out * W, name="out"), E, n_in, n_out, W, nnz,
+              _host_i32(ptr, "ptr"), _host_i32(k, "k"), _host_i32(blk, "blk"), _stream())
+
+
+def rotate_pattern_gc(g_out, x_in, gc, ii, jj, *, E, n_in, n_out, W):
+    """gc [E, nnz]: gc[e, k] = sum_w g_out[e, ii[k], w] x_in[e, jj[k], w]
+    (tta_rotate_pattern_gc)."""
+    nnz = len(ii)
+    if len(jj) != nnz:
+        raise RuntimeError("rotate_pattern_gc: ii and jj differ in length")
+    _hbm_call("k_rotate_pattern_gc", 4 * E * ((n_in + n_out) * W + nnz), "tta_rotate_pattern_gc",
+              _ptr(g_out, numel=E * n_out * W, name="g_out"),
+              _ptr(x_in, numel=E * n_in * W, name="x_in"), _ptr(gc, numel=E * nnz, name="gc"),
+              E, n_in, n_out, W, nnz, _host_i32(ii, "ii"), _host_i32(jj, "jj"), _stream())
+
+
+def segment_sum_table(msg, gather, out, *, N, Dmax, W):
+    """out [N, W] = per-node sums of msg [n_msg, W] rows over the [N, Dmax] int32 gather table
+    (entries outside [0, n_msg) add nothing; tta_segment_sum_table)."""
+    n_msg = msg.shape[0] if msg.dim() == 2 else msg.numel() // max(W, 1)
+    _hbm_call("k_segment_sum_table", 4 * (N * Dmax + 2 * N * W + N * Dmax * W),
+              "tta_segment_sum_table", _ptr(msg, numel=n_msg * W, name="msg"),
+              _i32(gather, N * Dmax, "gather"), _ptr(out, numel=N * W, name="out"), n_msg, N,
+              Dmax, W, _stream())
 
 
 def ln_silu_fwd(a, gamma, beta, nrm, s, *, R, n, groups=1, lda=None, lds=None, eps=1e-5):

@@ -70,33 +70,46 @@ COUNTER_TITLES = {
 
 
 class GemmEvents:
-    """HIP events around every GEMM launch (same stream as the launch), per kernel family."""
+    """HIP events around every GEMM launch (same stream as the launch), per kernel family, and
+    within a family per launch class (``part``: e.g. the gate epilogues; None = the rest)."""
 
     def __init__(self, torch):
         self.torch = torch
         self.kinds = {}
+        self.parts = {}
         self._cur = None
 
-    def before(self, flops, nbytes, kind="f32"):
+    def before(self, flops, nbytes, kind="f32", part=None):
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
-        self._cur = (e, kind)
-        k = self.kinds.setdefault(kind, {"pairs": [], "flops": 0.0, "nbytes": 0.0})
-        k["flops"] += flops
-        k["nbytes"] += nbytes
+        self._cur = (e, kind, part)
+        for key, table in ((kind, self.kinds), ((kind, part), self.parts)):
+            k = table.setdefault(key, {"pairs": [], "flops": 0.0, "nbytes": 0.0})
+            k["flops"] += flops
+            k["nbytes"] += nbytes
 
     def after(self):
         e = self.torch.cuda.Event(enable_timing=True)
         e.record()
-        start, kind = self._cur
+        start, kind, part = self._cur
         self.kinds[kind]["pairs"].append((start, e))
+        self.parts[(kind, part)]["pairs"].append((start, e))
+
+    @staticmethod
+    def _sum(table):
+        out = {}
+        for key, k in table.items():
+            ms = sum(a.elapsed_time(b) for a, b in k["pairs"])
+            out[key] = dict(n=len(k["pairs"]), flops=k["flops"], nbytes=k["nbytes"], ms=ms)
+        return out
 
     def summary(self):
-        out = {}
-        for kind, k in self.kinds.items():
-            ms = sum(a.elapsed_time(b) for a, b in k["pairs"])
-            out[kind] = dict(n=len(k["pairs"]), flops=k["flops"], nbytes=k["nbytes"], ms=ms)
-        return out
+        return self._sum(self.kinds)
+
+    def parts_of(self, kind):
+        """{part: stats} of one family, the launches of no named class under "other"."""
+        return {("other" if part is None else part): v
+                for (k, part), v in self._sum(self.parts).items() if k == kind}
 
 
 class HbmEvents:
@@ -889,6 +902,10 @@ def main():
                   "achieved_tflops": round(v["flops"] / max(1e-12, v["ms"] * 1e-3) / 1e12, 2),
                   "peak_tflops": round(PEAKS[k], 1), "share_of_step": round(v["ms"] / (dt * 1e3), 4)}
               for k, v in fam.items()}
+    classes = {p: {"launches": v["n"], "avg_launch_us": round(v["ms"] * 1e3 / max(1, v["n"]), 2),
+                   "achieved_tflops": round(v["flops"] / max(1e-12, v["ms"] * 1e-3) / 1e12, 2),
+                   "frac": round(v["flops"] / max(1e-12, v["ms"] * 1e-3) / 1e12 / PEAKS[dom], 4)}
+               for p, v in probe.parts_of(dom).items()}
     unit = "atom-steps/s"
     if wl == "c2":
         metric = "edge-steps/s (forward + edge-vector VJP), isolated edgewise kernel (C2)"
@@ -958,7 +975,15 @@ def main():
                      "gemm_share_of_step": round(gemm_ms / (dt * 1e3), 4),
                      "measured": ("HIP events around each launch, on the launch stream, over a "
                                   "second pass of the same steps"),
-                     "gemm_families": others},
+                     "gemm_families": others,
+                     "launch_classes": classes,
+                     "launch_classes_note": ("the dominant family's launches split by epilogue: "
+                                             "'gate' = the SO(2) conv-1 products with the gate "
+                                             "applied as they are written and the conv-2 adjoint "
+                                             "products with its input adjoint (the gate's "
+                                             "elementwise work, which no separate pass does any "
+                                             "more, counts in their time but not in their "
+                                             "flops)")},
         "hbm_kernels": hbm.summary(kernel_traffic),
         "hbm_kernels_note": ("frac = compulsory bytes (every distinct operand byte once) / HIP-event "
                              "time / 8 TB/s; algorithmic_GBps counts gathered node rows once per "

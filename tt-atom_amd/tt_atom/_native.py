@@ -226,7 +226,8 @@ EPI_GATE, EPI_GATE_BWD = 6, 7  # tta_gemm_bf16x_group_gate / _gate_bwd only
 # ``probe.before(flops, nbytes, kind)`` and ``probe.after()`` (the benchmark records HIP events on
 # the launch stream there).  nbytes is the algorithmic traffic: A, B and C once (C twice when
 # accumulated, plus the second output / auxiliary input of epilogues 3 and 4); kind is "f32" for
-# the fp32 MFMA kernel and MODE_KIND[mode] for the split kernel.
+# the fp32 MFMA kernel and MODE_KIND[mode] for the split kernel.  The gated SO(2) launches pass
+# ``part="gate"`` as well (a probe may file them separately within their family).
 _gemm_probe = None
 
 
@@ -455,7 +456,7 @@ def linear_group_gate(items, c0, sig, x0, idx8, H, backward=False):
             work = torch.empty(need, device=items[0][0].device, dtype=torch.float32)
     probe = _gemm_probe
     if probe is not None:
-        probe.before(flops, nbytes, MODE_KIND[mode])
+        probe.before(flops, nbytes, MODE_KIND[mode], part="gate")
     _call("tta_gemm_bf16x_group_gate_bwd" if backward else "tta_gemm_bf16x_group_gate", probs,
           len(items), mode,
           (ctypes.c_int64 * len(items))(*c0), gp, _ld(sig, "sig"), xp, _ld(x0, "x0"), H,

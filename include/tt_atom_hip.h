@@ -3,7 +3,10 @@
  *
  * Conventions (every entry point):
  *   - device pointers to caller-allocated buffers (the PyTorch caching allocator owns memory;
- *     nothing here allocates), int64_t sizes, fp32 data, int32 indices, row-major layouts;
+ *     nothing here allocates), int64_t sizes, fp32 data, int32 indices, row-major layouts; the
+ *     few small tables an entry point reads while it builds its launch (gate degree tables,
+ *     rotation patterns, per-product coefficient offsets) are host arrays, as their
+ *     declarations say;
  *   - work is enqueued on `stream` (hipStream_t, passed as void*), stream-ordered, reentrant
  *     (one exception: tta_virial_noalloc shares a per-GPU device array between calls, so calls
  *     of it that overlap on one GPU race; see its declaration);

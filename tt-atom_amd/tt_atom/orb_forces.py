@@ -17,10 +17,125 @@ from __future__ import annotations
 
 import torch
 
+from . import _native as nat
 from . import orb as _orb
 from .engine_cache import cached_engine
 
-__all__ = ["energy_and_forces", "energy_and_forces_batch"]
+__all__ = ["energy_and_forces", "energy_and_forces_batch", "rmsnorm_bw", "mlpnorm_bw",
+           "attn_layer_bw", "energy_bw", "energy_bw_batch", "backbone_bw", "backbone_bw_batch"]
+
+
+# ----------------------------------------------------------------------------- per-module reverse
+# The VJPs of the modules called one by one (orb_forces.py:67-254), over the activations the
+# modules' __call__ kept; the same kernels as the engine's reverse pass, launched per module.
+def _empty(*shape, like):
+    return torch.empty(*shape, device=like.device, dtype=torch.float32)
+
+
+def rmsnorm_bw(norm, g_out):
+    """Adjoint of ``RMSNorm.__call__``'s input (orb_forces.py:67-79)."""
+    x, inv = norm._cache_x, norm._cache_inv
+    g = g_out.to(device=x.device, dtype=torch.float32).contiguous()
+    g_x = torch.empty_like(x)
+    nat.rms_bwd(g, x, norm.w, inv, g_x)
+    return g_x
+
+
+def mlpnorm_bw(mlp, g_out):
+    """Adjoint of ``MLPNorm.__call__``'s input (orb_forces.py:82-91): the RMSNorm adjoint, then
+    each linear's transpose with the SiLU derivative of the kept pre-activation in its epilogue."""
+    p = mlp._p
+    g_h2 = rmsnorm_bw(mlp.norm, g_out)
+    R = g_h2.shape[0]
+    g_a1 = _empty(R, p.hidden, like=g_h2)
+    g_a0 = _empty(R, p.hidden, like=g_h2)
+    nat.linear(g_h2, p.w[2], out=g_a1, epilogue=nat.EPI_SILU_GRAD, aux=mlp._cache_a1)
+    nat.linear(g_a1, p.w[1], out=g_a0, epilogue=nat.EPI_SILU_GRAD, aux=mlp._cache_a0)
+    return nat.linear(g_a0, p.w[0])
+
+
+def attn_layer_bw(layer, graph, g_nodes_out, g_edges_out):
+    """Adjoints (nodes, edges, cutoff [E, 1]) of ``AttentionInteractionLayer.__call__``'s inputs
+    from those of its outputs (orb_forces.py:94-148), edges in the graph's edge order."""
+    c, p, C = layer._cache, layer._p, layer.C
+    t = graph._module_topology()
+    N, E, H = graph.N, graph.E, p.edge.hidden
+    dev = t.send.device
+    g_n = g_nodes_out.to(device=dev, dtype=torch.float32).clone()
+    g_e = g_edges_out.to(device=dev, dtype=torch.float32)[t.order].contiguous()
+    g_cut = torch.zeros(E, device=dev, dtype=torch.float32)
+    Hn = p.node.hidden
+    g_hn2, g_an1, g_an0 = _empty(N, C, like=g_n), _empty(N, Hn, like=g_n), _empty(N, Hn, like=g_n)
+    nat.rms_bwd(g_n, c["hn2"], p.node.norm, c["ninv"], g_hn2)
+    nat.linear(g_hn2, p.node.w[2], out=g_an1, epilogue=nat.EPI_SILU_GRAD, aux=c["an1"])
+    nat.linear(g_an1, p.node.w[1], out=g_an0, epilogue=nat.EPI_SILU_GRAD, aux=c["an0"])
+    g_node_in = nat.linear(g_an0, p.node.w[0])                          # [N, 3C]
+    g_h2 = _empty(E, C, like=g_n)
+    nat.orb_edge_bwd(g_e, g_node_in, c["ue"], c["sig"], t.cut, c["h2"], c["inv"], p.edge.norm,
+                     p.attn_w, t.send, t.recv, g_h2, g_cut)
+    g_a1, g_a0 = _empty(E, H, like=g_n), _empty(E, H, like=g_n)
+    nat.linear(g_h2, p.edge.w[2], out=g_a1, epilogue=nat.EPI_SILU_GRAD, aux=c["a1"])
+    nat.linear(g_a1, p.edge.w[1], out=g_a0, epilogue=nat.EPI_SILU_GRAD, aux=c["a0"])
+    G = _empty(N, 2 * H, like=g_n)
+    nat.orb_node_segsum2(g_a0, t.send_ptr, t.recv_ptr, t.recv_perm, G)
+    nat.add_rows(g_node_in[:, :C], g_n)
+    nat.linear_group([(g_a0, p.we, None, g_e, nat.EPI_ACCUM),
+                      (G, p.wsr, None, g_n, nat.EPI_ACCUM)])
+    return g_n, g_e[t.inv_order], g_cut[t.inv_order].reshape(E, 1)
+
+
+def energy_bw(ehead):
+    """Adjoint [N, C] of ``EnergyHead.__call__``'s node features for dE/dE = 1
+    (orb_forces.py:151-172): every row is the mean's adjoint over N."""
+    p = ehead._p
+    a0, N = ehead._cache_a0, ehead._cache_N
+    ones = torch.ones(1, 1, device=a0.device, dtype=torch.float32)
+    g_a0 = _empty(1, p.hidden, like=a0)
+    nat.linear(ones, p.w[1], out=g_a0, epilogue=nat.EPI_SILU_GRAD, aux=a0)
+    g_mean = nat.linear(g_a0, p.w[0])                                   # [1, C]
+    out = _empty(N, g_mean.shape[1], like=a0)
+    nat.segment_mean_bwd(g_mean, torch.zeros(N, dtype=torch.int32, device=a0.device),
+                         torch.tensor([0, N], dtype=torch.int32, device=a0.device), out)
+    return out
+
+
+def energy_bw_batch(ehead, seg_mean_T):
+    """Adjoint [N, C] of ``EnergyHead.batch``'s node features for the summed energies, with
+    ``seg_mean_T`` [N, K] the transposed row-normalised segment matrix (orb_forces.py:207-229)."""
+    p = ehead._p
+    a0 = ehead._cache_a0
+    K = a0.shape[0]
+    ones = torch.ones(K, 1, device=a0.device, dtype=torch.float32)
+    g_a0 = _empty(K, p.hidden, like=a0)
+    nat.linear(ones, p.w[1], out=g_a0, epilogue=nat.EPI_SILU_GRAD, aux=a0)
+    g_mean = nat.linear(g_a0, p.w[0])                                   # [K, C]
+    smt = seg_mean_T.to(device=a0.device, dtype=torch.float32).contiguous()
+    return nat.linear(smt, g_mean)
+
+
+def _backbone_bw(encoder, layers, g_nodes, graph):
+    g_edges = torch.zeros(graph.E, layers[0].C if layers else encoder.latent_dim,
+                          device=g_nodes.device, dtype=torch.float32)
+    g_cutoff = None
+    for layer in reversed(layers):
+        g_nodes, g_edges, g_c = attn_layer_bw(layer, graph, g_nodes, g_edges)
+        g_cutoff = g_c if g_cutoff is None else g_cutoff + g_c
+    return mlpnorm_bw(encoder.edge_fn, g_edges), g_cutoff
+
+
+def backbone_bw(encoder, layers, ehead, graph, e_true=None):
+    """Reverse pass from the energy head through every layer to the encoder's edge input:
+    (adjoint of the edge features, adjoint of the cutoff) (orb_forces.py:175-204).  ``e_true``
+    (the reference's bucketed edge count) must be None or the true count: graphs are not padded
+    here."""
+    if e_true is not None and int(e_true) != graph.E:
+        raise ValueError("padded (bucketed) graphs are not used by this build")
+    return _backbone_bw(encoder, layers, energy_bw(ehead), graph)
+
+
+def backbone_bw_batch(encoder, layers, ehead, graph, seg_mean_T):
+    """``backbone_bw`` for a disjoint-union batch (orb_forces.py:232-254)."""
+    return _backbone_bw(encoder, layers, energy_bw_batch(ehead, seg_mean_T), graph)
 
 
 def _model(encoder, layers, ehead, device, r_max, num_bases):

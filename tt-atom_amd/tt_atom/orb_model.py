@@ -7,11 +7,13 @@ per message-passing step, ``EnergyHead`` (and a direct checkpoint's ``ForceHead`
 the same constructor arguments and hold the weights in the layout of this build's kernels
 (fp32 ``[in, out]`` / ``[out, in]`` operands, packed planes for the split MFMA GEMM, the first
 edge-MLP weight split by input block); ``tt_atom.orb_forces`` assembles them into one
-``OrbEngine`` step, where the whole forward and backward run as a fixed sequence of HIP kernels.
-Calling a module by itself on device tensors (the reference's ttnn ``__call__``) is not part of
-this interface: the step is fused across module boundaries (RMSNorm + residual + the next
-layer's attention gates in one kernel, the first edge-MLP layer as node products plus a
-row-gather epilogue), so the engine is the unit of execution.
+``OrbEngine`` step, where the whole forward and backward run as a fixed sequence of HIP kernels
+fused across module boundaries (RMSNorm + residual + the next layer's attention gates in one
+kernel).  The modules can also be called one by one on fp32 device tensors, as the reference's
+ttnn ``__call__`` (orb_model.py:107-266, 329-355), with the reverse pass in
+``orb_forces.rmsnorm_bw / mlpnorm_bw / attn_layer_bw / energy_bw(_batch)`` over the activations a
+call keeps: the same kernels, launched per module (edges in the graph's edge order at the
+interface).
 
 ``fast=True`` (the reference's bfloat8 weights) selects bf16 GEMM operands here;
 ``precision=`` picks any of ``tt_atom.model.PRECISIONS`` explicitly.
@@ -23,6 +25,7 @@ from __future__ import annotations
 
 import torch
 
+from . import _native as nat
 from . import orb as _orb
 from .model import PRECISIONS
 
@@ -57,6 +60,11 @@ def _device(device):
     return torch.device("cuda") if device is None else torch.device(device)
 
 
+def _f32(t, device):
+    """An fp32 contiguous tensor on ``device`` (module calls take device tensors)."""
+    return torch.as_tensor(t).to(device=device, dtype=torch.float32).contiguous()
+
+
 # ----------------------------------------------------------------------------- modules
 class RMSNorm:
     """``torch.nn.RMSNorm`` weight over the last dim (orb_model.py:92-112); the normalisation
@@ -70,6 +78,16 @@ class RMSNorm:
             raise ValueError("the Orb RMSNorm kernels use eps = 1e-6")
         self.dim, self.eps = int(dim), float(eps)
         self.w = _orb._dev(w, _device(device))
+
+    def __call__(self, x):
+        """x [R, dim] -> x rsqrt(mean(x^2) + eps) w (orb_model.py:107-112); keeps x and the
+        per-row inverse RMS for ``orb_forces.rmsnorm_bw``."""
+        x = _f32(x, self.w.device)
+        y = torch.empty_like(x)
+        inv = torch.empty(x.shape[0], device=x.device, dtype=torch.float32)
+        nat.rms_residual(x, self.w, None, None, y, inv, eps=self.eps)
+        self._cache_x, self._cache_inv = x, inv
+        return y
 
 
 class MLPNorm:
@@ -87,6 +105,20 @@ class MLPNorm:
                              f"{(in_dim, hidden_dim, out_dim)}")
         self.norm = RMSNorm(weights, f"{prefix}.layer_norm", device, out_dim)
 
+    def __call__(self, x):
+        """x [R, in] -> RMSNorm(L2(silu(L1(silu(L0 x))))) (orb_model.py:155-173); keeps the
+        pre-SiLU activations for ``orb_forces.mlpnorm_bw``."""
+        p = self._p
+        x = _f32(x, p.b[0].device)
+        R = x.shape[0]
+        f = lambda n: torch.empty(R, n, device=x.device, dtype=torch.float32)
+        a0, h0, a1, h1, h2 = f(p.hidden), f(p.hidden), f(p.hidden), f(p.hidden), f(p.out_dim)
+        nat.linear(x, p.w_t[0], p.b[0], out=a0, epilogue=nat.EPI_PRE_SILU, out2=h0)
+        nat.linear(h0, p.w_t[1], p.b[1], out=a1, epilogue=nat.EPI_PRE_SILU, out2=h1)
+        nat.linear(h1, p.w_t[2], p.b[2], out=h2)
+        self._cache_a0, self._cache_a1 = a0, a1
+        return self.norm(h2)
+
 
 class Encoder:
     """``gns.Encoder``: node and edge MLPNorm blocks (orb_model.py:176-186)."""
@@ -100,6 +132,9 @@ class Encoder:
         self.node_in, self.edge_in = int(node_in), int(edge_in)
         self.latent_dim, self.hidden_dim = int(latent_dim), int(hidden_dim)
         self.precision = self.node_fn.precision
+
+    def __call__(self, node_features, edge_features):
+        return self.node_fn(node_features), self.edge_fn(edge_features)
 
 
 class AttentionInteractionLayer:
@@ -117,6 +152,52 @@ class AttentionInteractionLayer:
             raise ValueError(f"{prefix}: MLP hidden width is {self._p.edge.hidden}, expected "
                              f"{hidden_dim}")
         self.has_cond = self._p.cond_w_t is not None
+        # the two attention linears as one [C, 2] product (receive, send)
+        self._attn_w_t = self._p.attn_w.view(2, self.C).t().contiguous()
+
+    def __call__(self, nodes, edges, graph):
+        """(nodes [N, C], edges [E, C]) -> (nodes + node update, edges + edge update), one
+        message-passing step (orb_model.py:225-266): the conditioning projection (when the layer
+        and ``graph.cond_nodes`` have one), sigmoid attention gates times ``graph.cutoff``, the
+        edge MLPNorm on [e | n[send] | n[recv]] (its first layer as node products [W_s | W_r]
+        gathered per edge), the sender / receiver sums of the gated messages, the node MLPNorm on
+        [n | recv | sent].  Keeps what ``orb_forces.attn_layer_bw`` needs."""
+        p, C = self._p, self.C
+        t = graph._module_topology()
+        dev, order = t.send.device, t.order
+        N, E, H = graph.N, graph.E, p.edge.hidden
+        f = lambda *sh: torch.empty(*sh, device=dev, dtype=torch.float32)
+        n_l = _f32(nodes, dev).clone()
+        if self.has_cond and graph.cond_nodes is not None:
+            nat.linear(_f32(graph.cond_nodes, dev), p.cond_w_t, p.cond_b, out=n_l,
+                       epilogue=nat.EPI_ACCUM)
+        e_s = _f32(edges, dev)[order].contiguous()            # sender order inside
+        sig = f(E, 2)
+        nat.linear(e_s, self._attn_w_t, p.attn_b, out=sig, epilogue=nat.EPI_SIGMOID)
+        P = f(N, 2 * H)
+        nat.linear(n_l, p.wsr_t, out=P)
+        a0, h0, a1, h1, h2 = f(E, H), f(E, H), f(E, H), f(E, H), f(E, C)
+        nat.linear_gather(e_s, p.we_t, p.edge.b[0], a0, P, t.send, t.recv, H,
+                          epilogue=nat.EPI_PRE_SILU, out2=h0)
+        nat.linear(h0, p.edge.w_t[1], p.edge.b[1], out=a1, epilogue=nat.EPI_PRE_SILU, out2=h1)
+        nat.linear(h1, p.edge.w_t[2], p.edge.b[2], out=h2)
+        ue, e_new, inv = f(E, C), f(E, C), f(E)
+        nat.rms_residual(h2, p.edge.norm, e_s, ue, e_new, inv)
+        node_in = f(N, 3 * C)
+        nat.orb_segsum(ue, sig, t.cut, t.send_ptr, t.recv_ptr, t.recv_perm, n_l, node_in)
+        Hn = p.node.hidden
+        an0, hn0, an1, hn1, hn2 = f(N, Hn), f(N, Hn), f(N, Hn), f(N, Hn), f(N, C)
+        nat.linear(node_in, p.node.w_t[0], p.node.b[0], out=an0, epilogue=nat.EPI_PRE_SILU,
+                   out2=hn0)
+        nat.linear(hn0, p.node.w_t[1], p.node.b[1], out=an1, epilogue=nat.EPI_PRE_SILU, out2=hn1)
+        nat.linear(hn1, p.node.w_t[2], p.node.b[2], out=hn2)
+        n_new, ninv = f(N, C), f(N)
+        nat.rms_residual(hn2, p.node.norm, n_l, None, n_new, ninv)
+        self._cache = dict(sig=sig, a0=a0, a1=a1, h2=h2, ue=ue, inv=inv, an0=an0, an1=an1,
+                           hn2=hn2, ninv=ninv, graph=graph)
+        e_out = torch.empty_like(e_new)
+        e_out[order] = e_new
+        return n_new, e_out
 
 
 class _HeadModule:
@@ -136,6 +217,35 @@ class EnergyHead(_HeadModule):
     """``forcefield_heads.EnergyHead`` (orb_model.py:307-355): per-system mean of the node
     features, Linear-SiLU-Linear to one raw energy per system."""
     prefix, n_out = "energy_head", 1
+
+    def _mlp(self, mean):
+        p = self._p
+        K = mean.shape[0]
+        a0 = torch.empty(K, p.hidden, device=mean.device, dtype=torch.float32)
+        h = torch.empty_like(a0)
+        raw = torch.empty(K, 1, device=mean.device, dtype=torch.float32)
+        nat.linear(mean, p.w_t[0], p.b[0], out=a0, epilogue=nat.EPI_PRE_SILU, out2=h)
+        nat.linear(h, p.w_t[1], p.b[1], out=raw)
+        self._cache_a0 = a0
+        return raw
+
+    def __call__(self, node_features):
+        """node_features [N, C] of one system -> the raw energy [1, 1] (orb_model.py:329-338)."""
+        x = _f32(node_features, self._p.b[0].device)
+        N = x.shape[0]
+        ptr = torch.tensor([0, N], dtype=torch.int32, device=x.device)
+        mean = torch.empty(1, x.shape[1], device=x.device, dtype=torch.float32)
+        nat.segment_mean(x, ptr, mean)
+        self._cache_N = N
+        return self._mlp(mean)
+
+    def batch(self, node_features, seg_mean):
+        """node_features [N, C] of K systems, ``seg_mean`` [K, N] the row-normalised segment
+        matrix -> raw energies [K, 1] (orb_model.py:340-355)."""
+        x = _f32(node_features, self._p.b[0].device)
+        sm = _f32(seg_mean, x.device)
+        mean = nat.linear(sm, x)
+        return self._mlp(mean)
 
 
 class ForceHead(_HeadModule):
@@ -169,8 +279,25 @@ class OrbGraphContext:
         self.E, self.N = E, int(num_nodes)
         self.senders = torch.as_tensor(senders)
         self.receivers = torch.as_tensor(receivers)
+        self.cutoff = cutoff
         self.cond_nodes = cond_nodes
         self.natoms = natoms
+        self._topo = None
+
+    def _module_topology(self):
+        """The sender-sorted device topology and the cutoff in that order, for module calls
+        (built on first use)."""
+        if self._topo is None:
+            if self.cutoff is None:
+                raise ValueError("module calls need the graph's cutoff envelope")
+            t = _orb.OrbGraph(self.device, senders=self.senders, receivers=self.receivers,
+                              num_nodes=self.N,
+                              atomic_numbers=torch.zeros(self.N, dtype=torch.int64))
+            t.cut = _f32(self.cutoff, self.device).reshape(-1)[t.order].contiguous()
+            t.inv_order = torch.empty_like(t.order)
+            t.inv_order[t.order] = torch.arange(self.E, device=t.order.device)
+            self._topo = t
+        return self._topo
 
     def topology(self, atomic_numbers, cell_shift=None, natoms=None):
         return _orb.OrbGraph(self.device, senders=self.senders, receivers=self.receivers,

@@ -322,6 +322,27 @@ def test_orb_session_single_and_batch(nat, tmp_path):
         assert np.abs(batch["forces"][k] - r["forces"]).max() <= 2e-5
 
 
+def test_orb_session_systems_without_edges(nat, tmp_path):
+    """A system with no edge inside the cutoff (one atom; two atoms 20 A apart) is refused with
+    ValueError, alone and inside a batch, as the reference's batch assembly refuses it
+    (batch.py:171-174, disjoint.py:139-140); the session stays usable."""
+    from tt_atom import orb_calculator as OC
+    cfg = dict(S.CFG_ORB_TINY)
+    w = S.random_orb_weights(cfg, 32)
+    path = tmp_path / "orb.npz"
+    orb.save_orb_bundle(path, cfg, w)
+    sess = OC.OrbSession(str(path), pair_repulsion=False)
+    one = (np.zeros((1, 3)), np.array([8]))
+    two = (np.array([[0.0, 0.0, 0.0], [20.0, 0.0, 0.0]]), np.array([6, 1]))
+    for p, z in (one, two):
+        with pytest.raises(ValueError, match="no edges"):
+            sess.evaluate(p, z)
+    mol = S.c5_systems(14, K=1, n_min=6, n_max=8, side=5.0)[0]
+    with pytest.raises(ValueError, match="no edges"):
+        sess.evaluate_batch([mol, two])
+    assert np.isfinite(sess.evaluate(*mol)["energy"])
+
+
 def test_orb_step_graph_replays_match_eager():
     """OrbEngine: graph replays equal the eager kernel sequence bit for bit, across eager work in
     between and after a change of positions."""

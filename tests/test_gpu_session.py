@@ -82,3 +82,21 @@ def test_session_new_engine_on_cell_change(session):
     fresh = calculator.Session(sess.bundle).evaluate(pos, Z, cell=cell2, pbc=[True] * 3)
     assert r2["energy"] == fresh["energy"] and np.array_equal(r2["forces"], fresh["forces"])
     assert np.array_equal(r2["stress"], fresh["stress"])
+
+
+def test_session_systems_without_edges(session):
+    """A system with no edge inside the cutoff (one atom; two atoms 20 A apart) is refused with
+    ValueError, alone and inside a batch, as the reference's calculator and disjoint assembly
+    refuse it (calculator.py:132-133, disjoint.py:139-140)."""
+    cfg, w, host, sess = session
+    one = (np.zeros((1, 3)), np.array([8]))
+    two = (np.array([[0.0, 0.0, 0.0], [20.0, 0.0, 0.0]]), np.array([6, 1]))
+    for pos, Z in (one, two):
+        with pytest.raises(ValueError, match="no edges"):
+            sess.evaluate(pos, Z, charge=0.0, spin=1.0)
+    mol = _molecules()[0]
+    with pytest.raises(ValueError, match="no edges"):
+        sess.evaluate_batch([dict(positions=mol[0], numbers=mol[1]),
+                             dict(positions=two[0], numbers=two[1])])
+    # the session stays usable
+    assert np.isfinite(sess.evaluate(mol[0], mol[1])["energy"])

@@ -153,6 +153,29 @@ int tta_gather_rotate_bw_dst(const float* g_xf, const float* rad, const float* x
                              float* g_coef, float* tsum, int64_t N, int64_t E, int64_t C,
                              tta_stream_t stream);
 
+/* The same backward, rad required, walked from both ends of every edge so that the gather
+ * adjoint [E,9,2C] is never written: tta_gather_rotate_bw_srcwalk visits each node's outgoing
+ * edges (src_ptr [N+1], src_perm [E]: the source CSR) and does the source half of their channels
+ * [.., 0:C], tta_gather_rotate_bw_tgtwalk each node's incoming edges (tgt_ptr) and the
+ * destination half [.., C:2C]; call the source walk first, on the same stream.  Each walk reads
+ * a node's own row of x once and sums its half of the node adjoint over the node's edges: the
+ * source walk writes ssum [N,9,C], the destination walk out[n] = (ssum[n] + its sum) + res[n]
+ * (res may be NULL).  g_rad [E,6,2C]: each walk writes its half.  The coefficient adjoint: the
+ * source walk writes its channel sum to coef_half [E,35], the destination walk accumulates
+ * g_coef += (coef_half + its channel sum).  g_rad, g_coef and out are bit-identical to
+ * tta_gather_rotate_bw_dst followed by tta_node_gather_sum_dst.  C <= 256.  Same reference
+ * functions as tta_gather_rotate_bw_dst (rotation.py:225-260, forces.py:164-170 and the
+ * scatters of forces.py:384-412). */
+int tta_gather_rotate_bw_srcwalk(const float* g_xf, const float* rad, const float* x,
+                                 const int* src_ptr, const int* src_perm, const float* coef,
+                                 float* g_rad, float* coef_half, float* ssum, int64_t N, int64_t E,
+                                 int64_t C, tta_stream_t stream);
+int tta_gather_rotate_bw_tgtwalk(const float* g_xf, const float* rad, const float* x,
+                                 const int* tgt_ptr, const float* coef, float* g_rad,
+                                 float* g_coef, const float* coef_half, const float* ssum,
+                                 const float* res, float* out, int64_t N, int64_t E, int64_t C,
+                                 tta_stream_t stream);
+
 /* Source-only variant: out[e, m, :] = sum_j W[e,m,j] x[src_e, j, :], out [E, 9, C] m-primed --
  * rotation.rotate (rotation.py:211-222) applied to source features gathered by edge (the C2
  * isolated-edgewise pipeline).  Its backward writes g_in[e] = W[e]^T g_out[e] (skipped when g_in

@@ -608,13 +608,15 @@ def test_gather_rotate_fwd_bwd(nat, C):
     assert (gn.cpu().double() - gx).abs().max() < 1e-3
 
 
-@pytest.mark.parametrize("C", [16, 32, 64, 128])
+@pytest.mark.parametrize("C", [16, 32, 64, 128, 256])
 def test_gather_rotate_bw_dst_bit_equal(nat, C):
     """The destination-walked backward (a block per node, the destination half of the adjoint
     summed in registers) gives the same bits as the edge-walked kernel followed by the CSR node
-    sum for g_rad, the source half of g_mcat and the node adjoint, and the accumulated g_coef to
-    fp32 rounding (its channel sum runs per half, then adds the halves), on a graph with a
-    destination hub, nodes without incoming edges and isolated nodes."""
+    sum for g_rad, the source half of g_mcat and the node adjoint (with a residual), and the
+    accumulated g_coef to fp32 rounding (its channel sum runs per half, then adds the halves);
+    the walk from both ends of every edge (source walk, then destination walk, no g_mcat) gives
+    the destination walk's bits for all three.  A graph with a destination hub, nodes without
+    incoming edges and isolated nodes."""
     N, E = 60, 700
     g = torch.Generator().manual_seed(C + 7)
     tgt = torch.randint(0, N - 6, (E,), generator=g)
@@ -629,7 +631,8 @@ def test_gather_rotate_bw_dst_bit_equal(nat, C):
     f = lambda t: t.to(DEV).contiguous()
     sptr, perm, tptr = _csr(src, N), torch.argsort(src, stable=True), _csr(tgt, N)
     outs = {}
-    for walk in ("edge", "dst"):
+    res = torch.randn(N, 9, C, generator=g)
+    for walk in ("edge", "dst", "nodes"):
         g_rad = torch.full((E, 6, 2 * C), float("nan"), device=DEV)
         g_mcat = torch.zeros(E, 9, 2 * C, device=DEV)
         g_coef = f(gc0.clone())
@@ -637,18 +640,27 @@ def test_gather_rotate_bw_dst_bit_equal(nat, C):
         if walk == "edge":
             nat.gather_rotate_bw(f(gout), f(rad), f(x), _i32(src), _i32(tgt), f(coef), g_rad,
                                  g_mcat, g_coef)
-            nat.node_gather_sum(g_mcat, _i32(sptr), _i32(perm), _i32(tptr), None, gn)
-        else:
+            nat.node_gather_sum(g_mcat, _i32(sptr), _i32(perm), _i32(tptr), f(res), gn)
+        elif walk == "dst":
             tsum = torch.full((N, 9, C), float("nan"), device=DEV)
             nat.gather_rotate_bw_dst(f(gout), f(rad), f(x), _i32(src), _i32(tptr), f(coef), g_rad,
                                      g_mcat, g_coef, tsum)
-            nat.node_gather_sum_dst(g_mcat, _i32(sptr), _i32(perm), tsum, None, gn)
+            nat.node_gather_sum_dst(g_mcat, _i32(sptr), _i32(perm), tsum, f(res), gn)
+        else:
+            ssum = torch.full((N, 9, C), float("nan"), device=DEV)
+            half = torch.full((E, 35), float("nan"), device=DEV)
+            nat.gather_rotate_bw_nodes(f(gout), f(rad), f(x), _i32(sptr), _i32(perm), _i32(tptr),
+                                       f(coef), g_rad, g_coef, half, ssum, f(res), gn)
         torch.cuda.synchronize()
-        outs[walk] = (g_rad.cpu(), g_mcat.cpu()[:, :, :C], gn.cpu(), g_coef.cpu())
-    for a, b in zip(outs["edge"][:3], outs["dst"][:3]):
+        outs[walk] = (g_rad.cpu(), gn.cpu(), g_coef.cpu(), g_mcat.cpu()[:, :, :C])
+    for a, b in zip(outs["edge"][:2], outs["dst"][:2]):
         assert torch.equal(a, b)
-    ga, gb = outs["edge"][3].double(), outs["dst"][3].double()
+    assert torch.equal(outs["edge"][3], outs["dst"][3])        # the source half of g_mcat
+    ga, gb = outs["edge"][2].double(), outs["dst"][2].double()
     assert ((ga - gb).abs() / (ga.abs() + 1.0)).max() < 1e-5
+    # the walk from both ends: the bits of the destination walk, g_coef included
+    for a, b in zip(outs["dst"][:3], outs["nodes"][:3]):
+        assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("C", [16, 128, 256, 1024])

@@ -355,6 +355,103 @@ __global__ __launch_bounds__(128) void k_gather_rotate_bw_dst(
   }
 }
 
+// The same backward walked from both ends of every edge, so that the adjoint of the interleaved
+// gather never goes to memory: k_gather_rotate_bw_walk<V, false> takes the source half of each
+// edge's channels ([0, C)) from its source node (edges through the source CSR, src_perm order),
+// <V, true> the destination half ([C, 2C)) from its destination node (the contiguous destination
+// segment).  One wavefront per node: the node's own row x[n] is loaded once (not gathered per
+// edge), and the node's half of the gather adjoint is summed in registers over its edges in walk
+// order from zero -- the source walk's sum is the source loop of k_node_gather_sum, the
+// destination walk's that of k_gather_rotate_bw_dst -- and the destination walk writes
+// out[n] = (source sum + destination sum) (+ res), the order of k_node_gather_sum.  Per edge
+// the arithmetic is that of k_gather_rotate_bw_dst's wave for the half, so g_rad and the node
+// adjoint are bit-identical to it; the coefficient adjoint's channel sum of the source half goes
+// to coef_half [E, 35] and the destination walk accumulates g_coef = g_coef + (source half +
+// destination half), its grouping too.
+template <int V, bool TGT>
+__global__ __launch_bounds__(256) void k_gather_rotate_bw_walk(
+    const float* __restrict__ g_xf, const float* __restrict__ rad, const float* __restrict__ x,
+    const int* __restrict__ ptr, const int* __restrict__ perm, const float* __restrict__ coef,
+    float* __restrict__ g_rad, float* __restrict__ g_coef, float* __restrict__ coef_half,
+    const float* __restrict__ ssum, const float* __restrict__ res, float* __restrict__ out,
+    int N, int C) {
+  typedef typename VecT<V>::T T;
+  __shared__ float red[WAVES][NNZ * 4];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int n = wave_uniform(blockIdx.x * WAVES + w);
+  if (n >= N) return;
+  const int W = 2 * C, cq = C / V, q = lane;
+  const bool active = q < cq;
+  const int qq = active ? q : 0;  // idle lanes (C < 64 V) load channel 0 and store nothing
+  const int co = (TGT ? C : 0) + V * qq;  // this lane's first channel within a 2C row
+  const int k0 = wave_uniform(ptr[n]), k1 = wave_uniform(ptr[n + 1]);
+  T in[NSPH], acc[NSPH];
+#pragma unroll
+  for (int j = 0; j < NSPH; ++j) {
+    in[j] = ldv<V>(x + (int64_t)n * NSPH * C + j * C + V * qq);
+    acc[j] = zv<V>();
+  }
+  for (int k = k0; k < k1; ++k) {
+    const int64_t e = TGT ? k : wave_uniform(perm[k]);
+    float c[NNZ];
+    load_coef(coef, e, c);
+    float gc[NNZ];
+#pragma unroll
+    for (int kk = 0; kk < NNZ; ++kk) gc[kk] = 0.f;
+    // destination walk: the coefficient adjoint so far and the source walk's channel sum
+    const float before = (TGT && lane < NNZ) ? g_coef[e * NNZ + lane] : 0.f;
+    const float half0 = (TGT && lane < NNZ) ? coef_half[e * NNZ + lane] : 0.f;
+    if (active) {
+      const int64_t eo = e * NSPH * W + co;
+      T gm[NSPH], mr[NSPH];
+#pragma unroll
+      for (int m = 0; m < NSPH; ++m) gm[m] = ldv_nt<V>(g_xf + eo + m * W);
+      rot_fwd(c, in, mr);
+      float* grp = g_rad + e * 6 * W + co;
+      stv<V>(grp + 0 * W, gm[0] * mr[0]);
+      stv<V>(grp + 1 * W, gm[1] * mr[1]);
+      stv<V>(grp + 2 * W, gm[2] * mr[2]);
+      stv<V>(grp + 3 * W, gm[3] * mr[3] + gm[5] * mr[5]);
+      stv<V>(grp + 4 * W, gm[4] * mr[4] + gm[6] * mr[6]);
+      stv<V>(grp + 5 * W, gm[7] * mr[7] + gm[8] * mr[8]);
+      const float* rp = rad + e * 6 * W + co;
+#pragma unroll
+      for (int m = 0; m < NSPH; ++m) gm[m] = gm[m] * ldv_nt<V>(rp + rad_block(m) * W);
+      T gi[NSPH];
+      rot_inv<9>(c, gm, gi);
+      {
+        // every row rounded before it is added, as k_node_gather_sum adds the stored rows and
+        // k_gather_rotate_bw_dst adds them in a later block (gi[0] is a bare product, which the
+        // add would otherwise absorb into an fma)
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int j = 0; j < NSPH; ++j) acc[j] = acc[j] + gi[j];
+      }
+      coef_partials<9, V>(gm, in, gc);
+    }
+    const float tot = wave_sums<NNZ>(gc, red[w], lane);
+    if (lane < NNZ) {
+      if (TGT)
+        g_coef[e * NNZ + lane] = before + (half0 + tot);
+      else
+        coef_half[e * NNZ + lane] = tot;
+    }
+  }
+  if (!active) return;
+  const int64_t no = (int64_t)n * NSPH * C + V * q;
+#pragma unroll
+  for (int j = 0; j < NSPH; ++j) {
+    if (!TGT) {
+      stv<V>(out + no + j * C, acc[j]);
+    } else {
+      T v = ldv<V>(ssum + no + j * C) + acc[j];
+      if (res) v = v + ldv<V>(res + no + j * C);
+      stv<V>(out + no + j * C, v);
+    }
+  }
+}
+
 // -------------------------------------------------------------------------------------------
 // Inverse rotation + envelope + destination-sorted segmented sum (+ residual):
 //   out[n, j, :] = res[n, j, :] + sum_{e in [ptr[n], ptr[n+1])} contrib_e[j, :]
@@ -667,6 +764,55 @@ extern "C" int tta_gather_rotate_bw_dst(const float* g_xf, const float* rad, con
                        (int)C);
   });
   TTA_CHECK_LAUNCH("tta_gather_rotate_bw_dst");
+  return tta::kOk;
+}
+
+// The two walks of the rotation backward (k_gather_rotate_bw_walk); the source walk runs first.
+static int bw_walk_check(int64_t N, int64_t E, int64_t C, const char* who) {
+  TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C / pick_v(C) <= 64,
+                "%s: channel count C=%lld needs C / V <= 64 (C <= 256)", who, (long long)C);
+  TTA_CHECK_ARG(E >= 0 && N >= 0 && E < (1ll << 31) && N < (1ll << 31), "%s: bad sizes", who);
+  return tta::kOk;
+}
+
+extern "C" int tta_gather_rotate_bw_srcwalk(const float* g_xf, const float* rad, const float* x,
+                                            const int* src_ptr, const int* src_perm,
+                                            const float* coef, float* g_rad, float* coef_half,
+                                            float* ssum, int64_t N, int64_t E, int64_t C,
+                                            hipStream_t stream) {
+  const int rc = bw_walk_check(N, E, C, "tta_gather_rotate_bw_srcwalk");
+  if (rc != tta::kOk || N == 0) return rc;
+  TTA_CHECK_ARG(src_ptr && x && ssum && (E == 0 || (src_perm && g_xf && rad && coef && g_rad &&
+                                                     coef_half)),
+                "tta_gather_rotate_bw_srcwalk: null pointer");
+  const int V = pick_v(C);
+  TTA_V_DISPATCH(V, {
+    hipLaunchKernelGGL((k_gather_rotate_bw_walk<VV, false>), dim3(wave_blocks(N)), dim3(256), 0,
+                       stream, g_xf, rad, x, src_ptr, src_perm, coef, g_rad, nullptr, coef_half,
+                       nullptr, nullptr, ssum, (int)N, (int)C);
+  });
+  TTA_CHECK_LAUNCH("tta_gather_rotate_bw_srcwalk");
+  return tta::kOk;
+}
+
+extern "C" int tta_gather_rotate_bw_tgtwalk(const float* g_xf, const float* rad, const float* x,
+                                            const int* tgt_ptr, const float* coef, float* g_rad,
+                                            float* g_coef, const float* coef_half,
+                                            const float* ssum, const float* res, float* out,
+                                            int64_t N, int64_t E, int64_t C,
+                                            hipStream_t stream) {
+  const int rc = bw_walk_check(N, E, C, "tta_gather_rotate_bw_tgtwalk");
+  if (rc != tta::kOk || N == 0) return rc;
+  TTA_CHECK_ARG(tgt_ptr && x && ssum && out && (E == 0 || (g_xf && rad && coef && g_rad &&
+                                                           g_coef && coef_half)),
+                "tta_gather_rotate_bw_tgtwalk: null pointer");
+  const int V = pick_v(C);
+  TTA_V_DISPATCH(V, {
+    hipLaunchKernelGGL((k_gather_rotate_bw_walk<VV, true>), dim3(wave_blocks(N)), dim3(256), 0,
+                       stream, g_xf, rad, x, tgt_ptr, nullptr, coef, g_rad, g_coef,
+                       const_cast<float*>(coef_half), ssum, res, out, (int)N, (int)C);
+  });
+  TTA_CHECK_LAUNCH("tta_gather_rotate_bw_tgtwalk");
   return tta::kOk;
 }
 

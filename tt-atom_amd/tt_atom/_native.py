@@ -44,6 +44,9 @@ _SIGS = {
     "tta_gather_rotate": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_gather_rotate_bw_dst": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_node_gather_sum_dst": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "tta_gather_rotate_bw_srcwalk": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
+    "tta_gather_rotate_bw_tgtwalk": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+                                     _I64, _P],
     "tta_gather_rotate_bw": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "tta_rotate_env_segsum": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _F, _P],
     "tta_rotate_env_segsum_bw": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _F,
@@ -720,6 +723,40 @@ def node_gather_sum_dst(g_mcat, src_ptr, src_perm, tsum, res, out):
               _ptr(g_mcat, numel=E * 18 * C, name="g_mcat"),
               _i32(src_ptr, N + 1, "src_ptr"), _i32(src_perm, E, "src_perm"),
               _ptr(tsum, numel=N * 9 * C, name="tsum"), _ptr(res, numel=N * 9 * C, name="res"),
+              _ptr(out, numel=N * 9 * C, name="out"), N, E, C, _stream())
+    return out
+
+
+def gather_rotate_bw_nodes(g_xf, rad, x, src_ptr, src_perm, tgt_ptr, coef, g_rad, g_coef,
+                           coef_half, ssum, res, out):
+    """The backward of gather_rotate (rad given) walked from both ends of every edge: the source
+    walk (outgoing edges of each node through src_ptr / src_perm, source half of the channels)
+    writes ssum [N, 9, C] and the source half's coefficient sums coef_half [E, 35]; the
+    destination walk (incoming edges, tgt_ptr, destination half) writes out [N, 9, C] =
+    (ssum + its sum) + res and accumulates g_coef.  Both write their half of g_rad.  The bits of
+    gather_rotate_bw_dst + node_gather_sum_dst, without the [E, 9, C] gather adjoint.
+    C <= 256."""
+    N, _, C = x.shape
+    E = src_perm.numel()
+    V = _pick_v(C)
+    chk = dict(g_xf=(g_xf, E * 18 * C), rad=(rad, E * 12 * C), g_rad=(g_rad, E * 12 * C),
+               coef=(coef, E * 35), g_coef=(g_coef, E * 35), coef_half=(coef_half, E * 35))
+    p = {k: _ptr(t, numel=n, name=k) for k, (t, n) in chk.items()}
+    xp = _ptr(x, numel=N * 9 * C, name="x")
+    sp = _ptr(ssum, numel=N * 9 * C, name="ssum")
+    # per edge: the half rows of g_xf and rad read, of g_rad written; the coefficients (and the
+    # source walk's sums, and g_coef read and written); per node: its own row, the sums
+    e_src = 4 * (21 * C + 35 + 35 + 1)
+    _hbm_call(f"k_gather_rotate_bw_walk<{V},false>", E * e_src + 4 * N * (18 * C + 1),
+              "tta_gather_rotate_bw_srcwalk", p["g_xf"], p["rad"], xp,
+              _i32(src_ptr, N + 1, "src_ptr"), _i32(src_perm, E, "src_perm"), p["coef"],
+              p["g_rad"], p["coef_half"], sp, N, E, C, _stream())
+    e_tgt = 4 * (21 * C + 4 * 35)
+    _hbm_call(f"k_gather_rotate_bw_walk<{V},true>",
+              E * e_tgt + 4 * N * ((27 + 9 * (res is not None)) * C + 1),
+              "tta_gather_rotate_bw_tgtwalk", p["g_xf"], p["rad"], xp,
+              _i32(tgt_ptr, N + 1, "tgt_ptr"), p["coef"], p["g_rad"], p["g_coef"],
+              p["coef_half"], sp, _ptr(res, numel=N * 9 * C, name="res"),
               _ptr(out, numel=N * 9 * C, name="out"), N, E, C, _stream())
     return out
 

@@ -89,7 +89,13 @@ class TracedEngine:
         self.t1_all, self.t2_all = emp(E, nrad * hid), emp(E, nrad * hid)
         # shared edge temporaries
         self.LHc = L * H + NSPH * H                      # combined conv-1 row [gating | out]
-        self.xf, self.g_xf, self.g_mcat = emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C)
+        self.xf, self.g_xf = emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C)
+        # the rotation backward walks each node's edges from both ends (C <= 256), so the
+        # [E, 9, 2C] adjoint of the gather exists only for wider rows; coef_half: the source
+        # walk's coefficient sums
+        self.bw_walk = C <= 256
+        self.g_mcat = None if self.bw_walk else emp(E, NSPH, 2 * C)
+        self.coef_half = emp(E, 35) if self.bw_walk else None
         # the gate in the SO(2) GEMM epilogues for edge-level launches on the split kernel; below
         # 4096 edges (launch-latency bound) the separate gating product would add launches, so
         # the gate keeps its own passes there
@@ -97,7 +103,7 @@ class TracedEngine:
         if not self.gate_fused:
             # the gated conv-1 rows and their adjoint on the path with the gate as its own pass
             self.y, self.g_y = emp(E, NSPH, H), emp(E, NSPH, H)
-        self.g_tsum = emp(N, NSPH, C)                    # per-node destination adjoint sums
+        self.g_tsum = emp(N, NSPH, C)                    # per-node source-half adjoint sums
         self.g1c = emp(E, self.LHc)
         self.g_mso2 = emp(E, NSPH, C)
         # per-radial output caches and their adjoints (kept per block: the radial backward of all
@@ -371,12 +377,13 @@ class TracedEngine:
         nat.linear_group([(g1[:, :LH + 3 * H], s1w.wm0, None, gx[:, :3 * Cin]),
                           (g1[:, LH + 3 * H:LH + 7 * H], s1w.w1_t, None, gx[:, 3 * Cin:7 * Cin]),
                           (g1[:, LH + 7 * H:], s1w.w2_t, None, gx[:, 7 * Cin:])])
-        if self.C <= 256:
-            # walked by destination: the destination half of the adjoint is summed per node in
-            # the rotation backward instead of crossing HBM twice as [E, 9, C]
-            nat.gather_rotate_bw_dst(self.g_xf, c.rad.out, c.n1, g.src, g.tgt_ptr, self.coef,
-                                     c.rad.g_out, self.g_mcat, self.g_coef, self.g_tsum)
-            nat.node_gather_sum_dst(self.g_mcat, g.src_ptr, g.src_perm, self.g_tsum, None, g_n1)
+        if self.bw_walk:
+            # walked from both ends of every edge: each half of the gather adjoint is summed per
+            # node in registers instead of crossing HBM as [E, 9, C] (source half) and being
+            # gathered back
+            nat.gather_rotate_bw_nodes(self.g_xf, c.rad.out, c.n1, g.src_ptr, g.src_perm,
+                                       g.tgt_ptr, self.coef, c.rad.g_out, self.g_coef,
+                                       self.coef_half, self.g_tsum, None, g_n1)
         else:
             nat.gather_rotate_bw(self.g_xf, c.rad.out, c.n1, g.src, g.tgt, self.coef,
                                  c.rad.g_out, self.g_mcat, self.g_coef)

@@ -170,6 +170,71 @@ __device__ __forceinline__ float wave_sums(float* v, float* lds, int lane) {
   return t;
 }
 
+// The same sums as a reduce-scatter by recursive halving: six exchange steps, each pairing a lane
+// with a partner (lane xor 32, 16, 15, 7, 3, 1: v_permlane32_swap, v_permlane16_swap, DPP
+// row_mirror, row_half_mirror and two quad permutations) and halving the values a lane carries
+// (the lane keeps the lower or upper half of its slots by one lane bit: 5, 4, 3, 2, 1, 0 -- the
+// bits the later partners leave alone), so after the six steps a value's 64 lane partials are
+// summed in one lane: about 2.5 instructions per value against 5 and an LDS round trip.
+// halving_index(lane) is the value a lane ends with, or -1 (lanes past the NV values hold 0).
+template <int NV>
+struct Halving {
+  static_assert(NV >= 1 && NV <= 64, "1..64 values");
+  static constexpr int n0 = NV, h1 = (n0 + 1) / 2, h2 = (h1 + 1) / 2, h3 = (h2 + 1) / 2,
+                       h4 = (h3 + 1) / 2, h5 = (h4 + 1) / 2, h6 = (h5 + 1) / 2;
+};
+
+template <int NV>
+__device__ __forceinline__ int halving_index(int lane) {
+  typedef Halving<NV> H;
+  const int size[6] = {H::n0, H::h1, H::h2, H::h3, H::h4, H::h5};  // each step's input slots
+  const int half[6] = {H::h1, H::h2, H::h3, H::h4, H::h5, H::h6};
+  const int bit[6] = {5, 4, 3, 2, 1, 0};
+  int j = 0;  // the slot kept after the last step, traced back to the step's input
+  for (int st = 5; st >= 0; --st) {
+    j += ((lane >> bit[st]) & 1) * half[st];
+    if (j >= size[st]) return -1;
+  }
+  return j;
+}
+
+// one step over lanes paired by a swap builtin: r[0] + r[1] is the pair's sum of the kept slot
+template <int N, int HALF, bool X16>
+__device__ __forceinline__ void halve_swap(const float* in, float* out) {
+#pragma unroll
+  for (int j = 0; j < HALF; ++j) {
+    const unsigned a = __float_as_uint(in[j]), b = j + HALF < N ? __float_as_uint(in[j + HALF]) : 0u;
+    const auto r = X16 ? __builtin_amdgcn_permlane16_swap(a, b, false, false)
+                       : __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    out[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
+// one step over lanes paired by a DPP permutation CTRL; `upper`: this lane keeps the upper half
+template <int N, int HALF, int CTRL>
+__device__ __forceinline__ void halve_dpp(const float* in, float* out, bool upper) {
+#pragma unroll
+  for (int j = 0; j < HALF; ++j) {
+    const float a = in[j], b = j + HALF < N ? in[j + HALF] : 0.f;
+    const float keep = upper ? b : a, send = upper ? a : b;
+    out[j] = keep + __int_as_float(
+                        __builtin_amdgcn_update_dpp(0, __float_as_int(send), CTRL, 0xF, 0xF, true));
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ float halving_sums(const float* v, int lane) {
+  typedef Halving<NV> H;
+  float a[H::h1], b[H::h2], c[H::h3], d[H::h4], e[H::h5], f[H::h6];
+  halve_swap<H::n0, H::h1, false>(v, a);                // lane ^ 32, keeps by bit 5
+  halve_swap<H::h1, H::h2, true>(a, b);                 // lane ^ 16, bit 4
+  halve_dpp<H::h2, H::h3, 0x140>(b, c, lane & 8);       // row_mirror: lane ^ 15, bit 3
+  halve_dpp<H::h3, H::h4, 0x141>(c, d, lane & 4);       // row_half_mirror: lane ^ 7, bit 2
+  halve_dpp<H::h4, H::h5, 0x1B>(d, e, lane & 2);        // quad_perm [3,2,1,0]: lane ^ 3, bit 1
+  halve_dpp<H::h5, H::h6, 0xB1>(e, f, lane & 1);        // quad_perm [1,0,3,2]: lane ^ 1, bit 0
+  return f[0];
+}
+
 __device__ __forceinline__ int wave_uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 __device__ __forceinline__ void load_coef(const float* __restrict__ coef, int64_t e, float* c) {
@@ -376,10 +441,11 @@ __global__ __launch_bounds__(256) void k_gather_rotate_bw_walk(
     const float* __restrict__ ssum, const float* __restrict__ res, float* __restrict__ out,
     int N, int C) {
   typedef typename VecT<V>::T T;
-  __shared__ float red[WAVES][NNZ * 4];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int n = wave_uniform(blockIdx.x * WAVES + w);
+  const int ki = halving_index<NNZ>(lane);  // the coefficient whose sum this lane ends with
+  const int kl = ki < 0 ? 0 : ki;
   if (n >= N) return;
   const int W = 2 * C, cq = C / V, q = lane;
   const bool active = q < cq;
@@ -400,8 +466,8 @@ __global__ __launch_bounds__(256) void k_gather_rotate_bw_walk(
 #pragma unroll
     for (int kk = 0; kk < NNZ; ++kk) gc[kk] = 0.f;
     // destination walk: the coefficient adjoint so far and the source walk's channel sum
-    const float before = (TGT && lane < NNZ) ? g_coef[e * NNZ + lane] : 0.f;
-    const float half0 = (TGT && lane < NNZ) ? coef_half[e * NNZ + lane] : 0.f;
+    const float before = TGT ? g_coef[e * NNZ + kl] : 0.f;
+    const float half0 = TGT ? coef_half[e * NNZ + kl] : 0.f;
     if (active) {
       const int64_t eo = e * NSPH * W + co;
       T gm[NSPH], mr[NSPH];
@@ -430,12 +496,12 @@ __global__ __launch_bounds__(256) void k_gather_rotate_bw_walk(
       }
       coef_partials<9, V>(gm, in, gc);
     }
-    const float tot = wave_sums<NNZ>(gc, red[w], lane);
-    if (lane < NNZ) {
+    const float tot = halving_sums<NNZ>(gc, lane);
+    if (ki >= 0) {
       if (TGT)
-        g_coef[e * NNZ + lane] = before + (half0 + tot);
+        g_coef[e * NNZ + ki] = before + (half0 + tot);
       else
-        coef_half[e * NNZ + lane] = tot;
+        coef_half[e * NNZ + ki] = tot;
     }
   }
   if (!active) return;

@@ -637,7 +637,6 @@ __global__ __launch_bounds__(256) void k_rotate_env_segsum_bw(
     const float* __restrict__ coef, const float* __restrict__ env, float* __restrict__ g_m,
     float* __restrict__ g_coef, float* __restrict__ g_env, int E, int C, float div) {
   typedef typename VecT<V>::T T;
-  __shared__ float red[WAVES][(NNZ + 1) * 4];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int e = wave_uniform(blockIdx.x * WAVES + w);
@@ -684,9 +683,11 @@ __global__ __launch_bounds__(256) void k_rotate_env_segsum_bw(
       coef_partials<NIN, V>(mi, g1, gc);
     }
   }
-  const float tot = wave_sums<NNZ + 1>(gc, red[w], lane);
-  if (lane < NNZ) g_coef[(int64_t)e * NNZ + lane] += tot;
-  if (lane == NNZ) g_env[e] += tot;
+  // the 35 coefficient sums and the envelope's (value NNZ), each in one lane
+  const float tot = halving_sums<NNZ + 1>(gc, lane);
+  const int ki = halving_index<NNZ + 1>(lane);
+  if (ki >= 0 && ki < NNZ) g_coef[(int64_t)e * NNZ + ki] += tot;
+  if (ki == NNZ) g_env[e] += tot;
 }
 
 // -------------------------------------------------------------------------------------------

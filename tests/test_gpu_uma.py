@@ -94,6 +94,23 @@ def test_c1_tiny(golden, precision):
     assert not eng.gate_fused
 
 
+def test_c1_wide_rows_edge_walk(golden):
+    """C1 at 96 sphere channels: a width whose channels do not fit one lane vector per wavefront
+    (96 / pick_v = 96 > 64), so the rotation backward takes the edge walk with the node sum
+    instead of the walk from both ends of every edge; energy and forces against the oracle."""
+    from tt_atom import synthetic
+    from tt_atom.geometry import radius_graph
+    cfg = dict(synthetic.CFG_C1, sphere_channels=96)
+    w, host = synthetic.random_uma_bundle(cfg, synthetic.SEEDS["C1"] + 300,
+                                          grid_mats=(golden.host("to_grid_mat"),
+                                                     golden.host("from_grid_mat")))
+    pos, Z = synthetic.c1_system()
+    pos, Z = torch.from_numpy(pos), torch.from_numpy(Z)
+    ei, _ = radius_graph(pos, cfg["cutoff"], max_neighbors=cfg["max_neighbors"])
+    eng, _ = _check(w, cfg, host, pos, Z, ei, _system_embedding(w, cfg, len(Z)), label="C1 C=96")
+    assert not eng.bw_walk and eng.g_mcat is not None
+
+
 def test_c3_reduced():
     """uma-s-1 widths, 256 atoms at the C3 density (ball radius 17 (256/2048)^(1/3) A)."""
     from tt_atom import synthetic

@@ -93,8 +93,9 @@ __global__ __launch_bounds__(256) void k_gate_gating_bwd(
 }
 
 // ------------------------------------------------------------------ LayerNorm + SiLU (radial MLP)
-// G lanes per row (64, or 32 for rows of at most 128 so that a wavefront holds two rows and twice
-// the bytes are in flight per wave); the row stays in registers (element NPL lane + k in slot k,
+// G lanes per row (64; 16 for rows of 65 to 128, so that a wavefront holds four rows and a lane
+// two float4 groups of its row in flight; 32 below); the row stays in registers (element NPL
+// lane + k in slot k,
 // NPL slots) so that each operand crosses HBM once.  The per-lane partial sums run over k in
 // order.  The float4 path (VEC) and the element-wise path hold the same columns in the same
 // slots and are compiled without fused multiply-adds, so both round every operation alike
@@ -132,10 +133,13 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
   // in one float4
   float v[NPL];
   if constexpr (VEC) {
-    static_assert(NPL == 4, "float4 rows");
-    const floatx4 x = *reinterpret_cast<const floatx4*>(ar + 4 * lane);
+    static_assert(NPL % 4 == 0, "float4 groups");
 #pragma unroll
-    for (int k = 0; k < 4; ++k) v[k] = x[k];
+    for (int b = 0; b < NPL / 4; ++b) {
+      const floatx4 x = *reinterpret_cast<const floatx4*>(ar + NPL * lane + 4 * b);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * b + k] = x[k];
+    }
   }
   float sum = 0.f;
 #pragma unroll
@@ -157,16 +161,20 @@ __global__ __launch_bounds__(256) void k_ln_silu_fwd(const float* __restrict__ a
   const float rstd = 1.0f / sqrtf(var + eps);
   if (!valid) return;
   if constexpr (VEC) {
-    const floatx4 gm = *reinterpret_cast<const floatx4*>(gamma + 4 * lane);
-    const floatx4 bt = *reinterpret_cast<const floatx4*>(beta + 4 * lane);
-    floatx4 y, sv;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      y[k] = (v[k] - mean) * rstd * gm[k] + bt[k];
-      sv[k] = tta_silu(y[k]);
+    for (int b = 0; b < NPL / 4; ++b) {
+      const int c4 = NPL * lane + 4 * b;
+      const floatx4 gm = *reinterpret_cast<const floatx4*>(gamma + c4);
+      const floatx4 bt = *reinterpret_cast<const floatx4*>(beta + c4);
+      floatx4 y, sv;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        y[k] = (v[4 * b + k] - mean) * rstd * gm[k] + bt[k];
+        sv[k] = tta_silu(y[k]);
+      }
+      if (nrm) *reinterpret_cast<floatx4*>(nrm + row * lda + co + c4) = y;
+      *reinterpret_cast<floatx4*>(s + row * lds + co + c4) = sv;
     }
-    if (nrm) *reinterpret_cast<floatx4*>(nrm + row * lda + co + 4 * lane) = y;
-    *reinterpret_cast<floatx4*>(s + row * lds + co + 4 * lane) = sv;
     return;
   }
 #pragma unroll
@@ -212,19 +220,23 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   float sum = 0.f;
   // element layout as in k_ln_silu_fwd
   if constexpr (VEC) {
-    static_assert(NPL == 4, "float4 rows");
-    const floatx4 x = *reinterpret_cast<const floatx4*>(ar + 4 * lane);
-    const floatx4 gv = *reinterpret_cast<const floatx4*>(g + row * ldg + co + 4 * lane);
-    floatx4 nv = {0.f, 0.f, 0.f, 0.f}, gm = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (!RECOMP) {
-      nv = *reinterpret_cast<const floatx4*>(nrm + row * lda + co + 4 * lane);
-      gm = *reinterpret_cast<const floatx4*>(gamma + 4 * lane);
-    }
+    static_assert(NPL % 4 == 0, "float4 groups");
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      av[k] = x[k];
-      gy[k] = RECOMP ? gv[k] : gv[k] * tta_silu_grad(nv[k]) * gm[k];
-      sum += av[k];
+    for (int b = 0; b < NPL / 4; ++b) {
+      const int c4 = NPL * lane + 4 * b;
+      const floatx4 x = *reinterpret_cast<const floatx4*>(ar + c4);
+      const floatx4 gv = *reinterpret_cast<const floatx4*>(g + row * ldg + co + c4);
+      floatx4 nv = {0.f, 0.f, 0.f, 0.f}, gm = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (!RECOMP) {
+        nv = *reinterpret_cast<const floatx4*>(nrm + row * lda + co + c4);
+        gm = *reinterpret_cast<const floatx4*>(gamma + c4);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        av[4 * b + k] = x[k];
+        gy[4 * b + k] = RECOMP ? gv[k] : gv[k] * tta_silu_grad(nv[k]) * gm[k];
+        sum += av[4 * b + k];
+      }
     }
   } else {
 #pragma unroll
@@ -251,12 +263,16 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   const float rstd = 1.0f / sqrtf(var + eps);
   if (RECOMP) {
     if constexpr (VEC) {
-      const floatx4 gm = *reinterpret_cast<const floatx4*>(gamma + 4 * lane);
-      const floatx4 bt = *reinterpret_cast<const floatx4*>(beta + 4 * lane);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float y = (av[k] - mean) * rstd * gm[k] + bt[k];
-        gy[k] = gy[k] * tta_silu_grad(y) * gm[k];
+      for (int b = 0; b < NPL / 4; ++b) {
+        const int c4 = NPL * lane + 4 * b;
+        const floatx4 gm = *reinterpret_cast<const floatx4*>(gamma + c4);
+        const floatx4 bt = *reinterpret_cast<const floatx4*>(beta + c4);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float y = (av[4 * b + k] - mean) * rstd * gm[k] + bt[k];
+          gy[4 * b + k] = gy[4 * b + k] * tta_silu_grad(y) * gm[k];
+        }
       }
     } else {
 #pragma unroll
@@ -278,13 +294,16 @@ __global__ __launch_bounds__(256) void k_ln_silu_bwd(const float* __restrict__ g
   m2 = tta_group_sum(m2, G) / n;
   if (!valid) return;
   if constexpr (VEC) {
-    floatx4 o;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float xh = (av[k] - mean) * rstd;
-      o[k] = rstd * (gy[k] - m1 - xh * m2);
+    for (int b = 0; b < NPL / 4; ++b) {
+      floatx4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float xh = (av[4 * b + k] - mean) * rstd;
+        o[k] = rstd * (gy[4 * b + k] - m1 - xh * m2);
+      }
+      *reinterpret_cast<floatx4*>(g_a + row * ldo + co + NPL * lane + 4 * b) = o;
     }
-    *reinterpret_cast<floatx4*>(g_a + row * ldo + co + 4 * lane) = o;
     return;
   }
 #pragma unroll
@@ -606,9 +625,9 @@ extern "C" int tta_ln_silu_fwd(const float* a, const float* gamma, const float* 
   else if (n <= 64)
     TTA_LN_FWD(32, 2, false);
   else if (n <= 128 && vec)
-    TTA_LN_FWD(32, 4, true);
+    TTA_LN_FWD(16, 8, true);
   else if (n <= 128)
-    TTA_LN_FWD(32, 4, false);
+    TTA_LN_FWD(16, 8, false);
   else if (n <= 256 && vec)
     TTA_LN_FWD(64, 4, true);
   else if (n <= 256)
@@ -650,9 +669,9 @@ extern "C" int tta_ln_silu_bwd(const float* g, const float* a, const float* nrm,
   else if (n <= 64)
     TTA_LN_BWD(32, 2, false);
   else if (n <= 128 && vec)
-    TTA_LN_BWD(32, 4, true);
+    TTA_LN_BWD(16, 8, true);
   else if (n <= 128)
-    TTA_LN_BWD(32, 4, false);
+    TTA_LN_BWD(16, 8, false);
   else if (n <= 256 && vec)
     TTA_LN_BWD(64, 4, true);
   else if (n <= 256)

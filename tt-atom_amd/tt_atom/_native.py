@@ -633,7 +633,7 @@ def _ln_variant(n, vec):
     if n <= 64:
         return 32, 2, False
     if n <= 128:
-        return 32, 4, vec
+        return 16, 8, vec
     if n <= 256:
         return 64, 4, vec
     return 64, 8, False

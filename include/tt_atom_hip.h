@@ -162,8 +162,10 @@ int tta_gather_rotate_bw_dst(const float* g_xf, const float* rad, const float* x
  * source walk writes ssum [N,9,C], the destination walk out[n] = (ssum[n] + its sum) + res[n]
  * (res may be NULL).  g_rad [E,6,2C]: each walk writes its half.  The coefficient adjoint: the
  * source walk writes its channel sum to coef_half [E,35], the destination walk accumulates
- * g_coef += (coef_half + its channel sum).  g_rad, g_coef and out are bit-identical to
- * tta_gather_rotate_bw_dst followed by tta_node_gather_sum_dst.  C <= 256.  Same reference
+ * g_coef += (coef_half + its channel sum).  g_rad and out are bit-identical to
+ * tta_gather_rotate_bw_dst followed by tta_node_gather_sum_dst, g_coef equal to fp32 rounding
+ * (its channel sums run across lanes in another order).  C / V <= 64 (V = 4, 2, 1 for C >= 256,
+ * >= 128, smaller), so C <= 256.  Same reference
  * functions as tta_gather_rotate_bw_dst (rotation.py:225-260, forces.py:164-170 and the
  * scatters of forces.py:384-412). */
 int tta_gather_rotate_bw_srcwalk(const float* g_xf, const float* rad, const float* x,

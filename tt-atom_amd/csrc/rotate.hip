@@ -432,7 +432,8 @@ __global__ __launch_bounds__(128) void k_gather_rotate_bw_dst(
 // the arithmetic is that of k_gather_rotate_bw_dst's wave for the half, so g_rad and the node
 // adjoint are bit-identical to it; the coefficient adjoint's channel sum of the source half goes
 // to coef_half [E, 35] and the destination walk accumulates g_coef = g_coef + (source half +
-// destination half), its grouping too.
+// destination half), its grouping too (each half's channel sum runs across lanes by recursive
+// halving, so g_coef matches k_gather_rotate_bw_dst's to fp32 rounding).
 template <int V, bool TGT>
 __global__ __launch_bounds__(256) void k_gather_rotate_bw_walk(
     const float* __restrict__ g_xf, const float* __restrict__ rad, const float* __restrict__ x,

@@ -733,9 +733,9 @@ def gather_rotate_bw_nodes(g_xf, rad, x, src_ptr, src_perm, tgt_ptr, coef, g_rad
     walk (outgoing edges of each node through src_ptr / src_perm, source half of the channels)
     writes ssum [N, 9, C] and the source half's coefficient sums coef_half [E, 35]; the
     destination walk (incoming edges, tgt_ptr, destination half) writes out [N, 9, C] =
-    (ssum + its sum) + res and accumulates g_coef.  Both write their half of g_rad.  The bits of
-    gather_rotate_bw_dst + node_gather_sum_dst, without the [E, 9, C] gather adjoint.
-    C <= 256."""
+    (ssum + its sum) + res and accumulates g_coef.  Both write their half of g_rad.  g_rad and
+    out are the bits of gather_rotate_bw_dst + node_gather_sum_dst (g_coef to fp32 rounding),
+    without the [E, 9, C] gather adjoint.  C / _pick_v(C) <= 64."""
     N, _, C = x.shape
     E = src_perm.numel()
     V = _pick_v(C)

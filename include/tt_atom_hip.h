@@ -145,7 +145,8 @@ int tta_gather_rotate_bw(const float* g_xf, const float* rad, const float* x, co
  * edges (tgt_ptr [N+1]): g_rad and g_coef as there; g_mcat gets its source half [.., 0:C] only,
  * and tsum [N,9,C] = the destination half summed over each node's edges in edge order (zeros for
  * a node without edges), bit-identical to tta_node_gather_sum's destination sum; g_coef's channel
- * sum runs per half (equal to tta_gather_rotate_bw's to fp32 rounding).  C <= 256.  Same
+ * sum runs per half (equal to tta_gather_rotate_bw's to fp32 rounding).  C a multiple of 4 with
+ * C / V <= 64 (V = 4, 2, 1 for C >= 256, >= 128, smaller): C <= 64, C = 128 or C = 256.  Same
  * reference functions as tta_gather_rotate_bw plus the destination scatter of
  * forces.py:384-412, whose [E,9,C] half it never writes. */
 int tta_gather_rotate_bw_dst(const float* g_xf, const float* rad, const float* x, const int* src,
@@ -164,8 +165,8 @@ int tta_gather_rotate_bw_dst(const float* g_xf, const float* rad, const float* x
  * source walk writes its channel sum to coef_half [E,35], the destination walk accumulates
  * g_coef += (coef_half + its channel sum).  g_rad and out are bit-identical to
  * tta_gather_rotate_bw_dst followed by tta_node_gather_sum_dst, g_coef equal to fp32 rounding
- * (its channel sums run across lanes in another order).  C / V <= 64 (V = 4, 2, 1 for C >= 256,
- * >= 128, smaller), so C <= 256.  Same reference
+ * (its channel sums run across lanes in another order).  C as for tta_gather_rotate_bw_dst
+ * (C <= 64, C = 128 or C = 256; other widths take tta_gather_rotate_bw).  Same reference
  * functions as tta_gather_rotate_bw_dst (rotation.py:225-260, forces.py:164-170 and the
  * scatters of forces.py:384-412). */
 int tta_gather_rotate_bw_srcwalk(const float* g_xf, const float* rad, const float* x,

@@ -817,7 +817,8 @@ extern "C" int tta_gather_rotate_bw_dst(const float* g_xf, const float* rad, con
                                         float* g_rad, float* g_mcat, float* g_coef, float* tsum,
                                         int64_t N, int64_t E, int64_t C, hipStream_t stream) {
   TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C / pick_v(C) <= 64,
-                "tta_gather_rotate_bw_dst: channel count C=%lld needs C / V <= 64 (C <= 256)",
+                "tta_gather_rotate_bw_dst: channel count C=%lld needs C / V <= 64 "
+                "(C <= 64, 128 or 256)",
                 (long long)C);
   TTA_CHECK_ARG(E >= 0 && N >= 0 && E < (1ll << 31) && N < (1ll << 31),
                 "tta_gather_rotate_bw_dst: bad sizes");
@@ -838,7 +839,8 @@ extern "C" int tta_gather_rotate_bw_dst(const float* g_xf, const float* rad, con
 // The two walks of the rotation backward (k_gather_rotate_bw_walk); the source walk runs first.
 static int bw_walk_check(int64_t N, int64_t E, int64_t C, const char* who) {
   TTA_CHECK_ARG(C > 0 && C % 4 == 0 && C / pick_v(C) <= 64,
-                "%s: channel count C=%lld needs C / V <= 64 (C <= 256)", who, (long long)C);
+                "%s: channel count C=%lld needs C / V <= 64 (C <= 64, 128 or 256)", who,
+                (long long)C);
   TTA_CHECK_ARG(E >= 0 && N >= 0 && E < (1ll << 31) && N < (1ll << 31), "%s: bad sizes", who);
   return tta::kOk;
 }

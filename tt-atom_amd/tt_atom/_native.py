@@ -618,6 +618,13 @@ def _pick_v(W):
     return 4 if W >= 256 else 2 if W >= 128 else 1
 
 
+def bw_walk_width_ok(C):
+    """Whether the node walks of the rotation backward (gather_rotate_bw_dst / _nodes) take rows
+    of C channels: every channel of a half in one lane vector of a wavefront, C / V <= 64 with
+    C a multiple of 4, i.e. C <= 64, C = 128 or C = 256 (bw_walk_check in csrc/rotate.hip)."""
+    return C > 0 and C % 4 == 0 and C // _pick_v(C) <= 64
+
+
 def _tf(b):
     return "true" if b else "false"
 
@@ -735,7 +742,7 @@ def gather_rotate_bw_nodes(g_xf, rad, x, src_ptr, src_perm, tgt_ptr, coef, g_rad
     destination walk (incoming edges, tgt_ptr, destination half) writes out [N, 9, C] =
     (ssum + its sum) + res and accumulates g_coef.  Both write their half of g_rad.  g_rad and
     out are the bits of gather_rotate_bw_dst + node_gather_sum_dst (g_coef to fp32 rounding),
-    without the [E, 9, C] gather adjoint.  C / _pick_v(C) <= 64."""
+    without the [E, 9, C] gather adjoint.  bw_walk_width_ok(C) must hold."""
     N, _, C = x.shape
     E = src_perm.numel()
     V = _pick_v(C)

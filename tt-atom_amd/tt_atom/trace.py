@@ -90,10 +90,10 @@ class TracedEngine:
         # shared edge temporaries
         self.LHc = L * H + NSPH * H                      # combined conv-1 row [gating | out]
         self.xf, self.g_xf = emp(E, NSPH, 2 * C), emp(E, NSPH, 2 * C)
-        # the rotation backward walks each node's edges from both ends (C <= 256), so the
-        # [E, 9, 2C] adjoint of the gather exists only for wider rows; coef_half: the source
-        # walk's coefficient sums
-        self.bw_walk = C % 4 == 0 and C // nat._pick_v(C) <= 64     # every channel in one lane vector
+        # the rotation backward walks each node's edges from both ends (C <= 64, 128 or 256), so
+        # the [E, 9, 2C] adjoint of the gather exists only for other widths; coef_half: the
+        # source walk's coefficient sums
+        self.bw_walk = nat.bw_walk_width_ok(C)
         self.g_mcat = None if self.bw_walk else emp(E, NSPH, 2 * C)
         self.coef_half = emp(E, 35) if self.bw_walk else None
         # the gate in the SO(2) GEMM epilogues for edge-level launches on the split kernel; below
